@@ -1,0 +1,158 @@
+/*
+ * llmi_hip.h -- C ABI of the MI355X (gfx950) quantized-weight path.
+ *
+ * Every entry point replaces one function of llm-inference-cpp's
+ * quantized-weight path; the reference interface each one stands in for is
+ * cited beside it (paths relative to the reference repository root).  Plain
+ * pointers and sizes only: host pointers unless the name ends in _dev, in
+ * which case the pointers are device pointers and the work is queued on
+ * `stream` (a hipStream_t; NULL means the library's own stream) without a
+ * host synchronisation.
+ *
+ * Errors: every function returns LLMI_OK (0) or a non-zero LLMI_ERR_* code
+ * and leaves a message for llmi_hip_last_error() on the calling thread.  The
+ * reference's quant functions have no error channel (they return void and
+ * assume valid shapes); here bad shapes, unsupported types and HIP failures
+ * are reported instead of being undefined behaviour.
+ *
+ * Threading: like the reference (include/llmi/util/thread_pool.hpp:18-21,
+ * src/server/server.cpp:44-49) calls are not reentrant; serialise them.
+ */
+#ifndef LLMI_HIP_H
+#define LLMI_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  LLMI_OK = 0,
+  LLMI_ERR_ARG = 1,   /* bad shape, type, pointer or token id */
+  LLMI_ERR_HIP = 2,   /* HIP runtime failure (allocation, launch, copy) */
+  LLMI_ERR_STATE = 3, /* not initialised, cache full, cache from another model */
+};
+
+/* Weight storage types; the values of llmi::quant::Type
+ * (include/llmi/model/quant.hpp:17). */
+enum { LLMI_TYPE_F32 = 0, LLMI_TYPE_Q8_0 = 1, LLMI_TYPE_Q4_0 = 2 };
+
+/* Weights per quantization block (include/llmi/model/quant.hpp:15). */
+#define LLMI_BLOCK_SIZE 32
+
+/* Model hyper-parameters: the fields of llmi::ModelConfig
+ * (include/llmi/model/model.hpp:21-36) that the forward pass reads.
+ * head_dim = hidden_size / num_heads (src/model/model.cpp:100-105). */
+typedef struct llmi_model_config {
+  int32_t arch; /* 0 = Llama, 1 = Qwen2 (model.hpp:16) */
+  uint32_t vocab_size;
+  uint32_t hidden_size;
+  uint32_t intermediate_size;
+  uint32_t num_layers;
+  uint32_t num_heads;
+  uint32_t num_kv_heads;
+  uint32_t max_position_embeddings;
+  double rms_norm_eps;
+  double rope_theta;
+  int32_t tie_word_embeddings;
+  int32_t qkv_bias;
+} llmi_model_config;
+
+typedef struct llmi_hip_weight llmi_hip_weight; /* device-resident packed matrix */
+
+/* ----------------------------------------------------------------- runtime */
+
+/* Selects the GPU and creates the library stream.  Must precede every other
+ * call except llmi_hip_last_error and llmi_hip_version. */
+int llmi_hip_init(int device);
+/* Releases the library stream.  Weights stay valid until freed. */
+int llmi_hip_shutdown(void);
+const char* llmi_hip_last_error(void);
+const char* llmi_hip_version(void);
+/* The library's stream (hipStream_t), for callers that queue their own work. */
+void* llmi_hip_stream(void);
+int llmi_hip_synchronize(void);
+
+/* Plain device memory and copies, for callers without an allocator of
+ * their own (tests, bench.py).  Copies are synchronous. */
+int llmi_hip_malloc(void** ptr, size_t bytes);
+int llmi_hip_free(void* ptr);
+int llmi_hip_memcpy_h2d(void* dst_dev, const void* src, size_t bytes);
+int llmi_hip_memcpy_d2h(void* dst, const void* src_dev, size_t bytes);
+int llmi_hip_memset_dev(void* dst_dev, int value, size_t bytes);
+
+/* HIP events on `stream` (NULL = library stream), for kernel timing. */
+int llmi_hip_event_create(void** ev);
+int llmi_hip_event_destroy(void* ev);
+int llmi_hip_event_record(void* ev, void* stream);
+int llmi_hip_event_elapsed_ms(void* start, void* stop, float* ms);
+
+/* Fills dst_dev[i] = float32(mean + std * z_{offset+i}) from the deterministic
+ * "synth-v1" stream `seed` (the same values llm-inference-cpp_amd/synth.py
+ * produces on the host).  Test and benchmark input generation only. */
+int llmi_hip_synth_normal_dev(float* dst_dev, size_t n, uint64_t seed, uint64_t offset, double mean, double stdev,
+                              void* stream);
+
+/* ------------------------------------------------------- block quantizer */
+
+/* Bytes of packed codes per row: in (Q8_0) or ceil(in/2) (Q4_0)
+ * (src/model/quant.cpp:18-20). */
+size_t llmi_hip_row_bytes(size_t in, int type);
+
+/* Replaces llmi::quant::quantize (include/llmi/model/quant.hpp:51,
+ * src/model/quant.cpp:36-102), computed on the GPU.  w is the out x in
+ * row-major fp32 matrix; data (out * row_bytes) and scales
+ * (out * ceil(in/32)) receive the reference's planar layout
+ * (QuantizedMatrix::data / ::scales, quant.hpp:38-48), bit-exact. */
+int llmi_hip_quantize(const float* w, size_t out, size_t in, int type, uint8_t* data, float* scales);
+int llmi_hip_quantize_dev(const float* w_dev, size_t out, size_t in, int type, uint8_t* data_dev, float* scales_dev,
+                          void* stream);
+
+/* ------------------------------------------------ device-resident weights */
+
+/* Uploads a QuantizedMatrix (planar data + scales, as produced by
+ * quant::quantize) and re-lays it out for the GPU kernels.  Stands in for the
+ * storage of llmi::Weight (include/llmi/model/weight.hpp:18-39,
+ * src/model/weight.cpp:16-22). */
+int llmi_hip_weight_upload(const uint8_t* data, const float* scales, size_t out, size_t in, int type,
+                           llmi_hip_weight** weight);
+/* Weight::quantized (src/model/weight.cpp:16-22): quantizes an fp32 matrix on
+ * the GPU straight into the device layout.  w is a host pointer. */
+int llmi_hip_weight_quantize(const float* w, size_t out, size_t in, int type, llmi_hip_weight** weight);
+int llmi_hip_weight_quantize_dev(const float* w_dev, size_t out, size_t in, int type, llmi_hip_weight** weight);
+int llmi_hip_weight_free(llmi_hip_weight* weight);
+/* Copies the weight back into the reference's planar layout. */
+int llmi_hip_weight_download(const llmi_hip_weight* weight, uint8_t* data, float* scales);
+/* Shape/type queries; byte_size is QuantizedMatrix::byte_size
+ * (quant.hpp:47): packed code bytes + 4 * number of scales. */
+int llmi_hip_weight_info(const llmi_hip_weight* weight, size_t* out, size_t* in, int* type, size_t* byte_size);
+/* Device footprint of the re-laid-out matrix (codes + scales, with padding). */
+size_t llmi_hip_weight_device_bytes(const llmi_hip_weight* weight);
+
+/* Replaces llmi::quant::dequantize_row (quant.hpp:54, quant.cpp:104-117) and
+ * the embedding gather Weight::row (weight.cpp:39-45): dst[k] =
+ * code[row][k] * scale[row][k/32], one rounding, bit-exact. */
+int llmi_hip_dequantize_row(const llmi_hip_weight* weight, size_t row, float* dst);
+/* Gathers rows ids_dev[0..n) into dst_dev (n x in).  Ids must be in range. */
+int llmi_hip_dequantize_rows_dev(const llmi_hip_weight* weight, const int32_t* ids_dev, size_t n, float* dst_dev,
+                                 void* stream);
+
+/* Replaces llmi::quant::matmul (quant.hpp:64-65, quant.cpp:119-153) and
+ * Weight::matmul (weight.cpp:30-37): y[r*out + o] = sum_i x[r*in + i] *
+ * dequantized(w[o][i]) (+ bias[o]), for r < rows.  The arithmetic is the
+ * reference's, operation for operation (per 32-block a fused chain over the
+ * block, then a fused chain over the blocks, then + bias), so y is bit-exact.
+ * in and out must equal the weight's shape; bias may be NULL.
+ * llmi_hip_matmul takes host pointers and returns with y complete. */
+int llmi_hip_matmul(const llmi_hip_weight* weight, const float* x, size_t rows, size_t in, size_t out,
+                    const float* bias, float* y);
+int llmi_hip_matmul_dev(const llmi_hip_weight* weight, const float* x_dev, size_t rows, const float* bias_dev,
+                        float* y_dev, void* stream);
+
+#ifdef __cplusplus
+} /* extern "C" */
+#endif
+
+#endif /* LLMI_HIP_H */

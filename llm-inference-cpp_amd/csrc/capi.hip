@@ -1,0 +1,370 @@
+// The C ABI (include/llmi_hip.h): runtime state, error channel, device
+// memory helpers and the quantized-weight entry points.
+#include <cstring>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "common.hpp"
+
+namespace llmi_hip {
+
+namespace {
+thread_local std::string t_error;
+int g_device = -1;
+hipStream_t g_stream = nullptr;
+std::size_t g_max_lds = 64 * 1024;
+
+// A scoped device allocation used by the host-pointer entry points.
+struct DevBuf {
+  void* p = nullptr;
+  ~DevBuf() {
+    if (p != nullptr) (void)hipFree(p);
+  }
+  int alloc(std::size_t bytes) {
+    if (bytes == 0) return LLMI_OK;
+    LLMI_TRY_HIP(hipMalloc(&p, bytes));
+    return LLMI_OK;
+  }
+  template <typename T>
+  T* as() const {
+    return static_cast<T*>(p);
+  }
+};
+
+int check_type(int type) {
+  LLMI_REQUIRE(type == LLMI_TYPE_Q8_0 || type == LLMI_TYPE_Q4_0, "type must be LLMI_TYPE_Q8_0 or LLMI_TYPE_Q4_0");
+  return LLMI_OK;
+}
+
+// Allocates a tiled device matrix (zeroed, so padding rows/elements are 0).
+int alloc_matrix(std::size_t out, std::size_t in, int type, DeviceMatrix* m) {
+  m->type = type;
+  m->out = out;
+  m->in = in;
+  m->nblk = ceil_div(in, kBlock);
+  m->ntiles = ceil_div(out, kTileRows);
+  m->code_bytes = m->ntiles * m->nblk * kTileRows * block_code_bytes(type);
+  m->scale_bytes = m->ntiles * m->nblk * kTileRows * sizeof(float);
+  if (m->code_bytes == 0) return LLMI_OK;
+  LLMI_TRY_HIP(hipMalloc(reinterpret_cast<void**>(&m->codes), m->code_bytes));
+  const hipError_t e = hipMalloc(reinterpret_cast<void**>(&m->scales), m->scale_bytes);
+  if (e != hipSuccess) {
+    (void)hipFree(m->codes);
+    m->codes = nullptr;
+    return fail(LLMI_ERR_HIP, std::string("hipMalloc(scales): ") + hipGetErrorString(e));
+  }
+  LLMI_TRY_HIP(hipMemsetAsync(m->codes, 0, m->code_bytes, library_stream()));
+  LLMI_TRY_HIP(hipMemsetAsync(m->scales, 0, m->scale_bytes, library_stream()));
+  return LLMI_OK;
+}
+
+void free_matrix(DeviceMatrix* m) {
+  if (m->codes != nullptr) (void)hipFree(m->codes);
+  if (m->scales != nullptr) (void)hipFree(m->scales);
+  m->codes = nullptr;
+  m->scales = nullptr;
+}
+
+}  // namespace
+
+void set_error(const std::string& msg) { t_error = msg; }
+int fail(int code, const std::string& msg) {
+  t_error = msg;
+  return code;
+}
+hipStream_t library_stream() { return g_stream; }
+bool initialised() { return g_device >= 0; }
+std::size_t max_lds_per_block() { return g_max_lds; }
+
+}  // namespace llmi_hip
+
+using namespace llmi_hip;
+
+extern "C" {
+
+const char* llmi_hip_last_error(void) { return t_error.c_str(); }
+const char* llmi_hip_version(void) { return "llmi_hip 0.1 (gfx950, exact fused-chain GEMV)"; }
+
+int llmi_hip_init(int device) {
+  int count = 0;
+  LLMI_TRY_HIP(hipGetDeviceCount(&count));
+  LLMI_REQUIRE(device >= 0 && device < count, "llmi_hip_init: no such device");
+  if (g_device == device && g_stream != nullptr) return LLMI_OK;
+  LLMI_TRY_HIP(hipSetDevice(device));
+  if (g_stream != nullptr) {
+    LLMI_TRY_HIP(hipStreamDestroy(g_stream));
+    g_stream = nullptr;
+  }
+  LLMI_TRY_HIP(hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking));
+  hipDeviceProp_t prop{};
+  LLMI_TRY_HIP(hipGetDeviceProperties(&prop, device));
+  g_max_lds = prop.sharedMemPerBlock;
+  g_device = device;
+  return LLMI_OK;
+}
+
+int llmi_hip_shutdown(void) {
+  if (g_stream != nullptr) {
+    LLMI_TRY_HIP(hipStreamSynchronize(g_stream));
+    LLMI_TRY_HIP(hipStreamDestroy(g_stream));
+  }
+  g_stream = nullptr;
+  g_device = -1;
+  return LLMI_OK;
+}
+
+void* llmi_hip_stream(void) { return g_stream; }
+
+int llmi_hip_synchronize(void) {
+  LLMI_REQUIRE_INIT();
+  LLMI_TRY_HIP(hipStreamSynchronize(g_stream));
+  return LLMI_OK;
+}
+
+int llmi_hip_malloc(void** ptr, size_t bytes) {
+  LLMI_REQUIRE_INIT();
+  LLMI_REQUIRE(ptr != nullptr, "llmi_hip_malloc: null out-pointer");
+  *ptr = nullptr;
+  if (bytes == 0) return LLMI_OK;
+  LLMI_TRY_HIP(hipMalloc(ptr, bytes));
+  return LLMI_OK;
+}
+
+int llmi_hip_free(void* ptr) {
+  if (ptr != nullptr) LLMI_TRY_HIP(hipFree(ptr));
+  return LLMI_OK;
+}
+
+int llmi_hip_memcpy_h2d(void* dst, const void* src, size_t bytes) {
+  LLMI_REQUIRE_INIT();
+  if (bytes == 0) return LLMI_OK;
+  LLMI_TRY_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, g_stream));
+  LLMI_TRY_HIP(hipStreamSynchronize(g_stream));
+  return LLMI_OK;
+}
+
+int llmi_hip_memcpy_d2h(void* dst, const void* src, size_t bytes) {
+  LLMI_REQUIRE_INIT();
+  if (bytes == 0) return LLMI_OK;
+  LLMI_TRY_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, g_stream));
+  LLMI_TRY_HIP(hipStreamSynchronize(g_stream));
+  return LLMI_OK;
+}
+
+int llmi_hip_memset_dev(void* dst, int value, size_t bytes) {
+  LLMI_REQUIRE_INIT();
+  if (bytes == 0) return LLMI_OK;
+  LLMI_TRY_HIP(hipMemsetAsync(dst, value, bytes, g_stream));
+  LLMI_TRY_HIP(hipStreamSynchronize(g_stream));
+  return LLMI_OK;
+}
+
+int llmi_hip_event_create(void** ev) {
+  LLMI_REQUIRE_INIT();
+  hipEvent_t e = nullptr;
+  LLMI_TRY_HIP(hipEventCreate(&e));
+  *ev = e;
+  return LLMI_OK;
+}
+
+int llmi_hip_event_destroy(void* ev) {
+  if (ev != nullptr) LLMI_TRY_HIP(hipEventDestroy(static_cast<hipEvent_t>(ev)));
+  return LLMI_OK;
+}
+
+int llmi_hip_event_record(void* ev, void* stream) {
+  LLMI_REQUIRE_INIT();
+  LLMI_TRY_HIP(hipEventRecord(static_cast<hipEvent_t>(ev), pick(stream)));
+  return LLMI_OK;
+}
+
+int llmi_hip_event_elapsed_ms(void* start, void* stop, float* ms) {
+  LLMI_TRY_HIP(hipEventSynchronize(static_cast<hipEvent_t>(stop)));
+  LLMI_TRY_HIP(hipEventElapsedTime(ms, static_cast<hipEvent_t>(start), static_cast<hipEvent_t>(stop)));
+  return LLMI_OK;
+}
+
+int llmi_hip_synth_normal_dev(float* dst, size_t n, uint64_t seed, uint64_t offset, double mean, double stdev,
+                              void* stream) {
+  LLMI_REQUIRE_INIT();
+  return launch_synth_normal(dst, n, seed, offset, mean, stdev, pick(stream));
+}
+
+size_t llmi_hip_row_bytes(size_t in, int type) { return row_bytes(in, type); }
+
+int llmi_hip_quantize_dev(const float* w, size_t out, size_t in, int type, uint8_t* data, float* scales, void* stream) {
+  LLMI_REQUIRE_INIT();
+  if (const int rc = check_type(type)) return rc;
+  LLMI_REQUIRE(in <= 0x7FFFFFFFu, "quantize: in too large");
+  if (out == 0 || in == 0) return LLMI_OK;
+  LLMI_REQUIRE(w != nullptr && data != nullptr && scales != nullptr, "quantize: null pointer");
+  return launch_quantize(w, out, in, type, data, scales, nullptr, pick(stream));
+}
+
+int llmi_hip_quantize(const float* w, size_t out, size_t in, int type, uint8_t* data, float* scales) {
+  LLMI_REQUIRE_INIT();
+  if (const int rc = check_type(type)) return rc;
+  if (out == 0 || in == 0) return LLMI_OK;
+  LLMI_REQUIRE(w != nullptr && data != nullptr && scales != nullptr, "quantize: null pointer");
+  const std::size_t nw = out * in, nd = out * row_bytes(in, type), ns = out * ceil_div(in, kBlock);
+  DevBuf dw, dd, ds;
+  if (int rc = dw.alloc(nw * sizeof(float))) return rc;
+  if (int rc = dd.alloc(nd)) return rc;
+  if (int rc = ds.alloc(ns * sizeof(float))) return rc;
+  LLMI_TRY_HIP(hipMemcpyAsync(dw.p, w, nw * sizeof(float), hipMemcpyHostToDevice, g_stream));
+  if (int rc = launch_quantize(dw.as<float>(), out, in, type, dd.as<std::uint8_t>(), ds.as<float>(), nullptr, g_stream))
+    return rc;
+  LLMI_TRY_HIP(hipMemcpyAsync(data, dd.p, nd, hipMemcpyDeviceToHost, g_stream));
+  LLMI_TRY_HIP(hipMemcpyAsync(scales, ds.p, ns * sizeof(float), hipMemcpyDeviceToHost, g_stream));
+  LLMI_TRY_HIP(hipStreamSynchronize(g_stream));
+  return LLMI_OK;
+}
+
+int llmi_hip_weight_upload(const uint8_t* data, const float* scales, size_t out, size_t in, int type,
+                           llmi_hip_weight** weight) {
+  LLMI_REQUIRE_INIT();
+  if (const int rc = check_type(type)) return rc;
+  LLMI_REQUIRE(weight != nullptr, "weight_upload: null out-pointer");
+  LLMI_REQUIRE(in <= 0x7FFFFFFFu, "weight_upload: in too large");
+  *weight = nullptr;
+  auto h = std::make_unique<llmi_hip_weight>();
+  if (int rc = alloc_matrix(out, in, type, &h->m)) return rc;
+  const std::size_t nd = out * row_bytes(in, type), ns = out * ceil_div(in, kBlock);
+  if (nd > 0) {
+    DevBuf dd, ds;
+    int rc = dd.alloc(nd);
+    if (rc == LLMI_OK) rc = ds.alloc(ns * sizeof(float));
+    if (rc == LLMI_OK && hipMemcpyAsync(dd.p, data, nd, hipMemcpyHostToDevice, g_stream) != hipSuccess) rc = fail(LLMI_ERR_HIP, "weight_upload: copy");
+    if (rc == LLMI_OK && hipMemcpyAsync(ds.p, scales, ns * sizeof(float), hipMemcpyHostToDevice, g_stream) != hipSuccess) rc = fail(LLMI_ERR_HIP, "weight_upload: copy");
+    if (rc == LLMI_OK) rc = launch_relayout_to_tiled(dd.as<std::uint8_t>(), ds.as<float>(), h->m, g_stream);
+    if (rc == LLMI_OK && hipStreamSynchronize(g_stream) != hipSuccess) rc = fail(LLMI_ERR_HIP, "weight_upload: sync");
+    if (rc != LLMI_OK) {
+      free_matrix(&h->m);
+      return rc;
+    }
+  }
+  *weight = h.release();
+  return LLMI_OK;
+}
+
+int llmi_hip_weight_quantize_dev(const float* w, size_t out, size_t in, int type, llmi_hip_weight** weight) {
+  LLMI_REQUIRE_INIT();
+  if (const int rc = check_type(type)) return rc;
+  LLMI_REQUIRE(weight != nullptr, "weight_quantize: null out-pointer");
+  LLMI_REQUIRE(in <= 0x7FFFFFFFu, "weight_quantize: in too large");
+  *weight = nullptr;
+  auto h = std::make_unique<llmi_hip_weight>();
+  if (int rc = alloc_matrix(out, in, type, &h->m)) return rc;
+  if (out > 0 && in > 0) {
+    int rc = launch_quantize(w, out, in, type, nullptr, nullptr, &h->m, g_stream);
+    if (rc == LLMI_OK && hipStreamSynchronize(g_stream) != hipSuccess) rc = fail(LLMI_ERR_HIP, "weight_quantize: sync");
+    if (rc != LLMI_OK) {
+      free_matrix(&h->m);
+      return rc;
+    }
+  }
+  *weight = h.release();
+  return LLMI_OK;
+}
+
+int llmi_hip_weight_quantize(const float* w, size_t out, size_t in, int type, llmi_hip_weight** weight) {
+  LLMI_REQUIRE_INIT();
+  if (const int rc = check_type(type)) return rc;
+  DevBuf dw;
+  if (int rc = dw.alloc(out * in * sizeof(float))) return rc;
+  if (out * in > 0) LLMI_TRY_HIP(hipMemcpyAsync(dw.p, w, out * in * sizeof(float), hipMemcpyHostToDevice, g_stream));
+  return llmi_hip_weight_quantize_dev(dw.as<float>(), out, in, type, weight);
+}
+
+int llmi_hip_weight_free(llmi_hip_weight* weight) {
+  if (weight == nullptr) return LLMI_OK;
+  if (g_stream != nullptr) (void)hipStreamSynchronize(g_stream);
+  free_matrix(&weight->m);
+  delete weight;
+  return LLMI_OK;
+}
+
+int llmi_hip_weight_download(const llmi_hip_weight* weight, uint8_t* data, float* scales) {
+  LLMI_REQUIRE_INIT();
+  LLMI_REQUIRE(weight != nullptr, "weight_download: null weight");
+  const DeviceMatrix& m = weight->m;
+  const std::size_t nd = m.out * row_bytes(m.in, m.type), ns = m.out * m.nblk;
+  if (nd == 0) return LLMI_OK;
+  DevBuf dd, ds;
+  if (int rc = dd.alloc(nd)) return rc;
+  if (int rc = ds.alloc(ns * sizeof(float))) return rc;
+  LLMI_TRY_HIP(hipMemsetAsync(dd.p, 0, nd, g_stream));
+  if (int rc = launch_relayout_to_planar(m, dd.as<std::uint8_t>(), ds.as<float>(), g_stream)) return rc;
+  LLMI_TRY_HIP(hipMemcpyAsync(data, dd.p, nd, hipMemcpyDeviceToHost, g_stream));
+  LLMI_TRY_HIP(hipMemcpyAsync(scales, ds.p, ns * sizeof(float), hipMemcpyDeviceToHost, g_stream));
+  LLMI_TRY_HIP(hipStreamSynchronize(g_stream));
+  return LLMI_OK;
+}
+
+int llmi_hip_weight_info(const llmi_hip_weight* weight, size_t* out, size_t* in, int* type, size_t* byte_size) {
+  LLMI_REQUIRE(weight != nullptr, "weight_info: null weight");
+  const DeviceMatrix& m = weight->m;
+  if (out != nullptr) *out = m.out;
+  if (in != nullptr) *in = m.in;
+  if (type != nullptr) *type = m.type;
+  if (byte_size != nullptr) *byte_size = m.out * row_bytes(m.in, m.type) + m.out * m.nblk * sizeof(float);
+  return LLMI_OK;
+}
+
+size_t llmi_hip_weight_device_bytes(const llmi_hip_weight* weight) {
+  return weight == nullptr ? 0 : weight->m.code_bytes + weight->m.scale_bytes;
+}
+
+int llmi_hip_dequantize_rows_dev(const llmi_hip_weight* weight, const int32_t* ids, size_t n, float* dst, void* stream) {
+  LLMI_REQUIRE_INIT();
+  LLMI_REQUIRE(weight != nullptr, "dequantize_rows: null weight");
+  return launch_dequantize_rows(weight->m, ids, n, dst, pick(stream));
+}
+
+int llmi_hip_dequantize_row(const llmi_hip_weight* weight, size_t row, float* dst) {
+  LLMI_REQUIRE_INIT();
+  LLMI_REQUIRE(weight != nullptr, "dequantize_row: null weight");
+  const DeviceMatrix& m = weight->m;
+  LLMI_REQUIRE(row < m.out, "dequantize_row: row out of range");
+  if (m.in == 0) return LLMI_OK;
+  DevBuf did, dd;
+  if (int rc = did.alloc(sizeof(std::int32_t))) return rc;
+  if (int rc = dd.alloc(m.in * sizeof(float))) return rc;
+  const std::int32_t id = static_cast<std::int32_t>(row);
+  LLMI_TRY_HIP(hipMemcpyAsync(did.p, &id, sizeof(id), hipMemcpyHostToDevice, g_stream));
+  if (int rc = launch_dequantize_rows(m, did.as<std::int32_t>(), 1, dd.as<float>(), g_stream)) return rc;
+  LLMI_TRY_HIP(hipMemcpyAsync(dst, dd.p, m.in * sizeof(float), hipMemcpyDeviceToHost, g_stream));
+  LLMI_TRY_HIP(hipStreamSynchronize(g_stream));
+  return LLMI_OK;
+}
+
+int llmi_hip_matmul_dev(const llmi_hip_weight* weight, const float* x, size_t rows, const float* bias, float* y,
+                        void* stream) {
+  LLMI_REQUIRE_INIT();
+  LLMI_REQUIRE(weight != nullptr, "matmul: null weight");
+  return launch_matmul(weight->m, x, rows, bias, y, pick(stream));
+}
+
+int llmi_hip_matmul(const llmi_hip_weight* weight, const float* x, size_t rows, size_t in, size_t out,
+                    const float* bias, float* y) {
+  LLMI_REQUIRE_INIT();
+  LLMI_REQUIRE(weight != nullptr, "matmul: null weight");
+  const DeviceMatrix& m = weight->m;
+  LLMI_REQUIRE(in == m.in && out == m.out, "matmul: in/out do not match the weight's shape");
+  if (rows == 0 || out == 0) return LLMI_OK;
+  DevBuf dx, db, dy;
+  if (int rc = dx.alloc(rows * in * sizeof(float))) return rc;
+  if (int rc = dy.alloc(rows * out * sizeof(float))) return rc;
+  if (bias != nullptr) {
+    if (int rc = db.alloc(out * sizeof(float))) return rc;
+    LLMI_TRY_HIP(hipMemcpyAsync(db.p, bias, out * sizeof(float), hipMemcpyHostToDevice, g_stream));
+  }
+  LLMI_TRY_HIP(hipMemcpyAsync(dx.p, x, rows * in * sizeof(float), hipMemcpyHostToDevice, g_stream));
+  if (int rc = launch_matmul(m, dx.as<float>(), rows, db.as<float>(), dy.as<float>(), g_stream)) return rc;
+  LLMI_TRY_HIP(hipMemcpyAsync(y, dy.p, rows * out * sizeof(float), hipMemcpyDeviceToHost, g_stream));
+  LLMI_TRY_HIP(hipStreamSynchronize(g_stream));
+  return LLMI_OK;
+}
+
+}  // extern "C"

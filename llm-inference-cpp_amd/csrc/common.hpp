@@ -1,0 +1,84 @@
+// Shared definitions of the gfx950 quantized-weight library: error channel,
+// the device weight layout, and launch helpers.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <string>
+
+#include "../../include/llmi_hip.h"
+
+namespace llmi_hip {
+
+constexpr int kBlock = LLMI_BLOCK_SIZE;  // weights per quantization block
+constexpr int kTileRows = 64;            // output rows per wavefront tile (one row per lane)
+
+// Thread-local last error (llmi_hip_last_error).
+void set_error(const std::string& msg);
+int fail(int code, const std::string& msg);
+
+hipStream_t library_stream();
+bool initialised();
+std::size_t max_lds_per_block();  // bytes of LDS one workgroup may allocate
+inline hipStream_t pick(void* s) { return s != nullptr ? static_cast<hipStream_t>(s) : library_stream(); }
+
+#define LLMI_TRY_HIP(expr)                                                                        \
+  do {                                                                                            \
+    const hipError_t err_ = (expr);                                                               \
+    if (err_ != hipSuccess) return ::llmi_hip::fail(LLMI_ERR_HIP, std::string(#expr) + ": " + hipGetErrorString(err_)); \
+  } while (0)
+
+#define LLMI_REQUIRE(cond, msg)                                   \
+  do {                                                            \
+    if (!(cond)) return ::llmi_hip::fail(LLMI_ERR_ARG, (msg));    \
+  } while (0)
+
+#define LLMI_REQUIRE_INIT()                                                                   \
+  do {                                                                                        \
+    if (!::llmi_hip::initialised()) return ::llmi_hip::fail(LLMI_ERR_STATE, "llmi_hip_init has not been called"); \
+  } while (0)
+
+inline std::size_t ceil_div(std::size_t a, std::size_t b) { return (a + b - 1) / b; }
+inline std::size_t row_bytes(std::size_t in, int type) { return type == LLMI_TYPE_Q4_0 ? (in + 1) / 2 : in; }
+
+// Device layout of a packed matrix ("tiled"): rows are grouped in tiles of 64
+// (lane l of a wavefront owns row tile*64 + l).  For each tile and each
+// 32-weight block b the 64 rows' codes sit next to each other, so one
+// wavefront reads a block of 64 rows with fully coalesced 16-byte loads:
+//   Q4_0: codes[((tile*nblk + b)*64 + lane)*16 + j], j = 0..15, holding the
+//         block's elements in the reference's nibble order (element 2j in the
+//         low nibble of byte j, 2j+1 in the high nibble, +8 bias).
+//   Q8_0: codes[(((tile*nblk + b)*2 + h)*64 + lane)*16 + j] = int8 code of
+//         element 16h + j of the block.
+//   scales[(tile*nblk + b)*64 + lane] = the block's fp32 scale.
+// Rows past `out` in the last tile and elements past `in` in the last block
+// are zero bytes.  A block is 16 (Q4_0) or 32 (Q8_0) code bytes plus 4 scale
+// bytes, the reference's 0.625 / 1.125 bytes per weight.
+struct DeviceMatrix {
+  int type = 0;
+  std::size_t out = 0, in = 0, nblk = 0, ntiles = 0;
+  std::uint8_t* codes = nullptr;
+  float* scales = nullptr;
+  std::size_t code_bytes = 0, scale_bytes = 0;
+};
+
+inline std::size_t block_code_bytes(int type) { return type == LLMI_TYPE_Q4_0 ? 16 : 32; }
+
+// Kernel launchers (implemented next to their kernels).
+int launch_quantize(const float* w, std::size_t out, std::size_t in, int type, std::uint8_t* planar_data,
+                    float* planar_scales, DeviceMatrix* tiled, hipStream_t s);
+int launch_relayout_to_tiled(const std::uint8_t* planar_data, const float* planar_scales, const DeviceMatrix& m,
+                             hipStream_t s);
+int launch_relayout_to_planar(const DeviceMatrix& m, std::uint8_t* planar_data, float* planar_scales, hipStream_t s);
+int launch_dequantize_rows(const DeviceMatrix& m, const std::int32_t* ids, std::size_t n, float* dst, hipStream_t s);
+int launch_matmul(const DeviceMatrix& m, const float* x, std::size_t rows, const float* bias, float* y, hipStream_t s);
+int launch_synth_normal(float* dst, std::size_t n, std::uint64_t seed, std::uint64_t offset, double mean, double stdev,
+                        hipStream_t s);
+
+}  // namespace llmi_hip
+
+struct llmi_hip_weight {
+  llmi_hip::DeviceMatrix m;
+};

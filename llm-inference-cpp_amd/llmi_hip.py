@@ -1,0 +1,262 @@
+"""ctypes binding of libllmi_hip.so (include/llmi_hip.h) for Python callers:
+the tests, bench.py and __graft_entry__.smoke().
+
+The product is the shared library; this module only declares the C
+signatures and adds numpy conveniences.  It never falls back to another
+implementation: if the library is missing or a call fails, it raises.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libllmi_hip.so")
+
+F32, Q8_0, Q4_0 = 0, 1, 2
+BLOCK = 32
+TYPE_NAMES = {F32: "f32", Q8_0: "q8_0", Q4_0: "q4_0"}
+
+# Every symbol include/llmi_hip.h declares, with (restype, argtypes).
+_sz, _vp, _i, _f, _d, _u64 = C.c_size_t, C.c_void_p, C.c_int, C.c_float, C.c_double, C.c_uint64
+SIGNATURES = {
+    "llmi_hip_init": (_i, [_i]),
+    "llmi_hip_shutdown": (_i, []),
+    "llmi_hip_last_error": (C.c_char_p, []),
+    "llmi_hip_version": (C.c_char_p, []),
+    "llmi_hip_stream": (_vp, []),
+    "llmi_hip_synchronize": (_i, []),
+    "llmi_hip_malloc": (_i, [C.POINTER(_vp), _sz]),
+    "llmi_hip_free": (_i, [_vp]),
+    "llmi_hip_memcpy_h2d": (_i, [_vp, _vp, _sz]),
+    "llmi_hip_memcpy_d2h": (_i, [_vp, _vp, _sz]),
+    "llmi_hip_memset_dev": (_i, [_vp, _i, _sz]),
+    "llmi_hip_event_create": (_i, [C.POINTER(_vp)]),
+    "llmi_hip_event_destroy": (_i, [_vp]),
+    "llmi_hip_event_record": (_i, [_vp, _vp]),
+    "llmi_hip_event_elapsed_ms": (_i, [_vp, _vp, C.POINTER(_f)]),
+    "llmi_hip_synth_normal_dev": (_i, [_vp, _sz, _u64, _u64, _d, _d, _vp]),
+    "llmi_hip_row_bytes": (_sz, [_sz, _i]),
+    "llmi_hip_quantize": (_i, [_vp, _sz, _sz, _i, _vp, _vp]),
+    "llmi_hip_quantize_dev": (_i, [_vp, _sz, _sz, _i, _vp, _vp, _vp]),
+    "llmi_hip_weight_upload": (_i, [_vp, _vp, _sz, _sz, _i, C.POINTER(_vp)]),
+    "llmi_hip_weight_quantize": (_i, [_vp, _sz, _sz, _i, C.POINTER(_vp)]),
+    "llmi_hip_weight_quantize_dev": (_i, [_vp, _sz, _sz, _i, C.POINTER(_vp)]),
+    "llmi_hip_weight_free": (_i, [_vp]),
+    "llmi_hip_weight_download": (_i, [_vp, _vp, _vp]),
+    "llmi_hip_weight_info": (_i, [_vp, C.POINTER(_sz), C.POINTER(_sz), C.POINTER(_i), C.POINTER(_sz)]),
+    "llmi_hip_weight_device_bytes": (_sz, [_vp]),
+    "llmi_hip_dequantize_row": (_i, [_vp, _sz, _vp]),
+    "llmi_hip_dequantize_rows_dev": (_i, [_vp, _vp, _sz, _vp, _vp]),
+    "llmi_hip_matmul": (_i, [_vp, _vp, _sz, _sz, _sz, _vp, _vp]),
+    "llmi_hip_matmul_dev": (_i, [_vp, _vp, _sz, _vp, _vp, _vp]),
+}
+
+
+class HipError(RuntimeError):
+    pass
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data_as(C.c_void_p)
+
+
+def row_bytes(n_in: int, qtype: int) -> int:
+    return (n_in + 1) // 2 if qtype == Q4_0 else n_in
+
+
+def nblocks(n_in: int) -> int:
+    return (n_in + BLOCK - 1) // BLOCK
+
+
+_lib = None
+
+
+def load(path: str = LIB_PATH) -> C.CDLL:
+    """Loads the library and declares its signatures (no GPU call)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(path):
+            raise FileNotFoundError(f"{path} is not built; run __graft_entry__.build()")
+        lib = C.CDLL(path)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = lib
+    return _lib
+
+
+def check(rc: int) -> None:
+    if rc != 0:
+        raise HipError(f"llmi_hip error {rc}: {load().llmi_hip_last_error().decode()}")
+
+
+_initialised = False
+
+
+def init(device: int = 0) -> C.CDLL:
+    global _initialised
+    lib = load()
+    if not _initialised:
+        check(lib.llmi_hip_init(device))
+        _initialised = True
+    return lib
+
+
+class DeviceBuffer:
+    """A plain device allocation owned by Python."""
+
+    def __init__(self, nbytes: int):
+        self.lib = init()
+        self.nbytes = int(nbytes)
+        p = C.c_void_p()
+        check(self.lib.llmi_hip_malloc(C.byref(p), self.nbytes))
+        self.ptr = p.value
+
+    @classmethod
+    def from_array(cls, a: np.ndarray) -> "DeviceBuffer":
+        a = np.ascontiguousarray(a)
+        b = cls(a.nbytes)
+        b.upload(a)
+        return b
+
+    def upload(self, a: np.ndarray) -> None:
+        a = np.ascontiguousarray(a)
+        assert a.nbytes <= self.nbytes
+        check(self.lib.llmi_hip_memcpy_h2d(self.ptr, _p(a), a.nbytes))
+
+    def download(self, dtype, count: int | None = None) -> np.ndarray:
+        dtype = np.dtype(dtype)
+        n = self.nbytes // dtype.itemsize if count is None else count
+        out = np.empty(n, dtype=dtype)
+        check(self.lib.llmi_hip_memcpy_d2h(_p(out), self.ptr, out.nbytes))
+        return out
+
+    def free(self) -> None:
+        if self.ptr:
+            check(self.lib.llmi_hip_free(self.ptr))
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class Weight:
+    """A device-resident packed matrix (llmi_hip_weight)."""
+
+    def __init__(self, handle: int, lib):
+        self.h = handle
+        self.lib = lib
+        out, n_in, qt, bs = _sz(), _sz(), _i(), _sz()
+        check(lib.llmi_hip_weight_info(self.h, C.byref(out), C.byref(n_in), C.byref(qt), C.byref(bs)))
+        self.out, self.n_in, self.qtype, self.byte_size = out.value, n_in.value, qt.value, bs.value
+
+    @classmethod
+    def upload(cls, data: np.ndarray, scales: np.ndarray, out: int, n_in: int, qtype: int) -> "Weight":
+        lib = init()
+        h = C.c_void_p()
+        check(lib.llmi_hip_weight_upload(_p(np.ascontiguousarray(data)), _p(np.ascontiguousarray(scales)), out, n_in,
+                                         qtype, C.byref(h)))
+        return cls(h.value, lib)
+
+    @classmethod
+    def quantize(cls, w: np.ndarray, out: int, n_in: int, qtype: int) -> "Weight":
+        lib = init()
+        h = C.c_void_p()
+        check(lib.llmi_hip_weight_quantize(_p(np.ascontiguousarray(w, dtype=np.float32)), out, n_in, qtype, C.byref(h)))
+        return cls(h.value, lib)
+
+    @classmethod
+    def quantize_dev(cls, w_dev: int, out: int, n_in: int, qtype: int) -> "Weight":
+        lib = init()
+        h = C.c_void_p()
+        check(lib.llmi_hip_weight_quantize_dev(w_dev, out, n_in, qtype, C.byref(h)))
+        return cls(h.value, lib)
+
+    def download(self):
+        data = np.zeros(self.out * row_bytes(self.n_in, self.qtype), dtype=np.uint8)
+        scales = np.zeros(self.out * nblocks(self.n_in), dtype=np.float32)
+        check(self.lib.llmi_hip_weight_download(self.h, _p(data), _p(scales)))
+        return data, scales
+
+    def device_bytes(self) -> int:
+        return int(self.lib.llmi_hip_weight_device_bytes(self.h))
+
+    def dequantize_row(self, row: int) -> np.ndarray:
+        dst = np.zeros(self.n_in, dtype=np.float32)
+        check(self.lib.llmi_hip_dequantize_row(self.h, row, _p(dst)))
+        return dst
+
+    def matmul(self, x: np.ndarray, rows: int, bias: np.ndarray | None = None) -> np.ndarray:
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        y = np.zeros(rows * self.out, dtype=np.float32)
+        b = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
+        check(self.lib.llmi_hip_matmul(self.h, _p(x), rows, self.n_in, self.out, _p(b), _p(y)))
+        return y
+
+    def matmul_dev(self, x_dev: int, rows: int, bias_dev: int | None, y_dev: int, stream=None) -> None:
+        check(self.lib.llmi_hip_matmul_dev(self.h, x_dev, rows, bias_dev, y_dev, stream))
+
+    def free(self) -> None:
+        if self.h:
+            check(self.lib.llmi_hip_weight_free(self.h))
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+def quantize(w: np.ndarray, out: int, n_in: int, qtype: int):
+    """llmi_hip_quantize: planar (reference-layout) packed data and scales."""
+    lib = init()
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    data = np.zeros(out * row_bytes(n_in, qtype), dtype=np.uint8)
+    scales = np.zeros(out * nblocks(n_in), dtype=np.float32)
+    check(lib.llmi_hip_quantize(_p(w), out, n_in, qtype, _p(data), _p(scales)))
+    return data, scales
+
+
+def synth_normal_dev(buf: DeviceBuffer, n: int, seed: int, mean: float, std: float, offset: int = 0) -> None:
+    lib = init()
+    check(lib.llmi_hip_synth_normal_dev(buf.ptr, n, seed, offset, mean, std, None))
+
+
+class Timer:
+    """HIP events on the library stream."""
+
+    def __init__(self):
+        self.lib = init()
+        a, b = C.c_void_p(), C.c_void_p()
+        check(self.lib.llmi_hip_event_create(C.byref(a)))
+        check(self.lib.llmi_hip_event_create(C.byref(b)))
+        self.start_ev, self.stop_ev = a.value, b.value
+
+    def start(self):
+        check(self.lib.llmi_hip_event_record(self.start_ev, None))
+
+    def stop(self) -> float:
+        check(self.lib.llmi_hip_event_record(self.stop_ev, None))
+        ms = C.c_float()
+        check(self.lib.llmi_hip_event_elapsed_ms(self.start_ev, self.stop_ev, C.byref(ms)))
+        return ms.value
+
+    def __del__(self):
+        try:
+            self.lib.llmi_hip_event_destroy(self.start_ev)
+            self.lib.llmi_hip_event_destroy(self.stop_ev)
+        except Exception:
+            pass
+
+
+def synchronize() -> None:
+    check(init().llmi_hip_synchronize())

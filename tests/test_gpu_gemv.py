@@ -1,0 +1,90 @@
+"""GPU parity of the quantized matmul (decode GEMV, small batches and the
+exact multi-row path): bit-exact against the compiled reference's golden
+outputs and the oracle."""
+
+import hashlib
+
+import numpy as np
+import pytest
+
+import llmi_hip as H
+import oracle as O
+import synth
+
+pytestmark = pytest.mark.gpu
+
+
+def sha(a):
+    return hashlib.sha256(np.ascontiguousarray(a).tobytes()).hexdigest()
+
+
+def bits(a):
+    return np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
+
+
+def test_small_cases_match_reference(golden):
+    rec, arrays = golden
+    g = arrays["quant_small"]
+    for c in rec["quant_small"]:
+        k, qt, out, n_in, rows = c["key"], c["type"], c["out"], c["n_in"], c["rows"]
+        x = synth.normal(c["x_seed"], rows * n_in, 0.0, 1.0)
+        bias = synth.normal(c["bias_seed"], out, 0.0, 1.0)
+        dev = H.Weight.upload(g[k + "_data"], g[k + "_scales"], out, n_in, qt)
+        assert np.array_equal(bits(dev.matmul(x, rows, bias)), bits(g[k + "_y"])), k
+        assert np.array_equal(bits(dev.matmul(x, rows, None)), bits(g[k + "_ynb"])), k
+        for r in range(rows):  # batch-1 kernel on each row
+            y1 = dev.matmul(x[r * n_in:(r + 1) * n_in], 1, bias)
+            assert np.array_equal(bits(y1), bits(g[k + "_y"][r * out:(r + 1) * out])), (k, r)
+
+
+def test_baseline_shapes_match_reference(golden):
+    """C1 (Q8_0 1536x576 b1), every C2 SmolLM2 shape in Q4_0 at b1 and b8,
+    and the Qwen2.5-0.5B shapes (incl. the 151936x896 lm_head)."""
+    rec, _ = golden
+    for c in rec["shapes"]:
+        out, n_in, qt = c["out"], c["n_in"], c["type"]
+        buf = H.DeviceBuffer(out * n_in * 4)
+        H.synth_normal_dev(buf, out * n_in, c["w_seed"], 0.0, c["w_std"])
+        w = H.Weight.quantize_dev(buf.ptr, out, n_in, qt)
+        buf.free()
+        for b, yrec in c["y"].items():
+            x = synth.normal(c["x_seed"], int(b) * n_in, 0.0, 1.0)
+            y = w.matmul(x, int(b))
+            assert sha(y) == yrec["sha256"], (c["name"], qt, b, float(np.max(np.abs(y))), yrec["max_abs"])
+        w.free()
+
+
+@pytest.mark.parametrize("qt", [O.Q8_0, O.Q4_0])
+@pytest.mark.parametrize("rows", [1, 2, 3, 4, 5, 7, 8, 9, 17, 64])
+@pytest.mark.parametrize("out,n_in", [(1, 1), (63, 33), (65, 100), (200, 576), (130, 4864), (96, 8192)])
+def test_batches_and_ragged_shapes_match_oracle(qt, rows, out, n_in):
+    orc = O.oracle()
+    w = synth.normal(out * 7 + n_in, out * n_in, 0.0, 0.02)
+    x = synth.normal(rows * 13 + n_in, rows * n_in, 0.0, 1.0)
+    bias = synth.normal(5, out, 0.0, 0.5)
+    data, scales = orc.quantize(w, out, n_in, qt)
+    dev = H.Weight.upload(data, scales, out, n_in, qt)
+    for b in (bias, None):
+        got = dev.matmul(x, rows, b)
+        want = orc.matmul(x, rows, n_in, data, scales, qt, out, b)
+        assert np.array_equal(bits(got), bits(want)), (rows, out, n_in, b is None)
+
+
+def test_device_pointer_entry_point_and_determinism():
+    orc = O.oracle()
+    out, n_in, qt = 4864, 896, O.Q4_0
+    w = synth.normal(1, out * n_in, 0.0, 0.02)
+    data, scales = orc.quantize(w, out, n_in, qt)
+    dev = H.Weight.upload(data, scales, out, n_in, qt)
+    x = synth.normal(2, n_in, 0.0, 1.0)
+    xd = H.DeviceBuffer.from_array(x)
+    yd = H.DeviceBuffer(out * 4)
+    first = None
+    for _ in range(3):
+        dev.matmul_dev(xd.ptr, 1, None, yd.ptr)
+        H.synchronize()
+        y = yd.download(np.float32)
+        if first is None:
+            first = y
+        assert np.array_equal(bits(y), bits(first))
+    assert np.array_equal(bits(first), bits(orc.matmul(x, 1, n_in, data, scales, qt, out, None)))
