@@ -89,6 +89,16 @@ int llmi_hip_event_destroy(void* ev);
 int llmi_hip_event_record(void* ev, void* stream);
 int llmi_hip_event_elapsed_ms(void* start, void* stop, float* ms);
 
+/* Captures the work queued on the library stream between begin and end into
+ * a HIP graph (hipStreamBeginCapture / hipGraphInstantiate), for callers
+ * that replay a fixed sequence of _dev calls (a decode step, a benchmark
+ * pass) without per-launch host overhead.  Only _dev entry points may be
+ * called while capturing; the captured kernels allocate and clear nothing. */
+int llmi_hip_graph_begin(void);
+int llmi_hip_graph_end(void** graph);
+int llmi_hip_graph_launch(void* graph);
+int llmi_hip_graph_destroy(void* graph);
+
 /* Fills dst_dev[i] = float32(mean + std * z_{offset+i}) from the deterministic
  * "synth-v1" stream `seed` (the same values llm-inference-cpp_amd/synth.py
  * produces on the host).  Test and benchmark input generation only. */
@@ -150,6 +160,67 @@ int llmi_hip_matmul(const llmi_hip_weight* weight, const float* x, size_t rows, 
                     const float* bias, float* y);
 int llmi_hip_matmul_dev(const llmi_hip_weight* weight, const float* x_dev, size_t rows, const float* bias_dev,
                         float* y_dev, void* stream);
+
+/* ------------------------------------------------- glue kernels (device) */
+/* Device counterparts of llmi::kernels (include/llmi/model/kernels.hpp:13-32)
+ * and llmi::argmax (transformer.hpp:120), bit-identical to the reference.
+ * All pointers are device pointers. */
+
+/* kernels::dot (kernels.cpp:41-95, the AVX2 build's summation order):
+ * out[i] = dot(a, b, lens[i]) for i < count. */
+int llmi_hip_dot_dev(const float* a, const float* b, const int32_t* lens, size_t count, float* out, void* stream);
+/* kernels::rmsnorm (kernels.cpp:115-120) on each of `rows` rows of length n. */
+int llmi_hip_rmsnorm_dev(const float* x, const float* w, size_t rows, size_t n, float eps, float* y, void* stream);
+/* kernels::softmax (kernels.cpp:136-146), in place on each row. */
+int llmi_hip_softmax_dev(float* x, size_t rows, size_t n, void* stream);
+/* kernels::silu (kernels.cpp:148), in place. */
+int llmi_hip_silu_dev(float* x, size_t n, void* stream);
+/* argmax (transformer.cpp:22-24): index of the first maximum of x[0..n). */
+int llmi_hip_argmax_dev(const float* x, size_t n, int32_t* out, void* stream);
+
+/* ------------------------------------------------------------- the model */
+
+typedef struct llmi_hip_model llmi_hip_model; /* device-resident quantized decoder */
+typedef struct llmi_hip_cache llmi_hip_cache; /* device KV cache of one sequence */
+
+/* Replaces llmi::Transformer::load(model, Q8_0 | Q4_0)
+ * (include/llmi/model/transformer.hpp:58, src/model/transformer.cpp:26-67):
+ * quantizes every matrix (embedding, q/k/v/o, gate/up/down, untied lm_head)
+ * on the GPU; RMSNorm weights and q/k/v biases stay fp32.  `tensors` holds
+ * one fp32 array per tensor in the reference's expected_tensors() order
+ * (src/model/model.cpp:135-162): embed; per layer input_layernorm, q, k, v,
+ * [q_bias, k_bias, v_bias], o, post_attention_layernorm, gate, up, down;
+ * final norm; [lm_head when untied].  _dev: the arrays are device pointers. */
+int llmi_hip_model_create(const llmi_model_config* cfg, const float* const* tensors, int type, llmi_hip_model** model);
+int llmi_hip_model_create_dev(const llmi_model_config* cfg, const float* const* tensors_dev, int type,
+                              llmi_hip_model** model);
+int llmi_hip_model_free(llmi_hip_model* model);
+/* Transformer::weight_bytes (transformer.cpp:69-76). */
+size_t llmi_hip_model_weight_bytes(const llmi_hip_model* model);
+
+/* Transformer::new_cache (transformer.cpp:182-190): capacity
+ * min(max_len, max_position_embeddings) positions, head-major fp32 K/V. */
+int llmi_hip_model_new_cache(llmi_hip_model* model, size_t max_len, llmi_hip_cache** cache);
+int llmi_hip_cache_free(llmi_hip_cache* cache);
+/* KVCache::length / capacity / reset (transformer.hpp:29-45). */
+size_t llmi_hip_cache_length(const llmi_hip_cache* cache);
+size_t llmi_hip_cache_capacity(const llmi_hip_cache* cache);
+int llmi_hip_cache_reset(llmi_hip_cache* cache);
+
+/* Transformer::forward_cached (transformer.cpp:192-306): runs `n` new tokens
+ * through the model, appends their K/V to `cache`, and writes the logits of
+ * the last token (vocab floats) or of every new token (n x vocab) when
+ * all_positions is set.  Bit-identical to the reference's logits.  Errors
+ * (no tokens, id out of range, cache full or from another model) carry the
+ * reference's messages. */
+int llmi_hip_model_forward_cached(llmi_hip_model* model, llmi_hip_cache* cache, const int32_t* tokens, size_t n,
+                                  int all_positions, float* logits);
+
+/* Transformer::generate_greedy_cached (transformer.cpp:308-327): prefill,
+ * then up to max_new greedy tokens (first maximum), stopping after a token in
+ * stop_ids.  Writes *n_ids ids to `ids` (room for max_new). */
+int llmi_hip_model_generate_greedy(llmi_hip_model* model, const int32_t* prompt, size_t n, size_t max_new,
+                                   const int32_t* stop_ids, size_t n_stop, int32_t* ids, size_t* n_ids);
 
 #ifdef __cplusplus
 } /* extern "C" */

@@ -185,6 +185,37 @@ int llmi_hip_event_elapsed_ms(void* start, void* stop, float* ms) {
   return LLMI_OK;
 }
 
+int llmi_hip_graph_begin(void) {
+  LLMI_REQUIRE_INIT();
+  LLMI_TRY_HIP(hipStreamBeginCapture(g_stream, hipStreamCaptureModeThreadLocal));
+  return LLMI_OK;
+}
+
+int llmi_hip_graph_end(void** graph) {
+  LLMI_REQUIRE_INIT();
+  LLMI_REQUIRE(graph != nullptr, "graph_end: null out-pointer");
+  hipGraph_t g = nullptr;
+  LLMI_TRY_HIP(hipStreamEndCapture(g_stream, &g));
+  hipGraphExec_t exec = nullptr;
+  const hipError_t e = hipGraphInstantiate(&exec, g, nullptr, nullptr, 0);
+  (void)hipGraphDestroy(g);
+  if (e != hipSuccess) return fail(LLMI_ERR_HIP, std::string("hipGraphInstantiate: ") + hipGetErrorString(e));
+  *graph = exec;
+  return LLMI_OK;
+}
+
+int llmi_hip_graph_launch(void* graph) {
+  LLMI_REQUIRE_INIT();
+  LLMI_REQUIRE(graph != nullptr, "graph_launch: null graph");
+  LLMI_TRY_HIP(hipGraphLaunch(static_cast<hipGraphExec_t>(graph), g_stream));
+  return LLMI_OK;
+}
+
+int llmi_hip_graph_destroy(void* graph) {
+  if (graph != nullptr) LLMI_TRY_HIP(hipGraphExecDestroy(static_cast<hipGraphExec_t>(graph)));
+  return LLMI_OK;
+}
+
 int llmi_hip_synth_normal_dev(float* dst, size_t n, uint64_t seed, uint64_t offset, double mean, double stdev,
                               void* stream) {
   LLMI_REQUIRE_INIT();

@@ -73,7 +73,11 @@ int launch_relayout_to_tiled(const std::uint8_t* planar_data, const float* plana
                              hipStream_t s);
 int launch_relayout_to_planar(const DeviceMatrix& m, std::uint8_t* planar_data, float* planar_scales, hipStream_t s);
 int launch_dequantize_rows(const DeviceMatrix& m, const std::int32_t* ids, std::size_t n, float* dst, hipStream_t s);
-int launch_matmul(const DeviceMatrix& m, const float* x, std::size_t rows, const float* bias, float* y, hipStream_t s);
+// accumulate: y[r][o] = y[r][o] + (acc + bias) -- the reference's
+// `proj = W x; x += proj` residual update (transformer.cpp:283-284, :291-292)
+// done in the GEMV's epilogue with the same two roundings.
+int launch_matmul(const DeviceMatrix& m, const float* x, std::size_t rows, const float* bias, float* y, hipStream_t s,
+                  bool accumulate = false);
 int launch_synth_normal(float* dst, std::size_t n, std::uint64_t seed, std::uint64_t offset, double mean, double stdev,
                         hipStream_t s);
 

@@ -100,7 +100,8 @@ __device__ __noinline__ float tail_block_dot(const Block<TYPE> blk, const float*
 template <int TYPE, int CH>
 __global__ void __launch_bounds__(1024) qgemv_r1(const uint4* __restrict__ codes, const float* __restrict__ scales,
                                                  const float* __restrict__ x, const float* __restrict__ bias,
-                                                 float* __restrict__ y, int in, int nblk, int out, int bpw) {
+                                                 float* __restrict__ y, int in, int nblk, int out, int bpw,
+                                                 int accumulate) {
   extern __shared__ float lds[];
   float* part = lds;
   float* scl = lds + static_cast<std::size_t>(nblk) * kTileRows;
@@ -170,7 +171,10 @@ __global__ void __launch_bounds__(1024) qgemv_r1(const uint4* __restrict__ codes
     }
     for (; b < nblk; ++b) acc = __builtin_fmaf(part[b * kTileRows + lane], scl[b * kTileRows + lane], acc);
     const std::size_t o = tile * kTileRows + lane;
-    if (o < static_cast<std::size_t>(out)) y[o] = acc + (bias != nullptr ? bias[o] : 0.0f);
+    if (o < static_cast<std::size_t>(out)) {
+      const float v = acc + (bias != nullptr ? bias[o] : 0.0f);
+      y[o] = accumulate ? y[o] + v : v;
+    }
   }
 }
 
@@ -180,7 +184,7 @@ template <int TYPE, int R, int CH>
 __global__ void __launch_bounds__(256) qgemv_rows(const uint4* __restrict__ codes, const float* __restrict__ scales,
                                                   const float* __restrict__ x, const float* __restrict__ bias,
                                                   float* __restrict__ y, int in, int nblk, int out, int rows,
-                                                  int ntiles) {
+                                                  int ntiles, int accumulate) {
   const int lane = threadIdx.x & (kTileRows - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const std::size_t tile = static_cast<std::size_t>(blockIdx.x) * 4 + wave;
@@ -247,18 +251,24 @@ __global__ void __launch_bounds__(256) qgemv_rows(const uint4* __restrict__ code
   if (o < static_cast<std::size_t>(out)) {
     const float add = bias != nullptr ? bias[o] : 0.0f;
 #pragma unroll
-    for (int r = 0; r < R; ++r)
-      if (r < nr) y[static_cast<std::size_t>(r0 + r) * out + o] = acc[r] + add;
+    for (int r = 0; r < R; ++r) {
+      if (r < nr) {
+        float* dst = y + static_cast<std::size_t>(r0 + r) * out + o;
+        const float v = acc[r] + add;
+        *dst = accumulate ? *dst + v : v;
+      }
+    }
   }
 }
 
 constexpr int chunk_for(int type) { return type == LLMI_TYPE_Q8_0 ? 4 : 8; }
 
 template <int TYPE, int R>
-int launch_rows(const DeviceMatrix& m, const float* x, std::size_t rows, const float* bias, float* y, hipStream_t s);
+int launch_rows(const DeviceMatrix& m, const float* x, std::size_t rows, const float* bias, float* y, int acc,
+                hipStream_t s);
 
 template <int TYPE>
-int launch_r1(const DeviceMatrix& m, const float* x, const float* bias, float* y, hipStream_t s) {
+int launch_r1(const DeviceMatrix& m, const float* x, const float* bias, float* y, int acc, hipStream_t s) {
   constexpr int CH = chunk_for(TYPE);
   // Wavefronts per tile: enough to put ~16 wavefronts on each of the 256
   // CUs when the matrix has few tiles, at most 16 per workgroup, and at
@@ -269,42 +279,46 @@ int launch_r1(const DeviceMatrix& m, const float* x, const float* bias, float* y
   waves = ceil_div(m.nblk, bpw);
   const std::size_t lds = 2 * m.nblk * kTileRows * sizeof(float);
   // Rows too long for the LDS staging take the one-wavefront-per-tile path.
-  if (lds > max_lds_per_block()) return launch_rows<TYPE, 2>(m, x, 1, bias, y, s);
+  if (lds > max_lds_per_block()) return launch_rows<TYPE, 2>(m, x, 1, bias, y, acc, s);
   qgemv_r1<TYPE, CH><<<static_cast<unsigned>(m.ntiles), static_cast<unsigned>(waves * 64), lds, s>>>(
       reinterpret_cast<const uint4*>(m.codes), m.scales, x, bias, y, static_cast<int>(m.in), static_cast<int>(m.nblk),
-      static_cast<int>(m.out), bpw);
+      static_cast<int>(m.out), bpw, acc);
   return LLMI_OK;
 }
 
 template <int TYPE, int R>
-int launch_rows(const DeviceMatrix& m, const float* x, std::size_t rows, const float* bias, float* y, hipStream_t s) {
+int launch_rows(const DeviceMatrix& m, const float* x, std::size_t rows, const float* bias, float* y, int acc,
+                hipStream_t s) {
   constexpr int CH = chunk_for(TYPE) / 2;
   const dim3 grid(static_cast<unsigned>(ceil_div(m.ntiles, 4)), static_cast<unsigned>(ceil_div(rows, R)));
   qgemv_rows<TYPE, R, CH><<<grid, 256, 0, s>>>(reinterpret_cast<const uint4*>(m.codes), m.scales, x, bias, y,
                                                static_cast<int>(m.in), static_cast<int>(m.nblk),
                                                static_cast<int>(m.out), static_cast<int>(rows),
-                                               static_cast<int>(m.ntiles));
+                                               static_cast<int>(m.ntiles), acc);
   return LLMI_OK;
 }
 
 template <int TYPE>
-int launch_typed(const DeviceMatrix& m, const float* x, std::size_t rows, const float* bias, float* y, hipStream_t s) {
-  if (rows == 1) return launch_r1<TYPE>(m, x, bias, y, s);
-  if (rows == 2) return launch_rows<TYPE, 2>(m, x, rows, bias, y, s);
-  if (rows <= 4) return launch_rows<TYPE, 4>(m, x, rows, bias, y, s);
-  return launch_rows<TYPE, 8>(m, x, rows, bias, y, s);
+int launch_typed(const DeviceMatrix& m, const float* x, std::size_t rows, const float* bias, float* y, int acc,
+                 hipStream_t s) {
+  if (rows == 1) return launch_r1<TYPE>(m, x, bias, y, acc, s);
+  if (rows == 2) return launch_rows<TYPE, 2>(m, x, rows, bias, y, acc, s);
+  if (rows <= 4) return launch_rows<TYPE, 4>(m, x, rows, bias, y, acc, s);
+  return launch_rows<TYPE, 8>(m, x, rows, bias, y, acc, s);
 }
 
 }  // namespace
 
-int launch_matmul(const DeviceMatrix& m, const float* x, std::size_t rows, const float* bias, float* y, hipStream_t s) {
+int launch_matmul(const DeviceMatrix& m, const float* x, std::size_t rows, const float* bias, float* y, hipStream_t s,
+                  bool accumulate) {
   if (rows == 0 || m.out == 0) return LLMI_OK;
   LLMI_REQUIRE(m.in > 0, "matmul: in must be positive");
   LLMI_REQUIRE(m.in <= 0x7FFFFFFFu && m.out <= 0x7FFFFFFFu, "matmul: shape too large");
   LLMI_REQUIRE(ceil_div(rows, 8) <= 65535, "matmul: too many input rows for one launch");
   LLMI_REQUIRE(x != nullptr && y != nullptr, "matmul: null pointer");
-  const int rc = m.type == LLMI_TYPE_Q8_0 ? launch_typed<LLMI_TYPE_Q8_0>(m, x, rows, bias, y, s)
-                                          : launch_typed<LLMI_TYPE_Q4_0>(m, x, rows, bias, y, s);
+  const int acc = accumulate ? 1 : 0;
+  const int rc = m.type == LLMI_TYPE_Q8_0 ? launch_typed<LLMI_TYPE_Q8_0>(m, x, rows, bias, y, acc, s)
+                                          : launch_typed<LLMI_TYPE_Q4_0>(m, x, rows, bias, y, acc, s);
   if (rc != LLMI_OK) return rc;
   LLMI_TRY_HIP(hipGetLastError());
   return LLMI_OK;

@@ -1,0 +1,807 @@
+// Device-resident Llama / Qwen2 decoder for the quantized-weight path:
+// Transformer::load / new_cache / forward_cached / generate_greedy_cached of
+// the reference (src/model/transformer.cpp:26-67, :182-327) with every
+// weight matrix, activation and the KV cache in HBM.  Token ids go in, logits
+// (or greedy ids) come out.
+//
+// Every glue operation restates the reference's arithmetic so that logits
+// are bit-identical to the reference's on the same weights:
+//   rmsnorm   kernels.cpp:115-120  double sum of squares, float scale,
+//                                  y = w * (x * scale)
+//   rope      kernels.cpp:122-134  cos/sin of the float angle pos*inv_freq[i]
+//                                  (host sincosf tables), fused as
+//                                  v[i] = fma(a,c,-(b*s)), v[i+h] = fma(b,c,a*s)
+//   attention transformer.cpp:263-282  scores = dot(q, k_s) * (1/sqrt(hd))
+//                                  with kernels::dot's summation order,
+//                                  softmax (float max, expf, double sum,
+//                                  float reciprocal), out = sequential
+//                                  fma(p_s, v_s[i], out[i]) over positions
+//   silu*up   kernels.cpp:148      x / (1 + expf(-x)), times up
+//   residual  transformer.cpp:284  x += proj (GEMV epilogue)
+//   argmax    transformer.cpp:22   first maximum
+// expf is the exact restatement of the host libm's (exact_math.hpp).  The two
+// double-precision sums are reduced in parallel; their float result is taken
+// only when an error bound proves the reference's sequential sum rounds to
+// the same float, and recomputed sequentially otherwise.
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "common.hpp"
+#include "exact_math.hpp"
+
+namespace llmi_hip {
+namespace {
+
+constexpr int kThreads = 256;
+
+// ------------------------------------------------------------ reductions
+__device__ __forceinline__ double block_sum_double(double v, double* red) {
+  // Fixed-shape tree over the 256 threads: deterministic.
+  const int tid = threadIdx.x;
+  red[tid] = v;
+  __syncthreads();
+  for (int stride = kThreads / 2; stride > 0; stride >>= 1) {
+    if (tid < stride) red[tid] = red[tid] + red[tid + stride];
+    __syncthreads();
+  }
+  const double r = red[0];
+  __syncthreads();
+  return r;
+}
+
+__device__ __forceinline__ float block_max_float(float v, float* red) {
+  const int tid = threadIdx.x;
+  red[tid] = v;
+  __syncthreads();
+  for (int stride = kThreads / 2; stride > 0; stride >>= 1) {
+    if (tid < stride) red[tid] = fmaxf(red[tid], red[tid + stride]);
+    __syncthreads();
+  }
+  const float r = red[0];
+  __syncthreads();
+  return r;
+}
+
+// Bound on |sequential - parallel| for a sum of n non-negative doubles:
+// both are within (n-1)u of the exact sum (u = 2^-53); 4nu covers both.
+__device__ __forceinline__ double sum_slack(int n) { return 4.0 * static_cast<double>(n) * 0x1p-53; }
+
+// ------------------------------------------------------------ rmsnorm
+__device__ __forceinline__ float rms_scale(double ss, int n, float eps) {
+  return static_cast<float>(1.0 / sqrt(ss / static_cast<double>(n) + static_cast<double>(eps)));
+}
+
+// One workgroup per row: y = w * (x * scale), scale from the double sum of
+// squares (kernels.cpp:115-120).
+__global__ void __launch_bounds__(kThreads) rmsnorm_rows(const float* __restrict__ x, const float* __restrict__ w,
+                                                         float* __restrict__ y, int n, float eps) {
+  __shared__ double red[kThreads];
+  __shared__ float scale_s;
+  const float* xr = x + static_cast<std::size_t>(blockIdx.x) * n;
+  float* yr = y + static_cast<std::size_t>(blockIdx.x) * n;
+  double part = 0.0;
+  for (int i = threadIdx.x; i < n; i += kThreads) {
+    const double v = static_cast<double>(xr[i]);
+    part = __builtin_fma(v, v, part);
+  }
+  const double ss = block_sum_double(part, red);
+  if (threadIdx.x == 0) {
+    // The function ss -> scale is monotone; the reference's sequential sum
+    // lies in [lo, hi].  If both ends give one float, that is the answer.
+    const double slack = sum_slack(n) * ss;
+    const float a = rms_scale(ss - slack, n, eps);
+    const float b = rms_scale(ss + slack, n, eps);
+    float sc = rms_scale(ss, n, eps);
+    if (a != b) {
+      double seq = 0.0;
+      for (int i = 0; i < n; ++i) {
+        const double v = static_cast<double>(xr[i]);
+        seq = __builtin_fma(v, v, seq);
+      }
+      sc = rms_scale(seq, n, eps);
+    }
+    scale_s = sc;
+  }
+  __syncthreads();
+  const float sc = scale_s;
+  for (int i = threadIdx.x; i < n; i += kThreads) yr[i] = w[i] * (xr[i] * sc);
+}
+
+// --------------------------------------------------------- rope + cache
+// grid.x = token t.  q [T][nh][hd] is rotated in place; k [T][nkv][hd] is
+// rotated into the cache, v copied: cache[(kvh*cap + pos)*hd + i].
+__global__ void __launch_bounds__(kThreads) rope_and_cache(float* __restrict__ q, const float* __restrict__ knew,
+                                                           const float* __restrict__ vnew, float* __restrict__ kc,
+                                                           float* __restrict__ vc, const float* __restrict__ cos_t,
+                                                           const float* __restrict__ sin_t, int nh, int nkv, int hd,
+                                                           int cap, int base) {
+  const int t = blockIdx.x;
+  const int pos = base + t;
+  const int half = hd / 2;
+  const float* cr = cos_t + static_cast<std::size_t>(pos) * half;
+  const float* sr = sin_t + static_cast<std::size_t>(pos) * half;
+  for (int e = threadIdx.x; e < nh * half; e += kThreads) {
+    const int h = e / half, i = e % half;
+    float* v = q + (static_cast<std::size_t>(t) * nh + h) * hd;
+    const float a = v[i], b = v[i + half], c = cr[i], s = sr[i];
+    v[i] = __builtin_fmaf(a, c, -(b * s));
+    v[i + half] = __builtin_fmaf(b, c, a * s);
+  }
+  for (int e = threadIdx.x; e < nkv * half; e += kThreads) {
+    const int h = e / half, i = e % half;
+    const float* v = knew + (static_cast<std::size_t>(t) * nkv + h) * hd;
+    float* dst = kc + (static_cast<std::size_t>(h) * cap + pos) * hd;
+    const float a = v[i], b = v[i + half], c = cr[i], s = sr[i];
+    dst[i] = __builtin_fmaf(a, c, -(b * s));
+    dst[i + half] = __builtin_fmaf(b, c, a * s);
+  }
+  for (int e = threadIdx.x; e < nkv * hd; e += kThreads) {
+    const int h = e / hd, i = e % hd;
+    vc[(static_cast<std::size_t>(h) * cap + pos) * hd + i] = vnew[(static_cast<std::size_t>(t) * nkv + h) * hd + i];
+  }
+}
+
+// ------------------------------------------------------------- attention
+// kernels::dot (kernels.cpp:41-95, the AVX2 build): 16 fused lanes over
+// 16-element chunks reduced (j + j+8), (+4), (+2), (+1); then the scalar
+// tail: 8 fused lanes over 8-element chunks, then up to 7 leftovers (when 4
+// or more remain, the first 4 products are rounded on their own and added in
+// order), the 8 lanes reduced pairwise, plus the leftovers.
+__device__ __forceinline__ float ref_dot(const float* __restrict__ a, const float* __restrict__ b, int n) {
+  float lane[16];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) lane[j] = 0.0f;
+  int i = 0;
+  for (; i + 16 <= n; i += 16) {
+#pragma unroll
+    for (int j = 0; j < 16; ++j) lane[j] = __builtin_fmaf(a[i + j], b[i + j], lane[j]);
+  }
+  float s8[8], s4[4];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) s8[j] = lane[j] + lane[j + 8];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) s4[j] = s8[j] + s8[j + 4];
+  const float head = (s4[0] + s4[2]) + (s4[1] + s4[3]);
+  float acc[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) acc[j] = 0.0f;
+  for (; i + 8 <= n; i += 8) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[j] = __builtin_fmaf(a[i + j], b[i + j], acc[j]);
+  }
+  float tail = 0.0f;
+  if (n - i >= 4) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float p = a[i + j] * b[i + j];
+      tail = tail + p;
+    }
+    i += 4;
+  }
+  for (; i < n; ++i) tail = __builtin_fmaf(a[i], b[i], tail);
+  const float rest = ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7])) + tail;
+  return head + rest;
+}
+
+__device__ __forceinline__ float recip_float(double s) { return static_cast<float>(1.0 / s); }
+
+// grid = (head, token).  Dynamic LDS: the scores of positions 0..pos.
+__global__ void __launch_bounds__(kThreads) attention(const float* __restrict__ q, const float* __restrict__ kc,
+                                                      const float* __restrict__ vc, float* __restrict__ out, int nh,
+                                                      int nkv, int hd, int cap, int base, float scale) {
+  extern __shared__ float sc[];
+  __shared__ double red_d[kThreads];
+  __shared__ float red_f[kThreads];
+  __shared__ float inv_s;
+  const int h = blockIdx.x;
+  const int t = blockIdx.y;
+  const int pos = base + t;
+  const int npos = pos + 1;
+  const int kvh = h / (nh / nkv);
+  const float* qv = q + (static_cast<std::size_t>(t) * nh + h) * hd;
+  const float* kh = kc + static_cast<std::size_t>(kvh) * cap * hd;
+  const float* vh = vc + static_cast<std::size_t>(kvh) * cap * hd;
+
+  float mx_local = -__builtin_inff();
+  for (int s = threadIdx.x; s < npos; s += kThreads) {
+    const float v = ref_dot(qv, kh + static_cast<std::size_t>(s) * hd, hd) * scale;
+    sc[s] = v;
+    mx_local = fmaxf(mx_local, v);
+  }
+  const float mx = block_max_float(mx_local, red_f);
+
+  double part = 0.0;
+  for (int s = threadIdx.x; s < npos; s += kThreads) {
+    const float e = exact::expf(sc[s] - mx);
+    sc[s] = e;
+    part += static_cast<double>(e);
+  }
+  const double sum = block_sum_double(part, red_d);  // ends with a barrier: sc[] is complete
+  if (threadIdx.x == 0) {
+    const double slack = sum_slack(npos) * sum;
+    float inv = recip_float(sum);
+    if (recip_float(sum - slack) != recip_float(sum + slack)) {
+      double seq = 0.0;
+      for (int s = 0; s < npos; ++s) seq += static_cast<double>(sc[s]);
+      inv = recip_float(seq);
+    }
+    inv_s = inv;
+  }
+  __syncthreads();
+  const float inv = inv_s;
+  for (int s = threadIdx.x; s < npos; s += kThreads) sc[s] = sc[s] * inv;
+  __syncthreads();
+
+  // out[i] = fma(p_s, v_s[i], out[i]) over s in order, one thread per i.
+  for (int i = threadIdx.x; i < hd; i += kThreads) {
+    float acc = 0.0f;
+    const float* vp = vh + i;
+    int s = 0;
+    for (; s + 4 <= npos; s += 4) {
+      const float v0 = vp[static_cast<std::size_t>(s + 0) * hd];
+      const float v1 = vp[static_cast<std::size_t>(s + 1) * hd];
+      const float v2 = vp[static_cast<std::size_t>(s + 2) * hd];
+      const float v3 = vp[static_cast<std::size_t>(s + 3) * hd];
+      acc = __builtin_fmaf(sc[s + 0], v0, acc);
+      acc = __builtin_fmaf(sc[s + 1], v1, acc);
+      acc = __builtin_fmaf(sc[s + 2], v2, acc);
+      acc = __builtin_fmaf(sc[s + 3], v3, acc);
+    }
+    for (; s < npos; ++s) acc = __builtin_fmaf(sc[s], vp[static_cast<std::size_t>(s) * hd], acc);
+    out[(static_cast<std::size_t>(t) * nh + h) * hd + i] = acc;
+  }
+}
+
+// ------------------------------------------------------------- silu * up
+__global__ void __launch_bounds__(kThreads) silu_mul(float* __restrict__ g, const float* __restrict__ u,
+                                                     std::size_t n) {
+  const std::size_t i = static_cast<std::size_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (i >= n) return;
+  const float v = g[i];
+  const float silu = v / (1.0f + exact::expf(-v));
+  g[i] = silu * u[i];
+}
+
+// --------------------------------------------------------------- argmax
+// First maximum (lowest index on ties) of x[0..n); one 1024-thread block.
+__global__ void __launch_bounds__(1024) argmax_first(const float* __restrict__ x, int n, std::int32_t* __restrict__ out) {
+  __shared__ float bv[1024];
+  __shared__ int bi[1024];
+  const int tid = threadIdx.x;
+  float best = -__builtin_inff();
+  int idx = -1;
+  for (int i = tid; i < n; i += 1024) {
+    const float v = x[i];
+    if (idx < 0 || v > best) {
+      best = v;
+      idx = i;
+    }
+  }
+  bv[tid] = best;
+  bi[tid] = idx;
+  __syncthreads();
+  for (int stride = 512; stride > 0; stride >>= 1) {
+    if (tid < stride) {
+      const float ov = bv[tid + stride];
+      const int oi = bi[tid + stride];
+      if (oi >= 0 && (bi[tid] < 0 || ov > bv[tid] || (ov == bv[tid] && oi < bi[tid]))) {
+        bv[tid] = ov;
+        bi[tid] = oi;
+      }
+    }
+    __syncthreads();
+  }
+  if (tid == 0) *out = bi[0] < 0 ? 0 : bi[0];
+}
+
+// Standalone glue kernels (the device counterparts of kernels.hpp:13-32).
+__global__ void __launch_bounds__(kThreads) dot_many(const float* __restrict__ a, const float* __restrict__ b,
+                                                     const int* __restrict__ lens, int count, float* __restrict__ out) {
+  const int i = blockIdx.x * kThreads + threadIdx.x;
+  if (i < count) out[i] = ref_dot(a, b, lens[i]);
+}
+
+// kernels.cpp:136-146 on each row of x (rows x n), in place; n <= LDS.
+__global__ void __launch_bounds__(kThreads) softmax_rows(float* __restrict__ x, int n) {
+  extern __shared__ float sc[];
+  __shared__ double red_d[kThreads];
+  __shared__ float red_f[kThreads];
+  __shared__ float inv_s;
+  float* row = x + static_cast<std::size_t>(blockIdx.x) * n;
+  float mx_local = -__builtin_inff();
+  for (int s = threadIdx.x; s < n; s += kThreads) {
+    sc[s] = row[s];
+    mx_local = fmaxf(mx_local, sc[s]);
+  }
+  const float mx = block_max_float(mx_local, red_f);
+  double part = 0.0;
+  for (int s = threadIdx.x; s < n; s += kThreads) {
+    const float e = exact::expf(sc[s] - mx);
+    sc[s] = e;
+    part += static_cast<double>(e);
+  }
+  const double sum = block_sum_double(part, red_d);
+  if (threadIdx.x == 0) {
+    const double slack = sum_slack(n) * sum;
+    float inv = recip_float(sum);
+    if (recip_float(sum - slack) != recip_float(sum + slack)) {
+      double seq = 0.0;
+      for (int s = 0; s < n; ++s) seq += static_cast<double>(sc[s]);
+      inv = recip_float(seq);
+    }
+    inv_s = inv;
+  }
+  __syncthreads();
+  for (int s = threadIdx.x; s < n; s += kThreads) row[s] = sc[s] * inv_s;
+}
+
+__global__ void __launch_bounds__(kThreads) silu_inplace(float* __restrict__ x, std::size_t n) {
+  const std::size_t i = static_cast<std::size_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (i < n) x[i] = x[i] / (1.0f + exact::expf(-x[i]));
+}
+
+unsigned blocks_for(std::size_t n) { return static_cast<unsigned>(ceil_div(n, kThreads)); }
+
+}  // namespace
+
+// ---------------------------------------------------------------- model
+struct DeviceLayer {
+  float *attn_norm = nullptr, *mlp_norm = nullptr, *bq = nullptr, *bk = nullptr, *bv = nullptr;
+  DeviceMatrix wq, wk, wv, wo, gate, up, down;
+};
+
+struct Workspace {
+  std::size_t tokens = 0;  // capacity in tokens
+  float *x = nullptr, *h = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *att = nullptr, *g = nullptr,
+        *u = nullptr, *logits = nullptr;
+  std::int32_t* ids = nullptr;
+  std::int32_t* next = nullptr;  // argmax result
+};
+
+}  // namespace llmi_hip
+
+struct llmi_hip_model {
+  llmi_model_config c{};
+  int type = 0;
+  std::size_t H = 0, hd = 0, Q = 0, KV = 0, F = 0, V = 0;
+  llmi_hip::DeviceMatrix embed, lm_head;
+  bool tied = true;
+  float* final_norm = nullptr;
+  std::vector<llmi_hip::DeviceLayer> layers;
+  std::vector<float> inv_freq;
+  float* cos_t = nullptr;
+  float* sin_t = nullptr;
+  std::size_t table_len = 0;
+  llmi_hip::Workspace ws;
+  std::vector<void*> allocations;
+};
+
+struct llmi_hip_cache {
+  const llmi_hip_model* model = nullptr;
+  std::size_t cap = 0, len = 0;
+  float* k = nullptr;  // [layer][kv_head][cap][hd]
+  float* v = nullptr;
+};
+
+namespace llmi_hip {
+namespace {
+
+int dev_alloc(llmi_hip_model* m, void** p, std::size_t bytes) {
+  *p = nullptr;
+  if (bytes == 0) return LLMI_OK;
+  LLMI_TRY_HIP(hipMalloc(p, bytes));
+  m->allocations.push_back(*p);
+  return LLMI_OK;
+}
+
+// Copies n floats from host or device memory into a new device array.
+int dev_vector(llmi_hip_model* m, const float* src, std::size_t n, bool src_on_device, float** dst) {
+  if (int rc = dev_alloc(m, reinterpret_cast<void**>(dst), n * sizeof(float))) return rc;
+  if (n > 0)
+    LLMI_TRY_HIP(hipMemcpyAsync(*dst, src, n * sizeof(float), src_on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice,
+                                library_stream()));
+  return LLMI_OK;
+}
+
+// Quantizes an out x in fp32 matrix (host or device) into the tiled layout.
+int dev_matrix(llmi_hip_model* m, const float* src, std::size_t out, std::size_t in, bool src_on_device,
+               float* staging, DeviceMatrix* dm) {
+  dm->type = m->type;
+  dm->out = out;
+  dm->in = in;
+  dm->nblk = ceil_div(in, kBlock);
+  dm->ntiles = ceil_div(out, kTileRows);
+  dm->code_bytes = dm->ntiles * dm->nblk * kTileRows * block_code_bytes(m->type);
+  dm->scale_bytes = dm->ntiles * dm->nblk * kTileRows * sizeof(float);
+  if (int rc = dev_alloc(m, reinterpret_cast<void**>(&dm->codes), dm->code_bytes)) return rc;
+  if (int rc = dev_alloc(m, reinterpret_cast<void**>(&dm->scales), dm->scale_bytes)) return rc;
+  LLMI_TRY_HIP(hipMemsetAsync(dm->codes, 0, dm->code_bytes, library_stream()));
+  LLMI_TRY_HIP(hipMemsetAsync(dm->scales, 0, dm->scale_bytes, library_stream()));
+  const float* w = src;
+  if (!src_on_device) {
+    LLMI_TRY_HIP(hipMemcpyAsync(staging, src, out * in * sizeof(float), hipMemcpyHostToDevice, library_stream()));
+    w = staging;
+  }
+  if (int rc = launch_quantize(w, out, in, m->type, nullptr, nullptr, dm, library_stream())) return rc;
+  // The staging buffer is reused by the next matrix: finish this one first.
+  LLMI_TRY_HIP(hipStreamSynchronize(library_stream()));
+  return LLMI_OK;
+}
+
+int check_config(const llmi_model_config& c) {
+  LLMI_REQUIRE(c.arch == 0 || c.arch == 1, "model: arch must be 0 (Llama) or 1 (Qwen2)");
+  LLMI_REQUIRE(c.vocab_size > 0 && c.hidden_size > 0 && c.intermediate_size > 0 && c.num_layers > 0,
+               "model: sizes must be positive");
+  LLMI_REQUIRE(c.num_heads > 0 && c.num_kv_heads > 0, "model: head counts must be positive");
+  LLMI_REQUIRE(c.hidden_size % c.num_heads == 0, "model: hidden_size is not a multiple of num_attention_heads");
+  LLMI_REQUIRE((c.hidden_size / c.num_heads) % 2 == 0, "model: head_dim must be even for rotary embeddings");
+  LLMI_REQUIRE(c.num_heads % c.num_kv_heads == 0, "model: num_attention_heads is not a multiple of num_key_value_heads");
+  LLMI_REQUIRE(c.max_position_embeddings > 0, "model: max_position_embeddings must be positive");
+  return LLMI_OK;
+}
+
+int create_model(const llmi_model_config* cfg, const float* const* t, int type, bool on_device,
+                 llmi_hip_model** out) {
+  LLMI_REQUIRE_INIT();
+  LLMI_REQUIRE(cfg != nullptr && t != nullptr && out != nullptr, "model_create: null pointer");
+  LLMI_REQUIRE(type == LLMI_TYPE_Q8_0 || type == LLMI_TYPE_Q4_0,
+               "model_create: type must be Q8_0 or Q4_0 (the f32 path is not part of this library)");
+  if (int rc = check_config(*cfg)) return rc;
+  *out = nullptr;
+  auto m = std::make_unique<llmi_hip_model>();
+  m->c = *cfg;
+  m->type = type;
+  const auto& c = m->c;
+  m->H = c.hidden_size;
+  m->hd = c.hidden_size / c.num_heads;
+  m->Q = static_cast<std::size_t>(c.num_heads) * m->hd;
+  m->KV = static_cast<std::size_t>(c.num_kv_heads) * m->hd;
+  m->F = c.intermediate_size;
+  m->V = c.vocab_size;
+  m->tied = c.tie_word_embeddings != 0;
+  auto cleanup = [&](int rc) {
+    for (void* p : m->allocations) (void)hipFree(p);
+    m->allocations.clear();
+    return rc;
+  };
+  const std::size_t biggest = std::max({m->V * m->H, m->F * m->H, m->Q * m->H});
+  float* staging = nullptr;
+  if (!on_device) {
+    if (int rc = dev_alloc(m.get(), reinterpret_cast<void**>(&staging), biggest * sizeof(float))) return cleanup(rc);
+  }
+  std::size_t k = 0;
+  int rc = dev_matrix(m.get(), t[k++], m->V, m->H, on_device, staging, &m->embed);
+  m->layers.resize(c.num_layers);
+  for (auto& l : m->layers) {
+    if (rc == LLMI_OK) rc = dev_vector(m.get(), t[k++], m->H, on_device, &l.attn_norm);
+    if (rc == LLMI_OK) rc = dev_matrix(m.get(), t[k++], m->Q, m->H, on_device, staging, &l.wq);
+    if (rc == LLMI_OK) rc = dev_matrix(m.get(), t[k++], m->KV, m->H, on_device, staging, &l.wk);
+    if (rc == LLMI_OK) rc = dev_matrix(m.get(), t[k++], m->KV, m->H, on_device, staging, &l.wv);
+    if (c.qkv_bias) {
+      if (rc == LLMI_OK) rc = dev_vector(m.get(), t[k++], m->Q, on_device, &l.bq);
+      if (rc == LLMI_OK) rc = dev_vector(m.get(), t[k++], m->KV, on_device, &l.bk);
+      if (rc == LLMI_OK) rc = dev_vector(m.get(), t[k++], m->KV, on_device, &l.bv);
+    }
+    if (rc == LLMI_OK) rc = dev_matrix(m.get(), t[k++], m->H, m->Q, on_device, staging, &l.wo);
+    if (rc == LLMI_OK) rc = dev_vector(m.get(), t[k++], m->H, on_device, &l.mlp_norm);
+    if (rc == LLMI_OK) rc = dev_matrix(m.get(), t[k++], m->F, m->H, on_device, staging, &l.gate);
+    if (rc == LLMI_OK) rc = dev_matrix(m.get(), t[k++], m->F, m->H, on_device, staging, &l.up);
+    if (rc == LLMI_OK) rc = dev_matrix(m.get(), t[k++], m->H, m->F, on_device, staging, &l.down);
+  }
+  if (rc == LLMI_OK) rc = dev_vector(m.get(), t[k++], m->H, on_device, &m->final_norm);
+  if (rc == LLMI_OK && !m->tied) rc = dev_matrix(m.get(), t[k++], m->V, m->H, on_device, staging, &m->lm_head);
+  if (rc == LLMI_OK && hipStreamSynchronize(library_stream()) != hipSuccess) rc = fail(LLMI_ERR_HIP, "model_create: sync");
+  if (rc != LLMI_OK) return cleanup(rc);
+  if (staging != nullptr) {
+    (void)hipFree(staging);
+    m->allocations.erase(std::find(m->allocations.begin(), m->allocations.end(), static_cast<void*>(staging)));
+  }
+  // inv_freq[i] = 1 / theta^(2i/d) in float, as transformer.cpp:59-66.
+  m->inv_freq.resize(m->hd / 2);
+  for (std::size_t i = 0; i < m->hd / 2; ++i) {
+    const float e = static_cast<float>(2 * i) / static_cast<float>(m->hd);
+    m->inv_freq[i] = 1.0F / std::pow(static_cast<float>(c.rope_theta), e);
+  }
+  *out = m.release();
+  return LLMI_OK;
+}
+
+// cos/sin of the float angle pos*inv_freq[i] for pos < n, computed on the
+// host with the same libm call the reference makes (kernels.cpp:126-128).
+int ensure_tables(llmi_hip_model* m, std::size_t n) {
+  if (m->table_len >= n) return LLMI_OK;
+  const std::size_t half = m->hd / 2;
+  std::vector<float> c(n * half), s(n * half);
+  for (std::size_t pos = 0; pos < n; ++pos)
+    for (std::size_t i = 0; i < half; ++i) {
+      const float angle = static_cast<float>(pos) * m->inv_freq[i];
+      sincosf(angle, &s[pos * half + i], &c[pos * half + i]);
+    }
+  float *dc = nullptr, *dsn = nullptr;
+  LLMI_TRY_HIP(hipMalloc(&dc, c.size() * sizeof(float)));
+  const hipError_t e = hipMalloc(&dsn, s.size() * sizeof(float));
+  if (e != hipSuccess) {
+    (void)hipFree(dc);
+    return fail(LLMI_ERR_HIP, "rope tables: hipMalloc");
+  }
+  LLMI_TRY_HIP(hipMemcpy(dc, c.data(), c.size() * sizeof(float), hipMemcpyHostToDevice));
+  LLMI_TRY_HIP(hipMemcpy(dsn, s.data(), s.size() * sizeof(float), hipMemcpyHostToDevice));
+  LLMI_TRY_HIP(hipStreamSynchronize(library_stream()));
+  if (m->cos_t != nullptr) (void)hipFree(m->cos_t);
+  if (m->sin_t != nullptr) (void)hipFree(m->sin_t);
+  m->cos_t = dc;
+  m->sin_t = dsn;
+  m->table_len = n;
+  return LLMI_OK;
+}
+
+void free_workspace(Workspace& w) {
+  for (void* p : {static_cast<void*>(w.x), static_cast<void*>(w.h), static_cast<void*>(w.q), static_cast<void*>(w.k),
+                  static_cast<void*>(w.v), static_cast<void*>(w.att), static_cast<void*>(w.g), static_cast<void*>(w.u),
+                  static_cast<void*>(w.logits), static_cast<void*>(w.ids), static_cast<void*>(w.next)})
+    if (p != nullptr) (void)hipFree(p);
+  w = Workspace{};
+}
+
+int ensure_workspace(llmi_hip_model* m, std::size_t T) {
+  Workspace& w = m->ws;
+  if (w.tokens >= T) return LLMI_OK;
+  LLMI_TRY_HIP(hipStreamSynchronize(library_stream()));
+  free_workspace(w);
+  const std::size_t n = std::max<std::size_t>(T, 1);
+  auto get = [&](auto** p, std::size_t elems, std::size_t size) -> int {
+    LLMI_TRY_HIP(hipMalloc(reinterpret_cast<void**>(p), std::max<std::size_t>(elems, 1) * size));
+    return LLMI_OK;
+  };
+  int rc = get(&w.x, n * m->H, 4);
+  if (rc == LLMI_OK) rc = get(&w.h, n * m->H, 4);
+  if (rc == LLMI_OK) rc = get(&w.q, n * m->Q, 4);
+  if (rc == LLMI_OK) rc = get(&w.k, n * m->KV, 4);
+  if (rc == LLMI_OK) rc = get(&w.v, n * m->KV, 4);
+  if (rc == LLMI_OK) rc = get(&w.att, n * m->Q, 4);
+  if (rc == LLMI_OK) rc = get(&w.g, n * m->F, 4);
+  if (rc == LLMI_OK) rc = get(&w.u, n * m->F, 4);
+  if (rc == LLMI_OK) rc = get(&w.logits, n * m->V, 4);
+  if (rc == LLMI_OK) rc = get(&w.ids, n, 4);
+  if (rc == LLMI_OK) rc = get(&w.next, 1, 4);
+  if (rc != LLMI_OK) {
+    free_workspace(w);
+    return rc;
+  }
+  w.tokens = n;
+  return LLMI_OK;
+}
+
+std::size_t attention_lds(std::size_t cap) { return cap * sizeof(float); }
+
+// transformer.cpp:192-306 with the ids already on the device (ws.ids).  The
+// logits of rows first..T-1 land in ws.logits.
+int forward_device(llmi_hip_model* m, llmi_hip_cache* cache, std::size_t T, bool all_positions, hipStream_t s) {
+  const auto& c = m->c;
+  Workspace& w = m->ws;
+  const std::size_t base = cache->len;
+  const int nh = static_cast<int>(c.num_heads), nkv = static_cast<int>(c.num_kv_heads);
+  const int hd = static_cast<int>(m->hd);
+  const float eps = static_cast<float>(c.rms_norm_eps);
+  const float scale = 1.0F / std::sqrt(static_cast<float>(m->hd));
+  const std::size_t per_layer = static_cast<std::size_t>(c.num_kv_heads) * cache->cap * m->hd;
+  const unsigned tt = static_cast<unsigned>(T);
+
+  if (int rc = launch_dequantize_rows(m->embed, w.ids, T, w.x, s)) return rc;
+  for (std::size_t li = 0; li < m->layers.size(); ++li) {
+    const DeviceLayer& l = m->layers[li];
+    float* kc = cache->k + li * per_layer;
+    float* vc = cache->v + li * per_layer;
+    rmsnorm_rows<<<tt, kThreads, 0, s>>>(w.x, l.attn_norm, w.h, static_cast<int>(m->H), eps);
+    if (int rc = launch_matmul(l.wq, w.h, T, l.bq, w.q, s)) return rc;
+    if (int rc = launch_matmul(l.wk, w.h, T, l.bk, w.k, s)) return rc;
+    if (int rc = launch_matmul(l.wv, w.h, T, l.bv, w.v, s)) return rc;
+    rope_and_cache<<<tt, kThreads, 0, s>>>(w.q, w.k, w.v, kc, vc, m->cos_t, m->sin_t, nh, nkv, hd,
+                                           static_cast<int>(cache->cap), static_cast<int>(base));
+    attention<<<dim3(static_cast<unsigned>(nh), tt), kThreads, attention_lds(base + T), s>>>(
+        w.q, kc, vc, w.att, nh, nkv, hd, static_cast<int>(cache->cap), static_cast<int>(base), scale);
+    if (int rc = launch_matmul(l.wo, w.att, T, nullptr, w.x, s, true)) return rc;
+    rmsnorm_rows<<<tt, kThreads, 0, s>>>(w.x, l.mlp_norm, w.h, static_cast<int>(m->H), eps);
+    if (int rc = launch_matmul(l.gate, w.h, T, nullptr, w.g, s)) return rc;
+    if (int rc = launch_matmul(l.up, w.h, T, nullptr, w.u, s)) return rc;
+    silu_mul<<<blocks_for(T * m->F), kThreads, 0, s>>>(w.g, w.u, T * m->F);
+    if (int rc = launch_matmul(l.down, w.g, T, nullptr, w.x, s, true)) return rc;
+  }
+  const std::size_t first = all_positions ? 0 : T - 1;
+  const std::size_t rows = T - first;
+  rmsnorm_rows<<<static_cast<unsigned>(rows), kThreads, 0, s>>>(w.x + first * m->H, m->final_norm, w.h,
+                                                                static_cast<int>(m->H), eps);
+  const DeviceMatrix& head = m->tied ? m->embed : m->lm_head;
+  if (int rc = launch_matmul(head, w.h, rows, nullptr, w.logits, s)) return rc;
+  LLMI_TRY_HIP(hipGetLastError());
+  cache->len = base + T;
+  return LLMI_OK;
+}
+
+// Validation of transformer.cpp:204-212, with the reference's messages.
+int validate(llmi_hip_model* m, llmi_hip_cache* cache, const std::int32_t* tokens, std::size_t T) {
+  if (T == 0) return fail(LLMI_ERR_ARG, "forward_cached: no tokens");
+  if (cache == nullptr || cache->model != m) return fail(LLMI_ERR_STATE, "forward_cached: cache was not created by this model");
+  if (cache->len + T > cache->cap) return fail(LLMI_ERR_STATE, "forward_cached: cache is full");
+  if (cache->len + T > m->c.max_position_embeddings)
+    return fail(LLMI_ERR_STATE, "forward_cached: sequence longer than the model's context");
+  for (std::size_t t = 0; t < T; ++t)
+    if (tokens[t] < 0 || static_cast<std::size_t>(tokens[t]) >= m->V)
+      return fail(LLMI_ERR_ARG, "forward_cached: token id " + std::to_string(tokens[t]) + " out of range");
+  return LLMI_OK;
+}
+
+}  // namespace
+}  // namespace llmi_hip
+
+using namespace llmi_hip;
+
+extern "C" {
+
+int llmi_hip_dot_dev(const float* a, const float* b, const int32_t* lens, size_t count, float* out, void* stream) {
+  LLMI_REQUIRE_INIT();
+  if (count == 0) return LLMI_OK;
+  dot_many<<<blocks_for(count), kThreads, 0, pick(stream)>>>(a, b, lens, static_cast<int>(count), out);
+  LLMI_TRY_HIP(hipGetLastError());
+  return LLMI_OK;
+}
+
+int llmi_hip_rmsnorm_dev(const float* x, const float* w, size_t rows, size_t n, float eps, float* y, void* stream) {
+  LLMI_REQUIRE_INIT();
+  LLMI_REQUIRE(n > 0 && n <= 0x7FFFFFFFu && rows <= 0x7FFFFFFFu, "rmsnorm: bad shape");
+  if (rows == 0) return LLMI_OK;
+  rmsnorm_rows<<<static_cast<unsigned>(rows), kThreads, 0, pick(stream)>>>(x, w, y, static_cast<int>(n), eps);
+  LLMI_TRY_HIP(hipGetLastError());
+  return LLMI_OK;
+}
+
+int llmi_hip_softmax_dev(float* x, size_t rows, size_t n, void* stream) {
+  LLMI_REQUIRE_INIT();
+  LLMI_REQUIRE(n * sizeof(float) + 4096 <= max_lds_per_block(), "softmax: row longer than the kernel's LDS");
+  if (rows == 0 || n == 0) return LLMI_OK;
+  softmax_rows<<<static_cast<unsigned>(rows), kThreads, n * sizeof(float), pick(stream)>>>(x, static_cast<int>(n));
+  LLMI_TRY_HIP(hipGetLastError());
+  return LLMI_OK;
+}
+
+int llmi_hip_silu_dev(float* x, size_t n, void* stream) {
+  LLMI_REQUIRE_INIT();
+  if (n == 0) return LLMI_OK;
+  silu_inplace<<<blocks_for(n), kThreads, 0, pick(stream)>>>(x, n);
+  LLMI_TRY_HIP(hipGetLastError());
+  return LLMI_OK;
+}
+
+int llmi_hip_argmax_dev(const float* x, size_t n, int32_t* out, void* stream) {
+  LLMI_REQUIRE_INIT();
+  LLMI_REQUIRE(n > 0 && n <= 0x7FFFFFFFu, "argmax: bad length");
+  argmax_first<<<1, 1024, 0, pick(stream)>>>(x, static_cast<int>(n), out);
+  LLMI_TRY_HIP(hipGetLastError());
+  return LLMI_OK;
+}
+
+int llmi_hip_model_create(const llmi_model_config* cfg, const float* const* tensors, int type, llmi_hip_model** model) {
+  return create_model(cfg, tensors, type, false, model);
+}
+
+int llmi_hip_model_create_dev(const llmi_model_config* cfg, const float* const* tensors_dev, int type,
+                              llmi_hip_model** model) {
+  return create_model(cfg, tensors_dev, type, true, model);
+}
+
+int llmi_hip_model_free(llmi_hip_model* m) {
+  if (m == nullptr) return LLMI_OK;
+  if (library_stream() != nullptr) (void)hipStreamSynchronize(library_stream());
+  for (void* p : m->allocations) (void)hipFree(p);
+  if (m->cos_t != nullptr) (void)hipFree(m->cos_t);
+  if (m->sin_t != nullptr) (void)hipFree(m->sin_t);
+  free_workspace(m->ws);
+  delete m;
+  return LLMI_OK;
+}
+
+size_t llmi_hip_model_weight_bytes(const llmi_hip_model* m) {
+  if (m == nullptr) return 0;
+  auto qbytes = [&](std::size_t out, std::size_t in) {
+    return out * row_bytes(in, m->type) + out * ceil_div(in, kBlock) * sizeof(float);
+  };
+  std::size_t total = qbytes(m->V, m->H) + (m->tied ? 0 : qbytes(m->V, m->H));
+  total += m->layers.size() * (qbytes(m->Q, m->H) + 2 * qbytes(m->KV, m->H) + qbytes(m->H, m->Q) +
+                               2 * qbytes(m->F, m->H) + qbytes(m->H, m->F));
+  return total;
+}
+
+int llmi_hip_model_new_cache(llmi_hip_model* m, size_t max_len, llmi_hip_cache** cache) {
+  LLMI_REQUIRE_INIT();
+  LLMI_REQUIRE(m != nullptr && cache != nullptr, "new_cache: null pointer");
+  *cache = nullptr;
+  const std::size_t cap = std::min<std::size_t>(max_len, m->c.max_position_embeddings);
+  if (cap == 0) return fail(LLMI_ERR_ARG, "new_cache: max_len must be positive");
+  LLMI_REQUIRE(attention_lds(cap) + 4096 <= max_lds_per_block(), "new_cache: capacity exceeds the attention kernel's LDS");
+  if (int rc = ensure_tables(m, cap)) return rc;
+  auto c = std::make_unique<llmi_hip_cache>();
+  c->model = m;
+  c->cap = cap;
+  const std::size_t n = m->layers.size() * m->c.num_kv_heads * cap * m->hd;
+  LLMI_TRY_HIP(hipMalloc(&c->k, n * sizeof(float)));
+  if (hipMalloc(&c->v, n * sizeof(float)) != hipSuccess) {
+    (void)hipFree(c->k);
+    return fail(LLMI_ERR_HIP, "new_cache: hipMalloc");
+  }
+  *cache = c.release();
+  return LLMI_OK;
+}
+
+int llmi_hip_cache_free(llmi_hip_cache* c) {
+  if (c == nullptr) return LLMI_OK;
+  if (library_stream() != nullptr) (void)hipStreamSynchronize(library_stream());
+  (void)hipFree(c->k);
+  (void)hipFree(c->v);
+  delete c;
+  return LLMI_OK;
+}
+
+size_t llmi_hip_cache_length(const llmi_hip_cache* c) { return c == nullptr ? 0 : c->len; }
+size_t llmi_hip_cache_capacity(const llmi_hip_cache* c) { return c == nullptr ? 0 : c->cap; }
+int llmi_hip_cache_reset(llmi_hip_cache* c) {
+  LLMI_REQUIRE(c != nullptr, "cache_reset: null cache");
+  c->len = 0;
+  return LLMI_OK;
+}
+
+int llmi_hip_model_forward_cached(llmi_hip_model* m, llmi_hip_cache* cache, const int32_t* tokens, size_t n,
+                                  int all_positions, float* logits) {
+  LLMI_REQUIRE_INIT();
+  LLMI_REQUIRE(m != nullptr, "forward_cached: null model");
+  if (int rc = validate(m, cache, tokens, n)) return rc;
+  if (int rc = ensure_workspace(m, n)) return rc;
+  hipStream_t s = library_stream();
+  LLMI_TRY_HIP(hipMemcpyAsync(m->ws.ids, tokens, n * sizeof(std::int32_t), hipMemcpyHostToDevice, s));
+  if (int rc = forward_device(m, cache, n, all_positions != 0, s)) return rc;
+  const std::size_t rows = all_positions ? n : 1;
+  if (logits != nullptr)
+    LLMI_TRY_HIP(hipMemcpyAsync(logits, m->ws.logits, rows * m->V * sizeof(float), hipMemcpyDeviceToHost, s));
+  LLMI_TRY_HIP(hipStreamSynchronize(s));
+  return LLMI_OK;
+}
+
+// transformer.cpp:308-327: prefill once, then one token per step; the argmax
+// runs on the device and feeds the next step's embedding gather directly.
+int llmi_hip_model_generate_greedy(llmi_hip_model* m, const int32_t* prompt, size_t n, size_t max_new,
+                                   const int32_t* stop_ids, size_t n_stop, int32_t* ids, size_t* n_ids) {
+  LLMI_REQUIRE_INIT();
+  LLMI_REQUIRE(m != nullptr && ids != nullptr && n_ids != nullptr, "generate_greedy: null pointer");
+  *n_ids = 0;
+  llmi_hip_cache* cache = nullptr;
+  if (int rc = llmi_hip_model_new_cache(m, n + max_new, &cache)) return rc;
+  std::unique_ptr<llmi_hip_cache, int (*)(llmi_hip_cache*)> guard(cache, llmi_hip_cache_free);
+  if (int rc = validate(m, cache, prompt, n)) return rc;
+  if (max_new == 0) return LLMI_OK;
+  if (int rc = ensure_workspace(m, n)) return rc;
+  hipStream_t s = library_stream();
+  Workspace& w = m->ws;
+  LLMI_TRY_HIP(hipMemcpyAsync(w.ids, prompt, n * sizeof(std::int32_t), hipMemcpyHostToDevice, s));
+  if (int rc = forward_device(m, cache, n, false, s)) return rc;
+  const int V = static_cast<int>(m->V);
+  for (std::size_t step = 0; step < max_new; ++step) {
+    argmax_first<<<1, 1024, 0, s>>>(w.logits, V, w.ids);
+    LLMI_TRY_HIP(hipGetLastError());
+    std::int32_t next = 0;
+    LLMI_TRY_HIP(hipMemcpyAsync(&next, w.ids, sizeof(next), hipMemcpyDeviceToHost, s));
+    LLMI_TRY_HIP(hipStreamSynchronize(s));
+    ids[step] = next;
+    *n_ids = step + 1;
+    bool stop = false;
+    for (std::size_t k = 0; k < n_stop; ++k) stop = stop || stop_ids[k] == next;
+    if (stop || step + 1 == max_new) break;
+    if (cache->len + 1 > cache->cap) return fail(LLMI_ERR_STATE, "forward_cached: cache is full");
+    if (int rc = forward_device(m, cache, 1, false, s)) return rc;
+  }
+  return LLMI_OK;
+}
+
+}  // extern "C"

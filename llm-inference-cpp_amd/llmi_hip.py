@@ -38,6 +38,10 @@ SIGNATURES = {
     "llmi_hip_event_destroy": (_i, [_vp]),
     "llmi_hip_event_record": (_i, [_vp, _vp]),
     "llmi_hip_event_elapsed_ms": (_i, [_vp, _vp, C.POINTER(_f)]),
+    "llmi_hip_graph_begin": (_i, []),
+    "llmi_hip_graph_end": (_i, [C.POINTER(_vp)]),
+    "llmi_hip_graph_launch": (_i, [_vp]),
+    "llmi_hip_graph_destroy": (_i, [_vp]),
     "llmi_hip_synth_normal_dev": (_i, [_vp, _sz, _u64, _u64, _d, _d, _vp]),
     "llmi_hip_row_bytes": (_sz, [_sz, _i]),
     "llmi_hip_quantize": (_i, [_vp, _sz, _sz, _i, _vp, _vp]),
@@ -53,6 +57,22 @@ SIGNATURES = {
     "llmi_hip_dequantize_rows_dev": (_i, [_vp, _vp, _sz, _vp, _vp]),
     "llmi_hip_matmul": (_i, [_vp, _vp, _sz, _sz, _sz, _vp, _vp]),
     "llmi_hip_matmul_dev": (_i, [_vp, _vp, _sz, _vp, _vp, _vp]),
+    "llmi_hip_dot_dev": (_i, [_vp, _vp, _vp, _sz, _vp, _vp]),
+    "llmi_hip_rmsnorm_dev": (_i, [_vp, _vp, _sz, _sz, _f, _vp, _vp]),
+    "llmi_hip_softmax_dev": (_i, [_vp, _sz, _sz, _vp]),
+    "llmi_hip_silu_dev": (_i, [_vp, _sz, _vp]),
+    "llmi_hip_argmax_dev": (_i, [_vp, _sz, _vp, _vp]),
+    "llmi_hip_model_create": (_i, [_vp, _vp, _i, C.POINTER(_vp)]),
+    "llmi_hip_model_create_dev": (_i, [_vp, _vp, _i, C.POINTER(_vp)]),
+    "llmi_hip_model_free": (_i, [_vp]),
+    "llmi_hip_model_weight_bytes": (_sz, [_vp]),
+    "llmi_hip_model_new_cache": (_i, [_vp, _sz, C.POINTER(_vp)]),
+    "llmi_hip_cache_free": (_i, [_vp]),
+    "llmi_hip_cache_length": (_sz, [_vp]),
+    "llmi_hip_cache_capacity": (_sz, [_vp]),
+    "llmi_hip_cache_reset": (_i, [_vp]),
+    "llmi_hip_model_forward_cached": (_i, [_vp, _vp, _vp, _sz, _i, _vp]),
+    "llmi_hip_model_generate_greedy": (_i, [_vp, _vp, _sz, _sz, _vp, _sz, _vp, C.POINTER(_sz)]),
 }
 
 
@@ -254,6 +274,156 @@ class Timer:
         try:
             self.lib.llmi_hip_event_destroy(self.start_ev)
             self.lib.llmi_hip_event_destroy(self.stop_ev)
+        except Exception:
+            pass
+
+
+class ModelConfig(C.Structure):
+    """llmi_model_config (include/llmi_hip.h)."""
+
+    _fields_ = [
+        ("arch", C.c_int32),
+        ("vocab_size", C.c_uint32),
+        ("hidden_size", C.c_uint32),
+        ("intermediate_size", C.c_uint32),
+        ("num_layers", C.c_uint32),
+        ("num_heads", C.c_uint32),
+        ("num_kv_heads", C.c_uint32),
+        ("max_position_embeddings", C.c_uint32),
+        ("rms_norm_eps", C.c_double),
+        ("rope_theta", C.c_double),
+        ("tie_word_embeddings", C.c_int32),
+        ("qkv_bias", C.c_int32),
+    ]
+
+    @classmethod
+    def from_dict(cls, d: dict) -> "ModelConfig":
+        return cls(**{k: d[k] for k, _ in cls._fields_})
+
+
+class Cache:
+    def __init__(self, model: "Model", max_len: int):
+        self.lib = model.lib
+        h = C.c_void_p()
+        check(self.lib.llmi_hip_model_new_cache(model.h, max_len, C.byref(h)))
+        self.h = h.value
+
+    def length(self) -> int:
+        return int(self.lib.llmi_hip_cache_length(self.h))
+
+    def capacity(self) -> int:
+        return int(self.lib.llmi_hip_cache_capacity(self.h))
+
+    def reset(self) -> None:
+        check(self.lib.llmi_hip_cache_reset(self.h))
+
+    def free(self) -> None:
+        if self.h:
+            check(self.lib.llmi_hip_cache_free(self.h))
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class Model:
+    """A device-resident quantized decoder (llmi_hip_model)."""
+
+    def __init__(self, cfg: dict, tensors, qtype: int, on_device: bool = False):
+        self.lib = init()
+        self.cfg = dict(cfg)
+        self.c = ModelConfig.from_dict(cfg)
+        if on_device:
+            ptrs = [int(t) for t in tensors]
+        else:
+            self._host = [np.ascontiguousarray(t, dtype=np.float32) for t in tensors]
+            ptrs = [t.ctypes.data for t in self._host]
+        arr = (C.c_void_p * len(ptrs))(*ptrs)
+        h = C.c_void_p()
+        fn = self.lib.llmi_hip_model_create_dev if on_device else self.lib.llmi_hip_model_create
+        check(fn(C.byref(self.c), arr, qtype, C.byref(h)))
+        self._host = None
+        self.h = h.value
+
+    def weight_bytes(self) -> int:
+        return int(self.lib.llmi_hip_model_weight_bytes(self.h))
+
+    def new_cache(self, max_len: int) -> Cache:
+        return Cache(self, max_len)
+
+    def forward_cached(self, cache: Cache, tokens, all_positions: bool = False) -> np.ndarray:
+        toks = np.ascontiguousarray(tokens, dtype=np.int32)
+        rows = toks.size if all_positions else 1
+        logits = np.zeros(max(rows, 1) * self.cfg["vocab_size"], dtype=np.float32)
+        check(self.lib.llmi_hip_model_forward_cached(self.h, cache.h, _p(toks), toks.size, int(all_positions),
+                                                     _p(logits)))
+        return logits
+
+    def generate_greedy(self, prompt, max_new: int, stop_ids=()) -> np.ndarray:
+        p = np.ascontiguousarray(prompt, dtype=np.int32)
+        stop = np.ascontiguousarray(list(stop_ids), dtype=np.int32)
+        ids = np.zeros(max(max_new, 1), dtype=np.int32)
+        n = _sz()
+        check(self.lib.llmi_hip_model_generate_greedy(self.h, _p(p), p.size, max_new, _p(stop) if stop.size else None,
+                                                      stop.size, _p(ids), C.byref(n)))
+        return ids[: n.value]
+
+    def free(self) -> None:
+        if self.h:
+            check(self.lib.llmi_hip_model_free(self.h))
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+def synthetic_model_dev(cfg: dict, base_seed: int, qtype: int, convention: str = "bench") -> "Model":
+    """Builds a synthetic model whose fp32 tensors are generated on the device
+    by the synth-v1 generator (the same values synth.make_tensors gives)."""
+    import synth
+
+    bufs = []
+    for name, shape, seed, mean, std in synth.tensor_params(cfg, base_seed, convention):
+        n = int(np.prod(shape))
+        b = DeviceBuffer(n * 4)
+        if std == 0.0:
+            b.upload(np.full(n, np.float32(mean), dtype=np.float32))
+        else:
+            synth_normal_dev(b, n, seed, mean, std)
+        bufs.append(b)
+    synchronize()
+    m = Model(cfg, [b.ptr for b in bufs], qtype, on_device=True)
+    for b in bufs:
+        b.free()
+    return m
+
+
+class Graph:
+    """A captured sequence of _dev calls on the library stream."""
+
+    def __init__(self, record):
+        self.lib = init()
+        check(self.lib.llmi_hip_graph_begin())
+        try:
+            record()
+        finally:
+            g = C.c_void_p()
+            rc = self.lib.llmi_hip_graph_end(C.byref(g))
+        check(rc)
+        self.g = g.value
+
+    def launch(self) -> None:
+        check(self.lib.llmi_hip_graph_launch(self.g))
+
+    def __del__(self):
+        try:
+            self.lib.llmi_hip_graph_destroy(self.g)
         except Exception:
             pass
 

@@ -1,0 +1,194 @@
+"""GPU parity of the glue kernels and the device-resident model against the
+compiled reference: glue vectors, the reference's 2-layer test models
+(logits bit for bit), the KV-cache invariants of
+tests/transformer_test.cpp, and greedy ids of the synthetic SmolLM2-135M
+(Q8_0, 128 + 256 steps) and Qwen2.5-0.5B (Q4_0, 512 + 512 steps) models."""
+
+import hashlib
+import json
+import os
+
+import numpy as np
+import pytest
+
+import llmi_hip as H
+import oracle as O
+import synth
+
+pytestmark = pytest.mark.gpu
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def bits(a):
+    return np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
+
+
+def sha(a):
+    return hashlib.sha256(np.ascontiguousarray(a).tobytes()).hexdigest()
+
+
+# ----------------------------------------------------------------- glue
+def test_glue_kernels_match_reference(golden):
+    _, arrays = golden
+    g = arrays["kernels"]
+    lib = H.init()
+    a = H.DeviceBuffer.from_array(g["dot_a"])
+    b = H.DeviceBuffer.from_array(g["dot_b"])
+    lens = H.DeviceBuffer.from_array(g["dot_n"].astype(np.int32))
+    out = H.DeviceBuffer(4 * g["dot_n"].size)
+    H.check(lib.llmi_hip_dot_dev(a.ptr, b.ptr, lens.ptr, g["dot_n"].size, out.ptr, None))
+    H.synchronize()
+    assert np.array_equal(bits(out.download(np.float32)), bits(g["dot_out"]))
+
+    for n, eps, key in ((576, 1e-5, "rms_576"), (896, 1e-6, "rms_896")):
+        x = H.DeviceBuffer.from_array(g["rms_x"][:n])
+        w = H.DeviceBuffer.from_array(g["rms_w"][:n])
+        y = H.DeviceBuffer(4 * n)
+        H.check(lib.llmi_hip_rmsnorm_dev(x.ptr, w.ptr, 1, n, eps, y.ptr, None))
+        H.synchronize()
+        assert np.array_equal(bits(y.download(np.float32)), bits(g[key])), key
+
+    sm = H.DeviceBuffer.from_array(g["softmax_in"])
+    H.check(lib.llmi_hip_softmax_dev(sm.ptr, 1, g["softmax_in"].size, None))
+    H.synchronize()
+    assert np.array_equal(bits(sm.download(np.float32)), bits(g["softmax_out"]))
+
+    si = H.DeviceBuffer.from_array(g["silu_in"])
+    H.check(lib.llmi_hip_silu_dev(si.ptr, g["silu_in"].size, None))
+    H.synchronize()
+    assert np.array_equal(bits(si.download(np.float32)), bits(g["silu_out"]))
+
+
+def test_device_expf_and_silu_match_host_libm_over_the_range():
+    """SiLU exercises expf(-x); sweep every exponent range, including the
+    subnormal-result and overflow ends, against the oracle (host libm)."""
+    orc = O.oracle()
+    rng = np.random.default_rng(7)
+    x = np.concatenate([rng.uniform(-110, 110, 1 << 20).astype(np.float32),
+                        (rng.standard_normal(1 << 18) * 8).astype(np.float32),
+                        np.array([0.0, -0.0, 88.0, -88.0, 87.3, -87.3, 103.9, -103.9, 1e-30, -1e-30], np.float32)])
+    d = H.DeviceBuffer.from_array(x)
+    H.check(H.init().llmi_hip_silu_dev(d.ptr, x.size, None))
+    H.synchronize()
+    got = d.download(np.float32)
+    want = np.array([orc.silu(v) for v in x[:20000]] , dtype=np.float32)
+    assert np.array_equal(bits(got[:20000]), bits(want))
+    # The rest through softmax rows (expf of non-positive arguments).
+    rows = x[20000:20000 + 64 * 1000].reshape(64, 1000)
+    d2 = H.DeviceBuffer.from_array(rows)
+    H.check(H.init().llmi_hip_softmax_dev(d2.ptr, 64, 1000, None))
+    H.synchronize()
+    got2 = d2.download(np.float32).reshape(64, 1000)
+    for r in range(64):
+        assert np.array_equal(bits(got2[r]), bits(orc.softmax(rows[r]))), r
+
+
+def test_argmax_takes_the_first_maximum():
+    lib = H.init()
+    out = H.DeviceBuffer(4)
+    for x, want in (([1, 3, 2, 3], 1), ([5.0], 0), ([-1, -1, -1], 0)):
+        d = H.DeviceBuffer.from_array(np.array(x, np.float32))
+        H.check(lib.llmi_hip_argmax_dev(d.ptr, len(x), out.ptr, None))
+        H.synchronize()
+        assert int(out.download(np.int32)[0]) == want
+    big = synth.normal(3, 151936, 0.0, 1.0)
+    big[[100, 90000, 150000]] = 9.0
+    d = H.DeviceBuffer.from_array(big)
+    H.check(lib.llmi_hip_argmax_dev(d.ptr, big.size, out.ptr, None))
+    H.synchronize()
+    assert int(out.download(np.int32)[0]) == 100
+
+
+# ---------------------------------------------------------- tiny models
+def test_tiny_models_match_reference(golden):
+    rec, arrays = golden
+    g = arrays["tiny_models"]
+    for c in rec["tiny_models"]:
+        if c["type"] == O.F32:
+            continue  # the f32 path is not part of this library
+        m = H.Model(c["cfg"], synth.make_tensors(c["cfg"], c["seed"], c["convention"]), c["type"])
+        cache = m.new_cache(len(g["prompt"]) + len(g["steps"]))
+        pre = m.forward_cached(cache, g["prompt"], all_positions=True)
+        assert np.array_equal(bits(pre), bits(g[c["key"] + "_prefill"])), c["key"]
+        for i, s in enumerate(g["steps"]):
+            assert np.array_equal(bits(m.forward_cached(cache, [s])), bits(g[c["key"] + "_steps"][i])), (c["key"], i)
+        assert cache.length() == len(g["prompt"]) + len(g["steps"])
+        ids = m.generate_greedy(np.array([1, 2, 3], np.int32), 12)
+        assert np.array_equal(ids, g[c["key"] + "_greedy"]), c["key"]
+        cache.free()
+        m.free()
+
+
+def test_kv_cache_invariants_and_causality():
+    """transformer_test.cpp:322-381 and :201-218 on the device model."""
+    for arch in (0, 1):
+        cfg = synth.tiny(arch, True)
+        for qt in (H.Q8_0, H.Q4_0):
+            m = H.Model(cfg, synth.make_tensors(cfg, 11, "tiny"), qt)
+            ids = np.array([2, 17, 4, 9, 21, 0, 13], np.int32)
+            c1 = m.new_cache(len(ids))
+            allpos = m.forward_cached(c1, ids, all_positions=True).reshape(len(ids), -1)
+            c2 = m.new_cache(len(ids))
+            for t, tok in enumerate(ids):
+                assert np.array_equal(bits(m.forward_cached(c2, [tok])), bits(allpos[t])), (arch, qt, t)
+            c3 = m.new_cache(len(ids))
+            m.forward_cached(c3, ids[:3])
+            for t in range(3, len(ids)):
+                assert np.array_equal(bits(m.forward_cached(c3, [ids[t]])), bits(allpos[t]))
+            other = ids.copy()
+            other[4] = 1
+            c4 = m.new_cache(len(ids))
+            alt = m.forward_cached(c4, other, all_positions=True).reshape(len(ids), -1)
+            assert np.array_equal(bits(alt[:4]), bits(allpos[:4]))
+            assert not np.array_equal(alt[4:], allpos[4:])
+            # Stop ids end generation right after the stop token.
+            full = m.generate_greedy(np.array([1, 2], np.int32), 10)
+            stopped = m.generate_greedy(np.array([1, 2], np.int32), 10, stop_ids=[int(full[2])])
+            assert np.array_equal(stopped, full[:3])
+            for c in (c1, c2, c3, c4):
+                c.free()
+            m.free()
+
+
+def test_bad_input_is_reported_like_the_reference():
+    """transformer_test.cpp:242-250, :400-411."""
+    cfg = synth.tiny(0, True)
+    m = H.Model(cfg, synth.make_tensors(cfg, 6, "tiny"), H.Q8_0)
+    other = H.Model(cfg, synth.make_tensors(cfg, 7, "tiny"), H.Q8_0)
+    c = m.new_cache(3)
+    for bad, msg in (([], "no tokens"), ([32], "out of range"), ([-1], "out of range")):
+        with pytest.raises(H.HipError, match=msg):
+            m.forward_cached(c, bad)
+    with pytest.raises(H.HipError, match="not created by this model"):
+        other.forward_cached(c, [1])
+    m.forward_cached(c, [1, 2, 3])
+    with pytest.raises(H.HipError, match="cache is full"):
+        m.forward_cached(c, [4])
+    c.reset()
+    m.forward_cached(c, [1, 2, 3])
+    with pytest.raises(H.HipError, match="max_len must be positive"):
+        m.new_cache(0)
+    with pytest.raises(H.HipError):
+        H.Model(cfg, synth.make_tensors(cfg, 6, "tiny"), H.F32)
+
+
+# ---------------------------------------------------- full-size models
+@pytest.mark.parametrize("name", ["c3_smollm2_q8", "c4_qwen25_q4"])
+def test_synthetic_model_greedy_ids_match_reference(name):
+    with open(os.path.join(GOLDEN, name + ".json")) as f:
+        rec = json.load(f)
+    cfg = rec["cfg"]
+    m = H.synthetic_model_dev(cfg, rec["seed"], rec["type"], rec["convention"])
+    want_wb = {"c3_smollm2_q8": 151_289_856, "c4_qwen25_q4": 308_725_760}[name]
+    assert m.weight_bytes() == want_wb
+    prompt = synth.uniform_ids(rec["prompt_seed"], rec["n_prompt"], cfg["vocab_size"])
+    cache = m.new_cache(rec["n_prompt"] + 1)
+    logits = m.forward_cached(cache, prompt)
+    assert sha(logits) == rec["first_logits_sha256"], (name, np.argsort(-logits)[:8], rec["first_logits_top"])
+    cache.free()
+    ids = m.generate_greedy(prompt, rec["n_steps"])
+    want = np.array(rec["ids"], dtype=np.int32)
+    if not np.array_equal(ids, want):
+        k = int(np.argmax(ids != want))
+        pytest.fail(f"{name}: first divergence at step {k} (margin there {rec['margins'][k]:.3g})")
+    m.free()
