@@ -143,8 +143,10 @@ def test_kv_cache_invariants_and_causality():
             assert not np.array_equal(alt[4:], allpos[4:])
             # Stop ids end generation right after the stop token.
             full = m.generate_greedy(np.array([1, 2], np.int32), 10)
-            stopped = m.generate_greedy(np.array([1, 2], np.int32), 10, stop_ids=[int(full[2])])
-            assert np.array_equal(stopped, full[:3])
+            stop = int(full[2])
+            first = int(np.argmax(full == stop))
+            stopped = m.generate_greedy(np.array([1, 2], np.int32), 10, stop_ids=[stop])
+            assert np.array_equal(stopped, full[:first + 1])
             for c in (c1, c2, c3, c4):
                 c.free()
             m.free()
