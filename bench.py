@@ -96,16 +96,23 @@ def activations(shapes, batch, seed):
     return xs, ys, cache
 
 
-def time_steps(wset, batch, steps, warmup):
+def time_steps(wset, batch, steps, warmup, graphs=True):
+    """GPU time of `steps` passes; each pass replays one HIP graph holding its
+    weight copy's 211 launches (graphs=False: plain launches from Python)."""
     xs, ys, keep = activations(wset.shapes, batch, 77)
     n = len(wset.copies)
+    if graphs:
+        gs = [H.Graph(lambda ws=ws: run_step(ws, xs, ys, batch)) for ws in wset.copies]
+        run = lambda i: gs[i % n].launch()  # noqa: E731
+    else:
+        run = lambda i: run_step(wset.copies[i % n], xs, ys, batch)  # noqa: E731
     for i in range(warmup):
-        run_step(wset.copies[i % n], xs, ys, batch)
+        run(i)
     H.synchronize()
     t = H.Timer()
     t.start()
     for i in range(steps):
-        run_step(wset.copies[(warmup + i) % n], xs, ys, batch)
+        run(warmup + i)
     ms = t.stop()
     H.synchronize()
     del keep
@@ -159,6 +166,43 @@ def target_shapes():
             w.free()
     if stage is not None:
         stage.free()
+    return res
+
+
+DECODE_RUNS = [  # (key, golden fixture, model config, weight type): BASELINE.json configs[2], configs[3]
+    ("c3_smollm2_135m_q8_0", "c3_smollm2_q8", synth.SMOLLM2_135M, H.Q8_0),
+    ("c4_qwen25_05b_q4_0", "c4_qwen25_q4", synth.QWEN25_05B, H.Q4_0),
+]
+
+
+def decode_runs():
+    """Full-model greedy decode on the synthetic models: prefill the prompt,
+    then the configured number of greedy steps; ids are checked against the
+    reference's (tests/golden)."""
+    res = {}
+    for key, golden, cfg, qt in DECODE_RUNS:
+        with open(os.path.join(ROOT, "tests", "golden", golden + ".json")) as f:
+            rec = json.load(f)
+        m = H.synthetic_model_dev(cfg, rec["seed"], qt, rec["convention"])
+        prompt = synth.uniform_ids(rec["prompt_seed"], rec["n_prompt"], cfg["vocab_size"])
+        m.generate_greedy(prompt[:8], 4)  # warm-up (code objects, workspace)
+        ids = m.generate_greedy(prompt, rec["n_steps"])
+        pre_ms, dec_ms = m.last_timing()
+        wb = m.weight_bytes()
+        n_kv = cfg["num_layers"] * cfg["num_kv_heads"] * (cfg["hidden_size"] // cfg["num_heads"]) * 4 * 2
+        mean_ctx = rec["n_prompt"] + rec["n_steps"] / 2.0
+        bytes_per_token = wb + n_kv * mean_ctx
+        tok_s = rec["n_steps"] / (dec_ms * 1e-3)
+        roof = HBM_PEAK_GBS * 1e9 / bytes_per_token
+        res[key] = dict(prompt=rec["n_prompt"], steps=rec["n_steps"], weights=H.TYPE_NAMES[qt],
+                        prefill_ms=round(pre_ms, 2), prefill_tok_s=round(rec["n_prompt"] / (pre_ms * 1e-3), 1),
+                        decode_ms=round(dec_ms, 2), decode_tok_s=round(tok_s, 1),
+                        bytes_per_token=int(bytes_per_token), roofline_tok_s=round(roof, 1),
+                        frac_of_roofline=round(tok_s / roof, 4),
+                        ids_match_reference=bool(np.array_equal(ids, np.array(rec["ids"], np.int32))))
+        print(f"[bench] {key}: prefill {pre_ms:.1f} ms, decode {tok_s:.1f} tok/s, ids match "
+              f"{res[key]['ids_match_reference']}", file=sys.stderr, flush=True)
+        m.free()
     return res
 
 
@@ -216,6 +260,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-targets", action="store_true", help="skip the Qwen2.5 shape table")
+    ap.add_argument("--no-decode", action="store_true", help="skip the full-model decode runs")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
@@ -233,6 +278,7 @@ def main():
     wset = WeightSet(shapes, H.Q4_0, copies, 1)
 
     ms_b1 = time_steps(wset, 1, args.steps, args.warmup)
+    ms_b1_plain = time_steps(wset, 1, max(1, args.steps // 4), args.warmup, graphs=False)
     ms_b8 = time_steps(wset, 8, max(1, args.steps // 4), args.warmup)
     step_ms = ms_b1 / args.steps
     value = bytes_b1 / (step_ms * 1e-3) / 1e9
@@ -247,6 +293,7 @@ def main():
     wset.free()
 
     targets = {} if args.no_targets else target_shapes()
+    decode = {} if args.no_decode else decode_runs()
     cpu = None if args.no_cpu else cpu_baseline()
 
     line = {
@@ -270,6 +317,8 @@ def main():
             "algorithmic_bytes_per_step": bytes_b1,
             "rotating_weight_copies": copies,
             "pct_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
+            "launch": "one HIP graph replay per step (211 kernels)",
+            "ms_per_step_plain_launches": round(ms_b1_plain / max(1, args.steps // 4), 4),
             "batch8": {"ms_per_step": round(b8_step_ms, 4),
                        "gbs": round(bytes_b8 / (b8_step_ms * 1e-3) / 1e9, 2)},
         },
@@ -285,6 +334,7 @@ def main():
             "mean_launch_us": round(head_ms * 1e3, 3),
         },
         "targets_qwen25": targets,
+        "decode": decode,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -221,6 +221,10 @@ int llmi_hip_model_forward_cached(llmi_hip_model* model, llmi_hip_cache* cache, 
  * stop_ids.  Writes *n_ids ids to `ids` (room for max_new). */
 int llmi_hip_model_generate_greedy(llmi_hip_model* model, const int32_t* prompt, size_t n, size_t max_new,
                                    const int32_t* stop_ids, size_t n_stop, int32_t* ids, size_t* n_ids);
+/* GPU time of the last generate_greedy call: the prompt prefill and the
+ * decode loop (HIP events; the reference's llmi-generate --json reports the
+ * same split as wall-clock seconds, apps/llmi-generate/main.cpp:329-345). */
+int llmi_hip_model_last_timing(const llmi_hip_model* model, double* prefill_ms, double* decode_ms);
 
 #ifdef __cplusplus
 } /* extern "C" */

@@ -268,7 +268,8 @@ __global__ void __launch_bounds__(kThreads) silu_mul(float* __restrict__ g, cons
 
 // --------------------------------------------------------------- argmax
 // First maximum (lowest index on ties) of x[0..n); one 1024-thread block.
-__global__ void __launch_bounds__(1024) argmax_first(const float* __restrict__ x, int n, std::int32_t* __restrict__ out) {
+__global__ void __launch_bounds__(1024) argmax_first(const float* __restrict__ x, int n, std::int32_t* __restrict__ out,
+                                                     std::int32_t* __restrict__ also) {
   __shared__ float bv[1024];
   __shared__ int bi[1024];
   const int tid = threadIdx.x;
@@ -295,7 +296,11 @@ __global__ void __launch_bounds__(1024) argmax_first(const float* __restrict__ x
     }
     __syncthreads();
   }
-  if (tid == 0) *out = bi[0] < 0 ? 0 : bi[0];
+  if (tid == 0) {
+    const int r = bi[0] < 0 ? 0 : bi[0];
+    *out = r;
+    if (also != nullptr) *also = r;
+  }
 }
 
 // Standalone glue kernels (the device counterparts of kernels.hpp:13-32).
@@ -360,6 +365,8 @@ struct Workspace {
         *u = nullptr, *logits = nullptr;
   std::int32_t* ids = nullptr;
   std::int32_t* next = nullptr;  // argmax result
+  std::int32_t* gen = nullptr;   // generated ids of the current greedy run
+  std::size_t gen_cap = 0;
 };
 
 }  // namespace llmi_hip
@@ -378,6 +385,7 @@ struct llmi_hip_model {
   std::size_t table_len = 0;
   llmi_hip::Workspace ws;
   std::vector<void*> allocations;
+  double last_prefill_ms = 0.0, last_decode_ms = 0.0;  // of the last greedy run
 };
 
 struct llmi_hip_cache {
@@ -542,7 +550,8 @@ int ensure_tables(llmi_hip_model* m, std::size_t n) {
 void free_workspace(Workspace& w) {
   for (void* p : {static_cast<void*>(w.x), static_cast<void*>(w.h), static_cast<void*>(w.q), static_cast<void*>(w.k),
                   static_cast<void*>(w.v), static_cast<void*>(w.att), static_cast<void*>(w.g), static_cast<void*>(w.u),
-                  static_cast<void*>(w.logits), static_cast<void*>(w.ids), static_cast<void*>(w.next)})
+                  static_cast<void*>(w.logits), static_cast<void*>(w.ids), static_cast<void*>(w.next),
+                  static_cast<void*>(w.gen)})
     if (p != nullptr) (void)hipFree(p);
   w = Workspace{};
 }
@@ -679,7 +688,7 @@ int llmi_hip_silu_dev(float* x, size_t n, void* stream) {
 int llmi_hip_argmax_dev(const float* x, size_t n, int32_t* out, void* stream) {
   LLMI_REQUIRE_INIT();
   LLMI_REQUIRE(n > 0 && n <= 0x7FFFFFFFu, "argmax: bad length");
-  argmax_first<<<1, 1024, 0, pick(stream)>>>(x, static_cast<int>(n), out);
+  argmax_first<<<1, 1024, 0, pick(stream)>>>(x, static_cast<int>(n), out, nullptr);
   LLMI_TRY_HIP(hipGetLastError());
   return LLMI_OK;
 }
@@ -771,6 +780,8 @@ int llmi_hip_model_forward_cached(llmi_hip_model* m, llmi_hip_cache* cache, cons
 
 // transformer.cpp:308-327: prefill once, then one token per step; the argmax
 // runs on the device and feeds the next step's embedding gather directly.
+// Without stop ids nothing waits for the host between steps: the ids collect
+// in device memory and are copied back once.
 int llmi_hip_model_generate_greedy(llmi_hip_model* m, const int32_t* prompt, size_t n, size_t max_new,
                                    const int32_t* stop_ids, size_t n_stop, int32_t* ids, size_t* n_ids) {
   LLMI_REQUIRE_INIT();
@@ -782,25 +793,61 @@ int llmi_hip_model_generate_greedy(llmi_hip_model* m, const int32_t* prompt, siz
   if (int rc = validate(m, cache, prompt, n)) return rc;
   if (max_new == 0) return LLMI_OK;
   if (int rc = ensure_workspace(m, n)) return rc;
-  hipStream_t s = library_stream();
   Workspace& w = m->ws;
+  if (w.gen_cap < max_new) {
+    if (w.gen != nullptr) (void)hipFree(w.gen);
+    w.gen = nullptr;
+    w.gen_cap = 0;
+    LLMI_TRY_HIP(hipMalloc(&w.gen, max_new * sizeof(std::int32_t)));
+    w.gen_cap = max_new;
+  }
+  hipStream_t s = library_stream();
+  hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
+  for (auto& e : ev) LLMI_TRY_HIP(hipEventCreate(&e));
+  struct EvGuard {
+    hipEvent_t* e;
+    ~EvGuard() {
+      for (int i = 0; i < 3; ++i)
+        if (e[i] != nullptr) (void)hipEventDestroy(e[i]);
+    }
+  } ev_guard{ev};
   LLMI_TRY_HIP(hipMemcpyAsync(w.ids, prompt, n * sizeof(std::int32_t), hipMemcpyHostToDevice, s));
+  LLMI_TRY_HIP(hipEventRecord(ev[0], s));
   if (int rc = forward_device(m, cache, n, false, s)) return rc;
+  LLMI_TRY_HIP(hipEventRecord(ev[1], s));
   const int V = static_cast<int>(m->V);
+  std::size_t produced = 0;
   for (std::size_t step = 0; step < max_new; ++step) {
-    argmax_first<<<1, 1024, 0, s>>>(w.logits, V, w.ids);
+    argmax_first<<<1, 1024, 0, s>>>(w.logits, V, w.ids, w.gen + step);
     LLMI_TRY_HIP(hipGetLastError());
-    std::int32_t next = 0;
-    LLMI_TRY_HIP(hipMemcpyAsync(&next, w.ids, sizeof(next), hipMemcpyDeviceToHost, s));
-    LLMI_TRY_HIP(hipStreamSynchronize(s));
-    ids[step] = next;
-    *n_ids = step + 1;
-    bool stop = false;
-    for (std::size_t k = 0; k < n_stop; ++k) stop = stop || stop_ids[k] == next;
-    if (stop || step + 1 == max_new) break;
-    if (cache->len + 1 > cache->cap) return fail(LLMI_ERR_STATE, "forward_cached: cache is full");
+    produced = step + 1;
+    if (n_stop > 0) {
+      std::int32_t next = 0;
+      LLMI_TRY_HIP(hipMemcpyAsync(&next, w.ids, sizeof(next), hipMemcpyDeviceToHost, s));
+      LLMI_TRY_HIP(hipStreamSynchronize(s));
+      bool stop = false;
+      for (std::size_t k = 0; k < n_stop; ++k) stop = stop || stop_ids[k] == next;
+      if (stop) break;
+    }
+    if (step + 1 == max_new) break;
     if (int rc = forward_device(m, cache, 1, false, s)) return rc;
   }
+  LLMI_TRY_HIP(hipEventRecord(ev[2], s));
+  LLMI_TRY_HIP(hipMemcpyAsync(ids, w.gen, produced * sizeof(std::int32_t), hipMemcpyDeviceToHost, s));
+  LLMI_TRY_HIP(hipStreamSynchronize(s));
+  float pre = 0.0f, dec = 0.0f;
+  LLMI_TRY_HIP(hipEventElapsedTime(&pre, ev[0], ev[1]));
+  LLMI_TRY_HIP(hipEventElapsedTime(&dec, ev[1], ev[2]));
+  m->last_prefill_ms = pre;
+  m->last_decode_ms = dec;
+  *n_ids = produced;
+  return LLMI_OK;
+}
+
+int llmi_hip_model_last_timing(const llmi_hip_model* m, double* prefill_ms, double* decode_ms) {
+  LLMI_REQUIRE(m != nullptr, "last_timing: null model");
+  if (prefill_ms != nullptr) *prefill_ms = m->last_prefill_ms;
+  if (decode_ms != nullptr) *decode_ms = m->last_decode_ms;
   return LLMI_OK;
 }
 

@@ -73,6 +73,7 @@ SIGNATURES = {
     "llmi_hip_cache_reset": (_i, [_vp]),
     "llmi_hip_model_forward_cached": (_i, [_vp, _vp, _vp, _sz, _i, _vp]),
     "llmi_hip_model_generate_greedy": (_i, [_vp, _vp, _sz, _sz, _vp, _sz, _vp, C.POINTER(_sz)]),
+    "llmi_hip_model_last_timing": (_i, [_vp, C.POINTER(_d), C.POINTER(_d)]),
 }
 
 
@@ -370,6 +371,12 @@ class Model:
         check(self.lib.llmi_hip_model_generate_greedy(self.h, _p(p), p.size, max_new, _p(stop) if stop.size else None,
                                                       stop.size, _p(ids), C.byref(n)))
         return ids[: n.value]
+
+    def last_timing(self):
+        """(prefill_ms, decode_ms) of the last generate_greedy call."""
+        a, b = _d(), _d()
+        check(self.lib.llmi_hip_model_last_timing(self.h, C.byref(a), C.byref(b)))
+        return a.value, b.value
 
     def free(self) -> None:
         if self.h:

@@ -88,3 +88,35 @@ def test_device_pointer_entry_point_and_determinism():
             first = y
         assert np.array_equal(bits(y), bits(first))
     assert np.array_equal(bits(first), bits(orc.matmul(x, 1, n_in, data, scales, qt, out, None)))
+
+
+def test_graph_replays_match_eager_launches():
+    """A captured sequence of matmuls, replayed several times with other
+    eager work and synchronisations in between, gives the eager result on
+    every replay."""
+    orc = O.oracle()
+    shapes = [(576, 576, O.Q4_0), (1536, 576, O.Q8_0), (576, 1536, O.Q4_0), (49152, 576, O.Q4_0)]
+    weights, xs, ys, want = [], [], [], []
+    for i, (out, n_in, qt) in enumerate(shapes):
+        w = synth.normal(50 + i, out * n_in, 0.0, 0.02)
+        data, scales = orc.quantize(w, out, n_in, qt)
+        weights.append(H.Weight.upload(data, scales, out, n_in, qt))
+        x = synth.normal(60 + i, n_in, 0.0, 1.0)
+        xs.append(H.DeviceBuffer.from_array(x))
+        ys.append(H.DeviceBuffer(out * 4))
+        want.append(orc.matmul(x, 1, n_in, data, scales, qt, out, None))
+
+    def record():
+        for w, x, y in zip(weights, xs, ys):
+            w.matmul_dev(x.ptr, 1, None, y.ptr)
+
+    g = H.Graph(record)
+    other = weights[1]
+    for rep in range(4):
+        for y in ys:
+            y.upload(np.zeros(y.nbytes // 4, np.float32))
+        g.launch()
+        other.matmul_dev(xs[1].ptr, 1, None, ys[1].ptr)  # eager work between replays
+        H.synchronize()
+        for i, y in enumerate(ys):
+            assert np.array_equal(bits(y.download(np.float32)), bits(want[i])), (rep, i)
