@@ -120,28 +120,23 @@ def time_steps(wset, batch, steps, warmup, graphs=True):
 
 
 def time_launches(weights, batch, launches):
-    """Mean duration of single launches, each bracketed by its own events."""
+    """Mean GPU time per launch of `launches` back-to-back launches (cycling
+    through the rotating weight copies) between one pair of HIP events on
+    the library stream.  Includes the ~2 us stream dispatch gap between
+    kernels; an event pair around each single launch would add ~6 us more."""
     n_in, out = weights[0].n_in, weights[0].out
     xb = H.DeviceBuffer(batch * n_in * 4)
     H.synth_normal_dev(xb, batch * n_in, 5, 0.0, 1.0)
     yb = H.DeviceBuffer(batch * out * 4)
-    timers = [H.Timer() for _ in range(launches)]
     weights[0].matmul_dev(xb.ptr, batch, None, yb.ptr)  # warm-up (code load)
     H.synchronize()
-    lib = H.init()
-    for i, t in enumerate(timers):
-        H.check(lib.llmi_hip_event_record(t.start_ev, None))
+    t = H.Timer()
+    t.start()
+    for i in range(launches):
         weights[(i + 1) % len(weights)].matmul_dev(xb.ptr, batch, None, yb.ptr)
-        H.check(lib.llmi_hip_event_record(t.stop_ev, None))
+    ms = t.stop()
     H.synchronize()
-    import ctypes as C
-
-    total = 0.0
-    for t in timers:
-        ms = C.c_float()
-        H.check(lib.llmi_hip_event_elapsed_ms(t.start_ev, t.stop_ev, C.byref(ms)))
-        total += ms.value
-    return total / launches
+    return ms / launches
 
 
 def target_shapes():
@@ -261,6 +256,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-targets", action="store_true", help="skip the Qwen2.5 shape table")
     ap.add_argument("--no-decode", action="store_true", help="skip the full-model decode runs")
+    ap.add_argument("--no-graphs", action="store_true",
+                    help="time the linear pass with plain launches only (for profilers that do not follow graphs)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
@@ -277,9 +274,9 @@ def main():
           file=sys.stderr, flush=True)
     wset = WeightSet(shapes, H.Q4_0, copies, 1)
 
-    ms_b1 = time_steps(wset, 1, args.steps, args.warmup)
+    ms_b1 = time_steps(wset, 1, args.steps, args.warmup, graphs=not args.no_graphs)
     ms_b1_plain = time_steps(wset, 1, max(1, args.steps // 4), args.warmup, graphs=False)
-    ms_b8 = time_steps(wset, 8, max(1, args.steps // 4), args.warmup)
+    ms_b8 = time_steps(wset, 8, max(1, args.steps // 4), args.warmup, graphs=not args.no_graphs)
     step_ms = ms_b1 / args.steps
     value = bytes_b1 / (step_ms * 1e-3) / 1e9
     b8_step_ms = ms_b8 / max(1, args.steps // 4)
@@ -317,7 +314,7 @@ def main():
             "algorithmic_bytes_per_step": bytes_b1,
             "rotating_weight_copies": copies,
             "pct_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
-            "launch": "one HIP graph replay per step (211 kernels)",
+            "launch": "plain launches" if args.no_graphs else "one HIP graph replay per step (211 kernels)",
             "ms_per_step_plain_launches": round(ms_b1_plain / max(1, args.steps // 4), 4),
             "batch8": {"ms_per_step": round(b8_step_ms, 4),
                        "gbs": round(bytes_b8 / (b8_step_ms * 1e-3) / 1e9, 2)},

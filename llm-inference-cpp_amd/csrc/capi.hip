@@ -260,7 +260,10 @@ int llmi_hip_weight_upload(const uint8_t* data, const float* scales, size_t out,
   LLMI_REQUIRE(in <= 0x7FFFFFFFu, "weight_upload: in too large");
   *weight = nullptr;
   auto h = std::make_unique<llmi_hip_weight>();
-  if (int rc = alloc_matrix(out, in, type, &h->m)) return rc;
+  if (int rc = alloc_matrix(out, in, type, &h->m)) {
+    free_matrix(&h->m);
+    return rc;
+  }
   const std::size_t nd = out * row_bytes(in, type), ns = out * ceil_div(in, kBlock);
   if (nd > 0) {
     DevBuf dd, ds;
@@ -286,7 +289,10 @@ int llmi_hip_weight_quantize_dev(const float* w, size_t out, size_t in, int type
   LLMI_REQUIRE(in <= 0x7FFFFFFFu, "weight_quantize: in too large");
   *weight = nullptr;
   auto h = std::make_unique<llmi_hip_weight>();
-  if (int rc = alloc_matrix(out, in, type, &h->m)) return rc;
+  if (int rc = alloc_matrix(out, in, type, &h->m)) {
+    free_matrix(&h->m);
+    return rc;
+  }
   if (out > 0 && in > 0) {
     int rc = launch_quantize(w, out, in, type, nullptr, nullptr, &h->m, g_stream);
     if (rc == LLMI_OK && hipStreamSynchronize(g_stream) != hipSuccess) rc = fail(LLMI_ERR_HIP, "weight_quantize: sync");

@@ -64,6 +64,13 @@ struct DeviceMatrix {
   std::size_t code_bytes = 0, scale_bytes = 0;
 };
 
+struct GemvPlan {
+  bool narrow = false;  // qgemv_narrow (16-row tiles) instead of qgemv_r1
+  int waves = 1;        // wavefronts per workgroup
+  int bpw = 1;          // blocks per wavefront (narrow: per block group)
+};
+GemvPlan plan_gemv(const DeviceMatrix& m);
+
 inline std::size_t block_code_bytes(int type) { return type == LLMI_TYPE_Q4_0 ? 16 : 32; }
 
 // Kernel launchers (implemented next to their kernels).

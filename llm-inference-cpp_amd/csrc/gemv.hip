@@ -24,9 +24,37 @@
 // wavefront per tile walks all blocks in order with the chain in registers,
 // prefetching the next chunk of blocks while it computes the current one;
 // each decoded code is used for all R rows.
+#include <algorithm>
+
 #include "common.hpp"
 
 namespace llmi_hip {
+
+// Launch shape of the batch-1 GEMV.  Matrices with many 64-row tiles use
+// qgemv_r1 (one workgroup per tile, activations in SGPRs) with enough
+// wavefronts per tile to put ~kTargetWaves in the grid.  Matrices with fewer
+// tiles than kNarrowTiles use qgemv_narrow (16-row tiles), whose 4W block
+// groups per workgroup take ~kBlocksPerGroup blocks each.
+GemvPlan plan_gemv(const DeviceMatrix& m) {
+  constexpr std::size_t kTargetWaves = 8192;
+  constexpr std::size_t kNarrowTiles = 128;
+  constexpr std::size_t kBlocksPerGroup = 2;
+  GemvPlan p;
+  const std::size_t nblk = std::max<std::size_t>(m.nblk, 1);
+  if (m.ntiles < kNarrowTiles) {
+    p.narrow = true;
+    const std::size_t groups = std::min<std::size_t>(64, ceil_div(nblk, kBlocksPerGroup));
+    p.waves = static_cast<int>(ceil_div(groups, 4));
+    p.bpw = static_cast<int>(ceil_div(nblk, static_cast<std::size_t>(p.waves) * 4));  // blocks per group
+    return p;
+  }
+  const std::size_t per_tile = std::max<std::size_t>(1, ceil_div(kTargetWaves, m.ntiles));
+  std::size_t waves = std::max<std::size_t>(1, std::min<std::size_t>({16, nblk, per_tile}));
+  p.bpw = static_cast<int>(ceil_div(nblk, waves));
+  p.waves = static_cast<int>(ceil_div(nblk, p.bpw));
+  return p;
+}
+
 namespace {
 
 // Signed bit-field extract (v_bfe_i32).  The builtin is declared with an
@@ -96,7 +124,149 @@ __device__ __noinline__ float tail_block_dot(const Block<TYPE> blk, const float*
 }
 
 // ---------------------------------------------------------------- batch 1
-// Dynamic LDS: part[nblk][64] then scale[nblk][64].
+// One workgroup per tile.  Dynamic LDS: part[nblk][64] then scale[nblk][64].
+template <int TYPE, int CH>
+__global__ void __launch_bounds__(1024) qgemv_r1(const uint4* __restrict__ codes, const float* __restrict__ scales,
+                                                 const float* __restrict__ x, const float* __restrict__ bias,
+                                                 float* __restrict__ y, int in, int nblk, int out, int bpw,
+                                                 int accumulate);
+
+// Block sums of this wavefront's blocks [b_begin, b_end) of one tile into
+// part[] (stride 64 floats per block), scales into scl[] when non-null.
+template <int TYPE, int CH>
+__device__ __forceinline__ void block_sums(const uint4* __restrict__ codes, const float* __restrict__ scales,
+                                           const float* __restrict__ x, std::size_t tile, int in, int nblk, int b_begin,
+                                           int b_end, int lane, float* part, float* scl) {
+  const int nfull = in / kBlock;
+  const int f_end = min(b_end, nfull);
+  Block<TYPE> cur[CH];
+  float cur_s[CH];
+#pragma unroll
+  for (int j = 0; j < CH; ++j) {
+    if (b_begin + j < f_end) {
+      cur[j] = load_block<TYPE>(codes, tile * nblk + b_begin + j, lane);
+      if (scl != nullptr) cur_s[j] = scales[(tile * nblk + b_begin + j) * kTileRows + lane];
+    }
+  }
+  for (int b = b_begin; b < f_end; b += CH) {
+    Block<TYPE> nxt[CH];
+    float nxt_s[CH];
+#pragma unroll
+    for (int j = 0; j < CH; ++j) {
+      if (b + CH + j < f_end) {
+        nxt[j] = load_block<TYPE>(codes, tile * nblk + b + CH + j, lane);
+        if (scl != nullptr) nxt_s[j] = scales[(tile * nblk + b + CH + j) * kTileRows + lane];
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < CH; ++j) {
+      if (b + j < f_end) {
+        std::uint32_t w[8];
+        unpack_words<TYPE>(cur[j], w);
+        part[(b + j) * kTileRows + lane] = full_block_dot<TYPE>(w, x + (b + j) * kBlock);
+        if (scl != nullptr) scl[(b + j) * kTileRows + lane] = cur_s[j];
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < CH; ++j) {
+      cur[j] = nxt[j];
+      cur_s[j] = nxt_s[j];
+    }
+  }
+  if (nfull < nblk && nfull >= b_begin && nfull < b_end) {
+    const Block<TYPE> blk = load_block<TYPE>(codes, tile * nblk + nfull, lane);
+    part[nfull * kTileRows + lane] = tail_block_dot<TYPE>(blk, x + nfull * kBlock, in - nfull * kBlock);
+    if (scl != nullptr) scl[nfull * kTileRows + lane] = scales[(tile * nblk + nfull) * kTileRows + lane];
+  }
+}
+
+// The sequential chain over all blocks of a tile (wavefront 0), from LDS.
+__device__ __forceinline__ float chain_lds(const float* part, const float* scl, int nblk, int lane) {
+  float acc = 0.0f;
+  int b = 0;
+  for (; b + 4 <= nblk; b += 4) {
+    const float p0 = part[(b + 0) * kTileRows + lane], s0 = scl[(b + 0) * kTileRows + lane];
+    const float p1 = part[(b + 1) * kTileRows + lane], s1 = scl[(b + 1) * kTileRows + lane];
+    const float p2 = part[(b + 2) * kTileRows + lane], s2 = scl[(b + 2) * kTileRows + lane];
+    const float p3 = part[(b + 3) * kTileRows + lane], s3 = scl[(b + 3) * kTileRows + lane];
+    acc = __builtin_fmaf(p0, s0, acc);
+    acc = __builtin_fmaf(p1, s1, acc);
+    acc = __builtin_fmaf(p2, s2, acc);
+    acc = __builtin_fmaf(p3, s3, acc);
+  }
+  for (; b < nblk; ++b) acc = __builtin_fmaf(part[b * kTileRows + lane], scl[b * kTileRows + lane], acc);
+  return acc;
+}
+
+// Batch 1 for matrices with few rows (qgemv_narrow): 16-row tiles, so a
+// matrix gets 4x the workgroups of the 64-row kernel.  Lane l of a
+// wavefront owns row tile16*16 + (l & 15) and one of 4 block groups
+// (l >> 4); the W wavefronts of the workgroup give 4W groups, each taking a
+// contiguous range of blocks.  The 16 rows of one block are a contiguous
+// 256-byte piece of the 64-row tiled layout, so loads stay coalesced.  The
+// activations are staged in LDS once per workgroup and read with broadcast
+// loads (16 lanes per address).  Block sums and scales go to LDS; lanes 0-15
+// of wavefront 0 run the sequential chain.
+// Dynamic LDS: x[in], part[nblk][16], scale[nblk][16].
+template <int TYPE>
+__global__ void __launch_bounds__(1024) qgemv_narrow(const uint4* __restrict__ codes, const float* __restrict__ scales,
+                                                     const float* __restrict__ x, const float* __restrict__ bias,
+                                                     float* __restrict__ y, int in, int nblk, int out, int bpg,
+                                                     int accumulate) {
+  extern __shared__ float lds[];
+  float* xs = lds;
+  float* part = lds + ((in + 3) & ~3);
+  float* scl = part + nblk * 16;
+  const int lane = threadIdx.x & 63;
+  const int r = lane & 15;
+  const int wave = threadIdx.x >> 6;
+  const int group = wave * 4 + (lane >> 4);
+  const std::size_t row = static_cast<std::size_t>(blockIdx.x) * 16 + r;
+  const std::size_t tile = row / kTileRows;
+  const int sub = static_cast<int>(row % kTileRows);
+  for (int i = threadIdx.x; i < in; i += blockDim.x) xs[i] = x[i];
+  __syncthreads();
+  const int nfull = in / kBlock;
+  const int b_begin = group * bpg;
+  const int b_end = min(nblk, b_begin + bpg);
+  for (int b = b_begin; b < b_end; ++b) {
+    const Block<TYPE> blk = load_block<TYPE>(codes, tile * nblk + b, sub);
+    const float sc = scales[(tile * nblk + b) * kTileRows + sub];
+    std::uint32_t w[8];
+    unpack_words<TYPE>(blk, w);
+    float p;
+    if (b < nfull) {
+      p = full_block_dot<TYPE>(w, xs + b * kBlock);
+    } else {
+      p = 0.0f;
+      const int len = in - b * kBlock;
+      for (int i = 0; i < len; ++i) p = __builtin_fmaf(xs[b * kBlock + i], code_of<TYPE>(w, i), p);
+    }
+    part[b * 16 + r] = p;
+    scl[b * 16 + r] = sc;
+  }
+  __syncthreads();
+  if (threadIdx.x < 16) {
+    float acc = 0.0f;
+    int b = 0;
+    for (; b + 4 <= nblk; b += 4) {
+      const float p0 = part[(b + 0) * 16 + r], s0 = scl[(b + 0) * 16 + r];
+      const float p1 = part[(b + 1) * 16 + r], s1 = scl[(b + 1) * 16 + r];
+      const float p2 = part[(b + 2) * 16 + r], s2 = scl[(b + 2) * 16 + r];
+      const float p3 = part[(b + 3) * 16 + r], s3 = scl[(b + 3) * 16 + r];
+      acc = __builtin_fmaf(p0, s0, acc);
+      acc = __builtin_fmaf(p1, s1, acc);
+      acc = __builtin_fmaf(p2, s2, acc);
+      acc = __builtin_fmaf(p3, s3, acc);
+    }
+    for (; b < nblk; ++b) acc = __builtin_fmaf(part[b * 16 + r], scl[b * 16 + r], acc);
+    if (row < static_cast<std::size_t>(out)) {
+      const float v = acc + (bias != nullptr ? bias[row] : 0.0f);
+      y[row] = accumulate ? y[row] + v : v;
+    }
+  }
+}
+
 template <int TYPE, int CH>
 __global__ void __launch_bounds__(1024) qgemv_r1(const uint4* __restrict__ codes, const float* __restrict__ scales,
                                                  const float* __restrict__ x, const float* __restrict__ bias,
@@ -108,68 +278,12 @@ __global__ void __launch_bounds__(1024) qgemv_r1(const uint4* __restrict__ codes
   const int lane = threadIdx.x & (kTileRows - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const std::size_t tile = blockIdx.x;
-  const int nfull = in / kBlock;  // blocks with 32 elements
   const int b_begin = wave * bpw;
   const int b_end = min(nblk, b_begin + bpw);
-  const int f_end = min(b_end, nfull);  // full blocks of this wavefront end here
-
-  // Full blocks, CH at a time, with the next chunk's loads in flight.
-  Block<TYPE> cur[CH];
-  float cur_s[CH];
-#pragma unroll
-  for (int j = 0; j < CH; ++j) {
-    if (b_begin + j < f_end) {
-      cur[j] = load_block<TYPE>(codes, tile * nblk + b_begin + j, lane);
-      cur_s[j] = scales[(tile * nblk + b_begin + j) * kTileRows + lane];
-    }
-  }
-  for (int b = b_begin; b < f_end; b += CH) {
-    Block<TYPE> nxt[CH];
-    float nxt_s[CH];
-#pragma unroll
-    for (int j = 0; j < CH; ++j) {
-      if (b + CH + j < f_end) {
-        nxt[j] = load_block<TYPE>(codes, tile * nblk + b + CH + j, lane);
-        nxt_s[j] = scales[(tile * nblk + b + CH + j) * kTileRows + lane];
-      }
-    }
-#pragma unroll
-    for (int j = 0; j < CH; ++j) {
-      if (b + j < f_end) {
-        std::uint32_t w[8];
-        unpack_words<TYPE>(cur[j], w);
-        part[(b + j) * kTileRows + lane] = full_block_dot<TYPE>(w, x + (b + j) * kBlock);
-        scl[(b + j) * kTileRows + lane] = cur_s[j];
-      }
-    }
-#pragma unroll
-    for (int j = 0; j < CH; ++j) {
-      cur[j] = nxt[j];
-      cur_s[j] = nxt_s[j];
-    }
-  }
-  // The partial last block, if this wavefront owns it.
-  if (nfull < nblk && nfull >= b_begin && nfull < b_end) {
-    const Block<TYPE> blk = load_block<TYPE>(codes, tile * nblk + nfull, lane);
-    part[nfull * kTileRows + lane] = tail_block_dot<TYPE>(blk, x + nfull * kBlock, in - nfull * kBlock);
-    scl[nfull * kTileRows + lane] = scales[(tile * nblk + nfull) * kTileRows + lane];
-  }
+  block_sums<TYPE, CH>(codes, scales, x, tile, in, nblk, b_begin, b_end, lane, part, scl);
   __syncthreads();
-
   if (wave == 0) {
-    float acc = 0.0f;
-    int b = 0;
-    for (; b + 4 <= nblk; b += 4) {
-      const float p0 = part[(b + 0) * kTileRows + lane], s0 = scl[(b + 0) * kTileRows + lane];
-      const float p1 = part[(b + 1) * kTileRows + lane], s1 = scl[(b + 1) * kTileRows + lane];
-      const float p2 = part[(b + 2) * kTileRows + lane], s2 = scl[(b + 2) * kTileRows + lane];
-      const float p3 = part[(b + 3) * kTileRows + lane], s3 = scl[(b + 3) * kTileRows + lane];
-      acc = __builtin_fmaf(p0, s0, acc);
-      acc = __builtin_fmaf(p1, s1, acc);
-      acc = __builtin_fmaf(p2, s2, acc);
-      acc = __builtin_fmaf(p3, s3, acc);
-    }
-    for (; b < nblk; ++b) acc = __builtin_fmaf(part[b * kTileRows + lane], scl[b * kTileRows + lane], acc);
+    const float acc = chain_lds(part, scl, nblk, lane);
     const std::size_t o = tile * kTileRows + lane;
     if (o < static_cast<std::size_t>(out)) {
       const float v = acc + (bias != nullptr ? bias[o] : 0.0f);
@@ -267,22 +381,53 @@ template <int TYPE, int R>
 int launch_rows(const DeviceMatrix& m, const float* x, std::size_t rows, const float* bias, float* y, int acc,
                 hipStream_t s);
 
-template <int TYPE>
-int launch_r1(const DeviceMatrix& m, const float* x, const float* bias, float* y, int acc, hipStream_t s) {
-  constexpr int CH = chunk_for(TYPE);
-  // Wavefronts per tile: enough to put ~16 wavefronts on each of the 256
-  // CUs when the matrix has few tiles, at most 16 per workgroup, and at
-  // least one chunk of blocks per wavefront.
-  const std::size_t want = ceil_div(4096, m.ntiles);
-  std::size_t waves = std::min<std::size_t>(16, std::max<std::size_t>(1, std::min(want, ceil_div(m.nblk, CH))));
-  int bpw = static_cast<int>(ceil_div(ceil_div(m.nblk, waves), CH) * CH);
-  waves = ceil_div(m.nblk, bpw);
-  const std::size_t lds = 2 * m.nblk * kTileRows * sizeof(float);
-  // Rows too long for the LDS staging take the one-wavefront-per-tile path.
-  if (lds > max_lds_per_block()) return launch_rows<TYPE, 2>(m, x, 1, bias, y, acc, s);
+// Largest supported load chunk that does not exceed bpw blocks.
+int chunk_le(int bpw, int type) {
+  const int cap = chunk_for(type);
+  int ch = 1;
+  while (ch * 2 <= bpw && ch * 2 <= cap) ch *= 2;
+  return ch;
+}
+
+template <int TYPE, int CH>
+void launch_r1_ch(const DeviceMatrix& m, const float* x, const float* bias, float* y, int acc, int waves, int bpw,
+                  std::size_t lds, hipStream_t s) {
   qgemv_r1<TYPE, CH><<<static_cast<unsigned>(m.ntiles), static_cast<unsigned>(waves * 64), lds, s>>>(
       reinterpret_cast<const uint4*>(m.codes), m.scales, x, bias, y, static_cast<int>(m.in), static_cast<int>(m.nblk),
       static_cast<int>(m.out), bpw, acc);
+}
+
+template <int TYPE>
+int launch_narrow(const DeviceMatrix& m, const float* x, const float* bias, float* y, int acc, const GemvPlan& p,
+                  hipStream_t s) {
+  const std::size_t lds = (((m.in + 3) & ~std::size_t{3}) + 2 * m.nblk * 16) * sizeof(float);
+  qgemv_narrow<TYPE><<<static_cast<unsigned>(ceil_div(m.out, 16)), static_cast<unsigned>(p.waves * 64), lds, s>>>(
+      reinterpret_cast<const uint4*>(m.codes), m.scales, x, bias, y, static_cast<int>(m.in), static_cast<int>(m.nblk),
+      static_cast<int>(m.out), p.bpw, acc);
+  return LLMI_OK;
+}
+
+template <int TYPE>
+int launch_r1(const DeviceMatrix& m, const float* x, const float* bias, float* y, int acc, hipStream_t s) {
+  const GemvPlan p = plan_gemv(m);
+  if (p.narrow) {
+    const std::size_t lds = (((m.in + 3) & ~std::size_t{3}) + 2 * m.nblk * 16) * sizeof(float);
+    if (lds <= max_lds_per_block()) return launch_narrow<TYPE>(m, x, bias, y, acc, p, s);
+  }
+  const std::size_t lds = 2 * m.nblk * kTileRows * sizeof(float);
+  // Rows too long for the LDS staging take the one-wavefront-per-tile path.
+  if (lds > max_lds_per_block()) return launch_rows<TYPE, 2>(m, x, 1, bias, y, acc, s);
+  int waves = p.waves, bpw = p.bpw;
+  if (p.narrow) {  // narrow plan did not fit: fall back to the 64-row kernel
+    bpw = static_cast<int>(ceil_div(m.nblk, std::min<std::size_t>(16, m.nblk)));
+    waves = static_cast<int>(ceil_div(m.nblk, bpw));
+  }
+  switch (chunk_le(bpw, TYPE)) {
+    case 1: launch_r1_ch<TYPE, 1>(m, x, bias, y, acc, waves, bpw, lds, s); break;
+    case 2: launch_r1_ch<TYPE, 2>(m, x, bias, y, acc, waves, bpw, lds, s); break;
+    case 4: launch_r1_ch<TYPE, 4>(m, x, bias, y, acc, waves, bpw, lds, s); break;
+    default: launch_r1_ch<TYPE, 8>(m, x, bias, y, acc, waves, bpw, lds, s); break;
+  }
   return LLMI_OK;
 }
 

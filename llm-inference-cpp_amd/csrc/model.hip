@@ -189,31 +189,12 @@ __device__ __forceinline__ float ref_dot(const float* __restrict__ a, const floa
 
 __device__ __forceinline__ float recip_float(double s) { return static_cast<float>(1.0 / s); }
 
-// grid = (head, token).  Dynamic LDS: the scores of positions 0..pos.
-__global__ void __launch_bounds__(kThreads) attention(const float* __restrict__ q, const float* __restrict__ kc,
-                                                      const float* __restrict__ vc, float* __restrict__ out, int nh,
-                                                      int nkv, int hd, int cap, int base, float scale) {
-  extern __shared__ float sc[];
-  __shared__ double red_d[kThreads];
-  __shared__ float red_f[kThreads];
-  __shared__ float inv_s;
-  const int h = blockIdx.x;
-  const int t = blockIdx.y;
-  const int pos = base + t;
-  const int npos = pos + 1;
-  const int kvh = h / (nh / nkv);
-  const float* qv = q + (static_cast<std::size_t>(t) * nh + h) * hd;
-  const float* kh = kc + static_cast<std::size_t>(kvh) * cap * hd;
-  const float* vh = vc + static_cast<std::size_t>(kvh) * cap * hd;
-
-  float mx_local = -__builtin_inff();
-  for (int s = threadIdx.x; s < npos; s += kThreads) {
-    const float v = ref_dot(qv, kh + static_cast<std::size_t>(s) * hd, hd) * scale;
-    sc[s] = v;
-    mx_local = fmaxf(mx_local, v);
-  }
+// Softmax over sc[0..npos) in LDS (kernels.cpp:136-146): float max, exact
+// expf, double sum (order-checked), p = e * float(1/sum).  Ends with a
+// barrier; every thread of the 256 takes part.
+__device__ __forceinline__ void softmax_lds(float* sc, int npos, float mx_local, double* red_d, float* red_f,
+                                            float* inv_s) {
   const float mx = block_max_float(mx_local, red_f);
-
   double part = 0.0;
   for (int s = threadIdx.x; s < npos; s += kThreads) {
     const float e = exact::expf(sc[s] - mx);
@@ -229,30 +210,152 @@ __global__ void __launch_bounds__(kThreads) attention(const float* __restrict__ 
       for (int s = 0; s < npos; ++s) seq += static_cast<double>(sc[s]);
       inv = recip_float(seq);
     }
-    inv_s = inv;
+    *inv_s = inv;
   }
   __syncthreads();
-  const float inv = inv_s;
+  const float inv = *inv_s;
   for (int s = threadIdx.x; s < npos; s += kThreads) sc[s] = sc[s] * inv;
   __syncthreads();
+}
 
-  // out[i] = fma(p_s, v_s[i], out[i]) over s in order, one thread per i.
+// Generic head size: one thread per position with ref_dot, the P.V chain
+// read straight from the cache.  grid = (head, token); dynamic LDS: scores.
+__global__ void __launch_bounds__(kThreads) attention_generic(const float* __restrict__ q, const float* __restrict__ kc,
+                                                              const float* __restrict__ vc, float* __restrict__ out,
+                                                              int nh, int nkv, int hd, int cap, int base, float scale) {
+  extern __shared__ float sc[];
+  __shared__ double red_d[kThreads];
+  __shared__ float red_f[kThreads];
+  __shared__ float inv_s;
+  const int h = blockIdx.x;
+  const int t = blockIdx.y;
+  const int npos = base + t + 1;
+  const int kvh = h / (nh / nkv);
+  const float* qv = q + (static_cast<std::size_t>(t) * nh + h) * hd;
+  const float* kh = kc + static_cast<std::size_t>(kvh) * cap * hd;
+  const float* vh = vc + static_cast<std::size_t>(kvh) * cap * hd;
+  float mx_local = -__builtin_inff();
+  for (int s = threadIdx.x; s < npos; s += kThreads) {
+    const float v = ref_dot(qv, kh + static_cast<std::size_t>(s) * hd, hd) * scale;
+    sc[s] = v;
+    mx_local = fmaxf(mx_local, v);
+  }
+  softmax_lds(sc, npos, mx_local, red_d, red_f, &inv_s);
   for (int i = threadIdx.x; i < hd; i += kThreads) {
     float acc = 0.0f;
-    const float* vp = vh + i;
-    int s = 0;
-    for (; s + 4 <= npos; s += 4) {
-      const float v0 = vp[static_cast<std::size_t>(s + 0) * hd];
-      const float v1 = vp[static_cast<std::size_t>(s + 1) * hd];
-      const float v2 = vp[static_cast<std::size_t>(s + 2) * hd];
-      const float v3 = vp[static_cast<std::size_t>(s + 3) * hd];
-      acc = __builtin_fmaf(sc[s + 0], v0, acc);
-      acc = __builtin_fmaf(sc[s + 1], v1, acc);
-      acc = __builtin_fmaf(sc[s + 2], v2, acc);
-      acc = __builtin_fmaf(sc[s + 3], v3, acc);
-    }
-    for (; s < npos; ++s) acc = __builtin_fmaf(sc[s], vp[static_cast<std::size_t>(s) * hd], acc);
+    for (int s = 0; s < npos; ++s) acc = __builtin_fmaf(sc[s], vh[static_cast<std::size_t>(s) * hd + i], acc);
     out[(static_cast<std::size_t>(t) * nh + h) * hd + i] = acc;
+  }
+}
+
+// head_dim a multiple of 16 (64 for SmolLM2 and Qwen2.5).
+//  scores: 16 lanes per position; lane j accumulates elements j, j+16, ...
+//          with fused multiply-adds exactly like the AVX2 build's 16
+//          accumulators, and the xor-8/4/2/1 shuffle tree is its horizontal
+//          sum (j+8, then +4, +2, +1); + 0.0f is the empty scalar tail.
+//  P.V:    wavefront 0 runs out[i] = fma(p_s, v_s[i], out[i]) over s in
+//          order from LDS tiles of V that wavefronts 1-3 prefetch (double
+//          buffered), so the chain never waits on global memory.
+// grid = (head, token); dynamic LDS: scores (npos floats) then 2 V tiles.
+constexpr int kVTile = 64;  // positions per V tile
+
+__global__ void __launch_bounds__(kThreads) attention_hd16(const float* __restrict__ q, const float* __restrict__ kc,
+                                                           const float* __restrict__ vc, float* __restrict__ out,
+                                                           int nh, int nkv, int hd, int cap, int base, float scale,
+                                                           int sc_len) {
+  extern __shared__ float lds_dyn[];
+  float* sc = lds_dyn;
+  float* vtile = lds_dyn + sc_len;  // [2][kVTile][hd]
+  __shared__ double red_d[kThreads];
+  __shared__ float red_f[kThreads];
+  __shared__ float inv_s;
+  const int h = blockIdx.x;
+  const int t = blockIdx.y;
+  const int npos = base + t + 1;
+  const int kvh = h / (nh / nkv);
+  const float* qv = q + (static_cast<std::size_t>(t) * nh + h) * hd;
+  const float* kh = kc + static_cast<std::size_t>(kvh) * cap * hd;
+  const float* vh = vc + static_cast<std::size_t>(kvh) * cap * hd;
+  const int tid = threadIdx.x;
+  const int j = tid & 15;   // accumulator lane
+  const int grp = tid >> 4;  // 16 positions per pass of the 256 threads
+  const int nchunk = hd / 16;
+
+  float mx_local = -__builtin_inff();
+  for (int s0 = 0; s0 < npos; s0 += kThreads / 16) {
+    const int s = s0 + grp;
+    float lane = 0.0f;
+    if (s < npos) {
+      const float* kr = kh + static_cast<std::size_t>(s) * hd;
+      for (int c = 0; c < nchunk; ++c) lane = __builtin_fmaf(qv[16 * c + j], kr[16 * c + j], lane);
+    }
+    lane = lane + __shfl_xor(lane, 8, 16);
+    lane = lane + __shfl_xor(lane, 4, 16);
+    lane = lane + __shfl_xor(lane, 2, 16);
+    lane = lane + __shfl_xor(lane, 1, 16);
+    if (s < npos && j == 0) {
+      const float v = (lane + 0.0f) * scale;
+      sc[s] = v;
+      mx_local = fmaxf(mx_local, v);
+    }
+  }
+  softmax_lds(sc, npos, mx_local, red_d, red_f, &inv_s);
+
+  const int wave = tid >> 6;
+  const int tile_floats = kVTile * hd;
+  const int ntile = (npos + kVTile - 1) / kVTile;
+  auto load_tile = [&](int k, float* dst, int first_thread, int nthreads) {
+    const int s0 = k * kVTile;
+    const int count = min(kVTile, npos - s0) * hd;
+    const float* src = vh + static_cast<std::size_t>(s0) * hd;
+    for (int e = tid - first_thread; e < count; e += nthreads) dst[e] = src[e];
+  };
+  load_tile(0, vtile, 0, kThreads);
+  __syncthreads();
+  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // hd <= 256: lanes own i = lane + 64r
+  for (int k = 0; k < ntile; ++k) {
+    float* cur = vtile + (k & 1) * tile_floats;
+    if (wave != 0) {
+      if (k + 1 < ntile) load_tile(k + 1, vtile + ((k + 1) & 1) * tile_floats, 64, kThreads - 64);
+    } else {
+      const int s0 = k * kVTile;
+      const int cnt = min(kVTile, npos - s0);
+      for (int r = 0; r < 4; ++r) {
+        const int i = tid + 64 * r;
+        if (i < hd) {
+          float a = acc[r];
+          for (int s = 0; s < cnt; ++s) a = __builtin_fmaf(sc[s0 + s], cur[s * hd + i], a);
+          acc[r] = a;
+        }
+      }
+    }
+    __syncthreads();
+  }
+  if (wave == 0) {
+    for (int r = 0; r < 4; ++r) {
+      const int i = tid + 64 * r;
+      if (i < hd) out[(static_cast<std::size_t>(t) * nh + h) * hd + i] = acc[r];
+    }
+  }
+}
+
+std::size_t attention_static_lds() { return kThreads * (sizeof(double) + sizeof(float)) + 16; }
+
+// Dynamic LDS of the attention launch for npos positions.
+std::size_t attention_dyn_lds(std::size_t npos, std::size_t hd) {
+  return hd % 16 == 0 && hd <= 256 ? (npos + 2 * kVTile * hd) * sizeof(float) : npos * sizeof(float);
+}
+
+void launch_attention(const float* q, const float* kc, const float* vc, float* out, int nh, int nkv, int hd, int cap,
+                      int base, int T, float scale, hipStream_t s) {
+  const std::size_t npos = static_cast<std::size_t>(base) + T;
+  const dim3 grid(static_cast<unsigned>(nh), static_cast<unsigned>(T));
+  if (hd % 16 == 0 && hd <= 256) {
+    attention_hd16<<<grid, kThreads, attention_dyn_lds(npos, hd), s>>>(q, kc, vc, out, nh, nkv, hd, cap, base, scale,
+                                                                       static_cast<int>(npos));
+  } else {
+    attention_generic<<<grid, kThreads, attention_dyn_lds(npos, hd), s>>>(q, kc, vc, out, nh, nkv, hd, cap, base,
+                                                                          scale);
   }
 }
 
@@ -267,39 +370,91 @@ __global__ void __launch_bounds__(kThreads) silu_mul(float* __restrict__ g, cons
 }
 
 // --------------------------------------------------------------- argmax
-// First maximum (lowest index on ties) of x[0..n); one 1024-thread block.
+// First maximum (lowest index on ties), transformer.cpp:22-24.
+struct Best {
+  float v;
+  int i;  // -1: empty
+};
+
+__device__ __forceinline__ Best better(Best a, Best b) {
+  if (b.i < 0) return a;
+  if (a.i < 0) return b;
+  if (b.v > a.v || (b.v == a.v && b.i < a.i)) return b;
+  return a;
+}
+
+template <int NT>
+__device__ __forceinline__ Best block_best(Best b, float* bv, int* bi) {
+  const int tid = threadIdx.x;
+  bv[tid] = b.v;
+  bi[tid] = b.i;
+  __syncthreads();
+  for (int stride = NT / 2; stride > 0; stride >>= 1) {
+    if (tid < stride) {
+      const Best o = better(Best{bv[tid], bi[tid]}, Best{bv[tid + stride], bi[tid + stride]});
+      bv[tid] = o.v;
+      bi[tid] = o.i;
+    }
+    __syncthreads();
+  }
+  return Best{bv[0], bi[0]};
+}
+
+// One block over all of x (small n, and the standalone entry point).
 __global__ void __launch_bounds__(1024) argmax_first(const float* __restrict__ x, int n, std::int32_t* __restrict__ out,
                                                      std::int32_t* __restrict__ also) {
   __shared__ float bv[1024];
   __shared__ int bi[1024];
-  const int tid = threadIdx.x;
-  float best = -__builtin_inff();
-  int idx = -1;
-  for (int i = tid; i < n; i += 1024) {
-    const float v = x[i];
-    if (idx < 0 || v > best) {
-      best = v;
-      idx = i;
-    }
-  }
-  bv[tid] = best;
-  bi[tid] = idx;
-  __syncthreads();
-  for (int stride = 512; stride > 0; stride >>= 1) {
-    if (tid < stride) {
-      const float ov = bv[tid + stride];
-      const int oi = bi[tid + stride];
-      if (oi >= 0 && (bi[tid] < 0 || ov > bv[tid] || (ov == bv[tid] && oi < bi[tid]))) {
-        bv[tid] = ov;
-        bi[tid] = oi;
-      }
-    }
-    __syncthreads();
-  }
-  if (tid == 0) {
-    const int r = bi[0] < 0 ? 0 : bi[0];
+  Best b{-__builtin_inff(), -1};
+  for (int i = threadIdx.x; i < n; i += 1024) b = better(b, Best{x[i], i});
+  b = block_best<1024>(b, bv, bi);
+  if (threadIdx.x == 0) {
+    const int r = b.i < 0 ? 0 : b.i;
     *out = r;
     if (also != nullptr) *also = r;
+  }
+}
+
+// Many blocks, each over a contiguous slice; each block publishes its best
+// and the last block to finish (counted with a device-scope atomic) combines
+// them and resets the counter for the next launch.  No block waits.
+constexpr int kArgmaxBlocks = 128;
+
+__global__ void __launch_bounds__(kThreads) argmax_many(const float* __restrict__ x, int n, float* __restrict__ part_v,
+                                                        int* __restrict__ part_i, unsigned* __restrict__ counter,
+                                                        std::int32_t* __restrict__ out,
+                                                        std::int32_t* __restrict__ also) {
+  __shared__ float bv[kThreads];
+  __shared__ int bi[kThreads];
+  __shared__ bool last;
+  const int per = (n + gridDim.x - 1) / gridDim.x;
+  const int lo = blockIdx.x * per;
+  const int hi = min(n, lo + per);
+  Best b{-__builtin_inff(), -1};
+  for (int i = lo + threadIdx.x; i < hi; i += kThreads) b = better(b, Best{x[i], i});
+  b = block_best<kThreads>(b, bv, bi);
+  if (threadIdx.x == 0) {
+    part_v[blockIdx.x] = b.v;
+    part_i[blockIdx.x] = b.i;
+    __threadfence();
+    const unsigned done = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    last = done == gridDim.x - 1;
+  }
+  __syncthreads();
+  if (!last) return;
+  __threadfence();
+  Best r{-__builtin_inff(), -1};
+  for (int k = threadIdx.x; k < static_cast<int>(gridDim.x); k += kThreads) {
+    const float v = __hip_atomic_load(part_v + k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int i = __hip_atomic_load(part_i + k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    r = better(r, Best{v, i});
+  }
+  r = block_best<kThreads>(r, bv, bi);
+  if (threadIdx.x == 0) {
+    const int idx = r.i < 0 ? 0 : r.i;
+    *out = idx;
+    if (also != nullptr) *also = idx;
+    __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
@@ -322,26 +477,8 @@ __global__ void __launch_bounds__(kThreads) softmax_rows(float* __restrict__ x, 
     sc[s] = row[s];
     mx_local = fmaxf(mx_local, sc[s]);
   }
-  const float mx = block_max_float(mx_local, red_f);
-  double part = 0.0;
-  for (int s = threadIdx.x; s < n; s += kThreads) {
-    const float e = exact::expf(sc[s] - mx);
-    sc[s] = e;
-    part += static_cast<double>(e);
-  }
-  const double sum = block_sum_double(part, red_d);
-  if (threadIdx.x == 0) {
-    const double slack = sum_slack(n) * sum;
-    float inv = recip_float(sum);
-    if (recip_float(sum - slack) != recip_float(sum + slack)) {
-      double seq = 0.0;
-      for (int s = 0; s < n; ++s) seq += static_cast<double>(sc[s]);
-      inv = recip_float(seq);
-    }
-    inv_s = inv;
-  }
-  __syncthreads();
-  for (int s = threadIdx.x; s < n; s += kThreads) row[s] = sc[s] * inv_s;
+  softmax_lds(sc, n, mx_local, red_d, red_f, &inv_s);
+  for (int s = threadIdx.x; s < n; s += kThreads) row[s] = sc[s];
 }
 
 __global__ void __launch_bounds__(kThreads) silu_inplace(float* __restrict__ x, std::size_t n) {
@@ -367,6 +504,9 @@ struct Workspace {
   std::int32_t* next = nullptr;  // argmax result
   std::int32_t* gen = nullptr;   // generated ids of the current greedy run
   std::size_t gen_cap = 0;
+  float* am_v = nullptr;         // argmax partials and completion counter
+  int* am_i = nullptr;
+  unsigned* am_count = nullptr;
 };
 
 }  // namespace llmi_hip
@@ -551,7 +691,8 @@ void free_workspace(Workspace& w) {
   for (void* p : {static_cast<void*>(w.x), static_cast<void*>(w.h), static_cast<void*>(w.q), static_cast<void*>(w.k),
                   static_cast<void*>(w.v), static_cast<void*>(w.att), static_cast<void*>(w.g), static_cast<void*>(w.u),
                   static_cast<void*>(w.logits), static_cast<void*>(w.ids), static_cast<void*>(w.next),
-                  static_cast<void*>(w.gen)})
+                  static_cast<void*>(w.gen), static_cast<void*>(w.am_v), static_cast<void*>(w.am_i),
+                  static_cast<void*>(w.am_count)})
     if (p != nullptr) (void)hipFree(p);
   w = Workspace{};
 }
@@ -577,6 +718,11 @@ int ensure_workspace(llmi_hip_model* m, std::size_t T) {
   if (rc == LLMI_OK) rc = get(&w.logits, n * m->V, 4);
   if (rc == LLMI_OK) rc = get(&w.ids, n, 4);
   if (rc == LLMI_OK) rc = get(&w.next, 1, 4);
+  if (rc == LLMI_OK) rc = get(&w.am_v, kArgmaxBlocks, 4);
+  if (rc == LLMI_OK) rc = get(&w.am_i, kArgmaxBlocks, 4);
+  if (rc == LLMI_OK) rc = get(&w.am_count, 1, 4);
+  if (rc == LLMI_OK && hipMemsetAsync(w.am_count, 0, sizeof(unsigned), library_stream()) != hipSuccess)
+    rc = fail(LLMI_ERR_HIP, "workspace: memset");
   if (rc != LLMI_OK) {
     free_workspace(w);
     return rc;
@@ -584,8 +730,6 @@ int ensure_workspace(llmi_hip_model* m, std::size_t T) {
   w.tokens = n;
   return LLMI_OK;
 }
-
-std::size_t attention_lds(std::size_t cap) { return cap * sizeof(float); }
 
 // transformer.cpp:192-306 with the ids already on the device (ws.ids).  The
 // logits of rows first..T-1 land in ws.logits.
@@ -611,8 +755,8 @@ int forward_device(llmi_hip_model* m, llmi_hip_cache* cache, std::size_t T, bool
     if (int rc = launch_matmul(l.wv, w.h, T, l.bv, w.v, s)) return rc;
     rope_and_cache<<<tt, kThreads, 0, s>>>(w.q, w.k, w.v, kc, vc, m->cos_t, m->sin_t, nh, nkv, hd,
                                            static_cast<int>(cache->cap), static_cast<int>(base));
-    attention<<<dim3(static_cast<unsigned>(nh), tt), kThreads, attention_lds(base + T), s>>>(
-        w.q, kc, vc, w.att, nh, nkv, hd, static_cast<int>(cache->cap), static_cast<int>(base), scale);
+    launch_attention(w.q, kc, vc, w.att, nh, nkv, hd, static_cast<int>(cache->cap), static_cast<int>(base),
+                     static_cast<int>(T), scale, s);
     if (int rc = launch_matmul(l.wo, w.att, T, nullptr, w.x, s, true)) return rc;
     rmsnorm_rows<<<tt, kThreads, 0, s>>>(w.x, l.mlp_norm, w.h, static_cast<int>(m->H), eps);
     if (int rc = launch_matmul(l.gate, w.h, T, nullptr, w.g, s)) return rc;
@@ -730,7 +874,8 @@ int llmi_hip_model_new_cache(llmi_hip_model* m, size_t max_len, llmi_hip_cache**
   *cache = nullptr;
   const std::size_t cap = std::min<std::size_t>(max_len, m->c.max_position_embeddings);
   if (cap == 0) return fail(LLMI_ERR_ARG, "new_cache: max_len must be positive");
-  LLMI_REQUIRE(attention_lds(cap) + 4096 <= max_lds_per_block(), "new_cache: capacity exceeds the attention kernel's LDS");
+  LLMI_REQUIRE(attention_dyn_lds(cap, m->hd) + attention_static_lds() <= max_lds_per_block(),
+               "new_cache: capacity exceeds the attention kernel's LDS");
   if (int rc = ensure_tables(m, cap)) return rc;
   auto c = std::make_unique<llmi_hip_cache>();
   c->model = m;
@@ -818,7 +963,7 @@ int llmi_hip_model_generate_greedy(llmi_hip_model* m, const int32_t* prompt, siz
   const int V = static_cast<int>(m->V);
   std::size_t produced = 0;
   for (std::size_t step = 0; step < max_new; ++step) {
-    argmax_first<<<1, 1024, 0, s>>>(w.logits, V, w.ids, w.gen + step);
+    argmax_many<<<kArgmaxBlocks, kThreads, 0, s>>>(w.logits, V, w.am_v, w.am_i, w.am_count, w.ids, w.gen + step);
     LLMI_TRY_HIP(hipGetLastError());
     produced = step + 1;
     if (n_stop > 0) {
