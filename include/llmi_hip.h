@@ -215,6 +215,12 @@ int llmi_hip_cache_reset(llmi_hip_cache* cache);
  * reference's messages. */
 int llmi_hip_model_forward_cached(llmi_hip_model* model, llmi_hip_cache* cache, const int32_t* tokens, size_t n,
                                   int all_positions, float* logits);
+/* forward_cached filling the reference's ForwardTrace (transformer.hpp:14-19,
+ * transformer.cpp:218-221, :294, :299): states (host, NULL to skip) receives
+ * (num_layers + 2) x n x hidden_size floats -- the token embeddings, the
+ * output of every layer, then the final RMSNorm of every new token. */
+int llmi_hip_model_forward_cached_trace(llmi_hip_model* model, llmi_hip_cache* cache, const int32_t* tokens,
+                                        size_t n, int all_positions, float* logits, float* states);
 
 /* Transformer::generate_greedy_cached (transformer.cpp:308-327): prefill,
  * then up to max_new greedy tokens (first maximum), stopping after a token in

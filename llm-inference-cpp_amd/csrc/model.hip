@@ -732,8 +732,11 @@ int ensure_workspace(llmi_hip_model* m, std::size_t T) {
 }
 
 // transformer.cpp:192-306 with the ids already on the device (ws.ids).  The
-// logits of rows first..T-1 land in ws.logits.
-int forward_device(llmi_hip_model* m, llmi_hip_cache* cache, std::size_t T, bool all_positions, hipStream_t s) {
+// logits of rows first..T-1 land in ws.logits.  trace (host, optional):
+// (layers + 2) x T x H floats -- the embeddings, every layer's output and
+// the final RMSNorm, as the reference's ForwardTrace (transformer.hpp:14-19).
+int forward_device(llmi_hip_model* m, llmi_hip_cache* cache, std::size_t T, bool all_positions, hipStream_t s,
+                   float* trace = nullptr) {
   const auto& c = m->c;
   Workspace& w = m->ws;
   const std::size_t base = cache->len;
@@ -745,6 +748,8 @@ int forward_device(llmi_hip_model* m, llmi_hip_cache* cache, std::size_t T, bool
   const unsigned tt = static_cast<unsigned>(T);
 
   if (int rc = launch_dequantize_rows(m->embed, w.ids, T, w.x, s)) return rc;
+  const std::size_t state = T * m->H;
+  if (trace != nullptr) LLMI_TRY_HIP(hipMemcpyAsync(trace, w.x, state * sizeof(float), hipMemcpyDeviceToHost, s));
   for (std::size_t li = 0; li < m->layers.size(); ++li) {
     const DeviceLayer& l = m->layers[li];
     float* kc = cache->k + li * per_layer;
@@ -763,13 +768,21 @@ int forward_device(llmi_hip_model* m, llmi_hip_cache* cache, std::size_t T, bool
     if (int rc = launch_matmul(l.up, w.h, T, nullptr, w.u, s)) return rc;
     silu_mul<<<blocks_for(T * m->F), kThreads, 0, s>>>(w.g, w.u, T * m->F);
     if (int rc = launch_matmul(l.down, w.g, T, nullptr, w.x, s, true)) return rc;
+    if (trace != nullptr)
+      LLMI_TRY_HIP(hipMemcpyAsync(trace + (li + 1) * state, w.x, state * sizeof(float), hipMemcpyDeviceToHost, s));
   }
+  // The reference normalises every row (transformer.cpp:298), then applies the
+  // head to the last one or to all of them.
   const std::size_t first = all_positions ? 0 : T - 1;
   const std::size_t rows = T - first;
-  rmsnorm_rows<<<static_cast<unsigned>(rows), kThreads, 0, s>>>(w.x + first * m->H, m->final_norm, w.h,
-                                                                static_cast<int>(m->H), eps);
+  const std::size_t norm_first = trace != nullptr ? 0 : first;
+  rmsnorm_rows<<<static_cast<unsigned>(T - norm_first), kThreads, 0, s>>>(
+      w.x + norm_first * m->H, m->final_norm, w.h + norm_first * m->H, static_cast<int>(m->H), eps);
+  if (trace != nullptr)
+    LLMI_TRY_HIP(hipMemcpyAsync(trace + (m->layers.size() + 1) * state, w.h, state * sizeof(float),
+                                hipMemcpyDeviceToHost, s));
   const DeviceMatrix& head = m->tied ? m->embed : m->lm_head;
-  if (int rc = launch_matmul(head, w.h, rows, nullptr, w.logits, s)) return rc;
+  if (int rc = launch_matmul(head, w.h + first * m->H, rows, nullptr, w.logits, s)) return rc;
   LLMI_TRY_HIP(hipGetLastError());
   cache->len = base + T;
   return LLMI_OK;
@@ -907,20 +920,25 @@ int llmi_hip_cache_reset(llmi_hip_cache* c) {
   return LLMI_OK;
 }
 
-int llmi_hip_model_forward_cached(llmi_hip_model* m, llmi_hip_cache* cache, const int32_t* tokens, size_t n,
-                                  int all_positions, float* logits) {
+int llmi_hip_model_forward_cached_trace(llmi_hip_model* m, llmi_hip_cache* cache, const int32_t* tokens, size_t n,
+                                        int all_positions, float* logits, float* states) {
   LLMI_REQUIRE_INIT();
   LLMI_REQUIRE(m != nullptr, "forward_cached: null model");
   if (int rc = validate(m, cache, tokens, n)) return rc;
   if (int rc = ensure_workspace(m, n)) return rc;
   hipStream_t s = library_stream();
   LLMI_TRY_HIP(hipMemcpyAsync(m->ws.ids, tokens, n * sizeof(std::int32_t), hipMemcpyHostToDevice, s));
-  if (int rc = forward_device(m, cache, n, all_positions != 0, s)) return rc;
+  if (int rc = forward_device(m, cache, n, all_positions != 0, s, states)) return rc;
   const std::size_t rows = all_positions ? n : 1;
   if (logits != nullptr)
     LLMI_TRY_HIP(hipMemcpyAsync(logits, m->ws.logits, rows * m->V * sizeof(float), hipMemcpyDeviceToHost, s));
   LLMI_TRY_HIP(hipStreamSynchronize(s));
   return LLMI_OK;
+}
+
+int llmi_hip_model_forward_cached(llmi_hip_model* m, llmi_hip_cache* cache, const int32_t* tokens, size_t n,
+                                  int all_positions, float* logits) {
+  return llmi_hip_model_forward_cached_trace(m, cache, tokens, n, all_positions, logits, nullptr);
 }
 
 // transformer.cpp:308-327: prefill once, then one token per step; the argmax

@@ -1,0 +1,44 @@
+// llmi::Weight on the MI355X: the interface of the reference's
+// include/llmi/model/weight.hpp:18-39.  A quantized Weight lives in HBM (the
+// GPU quantizer packs it straight into the device layout); copies share the
+// device matrix, which is freed with the last copy.  matmul() and row() take
+// and return host memory like the reference's and return with the result
+// complete.  Type::F32 weights are not part of this GPU path: quantized()
+// with F32, from_float(), and matmul()/row() on them throw.
+#pragma once
+
+#include <cstddef>
+#include <memory>
+#include <vector>
+
+#include "llmi/model/quant.hpp"
+
+struct llmi_hip_weight;
+
+namespace llmi {
+
+class Weight {
+ public:
+  Weight() = default;
+  static Weight from_float(std::vector<float> w);
+  static Weight quantized(const std::vector<float>& w, std::size_t out, std::size_t in, quant::Type type);
+  // A Weight of an already quantized matrix (e.g. from a GGUF file).
+  static Weight from_quantized(const quant::QuantizedMatrix& m);
+
+  [[nodiscard]] bool empty() const;
+  [[nodiscard]] std::size_t byte_size() const;
+  [[nodiscard]] quant::Type type() const { return type_; }
+
+  void matmul(const float* x, std::size_t rows, std::size_t in, std::size_t out, const float* bias, float* y) const;
+  void row(std::size_t index, std::size_t in, float* dst) const;
+
+  // The device matrix, for device-pointer callers (llmi_hip_matmul_dev).
+  [[nodiscard]] const llmi_hip_weight* device() const { return dev_.get(); }
+
+ private:
+  quant::Type type_ = quant::Type::F32;
+  std::size_t out_ = 0, in_ = 0;
+  std::shared_ptr<llmi_hip_weight> dev_;
+};
+
+}  // namespace llmi

@@ -72,6 +72,7 @@ SIGNATURES = {
     "llmi_hip_cache_capacity": (_sz, [_vp]),
     "llmi_hip_cache_reset": (_i, [_vp]),
     "llmi_hip_model_forward_cached": (_i, [_vp, _vp, _vp, _sz, _i, _vp]),
+    "llmi_hip_model_forward_cached_trace": (_i, [_vp, _vp, _vp, _sz, _i, _vp, _vp]),
     "llmi_hip_model_generate_greedy": (_i, [_vp, _vp, _sz, _sz, _vp, _sz, _vp, C.POINTER(_sz)]),
     "llmi_hip_model_last_timing": (_i, [_vp, C.POINTER(_d), C.POINTER(_d)]),
 }
@@ -362,6 +363,16 @@ class Model:
         check(self.lib.llmi_hip_model_forward_cached(self.h, cache.h, _p(toks), toks.size, int(all_positions),
                                                      _p(logits)))
         return logits
+
+    def forward_cached_trace(self, cache: Cache, tokens, all_positions: bool = False):
+        """(logits, states[(layers + 2), n, hidden])."""
+        toks = np.ascontiguousarray(tokens, dtype=np.int32)
+        rows = toks.size if all_positions else 1
+        logits = np.zeros(max(rows, 1) * self.cfg["vocab_size"], dtype=np.float32)
+        states = np.zeros((self.cfg["num_layers"] + 2, toks.size, self.cfg["hidden_size"]), dtype=np.float32)
+        check(self.lib.llmi_hip_model_forward_cached_trace(self.h, cache.h, _p(toks), toks.size, int(all_positions),
+                                                           _p(logits), _p(states)))
+        return logits, states
 
     def generate_greedy(self, prompt, max_new: int, stop_ids=()) -> np.ndarray:
         p = np.ascontiguousarray(prompt, dtype=np.int32)

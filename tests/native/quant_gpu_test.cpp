@@ -1,0 +1,174 @@
+// The reference's tests/quant_test.cpp cases, run against the GPU drop-in
+// (llmi::quant and llmi::Weight of libllmi_gpu.so), plus bit-exact checks
+// against the CPU oracle (oracle/liboracle.so).
+#include <algorithm>
+
+#include "check.hpp"
+#include "llmi/model/quant.hpp"
+#include "llmi/model/weight.hpp"
+
+extern "C" {
+void oracle_quantize(const float* w, std::size_t out, std::size_t in, int type, std::uint8_t* data, float* scales);
+void oracle_matmul(const float* x, std::size_t rows, std::size_t in, const std::uint8_t* data, const float* scales,
+                   int type, std::size_t out, const float* bias, float* y, int threads);
+}
+
+using namespace llmi::quant;
+
+namespace {
+std::vector<float> random_matrix(std::size_t out, std::size_t in, unsigned seed) {
+  return check::normal(seed, out * in, 0.0, 0.3);
+}
+int t(Type type) { return type == Type::Q8_0 ? 1 : 2; }
+}  // namespace
+
+TEST(Quant, RoundTripQ8_0StaysWithinHalfAStepOfTheOriginal) {
+  for (std::size_t in : {1U, 7U, 31U, 32U, 33U, 100U}) {
+    constexpr std::size_t out = 3;
+    const auto w = random_matrix(out, in, 1);
+    const QuantizedMatrix q = quantize(w.data(), out, in, Type::Q8_0);
+    ASSERT_TRUE(q.blocks_per_row == (in + kBlockSize - 1) / kBlockSize);
+    std::vector<float> row(in);
+    for (std::size_t r = 0; r < out; ++r) {
+      dequantize_row(q, r, row.data());
+      for (std::size_t b = 0; b < q.blocks_per_row; ++b) {
+        const std::size_t start = b * kBlockSize, len = std::min(kBlockSize, in - start);
+        float amax = 0.0F;
+        for (std::size_t i = 0; i < len; ++i) amax = std::max(amax, std::fabs(w[r * in + start + i]));
+        for (std::size_t i = 0; i < len; ++i) EXPECT_NEAR(row[start + i], w[r * in + start + i], amax / 254.0F + 1e-6F);
+      }
+    }
+  }
+}
+
+TEST(Quant, RoundTripQ4_0StaysWithinOneStepOfTheOriginal) {
+  for (std::size_t in : {1U, 7U, 31U, 32U, 33U, 100U}) {
+    constexpr std::size_t out = 3;
+    const auto w = random_matrix(out, in, 2);
+    const QuantizedMatrix q = quantize(w.data(), out, in, Type::Q4_0);
+    std::vector<float> row(in);
+    for (std::size_t r = 0; r < out; ++r) {
+      dequantize_row(q, r, row.data());
+      for (std::size_t b = 0; b < q.blocks_per_row; ++b) {
+        const std::size_t start = b * kBlockSize, len = std::min(kBlockSize, in - start);
+        float amax = 0.0F;
+        for (std::size_t i = 0; i < len; ++i) amax = std::max(amax, std::fabs(w[r * in + start + i]));
+        for (std::size_t i = 0; i < len; ++i) EXPECT_NEAR(row[start + i], w[r * in + start + i], amax / 8.0F + 1e-6F);
+      }
+    }
+  }
+}
+
+TEST(Quant, Q4_0ExtremeValueInEachBlockRoundTripsExactly) {
+  const float positive_extreme[8] = {0.9F, -0.3F, 0.1F, 0.4F, -0.5F, 0.2F, -0.1F, 0.05F};
+  const float negative_extreme[8] = {-0.9F, 0.3F, 0.1F, 0.4F, -0.5F, 0.2F, -0.1F, 0.05F};
+  for (const float* w : {positive_extreme, negative_extreme}) {
+    const QuantizedMatrix q = quantize(w, 1, 8, Type::Q4_0);
+    std::vector<float> row(8);
+    dequantize_row(q, 0, row.data());
+    EXPECT_EQ(row[0], w[0]);
+  }
+}
+
+TEST(Quant, AllZeroBlockRoundTripsToExactlyZero) {
+  constexpr std::size_t in = 40;
+  std::vector<float> w(in, 0.0F);
+  for (Type type : {Type::Q8_0, Type::Q4_0}) {
+    const QuantizedMatrix q = quantize(w.data(), 1, in, type);
+    std::vector<float> row(in);
+    dequantize_row(q, 0, row.data());
+    for (float v : row) EXPECT_EQ(v, 0.0F);
+  }
+}
+
+TEST(Quant, ByteSizeMatchesTheDocumentedCompressionRatio) {
+  constexpr std::size_t out = 100, in = 3200;
+  const auto w = random_matrix(out, in, 3);
+  const auto f32_bytes = static_cast<double>(out * in * sizeof(float));
+  EXPECT_NEAR(f32_bytes / static_cast<double>(quantize(w.data(), out, in, Type::Q8_0).byte_size()), 3.55, 0.05);
+  EXPECT_NEAR(f32_bytes / static_cast<double>(quantize(w.data(), out, in, Type::Q4_0).byte_size()), 6.4, 0.1);
+}
+
+TEST(Quant, PackedBytesAreBitExactAgainstTheOracle) {
+  for (Type type : {Type::Q8_0, Type::Q4_0})
+    for (std::size_t in : {1U, 7U, 33U, 576U, 4864U}) {
+      const std::size_t out = 70;
+      const auto w = random_matrix(out, in, 9);
+      const QuantizedMatrix q = quantize(w.data(), out, in, type);
+      std::vector<std::uint8_t> data(q.data.size());
+      std::vector<float> scales(q.scales.size());
+      oracle_quantize(w.data(), out, in, t(type), data.data(), scales.data());
+      EXPECT_TRUE(data == q.data);
+      EXPECT_TRUE(std::memcmp(scales.data(), q.scales.data(), scales.size() * 4) == 0);
+    }
+}
+
+TEST(Quant, MatmulMatchesDequantizeThenDotProduct) {
+  constexpr std::size_t rows = 3, in = 300, out = 50;
+  const auto x = check::normal(4, rows * in, 0.0, 0.5);
+  const auto bias = check::normal(5, out, 0.0, 0.5);
+  const auto w = random_matrix(out, in, 5);
+  for (Type type : {Type::Q8_0, Type::Q4_0}) {
+    const QuantizedMatrix q = quantize(w.data(), out, in, type);
+    std::vector<float> y(rows * out), want(rows * out);
+    matmul(x.data(), rows, in, q, out, bias.data(), y.data());
+    std::vector<float> row(in);
+    for (std::size_t o = 0; o < out; ++o) {
+      dequantize_row(q, o, row.data());
+      for (std::size_t r = 0; r < rows; ++r) {
+        double dot = 0;
+        for (std::size_t i = 0; i < in; ++i) dot += static_cast<double>(x[r * in + i]) * row[i];
+        EXPECT_NEAR(y[r * out + o], dot + bias[o], 1e-3);
+      }
+    }
+    oracle_matmul(x.data(), rows, in, q.data.data(), q.scales.data(), t(type), out, bias.data(), want.data(), 1);
+    for (std::size_t i = 0; i < y.size(); ++i) EXPECT_TRUE(check::same_bits(y[i], want[i]));
+  }
+}
+
+TEST(Quant, MatmulAboveTheThreadingThresholdMatchesARowByRowReference) {
+  constexpr std::size_t rows = 3, in = 300, out = 4000;
+  const auto x = check::normal(6, rows * in, 0.0, 0.5);
+  const auto w = random_matrix(out, in, 7);
+  const QuantizedMatrix q = quantize(w.data(), out, in, Type::Q8_0);
+  std::vector<float> y(rows * out), want(rows * out);
+  matmul(x.data(), rows, in, q, out, nullptr, y.data());
+  oracle_matmul(x.data(), rows, in, q.data.data(), q.scales.data(), 1, out, nullptr, want.data(), 1);
+  for (std::size_t i = 0; i < y.size(); ++i) EXPECT_TRUE(check::same_bits(y[i], want[i]));
+}
+
+TEST(Weight, QuantizedWeightMatchesTheQuantFunctionsAndSharesDeviceMemory) {
+  const std::size_t out = 1536, in = 576;
+  const auto w = check::normal(11, out * in, 0.0, 0.02);
+  const auto x = check::normal(12, 2 * in, 0.0, 1.0);
+  for (Type type : {Type::Q8_0, Type::Q4_0}) {
+    const llmi::Weight weight = llmi::Weight::quantized(w, out, in, type);
+    const QuantizedMatrix q = quantize(w.data(), out, in, type);
+    EXPECT_EQ(weight.byte_size(), q.byte_size());
+    EXPECT_TRUE(weight.type() == type);
+    std::vector<float> y(2 * out), want(2 * out);
+    weight.matmul(x.data(), 2, in, out, nullptr, y.data());
+    matmul(x.data(), 2, in, q, out, nullptr, want.data());
+    for (std::size_t i = 0; i < y.size(); ++i) EXPECT_TRUE(check::same_bits(y[i], want[i]));
+    std::vector<float> r1(in), r2(in);
+    weight.row(77, in, r1.data());
+    dequantize_row(q, 77, r2.data());
+    EXPECT_TRUE(std::memcmp(r1.data(), r2.data(), in * 4) == 0);
+    const llmi::Weight copy = weight;  // copies share the device matrix
+    EXPECT_TRUE(copy.device() == weight.device());
+    const llmi::Weight again = llmi::Weight::from_quantized(q);
+    std::vector<float> y2(2 * out);
+    again.matmul(x.data(), 2, in, out, nullptr, y2.data());
+    EXPECT_TRUE(std::memcmp(y.data(), y2.data(), y.size() * 4) == 0);
+  }
+}
+
+TEST(Weight, Float32WeightsAreRejected) {
+  bool threw = false;
+  try {
+    (void)llmi::Weight::quantized(std::vector<float>(4, 1.0F), 2, 2, Type::F32);
+  } catch (const std::invalid_argument&) {
+    threw = true;
+  }
+  EXPECT_TRUE(threw);
+}

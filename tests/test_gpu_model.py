@@ -194,3 +194,25 @@ def test_synthetic_model_greedy_ids_match_reference(name):
         k = int(np.argmax(ids != want))
         pytest.fail(f"{name}: first divergence at step {k} (margin there {rec['margins'][k]:.3g})")
     m.free()
+
+
+def test_forward_trace_states():
+    """ForwardTrace (transformer.hpp:14-19): embeddings, each layer, final
+    norm; the embeddings are the dequantized rows and the head applied to
+    the final state gives the logits, bit for bit."""
+    orc = O.oracle()
+    cfg = synth.tiny(1, True)
+    tensors = synth.make_tensors(cfg, 21, "tiny")
+    m = H.Model(cfg, tensors, H.Q8_0)
+    c = m.new_cache(4)
+    ids = np.array([3, 30, 7], np.int32)
+    logits, states = m.forward_cached_trace(c, ids)
+    assert states.shape == (cfg["num_layers"] + 2, 3, cfg["hidden_size"])
+    data, scales = orc.quantize(tensors[0], cfg["vocab_size"], cfg["hidden_size"], H.Q8_0)
+    for t, tok in enumerate(ids):
+        want = orc.dequantize_row(data, scales, cfg["vocab_size"], cfg["hidden_size"], H.Q8_0, int(tok))
+        assert np.array_equal(bits(states[0, t]), bits(want))
+    head = orc.matmul(states[-1, 2], 1, cfg["hidden_size"], data, scales, H.Q8_0, cfg["vocab_size"])
+    assert np.array_equal(bits(head), bits(logits))
+    c2 = m.new_cache(4)
+    assert np.array_equal(bits(m.forward_cached(c2, ids)), bits(logits))
