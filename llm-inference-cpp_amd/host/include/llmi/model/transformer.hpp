@@ -4,10 +4,12 @@
 // only token ids go in and logits (or ids) come out.  Logits and greedy ids
 // are bit-identical to the reference's for the same weights.
 //
-// The reference's load(const Model&, Type) reads tensors from its safetensors
-// Model; here load() takes the same ModelConfig fields and a reader that
-// returns each tensor (by its expected_tensors() name) as fp32, so the
-// reference's Model plugs in through a two-line adapter.
+// load() takes the reference's ModelConfig fields and a reader that returns
+// each tensor (by its expected_tensors() name) as fp32.  Built inside the
+// reference engine (LLMI_GPU_WITH_REFERENCE_MODEL defined, its include
+// directory on the path), ModelConfig / Arch / TokenId are the reference's
+// own and the reference's load(const Model&, quant::Type) signature is
+// available too (host/integration/load_from_model.cpp).
 #pragma once
 
 #include <cstddef>
@@ -23,8 +25,14 @@
 struct llmi_hip_model;
 struct llmi_hip_cache;
 
+#if defined(LLMI_GPU_WITH_REFERENCE_MODEL)
+#include "llmi/model/model.hpp"
+#include "llmi/tokenizer/tokenizer.hpp"
+#endif
+
 namespace llmi {
 
+#if !defined(LLMI_GPU_WITH_REFERENCE_MODEL)
 using TokenId = std::int32_t;
 
 enum class Arch : std::uint8_t { Llama, Qwen2 };
@@ -46,6 +54,7 @@ struct ModelConfig {
   bool qkv_bias = false;
   std::vector<std::int32_t> eos_token_ids;
 };
+#endif
 
 // Tensor names in the reference's expected_tensors() order
 // (src/model/model.cpp:135-162).
@@ -71,6 +80,10 @@ using TensorReader = std::function<Result<std::vector<float>>(const std::string&
 class Transformer {
  public:
   static Result<Transformer> load(const ModelConfig& cfg, const TensorReader& read, quant::Type weight_type);
+#if defined(LLMI_GPU_WITH_REFERENCE_MODEL)
+  // The reference's signature (transformer.hpp:58).
+  static Result<Transformer> load(const Model& model, quant::Type weight_type = quant::Type::F32);
+#endif
 
   [[nodiscard]] const ModelConfig& config() const { return cfg_; }
   [[nodiscard]] std::size_t weight_bytes() const;
