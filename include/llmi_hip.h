@@ -161,6 +161,23 @@ int llmi_hip_matmul(const llmi_hip_weight* weight, const float* x, size_t rows, 
 int llmi_hip_matmul_dev(const llmi_hip_weight* weight, const float* x_dev, size_t rows, const float* bias_dev,
                         float* y_dev, void* stream);
 
+/* A fixed list of independent products launched as ONE kernel: for each i,
+ * y_dev[i] = quant::matmul(x_dev[i], rows[i], w[i]) (+ bias_dev[i]) exactly
+ * as llmi_hip_matmul_dev would compute it (quant.cpp:119-153, bit-identical),
+ * for callers that issue many small matmuls back to back (the per-layer
+ * Weight::matmul calls of transformer.cpp:245-304 when their inputs are
+ * ready together).  rows[i] is 1..8 (NULL: all 1); bias_dev may be NULL (no
+ * biases) or hold NULL entries.  Every weight must have in <= ~10k.  The
+ * group keeps the pointers, not the data: launch it whenever the inputs are
+ * in place.  Products must not write memory another product of the group
+ * reads.  llmi_hip_group_launch queues the kernel on `stream` (capturable in
+ * a graph). */
+typedef struct llmi_hip_group llmi_hip_group;
+int llmi_hip_group_create(const llmi_hip_weight* const* w, const float* const* x_dev, const size_t* rows,
+                          const float* const* bias_dev, float* const* y_dev, size_t count, llmi_hip_group** out);
+int llmi_hip_group_launch(const llmi_hip_group* group, void* stream);
+void llmi_hip_group_free(llmi_hip_group* group);
+
 /* ------------------------------------------------- glue kernels (device) */
 /* Device counterparts of llmi::kernels (include/llmi/model/kernels.hpp:13-32)
  * and llmi::argmax (transformer.hpp:120), bit-identical to the reference.

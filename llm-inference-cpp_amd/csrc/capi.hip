@@ -81,6 +81,16 @@ std::size_t max_lds_per_block() { return g_max_lds; }
 
 using namespace llmi_hip;
 
+struct llmi_hip_group {
+  GroupProblem* table = nullptr;  // device copy of the problem table
+  int nprob = 0;
+  int total_wgs = 0;
+  std::size_t lds = 0;
+  ~llmi_hip_group() {
+    if (table != nullptr) (void)hipFree(table);
+  }
+};
+
 extern "C" {
 
 const char* llmi_hip_last_error(void) { return t_error.c_str(); }
@@ -403,5 +413,38 @@ int llmi_hip_matmul(const llmi_hip_weight* weight, const float* x, size_t rows, 
   LLMI_TRY_HIP(hipStreamSynchronize(g_stream));
   return LLMI_OK;
 }
+
+int llmi_hip_group_create(const llmi_hip_weight* const* w, const float* const* x, const size_t* rows,
+                          const float* const* bias, float* const* y, size_t count, llmi_hip_group** out) {
+  LLMI_REQUIRE_INIT();
+  LLMI_REQUIRE(out != nullptr, "group: null output handle");
+  *out = nullptr;
+  LLMI_REQUIRE(count == 0 || (w != nullptr && x != nullptr && y != nullptr), "group: null array");
+  std::vector<GroupEntry> entries(count);
+  for (size_t i = 0; i < count; ++i) {
+    LLMI_REQUIRE(w[i] != nullptr, "group: null weight");
+    entries[i] = GroupEntry{&w[i]->m, x[i], bias != nullptr ? bias[i] : nullptr, y[i], rows != nullptr ? rows[i] : 1,
+                            false};
+  }
+  auto g = std::make_unique<llmi_hip_group>();
+  std::vector<GroupProblem> probs;
+  if (int rc = plan_group(entries.data(), count, &probs, &g->total_wgs, &g->lds)) return rc;
+  LLMI_REQUIRE(g->lds <= g_max_lds, "group: a product needs more LDS than one workgroup may use");
+  g->nprob = static_cast<int>(probs.size());
+  if (!probs.empty()) {
+    LLMI_TRY_HIP(hipMalloc(reinterpret_cast<void**>(&g->table), probs.size() * sizeof(GroupProblem)));
+    LLMI_TRY_HIP(hipMemcpy(g->table, probs.data(), probs.size() * sizeof(GroupProblem), hipMemcpyHostToDevice));
+  }
+  *out = g.release();
+  return LLMI_OK;
+}
+
+int llmi_hip_group_launch(const llmi_hip_group* g, void* stream) {
+  LLMI_REQUIRE_INIT();
+  LLMI_REQUIRE(g != nullptr, "group: null group");
+  return launch_group(g->table, g->nprob, g->total_wgs, g->lds, pick(stream));
+}
+
+void llmi_hip_group_free(llmi_hip_group* g) { delete g; }
 
 }  // extern "C"

@@ -7,6 +7,7 @@
 #include <cstddef>
 #include <cstdint>
 #include <string>
+#include <vector>
 
 #include "../../include/llmi_hip.h"
 
@@ -64,12 +65,32 @@ struct DeviceMatrix {
   std::size_t code_bytes = 0, scale_bytes = 0;
 };
 
-struct GemvPlan {
-  bool narrow = false;  // qgemv_narrow (16-row tiles) instead of qgemv_r1
-  int waves = 1;        // wavefronts per workgroup
-  int bpw = 1;          // blocks per wavefront (narrow: per block group)
+// One product of a grouped launch (qgemv_group), as the kernel reads it.
+struct GroupProblem {
+  static constexpr int kNarrow = 16;  // kind: 16-row tiles, batch 1; else the row chunk R (1, 2, 4, 8)
+  const std::uint8_t* codes;
+  const float* scales;
+  const float* x;
+  const float* bias;
+  float* y;
+  int type, kind, in, nblk, out, rows, ntiles, bpw, accumulate, first_wg;
 };
-GemvPlan plan_gemv(const DeviceMatrix& m);
+constexpr int kGroupThreads = 256;  // threads per workgroup of qgemv_group
+
+// One product y = W x (+ bias), rows 1..8, as the caller describes it.
+struct GroupEntry {
+  const DeviceMatrix* m;
+  const float* x;
+  const float* bias;
+  float* y;
+  std::size_t rows;
+  bool accumulate;
+};
+// Lays out the products (skipping empty ones) as consecutive workgroup
+// ranges; *lds = the dynamic LDS every workgroup gets.
+int plan_group(const GroupEntry* entries, std::size_t count, std::vector<GroupProblem>* probs, int* total_wgs,
+               std::size_t* lds);
+int launch_group(const GroupProblem* probs_dev, int nprob, int total_wgs, std::size_t lds, hipStream_t s);
 
 inline std::size_t block_code_bytes(int type) { return type == LLMI_TYPE_Q4_0 ? 16 : 32; }
 

@@ -57,6 +57,9 @@ SIGNATURES = {
     "llmi_hip_dequantize_rows_dev": (_i, [_vp, _vp, _sz, _vp, _vp]),
     "llmi_hip_matmul": (_i, [_vp, _vp, _sz, _sz, _sz, _vp, _vp]),
     "llmi_hip_matmul_dev": (_i, [_vp, _vp, _sz, _vp, _vp, _vp]),
+    "llmi_hip_group_create": (_i, [_vp, _vp, _vp, _vp, _vp, _sz, C.POINTER(_vp)]),
+    "llmi_hip_group_launch": (_i, [_vp, _vp]),
+    "llmi_hip_group_free": (None, [_vp]),
     "llmi_hip_dot_dev": (_i, [_vp, _vp, _vp, _sz, _vp, _vp]),
     "llmi_hip_rmsnorm_dev": (_i, [_vp, _vp, _sz, _sz, _f, _vp, _vp]),
     "llmi_hip_softmax_dev": (_i, [_vp, _sz, _sz, _vp]),
@@ -420,6 +423,37 @@ def synthetic_model_dev(cfg: dict, base_seed: int, qtype: int, convention: str =
     for b in bufs:
         b.free()
     return m
+
+
+class Group:
+    """A fixed list of products (Weight, x device pointer, y device pointer,
+    rows 1..8, optional bias device pointer) launched as one kernel."""
+
+    def __init__(self, items):
+        self.lib = init()
+        n = len(items)
+        ws = (C.c_void_p * n)(*[it[0].h for it in items])
+        xs = (C.c_void_p * n)(*[it[1] for it in items])
+        ys = (C.c_void_p * n)(*[it[2] for it in items])
+        rows = (C.c_size_t * n)(*[it[3] if len(it) > 3 else 1 for it in items])
+        bs = (C.c_void_p * n)(*[it[4] if len(it) > 4 else None for it in items])
+        h = C.c_void_p()
+        check(self.lib.llmi_hip_group_create(ws, xs, rows, bs, ys, n, C.byref(h)))
+        self.h = h
+
+    def launch(self, stream=None) -> None:
+        check(self.lib.llmi_hip_group_launch(self.h, stream))
+
+    def free(self) -> None:
+        if self.h:
+            self.lib.llmi_hip_group_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
 
 
 class Graph:

@@ -56,7 +56,8 @@ def test_baseline_shapes_match_reference(golden):
 
 @pytest.mark.parametrize("qt", [O.Q8_0, O.Q4_0])
 @pytest.mark.parametrize("rows", [1, 2, 3, 4, 5, 7, 8, 9, 17, 64])
-@pytest.mark.parametrize("out,n_in", [(1, 1), (63, 33), (65, 100), (200, 576), (130, 4864), (96, 8192)])
+@pytest.mark.parametrize("out,n_in", [(1, 1), (63, 33), (65, 100), (200, 576), (130, 4864), (96, 8192),
+                                      (40, 20000)])
 def test_batches_and_ragged_shapes_match_oracle(qt, rows, out, n_in):
     orc = O.oracle()
     w = synth.normal(out * 7 + n_in, out * n_in, 0.0, 0.02)
@@ -120,3 +121,69 @@ def test_graph_replays_match_eager_launches():
         H.synchronize()
         for i, y in enumerate(ys):
             assert np.array_equal(bits(y.download(np.float32)), bits(want[i])), (rep, i)
+
+
+def _group_case(specs, seed):
+    """Weights, device inputs/outputs and oracle outputs for a group."""
+    orc = O.oracle()
+    items, want, keep = [], [], []
+    for i, (out, n_in, qt, rows, with_bias) in enumerate(specs):
+        w = synth.normal(seed + 31 * i, out * n_in, 0.0, 0.02)
+        data, scales = orc.quantize(w, out, n_in, qt)
+        dev = H.Weight.upload(data, scales, out, n_in, qt)
+        x = synth.normal(seed + 31 * i + 1, rows * n_in, 0.0, 1.0)
+        bias = synth.normal(seed + 31 * i + 2, out, 0.0, 0.5) if with_bias else None
+        xd, yd = H.DeviceBuffer.from_array(x), H.DeviceBuffer(rows * out * 4)
+        bd = H.DeviceBuffer.from_array(bias) if with_bias else None
+        keep += [dev, xd, yd, bd]
+        items.append((dev, xd.ptr, yd.ptr, rows, bd.ptr if bd is not None else None))
+        want.append(orc.matmul(x, rows, n_in, data, scales, qt, out, bias))
+    return items, want, keep
+
+
+GROUP_SMALL = [(576, 576, O.Q8_0, 1, True), (192, 576, O.Q4_0, 1, False), (63, 33, O.Q4_0, 3, True),
+               (130, 4864, O.Q8_0, 8, False), (1, 1, O.Q4_0, 2, True), (96, 8192, O.Q8_0, 1, False),
+               (65, 100, O.Q4_0, 5, False), (1536, 576, O.Q4_0, 1, False)]
+
+
+@pytest.mark.parametrize("big", [False, True])
+def test_grouped_launch_matches_oracle(big):
+    """llmi_hip_group: every product of one launch bit-identical to the
+    oracle, in the few-tiles regime (16-row tiles at batch 1) and, with a
+    70000-row matrix in the list, the many-tiles regime (64-row tiles)."""
+    specs = GROUP_SMALL + ([(70000, 96, O.Q8_0, 1, True), (2000, 600, O.Q4_0, 7, False)] if big else [])
+    items, want, keep = _group_case(specs, 700 + big)
+    g = H.Group(items)
+    for rep in range(2):
+        for i in range(len(items)):
+            keep[4 * i + 2].upload(np.full(keep[4 * i + 2].nbytes // 4, np.nan, np.float32))
+        g.launch()
+        H.synchronize()
+        for i, it in enumerate(items):
+            got = keep[4 * i + 2].download(np.float32)
+            assert np.array_equal(bits(got), bits(want[i])), (rep, specs[i])
+    g.free()
+
+
+def test_grouped_launch_in_a_graph():
+    items, want, keep = _group_case(GROUP_SMALL[:4], 900)
+    g = H.Group(items)
+    graph = H.Graph(lambda: g.launch())
+    for rep in range(3):
+        for i in range(len(items)):
+            keep[4 * i + 2].upload(np.zeros(keep[4 * i + 2].nbytes // 4, np.float32))
+        graph.launch()
+        H.synchronize()
+        for i in range(len(items)):
+            assert np.array_equal(bits(keep[4 * i + 2].download(np.float32)), bits(want[i])), (rep, i)
+    g.free()
+
+
+def test_grouped_launch_rejects_bad_input():
+    items, _, keep = _group_case([(64, 64, O.Q4_0, 1, False)], 5)
+    dev, xp, yp = items[0][:3]
+    with pytest.raises(H.HipError, match="1..8"):
+        H.Group([(dev, xp, yp, 9)])
+    with pytest.raises(H.HipError, match="null"):
+        H.Group([(dev, None, yp, 1)])
+    H.Group([]).launch()  # an empty group is a no-op
