@@ -82,10 +82,10 @@ std::size_t max_lds_per_block() { return g_max_lds; }
 using namespace llmi_hip;
 
 struct llmi_hip_group {
-  GroupProblem* table = nullptr;  // device copy of the problem table
-  int nprob = 0;
-  int total_wgs = 0;
-  std::size_t lds = 0;
+  void* table = nullptr;  // device copy of the problem table, then the workgroup -> problem map
+  const GroupProblem* probs = nullptr;
+  const std::uint32_t* map = nullptr;
+  std::vector<GroupLaunch> launches;
   ~llmi_hip_group() {
     if (table != nullptr) (void)hipFree(table);
   }
@@ -427,13 +427,18 @@ int llmi_hip_group_create(const llmi_hip_weight* const* w, const float* const* x
                             false};
   }
   auto g = std::make_unique<llmi_hip_group>();
-  std::vector<GroupProblem> probs;
-  if (int rc = plan_group(entries.data(), count, &probs, &g->total_wgs, &g->lds)) return rc;
-  LLMI_REQUIRE(g->lds <= g_max_lds, "group: a product needs more LDS than one workgroup may use");
-  g->nprob = static_cast<int>(probs.size());
-  if (!probs.empty()) {
-    LLMI_TRY_HIP(hipMalloc(reinterpret_cast<void**>(&g->table), probs.size() * sizeof(GroupProblem)));
-    LLMI_TRY_HIP(hipMemcpy(g->table, probs.data(), probs.size() * sizeof(GroupProblem), hipMemcpyHostToDevice));
+  GroupPlan plan;
+  if (int rc = plan_group(entries.data(), count, &plan)) return rc;
+  g->launches = plan.launches;
+  const std::size_t pbytes = plan.probs.size() * sizeof(GroupProblem);
+  const std::size_t mbytes = plan.wg_prob.size() * sizeof(std::uint32_t);
+  if (pbytes + mbytes > 0) {
+    LLMI_TRY_HIP(hipMalloc(&g->table, pbytes + mbytes));
+    auto* base = static_cast<std::uint8_t*>(g->table);
+    LLMI_TRY_HIP(hipMemcpy(base, plan.probs.data(), pbytes, hipMemcpyHostToDevice));
+    if (mbytes > 0) LLMI_TRY_HIP(hipMemcpy(base + pbytes, plan.wg_prob.data(), mbytes, hipMemcpyHostToDevice));
+    g->probs = reinterpret_cast<const GroupProblem*>(base);
+    g->map = reinterpret_cast<const std::uint32_t*>(base + pbytes);
   }
   *out = g.release();
   return LLMI_OK;
@@ -442,7 +447,9 @@ int llmi_hip_group_create(const llmi_hip_weight* const* w, const float* const* x
 int llmi_hip_group_launch(const llmi_hip_group* g, void* stream) {
   LLMI_REQUIRE_INIT();
   LLMI_REQUIRE(g != nullptr, "group: null group");
-  return launch_group(g->table, g->nprob, g->total_wgs, g->lds, pick(stream));
+  for (const GroupLaunch& l : g->launches)
+    if (int rc = launch_group(g->probs, g->map, l, pick(stream))) return rc;
+  return LLMI_OK;
 }
 
 void llmi_hip_group_free(llmi_hip_group* g) { delete g; }

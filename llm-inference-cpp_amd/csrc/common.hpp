@@ -75,7 +75,6 @@ struct GroupProblem {
   float* y;
   int type, kind, in, nblk, out, rows, ntiles, bpw, accumulate, first_wg;
 };
-constexpr int kGroupThreads = 256;  // threads per workgroup of qgemv_group
 
 // One product y = W x (+ bias), rows 1..8, as the caller describes it.
 struct GroupEntry {
@@ -86,11 +85,20 @@ struct GroupEntry {
   std::size_t rows;
   bool accumulate;
 };
-// Lays out the products (skipping empty ones) as consecutive workgroup
-// ranges; *lds = the dynamic LDS every workgroup gets.
-int plan_group(const GroupEntry* entries, std::size_t count, std::vector<GroupProblem>* probs, int* total_wgs,
-               std::size_t* lds);
-int launch_group(const GroupProblem* probs_dev, int nprob, int total_wgs, std::size_t lds, hipStream_t s);
+// One kernel launch of a group: the products of weight type `type` and row
+// chunk `rchunk`, at probs[prob_offset...], workgroup w running product
+// wg_prob[map_offset + w].
+struct GroupLaunch {
+  int type = 0, rchunk = 1, waves = 1, total_wgs = 0;
+  std::size_t lds = 0, prob_offset = 0, map_offset = 0;
+};
+struct GroupPlan {
+  std::vector<GroupProblem> probs;
+  std::vector<std::uint32_t> wg_prob;
+  std::vector<GroupLaunch> launches;
+};
+int plan_group(const GroupEntry* entries, std::size_t count, GroupPlan* plan);
+int launch_group(const GroupProblem* probs_dev, const std::uint32_t* map_dev, const GroupLaunch& l, hipStream_t s);
 
 inline std::size_t block_code_bytes(int type) { return type == LLMI_TYPE_Q4_0 ? 16 : 32; }
 

@@ -25,8 +25,9 @@
 // qgemv_narrow (batch 1, matrices with few rows): 16-row tiles, 4x the
 // workgroups of qgemv_tile.
 //
-// qgemv_group: a fixed list of products (each batch 1..8) as one launch; each
-// workgroup runs one tile of one problem with the same tile functions.
+// qgemv_group: a fixed list of products (each batch 1..8) launched together
+// (one kernel per row chunk R present); each workgroup runs one tile of one
+// product with the same tile functions.
 //
 // qgemv_rows (batch > 8, the exact prefill path): one wavefront per tile
 // walks all blocks in order with the chains in registers.
@@ -46,17 +47,48 @@ __device__ __forceinline__ int sfield(std::uint32_t w, int offset, int width) {
   return static_cast<int>(__builtin_amdgcn_sbfe(w, offset, width));
 }
 
+// Global-memory pointers.  The grouped kernel reads its pointers from a
+// table, where the compiler cannot see that they point to global memory;
+// typing them keeps global (not flat) loads for the weights and scalar
+// loads for the activations.
+#define GMEM __attribute__((address_space(1)))
+template <typename T>
+__device__ __forceinline__ const GMEM T* gmem(const T* p) {
+  return (const GMEM T*)p;
+}
+template <typename T>
+__device__ __forceinline__ GMEM T* gmem_out(T* p) {
+  return (GMEM T*)p;
+}
+
 template <int TYPE>
 struct Block {
   static constexpr int kU = TYPE == LLMI_TYPE_Q8_0 ? 2 : 1;  // 16-byte loads per lane per block
   uint4 c[kU];
 };
 
-template <int TYPE>
-__device__ __forceinline__ Block<TYPE> load_block(const uint4* __restrict__ codes, std::size_t slot, int lane) {
+// Weights are streamed through once per product, so the batch 1..8 kernels
+// load them with the nontemporal hint (they are not kept in the caches for
+// reuse); the multi-row prefill kernel re-reads a tile per row chunk and uses
+// ordinary loads.
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+template <bool NT>
+__device__ __forceinline__ uint4 load16(const GMEM uint4* p) {
+  const GMEM u32x4* q = reinterpret_cast<const GMEM u32x4*>(p);
+  const u32x4 v = NT ? __builtin_nontemporal_load(q) : *q;
+  return uint4{v.x, v.y, v.z, v.w};
+}
+template <bool NT>
+__device__ __forceinline__ float loadf(const GMEM float* p) {
+  if (NT) return __builtin_nontemporal_load(p);
+  return *p;
+}
+
+template <int TYPE, bool NT>
+__device__ __forceinline__ Block<TYPE> load_block(const GMEM uint4* __restrict__ codes, std::size_t slot, int lane) {
   Block<TYPE> b;
 #pragma unroll
-  for (int u = 0; u < Block<TYPE>::kU; ++u) b.c[u] = codes[(slot * Block<TYPE>::kU + u) * kTileRows + lane];
+  for (int u = 0; u < Block<TYPE>::kU; ++u) b.c[u] = load16<NT>(codes + (slot * Block<TYPE>::kU + u) * kTileRows + lane);
   return b;
 }
 
@@ -84,18 +116,89 @@ __device__ __forceinline__ void unpack_words(const Block<TYPE>& b, std::uint32_t
   }
 }
 
-// Block sum of one full block: part = fma(x[i], code[i], part), i = 0..31.
+// Q4_0 decode constants, kept in VGPRs (v_and_or_b32 takes no literal).
+// Two 4-bit codes n (element value n - 8) are moved into the mantissas of an
+// f16 pair whose exponent makes the pair (1024 + n) (nibble at bits 0-3 of a
+// half) or (64 + n) (bits 4-7); one packed f16 subtraction of 1032 or 72
+// then gives n - 8 exactly, and v_fma_mix_f32 takes the f16 operand into an
+// fp32 fused multiply-add with no separate conversion.  The products and
+// sums are the same fp32 operations as with an fp32 code operand.
+struct Q4Magic {
+  std::uint32_t lo_mask, hi_mask, lo_exp, hi_exp;
+};
+__device__ __forceinline__ Q4Magic q4_magic() {
+  Q4Magic k{0x000F000Fu, 0x00F000F0u, 0x64006400u, 0x54005400u};
+  asm("" : "+v"(k.lo_mask), "+v"(k.hi_mask), "+v"(k.lo_exp), "+v"(k.hi_exp));
+  return k;
+}
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ half2_t f16_pair(std::uint32_t w, std::uint32_t mask, std::uint32_t exp_bits) {
+  std::uint32_t d;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(d) : "v"(w), "v"(mask), "v"(exp_bits));
+  return __builtin_bit_cast(half2_t, d);
+}
+
+// Block sum of one full block: part = fma(x[i], code[i], part), i = 0..31;
+// XP points to the block's 32 activations (global memory or LDS).  For one
+// input row Q4_0 codes go to v_fma_mix_f32 as f16 pairs; the multi-row
+// kernels instead convert each code to fp32 once (block_codes) and use it in
+// R v_fmac_f32, which issue at twice the rate of the mixed-precision FMA on
+// gfx950.
+template <int TYPE, typename XP>
+__device__ __forceinline__ float full_block_dot(const Block<TYPE>& b, XP __restrict__ xr, const Q4Magic& k) {
+  float part = 0.0f;
+  if (TYPE == LLMI_TYPE_Q8_0) {
+    const std::uint32_t w[8] = {b.c[0].x, b.c[0].y, b.c[0].z, b.c[0].w, b.c[Block<TYPE>::kU - 1].x,
+                                b.c[Block<TYPE>::kU - 1].y, b.c[Block<TYPE>::kU - 1].z, b.c[Block<TYPE>::kU - 1].w};
+#pragma unroll
+    for (int i = 0; i < kBlock; ++i) part = __builtin_fmaf(xr[i], code_of<TYPE>(w, i), part);
+    return part;
+  }
+  // Word j holds elements 8j..8j+7 as nibbles 0..7 (element 8j+2m in the low
+  // nibble of byte m, 8j+2m+1 in the high nibble).
+  const half2_t lo_off = {static_cast<_Float16>(-1032.0f), static_cast<_Float16>(-1032.0f)};
+  const half2_t hi_off = {static_cast<_Float16>(-72.0f), static_cast<_Float16>(-72.0f)};
+  const std::uint32_t w[4] = {b.c[0].x, b.c[0].y, b.c[0].z, b.c[0].w};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const std::uint32_t s = w[j] >> 8;
+    const half2_t e04 = f16_pair(w[j], k.lo_mask, k.lo_exp) + lo_off;  // elements 0, 4 of the word
+    const half2_t e15 = f16_pair(w[j], k.hi_mask, k.hi_exp) + hi_off;  // 1, 5
+    const half2_t e26 = f16_pair(s, k.lo_mask, k.lo_exp) + lo_off;     // 2, 6
+    const half2_t e37 = f16_pair(s, k.hi_mask, k.hi_exp) + hi_off;     // 3, 7
+    const XP xj = xr + 8 * j;
+    part = __builtin_fmaf(xj[0], static_cast<float>(e04.x), part);
+    part = __builtin_fmaf(xj[1], static_cast<float>(e15.x), part);
+    part = __builtin_fmaf(xj[2], static_cast<float>(e26.x), part);
+    part = __builtin_fmaf(xj[3], static_cast<float>(e37.x), part);
+    part = __builtin_fmaf(xj[4], static_cast<float>(e04.y), part);
+    part = __builtin_fmaf(xj[5], static_cast<float>(e15.y), part);
+    part = __builtin_fmaf(xj[6], static_cast<float>(e26.y), part);
+    part = __builtin_fmaf(xj[7], static_cast<float>(e37.y), part);
+  }
+  return part;
+}
+
+// The 32 codes of a full block as fp32 (for the multi-row kernels).
 template <int TYPE>
-__device__ __forceinline__ float full_block_dot(const std::uint32_t* w, const float* __restrict__ xr) {
+__device__ __forceinline__ void block_codes(const Block<TYPE>& b, float* c) {
+  std::uint32_t w[8];
+  unpack_words<TYPE>(b, w);
+#pragma unroll
+  for (int i = 0; i < kBlock; ++i) c[i] = code_of<TYPE>(w, i);
+}
+
+template <typename XP>
+__device__ __forceinline__ float codes_dot(const float* c, XP __restrict__ xr) {
   float part = 0.0f;
 #pragma unroll
-  for (int i = 0; i < kBlock; ++i) part = __builtin_fmaf(xr[i], code_of<TYPE>(w, i), part);
+  for (int i = 0; i < kBlock; ++i) part = __builtin_fmaf(xr[i], c[i], part);
   return part;
 }
 
 // Block sum of the final partial block (len < 32 elements).
-template <int TYPE>
-__device__ __noinline__ float tail_block_dot(const Block<TYPE> blk, const float* __restrict__ xr, int len) {
+template <int TYPE, typename XP>
+__device__ __noinline__ float tail_block_dot(const Block<TYPE> blk, XP __restrict__ xr, int len) {
   std::uint32_t w[8];
   unpack_words<TYPE>(blk, w);
   float part = 0.0f;
@@ -109,9 +212,10 @@ __device__ __noinline__ float tail_block_dot(const Block<TYPE> blk, const float*
 // (nr <= R; row r starts at x + r*in) into part[(r*nblk + b)*64 + lane], and
 // the blocks' scales into scl[b*64 + lane].  Loads run CH blocks ahead.
 template <int TYPE, int R, int CH>
-__device__ __forceinline__ void block_sums(const uint4* __restrict__ codes, const float* __restrict__ scales,
-                                           const float* __restrict__ x, std::size_t tile, int in, int nblk, int nr,
+__device__ __forceinline__ void block_sums(const GMEM uint4* __restrict__ codes, const GMEM float* __restrict__ scales,
+                                           const GMEM float* __restrict__ x, std::size_t tile, int in, int nblk, int nr,
                                            int b_begin, int b_end, int lane, float* part, float* scl) {
+  const Q4Magic k = q4_magic();
   const int nfull = in / kBlock;
   const int f_end = min(b_end, nfull);
   const std::size_t base = tile * nblk;
@@ -120,8 +224,8 @@ __device__ __forceinline__ void block_sums(const uint4* __restrict__ codes, cons
 #pragma unroll
   for (int j = 0; j < CH; ++j) {
     if (b_begin + j < f_end) {
-      cur[j] = load_block<TYPE>(codes, base + b_begin + j, lane);
-      cur_s[j] = scales[(base + b_begin + j) * kTileRows + lane];
+      cur[j] = load_block<TYPE, true>(codes, base + b_begin + j, lane);
+      cur_s[j] = loadf<true>(scales + (base + b_begin + j) * kTileRows + lane);
     }
   }
   for (int b = b_begin; b < f_end; b += CH) {
@@ -130,20 +234,24 @@ __device__ __forceinline__ void block_sums(const uint4* __restrict__ codes, cons
 #pragma unroll
     for (int j = 0; j < CH; ++j) {
       if (b + CH + j < f_end) {
-        nxt[j] = load_block<TYPE>(codes, base + b + CH + j, lane);
-        nxt_s[j] = scales[(base + b + CH + j) * kTileRows + lane];
+        nxt[j] = load_block<TYPE, true>(codes, base + b + CH + j, lane);
+        nxt_s[j] = loadf<true>(scales + (base + b + CH + j) * kTileRows + lane);
       }
     }
 #pragma unroll
     for (int j = 0; j < CH; ++j) {
       if (b + j < f_end) {
-        std::uint32_t w[8];
-        unpack_words<TYPE>(cur[j], w);
+        if (R == 1) {
+          part[(b + j) * kTileRows + lane] = full_block_dot<TYPE>(cur[j], x + (b + j) * kBlock, k);
+        } else {
+          float c[kBlock];
+          block_codes<TYPE>(cur[j], c);
 #pragma unroll
-        for (int r = 0; r < R; ++r) {
-          if (r < nr)
-            part[(r * nblk + b + j) * kTileRows + lane] =
-                full_block_dot<TYPE>(w, x + static_cast<std::size_t>(r) * in + (b + j) * kBlock);
+          for (int r = 0; r < R; ++r) {
+            if (r < nr)
+              part[(r * nblk + b + j) * kTileRows + lane] =
+                  codes_dot(c, x + static_cast<std::size_t>(r) * in + (b + j) * kBlock);
+          }
         }
         scl[(b + j) * kTileRows + lane] = cur_s[j];
       }
@@ -155,11 +263,11 @@ __device__ __forceinline__ void block_sums(const uint4* __restrict__ codes, cons
     }
   }
   if (nfull < nblk && nfull >= b_begin && nfull < b_end) {
-    const Block<TYPE> blk = load_block<TYPE>(codes, base + nfull, lane);
+    const Block<TYPE> blk = load_block<TYPE, true>(codes, base + nfull, lane);
     for (int r = 0; r < nr; ++r)
       part[(r * nblk + nfull) * kTileRows + lane] =
           tail_block_dot<TYPE>(blk, x + static_cast<std::size_t>(r) * in + nfull * kBlock, in - nfull * kBlock);
-    scl[nfull * kTileRows + lane] = scales[(base + nfull) * kTileRows + lane];
+    scl[nfull * kTileRows + lane] = loadf<true>(scales + (base + nfull) * kTileRows + lane);
   }
 }
 
@@ -182,8 +290,16 @@ __device__ __forceinline__ float chain_lds(const float* part, const float* scl, 
   return acc;
 }
 
-__device__ __forceinline__ void store_out(float* __restrict__ y, std::size_t o, float v, int accumulate) {
+__device__ __forceinline__ void store_out(GMEM float* __restrict__ y, std::size_t o, float v, int accumulate) {
   y[o] = accumulate ? y[o] + v : v;
+}
+
+// Load chunk (blocks in flight per wavefront) of the 64-row tile kernels,
+// from launch-shape sweeps on MI355X: Q4_0 takes up to 4 blocks (one 16-byte
+// load each), Q8_0 one block (two loads).
+template <int TYPE>
+constexpr int wide_chunk() {
+  return TYPE == LLMI_TYPE_Q8_0 ? 1 : 4;
 }
 
 // One 64-row tile for input rows [0, nr), nr <= R (x, y already point at the
@@ -191,10 +307,10 @@ __device__ __forceinline__ void store_out(float* __restrict__ y, std::size_t o, 
 // each, and park block sums and scales in LDS (part[nr][nblk][64] then
 // scale[nblk][64]); wavefront w then runs the chains of rows w, w + W, ...
 // Every thread of the workgroup must call it (it has a barrier).
-template <int TYPE, int R, int CH>
-__device__ __forceinline__ void wide_tile(const uint4* __restrict__ codes, const float* __restrict__ scales,
-                                          const float* __restrict__ x, const float* __restrict__ bias,
-                                          float* __restrict__ y, int in, int nblk, int out, int nr, int bpw,
+template <int TYPE, int R>
+__device__ __forceinline__ void wide_tile(const GMEM uint4* __restrict__ codes, const GMEM float* __restrict__ scales,
+                                          const GMEM float* __restrict__ x, const GMEM float* __restrict__ bias,
+                                          GMEM float* __restrict__ y, int in, int nblk, int out, int nr, int bpw,
                                           int accumulate, std::size_t tile, float* lds) {
   float* part = lds;
   float* scl = lds + static_cast<std::size_t>(nr) * nblk * kTileRows;
@@ -203,7 +319,7 @@ __device__ __forceinline__ void wide_tile(const uint4* __restrict__ codes, const
   const int nwaves = blockDim.x >> 6;
   const int b_begin = wave * bpw;
   const int b_end = min(nblk, b_begin + bpw);
-  block_sums<TYPE, R, CH>(codes, scales, x, tile, in, nblk, nr, b_begin, b_end, lane, part, scl);
+  block_sums<TYPE, R, wide_chunk<TYPE>()>(codes, scales, x, tile, in, nblk, nr, b_begin, b_end, lane, part, scl);
   __syncthreads();
   const std::size_t o = tile * kTileRows + lane;
   for (int r = wave; r < nr; r += nwaves) {
@@ -222,10 +338,11 @@ __device__ __forceinline__ void wide_tile(const uint4* __restrict__ codes, const
 // and lanes 0-15 run the chain.  LDS: x[in (padded to 4)], part[nblk][16],
 // scale[nblk][16].
 template <int TYPE>
-__device__ __forceinline__ void narrow_tile(const uint4* __restrict__ codes, const float* __restrict__ scales,
-                                            const float* __restrict__ x, const float* __restrict__ bias,
-                                            float* __restrict__ y, int in, int nblk, int out, int bpg, int accumulate,
+__device__ __forceinline__ void narrow_tile(const GMEM uint4* __restrict__ codes, const GMEM float* __restrict__ scales,
+                                            const GMEM float* __restrict__ x, const GMEM float* __restrict__ bias,
+                                            GMEM float* __restrict__ y, int in, int nblk, int out, int bpg, int accumulate,
                                             std::size_t tile16, float* lds) {
+  const Q4Magic k = q4_magic();
   float* xs = lds;
   float* part = lds + ((in + 3) & ~3);
   float* scl = part + nblk * 16;
@@ -241,18 +358,10 @@ __device__ __forceinline__ void narrow_tile(const uint4* __restrict__ codes, con
   const int b_begin = group * bpg;
   const int b_end = min(nblk, b_begin + bpg);
   for (int b = b_begin; b < b_end; ++b) {
-    const Block<TYPE> blk = load_block<TYPE>(codes, tile * nblk + b, sub);
-    const float sc = scales[(tile * nblk + b) * kTileRows + sub];
-    std::uint32_t w[8];
-    unpack_words<TYPE>(blk, w);
-    float p;
-    if (b < nfull) {
-      p = full_block_dot<TYPE>(w, xs + b * kBlock);
-    } else {
-      p = 0.0f;
-      const int len = in - b * kBlock;
-      for (int i = 0; i < len; ++i) p = __builtin_fmaf(xs[b * kBlock + i], code_of<TYPE>(w, i), p);
-    }
+    const Block<TYPE> blk = load_block<TYPE, true>(codes, tile * nblk + b, sub);
+    const float sc = loadf<true>(scales + (tile * nblk + b) * kTileRows + sub);
+    const float p = b < nfull ? full_block_dot<TYPE>(blk, xs + b * kBlock, k)
+                              : tail_block_dot<TYPE>(blk, xs + b * kBlock, in - b * kBlock);
     part[b * 16 + r] = p;
     scl[b * 16 + r] = sc;
   }
@@ -263,8 +372,6 @@ __device__ __forceinline__ void narrow_tile(const uint4* __restrict__ codes, con
   }
 }
 
-constexpr int chunk_for(int type) { return type == LLMI_TYPE_Q8_0 ? 2 : 4; }
-
 // grid (ntiles, ceil(rows / R)).
 template <int TYPE, int R>
 __global__ void __launch_bounds__(1024) qgemv_tile(const uint4* __restrict__ codes, const float* __restrict__ scales,
@@ -274,9 +381,9 @@ __global__ void __launch_bounds__(1024) qgemv_tile(const uint4* __restrict__ cod
   extern __shared__ float lds[];
   const int r0 = blockIdx.y * R;
   const int nr = min(R, rows - r0);
-  wide_tile<TYPE, R, chunk_for(TYPE)>(codes, scales, x + static_cast<std::size_t>(r0) * in, bias,
-                                      y + static_cast<std::size_t>(r0) * out, in, nblk, out, nr, bpw, accumulate,
-                                      blockIdx.x, lds);
+  wide_tile<TYPE, R>(gmem(codes), gmem(scales), gmem(x + static_cast<std::size_t>(r0) * in), gmem(bias),
+                     gmem_out(y + static_cast<std::size_t>(r0) * out), in, nblk, out, nr, bpw, accumulate, blockIdx.x,
+                     lds);
 }
 
 template <int TYPE>
@@ -285,54 +392,36 @@ __global__ void __launch_bounds__(1024) qgemv_narrow(const uint4* __restrict__ c
                                                      float* __restrict__ y, int in, int nblk, int out, int bpg,
                                                      int accumulate) {
   extern __shared__ float lds[];
-  narrow_tile<TYPE>(codes, scales, x, bias, y, in, nblk, out, bpg, accumulate, blockIdx.x, lds);
+  narrow_tile<TYPE>(gmem(codes), gmem(scales), gmem(x), gmem(bias), gmem_out(y), in, nblk, out, bpg, accumulate,
+                    blockIdx.x, lds);
 }
 
-// Workgroup w runs workgroup (w - first_wg) of the problem whose range holds
-// w, found by binary search over the table (sorted by first_wg).
-__global__ void __launch_bounds__(kGroupThreads) qgemv_group(const GroupProblem* __restrict__ probs, int nprob) {
+// One launch over a group's products that share the weight type and the row
+// chunk R (R == 1 also runs the 16-row tiles).  Workgroup w runs workgroup
+// (w - first_wg) of problem wg_prob[w].
+template <int TYPE, int R>
+__global__ void __launch_bounds__(1024) qgemv_group(const GroupProblem* __restrict__ probs,
+                                                    const std::uint32_t* __restrict__ wg_prob) {
   extern __shared__ float lds[];
   const int wg = blockIdx.x;
-  int lo = 0, hi = nprob - 1;
-  while (lo < hi) {
-    const int mid = (lo + hi + 1) >> 1;
-    if (probs[mid].first_wg <= wg) lo = mid;
-    else hi = mid - 1;
-  }
-  const GroupProblem p = probs[lo];
+  // Uniform by construction; readfirstlane keeps the descriptor in SGPRs.
+  const int idx = __builtin_amdgcn_readfirstlane(static_cast<int>(wg_prob[wg]));
+  const GroupProblem p = probs[idx];
   const int local = wg - p.first_wg;
-  const uint4* codes = reinterpret_cast<const uint4*>(p.codes);
-  if (p.kind == GroupProblem::kNarrow) {
-    if (p.type == LLMI_TYPE_Q8_0)
-      narrow_tile<LLMI_TYPE_Q8_0>(codes, p.scales, p.x, p.bias, p.y, p.in, p.nblk, p.out, p.bpw, p.accumulate, local, lds);
-    else
-      narrow_tile<LLMI_TYPE_Q4_0>(codes, p.scales, p.x, p.bias, p.y, p.in, p.nblk, p.out, p.bpw, p.accumulate, local, lds);
+  const GMEM uint4* codes = gmem(reinterpret_cast<const uint4*>(p.codes));
+  const GMEM float* scales = gmem(p.scales);
+  const GMEM float* bias = gmem(p.bias);
+  if (R == 1 && p.kind == GroupProblem::kNarrow) {
+    narrow_tile<TYPE>(codes, scales, gmem(p.x), bias, gmem_out(p.y), p.in, p.nblk, p.out, p.bpw, p.accumulate, local,
+                      lds);
     return;
   }
   const int tile = local % p.ntiles;
-  const int r0 = (local / p.ntiles) * p.kind;
-  const int nr = min(p.kind, p.rows - r0);
-  const float* x = p.x + static_cast<std::size_t>(r0) * p.in;
-  float* y = p.y + static_cast<std::size_t>(r0) * p.out;
-#define LLMI_GROUP_WIDE(T, RR)                                                                                  \
-  wide_tile<T, RR, chunk_for(T)>(codes, p.scales, x, p.bias, y, p.in, p.nblk, p.out, nr, p.bpw, p.accumulate, \
-                                 tile, lds)
-  if (p.type == LLMI_TYPE_Q8_0) {
-    switch (p.kind) {
-      case 1: LLMI_GROUP_WIDE(LLMI_TYPE_Q8_0, 1); break;
-      case 2: LLMI_GROUP_WIDE(LLMI_TYPE_Q8_0, 2); break;
-      case 4: LLMI_GROUP_WIDE(LLMI_TYPE_Q8_0, 4); break;
-      default: LLMI_GROUP_WIDE(LLMI_TYPE_Q8_0, 8); break;
-    }
-  } else {
-    switch (p.kind) {
-      case 1: LLMI_GROUP_WIDE(LLMI_TYPE_Q4_0, 1); break;
-      case 2: LLMI_GROUP_WIDE(LLMI_TYPE_Q4_0, 2); break;
-      case 4: LLMI_GROUP_WIDE(LLMI_TYPE_Q4_0, 4); break;
-      default: LLMI_GROUP_WIDE(LLMI_TYPE_Q4_0, 8); break;
-    }
-  }
-#undef LLMI_GROUP_WIDE
+  const int r0 = (local / p.ntiles) * R;
+  const int nr = min(R, p.rows - r0);
+  const GMEM float* x = gmem(p.x + static_cast<std::size_t>(r0) * p.in);
+  GMEM float* y = gmem_out(p.y + static_cast<std::size_t>(r0) * p.out);
+  wide_tile<TYPE, R>(codes, scales, x, bias, y, p.in, p.nblk, p.out, nr, p.bpw, p.accumulate, tile, lds);
 }
 
 // ------------------------------------------------------------ batch > 8
@@ -361,8 +450,8 @@ __global__ void __launch_bounds__(256) qgemv_rows(const uint4* __restrict__ code
 #pragma unroll
   for (int j = 0; j < CH; ++j) {
     if (j < nfull) {
-      cur[j] = load_block<TYPE>(codes, tile * nblk + j, lane);
-      cur_s[j] = scales[(tile * nblk + j) * kTileRows + lane];
+      cur[j] = load_block<TYPE, false>(gmem(codes), tile * nblk + j, lane);
+      cur_s[j] = loadf<false>(gmem(scales + (tile * nblk + j) * kTileRows + lane));
     }
   }
   for (int b = 0; b < nfull; b += CH) {
@@ -371,19 +460,19 @@ __global__ void __launch_bounds__(256) qgemv_rows(const uint4* __restrict__ code
 #pragma unroll
     for (int j = 0; j < CH; ++j) {
       if (b + CH + j < nfull) {
-        nxt[j] = load_block<TYPE>(codes, tile * nblk + b + CH + j, lane);
-        nxt_s[j] = scales[(tile * nblk + b + CH + j) * kTileRows + lane];
+        nxt[j] = load_block<TYPE, false>(gmem(codes), tile * nblk + b + CH + j, lane);
+        nxt_s[j] = loadf<false>(gmem(scales + (tile * nblk + b + CH + j) * kTileRows + lane));
       }
     }
 #pragma unroll
     for (int j = 0; j < CH; ++j) {
       if (b + j < nfull) {
-        std::uint32_t w[8];
-        unpack_words<TYPE>(cur[j], w);
+        float c[kBlock];
+        block_codes<TYPE>(cur[j], c);
 #pragma unroll
         for (int r = 0; r < R; ++r) {
           if (r < nr) {
-            const float p = full_block_dot<TYPE>(w, xb + static_cast<std::size_t>(r) * in + (b + j) * kBlock);
+            const float p = codes_dot(c, xb + static_cast<std::size_t>(r) * in + (b + j) * kBlock);
             acc[r] = __builtin_fmaf(p, cur_s[j], acc[r]);
           }
         }
@@ -396,8 +485,8 @@ __global__ void __launch_bounds__(256) qgemv_rows(const uint4* __restrict__ code
     }
   }
   if (nfull < nblk) {
-    const Block<TYPE> blk = load_block<TYPE>(codes, tile * nblk + nfull, lane);
-    const float s = scales[(tile * nblk + nfull) * kTileRows + lane];
+    const Block<TYPE> blk = load_block<TYPE, false>(gmem(codes), tile * nblk + nfull, lane);
+    const float s = loadf<false>(gmem(scales + (tile * nblk + nfull) * kTileRows + lane));
     for (int r = 0; r < nr; ++r) {
       const float p = tail_block_dot<TYPE>(blk, xb + static_cast<std::size_t>(r) * in + nfull * kBlock, in - nfull * kBlock);
 #pragma unroll
@@ -438,6 +527,14 @@ int pick_chunk(std::size_t rows, std::size_t nblk, std::size_t budget) {
   return 0;
 }
 
+// Wavefronts per 64-row tile: each takes about kBlocksPerWave blocks (4 for
+// Q4_0, 2 for Q8_0: about 4 KB of codes and scales in flight per
+// wavefront), at most 16.  Measured on MI355X over the 151936x896 lm_head.
+int wide_waves(std::size_t nblk, int type) {
+  const std::size_t per = type == LLMI_TYPE_Q8_0 ? 2 : 4;
+  return static_cast<int>(std::clamp<std::size_t>(ceil_div(nblk, per), 1, 16));
+}
+
 struct TilePlan {
   int kind = 0;  // 0: qgemv_rows; GroupProblem::kNarrow; or the row chunk R of qgemv_tile
   int waves = 1;
@@ -446,10 +543,9 @@ struct TilePlan {
 };
 
 // Launch shape of a single product.  Batch 1 matrices with fewer than
-// kNarrowTiles 64-row tiles use 16-row tiles; otherwise the wide tile with
-// enough wavefronts per workgroup to put ~kTargetWaves in the grid.
+// kNarrowTiles 64-row tiles use 16-row tiles (more workgroups); otherwise
+// the wide tile.
 TilePlan plan_single(const DeviceMatrix& m, std::size_t rows) {
-  constexpr std::size_t kTargetWaves = 8192;
   constexpr std::size_t kNarrowTiles = 128;
   constexpr std::size_t kBlocksPerGroup = 2;
   const std::size_t nblk = std::max<std::size_t>(m.nblk, 1);
@@ -466,11 +562,8 @@ TilePlan plan_single(const DeviceMatrix& m, std::size_t rows) {
   int r = pick_chunk(rows, nblk, kLdsTarget);
   if (r == 0) r = pick_chunk(1, nblk, max_lds_per_block());
   if (r == 0) return p;  // rows too long for LDS staging: qgemv_rows
-  const std::size_t wgs = m.ntiles * ceil_div(rows, r);
-  const std::size_t per_wg = std::max<std::size_t>(1, ceil_div(kTargetWaves, wgs));
-  const std::size_t waves = std::max<std::size_t>(1, std::min<std::size_t>({16, nblk, per_wg}));
   p.kind = r;
-  p.bpw = static_cast<int>(ceil_div(nblk, waves));
+  p.bpw = static_cast<int>(ceil_div(nblk, wide_waves(nblk, m.type)));
   p.waves = static_cast<int>(ceil_div(nblk, p.bpw));
   p.lds = wide_lds(nblk, std::min<std::size_t>(rows, r));
   return p;
@@ -535,12 +628,11 @@ int launch_matmul(const DeviceMatrix& m, const float* x, std::size_t rows, const
   return LLMI_OK;
 }
 
-int plan_group(const GroupEntry* entries, std::size_t count, std::vector<GroupProblem>* probs, int* total_wgs,
-               std::size_t* lds) {
-  constexpr std::size_t kWaves = kGroupThreads / 64;
-  // Narrow 16-row tiles only when the wide tiles would leave the GPU mostly
-  // idle (fewer than ~4 workgroups per CU).
+int plan_group(const GroupEntry* entries, std::size_t count, GroupPlan* plan) {
+  // Narrow 16-row tiles for batch-1 products only when the 64-row tiles would
+  // leave the GPU mostly idle (fewer than ~4 workgroups per CU).
   constexpr std::size_t kNarrowBelow = 1024;
+  *plan = GroupPlan{};
   std::size_t wide_total = 0;
   for (std::size_t i = 0; i < count; ++i) {
     const GroupEntry& e = entries[i];
@@ -550,54 +642,99 @@ int plan_group(const GroupEntry* entries, std::size_t count, std::vector<GroupPr
     if (int rc = check_shape(*e.m, e.rows)) return rc;
     wide_total += e.m->ntiles * ceil_div(e.rows, 8);
   }
-  probs->clear();
-  std::size_t wg = 0, max_lds = 0;
-  for (std::size_t i = 0; i < count; ++i) {
-    const GroupEntry& e = entries[i];
-    const DeviceMatrix& m = *e.m;
-    if (m.out == 0) continue;
-    GroupProblem p{};
-    p.codes = m.codes;
-    p.scales = m.scales;
-    p.x = e.x;
-    p.bias = e.bias;
-    p.y = e.y;
-    p.type = m.type;
-    p.in = static_cast<int>(m.in);
-    p.nblk = static_cast<int>(m.nblk);
-    p.out = static_cast<int>(m.out);
-    p.rows = static_cast<int>(e.rows);
-    p.ntiles = static_cast<int>(m.ntiles);
-    p.accumulate = e.accumulate ? 1 : 0;
-    std::size_t wgs = 0, need = 0;
-    if (e.rows == 1 && wide_total < kNarrowBelow && narrow_lds(m.in, m.nblk) <= max_lds_per_block()) {
-      p.kind = GroupProblem::kNarrow;
-      p.bpw = static_cast<int>(ceil_div(m.nblk, kWaves * 4));
-      wgs = ceil_div(m.out, 16);
-      need = narrow_lds(m.in, m.nblk);
-    } else {
-      int r = pick_chunk(e.rows, m.nblk, kLdsTarget);
+  // Products are launched by weight type and row chunk R (one kernel
+  // instance each).
+  for (int type : {LLMI_TYPE_Q8_0, LLMI_TYPE_Q4_0})
+  for (int R : {1, 2, 4, 8}) {
+    std::vector<GroupProblem> probs;
+    std::vector<std::size_t> nblks;
+    std::size_t biggest = 0;
+    int waves = 1;
+    for (std::size_t i = 0; i < count; ++i) {
+      const GroupEntry& e = entries[i];
+      const DeviceMatrix& m = *e.m;
+      if (m.out == 0) continue;
+      const bool narrow = e.rows == 1 && wide_total < kNarrowBelow && narrow_lds(m.in, m.nblk) <= max_lds_per_block();
+      int r = narrow ? 1 : pick_chunk(e.rows, m.nblk, kLdsTarget);
       if (r == 0) r = pick_chunk(1, m.nblk, max_lds_per_block());
       LLMI_REQUIRE(r != 0, "group: rows too long for the grouped GEMV (in above ~10k)");
-      p.kind = r;
-      p.bpw = static_cast<int>(ceil_div(m.nblk, kWaves));
-      wgs = m.ntiles * ceil_div(e.rows, r);
-      need = wide_lds(m.nblk, std::min<std::size_t>(e.rows, r));
+      if (r != R || m.type != type) continue;
+      GroupProblem p{};
+      p.codes = m.codes;
+      p.scales = m.scales;
+      p.x = e.x;
+      p.bias = e.bias;
+      p.y = e.y;
+      p.type = m.type;
+      p.kind = narrow ? GroupProblem::kNarrow : r;
+      p.in = static_cast<int>(m.in);
+      p.nblk = static_cast<int>(m.nblk);
+      p.out = static_cast<int>(m.out);
+      p.rows = static_cast<int>(e.rows);
+      p.ntiles = static_cast<int>(m.ntiles);
+      p.accumulate = e.accumulate ? 1 : 0;
+      probs.push_back(p);
+      // The launch's wavefront count follows its largest product.
+      const std::size_t bytes = m.code_bytes + m.scale_bytes;
+      if (bytes > biggest) {
+        biggest = bytes;
+        waves = wide_waves(m.nblk, m.type);
+      }
     }
-    p.first_wg = static_cast<int>(wg);
-    wg += wgs;
-    LLMI_REQUIRE(wg <= 0x7FFFFFFFu, "group: too many workgroups");
-    max_lds = std::max(max_lds, need);
-    probs->push_back(p);
+    if (probs.empty()) continue;
+    GroupLaunch l;
+    l.type = type;
+    l.rchunk = R;
+    l.waves = waves;
+    l.prob_offset = plan->probs.size();
+    l.map_offset = plan->wg_prob.size();
+    std::size_t wg = 0;
+    for (std::size_t j = 0; j < probs.size(); ++j) {
+      GroupProblem& p = probs[j];
+      std::size_t wgs = 0, need = 0;
+      if (p.kind == GroupProblem::kNarrow) {
+        p.bpw = static_cast<int>(ceil_div(p.nblk, static_cast<std::size_t>(waves) * 4));
+        wgs = ceil_div(p.out, 16);
+        need = narrow_lds(p.in, p.nblk);
+      } else {
+        p.bpw = static_cast<int>(ceil_div(p.nblk, waves));
+        wgs = static_cast<std::size_t>(p.ntiles) * ceil_div(p.rows, R);
+        need = wide_lds(p.nblk, std::min(p.rows, R));
+      }
+      p.first_wg = static_cast<int>(wg);
+      wg += wgs;
+      LLMI_REQUIRE(wg <= 0x7FFFFFFFu, "group: too many workgroups");
+      l.lds = std::max(l.lds, need);
+      plan->wg_prob.insert(plan->wg_prob.end(), wgs, static_cast<std::uint32_t>(j));
+    }
+    LLMI_REQUIRE(l.lds <= max_lds_per_block(), "group: a product needs more LDS than one workgroup may use");
+    l.total_wgs = static_cast<int>(wg);
+    plan->probs.insert(plan->probs.end(), probs.begin(), probs.end());
+    plan->launches.push_back(l);
   }
-  *total_wgs = static_cast<int>(wg);
-  *lds = max_lds;
   return LLMI_OK;
 }
 
-int launch_group(const GroupProblem* probs_dev, int nprob, int total_wgs, std::size_t lds, hipStream_t s) {
-  if (nprob == 0 || total_wgs == 0) return LLMI_OK;
-  qgemv_group<<<static_cast<unsigned>(total_wgs), kGroupThreads, lds, s>>>(probs_dev, nprob);
+int launch_group(const GroupProblem* probs_dev, const std::uint32_t* map_dev, const GroupLaunch& l, hipStream_t s) {
+  if (l.total_wgs == 0) return LLMI_OK;
+  const dim3 grid(static_cast<unsigned>(l.total_wgs)), block(static_cast<unsigned>(l.waves * 64));
+  const GroupProblem* probs = probs_dev + l.prob_offset;
+  const std::uint32_t* map = map_dev + l.map_offset;
+  if (l.type == LLMI_TYPE_Q8_0) {
+    switch (l.rchunk) {
+      case 1: qgemv_group<LLMI_TYPE_Q8_0, 1><<<grid, block, l.lds, s>>>(probs, map); break;
+      case 2: qgemv_group<LLMI_TYPE_Q8_0, 2><<<grid, block, l.lds, s>>>(probs, map); break;
+      case 4: qgemv_group<LLMI_TYPE_Q8_0, 4><<<grid, block, l.lds, s>>>(probs, map); break;
+      default: qgemv_group<LLMI_TYPE_Q8_0, 8><<<grid, block, l.lds, s>>>(probs, map); break;
+    }
+  } else {
+    switch (l.rchunk) {
+      case 1: qgemv_group<LLMI_TYPE_Q4_0, 1><<<grid, block, l.lds, s>>>(probs, map); break;
+      case 2: qgemv_group<LLMI_TYPE_Q4_0, 2><<<grid, block, l.lds, s>>>(probs, map); break;
+      case 4: qgemv_group<LLMI_TYPE_Q4_0, 4><<<grid, block, l.lds, s>>>(probs, map); break;
+      default: qgemv_group<LLMI_TYPE_Q4_0, 8><<<grid, block, l.lds, s>>>(probs, map); break;
+    }
+  }
   LLMI_TRY_HIP(hipGetLastError());
   return LLMI_OK;
 }

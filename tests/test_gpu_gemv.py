@@ -71,6 +71,30 @@ def test_batches_and_ragged_shapes_match_oracle(qt, rows, out, n_in):
         assert np.array_equal(bits(got), bits(want)), (rows, out, n_in, b is None)
 
 
+@pytest.mark.parametrize("qt", [O.Q8_0, O.Q4_0])
+def test_extreme_activations_match_oracle(qt):
+    """Subnormal, zero, negative-zero and very large activations: the f16
+    code operands of the Q4_0 fused multiply-adds and the Q8_0 conversions
+    give the oracle's fp32 results bit for bit in every kernel shape."""
+    orc = O.oracle()
+    rng = np.random.default_rng(11)
+    for out, n_in, rows in ((200, 576, 1), (4000, 96, 1), (200, 576, 3), (130, 100, 9), (65, 33, 1)):
+        w = synth.normal(out + n_in, out * n_in, 0.0, 0.02)
+        data, scales = orc.quantize(w, out, n_in, qt)
+        dev = H.Weight.upload(data, scales, out, n_in, qt)
+        x = synth.normal(rows + n_in, rows * n_in, 0.0, 1.0)
+        kind = rng.integers(0, 6, x.size)
+        sub = (rng.uniform(-1, 1, x.size) * 2.0 ** -127).astype(np.float32)  # subnormal
+        x = np.where(kind == 0, sub, x)
+        x = np.where(kind == 1, np.float32(0.0), x)
+        x = np.where(kind == 2, np.float32(-0.0), x)
+        x = np.where(kind == 3, x * np.float32(1e30), x).astype(np.float32)
+        assert np.count_nonzero(np.abs(x[kind == 0]) < 2.0 ** -126) > 0
+        got = dev.matmul(x, rows, None)
+        want = orc.matmul(x, rows, n_in, data, scales, qt, out, None)
+        assert np.array_equal(bits(got), bits(want)), (out, n_in, rows)
+
+
 def test_device_pointer_entry_point_and_determinism():
     orc = O.oracle()
     out, n_in, qt = 4864, 896, O.Q4_0
