@@ -170,6 +170,67 @@ def target_shapes():
     return res
 
 
+QWEN_LAYER = [("q_proj", 896, 896), ("k_proj", 128, 896), ("v_proj", 128, 896), ("o_proj", 896, 896),
+              ("gate_proj", 4864, 896), ("up_proj", 4864, 896), ("down_proj", 896, 4864)]
+MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense bf16
+
+
+def prefill_gemm(steps=20, warmup=3):
+    """M=512 tokens of fp32 activations against
+    every Qwen2.5-0.5B linear layer (24 layers x 7 products) in Q8_0, on the
+    bf16-MFMA GEMM.  All 168 products run as one grouped launch per step
+    (llmi_hip_gemm_group); a second figure runs them as 24 per-layer groups."""
+    M, L = 512, 24
+    xs = {}
+    for n_in in sorted({i for _, _, i in QWEN_LAYER}):
+        xb = H.DeviceBuffer(M * n_in * 4)
+        H.synth_normal_dev(xb, M * n_in, 300 + n_in, 0.0, 1.0)
+        xs[n_in] = xb
+    stage = H.DeviceBuffer(4864 * 896 * 4)
+    ws, ys, items, layers = [], [], [], []
+    for layer in range(L):
+        li = []
+        for j, (_, out, n_in) in enumerate(QWEN_LAYER):
+            H.synth_normal_dev(stage, out * n_in, 7000 + 16 * layer + j, 0.0, 0.02)
+            w = H.Weight.quantize_dev(stage.ptr, out, n_in, H.Q8_0)
+            y = H.DeviceBuffer(M * out * 4)
+            ws.append(w)
+            ys.append(y)
+            li.append((w, xs[n_in].ptr, y.ptr, M))
+        items += li
+        layers.append(li)
+    stage.free()
+    flops = 2.0 * M * sum(o * i for _, o, i in QWEN_LAYER) * L
+    wbytes = sum(w.byte_size for w in ws)
+    res = {}
+    for mode, groups in (("one_launch", [H.GemmGroup(items)]), ("per_layer", [H.GemmGroup(li) for li in layers])):
+        for _ in range(warmup):
+            for g in groups:
+                g.launch()
+        H.synchronize()
+        t = H.Timer()
+        t.start()
+        for _ in range(steps):
+            for g in groups:
+                g.launch()
+        ms = t.stop() / steps
+        H.synchronize()
+        tf = flops / (ms * 1e-3) / 1e12
+        res[mode] = dict(ms=round(ms, 4), tflops=round(tf, 1), frac_of_mfma_peak=round(tf / MFMA_PEAK_TFLOPS, 4),
+                         launches=len(groups))
+        for g in groups:
+            g.free()
+    for b in list(xs.values()) + ys:
+        b.free()
+    for w in ws:
+        w.free()
+    res.update(workload="24 layers x {q,k,v,o 896/128 x 896; gate,up 4864x896; down 896x4864} Q8_0, M=512, fp32 in/out",
+               gflop=round(flops / 1e9, 2), weight_bytes=wbytes, precision="bf16 operands, fp32 accumulate (tolerance 2e-2)")
+    print(f"[bench] c5 prefill GEMM: {res['one_launch']['tflops']} TFLOP/s one launch, "
+          f"{res['per_layer']['tflops']} per-layer", file=sys.stderr, flush=True)
+    return res
+
+
 DECODE_RUNS = [  # (key, golden fixture, model config, weight type): BASELINE.json configs[2], configs[3]
     ("c3_smollm2_135m_q8_0", "c3_smollm2_q8", synth.SMOLLM2_135M, H.Q8_0),
     ("c4_qwen25_05b_q4_0", "c4_qwen25_q4", synth.QWEN25_05B, H.Q4_0),
@@ -262,6 +323,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-targets", action="store_true", help="skip the Qwen2.5 shape table")
     ap.add_argument("--no-decode", action="store_true", help="skip the full-model decode runs")
+    ap.add_argument("--no-gemm", action="store_true", help="skip the prefill GEMM (configs[4])")
     ap.add_argument("--no-graphs", action="store_true",
                     help="time the linear pass with plain launches only (for profilers that do not follow graphs)")
     args = ap.parse_args()
@@ -298,6 +360,7 @@ def main():
 
     targets = {} if args.no_targets else target_shapes()
     decode = {} if args.no_decode else decode_runs()
+    gemm = {} if args.no_gemm else prefill_gemm()
     cpu = None if args.no_cpu else cpu_baseline()
 
     line = {
@@ -344,6 +407,7 @@ def main():
         },
         "targets_qwen25": targets,
         "decode": decode,
+        "prefill_gemm_c5": gemm,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -178,6 +178,23 @@ int llmi_hip_group_create(const llmi_hip_weight* const* w, const float* const* x
 int llmi_hip_group_launch(const llmi_hip_group* group, void* stream);
 void llmi_hip_group_free(llmi_hip_group* group);
 
+/* Prefill GEMM on the matrix cores: quant::matmul (quant.cpp:119-153) as the
+ * reference's prefill calls it with rows = T tokens (transformer.cpp:245-291),
+ * computed with x and the dequantized weights rounded to bf16 and fp32
+ * accumulation (bf16 MFMA).  NOT bit-exact: |y - y_ref| <= 2e-2 * max|y_ref|
+ * (typically ~1e-3).  Use llmi_hip_matmul_dev where the reference's exact
+ * results are needed.  Any rows >= 1; efficient for rows >= 64.
+ * llmi_hip_gemm_group_* run a list of such products as one launch (per
+ * weight type), e.g. the q/k/v or gate/up products of a layer. */
+int llmi_hip_matmul_mfma_dev(const llmi_hip_weight* weight, const float* x_dev, size_t rows, const float* bias_dev,
+                             float* y_dev, void* stream);
+typedef struct llmi_hip_gemm_group llmi_hip_gemm_group;
+int llmi_hip_gemm_group_create(const llmi_hip_weight* const* w, const float* const* x_dev, const size_t* rows,
+                               const float* const* bias_dev, float* const* y_dev, size_t count,
+                               llmi_hip_gemm_group** out);
+int llmi_hip_gemm_group_launch(const llmi_hip_gemm_group* group, void* stream);
+void llmi_hip_gemm_group_free(llmi_hip_gemm_group* group);
+
 /* ------------------------------------------------- glue kernels (device) */
 /* Device counterparts of llmi::kernels (include/llmi/model/kernels.hpp:13-32)
  * and llmi::argmax (transformer.hpp:120), bit-identical to the reference.

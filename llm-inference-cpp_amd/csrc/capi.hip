@@ -91,6 +91,49 @@ struct llmi_hip_group {
   }
 };
 
+struct llmi_hip_gemm_group {
+  void* table = nullptr;  // device copy of the problem table, then the work -> problem map
+  const GemmProblem* probs = nullptr;
+  const std::uint32_t* map = nullptr;
+  std::vector<GemmLaunch> launches;
+  ~llmi_hip_gemm_group() {
+    if (table != nullptr) (void)hipFree(table);
+  }
+};
+
+namespace {
+
+template <typename Plan, typename Group>
+int upload_plan(const Plan& plan, const std::vector<typename decltype(Plan::probs)::value_type>& probs,
+                const std::vector<std::uint32_t>& map, Group* g) {
+  using Prob = typename decltype(Plan::probs)::value_type;
+  const std::size_t pbytes = probs.size() * sizeof(Prob);
+  const std::size_t mbytes = map.size() * sizeof(std::uint32_t);
+  if (pbytes + mbytes == 0) return LLMI_OK;
+  LLMI_TRY_HIP(hipMalloc(&g->table, pbytes + mbytes));
+  auto* base = static_cast<std::uint8_t*>(g->table);
+  LLMI_TRY_HIP(hipMemcpy(base, probs.data(), pbytes, hipMemcpyHostToDevice));
+  if (mbytes > 0) LLMI_TRY_HIP(hipMemcpy(base + pbytes, map.data(), mbytes, hipMemcpyHostToDevice));
+  g->probs = reinterpret_cast<const Prob*>(base);
+  g->map = reinterpret_cast<const std::uint32_t*>(base + pbytes);
+  (void)plan;
+  return LLMI_OK;
+}
+
+int group_entries(const llmi_hip_weight* const* w, const float* const* x, const size_t* rows, const float* const* bias,
+                  float* const* y, size_t count, std::size_t default_rows, std::vector<GroupEntry>* entries) {
+  LLMI_REQUIRE(count == 0 || (w != nullptr && x != nullptr && y != nullptr), "group: null array");
+  entries->resize(count);
+  for (size_t i = 0; i < count; ++i) {
+    LLMI_REQUIRE(w[i] != nullptr, "group: null weight");
+    (*entries)[i] = GroupEntry{&w[i]->m, x[i], bias != nullptr ? bias[i] : nullptr, y[i],
+                               rows != nullptr ? rows[i] : default_rows, false};
+  }
+  return LLMI_OK;
+}
+
+}  // namespace
+
 extern "C" {
 
 const char* llmi_hip_last_error(void) { return t_error.c_str(); }
@@ -419,27 +462,13 @@ int llmi_hip_group_create(const llmi_hip_weight* const* w, const float* const* x
   LLMI_REQUIRE_INIT();
   LLMI_REQUIRE(out != nullptr, "group: null output handle");
   *out = nullptr;
-  LLMI_REQUIRE(count == 0 || (w != nullptr && x != nullptr && y != nullptr), "group: null array");
-  std::vector<GroupEntry> entries(count);
-  for (size_t i = 0; i < count; ++i) {
-    LLMI_REQUIRE(w[i] != nullptr, "group: null weight");
-    entries[i] = GroupEntry{&w[i]->m, x[i], bias != nullptr ? bias[i] : nullptr, y[i], rows != nullptr ? rows[i] : 1,
-                            false};
-  }
+  std::vector<GroupEntry> entries;
+  if (int rc = group_entries(w, x, rows, bias, y, count, 1, &entries)) return rc;
   auto g = std::make_unique<llmi_hip_group>();
   GroupPlan plan;
   if (int rc = plan_group(entries.data(), count, &plan)) return rc;
   g->launches = plan.launches;
-  const std::size_t pbytes = plan.probs.size() * sizeof(GroupProblem);
-  const std::size_t mbytes = plan.wg_prob.size() * sizeof(std::uint32_t);
-  if (pbytes + mbytes > 0) {
-    LLMI_TRY_HIP(hipMalloc(&g->table, pbytes + mbytes));
-    auto* base = static_cast<std::uint8_t*>(g->table);
-    LLMI_TRY_HIP(hipMemcpy(base, plan.probs.data(), pbytes, hipMemcpyHostToDevice));
-    if (mbytes > 0) LLMI_TRY_HIP(hipMemcpy(base + pbytes, plan.wg_prob.data(), mbytes, hipMemcpyHostToDevice));
-    g->probs = reinterpret_cast<const GroupProblem*>(base);
-    g->map = reinterpret_cast<const std::uint32_t*>(base + pbytes);
-  }
+  if (int rc = upload_plan(plan, plan.probs, plan.wg_prob, g.get())) return rc;
   *out = g.release();
   return LLMI_OK;
 }
@@ -453,5 +482,45 @@ int llmi_hip_group_launch(const llmi_hip_group* g, void* stream) {
 }
 
 void llmi_hip_group_free(llmi_hip_group* g) { delete g; }
+
+int llmi_hip_gemm_group_create(const llmi_hip_weight* const* w, const float* const* x, const size_t* rows,
+                               const float* const* bias, float* const* y, size_t count, llmi_hip_gemm_group** out) {
+  LLMI_REQUIRE_INIT();
+  LLMI_REQUIRE(out != nullptr, "gemm: null output handle");
+  LLMI_REQUIRE(rows != nullptr || count == 0, "gemm: null rows");
+  *out = nullptr;
+  std::vector<GroupEntry> entries;
+  if (int rc = group_entries(w, x, rows, bias, y, count, 0, &entries)) return rc;
+  auto g = std::make_unique<llmi_hip_gemm_group>();
+  GemmPlan plan;
+  if (int rc = plan_gemm_group(entries.data(), count, &plan)) return rc;
+  g->launches = plan.launches;
+  if (int rc = upload_plan(plan, plan.probs, plan.work_prob, g.get())) return rc;
+  *out = g.release();
+  return LLMI_OK;
+}
+
+int llmi_hip_gemm_group_launch(const llmi_hip_gemm_group* g, void* stream) {
+  LLMI_REQUIRE_INIT();
+  LLMI_REQUIRE(g != nullptr, "gemm: null group");
+  for (const GemmLaunch& l : g->launches)
+    if (int rc = launch_gemm(g->probs, g->map, l, pick(stream))) return rc;
+  return LLMI_OK;
+}
+
+void llmi_hip_gemm_group_free(llmi_hip_gemm_group* g) { delete g; }
+
+int llmi_hip_matmul_mfma_dev(const llmi_hip_weight* weight, const float* x, size_t rows, const float* bias, float* y,
+                             void* stream) {
+  LLMI_REQUIRE_INIT();
+  LLMI_REQUIRE(weight != nullptr, "gemm: null weight");
+  if (rows == 0 || weight->m.out == 0) return LLMI_OK;
+  const GroupEntry e{&weight->m, x, bias, y, rows, false};
+  GemmPlan plan;
+  if (int rc = plan_gemm_group(&e, 1, &plan)) return rc;
+  for (const GemmLaunch& l : plan.launches)
+    if (int rc = launch_gemm(nullptr, nullptr, l, pick(stream), &plan.probs[l.prob_offset])) return rc;
+  return LLMI_OK;
+}
 
 }  // extern "C"

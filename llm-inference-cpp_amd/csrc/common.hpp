@@ -100,6 +100,30 @@ struct GroupPlan {
 int plan_group(const GroupEntry* entries, std::size_t count, GroupPlan* plan);
 int launch_group(const GroupProblem* probs_dev, const std::uint32_t* map_dev, const GroupLaunch& l, hipStream_t s);
 
+// One product of a grouped bf16-MFMA GEMM launch (qgemm_mfma).
+struct GemmProblem {
+  const std::uint8_t* codes;
+  const float* scales;
+  const float* x;
+  const float* bias;
+  float* y;
+  int rows, in, out, nblk, ntiles, mtiles, first_wg;
+};
+struct GemmLaunch {
+  int type = 0, total_wgs = 0;
+  std::size_t prob_offset = 0, map_offset = 0;
+};
+struct GemmPlan {
+  std::vector<GemmProblem> probs;
+  std::vector<std::uint32_t> work_prob;
+  std::vector<GemmLaunch> launches;
+};
+int plan_gemm_group(const GroupEntry* entries, std::size_t count, GemmPlan* plan);
+// one != nullptr: launch the single product *one (plan of one entry) without
+// a device table.
+int launch_gemm(const GemmProblem* probs_dev, const std::uint32_t* map_dev, const GemmLaunch& l, hipStream_t s,
+                const GemmProblem* one = nullptr);
+
 inline std::size_t block_code_bytes(int type) { return type == LLMI_TYPE_Q4_0 ? 16 : 32; }
 
 // Kernel launchers (implemented next to their kernels).

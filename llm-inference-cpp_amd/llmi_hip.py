@@ -60,6 +60,10 @@ SIGNATURES = {
     "llmi_hip_group_create": (_i, [_vp, _vp, _vp, _vp, _vp, _sz, C.POINTER(_vp)]),
     "llmi_hip_group_launch": (_i, [_vp, _vp]),
     "llmi_hip_group_free": (None, [_vp]),
+    "llmi_hip_matmul_mfma_dev": (_i, [_vp, _vp, _sz, _vp, _vp, _vp]),
+    "llmi_hip_gemm_group_create": (_i, [_vp, _vp, _vp, _vp, _vp, _sz, C.POINTER(_vp)]),
+    "llmi_hip_gemm_group_launch": (_i, [_vp, _vp]),
+    "llmi_hip_gemm_group_free": (None, [_vp]),
     "llmi_hip_dot_dev": (_i, [_vp, _vp, _vp, _sz, _vp, _vp]),
     "llmi_hip_rmsnorm_dev": (_i, [_vp, _vp, _sz, _sz, _f, _vp, _vp]),
     "llmi_hip_softmax_dev": (_i, [_vp, _sz, _sz, _vp]),
@@ -228,6 +232,22 @@ class Weight:
 
     def matmul_dev(self, x_dev: int, rows: int, bias_dev: int | None, y_dev: int, stream=None) -> None:
         check(self.lib.llmi_hip_matmul_dev(self.h, x_dev, rows, bias_dev, y_dev, stream))
+
+    def matmul_mfma_dev(self, x_dev: int, rows: int, bias_dev: int | None, y_dev: int, stream=None) -> None:
+        check(self.lib.llmi_hip_matmul_mfma_dev(self.h, x_dev, rows, bias_dev, y_dev, stream))
+
+    def matmul_mfma(self, x: np.ndarray, rows: int, bias: np.ndarray | None = None) -> np.ndarray:
+        """The bf16-MFMA prefill product on host arrays (tolerance, not exact)."""
+        xd = DeviceBuffer.from_array(np.ascontiguousarray(x, dtype=np.float32))
+        yd = DeviceBuffer(max(1, rows * self.out) * 4)
+        bd = None if bias is None else DeviceBuffer.from_array(np.ascontiguousarray(bias, dtype=np.float32))
+        self.matmul_mfma_dev(xd.ptr, rows, None if bd is None else bd.ptr, yd.ptr)
+        synchronize()
+        y = yd.download(np.float32, rows * self.out)
+        for b in (xd, yd, bd):
+            if b is not None:
+                b.free()
+        return y
 
     def free(self) -> None:
         if self.h:
@@ -429,6 +449,8 @@ class Group:
     """A fixed list of products (Weight, x device pointer, y device pointer,
     rows 1..8, optional bias device pointer) launched as one kernel."""
 
+    _create, _launch, _free = "llmi_hip_group_create", "llmi_hip_group_launch", "llmi_hip_group_free"
+
     def __init__(self, items):
         self.lib = init()
         n = len(items)
@@ -438,15 +460,15 @@ class Group:
         rows = (C.c_size_t * n)(*[it[3] if len(it) > 3 else 1 for it in items])
         bs = (C.c_void_p * n)(*[it[4] if len(it) > 4 else None for it in items])
         h = C.c_void_p()
-        check(self.lib.llmi_hip_group_create(ws, xs, rows, bs, ys, n, C.byref(h)))
+        check(getattr(self.lib, self._create)(ws, xs, rows, bs, ys, n, C.byref(h)))
         self.h = h
 
     def launch(self, stream=None) -> None:
-        check(self.lib.llmi_hip_group_launch(self.h, stream))
+        check(getattr(self.lib, self._launch)(self.h, stream))
 
     def free(self) -> None:
         if self.h:
-            self.lib.llmi_hip_group_free(self.h)
+            getattr(self.lib, self._free)(self.h)
             self.h = None
 
     def __del__(self):
@@ -454,6 +476,13 @@ class Group:
             self.free()
         except Exception:
             pass
+
+
+class GemmGroup(Group):
+    """A list of bf16-MFMA prefill products (Weight, x, y, rows, bias)
+    launched together (llmi_hip_gemm_group_*)."""
+
+    _create, _launch, _free = "llmi_hip_gemm_group_create", "llmi_hip_gemm_group_launch", "llmi_hip_gemm_group_free"
 
 
 class Graph:

@@ -1,0 +1,114 @@
+"""GPU tests of the bf16-MFMA prefill GEMM (llmi_hip_matmul_mfma_dev and the
+grouped launch).  Two checks per case:
+
+* the contract: against the oracle's exact quant::matmul,
+  max|y - y_ref| <= 2e-2 * max|y_ref| (the bound stated for this path);
+* the kernel's arithmetic: against a float64 product of the same operands
+  rounded to bf16 (activations; weights as code * scale in fp32, then bf16)
+  -- the only remaining difference is fp32 accumulation, so the bound is
+  tight (1e-5 of max|y|) and a wrong operand layout, K offset or tail
+  handling fails it.
+"""
+
+import numpy as np
+import pytest
+
+import llmi_hip as H
+import oracle as O
+import synth
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-2
+
+
+def bf16_round(a):
+    """IEEE round-to-nearest-even of fp32 values to bf16 (as fp32)."""
+    u = np.ascontiguousarray(a, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    r = (u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000
+    return r.astype(np.uint32).view(np.float32)
+
+
+def dequantized(data, scales, out, n_in, qt):
+    """code * scale in fp32, [out][n_in] (numpy restatement of the packed
+    formats; checked against oracle.dequantize_row below)."""
+    nb = (n_in + 31) // 32
+    if qt == O.Q8_0:
+        codes = data.view(np.int8).reshape(out, n_in).astype(np.float32)
+    else:
+        b = data.reshape(out, (n_in + 1) // 2)
+        codes = np.empty((out, 2 * b.shape[1]), np.float32)
+        codes[:, 0::2] = (b & 0xF).astype(np.float32) - 8
+        codes[:, 1::2] = (b >> 4).astype(np.float32) - 8
+        codes = codes[:, :n_in]
+    s = np.repeat(scales.reshape(out, nb), 32, axis=1)[:, :n_in]
+    return (codes * s).astype(np.float32)
+
+
+def case(out, n_in, rows, qt, seed, with_bias):
+    orc = O.oracle()
+    w = synth.normal(seed, out * n_in, 0.0, 0.02)
+    data, scales = orc.quantize(w, out, n_in, qt)
+    x = synth.normal(seed + 1, rows * n_in, 0.0, 1.0)
+    bias = synth.normal(seed + 2, out, 0.0, 0.5) if with_bias else None
+    return orc, data, scales, x, bias
+
+
+def check(y, orc, data, scales, x, bias, out, n_in, rows, qt):
+    y = y.reshape(rows, out).astype(np.float64)
+    ref = orc.matmul(x, rows, n_in, data, scales, qt, out, bias).reshape(rows, out).astype(np.float64)
+    scale = max(float(np.max(np.abs(ref))), 1e-30)
+    err = float(np.max(np.abs(y - ref)))
+    assert err <= TOL * scale, (out, n_in, rows, err / scale)
+    wq = dequantized(data, scales, out, n_in, qt)
+    tight = bf16_round(x).reshape(rows, n_in).astype(np.float64) @ bf16_round(wq).astype(np.float64).T
+    if bias is not None:
+        tight = tight + bias.astype(np.float64)
+    err2 = float(np.max(np.abs(y - tight)))
+    assert err2 <= 1e-5 * scale, (out, n_in, rows, err2 / scale)
+    return err / scale
+
+
+def test_dequantized_restatement_matches_oracle():
+    for qt in (O.Q8_0, O.Q4_0):
+        orc, data, scales, _, _ = case(7, 77, 1, qt, 3, False)
+        wq = dequantized(data, scales, 7, 77, qt)
+        for r in range(7):
+            assert np.array_equal(wq[r], orc.dequantize_row(data, scales, 7, 77, qt, r))
+
+
+@pytest.mark.parametrize("qt", [O.Q8_0, O.Q4_0])
+@pytest.mark.parametrize("out,n_in,rows", [(896, 896, 512), (128, 896, 512), (200, 100, 130), (65, 33, 1),
+                                           (300, 99, 77), (1, 64, 129), (257, 4864, 64)])
+def test_mfma_gemm_within_tolerance(qt, out, n_in, rows):
+    orc, data, scales, x, bias = case(out, n_in, rows, qt, out + 3 * n_in + rows, with_bias=(out % 2 == 0))
+    dev = H.Weight.upload(data, scales, out, n_in, qt)
+    y = dev.matmul_mfma(x, rows, bias)
+    rel = check(y, orc, data, scales, x, bias, out, n_in, rows, qt)
+    assert rel < 5e-3  # typical bf16 error is ~1e-3 of max|y|
+    dev.free()
+
+
+def test_gemm_group_matches_single_launches():
+    specs = [(896, 896, 512, O.Q8_0, True), (128, 896, 512, O.Q8_0, True), (4864, 896, 64, O.Q4_0, False),
+             (896, 4864, 64, O.Q8_0, False), (33, 65, 3, O.Q4_0, True)]
+    items, keep, singles = [], [], []
+    for i, (out, n_in, rows, qt, wb) in enumerate(specs):
+        orc, data, scales, x, bias = case(out, n_in, rows, qt, 40 + i, wb)
+        dev = H.Weight.upload(data, scales, out, n_in, qt)
+        xd, yd = H.DeviceBuffer.from_array(x), H.DeviceBuffer(rows * out * 4)
+        bd = H.DeviceBuffer.from_array(bias) if wb else None
+        keep.append((dev, xd, yd, bd, orc, data, scales, x, bias, out, n_in, rows, qt))
+        items.append((dev, xd.ptr, yd.ptr, rows, bd.ptr if bd is not None else None))
+        singles.append(dev.matmul_mfma(x, rows, bias))
+    g = H.GemmGroup(items)
+    for rep in range(2):
+        for k in keep:
+            k[2].upload(np.full(k[2].nbytes // 4, np.nan, np.float32))
+        g.launch()
+        H.synchronize()
+        for i, k in enumerate(keep):
+            got = k[2].download(np.float32)
+            assert np.array_equal(got.view(np.uint32), singles[i].view(np.uint32)), (rep, specs[i])
+    check(keep[0][2].download(np.float32), *keep[0][4:])
+    g.free()
