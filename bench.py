@@ -35,6 +35,10 @@ import synth  # noqa: E402
 
 METRIC = "Q4_0/Q8_0 GEMV achieved HBM GB/s (% of peak); decode tokens/s, 1 GPU"
 HBM_PEAK_GBS = 8000.0
+# HBM bytes per qgemv_group launch of the batch-1 step, from the two
+# rocprofv3 --pmc passes (FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0, the factors a
+# 256 MiB copy kernel reads) recorded in profiles/qgemv_group_smollm2_q4_b1.md.
+GROUP_B1_HBM_BYTES = 85_127_580
 ROTATE_BYTES = 1 << 30
 
 SMOL_LAYER = [("q_proj", 576, 576), ("k_proj", 192, 576), ("v_proj", 192, 576), ("o_proj", 576, 576),
@@ -324,6 +328,9 @@ def main():
     ap.add_argument("--no-targets", action="store_true", help="skip the Qwen2.5 shape table")
     ap.add_argument("--no-decode", action="store_true", help="skip the full-model decode runs")
     ap.add_argument("--no-gemm", action="store_true", help="skip the prefill GEMM (configs[4])")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="also run one plain 256 MiB device-to-device copy, the reference kernel for scaling "
+                         "rocprofv3 FETCH_SIZE / WRITE_SIZE readings")
     ap.add_argument("--no-graphs", action="store_true",
                     help="time the linear pass with plain launches only (for profilers that do not follow graphs)")
     args = ap.parse_args()
@@ -357,6 +364,17 @@ def main():
     head_ms = time_launches(heads, 1, 2 * len(heads) * 4)
     head_bytes = algo_bytes(SMOL_HEAD[1], SMOL_HEAD[2], H.Q4_0, 1)
     wset.free()
+
+    if args.calibrate_copy:
+        nbytes = 256 << 20
+        src, dst = H.DeviceBuffer(nbytes), H.DeviceBuffer(nbytes)
+        H.synth_normal_dev(src, nbytes // 4, 1, 0.0, 1.0)
+        H.synchronize()
+        H.check(H.init().llmi_hip_memcpy_d2d(dst.ptr, src.ptr, nbytes, None))
+        H.synchronize()
+        print(f"[bench] calibration copy: {nbytes} bytes read and written", file=sys.stderr, flush=True)
+        src.free()
+        dst.free()
 
     targets = {} if args.no_targets else target_shapes()
     decode = {} if args.no_decode else decode_runs()
@@ -401,7 +419,8 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(value / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": GROUP_B1_HBM_BYTES,
+            "traffic_source": "rocprofv3 --pmc FETCH_SIZE/WRITE_SIZE, profiles/qgemv_group_smollm2_q4_b1.md",
             "algorithmic_bytes_per_launch": bytes_b1,
             "mean_launch_us": round(step_ms * 1e3, 3),
         },

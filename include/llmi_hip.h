@@ -81,6 +81,8 @@ int llmi_hip_malloc(void** ptr, size_t bytes);
 int llmi_hip_free(void* ptr);
 int llmi_hip_memcpy_h2d(void* dst_dev, const void* src, size_t bytes);
 int llmi_hip_memcpy_d2h(void* dst, const void* src_dev, size_t bytes);
+/* Device-to-device copy queued on `stream` (a plain copy kernel). */
+int llmi_hip_memcpy_d2d(void* dst_dev, const void* src_dev, size_t bytes, void* stream);
 int llmi_hip_memset_dev(void* dst_dev, int value, size_t bytes);
 
 /* HIP events on `stream` (NULL = library stream), for kernel timing. */

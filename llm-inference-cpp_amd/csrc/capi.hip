@@ -205,6 +205,13 @@ int llmi_hip_memcpy_d2h(void* dst, const void* src, size_t bytes) {
   return LLMI_OK;
 }
 
+int llmi_hip_memcpy_d2d(void* dst, const void* src, size_t bytes, void* stream) {
+  LLMI_REQUIRE_INIT();
+  if (bytes == 0) return LLMI_OK;
+  LLMI_TRY_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, pick(stream)));
+  return LLMI_OK;
+}
+
 int llmi_hip_memset_dev(void* dst, int value, size_t bytes) {
   LLMI_REQUIRE_INIT();
   if (bytes == 0) return LLMI_OK;

@@ -33,6 +33,7 @@ SIGNATURES = {
     "llmi_hip_free": (_i, [_vp]),
     "llmi_hip_memcpy_h2d": (_i, [_vp, _vp, _sz]),
     "llmi_hip_memcpy_d2h": (_i, [_vp, _vp, _sz]),
+    "llmi_hip_memcpy_d2d": (_i, [_vp, _vp, _sz, _vp]),
     "llmi_hip_memset_dev": (_i, [_vp, _i, _sz]),
     "llmi_hip_event_create": (_i, [C.POINTER(_vp)]),
     "llmi_hip_event_destroy": (_i, [_vp]),
