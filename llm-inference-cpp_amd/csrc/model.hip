@@ -339,6 +339,144 @@ __global__ void __launch_bounds__(kThreads) attention_hd16(const float* __restri
   }
 }
 
+// ------------------------------------------------- decode attention (T = 1)
+// The same arithmetic as attention_hd16 for one new token, restructured for
+// latency: the one-workgroup-per-head kernel spends ~140 ns per cached
+// position waiting on K and V loads, because each output element is one
+// sequential chain over the positions.  Here
+//  1. attn_scores_1: grid (position tiles of 64, KV heads) computes every
+//     score of the GQA group with all K loads of a thread issued at once, and
+//     writes them to the cache's score buffer [head][cap];
+//  2. attn_pv_1: grid (KV heads, head_dim / 16) -- each workgroup runs the
+//     softmax of the group's heads (softmax_lds, as before) and the P.V chains
+//     of 16 output columns of every head of the group, with the whole V slice
+//     (positions x 16 columns) staged transposed in LDS first, so the chains
+//     read 4 positions per 16-byte LDS load and never wait on HBM.
+// Positions are padded to a multiple of 4 with p = 0 and v = 0: the chains
+// never hold -0.0 (they start at +0.0 and p >= 0), so fma(0, 0, acc) == acc.
+constexpr int kScoreTile = 64;  // positions per attn_scores_1 workgroup
+
+template <int NCH>  // head_dim / 16
+__global__ void __launch_bounds__(kThreads) attn_scores_1(const float* __restrict__ q, const float* __restrict__ kc,
+                                                          float* __restrict__ scores, int nh, int nkv, int cap,
+                                                          int npos, float scale) {
+  constexpr int hd = 16 * NCH;
+  const int kvh = blockIdx.y;
+  const int G = nh / nkv;
+  const int j = threadIdx.x & 15, grp = threadIdx.x >> 4;
+  const int s0 = blockIdx.x * kScoreTile;
+  const float* kh = kc + static_cast<std::size_t>(kvh) * cap * hd;
+  float kv[kScoreTile / 16][NCH];
+#pragma unroll
+  for (int p = 0; p < kScoreTile / 16; ++p) {
+    const int s = s0 + 16 * p + grp;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) kv[p][c] = s < npos ? kh[static_cast<std::size_t>(s) * hd + 16 * c + j] : 0.0f;
+  }
+  for (int g = 0; g < G; ++g) {
+    const int h = kvh * G + g;
+    float qv[NCH];
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) qv[c] = q[static_cast<std::size_t>(h) * hd + 16 * c + j];
+#pragma unroll
+    for (int p = 0; p < kScoreTile / 16; ++p) {
+      float lane = 0.0f;
+#pragma unroll
+      for (int c = 0; c < NCH; ++c) lane = __builtin_fmaf(qv[c], kv[p][c], lane);
+      lane = lane + __shfl_xor(lane, 8, 16);
+      lane = lane + __shfl_xor(lane, 4, 16);
+      lane = lane + __shfl_xor(lane, 2, 16);
+      lane = lane + __shfl_xor(lane, 1, 16);
+      const int s = s0 + 16 * p + grp;
+      if (j == 0 && s < npos) scores[static_cast<std::size_t>(h) * cap + s] = (lane + 0.0f) * scale;
+    }
+  }
+}
+
+// Dynamic LDS: p[G][npad], vt[16][npad].  Threads g*16 + i run the chains.
+template <int NCH>
+__global__ void __launch_bounds__(kThreads) attn_pv_1(const float* __restrict__ scores, const float* __restrict__ vc,
+                                                      float* __restrict__ out, int nh, int nkv, int cap, int npos) {
+  constexpr int hd = 16 * NCH;
+  extern __shared__ float4 pv_lds[];  // 16-byte aligned: the chains read float4
+  float* lds_dyn = reinterpret_cast<float*>(pv_lds);
+  __shared__ double red_d[kThreads];
+  __shared__ float red_f[kThreads];
+  __shared__ float inv_s;
+  const int kvh = blockIdx.x;
+  const int i0 = blockIdx.y * 16;
+  const int G = nh / nkv;
+  const int npad = (npos + 3) & ~3;
+  float* p = lds_dyn;
+  float* vt = lds_dyn + static_cast<std::size_t>(G) * npad;
+  const int tid = threadIdx.x;
+
+  // V slice, transposed: vt[i][s] = V[kvh][s][i0 + i]; issued first so the
+  // loads overlap the softmax.
+  const float* vh = vc + static_cast<std::size_t>(kvh) * cap * hd + i0;
+  for (int e = tid; e < npad * 4; e += kThreads) {
+    const int s = e >> 2, qd = e & 3;
+    float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (s < npos) v = *reinterpret_cast<const float4*>(vh + static_cast<std::size_t>(s) * hd + 4 * qd);
+    vt[(4 * qd + 0) * npad + s] = v.x;
+    vt[(4 * qd + 1) * npad + s] = v.y;
+    vt[(4 * qd + 2) * npad + s] = v.z;
+    vt[(4 * qd + 3) * npad + s] = v.w;
+  }
+  for (int g = 0; g < G; ++g) {
+    float* sc = p + static_cast<std::size_t>(g) * npad;
+    const float* src = scores + static_cast<std::size_t>(kvh * G + g) * cap;
+    float mx_local = -__builtin_inff();
+    for (int s = tid; s < npad; s += kThreads) {
+      const float v = s < npos ? src[s] : 0.0f;
+      sc[s] = v;
+      if (s < npos) mx_local = fmaxf(mx_local, v);
+    }
+    __syncthreads();
+    softmax_lds(sc, npos, mx_local, red_d, red_f, &inv_s);
+    for (int s = npos + tid; s < npad; s += kThreads) sc[s] = 0.0f;
+  }
+  __syncthreads();
+  if (tid < G * 16) {
+    const int g = tid >> 4, i = tid & 15;
+    const float4* pr = reinterpret_cast<const float4*>(p + static_cast<std::size_t>(g) * npad);
+    const float4* vr = reinterpret_cast<const float4*>(vt + static_cast<std::size_t>(i) * npad);
+    float acc = 0.0f;
+    for (int s4 = 0; s4 < npad / 4; ++s4) {
+      const float4 pp = pr[s4], vv = vr[s4];
+      acc = __builtin_fmaf(pp.x, vv.x, acc);
+      acc = __builtin_fmaf(pp.y, vv.y, acc);
+      acc = __builtin_fmaf(pp.z, vv.z, acc);
+      acc = __builtin_fmaf(pp.w, vv.w, acc);
+    }
+    out[static_cast<std::size_t>(kvh * G + g) * hd + i0 + i] = acc;
+  }
+}
+
+std::size_t attn_pv_lds(std::size_t npos, std::size_t group) { return (group + 16) * ((npos + 3) & ~std::size_t{3}) * sizeof(float); }
+
+// The two-kernel decode path applies to one token with head_dim 64 or 128,
+// at most 16 query heads per KV head and a V slice that fits in LDS.
+bool decode_attention_fits(int nh, int nkv, int hd, std::size_t npos) {
+  const int G = nh / nkv;
+  return (hd == 64 || hd == 128) && G >= 1 && G <= 16 && nh % nkv == 0 &&
+         attn_pv_lds(npos, G) + kThreads * (sizeof(double) + sizeof(float)) + 16 <= max_lds_per_block();
+}
+
+void launch_decode_attention(const float* q, const float* kc, const float* vc, float* scores, float* out, int nh,
+                             int nkv, int hd, int cap, int npos, float scale, hipStream_t s) {
+  const dim3 sgrid(static_cast<unsigned>((npos + kScoreTile - 1) / kScoreTile), static_cast<unsigned>(nkv));
+  const dim3 pgrid(static_cast<unsigned>(nkv), static_cast<unsigned>(hd / 16));
+  const std::size_t lds = attn_pv_lds(npos, nh / nkv);
+  if (hd == 64) {
+    attn_scores_1<4><<<sgrid, kThreads, 0, s>>>(q, kc, scores, nh, nkv, cap, npos, scale);
+    attn_pv_1<4><<<pgrid, kThreads, lds, s>>>(scores, vc, out, nh, nkv, cap, npos);
+  } else {
+    attn_scores_1<8><<<sgrid, kThreads, 0, s>>>(q, kc, scores, nh, nkv, cap, npos, scale);
+    attn_pv_1<8><<<pgrid, kThreads, lds, s>>>(scores, vc, out, nh, nkv, cap, npos);
+  }
+}
+
 std::size_t attention_static_lds() { return kThreads * (sizeof(double) + sizeof(float)) + 16; }
 
 // Dynamic LDS of the attention launch for npos positions.
@@ -533,6 +671,7 @@ struct llmi_hip_cache {
   std::size_t cap = 0, len = 0;
   float* k = nullptr;  // [layer][kv_head][cap][hd]
   float* v = nullptr;
+  float* scores = nullptr;  // [head][cap], decode attention scratch
 };
 
 namespace llmi_hip {
@@ -760,8 +899,12 @@ int forward_device(llmi_hip_model* m, llmi_hip_cache* cache, std::size_t T, bool
     if (int rc = launch_matmul(l.wv, w.h, T, l.bv, w.v, s)) return rc;
     rope_and_cache<<<tt, kThreads, 0, s>>>(w.q, w.k, w.v, kc, vc, m->cos_t, m->sin_t, nh, nkv, hd,
                                            static_cast<int>(cache->cap), static_cast<int>(base));
-    launch_attention(w.q, kc, vc, w.att, nh, nkv, hd, static_cast<int>(cache->cap), static_cast<int>(base),
-                     static_cast<int>(T), scale, s);
+    if (T == 1 && decode_attention_fits(nh, nkv, hd, base + 1))
+      launch_decode_attention(w.q, kc, vc, cache->scores, w.att, nh, nkv, hd, static_cast<int>(cache->cap),
+                              static_cast<int>(base + 1), scale, s);
+    else
+      launch_attention(w.q, kc, vc, w.att, nh, nkv, hd, static_cast<int>(cache->cap), static_cast<int>(base),
+                       static_cast<int>(T), scale, s);
     if (int rc = launch_matmul(l.wo, w.att, T, nullptr, w.x, s, true)) return rc;
     rmsnorm_rows<<<tt, kThreads, 0, s>>>(w.x, l.mlp_norm, w.h, static_cast<int>(m->H), eps);
     if (int rc = launch_matmul(l.gate, w.h, T, nullptr, w.g, s)) return rc;
@@ -899,6 +1042,11 @@ int llmi_hip_model_new_cache(llmi_hip_model* m, size_t max_len, llmi_hip_cache**
     (void)hipFree(c->k);
     return fail(LLMI_ERR_HIP, "new_cache: hipMalloc");
   }
+  if (hipMalloc(&c->scores, m->c.num_heads * cap * sizeof(float)) != hipSuccess) {
+    (void)hipFree(c->k);
+    (void)hipFree(c->v);
+    return fail(LLMI_ERR_HIP, "new_cache: hipMalloc");
+  }
   *cache = c.release();
   return LLMI_OK;
 }
@@ -908,6 +1056,7 @@ int llmi_hip_cache_free(llmi_hip_cache* c) {
   if (library_stream() != nullptr) (void)hipStreamSynchronize(library_stream());
   (void)hipFree(c->k);
   (void)hipFree(c->v);
+  (void)hipFree(c->scores);
   delete c;
   return LLMI_OK;
 }

@@ -216,3 +216,30 @@ def test_forward_trace_states():
     assert np.array_equal(bits(head), bits(logits))
     c2 = m.new_cache(4)
     assert np.array_equal(bits(m.forward_cached(c2, ids)), bits(logits))
+
+
+# ------------------------------------------------ decode attention shapes
+@pytest.mark.parametrize("hidden,heads,kv", [(256, 4, 2), (256, 2, 1), (448, 7, 1), (192, 3, 1)])
+def test_decode_attention_matches_reference(hidden, heads, kv):
+    """Head sizes 64 and 128 with GQA groups of 2, 3 and 7 take the two-kernel
+    decode attention (scores over position tiles, then softmax + P.V per
+    16-column slice); logits of every decode step up to 75 positions (all
+    residues of the position padding) equal the reference's bit for bit."""
+    cpu = O.reference() or O.oracle()
+    cfg = dict(arch=1, vocab_size=64, hidden_size=hidden, intermediate_size=2 * hidden, num_layers=2,
+               num_heads=heads, num_kv_heads=kv, max_position_embeddings=128, rms_norm_eps=1e-6,
+               rope_theta=10000.0, tie_word_embeddings=1, qkv_bias=1)
+    tensors = synth.make_tensors(cfg, hidden + heads, "bench")
+    gm = H.Model(cfg, tensors, H.Q8_0)
+    cm = O.CpuModel(cpu, cfg, tensors, O.Q8_0)
+    ids = synth.uniform_ids(hidden, 75, cfg["vocab_size"])
+    cache = gm.new_cache(80)
+    assert cm.new_cache(80)
+    assert np.array_equal(bits(gm.forward_cached(cache, ids[:5])), bits(cm.forward_cached(ids[:5])))
+    for t in range(5, 75):
+        got = gm.forward_cached(cache, ids[t:t + 1])
+        want = cm.forward_cached(ids[t:t + 1])
+        assert np.array_equal(bits(got), bits(want)), (hidden, heads, kv, t)
+    cache.free()
+    gm.free()
+    cm.close()
