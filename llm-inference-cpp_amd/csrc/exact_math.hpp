@@ -46,7 +46,10 @@ LLMI_EXPF_TABLE_SPACE static const std::uint64_t kExp2Tab[32] = {
     0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull,
 };
 
-LLMI_HD float expf(float x) {
+// tab: the 32-entry table above, or a copy of it (e.g. in LDS, where a
+// kernel calls expf many times per thread: a table index differs per lane, so
+// every lookup is a memory load).
+LLMI_HD float expf_with(float x, const std::uint64_t* tab) {
   constexpr double kN = 32.0;
   constexpr double kInvLn2N = 0x1.71547652b82fep+0 * kN;
   constexpr double kShift = 0x1.8p+52;
@@ -66,7 +69,7 @@ LLMI_HD float expf(float x) {
   const std::uint64_t ki = d2u(kd);
   kd -= kShift;
   const double r = __builtin_fma(kInvLn2N, xd, -kd);
-  std::uint64_t t = kExp2Tab[ki % 32];
+  std::uint64_t t = tab[ki % 32];
   t += ki << 47;
   const double s = u2d(t);
   const double zp = __builtin_fma(kC0, r, kC1);
@@ -76,6 +79,8 @@ LLMI_HD float expf(float x) {
   y = y * s;
   return static_cast<float>(y);
 }
+
+LLMI_HD float expf(float x) { return expf_with(x, kExp2Tab); }
 
 }  // namespace exact
 }  // namespace llmi_hip

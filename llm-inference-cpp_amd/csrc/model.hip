@@ -347,20 +347,28 @@ __global__ void __launch_bounds__(kThreads) attention_hd16(const float* __restri
 //  1. attn_scores_1: grid (position tiles of 64, KV heads) computes every
 //     score of the GQA group with all K loads of a thread issued at once, and
 //     writes them to the cache's score buffer [head][cap];
-//  2. attn_pv_1: grid (KV heads, head_dim / 16) -- each workgroup runs the
-//     softmax of the group's heads (softmax_lds, as before) and the P.V chains
-//     of 16 output columns of every head of the group, with the whole V slice
-//     (positions x 16 columns) staged transposed in LDS first, so the chains
-//     read 4 positions per 16-byte LDS load and never wait on HBM.
+//  2. attn_pv_1: grid (query heads, head_dim / 16) -- each workgroup runs
+//     the softmax of its head and the P.V chains of 16 output columns, with
+//     the V slice (positions x 16 columns) staged transposed in LDS first,
+//     so the chains read 4 positions per 16-byte LDS load and never wait on
+//     HBM.
 // Positions are padded to a multiple of 4 with p = 0 and v = 0: the chains
 // never hold -0.0 (they start at +0.0 and p >= 0), so fma(0, 0, acc) == acc.
 constexpr int kScoreTile = 64;  // positions per attn_scores_1 workgroup
+
+// v + (v of the lane n above, within each row of 16 lanes): one DPP add.
+template <int N>
+__device__ __forceinline__ float add_row_shl(float v) {
+  const int src = __builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x100 + N, 0xF, 0xF, true);
+  return v + __int_as_float(src);
+}
 
 template <int NCH>  // head_dim / 16
 __global__ void __launch_bounds__(kThreads) attn_scores_1(const float* __restrict__ q, const float* __restrict__ kc,
                                                           float* __restrict__ scores, int nh, int nkv, int cap,
                                                           int npos, float scale) {
   constexpr int hd = 16 * NCH;
+  __shared__ float qs[16 * hd];  // the group's query heads (G <= 16)
   const int kvh = blockIdx.y;
   const int G = nh / nkv;
   const int j = threadIdx.x & 15, grp = threadIdx.x >> 4;
@@ -373,75 +381,140 @@ __global__ void __launch_bounds__(kThreads) attn_scores_1(const float* __restric
 #pragma unroll
     for (int c = 0; c < NCH; ++c) kv[p][c] = s < npos ? kh[static_cast<std::size_t>(s) * hd + 16 * c + j] : 0.0f;
   }
+  for (int e = threadIdx.x; e < G * hd; e += kThreads) qs[e] = q[static_cast<std::size_t>(kvh) * G * hd + e];
+  __syncthreads();
   for (int g = 0; g < G; ++g) {
     const int h = kvh * G + g;
     float qv[NCH];
 #pragma unroll
-    for (int c = 0; c < NCH; ++c) qv[c] = q[static_cast<std::size_t>(h) * hd + 16 * c + j];
+    for (int c = 0; c < NCH; ++c) qv[c] = qs[g * hd + 16 * c + j];
 #pragma unroll
     for (int p = 0; p < kScoreTile / 16; ++p) {
       float lane = 0.0f;
 #pragma unroll
       for (int c = 0; c < NCH; ++c) lane = __builtin_fmaf(qv[c], kv[p][c], lane);
-      lane = lane + __shfl_xor(lane, 8, 16);
-      lane = lane + __shfl_xor(lane, 4, 16);
-      lane = lane + __shfl_xor(lane, 2, 16);
-      lane = lane + __shfl_xor(lane, 1, 16);
+      // Lane 0 of each row of 16 ends with ((l0+l8)+(l4+l12)) + ... -- the
+      // j+8, +4, +2, +1 tree of the 16 accumulators.
+      lane = add_row_shl<8>(lane);
+      lane = add_row_shl<4>(lane);
+      lane = add_row_shl<2>(lane);
+      lane = add_row_shl<1>(lane);
       const int s = s0 + 16 * p + grp;
       if (j == 0 && s < npos) scores[static_cast<std::size_t>(h) * cap + s] = (lane + 0.0f) * scale;
     }
   }
 }
 
-// Dynamic LDS: p[G][npad], vt[16][npad].  Threads g*16 + i run the chains.
+// Dynamic LDS: p[npad] then vt[16][stride] (stride = npad rounded up to 32,
+// plus 4: consecutive rows start 4 banks apart).  grid (query heads,
+// head_dim / 16): each workgroup runs the softmax of its head (softmax_lds's
+// arithmetic: float max, exact expf with an LDS copy of its table, double sum
+// taken when the error bound proves it rounds like the sequential sum, else
+// summed sequentially) and the P.V chains of 16 output columns.  All of its
+// global loads (the V slice, one float4 per position and quarter, and the
+// head's scores) are issued before any is used.
+constexpr int kPvCols = 16;
+constexpr int kPvBatch = 8;  // V loads per thread per round
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+__device__ __forceinline__ double wave_sum(double v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = v + __shfl_xor(v, o, 64);
+  return v;
+}
+
+__device__ __forceinline__ int pv_stride(int npad) { return ((npad + 31) & ~31) + 4; }
+
 template <int NCH>
 __global__ void __launch_bounds__(kThreads) attn_pv_1(const float* __restrict__ scores, const float* __restrict__ vc,
                                                       float* __restrict__ out, int nh, int nkv, int cap, int npos) {
   constexpr int hd = 16 * NCH;
+  constexpr int kWaves = kThreads / 64;
   extern __shared__ float4 pv_lds[];  // 16-byte aligned: the chains read float4
-  float* lds_dyn = reinterpret_cast<float*>(pv_lds);
-  __shared__ double red_d[kThreads];
-  __shared__ float red_f[kThreads];
-  __shared__ float inv_s;
-  const int kvh = blockIdx.x;
-  const int i0 = blockIdx.y * 16;
-  const int G = nh / nkv;
+  __shared__ std::uint64_t exp_tab[32];
+  __shared__ float red_f[kWaves];
+  __shared__ double red_d[kWaves];
+  float* lds = reinterpret_cast<float*>(pv_lds);
+  const int h = blockIdx.x;
+  const int kvh = h / (nh / nkv);
+  const int i0 = blockIdx.y * kPvCols;
   const int npad = (npos + 3) & ~3;
-  float* p = lds_dyn;
-  float* vt = lds_dyn + static_cast<std::size_t>(G) * npad;
-  const int tid = threadIdx.x;
+  const int stride = pv_stride(npad);
+  float* p = lds;
+  float* vt = lds + npad;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  if (tid < 32) exp_tab[tid] = exact::kExp2Tab[tid];
 
-  // V slice, transposed: vt[i][s] = V[kvh][s][i0 + i]; issued first so the
-  // loads overlap the softmax.
   const float* vh = vc + static_cast<std::size_t>(kvh) * cap * hd + i0;
-  for (int e = tid; e < npad * 4; e += kThreads) {
-    const int s = e >> 2, qd = e & 3;
-    float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    if (s < npos) v = *reinterpret_cast<const float4*>(vh + static_cast<std::size_t>(s) * hd + 4 * qd);
-    vt[(4 * qd + 0) * npad + s] = v.x;
-    vt[(4 * qd + 1) * npad + s] = v.y;
-    vt[(4 * qd + 2) * npad + s] = v.z;
-    vt[(4 * qd + 3) * npad + s] = v.w;
-  }
-  for (int g = 0; g < G; ++g) {
-    float* sc = p + static_cast<std::size_t>(g) * npad;
-    const float* src = scores + static_cast<std::size_t>(kvh * G + g) * cap;
-    float mx_local = -__builtin_inff();
-    for (int s = tid; s < npad; s += kThreads) {
-      const float v = s < npos ? src[s] : 0.0f;
-      sc[s] = v;
-      if (s < npos) mx_local = fmaxf(mx_local, v);
+  const float* src = scores + static_cast<std::size_t>(h) * cap;
+  const int n4 = npad * 4;
+  for (int e0 = 0; e0 < max(n4, npad); e0 += kThreads * kPvBatch) {
+    float4 v[kPvBatch];
+    float sv[kPvBatch];
+#pragma unroll
+    for (int u = 0; u < kPvBatch; ++u) {
+      const int e = e0 + u * kThreads + tid;
+      const int sp = e >> 2;
+      v[u] = sp < npos ? *reinterpret_cast<const float4*>(vh + static_cast<std::size_t>(sp) * hd + 4 * (e & 3))
+                       : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      sv[u] = e < npos ? src[e] : 0.0f;
     }
-    __syncthreads();
-    softmax_lds(sc, npos, mx_local, red_d, red_f, &inv_s);
-    for (int s = npos + tid; s < npad; s += kThreads) sc[s] = 0.0f;
+#pragma unroll
+    for (int u = 0; u < kPvBatch; ++u) {
+      const int e = e0 + u * kThreads + tid;
+      if (e < n4) {
+        const int sp = e >> 2, qd = e & 3;
+        vt[(4 * qd + 0) * stride + sp] = v[u].x;
+        vt[(4 * qd + 1) * stride + sp] = v[u].y;
+        vt[(4 * qd + 2) * stride + sp] = v[u].z;
+        vt[(4 * qd + 3) * stride + sp] = v[u].w;
+      }
+      if (e < npad) p[e] = sv[u];
+    }
   }
   __syncthreads();
-  if (tid < G * 16) {
-    const int g = tid >> 4, i = tid & 15;
-    const float4* pr = reinterpret_cast<const float4*>(p + static_cast<std::size_t>(g) * npad);
-    const float4* vr = reinterpret_cast<const float4*>(vt + static_cast<std::size_t>(i) * npad);
+
+  // Softmax of p[0..npos): each thread owns positions tid, tid + 256, ...
+  float mx = -__builtin_inff();
+  for (int sp = tid; sp < npos; sp += kThreads) mx = fmaxf(mx, p[sp]);
+  mx = wave_max(mx);
+  if (lane == 0) red_f[wave] = mx;
+  __syncthreads();
+  mx = red_f[0];
+#pragma unroll
+  for (int w = 1; w < kWaves; ++w) mx = fmaxf(mx, red_f[w]);
+  double part = 0.0;
+  for (int sp = tid; sp < npos; sp += kThreads) {
+    const float e = exact::expf_with(p[sp] - mx, exp_tab);
+    p[sp] = e;
+    part += static_cast<double>(e);
+  }
+  part = wave_sum(part);
+  if (lane == 0) red_d[wave] = part;
+  __syncthreads();
+  double sum = red_d[0];
+#pragma unroll
+  for (int w = 1; w < kWaves; ++w) sum = sum + red_d[w];
+  const double slack = sum_slack(npos) * sum;
+  float inv = recip_float(sum);
+  if (recip_float(sum - slack) != recip_float(sum + slack)) {
+    double seq = 0.0;  // every e is in LDS (the barrier above)
+    for (int sp = 0; sp < npos; ++sp) seq += static_cast<double>(p[sp]);
+    inv = recip_float(seq);
+  }
+  __syncthreads();  // the sequential sum has read p before it is scaled
+  for (int sp = tid; sp < npos; sp += kThreads) p[sp] = p[sp] * inv;
+  __syncthreads();
+
+  if (tid < kPvCols) {
+    const float4* pr = reinterpret_cast<const float4*>(p);
+    const float4* vr = reinterpret_cast<const float4*>(vt + static_cast<std::size_t>(tid) * stride);
     float acc = 0.0f;
+#pragma unroll 8
     for (int s4 = 0; s4 < npad / 4; ++s4) {
       const float4 pp = pr[s4], vv = vr[s4];
       acc = __builtin_fmaf(pp.x, vv.x, acc);
@@ -449,25 +522,28 @@ __global__ void __launch_bounds__(kThreads) attn_pv_1(const float* __restrict__ 
       acc = __builtin_fmaf(pp.z, vv.z, acc);
       acc = __builtin_fmaf(pp.w, vv.w, acc);
     }
-    out[static_cast<std::size_t>(kvh * G + g) * hd + i0 + i] = acc;
+    out[static_cast<std::size_t>(h) * hd + i0 + tid] = acc;
   }
 }
 
-std::size_t attn_pv_lds(std::size_t npos, std::size_t group) { return (group + 16) * ((npos + 3) & ~std::size_t{3}) * sizeof(float); }
+std::size_t attn_pv_lds(std::size_t npos) {
+  const std::size_t npad = (npos + 3) & ~std::size_t{3};
+  return (npad + kPvCols * (((npad + 31) & ~std::size_t{31}) + 4)) * sizeof(float);
+}
 
 // The two-kernel decode path applies to one token with head_dim 64 or 128,
 // at most 16 query heads per KV head and a V slice that fits in LDS.
 bool decode_attention_fits(int nh, int nkv, int hd, std::size_t npos) {
   const int G = nh / nkv;
   return (hd == 64 || hd == 128) && G >= 1 && G <= 16 && nh % nkv == 0 &&
-         attn_pv_lds(npos, G) + kThreads * (sizeof(double) + sizeof(float)) + 16 <= max_lds_per_block();
+         attn_pv_lds(npos) <= max_lds_per_block();
 }
 
 void launch_decode_attention(const float* q, const float* kc, const float* vc, float* scores, float* out, int nh,
                              int nkv, int hd, int cap, int npos, float scale, hipStream_t s) {
   const dim3 sgrid(static_cast<unsigned>((npos + kScoreTile - 1) / kScoreTile), static_cast<unsigned>(nkv));
-  const dim3 pgrid(static_cast<unsigned>(nkv), static_cast<unsigned>(hd / 16));
-  const std::size_t lds = attn_pv_lds(npos, nh / nkv);
+  const dim3 pgrid(static_cast<unsigned>(nh), static_cast<unsigned>(hd / kPvCols));
+  const std::size_t lds = attn_pv_lds(npos);
   if (hd == 64) {
     attn_scores_1<4><<<sgrid, kThreads, 0, s>>>(q, kc, scores, nh, nkv, cap, npos, scale);
     attn_pv_1<4><<<pgrid, kThreads, lds, s>>>(scores, vc, out, nh, nkv, cap, npos);
