@@ -82,13 +82,8 @@ std::size_t max_lds_per_block() { return g_max_lds; }
 using namespace llmi_hip;
 
 struct llmi_hip_group {
-  void* table = nullptr;  // device copy of the problem table, then the workgroup -> problem map
-  const GroupProblem* probs = nullptr;
-  const std::uint32_t* map = nullptr;
-  std::vector<GroupLaunch> launches;
-  ~llmi_hip_group() {
-    if (table != nullptr) (void)hipFree(table);
-  }
+  DeviceGroup g;
+  ~llmi_hip_group() { g.release(); }
 };
 
 struct llmi_hip_gemm_group {
@@ -472,10 +467,7 @@ int llmi_hip_group_create(const llmi_hip_weight* const* w, const float* const* x
   std::vector<GroupEntry> entries;
   if (int rc = group_entries(w, x, rows, bias, y, count, 1, &entries)) return rc;
   auto g = std::make_unique<llmi_hip_group>();
-  GroupPlan plan;
-  if (int rc = plan_group(entries.data(), count, &plan)) return rc;
-  g->launches = plan.launches;
-  if (int rc = upload_plan(plan, plan.probs, plan.wg_prob, g.get())) return rc;
+  if (int rc = g->g.build(entries.data(), count)) return rc;
   *out = g.release();
   return LLMI_OK;
 }
@@ -483,9 +475,7 @@ int llmi_hip_group_create(const llmi_hip_weight* const* w, const float* const* x
 int llmi_hip_group_launch(const llmi_hip_group* g, void* stream) {
   LLMI_REQUIRE_INIT();
   LLMI_REQUIRE(g != nullptr, "group: null group");
-  for (const GroupLaunch& l : g->launches)
-    if (int rc = launch_group(g->probs, g->map, l, pick(stream))) return rc;
-  return LLMI_OK;
+  return g->g.launch(pick(stream));
 }
 
 void llmi_hip_group_free(llmi_hip_group* g) { delete g; }

@@ -65,6 +65,13 @@ struct DeviceMatrix {
   std::size_t code_bytes = 0, scale_bytes = 0;
 };
 
+// How a 16-row tile stages its activations in LDS (GroupProblem::prologue):
+// kPlain x; kRmsNorm w * (x * scale), the reference's RMSNorm of x
+// (kernels.cpp:115-120) with pw = w; kSiluUp silu(x) * pw, the reference's
+// SiLU times up (transformer.cpp:290, kernels.cpp:148).  Either one is the
+// same arithmetic as the separate glue kernel it replaces.
+enum { kPlain = 0, kRmsNorm = 1, kSiluUp = 2 };
+
 // One product of a grouped launch (qgemv_group), as the kernel reads it.
 struct GroupProblem {
   static constexpr int kNarrow = 16;  // kind: 16-row tiles, batch 1; else the row chunk R (1, 2, 4, 8)
@@ -73,10 +80,13 @@ struct GroupProblem {
   const float* x;
   const float* bias;
   float* y;
-  int type, kind, in, nblk, out, rows, ntiles, bpw, accumulate, first_wg;
+  const float* pw;  // prologue operand (RMSNorm weight or the up vector)
+  float eps;        // RMSNorm epsilon
+  int type, kind, in, nblk, out, rows, ntiles, bpw, accumulate, first_wg, prologue;
 };
 
-// One product y = W x (+ bias), rows 1..8, as the caller describes it.
+// One product y = W x (+ bias) (y += ... with accumulate), rows 1..8, as the
+// caller describes it; a prologue (batch 1 only) transforms x first.
 struct GroupEntry {
   const DeviceMatrix* m;
   const float* x;
@@ -84,6 +94,9 @@ struct GroupEntry {
   float* y;
   std::size_t rows;
   bool accumulate;
+  int prologue = kPlain;
+  const float* pw = nullptr;
+  float eps = 0.0f;
 };
 // One kernel launch of a group: the products of weight type `type` and row
 // chunk `rchunk`, at probs[prob_offset...], workgroup w running product
@@ -99,6 +112,17 @@ struct GroupPlan {
 };
 int plan_group(const GroupEntry* entries, std::size_t count, GroupPlan* plan);
 int launch_group(const GroupProblem* probs_dev, const std::uint32_t* map_dev, const GroupLaunch& l, hipStream_t s);
+
+// A planned group resident on the device (its table and workgroup map).
+struct DeviceGroup {
+  void* table = nullptr;
+  const GroupProblem* probs = nullptr;
+  const std::uint32_t* map = nullptr;
+  std::vector<GroupLaunch> launches;
+  int build(const GroupEntry* entries, std::size_t count);
+  int launch(hipStream_t s) const;
+  void release();
+};
 
 // One product of a grouped bf16-MFMA GEMM launch (qgemm_mfma).
 struct GemmProblem {

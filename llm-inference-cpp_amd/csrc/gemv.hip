@@ -35,6 +35,7 @@
 #include <vector>
 
 #include "common.hpp"
+#include "glue_math.hpp"
 
 namespace llmi_hip {
 
@@ -329,19 +330,72 @@ __device__ __forceinline__ void wide_tile(const GMEM uint4* __restrict__ codes, 
   }
 }
 
+// Stages the activations of a 16-row tile in LDS, applying the prologue
+// (see kPlain, kRmsNorm, kSiluUp).  Every thread of the workgroup calls it;
+// it ends with a barrier.
+__device__ __forceinline__ void stage_x(const GMEM float* __restrict__ x, int in, int prologue,
+                                        const GMEM float* __restrict__ pw, float eps, float* xs) {
+  __shared__ double red[16];
+  __shared__ std::uint64_t tab[32];
+  const int tid = threadIdx.x, nthreads = blockDim.x;
+  if (prologue == kSiluUp) {
+    if (tid < 32) tab[tid] = exact::kExp2Tab[tid];
+    __syncthreads();
+    for (int i = tid; i < in; i += nthreads) xs[i] = silu_exact(x[i], tab) * pw[i];
+    __syncthreads();
+    return;
+  }
+  if (prologue == kPlain) {
+    for (int i = tid; i < in; i += nthreads) xs[i] = x[i];
+    __syncthreads();
+    return;
+  }
+  // RMSNorm: the double sum of squares in any order, taken when the error
+  // bound proves the reference's sequential sum gives the same float scale
+  // (else summed sequentially), then y = w * (x * scale).
+  double part = 0.0;
+  for (int i = tid; i < in; i += nthreads) {
+    const float v = x[i];
+    xs[i] = v;
+    const double d = static_cast<double>(v);
+    part = __builtin_fma(d, d, part);
+  }
+  part = wave_sum(part);
+  if ((tid & 63) == 0) red[tid >> 6] = part;
+  __syncthreads();
+  double ss = 0.0;
+  for (int w = 0; w < (nthreads >> 6); ++w) ss += red[w];
+  const double slack = sum_slack(in) * ss;
+  float sc = rms_scale(ss, in, eps);
+  if (rms_scale(ss - slack, in, eps) != rms_scale(ss + slack, in, eps)) {
+    double seq = 0.0;  // every x is in LDS (the barrier above)
+    for (int i = 0; i < in; ++i) {
+      const double d = static_cast<double>(xs[i]);
+      seq = __builtin_fma(d, d, seq);
+    }
+    sc = rms_scale(seq, in, eps);
+  }
+  __syncthreads();  // the sequential sum has read xs before it is scaled
+  for (int i = tid; i < in; i += nthreads) xs[i] = pw[i] * (xs[i] * sc);
+  __syncthreads();
+}
+
 // One 16-row tile (batch 1), for matrices with few rows.  Lane l of a
 // wavefront owns row tile16*16 + (l & 15) and one of 4 block groups (l >> 4);
 // the W wavefronts give 4W groups of bpg contiguous blocks.  The 16 rows of
 // one block are a contiguous 256-byte piece of the 64-row layout, so loads
-// stay coalesced.  The activations are staged in LDS once and read with
-// broadcast loads (16 lanes per address); block sums and scales go to LDS,
-// and lanes 0-15 run the chain.  LDS: x[in (padded to 4)], part[nblk][16],
-// scale[nblk][16].
+// stay coalesced.  The first kHoist blocks of a lane are loaded before the
+// activations are staged (the two round trips overlap).  The activations sit
+// in LDS and are read with broadcast loads (16 lanes per address); block
+// sums and scales go to LDS, and lanes 0-15 run the chain.  LDS: x[in
+// (padded to 4)], part[nblk][16], scale[nblk][16].
 template <int TYPE>
 __device__ __forceinline__ void narrow_tile(const GMEM uint4* __restrict__ codes, const GMEM float* __restrict__ scales,
                                             const GMEM float* __restrict__ x, const GMEM float* __restrict__ bias,
                                             GMEM float* __restrict__ y, int in, int nblk, int out, int bpg, int accumulate,
-                                            std::size_t tile16, float* lds) {
+                                            std::size_t tile16, float* lds, int prologue = kPlain,
+                                            const GMEM float* __restrict__ pw = nullptr, float eps = 0.0f) {
+  constexpr int kHoist = 4;
   const Q4Magic k = q4_magic();
   float* xs = lds;
   float* part = lds + ((in + 3) & ~3);
@@ -352,17 +406,34 @@ __device__ __forceinline__ void narrow_tile(const GMEM uint4* __restrict__ codes
   const std::size_t row = tile16 * 16 + r;
   const std::size_t tile = row / kTileRows;
   const int sub = static_cast<int>(row % kTileRows);
-  for (int i = threadIdx.x; i < in; i += blockDim.x) xs[i] = x[i];
-  __syncthreads();
   const int nfull = in / kBlock;
   const int b_begin = group * bpg;
   const int b_end = min(nblk, b_begin + bpg);
-  for (int b = b_begin; b < b_end; ++b) {
+  Block<TYPE> pre[kHoist];
+  float pre_s[kHoist];
+#pragma unroll
+  for (int j = 0; j < kHoist; ++j) {
+    const int b = b_begin + j;
+    if (b < b_end) {
+      pre[j] = load_block<TYPE, true>(codes, tile * nblk + b, sub);
+      pre_s[j] = loadf<true>(scales + (tile * nblk + b) * kTileRows + sub);
+    }
+  }
+  stage_x(x, in, prologue, pw, eps, xs);
+#pragma unroll
+  for (int j = 0; j < kHoist; ++j) {
+    const int b = b_begin + j;
+    if (b < b_end) {
+      part[b * 16 + r] = b < nfull ? full_block_dot<TYPE>(pre[j], xs + b * kBlock, k)
+                                   : tail_block_dot<TYPE>(pre[j], xs + b * kBlock, in - b * kBlock);
+      scl[b * 16 + r] = pre_s[j];
+    }
+  }
+  for (int b = b_begin + kHoist; b < b_end; ++b) {
     const Block<TYPE> blk = load_block<TYPE, true>(codes, tile * nblk + b, sub);
     const float sc = loadf<true>(scales + (tile * nblk + b) * kTileRows + sub);
-    const float p = b < nfull ? full_block_dot<TYPE>(blk, xs + b * kBlock, k)
-                              : tail_block_dot<TYPE>(blk, xs + b * kBlock, in - b * kBlock);
-    part[b * 16 + r] = p;
+    part[b * 16 + r] = b < nfull ? full_block_dot<TYPE>(blk, xs + b * kBlock, k)
+                                 : tail_block_dot<TYPE>(blk, xs + b * kBlock, in - b * kBlock);
     scl[b * 16 + r] = sc;
   }
   __syncthreads();
@@ -413,7 +484,7 @@ __global__ void __launch_bounds__(1024) qgemv_group(const GroupProblem* __restri
   const GMEM float* bias = gmem(p.bias);
   if (R == 1 && p.kind == GroupProblem::kNarrow) {
     narrow_tile<TYPE>(codes, scales, gmem(p.x), bias, gmem_out(p.y), p.in, p.nblk, p.out, p.bpw, p.accumulate, local,
-                      lds);
+                      lds, p.prologue, gmem(p.pw), p.eps);
     return;
   }
   const int tile = local % p.ntiles;
@@ -654,7 +725,9 @@ int plan_group(const GroupEntry* entries, std::size_t count, GroupPlan* plan) {
       const GroupEntry& e = entries[i];
       const DeviceMatrix& m = *e.m;
       if (m.out == 0) continue;
-      const bool narrow = e.rows == 1 && wide_total < kNarrowBelow && narrow_lds(m.in, m.nblk) <= max_lds_per_block();
+      const bool fits = narrow_lds(m.in, m.nblk) <= max_lds_per_block();
+      const bool narrow = e.rows == 1 && (wide_total < kNarrowBelow || e.prologue != kPlain) && fits;
+      LLMI_REQUIRE(e.prologue == kPlain || narrow, "group: a prologue needs batch 1 and in <= ~20k");
       int r = narrow ? 1 : pick_chunk(e.rows, m.nblk, kLdsTarget);
       if (r == 0) r = pick_chunk(1, m.nblk, max_lds_per_block());
       LLMI_REQUIRE(r != 0, "group: rows too long for the grouped GEMV (in above ~10k)");
@@ -673,6 +746,9 @@ int plan_group(const GroupEntry* entries, std::size_t count, GroupPlan* plan) {
       p.rows = static_cast<int>(e.rows);
       p.ntiles = static_cast<int>(m.ntiles);
       p.accumulate = e.accumulate ? 1 : 0;
+      p.prologue = e.prologue;
+      p.pw = e.pw;
+      p.eps = e.eps;
       probs.push_back(p);
       // The launch's wavefront count follows its largest product.
       const std::size_t bytes = m.code_bytes + m.scale_bytes;
@@ -737,6 +813,37 @@ int launch_group(const GroupProblem* probs_dev, const std::uint32_t* map_dev, co
   }
   LLMI_TRY_HIP(hipGetLastError());
   return LLMI_OK;
+}
+
+int DeviceGroup::build(const GroupEntry* entries, std::size_t count) {
+  release();
+  GroupPlan plan;
+  if (int rc = plan_group(entries, count, &plan)) return rc;
+  launches = plan.launches;
+  const std::size_t pbytes = plan.probs.size() * sizeof(GroupProblem);
+  const std::size_t mbytes = plan.wg_prob.size() * sizeof(std::uint32_t);
+  if (pbytes + mbytes == 0) return LLMI_OK;
+  LLMI_TRY_HIP(hipMalloc(&table, pbytes + mbytes));
+  auto* base = static_cast<std::uint8_t*>(table);
+  LLMI_TRY_HIP(hipMemcpy(base, plan.probs.data(), pbytes, hipMemcpyHostToDevice));
+  if (mbytes > 0) LLMI_TRY_HIP(hipMemcpy(base + pbytes, plan.wg_prob.data(), mbytes, hipMemcpyHostToDevice));
+  probs = reinterpret_cast<const GroupProblem*>(base);
+  map = reinterpret_cast<const std::uint32_t*>(base + pbytes);
+  return LLMI_OK;
+}
+
+int DeviceGroup::launch(hipStream_t s) const {
+  for (const GroupLaunch& l : launches)
+    if (int rc = launch_group(probs, map, l, s)) return rc;
+  return LLMI_OK;
+}
+
+void DeviceGroup::release() {
+  if (table != nullptr) (void)hipFree(table);
+  table = nullptr;
+  probs = nullptr;
+  map = nullptr;
+  launches.clear();
 }
 
 }  // namespace llmi_hip

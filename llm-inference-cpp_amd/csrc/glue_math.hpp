@@ -1,0 +1,42 @@
+// Exact glue arithmetic shared by the model kernels and the fused GEMV
+// prologues: the reference's RMSNorm scale and SiLU (src/model/kernels.cpp:
+// 115-120, :148) and the bound that lets a parallel double sum stand in for
+// the reference's sequential one.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "exact_math.hpp"
+
+namespace llmi_hip {
+
+// Bound on |sequential - parallel| for a sum of n non-negative doubles:
+// both are within (n-1)u of the exact sum (u = 2^-53); 4nu covers both.
+__device__ __forceinline__ double sum_slack(int n) { return 4.0 * static_cast<double>(n) * 0x1p-53; }
+
+// kernels.cpp:115-120: scale = float(1 / sqrt(ss / n + eps)), ss the double
+// sum of squares.
+__device__ __forceinline__ float rms_scale(double ss, int n, float eps) {
+  return static_cast<float>(1.0 / sqrt(ss / static_cast<double>(n) + static_cast<double>(eps)));
+}
+
+// kernels.cpp:148: x / (1 + exp(-x)) in float (IEEE division), with the
+// exact expf (table `tab`: exact::kExp2Tab or a copy of it).
+__device__ __forceinline__ float silu_exact(float v, const std::uint64_t* tab) {
+  return v / (1.0f + exact::expf_with(-v, tab));
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+__device__ __forceinline__ double wave_sum(double v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = v + __shfl_xor(v, o, 64);
+  return v;
+}
+
+}  // namespace llmi_hip

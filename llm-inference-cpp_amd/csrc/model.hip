@@ -32,6 +32,7 @@
 
 #include "common.hpp"
 #include "exact_math.hpp"
+#include "glue_math.hpp"
 
 namespace llmi_hip {
 namespace {
@@ -66,15 +67,7 @@ __device__ __forceinline__ float block_max_float(float v, float* red) {
   return r;
 }
 
-// Bound on |sequential - parallel| for a sum of n non-negative doubles:
-// both are within (n-1)u of the exact sum (u = 2^-53); 4nu covers both.
-__device__ __forceinline__ double sum_slack(int n) { return 4.0 * static_cast<double>(n) * 0x1p-53; }
-
 // ------------------------------------------------------------ rmsnorm
-__device__ __forceinline__ float rms_scale(double ss, int n, float eps) {
-  return static_cast<float>(1.0 / sqrt(ss / static_cast<double>(n) + static_cast<double>(eps)));
-}
-
 // One workgroup per row: y = w * (x * scale), scale from the double sum of
 // squares (kernels.cpp:115-120).
 __global__ void __launch_bounds__(kThreads) rmsnorm_rows(const float* __restrict__ x, const float* __restrict__ w,
@@ -363,25 +356,50 @@ __device__ __forceinline__ float add_row_shl(float v) {
   return v + __int_as_float(src);
 }
 
+// RoPE of the new token is fused (rope_and_cache's arithmetic): q is rotated
+// while it is staged, and the workgroup holding position npos - 1 rotates
+// the new k (knew), uses it and writes it to the cache.  cr/sr: the cos/sin
+// table rows of that position.
 template <int NCH>  // head_dim / 16
-__global__ void __launch_bounds__(kThreads) attn_scores_1(const float* __restrict__ q, const float* __restrict__ kc,
-                                                          float* __restrict__ scores, int nh, int nkv, int cap,
-                                                          int npos, float scale) {
-  constexpr int hd = 16 * NCH;
+__global__ void __launch_bounds__(kThreads) attn_scores_1(const float* __restrict__ q, const float* __restrict__ knew,
+                                                          float* __restrict__ kc, const float* __restrict__ cr,
+                                                          const float* __restrict__ sr, float* __restrict__ scores,
+                                                          int nh, int nkv, int cap, int npos, float scale) {
+  constexpr int hd = 16 * NCH, half = hd / 2;
   __shared__ float qs[16 * hd];  // the group's query heads (G <= 16)
   const int kvh = blockIdx.y;
   const int G = nh / nkv;
   const int j = threadIdx.x & 15, grp = threadIdx.x >> 4;
   const int s0 = blockIdx.x * kScoreTile;
-  const float* kh = kc + static_cast<std::size_t>(kvh) * cap * hd;
+  const int pos = npos - 1;
+  float* kh = kc + static_cast<std::size_t>(kvh) * cap * hd;
   float kv[kScoreTile / 16][NCH];
 #pragma unroll
   for (int p = 0; p < kScoreTile / 16; ++p) {
     const int s = s0 + 16 * p + grp;
+    if (s == pos) {
+      const float* kn = knew + static_cast<std::size_t>(kvh) * hd;
 #pragma unroll
-    for (int c = 0; c < NCH; ++c) kv[p][c] = s < npos ? kh[static_cast<std::size_t>(s) * hd + 16 * c + j] : 0.0f;
+      for (int c = 0; c < NCH / 2; ++c) {
+        const int i = 16 * c + j;
+        const float a = kn[i], b = kn[i + half], cs = cr[i], sn = sr[i];
+        kv[p][c] = __builtin_fmaf(a, cs, -(b * sn));
+        kv[p][c + NCH / 2] = __builtin_fmaf(b, cs, a * sn);
+      }
+#pragma unroll
+      for (int c = 0; c < NCH; ++c) kh[static_cast<std::size_t>(s) * hd + 16 * c + j] = kv[p][c];
+    } else {
+#pragma unroll
+      for (int c = 0; c < NCH; ++c) kv[p][c] = s < npos ? kh[static_cast<std::size_t>(s) * hd + 16 * c + j] : 0.0f;
+    }
   }
-  for (int e = threadIdx.x; e < G * hd; e += kThreads) qs[e] = q[static_cast<std::size_t>(kvh) * G * hd + e];
+  for (int e = threadIdx.x; e < G * half; e += kThreads) {
+    const int g = e / half, i = e % half;
+    const float* qh = q + static_cast<std::size_t>(kvh * G + g) * hd;
+    const float a = qh[i], b = qh[i + half], cs = cr[i], sn = sr[i];
+    qs[g * hd + i] = __builtin_fmaf(a, cs, -(b * sn));
+    qs[g * hd + i + half] = __builtin_fmaf(b, cs, a * sn);
+  }
   __syncthreads();
   for (int g = 0; g < G; ++g) {
     const int h = kvh * G + g;
@@ -416,22 +434,14 @@ __global__ void __launch_bounds__(kThreads) attn_scores_1(const float* __restric
 constexpr int kPvCols = 16;
 constexpr int kPvBatch = 8;  // V loads per thread per round
 
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-  return v;
-}
-__device__ __forceinline__ double wave_sum(double v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = v + __shfl_xor(v, o, 64);
-  return v;
-}
-
 __device__ __forceinline__ int pv_stride(int npad) { return ((npad + 31) & ~31) + 4; }
 
+// The new token's v (vnew) is read in place of cache row npos - 1, and the
+// first head of each group writes its slice of it to the cache.
 template <int NCH>
-__global__ void __launch_bounds__(kThreads) attn_pv_1(const float* __restrict__ scores, const float* __restrict__ vc,
-                                                      float* __restrict__ out, int nh, int nkv, int cap, int npos) {
+__global__ void __launch_bounds__(kThreads) attn_pv_1(const float* __restrict__ scores, const float* __restrict__ vnew,
+                                                      float* __restrict__ vc, float* __restrict__ out, int nh, int nkv,
+                                                      int cap, int npos) {
   constexpr int hd = 16 * NCH;
   constexpr int kWaves = kThreads / 64;
   extern __shared__ float4 pv_lds[];  // 16-byte aligned: the chains read float4
@@ -450,7 +460,10 @@ __global__ void __launch_bounds__(kThreads) attn_pv_1(const float* __restrict__ 
   if (tid < 32) exp_tab[tid] = exact::kExp2Tab[tid];
 
   const float* vh = vc + static_cast<std::size_t>(kvh) * cap * hd + i0;
+  const float* vn = vnew + static_cast<std::size_t>(kvh) * hd + i0;
   const float* src = scores + static_cast<std::size_t>(h) * cap;
+  if (h % (nh / nkv) == 0 && tid < kPvCols)
+    vc[(static_cast<std::size_t>(kvh) * cap + npos - 1) * hd + i0 + tid] = vn[tid];
   const int n4 = npad * 4;
   for (int e0 = 0; e0 < max(n4, npad); e0 += kThreads * kPvBatch) {
     float4 v[kPvBatch];
@@ -459,8 +472,9 @@ __global__ void __launch_bounds__(kThreads) attn_pv_1(const float* __restrict__ 
     for (int u = 0; u < kPvBatch; ++u) {
       const int e = e0 + u * kThreads + tid;
       const int sp = e >> 2;
-      v[u] = sp < npos ? *reinterpret_cast<const float4*>(vh + static_cast<std::size_t>(sp) * hd + 4 * (e & 3))
-                       : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      v[u] = sp < npos - 1 ? *reinterpret_cast<const float4*>(vh + static_cast<std::size_t>(sp) * hd + 4 * (e & 3))
+             : sp == npos - 1 ? *reinterpret_cast<const float4*>(vn + 4 * (e & 3))
+                              : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
       sv[u] = e < npos ? src[e] : 0.0f;
     }
 #pragma unroll
@@ -539,17 +553,18 @@ bool decode_attention_fits(int nh, int nkv, int hd, std::size_t npos) {
          attn_pv_lds(npos) <= max_lds_per_block();
 }
 
-void launch_decode_attention(const float* q, const float* kc, const float* vc, float* scores, float* out, int nh,
-                             int nkv, int hd, int cap, int npos, float scale, hipStream_t s) {
+void launch_decode_attention(const float* q, const float* knew, const float* vnew, float* kc, float* vc,
+                             const float* cr, const float* sr, float* scores, float* out, int nh, int nkv, int hd,
+                             int cap, int npos, float scale, hipStream_t s) {
   const dim3 sgrid(static_cast<unsigned>((npos + kScoreTile - 1) / kScoreTile), static_cast<unsigned>(nkv));
   const dim3 pgrid(static_cast<unsigned>(nh), static_cast<unsigned>(hd / kPvCols));
   const std::size_t lds = attn_pv_lds(npos);
   if (hd == 64) {
-    attn_scores_1<4><<<sgrid, kThreads, 0, s>>>(q, kc, scores, nh, nkv, cap, npos, scale);
-    attn_pv_1<4><<<pgrid, kThreads, lds, s>>>(scores, vc, out, nh, nkv, cap, npos);
+    attn_scores_1<4><<<sgrid, kThreads, 0, s>>>(q, knew, kc, cr, sr, scores, nh, nkv, cap, npos, scale);
+    attn_pv_1<4><<<pgrid, kThreads, lds, s>>>(scores, vnew, vc, out, nh, nkv, cap, npos);
   } else {
-    attn_scores_1<8><<<sgrid, kThreads, 0, s>>>(q, kc, scores, nh, nkv, cap, npos, scale);
-    attn_pv_1<8><<<pgrid, kThreads, lds, s>>>(scores, vc, out, nh, nkv, cap, npos);
+    attn_scores_1<8><<<sgrid, kThreads, 0, s>>>(q, knew, kc, cr, sr, scores, nh, nkv, cap, npos, scale);
+    attn_pv_1<8><<<pgrid, kThreads, lds, s>>>(scores, vnew, vc, out, nh, nkv, cap, npos);
   }
 }
 
@@ -708,6 +723,14 @@ unsigned blocks_for(std::size_t n) { return static_cast<unsigned>(ceil_div(n, kT
 struct DeviceLayer {
   float *attn_norm = nullptr, *mlp_norm = nullptr, *bq = nullptr, *bk = nullptr, *bv = nullptr;
   DeviceMatrix wq, wk, wv, wo, gate, up, down;
+  // The fused one-token step's launches (see decode_step).
+  DeviceGroup qkv, gate_up, down_silu;
+};
+
+// Fixed one-token buffers of the fused decode step.
+struct DecodeBuffers {
+  float *x = nullptr, *h = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *att = nullptr, *g = nullptr,
+        *u = nullptr;
 };
 
 struct Workspace {
@@ -738,6 +761,7 @@ struct llmi_hip_model {
   float* sin_t = nullptr;
   std::size_t table_len = 0;
   llmi_hip::Workspace ws;
+  llmi_hip::DecodeBuffers dec;
   std::vector<void*> allocations;
   double last_prefill_ms = 0.0, last_decode_ms = 0.0;  // of the last greedy run
 };
@@ -807,6 +831,48 @@ int check_config(const llmi_model_config& c) {
   return LLMI_OK;
 }
 
+// The fused one-token step (decode_step): per layer
+//   qkv:       RMSNorm(x) staged in each workgroup, then q, k, v (+ biases)
+//   attention: attn_scores_1 (RoPE of q and of the new k fused, the k written
+//              to the cache) and attn_pv_1 (the new v written to the cache)
+//   o_proj:    x += W_o att
+//   gate_up:   RMSNorm(x) staged again, then gate and up
+//   down_silu: SiLU(gate) * up staged, then x += W_down (...)
+// -- 6 launches instead of 13, with the same arithmetic.
+int build_decode(llmi_hip_model* m) {
+  DecodeBuffers& d = m->dec;
+  const auto get = [&](float** p, std::size_t n) { return dev_alloc(m, reinterpret_cast<void**>(p), n * sizeof(float)); };
+  if (int rc = get(&d.x, m->H)) return rc;
+  if (int rc = get(&d.h, m->H)) return rc;
+  if (int rc = get(&d.q, m->Q)) return rc;
+  if (int rc = get(&d.k, m->KV)) return rc;
+  if (int rc = get(&d.v, m->KV)) return rc;
+  if (int rc = get(&d.att, m->Q)) return rc;
+  if (int rc = get(&d.g, m->F)) return rc;
+  if (int rc = get(&d.u, m->F)) return rc;
+  const float eps = static_cast<float>(m->c.rms_norm_eps);
+  for (DeviceLayer& l : m->layers) {
+    const GroupEntry qkv[3] = {{&l.wq, d.x, l.bq, d.q, 1, false, kRmsNorm, l.attn_norm, eps},
+                               {&l.wk, d.x, l.bk, d.k, 1, false, kRmsNorm, l.attn_norm, eps},
+                               {&l.wv, d.x, l.bv, d.v, 1, false, kRmsNorm, l.attn_norm, eps}};
+    const GroupEntry gu[2] = {{&l.gate, d.x, nullptr, d.g, 1, false, kRmsNorm, l.mlp_norm, eps},
+                              {&l.up, d.x, nullptr, d.u, 1, false, kRmsNorm, l.mlp_norm, eps}};
+    const GroupEntry dn[1] = {{&l.down, d.g, nullptr, d.x, 1, true, kSiluUp, d.u, 0.0f}};
+    if (int rc = l.qkv.build(qkv, 3)) return rc;
+    if (int rc = l.gate_up.build(gu, 2)) return rc;
+    if (int rc = l.down_silu.build(dn, 1)) return rc;
+  }
+  return LLMI_OK;
+}
+
+void release_decode(llmi_hip_model* m) {
+  for (DeviceLayer& l : m->layers) {
+    l.qkv.release();
+    l.gate_up.release();
+    l.down_silu.release();
+  }
+}
+
 int create_model(const llmi_model_config* cfg, const float* const* t, int type, bool on_device,
                  llmi_hip_model** out) {
   LLMI_REQUIRE_INIT();
@@ -827,6 +893,7 @@ int create_model(const llmi_model_config* cfg, const float* const* t, int type, 
   m->V = c.vocab_size;
   m->tied = c.tie_word_embeddings != 0;
   auto cleanup = [&](int rc) {
+    release_decode(m.get());
     for (void* p : m->allocations) (void)hipFree(p);
     m->allocations.clear();
     return rc;
@@ -863,6 +930,7 @@ int create_model(const llmi_model_config* cfg, const float* const* t, int type, 
     (void)hipFree(staging);
     m->allocations.erase(std::find(m->allocations.begin(), m->allocations.end(), static_cast<void*>(staging)));
   }
+  if (int rc2 = build_decode(m.get())) return cleanup(rc2);
   // inv_freq[i] = 1 / theta^(2i/d) in float, as transformer.cpp:59-66.
   m->inv_freq.resize(m->hd / 2);
   for (std::size_t i = 0; i < m->hd / 2; ++i) {
@@ -946,6 +1014,40 @@ int ensure_workspace(llmi_hip_model* m, std::size_t T) {
   return LLMI_OK;
 }
 
+// One token (T = 1) through the fused per-layer launches built by
+// build_decode; the same arithmetic as forward_device.  Logits land in
+// ws.logits.
+int decode_step(llmi_hip_model* m, llmi_hip_cache* cache, hipStream_t s) {
+  const auto& c = m->c;
+  Workspace& w = m->ws;
+  DecodeBuffers& d = m->dec;
+  const std::size_t pos = cache->len;
+  const int nh = static_cast<int>(c.num_heads), nkv = static_cast<int>(c.num_kv_heads);
+  const int hd = static_cast<int>(m->hd);
+  const float eps = static_cast<float>(c.rms_norm_eps);
+  const float scale = 1.0F / std::sqrt(static_cast<float>(m->hd));
+  const std::size_t per_layer = static_cast<std::size_t>(c.num_kv_heads) * cache->cap * m->hd;
+  const float* cr = m->cos_t + pos * (m->hd / 2);
+  const float* sr = m->sin_t + pos * (m->hd / 2);
+  if (int rc = launch_dequantize_rows(m->embed, w.ids, 1, d.x, s)) return rc;
+  for (std::size_t li = 0; li < m->layers.size(); ++li) {
+    const DeviceLayer& l = m->layers[li];
+    if (int rc = l.qkv.launch(s)) return rc;
+    launch_decode_attention(d.q, d.k, d.v, cache->k + li * per_layer, cache->v + li * per_layer, cr, sr,
+                            cache->scores, d.att, nh, nkv, hd, static_cast<int>(cache->cap), static_cast<int>(pos + 1),
+                            scale, s);
+    if (int rc = launch_matmul(l.wo, d.att, 1, nullptr, d.x, s, true)) return rc;
+    if (int rc = l.gate_up.launch(s)) return rc;
+    if (int rc = l.down_silu.launch(s)) return rc;
+  }
+  rmsnorm_rows<<<1, kThreads, 0, s>>>(d.x, m->final_norm, d.h, static_cast<int>(m->H), eps);
+  const DeviceMatrix& head = m->tied ? m->embed : m->lm_head;
+  if (int rc = launch_matmul(head, d.h, 1, nullptr, w.logits, s)) return rc;
+  LLMI_TRY_HIP(hipGetLastError());
+  cache->len = pos + 1;
+  return LLMI_OK;
+}
+
 // transformer.cpp:192-306 with the ids already on the device (ws.ids).  The
 // logits of rows first..T-1 land in ws.logits.  trace (host, optional):
 // (layers + 2) x T x H floats -- the embeddings, every layer's output and
@@ -956,6 +1058,8 @@ int forward_device(llmi_hip_model* m, llmi_hip_cache* cache, std::size_t T, bool
   Workspace& w = m->ws;
   const std::size_t base = cache->len;
   const int nh = static_cast<int>(c.num_heads), nkv = static_cast<int>(c.num_kv_heads);
+  if (T == 1 && trace == nullptr && decode_attention_fits(nh, nkv, static_cast<int>(m->hd), base + 1))
+    return decode_step(m, cache, s);
   const int hd = static_cast<int>(m->hd);
   const float eps = static_cast<float>(c.rms_norm_eps);
   const float scale = 1.0F / std::sqrt(static_cast<float>(m->hd));
@@ -975,12 +1079,8 @@ int forward_device(llmi_hip_model* m, llmi_hip_cache* cache, std::size_t T, bool
     if (int rc = launch_matmul(l.wv, w.h, T, l.bv, w.v, s)) return rc;
     rope_and_cache<<<tt, kThreads, 0, s>>>(w.q, w.k, w.v, kc, vc, m->cos_t, m->sin_t, nh, nkv, hd,
                                            static_cast<int>(cache->cap), static_cast<int>(base));
-    if (T == 1 && decode_attention_fits(nh, nkv, hd, base + 1))
-      launch_decode_attention(w.q, kc, vc, cache->scores, w.att, nh, nkv, hd, static_cast<int>(cache->cap),
-                              static_cast<int>(base + 1), scale, s);
-    else
-      launch_attention(w.q, kc, vc, w.att, nh, nkv, hd, static_cast<int>(cache->cap), static_cast<int>(base),
-                       static_cast<int>(T), scale, s);
+    launch_attention(w.q, kc, vc, w.att, nh, nkv, hd, static_cast<int>(cache->cap), static_cast<int>(base),
+                     static_cast<int>(T), scale, s);
     if (int rc = launch_matmul(l.wo, w.att, T, nullptr, w.x, s, true)) return rc;
     rmsnorm_rows<<<tt, kThreads, 0, s>>>(w.x, l.mlp_norm, w.h, static_cast<int>(m->H), eps);
     if (int rc = launch_matmul(l.gate, w.h, T, nullptr, w.g, s)) return rc;
@@ -1081,6 +1181,7 @@ int llmi_hip_model_create_dev(const llmi_model_config* cfg, const float* const* 
 int llmi_hip_model_free(llmi_hip_model* m) {
   if (m == nullptr) return LLMI_OK;
   if (library_stream() != nullptr) (void)hipStreamSynchronize(library_stream());
+  release_decode(m);
   for (void* p : m->allocations) (void)hipFree(p);
   if (m->cos_t != nullptr) (void)hipFree(m->cos_t);
   if (m->sin_t != nullptr) (void)hipFree(m->sin_t);
