@@ -32,6 +32,24 @@ struct DevBuf {
   }
 };
 
+// The single-product GEMM's bf16 copy of x: grown when a call needs more (the
+// stream is drained first, since queued work may still read the old one).
+struct Scratch {
+  void* p = nullptr;
+  std::size_t bytes = 0;
+  int reserve(std::size_t need, hipStream_t s) {
+    if (need <= bytes) return LLMI_OK;
+    LLMI_TRY_HIP(hipStreamSynchronize(s));
+    if (p != nullptr) LLMI_TRY_HIP(hipFree(p));
+    p = nullptr;
+    bytes = 0;
+    LLMI_TRY_HIP(hipMalloc(&p, need));
+    bytes = need;
+    return LLMI_OK;
+  }
+};
+Scratch g_gemm_scratch;
+
 int check_type(int type) {
   LLMI_REQUIRE(type == LLMI_TYPE_Q8_0 || type == LLMI_TYPE_Q4_0, "type must be LLMI_TYPE_Q8_0 or LLMI_TYPE_Q4_0");
   return LLMI_OK;
@@ -88,11 +106,13 @@ struct llmi_hip_group {
 
 struct llmi_hip_gemm_group {
   void* table = nullptr;  // device copy of the problem table, then the work -> problem map
+  std::uint16_t* scratch = nullptr;  // bf16 copies of the inputs
   const GemmProblem* probs = nullptr;
   const std::uint32_t* map = nullptr;
-  std::vector<GemmLaunch> launches;
+  GemmPlan plan;
   ~llmi_hip_gemm_group() {
     if (table != nullptr) (void)hipFree(table);
+    if (scratch != nullptr) (void)hipFree(scratch);
   }
 };
 
@@ -489,10 +509,12 @@ int llmi_hip_gemm_group_create(const llmi_hip_weight* const* w, const float* con
   std::vector<GroupEntry> entries;
   if (int rc = group_entries(w, x, rows, bias, y, count, 0, &entries)) return rc;
   auto g = std::make_unique<llmi_hip_gemm_group>();
-  GemmPlan plan;
-  if (int rc = plan_gemm_group(entries.data(), count, &plan)) return rc;
-  g->launches = plan.launches;
-  if (int rc = upload_plan(plan, plan.probs, plan.work_prob, g.get())) return rc;
+  if (int rc = plan_gemm_group(entries.data(), count, &g->plan)) return rc;
+  if (g->plan.scratch_elems > 0) {
+    LLMI_TRY_HIP(hipMalloc(reinterpret_cast<void**>(&g->scratch), g->plan.scratch_elems * sizeof(std::uint16_t)));
+    bind_gemm_scratch(&g->plan, g->scratch);
+  }
+  if (int rc = upload_plan(g->plan, g->plan.probs, g->plan.work_prob, g.get())) return rc;
   *out = g.release();
   return LLMI_OK;
 }
@@ -500,7 +522,8 @@ int llmi_hip_gemm_group_create(const llmi_hip_weight* const* w, const float* con
 int llmi_hip_gemm_group_launch(const llmi_hip_gemm_group* g, void* stream) {
   LLMI_REQUIRE_INIT();
   LLMI_REQUIRE(g != nullptr, "gemm: null group");
-  for (const GemmLaunch& l : g->launches)
+  if (int rc = launch_gemm_inputs(g->plan, g->scratch, pick(stream))) return rc;
+  for (const GemmLaunch& l : g->plan.launches)
     if (int rc = launch_gemm(g->probs, g->map, l, pick(stream))) return rc;
   return LLMI_OK;
 }
@@ -515,6 +538,10 @@ int llmi_hip_matmul_mfma_dev(const llmi_hip_weight* weight, const float* x, size
   const GroupEntry e{&weight->m, x, bias, y, rows, false};
   GemmPlan plan;
   if (int rc = plan_gemm_group(&e, 1, &plan)) return rc;
+  if (int rc = g_gemm_scratch.reserve(plan.scratch_elems * sizeof(std::uint16_t), pick(stream))) return rc;
+  auto* scratch = static_cast<std::uint16_t*>(g_gemm_scratch.p);
+  bind_gemm_scratch(&plan, scratch);
+  if (int rc = launch_gemm_inputs(plan, scratch, pick(stream))) return rc;
   for (const GemmLaunch& l : plan.launches)
     if (int rc = launch_gemm(nullptr, nullptr, l, pick(stream), &plan.probs[l.prob_offset])) return rc;
   return LLMI_OK;

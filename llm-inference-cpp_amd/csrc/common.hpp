@@ -124,14 +124,21 @@ struct DeviceGroup {
   void release();
 };
 
-// One product of a grouped bf16-MFMA GEMM launch (qgemm_mfma).
+// One product of a grouped bf16-MFMA GEMM launch (qgemm_mfma).  xb: the
+// activations converted to bf16, [rows][ldx] (ldx = in rounded up to 64).
 struct GemmProblem {
   const std::uint8_t* codes;
   const float* scales;
-  const float* x;
+  const std::uint16_t* xb;
   const float* bias;
   float* y;
-  int rows, in, out, nblk, ntiles, mtiles, first_wg;
+  int rows, in, ldx, out, nblk, ntiles, mtiles, first_wg, input;
+};
+// A distinct fp32 activation matrix of a GEMM group and where its bf16 copy
+// lives in the group's scratch (element offset).
+struct GemmInput {
+  const float* x = nullptr;
+  std::size_t rows = 0, in = 0, ldx = 0, offset = 0;
 };
 struct GemmLaunch {
   int type = 0, total_wgs = 0;
@@ -141,8 +148,14 @@ struct GemmPlan {
   std::vector<GemmProblem> probs;
   std::vector<std::uint32_t> work_prob;
   std::vector<GemmLaunch> launches;
+  std::vector<GemmInput> inputs;
+  std::size_t scratch_elems = 0;  // bf16 elements of scratch the inputs need
 };
 int plan_gemm_group(const GroupEntry* entries, std::size_t count, GemmPlan* plan);
+// Points every problem at its input's bf16 copy inside `scratch`.
+void bind_gemm_scratch(GemmPlan* plan, std::uint16_t* scratch);
+// Queues the fp32 -> bf16 conversion of every input into `scratch`.
+int launch_gemm_inputs(const GemmPlan& plan, std::uint16_t* scratch, hipStream_t s);
 // one != nullptr: launch the single product *one (plan of one entry) without
 // a device table.
 int launch_gemm(const GemmProblem* probs_dev, const std::uint32_t* map_dev, const GemmLaunch& l, hipStream_t s,

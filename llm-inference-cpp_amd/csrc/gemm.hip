@@ -8,20 +8,24 @@
 // the tested bound is max|dy| <= 2e-2 * max|y|).  The exact path for the
 // same shapes is llmi_hip_matmul_dev.
 //
-// One workgroup computes a 128 (tokens) x 128 (outputs) tile of y; its 4
-// wavefronts each own a 64 x 64 quarter (4 x 4 MFMA tiles of 16 x 16).  Per
-// K-step of 64 (two quantization blocks) every thread loads 32 activations
-// (fp32) and 32 weight codes (one row of one block) from HBM into registers,
-// converts them to bf16 (weights: code * scale) and stores them to LDS
-// ([row][k], k contiguous, rows padded by 16 bytes so that the 16-byte
-// operand reads of 8 consecutive lanes hit distinct banks).  The loads of the
-// next K-step are issued before the MFMAs of the current one.
+// x is first converted to bf16 once (x_to_bf16: rows padded to a multiple of
+// 64 with zeros), so the GEMM reads half the activation bytes and never
+// converts them again.  One workgroup (8 wavefronts) computes a 128 (tokens)
+// x 256 (outputs) tile of y; wavefront w owns the 64 x 64 block (w / 4, w % 4)
+// as 4 x 4 MFMA tiles of 16 x 16.  Per K-step of 64 (two quantization blocks)
+// the workgroup stages 128 x 64 activations and 256 x 64 dequantized weights
+// (code * scale, rounded to bf16) in LDS, double-buffered: while the MFMAs of
+// step k read one buffer, the threads dequantize step k + 1 (already in
+// registers) into the other and issue the global loads of step k + 3, so the
+// loads have two steps to arrive; one barrier per step.  LDS rows are padded
+// by 16 bytes so that the 16-byte operand reads of 8 consecutive lanes hit
+// distinct banks.
 //
 // Products are launched as groups (one kernel for many products; a single
-// product is passed by value): workgroup w first maps to a work index so that consecutive work items -- the token
-// tiles sharing one weight tile -- run on the same XCD (workgroups are
-// dealt to the 8 XCDs round-robin), then finds its product through a
-// work -> product map.
+// product is passed by value): workgroup w first maps to a work index so that
+// consecutive work items -- the token tiles sharing one weight tile -- run on
+// the same XCD (workgroups are dealt to the 8 XCDs round-robin), then finds
+// its product through a work -> product map.
 #include <algorithm>
 #include <vector>
 
@@ -33,7 +37,8 @@ namespace {
 
 #define GMEM __attribute__((address_space(1)))
 
-constexpr int kBM = 128, kBN = 128, kBK = 64;
+constexpr int kBM = 128, kBN = 256, kBK = 64;
+constexpr int kGemmThreads = 512;
 constexpr int kLdsRow = kBK + 8;  // bf16 per LDS row (16 bytes of padding)
 constexpr int kXcds = 8;
 
@@ -54,18 +59,44 @@ __device__ __forceinline__ int snib(std::uint32_t w, int i) {
   return static_cast<int>(__builtin_amdgcn_sbfe(w ^ 0x88888888u, i * 4, 4));
 }
 
+// xb[r][k] = bf16(x[r][k]) for k < in, 0 for in <= k < ldx.  One thread per 4
+// elements of a row.
+__global__ void __launch_bounds__(256) x_to_bf16(const float* __restrict__ x, std::uint16_t* __restrict__ xb,
+                                                 int rows, int in, int ldx) {
+  const std::size_t quads = static_cast<std::size_t>(rows) * (ldx / 4);
+  for (std::size_t q = static_cast<std::size_t>(blockIdx.x) * blockDim.x + threadIdx.x; q < quads;
+       q += static_cast<std::size_t>(gridDim.x) * blockDim.x) {
+    const std::size_t r = q / (ldx / 4);
+    const int k = static_cast<int>(q % (ldx / 4)) * 4;
+    const float* src = x + r * in + k;
+    float v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) v[u] = k + u < in ? src[u] : 0.0f;
+    *reinterpret_cast<uint2*>(xb + r * ldx + k) = make_uint2(pack_bf16(v[0], v[1]), pack_bf16(v[2], v[3]));
+  }
+}
+
+// Raw data of one K-step held by one thread: 16 activations (bf16) of row
+// t/4, and the 32 codes + scale of row t/2, block t%2.
 template <int TYPE>
-__global__ void __launch_bounds__(256) qgemm_mfma(const GemmProblem* __restrict__ probs,
-                                                  const std::uint32_t* __restrict__ work_prob, int total,
-                                                  GemmProblem one) {
-  __shared__ __attribute__((aligned(16))) std::uint16_t xs[kBM * kLdsRow];
-  __shared__ __attribute__((aligned(16))) std::uint16_t ws[kBN * kLdsRow];
+struct Stage {
+  u32x4 x0, x1;
+  u32x4 w[TYPE == LLMI_TYPE_Q8_0 ? 2 : 1];
+  float sc;
+};
+
+template <int TYPE>
+__global__ void __launch_bounds__(kGemmThreads) qgemm_mfma(const GemmProblem* __restrict__ probs,
+                                                           const std::uint32_t* __restrict__ work_prob, int total,
+                                                           GemmProblem one) {
+  __shared__ __attribute__((aligned(16))) std::uint16_t xs[2][kBM * kLdsRow];
+  __shared__ __attribute__((aligned(16))) std::uint16_t ws[2][kBN * kLdsRow];
 
   // Work index: workgroup w runs on XCD w % 8; give each XCD a contiguous
   // range of work items.
-  const int w = blockIdx.x;
+  const int wgi = blockIdx.x;
   const int per = total / kXcds, extra = total % kXcds;
-  const int xcd = w % kXcds, slot = w / kXcds;
+  const int xcd = wgi % kXcds, slot = wgi / kXcds;
   const int work = xcd * per + min(xcd, extra) + slot;
   // A single product comes by value (no table); a group through the map.
   GemmProblem p = one;
@@ -73,90 +104,65 @@ __global__ void __launch_bounds__(256) qgemm_mfma(const GemmProblem* __restrict_
   const int local = work - p.first_wg;
   const int mt = local % p.mtiles, nt = local / p.mtiles;
   const int m0 = mt * kBM, n0 = nt * kBN;
-  const int M = p.rows, K = p.in, N = p.out, nblk = p.nblk;
-  const GMEM float* x = (const GMEM float*)p.x;
+  const int M = p.rows, N = p.out, nblk = p.nblk, ldx = p.ldx;
+  const int nk = (p.in + kBK - 1) / kBK;
+  const GMEM u32x4* xb = (const GMEM u32x4*)p.xb;
   const GMEM u32x4* codes = (const GMEM u32x4*)p.codes;
   const GMEM float* scales = (const GMEM float*)p.scales;
 
   const int t = threadIdx.x;
   const int lane = t & 63, wave = t >> 6;
-  // Staging map: thread t loads row t/2 of the tile, K half t%2 (32 values).
-  const int lr = t >> 1, lh = t & 1;
-  const int xm = m0 + lr;
-  const int wn = n0 + lr;
-  const int wtile = wn / kTileRows, wlane = wn % kTileRows;
-  const bool xrow_ok = xm < M;
+  // Staging map: activations row t/4, 16 values from column 16*(t%4);
+  // weights row t/2, quantization block t%2 of the step.
+  const int xr = t >> 2, xq = t & 3;
+  const int wr = t >> 1, lh = t & 1;
+  const int wrow = n0 + wr;
+  const int wtile = wrow / kTileRows, wlane = wrow % kTileRows;
+  const bool xrow_ok = m0 + xr < M;
   const bool wrow_ok = wtile < p.ntiles;
-  const bool xvec = (K & 3) == 0;
+  // u32x4 index of this thread's activations at step 0.
+  const std::size_t xbase = (static_cast<std::size_t>(m0 + xr) * ldx + xq * 16) / 8;
 
-  float xv[32];
-  std::uint32_t wc[8];
-  float wscale = 0.0f;
-
-  auto gload = [&](int k0) {
-    const int kb = k0 + lh * 32;
-    if (xrow_ok && xvec && kb + 32 <= K) {
-      const GMEM f32x4* src = (const GMEM f32x4*)(x + static_cast<std::size_t>(xm) * K + kb);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const f32x4 v = src[i];
-        xv[4 * i] = v.x;
-        xv[4 * i + 1] = v.y;
-        xv[4 * i + 2] = v.z;
-        xv[4 * i + 3] = v.w;
-      }
+  auto gload = [&](Stage<TYPE>& st, int k) {
+    if (xrow_ok) {
+      st.x0 = xb[xbase + static_cast<std::size_t>(k) * (kBK / 8)];
+      st.x1 = xb[xbase + static_cast<std::size_t>(k) * (kBK / 8) + 1];
     } else {
-#pragma unroll
-      for (int i = 0; i < 32; ++i)
-        xv[i] = (xrow_ok && kb + i < K) ? x[static_cast<std::size_t>(xm) * K + kb + i] : 0.0f;
+      st.x0 = st.x1 = u32x4{0, 0, 0, 0};
     }
-    const int b = k0 / kBlock + lh;
+    const int b = 2 * k + lh;
     if (wrow_ok && b < nblk) {
-      const std::size_t slot = static_cast<std::size_t>(wtile) * nblk + b;
+      const std::size_t sl = static_cast<std::size_t>(wtile) * nblk + b;
       if (TYPE == LLMI_TYPE_Q8_0) {
-        const u32x4 c0 = codes[(slot * 2 + 0) * kTileRows + wlane];
-        const u32x4 c1 = codes[(slot * 2 + 1) * kTileRows + wlane];
-        wc[0] = c0.x; wc[1] = c0.y; wc[2] = c0.z; wc[3] = c0.w;
-        wc[4] = c1.x; wc[5] = c1.y; wc[6] = c1.z; wc[7] = c1.w;
+        st.w[0] = codes[(sl * 2 + 0) * kTileRows + wlane];
+        st.w[TYPE == LLMI_TYPE_Q8_0 ? 1 : 0] = codes[(sl * 2 + 1) * kTileRows + wlane];
       } else {
-        const u32x4 c0 = codes[slot * kTileRows + wlane];
-        wc[0] = c0.x; wc[1] = c0.y; wc[2] = c0.z; wc[3] = c0.w;
+        st.w[0] = codes[sl * kTileRows + wlane];
       }
-      wscale = scales[slot * kTileRows + wlane];
+      st.sc = scales[sl * kTileRows + wlane];
     } else {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) wc[i] = 0;
-      wscale = 0.0f;
+      for (int u = 0; u < (TYPE == LLMI_TYPE_Q8_0 ? 2 : 1); ++u) st.w[u] = u32x4{0, 0, 0, 0};
+      st.sc = 0.0f;
     }
   };
 
-  auto lstore = [&]() {
-    uint4* xd = reinterpret_cast<uint4*>(xs + lr * kLdsRow + lh * 32);
-    uint4* wd = reinterpret_cast<uint4*>(ws + lr * kLdsRow + lh * 32);
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      uint4 v;
-      v.x = pack_bf16(xv[8 * q + 0], xv[8 * q + 1]);
-      v.y = pack_bf16(xv[8 * q + 2], xv[8 * q + 3]);
-      v.z = pack_bf16(xv[8 * q + 4], xv[8 * q + 5]);
-      v.w = pack_bf16(xv[8 * q + 6], xv[8 * q + 7]);
-      xd[q] = v;
-    }
+  auto lstore = [&](const Stage<TYPE>& st, int buf) {
+    u32x4* xd = reinterpret_cast<u32x4*>(&xs[buf][xr * kLdsRow + xq * 16]);
+    xd[0] = st.x0;
+    xd[1] = st.x1;
+    u32x4* wd = reinterpret_cast<u32x4*>(&ws[buf][wr * kLdsRow + lh * 32]);
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       float c[8];
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         const int e = 8 * q + i;
-        c[i] = static_cast<float>(TYPE == LLMI_TYPE_Q8_0 ? sbyte(wc[e >> 2], e & 3) : snib(wc[e >> 3], e & 7)) *
-               wscale;
+        const int code = TYPE == LLMI_TYPE_Q8_0 ? sbyte(st.w[e >> 4][(e >> 2) & 3], e & 3)
+                                                : snib(st.w[0][e >> 3], e & 7);
+        c[i] = static_cast<float>(code) * st.sc;
       }
-      uint4 v;
-      v.x = pack_bf16(c[0], c[1]);
-      v.y = pack_bf16(c[2], c[3]);
-      v.z = pack_bf16(c[4], c[5]);
-      v.w = pack_bf16(c[6], c[7]);
-      wd[q] = v;
+      wd[q] = u32x4{pack_bf16(c[0], c[1]), pack_bf16(c[2], c[3]), pack_bf16(c[4], c[5]), pack_bf16(c[6], c[7])};
     }
   };
 
@@ -166,28 +172,43 @@ __global__ void __launch_bounds__(256) qgemm_mfma(const GemmProblem* __restrict_
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-  const int wm0 = (wave >> 1) * 64, wn0 = (wave & 1) * 64;
+  const int wm0 = (wave >> 2) * 64, wn0 = (wave & 3) * 64;
   const int arow = lane & 15, akoff = (lane >> 4) * 8;
 
-  gload(0);
-  for (int k0 = 0; k0 < K; k0 += kBK) {
-    lstore();
-    __syncthreads();
-    if (k0 + kBK < K) gload(k0 + kBK);
+  auto mfma_step = [&](int buf) {
 #pragma unroll
     for (int kk = 0; kk < kBK; kk += 32) {
       bf16x8 a[4], b[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        a[i] = *reinterpret_cast<const bf16x8*>(xs + (wm0 + 16 * i + arow) * kLdsRow + kk + akoff);
+        a[i] = *reinterpret_cast<const bf16x8*>(&xs[buf][(wm0 + 16 * i + arow) * kLdsRow + kk + akoff]);
 #pragma unroll
       for (int j = 0; j < 4; ++j)
-        b[j] = *reinterpret_cast<const bf16x8*>(ws + (wn0 + 16 * j + arow) * kLdsRow + kk + akoff);
+        b[j] = *reinterpret_cast<const bf16x8*>(&ws[buf][(wn0 + 16 * j + arow) * kLdsRow + kk + akoff]);
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
     }
+  };
+
+  // Ring: at step k (even), buffer 0 holds step k, registers B step k + 1
+  // and registers A the loads of step k + 2 in flight; the odd step swaps.
+  Stage<TYPE> A, B;
+  gload(A, 0);
+  if (nk > 1) gload(B, 1);
+  lstore(A, 0);
+  if (nk > 2) gload(A, 2);
+  __syncthreads();
+  for (int k = 0; k < nk; k += 2) {
+    mfma_step(0);
+    if (k + 1 < nk) lstore(B, 1);
+    if (k + 3 < nk) gload(B, k + 3);
+    __syncthreads();
+    if (k + 1 >= nk) break;
+    mfma_step(1);
+    if (k + 2 < nk) lstore(A, 0);
+    if (k + 4 < nk) gload(A, k + 4);
     __syncthreads();
   }
 
@@ -211,8 +232,36 @@ __global__ void __launch_bounds__(256) qgemm_mfma(const GemmProblem* __restrict_
 
 }  // namespace
 
+std::size_t gemm_ldx(std::size_t in) { return (in + kBK - 1) / kBK * kBK; }
+
 int plan_gemm_group(const GroupEntry* entries, std::size_t count, GemmPlan* plan) {
   *plan = GemmPlan{};
+  // Distinct activation matrices, each converted to bf16 once per launch.
+  for (std::size_t i = 0; i < count; ++i) {
+    const GroupEntry& e = entries[i];
+    LLMI_REQUIRE(e.m != nullptr, "gemm: null weight");
+    LLMI_REQUIRE(e.x != nullptr && e.y != nullptr, "gemm: null x or y");
+    const DeviceMatrix& m = *e.m;
+    LLMI_REQUIRE(m.in > 0 && m.in <= 0x7FFFFFFFu && m.out <= 0x7FFFFFFFu, "gemm: bad shape");
+    LLMI_REQUIRE(e.rows <= 0x7FFFFFFFu, "gemm: too many rows");
+    if (e.rows == 0 || m.out == 0) continue;
+    bool seen = false;
+    for (const GemmInput& in : plan->inputs)
+      if (in.x == e.x) {
+        LLMI_REQUIRE(in.rows == e.rows && in.in == m.in, "gemm: one x used with two shapes");
+        seen = true;
+      }
+    if (!seen) {
+      GemmInput in;
+      in.x = e.x;
+      in.rows = e.rows;
+      in.in = m.in;
+      in.ldx = gemm_ldx(m.in);
+      in.offset = plan->scratch_elems;
+      plan->scratch_elems += in.rows * in.ldx;
+      plan->inputs.push_back(in);
+    }
+  }
   for (int type : {LLMI_TYPE_Q8_0, LLMI_TYPE_Q4_0}) {
     GemmLaunch l;
     l.type = type;
@@ -221,24 +270,22 @@ int plan_gemm_group(const GroupEntry* entries, std::size_t count, GemmPlan* plan
     std::size_t wg = 0, nprob = 0;
     for (std::size_t i = 0; i < count; ++i) {
       const GroupEntry& e = entries[i];
-      LLMI_REQUIRE(e.m != nullptr, "gemm: null weight");
-      LLMI_REQUIRE(e.x != nullptr && e.y != nullptr, "gemm: null x or y");
       const DeviceMatrix& m = *e.m;
-      LLMI_REQUIRE(m.in > 0 && m.in <= 0x7FFFFFFFu && m.out <= 0x7FFFFFFFu, "gemm: bad shape");
-      LLMI_REQUIRE(e.rows <= 0x7FFFFFFFu, "gemm: too many rows");
       if (m.type != type || e.rows == 0 || m.out == 0) continue;
       GemmProblem p{};
       p.codes = m.codes;
       p.scales = m.scales;
-      p.x = e.x;
       p.bias = e.bias;
       p.y = e.y;
       p.rows = static_cast<int>(e.rows);
       p.in = static_cast<int>(m.in);
+      p.ldx = static_cast<int>(gemm_ldx(m.in));
       p.out = static_cast<int>(m.out);
       p.nblk = static_cast<int>(m.nblk);
       p.ntiles = static_cast<int>(m.ntiles);
       p.mtiles = static_cast<int>(ceil_div(e.rows, kBM));
+      for (std::size_t j = 0; j < plan->inputs.size(); ++j)
+        if (plan->inputs[j].x == e.x) p.input = static_cast<int>(j);
       const std::size_t ntiles_n = ceil_div(m.out, kBN);
       p.first_wg = static_cast<int>(wg);
       const std::size_t wgs = static_cast<std::size_t>(p.mtiles) * ntiles_n;
@@ -255,6 +302,21 @@ int plan_gemm_group(const GroupEntry* entries, std::size_t count, GemmPlan* plan
   return LLMI_OK;
 }
 
+void bind_gemm_scratch(GemmPlan* plan, std::uint16_t* scratch) {
+  for (GemmProblem& p : plan->probs) p.xb = scratch + plan->inputs[p.input].offset;
+}
+
+int launch_gemm_inputs(const GemmPlan& plan, std::uint16_t* scratch, hipStream_t s) {
+  for (const GemmInput& in : plan.inputs) {
+    const std::size_t quads = in.rows * (in.ldx / 4);
+    const unsigned blocks = static_cast<unsigned>(std::min<std::size_t>(ceil_div(quads, 256), 4096));
+    x_to_bf16<<<blocks, 256, 0, s>>>(in.x, scratch + in.offset, static_cast<int>(in.rows), static_cast<int>(in.in),
+                                     static_cast<int>(in.ldx));
+  }
+  LLMI_TRY_HIP(hipGetLastError());
+  return LLMI_OK;
+}
+
 int launch_gemm(const GemmProblem* probs_dev, const std::uint32_t* map_dev, const GemmLaunch& l, hipStream_t s,
                 const GemmProblem* one) {
   if (l.total_wgs == 0) return LLMI_OK;
@@ -262,9 +324,9 @@ int launch_gemm(const GemmProblem* probs_dev, const std::uint32_t* map_dev, cons
   const std::uint32_t* map = one != nullptr ? nullptr : map_dev + l.map_offset;
   const GemmProblem single = one != nullptr ? *one : GemmProblem{};
   if (l.type == LLMI_TYPE_Q8_0)
-    qgemm_mfma<LLMI_TYPE_Q8_0><<<l.total_wgs, 256, 0, s>>>(probs, map, l.total_wgs, single);
+    qgemm_mfma<LLMI_TYPE_Q8_0><<<l.total_wgs, kGemmThreads, 0, s>>>(probs, map, l.total_wgs, single);
   else
-    qgemm_mfma<LLMI_TYPE_Q4_0><<<l.total_wgs, 256, 0, s>>>(probs, map, l.total_wgs, single);
+    qgemm_mfma<LLMI_TYPE_Q4_0><<<l.total_wgs, kGemmThreads, 0, s>>>(probs, map, l.total_wgs, single);
   LLMI_TRY_HIP(hipGetLastError());
   return LLMI_OK;
 }
