@@ -272,6 +272,48 @@ def decode_runs():
     return res
 
 
+def cpu_decode(runs, max_prompt: int = 128, steps: int = 16):
+    """The reference's own forward_cached (oracle/_ref) on the same synthetic
+    models, as a bounded sample: the first min(prompt, max_prompt) prompt ids,
+    then `steps` greedy steps (checked against the reference's ids when the
+    whole prompt fits); adds cpu_* fields to each run's entry."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+
+    ref = O.reference()
+    use_ref = ref is not None and ref.pool_workers() + 1 <= 16
+    cpu = ref if use_ref else O.oracle()
+    if not use_ref:
+        cpu.set_pool_workers(15)
+    for key, golden, cfg, qt in DECODE_RUNS:
+        with open(os.path.join(ROOT, "tests", "golden", golden + ".json")) as f:
+            rec = json.load(f)
+        tensors = synth.make_tensors(cfg, rec["seed"], rec["convention"])
+        t0 = time.perf_counter()
+        cm = O.CpuModel(cpu, cfg, tensors, qt)
+        load_s = time.perf_counter() - t0
+        del tensors
+        prompt_len = min(rec["n_prompt"], max_prompt)
+        cm.new_cache(prompt_len + steps + 1)
+        prompt = synth.uniform_ids(rec["prompt_seed"], rec["n_prompt"], cfg["vocab_size"])[:prompt_len]
+        t0 = time.perf_counter()
+        logits = cm.forward_cached(prompt)
+        t1 = time.perf_counter()
+        ids = []
+        for _ in range(steps):
+            nxt = int(np.argmax(logits))
+            ids.append(nxt)
+            logits = cm.forward_cached(np.array([nxt], np.int32))
+        t2 = time.perf_counter()
+        cm.close()
+        same = ids == list(rec["ids"][:steps]) if prompt_len == rec["n_prompt"] else None
+        runs[key].update(cpu_kind="reference" if use_ref else "port", cpu_threads=cpu.pool_workers() + 1,
+                         cpu_sample=f"prompt {prompt_len} ids, {steps} greedy steps (load/quantize {load_s:.1f} s)",
+                         cpu_prefill_tok_s=round(prompt_len / (t1 - t0), 1),
+                         cpu_decode_tok_s=round(steps / (t2 - t1), 2), cpu_ids_match=same)
+        print(f"[bench] {key} CPU: decode {steps / (t2 - t1):.2f} tok/s", file=sys.stderr, flush=True)
+
+
 def cpu_baseline(seconds_budget: float = 12.0):
     """The reference's threaded CPU quant::matmul (oracle/_ref, built from the
     reference sources) -- or, where its pool would exceed the 16 host cores
@@ -380,6 +422,8 @@ def main():
     decode = {} if args.no_decode else decode_runs()
     gemm = {} if args.no_gemm else prefill_gemm()
     cpu = None if args.no_cpu else cpu_baseline()
+    if decode and not args.no_cpu:
+        cpu_decode(decode)
 
     line = {
         "metric": METRIC,
