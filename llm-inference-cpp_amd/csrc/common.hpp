@@ -99,8 +99,8 @@ struct GroupEntry {
   float eps = 0.0f;
 };
 // One kernel launch of a group: the products of weight type `type` and row
-// chunk `rchunk`, at probs[prob_offset...], workgroup w running product
-// wg_prob[map_offset + w].
+// chunk `rchunk` (GroupProblem::kNarrow: the 16-row tiles), at
+// probs[prob_offset...], workgroup w running product wg_prob[map_offset + w].
 struct GroupLaunch {
   int type = 0, rchunk = 1, waves = 1, total_wgs = 0;
   std::size_t lds = 0, prob_offset = 0, map_offset = 0;

@@ -333,38 +333,56 @@ __device__ __forceinline__ void wide_tile(const GMEM uint4* __restrict__ codes, 
 // Stages the activations of a 16-row tile in LDS, applying the prologue
 // (see kPlain, kRmsNorm, kSiluUp).  Every thread of the workgroup calls it;
 // it ends with a barrier.
+// Elements each thread loads per round of stage_x: a round's loads are all
+// issued before the first one is used, so a row of `in` activations costs
+// one memory round trip while in <= kStageBatch * blockDim.x.
+constexpr int kStageBatch = 8;
+
 __device__ __forceinline__ void stage_x(const GMEM float* __restrict__ x, int in, int prologue,
                                         const GMEM float* __restrict__ pw, float eps, float* xs) {
-  __shared__ double red[16];
+  __shared__ double red[64];
   __shared__ std::uint64_t tab[32];
   const int tid = threadIdx.x, nthreads = blockDim.x;
-  if (prologue == kSiluUp) {
-    if (tid < 32) tab[tid] = exact::kExp2Tab[tid];
-    __syncthreads();
-    for (int i = tid; i < in; i += nthreads) xs[i] = silu_exact(x[i], tab) * pw[i];
-    __syncthreads();
-    return;
+  const bool one_round = in <= nthreads * kStageBatch;
+  float v[kStageBatch], w[kStageBatch];
+  double part = 0.0;
+  for (int i0 = 0; i0 < in; i0 += nthreads * kStageBatch) {
+#pragma unroll
+    for (int u = 0; u < kStageBatch; ++u) {
+      const int i = i0 + u * nthreads + tid;
+      v[u] = i < in ? x[i] : 0.0f;
+      w[u] = prologue != kPlain && i < in ? pw[i] : 0.0f;
+    }
+    if (prologue == kSiluUp && i0 == 0) {
+      if (tid < 32) tab[tid] = exact::kExp2Tab[tid];
+      __syncthreads();
+    }
+#pragma unroll
+    for (int u = 0; u < kStageBatch; ++u) {
+      const int i = i0 + u * nthreads + tid;
+      if (i < in) {
+        if (prologue == kSiluUp) {
+          xs[i] = silu_exact(v[u], tab) * w[u];
+        } else {
+          xs[i] = v[u];
+          const double d = static_cast<double>(v[u]);
+          part = __builtin_fma(d, d, part);
+        }
+      }
+    }
   }
-  if (prologue == kPlain) {
-    for (int i = tid; i < in; i += nthreads) xs[i] = x[i];
+  if (prologue != kRmsNorm) {
     __syncthreads();
     return;
   }
   // RMSNorm: the double sum of squares in any order, taken when the error
   // bound proves the reference's sequential sum gives the same float scale
   // (else summed sequentially), then y = w * (x * scale).
-  double part = 0.0;
-  for (int i = tid; i < in; i += nthreads) {
-    const float v = x[i];
-    xs[i] = v;
-    const double d = static_cast<double>(v);
-    part = __builtin_fma(d, d, part);
-  }
-  part = wave_sum(part);
-  if ((tid & 63) == 0) red[tid >> 6] = part;
+  part = row_sum16_f64(part);
+  if ((tid & 15) == 15) red[tid >> 4] = part;
   __syncthreads();
   double ss = 0.0;
-  for (int w = 0; w < (nthreads >> 6); ++w) ss += red[w];
+  for (int r = 0; r < (nthreads >> 4); ++r) ss += red[r];
   const double slack = sum_slack(in) * ss;
   float sc = rms_scale(ss, in, eps);
   if (rms_scale(ss - slack, in, eps) != rms_scale(ss + slack, in, eps)) {
@@ -374,10 +392,44 @@ __device__ __forceinline__ void stage_x(const GMEM float* __restrict__ x, int in
       seq = __builtin_fma(d, d, seq);
     }
     sc = rms_scale(seq, in, eps);
+    __syncthreads();  // (uniform branch) xs is read before it is scaled
   }
-  __syncthreads();  // the sequential sum has read xs before it is scaled
-  for (int i = tid; i < in; i += nthreads) xs[i] = pw[i] * (xs[i] * sc);
+  if (one_round) {
+    // This thread's x and w are still in registers.
+#pragma unroll
+    for (int u = 0; u < kStageBatch; ++u) {
+      const int i = u * nthreads + tid;
+      if (i < in) xs[i] = w[u] * (v[u] * sc);
+    }
+  } else {
+    // Each thread scales the elements it staged.
+    for (int i = tid; i < in; i += nthreads) xs[i] = pw[i] * (xs[i] * sc);
+  }
   __syncthreads();
+}
+
+// LDS row stride (floats) of a 16-row tile's (block sum, scale) pairs: nblk
+// pairs rounded up to 16, plus 4 floats, so the 16 rows start 4 banks apart.
+__host__ __device__ __forceinline__ int pair_stride(int nblk) { return 2 * ((nblk + 15) & ~15) + 4; }
+
+// The sequential chain over the (block sum, scale) pairs of one row, two
+// blocks per 16-byte LDS read, eight reads issued per round.
+__device__ __forceinline__ float chain_pairs(const float* row, int nblk) {
+  const float4* pr = reinterpret_cast<const float4*>(row);
+  float acc = 0.0f;
+  int b = 0;
+  for (; b + 16 <= nblk; b += 16) {
+    float4 a[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) a[u] = pr[b / 2 + u];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      acc = __builtin_fmaf(a[u].x, a[u].y, acc);
+      acc = __builtin_fmaf(a[u].z, a[u].w, acc);
+    }
+  }
+  for (; b < nblk; ++b) acc = __builtin_fmaf(row[2 * b], row[2 * b + 1], acc);
+  return acc;
 }
 
 // One 16-row tile (batch 1), for matrices with few rows.  Lane l of a
@@ -387,8 +439,8 @@ __device__ __forceinline__ void stage_x(const GMEM float* __restrict__ x, int in
 // stay coalesced.  The first kHoist blocks of a lane are loaded before the
 // activations are staged (the two round trips overlap).  The activations sit
 // in LDS and are read with broadcast loads (16 lanes per address); block
-// sums and scales go to LDS, and lanes 0-15 run the chain.  LDS: x[in
-// (padded to 4)], part[nblk][16], scale[nblk][16].
+// sums and scales go to LDS as pairs, and lanes 0-15 run the chains.  LDS:
+// x[in (padded to 4)], then 16 rows of pair_stride(nblk) floats.
 template <int TYPE>
 __device__ __forceinline__ void narrow_tile(const GMEM uint4* __restrict__ codes, const GMEM float* __restrict__ scales,
                                             const GMEM float* __restrict__ x, const GMEM float* __restrict__ bias,
@@ -398,8 +450,8 @@ __device__ __forceinline__ void narrow_tile(const GMEM uint4* __restrict__ codes
   constexpr int kHoist = 4;
   const Q4Magic k = q4_magic();
   float* xs = lds;
-  float* part = lds + ((in + 3) & ~3);
-  float* scl = part + nblk * 16;
+  const int stride = pair_stride(nblk);
+  float* pairs = lds + ((in + 3) & ~3);
   const int lane = threadIdx.x & 63;
   const int r = lane & 15;
   const int group = (threadIdx.x >> 6) * 4 + (lane >> 4);
@@ -419,27 +471,37 @@ __device__ __forceinline__ void narrow_tile(const GMEM uint4* __restrict__ codes
       pre_s[j] = loadf<true>(scales + (tile * nblk + b) * kTileRows + sub);
     }
   }
+  // The chain lanes fetch their bias and (accumulating) old y now, so that
+  // the store at the end does not wait for them.  y is this product's
+  // output only, so reading it early is safe.
+  float add = 0.0f, old = 0.0f;
+  const bool owner = threadIdx.x < 16 && row < static_cast<std::size_t>(out);
+  if (owner) {
+    if (bias != nullptr) add = bias[row];
+    if (accumulate) old = y[row];
+  }
   stage_x(x, in, prologue, pw, eps, xs);
+  float2* mine = reinterpret_cast<float2*>(pairs + r * stride);
 #pragma unroll
   for (int j = 0; j < kHoist; ++j) {
     const int b = b_begin + j;
     if (b < b_end) {
-      part[b * 16 + r] = b < nfull ? full_block_dot<TYPE>(pre[j], xs + b * kBlock, k)
+      const float part = b < nfull ? full_block_dot<TYPE>(pre[j], xs + b * kBlock, k)
                                    : tail_block_dot<TYPE>(pre[j], xs + b * kBlock, in - b * kBlock);
-      scl[b * 16 + r] = pre_s[j];
+      mine[b] = make_float2(part, pre_s[j]);
     }
   }
   for (int b = b_begin + kHoist; b < b_end; ++b) {
     const Block<TYPE> blk = load_block<TYPE, true>(codes, tile * nblk + b, sub);
     const float sc = loadf<true>(scales + (tile * nblk + b) * kTileRows + sub);
-    part[b * 16 + r] = b < nfull ? full_block_dot<TYPE>(blk, xs + b * kBlock, k)
+    const float part = b < nfull ? full_block_dot<TYPE>(blk, xs + b * kBlock, k)
                                  : tail_block_dot<TYPE>(blk, xs + b * kBlock, in - b * kBlock);
-    scl[b * 16 + r] = sc;
+    mine[b] = make_float2(part, sc);
   }
   __syncthreads();
-  if (threadIdx.x < 16) {
-    const float acc = chain_lds(part, scl, nblk, r, 16);
-    if (row < static_cast<std::size_t>(out)) store_out(y, row, acc + (bias != nullptr ? bias[row] : 0.0f), accumulate);
+  if (owner) {
+    const float v = chain_pairs(pairs + r * stride, nblk) + add;
+    y[row] = accumulate ? old + v : v;
   }
 }
 
@@ -462,14 +524,14 @@ __global__ void __launch_bounds__(1024) qgemv_narrow(const uint4* __restrict__ c
                                                      const float* __restrict__ x, const float* __restrict__ bias,
                                                      float* __restrict__ y, int in, int nblk, int out, int bpg,
                                                      int accumulate) {
-  extern __shared__ float lds[];
+  extern __shared__ float4 lds4[];  // 16-byte aligned: the chains read float4
   narrow_tile<TYPE>(gmem(codes), gmem(scales), gmem(x), gmem(bias), gmem_out(y), in, nblk, out, bpg, accumulate,
-                    blockIdx.x, lds);
+                    blockIdx.x, reinterpret_cast<float*>(lds4));
 }
 
 // One launch over a group's products that share the weight type and the row
-// chunk R (R == 1 also runs the 16-row tiles).  Workgroup w runs workgroup
-// (w - first_wg) of problem wg_prob[w].
+// chunk R (64-row tiles).  Workgroup w runs workgroup (w - first_wg) of
+// problem wg_prob[w].
 template <int TYPE, int R>
 __global__ void __launch_bounds__(1024) qgemv_group(const GroupProblem* __restrict__ probs,
                                                     const std::uint32_t* __restrict__ wg_prob) {
@@ -482,17 +544,27 @@ __global__ void __launch_bounds__(1024) qgemv_group(const GroupProblem* __restri
   const GMEM uint4* codes = gmem(reinterpret_cast<const uint4*>(p.codes));
   const GMEM float* scales = gmem(p.scales);
   const GMEM float* bias = gmem(p.bias);
-  if (R == 1 && p.kind == GroupProblem::kNarrow) {
-    narrow_tile<TYPE>(codes, scales, gmem(p.x), bias, gmem_out(p.y), p.in, p.nblk, p.out, p.bpw, p.accumulate, local,
-                      lds, p.prologue, gmem(p.pw), p.eps);
-    return;
-  }
   const int tile = local % p.ntiles;
   const int r0 = (local / p.ntiles) * R;
   const int nr = min(R, p.rows - r0);
   const GMEM float* x = gmem(p.x + static_cast<std::size_t>(r0) * p.in);
   GMEM float* y = gmem_out(p.y + static_cast<std::size_t>(r0) * p.out);
   wide_tile<TYPE, R>(codes, scales, x, bias, y, p.in, p.nblk, p.out, nr, p.bpw, p.accumulate, tile, lds);
+}
+
+// The 16-row tiles of a group (batch 1, optional prologue), in a kernel of
+// their own so that their staging registers do not lower the occupancy of
+// qgemv_group.
+template <int TYPE>
+__global__ void __launch_bounds__(1024) qgemv_group_narrow(const GroupProblem* __restrict__ probs,
+                                                           const std::uint32_t* __restrict__ wg_prob) {
+  extern __shared__ float4 lds4[];  // 16-byte aligned: the chains read float4
+  const int wg = blockIdx.x;
+  const int idx = __builtin_amdgcn_readfirstlane(static_cast<int>(wg_prob[wg]));
+  const GroupProblem p = probs[idx];
+  narrow_tile<TYPE>(gmem(reinterpret_cast<const uint4*>(p.codes)), gmem(p.scales), gmem(p.x), gmem(p.bias),
+                    gmem_out(p.y), p.in, p.nblk, p.out, p.bpw, p.accumulate, wg - p.first_wg,
+                    reinterpret_cast<float*>(lds4), p.prologue, gmem(p.pw), p.eps);
 }
 
 // ------------------------------------------------------------ batch > 8
@@ -582,7 +654,10 @@ __global__ void __launch_bounds__(256) qgemv_rows(const uint4* __restrict__ code
 // ------------------------------------------------------------ planning
 // LDS bytes of one workgroup of each kind.
 std::size_t wide_lds(std::size_t nblk, std::size_t nr) { return (nr + 1) * nblk * kTileRows * sizeof(float); }
-std::size_t narrow_lds(std::size_t in, std::size_t nblk) { return (((in + 3) & ~std::size_t{3}) + 2 * nblk * 16) * sizeof(float); }
+std::size_t narrow_lds(std::size_t in, std::size_t nblk) {
+  return (((in + 3) & ~std::size_t{3}) + 16 * static_cast<std::size_t>(pair_stride(static_cast<int>(nblk)))) *
+         sizeof(float);
+}
 
 // LDS a wide workgroup aims to stay within, so that several workgroups share
 // a CU; longer rows may use up to the per-workgroup maximum.
@@ -606,6 +681,14 @@ int wide_waves(std::size_t nblk, int type) {
   return static_cast<int>(std::clamp<std::size_t>(ceil_div(nblk, per), 1, 16));
 }
 
+// Wavefronts of a 16-row tile: about two blocks per lane group (4 groups per
+// wavefront), at most 64 groups.
+int narrow_waves(std::size_t nblk) {
+  constexpr std::size_t kBlocksPerGroup = 2;
+  const std::size_t groups = std::clamp<std::size_t>(ceil_div(nblk, kBlocksPerGroup), 1, 64);
+  return static_cast<int>(ceil_div(groups, 4));
+}
+
 struct TilePlan {
   int kind = 0;  // 0: qgemv_rows; GroupProblem::kNarrow; or the row chunk R of qgemv_tile
   int waves = 1;
@@ -618,14 +701,12 @@ struct TilePlan {
 // the wide tile.
 TilePlan plan_single(const DeviceMatrix& m, std::size_t rows) {
   constexpr std::size_t kNarrowTiles = 128;
-  constexpr std::size_t kBlocksPerGroup = 2;
   const std::size_t nblk = std::max<std::size_t>(m.nblk, 1);
   TilePlan p;
   if (rows > 8) return p;  // qgemv_rows
   if (rows == 1 && m.ntiles < kNarrowTiles && narrow_lds(m.in, nblk) <= max_lds_per_block()) {
     p.kind = GroupProblem::kNarrow;
-    const std::size_t groups = std::min<std::size_t>(64, ceil_div(nblk, kBlocksPerGroup));
-    p.waves = static_cast<int>(ceil_div(groups, 4));
+    p.waves = narrow_waves(nblk);
     p.bpw = static_cast<int>(ceil_div(nblk, static_cast<std::size_t>(p.waves) * 4));
     p.lds = narrow_lds(m.in, nblk);
     return p;
@@ -716,9 +797,8 @@ int plan_group(const GroupEntry* entries, std::size_t count, GroupPlan* plan) {
   // Products are launched by weight type and row chunk R (one kernel
   // instance each).
   for (int type : {LLMI_TYPE_Q8_0, LLMI_TYPE_Q4_0})
-  for (int R : {1, 2, 4, 8}) {
+  for (int R : {int{GroupProblem::kNarrow}, 1, 2, 4, 8}) {
     std::vector<GroupProblem> probs;
-    std::vector<std::size_t> nblks;
     std::size_t biggest = 0;
     int waves = 1;
     for (std::size_t i = 0; i < count; ++i) {
@@ -728,7 +808,7 @@ int plan_group(const GroupEntry* entries, std::size_t count, GroupPlan* plan) {
       const bool fits = narrow_lds(m.in, m.nblk) <= max_lds_per_block();
       const bool narrow = e.rows == 1 && (wide_total < kNarrowBelow || e.prologue != kPlain) && fits;
       LLMI_REQUIRE(e.prologue == kPlain || narrow, "group: a prologue needs batch 1 and in <= ~20k");
-      int r = narrow ? 1 : pick_chunk(e.rows, m.nblk, kLdsTarget);
+      int r = narrow ? int{GroupProblem::kNarrow} : pick_chunk(e.rows, m.nblk, kLdsTarget);
       if (r == 0) r = pick_chunk(1, m.nblk, max_lds_per_block());
       LLMI_REQUIRE(r != 0, "group: rows too long for the grouped GEMV (in above ~10k)");
       if (r != R || m.type != type) continue;
@@ -739,7 +819,7 @@ int plan_group(const GroupEntry* entries, std::size_t count, GroupPlan* plan) {
       p.bias = e.bias;
       p.y = e.y;
       p.type = m.type;
-      p.kind = narrow ? GroupProblem::kNarrow : r;
+      p.kind = r;
       p.in = static_cast<int>(m.in);
       p.nblk = static_cast<int>(m.nblk);
       p.out = static_cast<int>(m.out);
@@ -750,9 +830,12 @@ int plan_group(const GroupEntry* entries, std::size_t count, GroupPlan* plan) {
       p.pw = e.pw;
       p.eps = e.eps;
       probs.push_back(p);
-      // The launch's wavefront count follows its largest product.
+      // The launch's wavefront count: the most any 16-row tile wants, or
+      // what the largest product wants for 64-row tiles.
       const std::size_t bytes = m.code_bytes + m.scale_bytes;
-      if (bytes > biggest) {
+      if (narrow) {
+        waves = std::max(waves, narrow_waves(m.nblk));
+      } else if (bytes > biggest) {
         biggest = bytes;
         waves = wide_waves(m.nblk, m.type);
       }
@@ -796,7 +879,10 @@ int launch_group(const GroupProblem* probs_dev, const std::uint32_t* map_dev, co
   const dim3 grid(static_cast<unsigned>(l.total_wgs)), block(static_cast<unsigned>(l.waves * 64));
   const GroupProblem* probs = probs_dev + l.prob_offset;
   const std::uint32_t* map = map_dev + l.map_offset;
-  if (l.type == LLMI_TYPE_Q8_0) {
+  if (l.rchunk == GroupProblem::kNarrow) {
+    if (l.type == LLMI_TYPE_Q8_0) qgemv_group_narrow<LLMI_TYPE_Q8_0><<<grid, block, l.lds, s>>>(probs, map);
+    else qgemv_group_narrow<LLMI_TYPE_Q4_0><<<grid, block, l.lds, s>>>(probs, map);
+  } else if (l.type == LLMI_TYPE_Q8_0) {
     switch (l.rchunk) {
       case 1: qgemv_group<LLMI_TYPE_Q8_0, 1><<<grid, block, l.lds, s>>>(probs, map); break;
       case 2: qgemv_group<LLMI_TYPE_Q8_0, 2><<<grid, block, l.lds, s>>>(probs, map); break;

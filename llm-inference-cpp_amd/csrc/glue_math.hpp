@@ -39,4 +39,26 @@ __device__ __forceinline__ double wave_sum(double v) {
   return v;
 }
 
+// v of lane l - N within its row of 16 lanes, 0.0 for the first N lanes of
+// the row (DPP row_shr on both halves of the double).
+template <int N>
+__device__ __forceinline__ double row_shr_f64(double v) {
+  const std::uint64_t u = __builtin_bit_cast(std::uint64_t, v);
+  const int lo = __builtin_amdgcn_update_dpp(0, static_cast<int>(u), 0x110 + N, 0xF, 0xF, true);
+  const int hi = __builtin_amdgcn_update_dpp(0, static_cast<int>(u >> 32), 0x110 + N, 0xF, 0xF, true);
+  return __builtin_bit_cast(double, (static_cast<std::uint64_t>(static_cast<std::uint32_t>(hi)) << 32) |
+                                        static_cast<std::uint32_t>(lo));
+}
+
+// Sum of v over each row of 16 lanes, complete in the row's last lane
+// (lanes 15, 31, 47, 63).  The order is a tree; callers use it only where
+// any order of the double additions is acceptable.
+__device__ __forceinline__ double row_sum16_f64(double v) {
+  v = v + row_shr_f64<1>(v);
+  v = v + row_shr_f64<2>(v);
+  v = v + row_shr_f64<4>(v);
+  v = v + row_shr_f64<8>(v);
+  return v;
+}
+
 }  // namespace llmi_hip

@@ -362,16 +362,21 @@ __device__ __forceinline__ float add_row_shl(float v) {
 // table rows of that position.
 template <int NCH>  // head_dim / 16
 __global__ void __launch_bounds__(kThreads) attn_scores_1(const float* __restrict__ q, const float* __restrict__ knew,
-                                                          float* __restrict__ kc, const float* __restrict__ cr,
-                                                          const float* __restrict__ sr, float* __restrict__ scores,
-                                                          int nh, int nkv, int cap, int npos, float scale) {
+                                                          float* __restrict__ kc, const float* __restrict__ cos_t,
+                                                          const float* __restrict__ sin_t, float* __restrict__ scores,
+                                                          int nh, int nkv, int cap, int npos_arg,
+                                                          const int* __restrict__ dev_len, float scale) {
   constexpr int hd = 16 * NCH, half = hd / 2;
   __shared__ float qs[16 * hd];  // the group's query heads (G <= 16)
+  const int npos = dev_len != nullptr ? *dev_len + 1 : npos_arg;
+  const int s0 = blockIdx.x * kScoreTile;
+  if (s0 >= npos) return;  // (grid sized for the cache capacity)
   const int kvh = blockIdx.y;
   const int G = nh / nkv;
   const int j = threadIdx.x & 15, grp = threadIdx.x >> 4;
-  const int s0 = blockIdx.x * kScoreTile;
   const int pos = npos - 1;
+  const float* cr = cos_t + static_cast<std::size_t>(pos) * half;
+  const float* sr = sin_t + static_cast<std::size_t>(pos) * half;
   float* kh = kc + static_cast<std::size_t>(kvh) * cap * hd;
   float kv[kScoreTile / 16][NCH];
 #pragma unroll
@@ -423,40 +428,55 @@ __global__ void __launch_bounds__(kThreads) attn_scores_1(const float* __restric
   }
 }
 
-// Dynamic LDS: p[npad] then vt[16][stride] (stride = npad rounded up to 32,
-// plus 4: consecutive rows start 4 banks apart).  grid (query heads,
-// head_dim / 16): each workgroup runs the softmax of its head (softmax_lds's
-// arithmetic: float max, exact expf with an LDS copy of its table, double sum
-// taken when the error bound proves it rounds like the sequential sum, else
-// summed sequentially) and the P.V chains of 16 output columns.  All of its
-// global loads (the V slice, one float4 per position and quarter, and the
-// head's scores) are issued before any is used.
+// grid (query heads, head_dim / 16), 256 threads.  Each workgroup first
+// issues its loads: the head's scores (registers, positions tid, tid + 256,
+// ...) and the first kPvBatch * 256 float4s of its V slice (positions x 16
+// columns).  While the V loads are in flight it runs the head's softmax on
+// the scores (softmax_lds's arithmetic: float max, exact expf with an LDS
+// copy of its table, double sum taken when the error bound proves it rounds
+// like the sequential sum, else summed sequentially); then it parks p and
+// the transposed V slice in LDS and lanes 0-15 run the P.V chains of the 16
+// columns.  Dynamic LDS: p[npad] then vt[16][npad + 4] (npad = npos rounded
+// up to 32, zero-padded; rows start 4 banks apart).  The padding adds
+// fma(0, 0, acc) = acc: acc starts at +0 and never becomes -0.
 constexpr int kPvCols = 16;
-constexpr int kPvBatch = 8;  // V loads per thread per round
+constexpr int kPvBatch = 16;   // V float4 loads per thread per round (1024 positions)
+constexpr int kPvScores = 10;  // score registers per thread: npos <= 2560
+constexpr int kPvChain = 8;    // float4 reads per operand per chain round
 
-__device__ __forceinline__ int pv_stride(int npad) { return ((npad + 31) & ~31) + 4; }
+__host__ __device__ __forceinline__ int pv_pad(int npos) { return (npos + 31) & ~31; }
+
+__device__ __forceinline__ float row_max16(float v) {
+  // Lanes whose source is outside the row keep their own value.
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), 0x111, 0xF, 0xF, false)));
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), 0x112, 0xF, 0xF, false)));
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), 0x114, 0xF, 0xF, false)));
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), 0x118, 0xF, 0xF, false)));
+  return v;
+}
 
 // The new token's v (vnew) is read in place of cache row npos - 1, and the
 // first head of each group writes its slice of it to the cache.
 template <int NCH>
 __global__ void __launch_bounds__(kThreads) attn_pv_1(const float* __restrict__ scores, const float* __restrict__ vnew,
                                                       float* __restrict__ vc, float* __restrict__ out, int nh, int nkv,
-                                                      int cap, int npos) {
+                                                      int cap, int npos_arg, const int* __restrict__ dev_len) {
   constexpr int hd = 16 * NCH;
-  constexpr int kWaves = kThreads / 64;
+  constexpr int kRows = kThreads / 16;
+  const int npos = dev_len != nullptr ? *dev_len + 1 : npos_arg;
   extern __shared__ float4 pv_lds[];  // 16-byte aligned: the chains read float4
   __shared__ std::uint64_t exp_tab[32];
-  __shared__ float red_f[kWaves];
-  __shared__ double red_d[kWaves];
+  __shared__ float red_f[kRows];
+  __shared__ double red_d[kRows];
   float* lds = reinterpret_cast<float*>(pv_lds);
   const int h = blockIdx.x;
   const int kvh = h / (nh / nkv);
   const int i0 = blockIdx.y * kPvCols;
-  const int npad = (npos + 3) & ~3;
-  const int stride = pv_stride(npad);
+  const int npad = pv_pad(npos);
+  const int stride = npad + 4;
   float* p = lds;
   float* vt = lds + npad;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x;
   if (tid < 32) exp_tab[tid] = exact::kExp2Tab[tid];
 
   const float* vh = vc + static_cast<std::size_t>(kvh) * cap * hd + i0;
@@ -464,10 +484,17 @@ __global__ void __launch_bounds__(kThreads) attn_pv_1(const float* __restrict__ 
   const float* src = scores + static_cast<std::size_t>(h) * cap;
   if (h % (nh / nkv) == 0 && tid < kPvCols)
     vc[(static_cast<std::size_t>(kvh) * cap + npos - 1) * hd + i0 + tid] = vn[tid];
+
+  float sv[kPvScores];
+#pragma unroll
+  for (int u = 0; u < kPvScores; ++u) {
+    const int sp = u * kThreads + tid;
+    sv[u] = sp < npos ? src[sp] : -__builtin_inff();
+  }
+  // V element e: position e / 4, columns 4 * (e % 4) .. + 3 of the slice.
   const int n4 = npad * 4;
-  for (int e0 = 0; e0 < max(n4, npad); e0 += kThreads * kPvBatch) {
-    float4 v[kPvBatch];
-    float sv[kPvBatch];
+  float4 v[kPvBatch];
+  const auto load_v = [&](int e0) {
 #pragma unroll
     for (int u = 0; u < kPvBatch; ++u) {
       const int e = e0 + u * kThreads + tid;
@@ -475,8 +502,9 @@ __global__ void __launch_bounds__(kThreads) attn_pv_1(const float* __restrict__ 
       v[u] = sp < npos - 1 ? *reinterpret_cast<const float4*>(vh + static_cast<std::size_t>(sp) * hd + 4 * (e & 3))
              : sp == npos - 1 ? *reinterpret_cast<const float4*>(vn + 4 * (e & 3))
                               : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-      sv[u] = e < npos ? src[e] : 0.0f;
     }
+  };
+  const auto store_v = [&](int e0) {
 #pragma unroll
     for (int u = 0; u < kPvBatch; ++u) {
       const int e = e0 + u * kThreads + tid;
@@ -487,62 +515,99 @@ __global__ void __launch_bounds__(kThreads) attn_pv_1(const float* __restrict__ 
         vt[(4 * qd + 2) * stride + sp] = v[u].z;
         vt[(4 * qd + 3) * stride + sp] = v[u].w;
       }
-      if (e < npad) p[e] = sv[u];
     }
-  }
-  __syncthreads();
+  };
+  load_v(0);
 
-  // Softmax of p[0..npos): each thread owns positions tid, tid + 256, ...
+  // Softmax while the V loads are in flight.
   float mx = -__builtin_inff();
-  for (int sp = tid; sp < npos; sp += kThreads) mx = fmaxf(mx, p[sp]);
-  mx = wave_max(mx);
-  if (lane == 0) red_f[wave] = mx;
-  __syncthreads();
+#pragma unroll
+  for (int u = 0; u < kPvScores; ++u) mx = fmaxf(mx, sv[u]);
+  mx = row_max16(mx);
+  if ((tid & 15) == 15) red_f[tid >> 4] = mx;
+  __syncthreads();  // red_f and exp_tab
   mx = red_f[0];
 #pragma unroll
-  for (int w = 1; w < kWaves; ++w) mx = fmaxf(mx, red_f[w]);
+  for (int r = 1; r < kRows; ++r) mx = fmaxf(mx, red_f[r]);
   double part = 0.0;
-  for (int sp = tid; sp < npos; sp += kThreads) {
-    const float e = exact::expf_with(p[sp] - mx, exp_tab);
-    p[sp] = e;
-    part += static_cast<double>(e);
+#pragma unroll
+  for (int u = 0; u < kPvScores; ++u) {
+    const int sp = u * kThreads + tid;
+    if (sp < npos) {
+      const float e = exact::expf_with(sv[u] - mx, exp_tab);
+      sv[u] = e;
+      p[sp] = e;
+      part += static_cast<double>(e);
+    }
   }
-  part = wave_sum(part);
-  if (lane == 0) red_d[wave] = part;
-  __syncthreads();
+  part = row_sum16_f64(part);
+  if ((tid & 15) == 15) red_d[tid >> 4] = part;
+  __syncthreads();  // red_d and every e in p
   double sum = red_d[0];
 #pragma unroll
-  for (int w = 1; w < kWaves; ++w) sum = sum + red_d[w];
+  for (int r = 1; r < kRows; ++r) sum = sum + red_d[r];
   const double slack = sum_slack(npos) * sum;
   float inv = recip_float(sum);
   if (recip_float(sum - slack) != recip_float(sum + slack)) {
-    double seq = 0.0;  // every e is in LDS (the barrier above)
+    double seq = 0.0;
     for (int sp = 0; sp < npos; ++sp) seq += static_cast<double>(p[sp]);
     inv = recip_float(seq);
+    __syncthreads();  // (uniform branch) p is read before it is scaled
   }
-  __syncthreads();  // the sequential sum has read p before it is scaled
-  for (int sp = tid; sp < npos; sp += kThreads) p[sp] = p[sp] * inv;
+#pragma unroll
+  for (int u = 0; u < kPvScores; ++u) {
+    const int sp = u * kThreads + tid;
+    if (sp < npos) p[sp] = sv[u] * inv;
+  }
+  for (int sp = npos + tid; sp < npad; sp += kThreads) p[sp] = 0.0f;
+  store_v(0);
+  for (int e0 = kPvBatch * kThreads; e0 < n4; e0 += kPvBatch * kThreads) {
+    load_v(e0);
+    store_v(e0);
+  }
   __syncthreads();
 
   if (tid < kPvCols) {
     const float4* pr = reinterpret_cast<const float4*>(p);
     const float4* vr = reinterpret_cast<const float4*>(vt + static_cast<std::size_t>(tid) * stride);
+    const int nq = npad / 4;  // a multiple of kPvChain
+    float4 pa[kPvChain], va[kPvChain];
+#pragma unroll
+    for (int u = 0; u < kPvChain; ++u) {
+      pa[u] = pr[u];
+      va[u] = vr[u];
+    }
     float acc = 0.0f;
-#pragma unroll 8
-    for (int s4 = 0; s4 < npad / 4; ++s4) {
-      const float4 pp = pr[s4], vv = vr[s4];
-      acc = __builtin_fmaf(pp.x, vv.x, acc);
-      acc = __builtin_fmaf(pp.y, vv.y, acc);
-      acc = __builtin_fmaf(pp.z, vv.z, acc);
-      acc = __builtin_fmaf(pp.w, vv.w, acc);
+    for (int q4 = 0; q4 < nq; q4 += kPvChain) {
+      // The next round's reads are issued before this round's chain (the
+      // last round re-reads its own, unused).
+      const int nx = q4 + kPvChain < nq ? q4 + kPvChain : q4;
+      float4 pb[kPvChain], vb[kPvChain];
+#pragma unroll
+      for (int u = 0; u < kPvChain; ++u) {
+        pb[u] = pr[nx + u];
+        vb[u] = vr[nx + u];
+      }
+#pragma unroll
+      for (int u = 0; u < kPvChain; ++u) {
+        acc = __builtin_fmaf(pa[u].x, va[u].x, acc);
+        acc = __builtin_fmaf(pa[u].y, va[u].y, acc);
+        acc = __builtin_fmaf(pa[u].z, va[u].z, acc);
+        acc = __builtin_fmaf(pa[u].w, va[u].w, acc);
+      }
+#pragma unroll
+      for (int u = 0; u < kPvChain; ++u) {
+        pa[u] = pb[u];
+        va[u] = vb[u];
+      }
     }
     out[static_cast<std::size_t>(h) * hd + i0 + tid] = acc;
   }
 }
 
 std::size_t attn_pv_lds(std::size_t npos) {
-  const std::size_t npad = (npos + 3) & ~std::size_t{3};
-  return (npad + kPvCols * (((npad + 31) & ~std::size_t{31}) + 4)) * sizeof(float);
+  const std::size_t npad = static_cast<std::size_t>(pv_pad(static_cast<int>(npos)));
+  return (npad + kPvCols * (npad + 4)) * sizeof(float);
 }
 
 // The two-kernel decode path applies to one token with head_dim 64 or 128,
@@ -550,21 +615,25 @@ std::size_t attn_pv_lds(std::size_t npos) {
 bool decode_attention_fits(int nh, int nkv, int hd, std::size_t npos) {
   const int G = nh / nkv;
   return (hd == 64 || hd == 128) && G >= 1 && G <= 16 && nh % nkv == 0 &&
-         attn_pv_lds(npos) <= max_lds_per_block();
+         npos <= static_cast<std::size_t>(kPvScores) * kThreads && attn_pv_lds(npos) <= max_lds_per_block();
 }
 
+// npos positions (the new token at npos - 1), or, with dev_len, *dev_len + 1
+// read on the device (launch shapes then cover the cache capacity, so that
+// one recorded launch serves every position).
 void launch_decode_attention(const float* q, const float* knew, const float* vnew, float* kc, float* vc,
-                             const float* cr, const float* sr, float* scores, float* out, int nh, int nkv, int hd,
-                             int cap, int npos, float scale, hipStream_t s) {
-  const dim3 sgrid(static_cast<unsigned>((npos + kScoreTile - 1) / kScoreTile), static_cast<unsigned>(nkv));
+                             const float* cos_t, const float* sin_t, float* scores, float* out, int nh, int nkv,
+                             int hd, int cap, int npos, const int* dev_len, float scale, hipStream_t s) {
+  const int span = dev_len != nullptr ? cap : npos;
+  const dim3 sgrid(static_cast<unsigned>((span + kScoreTile - 1) / kScoreTile), static_cast<unsigned>(nkv));
   const dim3 pgrid(static_cast<unsigned>(nh), static_cast<unsigned>(hd / kPvCols));
-  const std::size_t lds = attn_pv_lds(npos);
+  const std::size_t lds = attn_pv_lds(static_cast<std::size_t>(span));
   if (hd == 64) {
-    attn_scores_1<4><<<sgrid, kThreads, 0, s>>>(q, knew, kc, cr, sr, scores, nh, nkv, cap, npos, scale);
-    attn_pv_1<4><<<pgrid, kThreads, lds, s>>>(scores, vnew, vc, out, nh, nkv, cap, npos);
+    attn_scores_1<4><<<sgrid, kThreads, 0, s>>>(q, knew, kc, cos_t, sin_t, scores, nh, nkv, cap, npos, dev_len, scale);
+    attn_pv_1<4><<<pgrid, kThreads, lds, s>>>(scores, vnew, vc, out, nh, nkv, cap, npos, dev_len);
   } else {
-    attn_scores_1<8><<<sgrid, kThreads, 0, s>>>(q, knew, kc, cr, sr, scores, nh, nkv, cap, npos, scale);
-    attn_pv_1<8><<<pgrid, kThreads, lds, s>>>(scores, vnew, vc, out, nh, nkv, cap, npos);
+    attn_scores_1<8><<<sgrid, kThreads, 0, s>>>(q, knew, kc, cos_t, sin_t, scores, nh, nkv, cap, npos, dev_len, scale);
+    attn_pv_1<8><<<pgrid, kThreads, lds, s>>>(scores, vnew, vc, out, nh, nkv, cap, npos, dev_len);
   }
 }
 
@@ -652,7 +721,9 @@ constexpr int kArgmaxBlocks = 128;
 __global__ void __launch_bounds__(kThreads) argmax_many(const float* __restrict__ x, int n, float* __restrict__ part_v,
                                                         int* __restrict__ part_i, unsigned* __restrict__ counter,
                                                         std::int32_t* __restrict__ out,
-                                                        std::int32_t* __restrict__ also) {
+                                                        std::int32_t* __restrict__ also,
+                                                        std::int32_t* __restrict__ gen = nullptr,
+                                                        int* __restrict__ advance = nullptr) {
   __shared__ float bv[kThreads];
   __shared__ int bi[kThreads];
   __shared__ bool last;
@@ -683,8 +754,22 @@ __global__ void __launch_bounds__(kThreads) argmax_many(const float* __restrict_
     const int idx = r.i < 0 ? 0 : r.i;
     *out = idx;
     if (also != nullptr) *also = idx;
+    if (advance != nullptr) {
+      // Recorded decode steps: advance[0] is the cache length, advance[1]
+      // the next slot of gen.
+      const int k = advance[1];
+      gen[k] = idx;
+      advance[0] = advance[0] + 1;
+      advance[1] = k + 1;
+    }
     __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
+}
+
+// The recorded-step state argmax_many advances: cache length and next slot.
+__global__ void set_advance(int* adv, int len, int slot) {
+  adv[0] = len;
+  adv[1] = slot;
 }
 
 // Standalone glue kernels (the device counterparts of kernels.hpp:13-32).
@@ -744,6 +829,7 @@ struct Workspace {
   float* am_v = nullptr;         // argmax partials and completion counter
   int* am_i = nullptr;
   unsigned* am_count = nullptr;
+  int* adv = nullptr;            // recorded decode steps: cache length, next slot of gen
 };
 
 }  // namespace llmi_hip
@@ -975,7 +1061,7 @@ void free_workspace(Workspace& w) {
                   static_cast<void*>(w.v), static_cast<void*>(w.att), static_cast<void*>(w.g), static_cast<void*>(w.u),
                   static_cast<void*>(w.logits), static_cast<void*>(w.ids), static_cast<void*>(w.next),
                   static_cast<void*>(w.gen), static_cast<void*>(w.am_v), static_cast<void*>(w.am_i),
-                  static_cast<void*>(w.am_count)})
+                  static_cast<void*>(w.am_count), static_cast<void*>(w.adv)})
     if (p != nullptr) (void)hipFree(p);
   w = Workspace{};
 }
@@ -1004,6 +1090,7 @@ int ensure_workspace(llmi_hip_model* m, std::size_t T) {
   if (rc == LLMI_OK) rc = get(&w.am_v, kArgmaxBlocks, 4);
   if (rc == LLMI_OK) rc = get(&w.am_i, kArgmaxBlocks, 4);
   if (rc == LLMI_OK) rc = get(&w.am_count, 1, 4);
+  if (rc == LLMI_OK) rc = get(&w.adv, 2, 4);
   if (rc == LLMI_OK && hipMemsetAsync(w.am_count, 0, sizeof(unsigned), library_stream()) != hipSuccess)
     rc = fail(LLMI_ERR_HIP, "workspace: memset");
   if (rc != LLMI_OK) {
@@ -1017,7 +1104,7 @@ int ensure_workspace(llmi_hip_model* m, std::size_t T) {
 // One token (T = 1) through the fused per-layer launches built by
 // build_decode; the same arithmetic as forward_device.  Logits land in
 // ws.logits.
-int decode_step(llmi_hip_model* m, llmi_hip_cache* cache, hipStream_t s) {
+int decode_step(llmi_hip_model* m, llmi_hip_cache* cache, hipStream_t s, const int* dev_len = nullptr) {
   const auto& c = m->c;
   Workspace& w = m->ws;
   DecodeBuffers& d = m->dec;
@@ -1027,15 +1114,13 @@ int decode_step(llmi_hip_model* m, llmi_hip_cache* cache, hipStream_t s) {
   const float eps = static_cast<float>(c.rms_norm_eps);
   const float scale = 1.0F / std::sqrt(static_cast<float>(m->hd));
   const std::size_t per_layer = static_cast<std::size_t>(c.num_kv_heads) * cache->cap * m->hd;
-  const float* cr = m->cos_t + pos * (m->hd / 2);
-  const float* sr = m->sin_t + pos * (m->hd / 2);
   if (int rc = launch_dequantize_rows(m->embed, w.ids, 1, d.x, s)) return rc;
   for (std::size_t li = 0; li < m->layers.size(); ++li) {
     const DeviceLayer& l = m->layers[li];
     if (int rc = l.qkv.launch(s)) return rc;
-    launch_decode_attention(d.q, d.k, d.v, cache->k + li * per_layer, cache->v + li * per_layer, cr, sr,
+    launch_decode_attention(d.q, d.k, d.v, cache->k + li * per_layer, cache->v + li * per_layer, m->cos_t, m->sin_t,
                             cache->scores, d.att, nh, nkv, hd, static_cast<int>(cache->cap), static_cast<int>(pos + 1),
-                            scale, s);
+                            dev_len, scale, s);
     if (int rc = launch_matmul(l.wo, d.att, 1, nullptr, d.x, s, true)) return rc;
     if (int rc = l.gate_up.launch(s)) return rc;
     if (int rc = l.down_silu.launch(s)) return rc;
@@ -1044,7 +1129,7 @@ int decode_step(llmi_hip_model* m, llmi_hip_cache* cache, hipStream_t s) {
   const DeviceMatrix& head = m->tied ? m->embed : m->lm_head;
   if (int rc = launch_matmul(head, d.h, 1, nullptr, w.logits, s)) return rc;
   LLMI_TRY_HIP(hipGetLastError());
-  cache->len = pos + 1;
+  if (dev_len == nullptr) cache->len = pos + 1;
   return LLMI_OK;
 }
 
@@ -1267,6 +1352,83 @@ int llmi_hip_model_forward_cached(llmi_hip_model* m, llmi_hip_cache* cache, cons
   return llmi_hip_model_forward_cached_trace(m, cache, tokens, n, all_positions, logits, nullptr);
 }
 
+namespace {
+
+// First index in ids[0..count) holding one of the stop ids, or count.
+std::size_t first_stop(const std::int32_t* ids, std::size_t count, const int32_t* stop_ids, std::size_t n_stop) {
+  for (std::size_t i = 0; i < count; ++i)
+    for (std::size_t k = 0; k < n_stop; ++k)
+      if (ids[i] == stop_ids[k]) return i;
+  return count;
+}
+
+// The decode steps of a greedy run after the prefill (whose logits are in
+// ws.logits), with every step recorded once as a HIP graph and replayed:
+// one graph launch per token instead of one host launch per kernel.  The
+// attention kernels read the cache length from ws.adv[0] and the argmax
+// advances it and stores the id at gen[ws.adv[1]], so the same recording
+// serves every step.  With stop ids the host checks the ids every
+// kStopChunk steps; steps run past a stop id are discarded (they cannot
+// change the ids before it).  *produced: ids in ws.gen.
+int generate_recorded(llmi_hip_model* m, llmi_hip_cache* cache, std::size_t n, std::size_t max_new,
+                      const int32_t* stop_ids, std::size_t n_stop, std::size_t* produced) {
+  constexpr std::size_t kStopChunk = 8;
+  Workspace& w = m->ws;
+  hipStream_t s = library_stream();
+  const int V = static_cast<int>(m->V);
+  argmax_many<<<kArgmaxBlocks, kThreads, 0, s>>>(w.logits, V, w.am_v, w.am_i, w.am_count, w.ids, w.gen);
+  set_advance<<<1, 1, 0, s>>>(w.adv, static_cast<int>(n), 1);
+  LLMI_TRY_HIP(hipGetLastError());
+  std::vector<std::int32_t> host(kStopChunk);
+  if (n_stop > 0) {
+    LLMI_TRY_HIP(hipMemcpyAsync(host.data(), w.gen, sizeof(std::int32_t), hipMemcpyDeviceToHost, s));
+    LLMI_TRY_HIP(hipStreamSynchronize(s));
+    if (first_stop(host.data(), 1, stop_ids, n_stop) == 0) {
+      *produced = 1;
+      return LLMI_OK;
+    }
+  }
+  LLMI_TRY_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+  int rc = decode_step(m, cache, s, w.adv);
+  if (rc == LLMI_OK) {
+    argmax_many<<<kArgmaxBlocks, kThreads, 0, s>>>(w.logits, V, w.am_v, w.am_i, w.am_count, w.ids, nullptr, w.gen,
+                                                   w.adv);
+    if (hipGetLastError() != hipSuccess) rc = fail(LLMI_ERR_HIP, "generate: launch while recording");
+  }
+  hipGraph_t graph = nullptr;
+  const hipError_t end = hipStreamEndCapture(s, &graph);
+  if (rc == LLMI_OK && end != hipSuccess) rc = fail(LLMI_ERR_HIP, "generate: hipStreamEndCapture");
+  hipGraphExec_t exec = nullptr;
+  if (rc == LLMI_OK && hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0) != hipSuccess)
+    rc = fail(LLMI_ERR_HIP, "generate: hipGraphInstantiate");
+  std::size_t done = 1;
+  while (rc == LLMI_OK && done < max_new) {
+    const std::size_t chunk = n_stop > 0 ? std::min(kStopChunk, max_new - done) : max_new - done;
+    for (std::size_t i = 0; i < chunk && rc == LLMI_OK; ++i)
+      if (hipGraphLaunch(exec, s) != hipSuccess) rc = fail(LLMI_ERR_HIP, "generate: hipGraphLaunch");
+    if (rc == LLMI_OK && n_stop > 0) {
+      if (hipMemcpyAsync(host.data(), w.gen + done, chunk * sizeof(std::int32_t), hipMemcpyDeviceToHost, s) !=
+              hipSuccess ||
+          hipStreamSynchronize(s) != hipSuccess) {
+        rc = fail(LLMI_ERR_HIP, "generate: reading ids");
+        break;
+      }
+      const std::size_t at = first_stop(host.data(), chunk, stop_ids, n_stop);
+      if (at < chunk) {
+        done += at + 1;
+        break;
+      }
+    }
+    done += chunk;
+  }
+  if (exec != nullptr) (void)hipGraphExecDestroy(exec);
+  if (graph != nullptr) (void)hipGraphDestroy(graph);
+  *produced = done;
+  return rc;
+}
+
+}  // namespace
+
 // transformer.cpp:308-327: prefill once, then one token per step; the argmax
 // runs on the device and feeds the next step's embedding gather directly.
 // Without stop ids nothing waits for the host between steps: the ids collect
@@ -1306,6 +1468,12 @@ int llmi_hip_model_generate_greedy(llmi_hip_model* m, const int32_t* prompt, siz
   LLMI_TRY_HIP(hipEventRecord(ev[1], s));
   const int V = static_cast<int>(m->V);
   std::size_t produced = 0;
+  const int nh = static_cast<int>(m->c.num_heads), nkv = static_cast<int>(m->c.num_kv_heads);
+  if (max_new > 1 && decode_attention_fits(nh, nkv, static_cast<int>(m->hd), cache->cap)) {
+    if (int rc = generate_recorded(m, cache, n, max_new, stop_ids, n_stop, &produced)) return rc;
+    cache->len = n + produced - 1;
+    max_new = 0;  // done: skip the step-by-step loop
+  }
   for (std::size_t step = 0; step < max_new; ++step) {
     argmax_many<<<kArgmaxBlocks, kThreads, 0, s>>>(w.logits, V, w.am_v, w.am_i, w.am_count, w.ids, w.gen + step);
     LLMI_TRY_HIP(hipGetLastError());
