@@ -364,13 +364,10 @@ template <int NCH>  // head_dim / 16
 __global__ void __launch_bounds__(kThreads) attn_scores_1(const float* __restrict__ q, const float* __restrict__ knew,
                                                           float* __restrict__ kc, const float* __restrict__ cos_t,
                                                           const float* __restrict__ sin_t, float* __restrict__ scores,
-                                                          int nh, int nkv, int cap, int npos_arg,
-                                                          const int* __restrict__ dev_len, float scale) {
+                                                          int nh, int nkv, int cap, int npos, float scale) {
   constexpr int hd = 16 * NCH, half = hd / 2;
   __shared__ float qs[16 * hd];  // the group's query heads (G <= 16)
-  const int npos = dev_len != nullptr ? *dev_len + 1 : npos_arg;
   const int s0 = blockIdx.x * kScoreTile;
-  if (s0 >= npos) return;  // (grid sized for the cache capacity)
   const int kvh = blockIdx.y;
   const int G = nh / nkv;
   const int j = threadIdx.x & 15, grp = threadIdx.x >> 4;
@@ -442,7 +439,7 @@ __global__ void __launch_bounds__(kThreads) attn_scores_1(const float* __restric
 constexpr int kPvCols = 16;
 constexpr int kPvBatch = 16;   // V float4 loads per thread per round (1024 positions)
 constexpr int kPvScores = 10;  // score registers per thread: npos <= 2560
-constexpr int kPvChain = 8;    // float4 reads per operand per chain round
+constexpr int kPvChain = 4;    // float4 reads per operand per chain round (8 LDS reads in flight)
 
 __host__ __device__ __forceinline__ int pv_pad(int npos) { return (npos + 31) & ~31; }
 
@@ -460,10 +457,9 @@ __device__ __forceinline__ float row_max16(float v) {
 template <int NCH>
 __global__ void __launch_bounds__(kThreads) attn_pv_1(const float* __restrict__ scores, const float* __restrict__ vnew,
                                                       float* __restrict__ vc, float* __restrict__ out, int nh, int nkv,
-                                                      int cap, int npos_arg, const int* __restrict__ dev_len) {
+                                                      int cap, int npos) {
   constexpr int hd = 16 * NCH;
   constexpr int kRows = kThreads / 16;
-  const int npos = dev_len != nullptr ? *dev_len + 1 : npos_arg;
   extern __shared__ float4 pv_lds[];  // 16-byte aligned: the chains read float4
   __shared__ std::uint64_t exp_tab[32];
   __shared__ float red_f[kRows];
@@ -571,35 +567,39 @@ __global__ void __launch_bounds__(kThreads) attn_pv_1(const float* __restrict__ 
     const float4* pr = reinterpret_cast<const float4*>(p);
     const float4* vr = reinterpret_cast<const float4*>(vt + static_cast<std::size_t>(tid) * stride);
     const int nq = npad / 4;  // a multiple of kPvChain
-    float4 pa[kPvChain], va[kPvChain];
+    // Two register sets, A and B: the reads of one round are issued before
+    // the chain steps of the other, so LDS latency overlaps the chain.
+    float4 pa[kPvChain], va[kPvChain], pb[kPvChain], vb[kPvChain];
+    const auto read = [&](float4* pp, float4* vv, int q) {
 #pragma unroll
-    for (int u = 0; u < kPvChain; ++u) {
-      pa[u] = pr[u];
-      va[u] = vr[u];
-    }
+      for (int u = 0; u < kPvChain; ++u) {
+        pp[u] = pr[q + u];
+        vv[u] = vr[q + u];
+      }
+    };
     float acc = 0.0f;
-    for (int q4 = 0; q4 < nq; q4 += kPvChain) {
-      // The next round's reads are issued before this round's chain (the
-      // last round re-reads its own, unused).
-      const int nx = q4 + kPvChain < nq ? q4 + kPvChain : q4;
-      float4 pb[kPvChain], vb[kPvChain];
+    const auto steps = [&](const float4* pp, const float4* vv) {
 #pragma unroll
       for (int u = 0; u < kPvChain; ++u) {
-        pb[u] = pr[nx + u];
-        vb[u] = vr[nx + u];
+        acc = __builtin_fmaf(pp[u].x, vv[u].x, acc);
+        acc = __builtin_fmaf(pp[u].y, vv[u].y, acc);
+        acc = __builtin_fmaf(pp[u].z, vv[u].z, acc);
+        acc = __builtin_fmaf(pp[u].w, vv[u].w, acc);
       }
-#pragma unroll
-      for (int u = 0; u < kPvChain; ++u) {
-        acc = __builtin_fmaf(pa[u].x, va[u].x, acc);
-        acc = __builtin_fmaf(pa[u].y, va[u].y, acc);
-        acc = __builtin_fmaf(pa[u].z, va[u].z, acc);
-        acc = __builtin_fmaf(pa[u].w, va[u].w, acc);
-      }
-#pragma unroll
-      for (int u = 0; u < kPvChain; ++u) {
-        pa[u] = pb[u];
-        va[u] = vb[u];
-      }
+    };
+    // Every round issues its reads unconditionally (re-reading the last
+    // round when there is no next one), so the number of reads in flight is
+    // the same on every path and the waits before each chain round only
+    // cover that round's own reads.
+    read(pa, va, 0);
+    for (int q4 = 0; q4 < nq; q4 += 2 * kPvChain) {
+      read(pb, vb, q4 + kPvChain < nq ? q4 + kPvChain : q4);
+      __builtin_amdgcn_sched_barrier(0);
+      steps(pa, va);
+      if (q4 + kPvChain >= nq) break;
+      read(pa, va, q4 + 2 * kPvChain < nq ? q4 + 2 * kPvChain : q4);
+      __builtin_amdgcn_sched_barrier(0);
+      steps(pb, vb);
     }
     out[static_cast<std::size_t>(h) * hd + i0 + tid] = acc;
   }
@@ -618,22 +618,19 @@ bool decode_attention_fits(int nh, int nkv, int hd, std::size_t npos) {
          npos <= static_cast<std::size_t>(kPvScores) * kThreads && attn_pv_lds(npos) <= max_lds_per_block();
 }
 
-// npos positions (the new token at npos - 1), or, with dev_len, *dev_len + 1
-// read on the device (launch shapes then cover the cache capacity, so that
-// one recorded launch serves every position).
+// npos positions, the new token at npos - 1.
 void launch_decode_attention(const float* q, const float* knew, const float* vnew, float* kc, float* vc,
                              const float* cos_t, const float* sin_t, float* scores, float* out, int nh, int nkv,
-                             int hd, int cap, int npos, const int* dev_len, float scale, hipStream_t s) {
-  const int span = dev_len != nullptr ? cap : npos;
-  const dim3 sgrid(static_cast<unsigned>((span + kScoreTile - 1) / kScoreTile), static_cast<unsigned>(nkv));
+                             int hd, int cap, int npos, float scale, hipStream_t s) {
+  const dim3 sgrid(static_cast<unsigned>((npos + kScoreTile - 1) / kScoreTile), static_cast<unsigned>(nkv));
   const dim3 pgrid(static_cast<unsigned>(nh), static_cast<unsigned>(hd / kPvCols));
-  const std::size_t lds = attn_pv_lds(static_cast<std::size_t>(span));
+  const std::size_t lds = attn_pv_lds(static_cast<std::size_t>(npos));
   if (hd == 64) {
-    attn_scores_1<4><<<sgrid, kThreads, 0, s>>>(q, knew, kc, cos_t, sin_t, scores, nh, nkv, cap, npos, dev_len, scale);
-    attn_pv_1<4><<<pgrid, kThreads, lds, s>>>(scores, vnew, vc, out, nh, nkv, cap, npos, dev_len);
+    attn_scores_1<4><<<sgrid, kThreads, 0, s>>>(q, knew, kc, cos_t, sin_t, scores, nh, nkv, cap, npos, scale);
+    attn_pv_1<4><<<pgrid, kThreads, lds, s>>>(scores, vnew, vc, out, nh, nkv, cap, npos);
   } else {
-    attn_scores_1<8><<<sgrid, kThreads, 0, s>>>(q, knew, kc, cos_t, sin_t, scores, nh, nkv, cap, npos, dev_len, scale);
-    attn_pv_1<8><<<pgrid, kThreads, lds, s>>>(scores, vnew, vc, out, nh, nkv, cap, npos, dev_len);
+    attn_scores_1<8><<<sgrid, kThreads, 0, s>>>(q, knew, kc, cos_t, sin_t, scores, nh, nkv, cap, npos, scale);
+    attn_pv_1<8><<<pgrid, kThreads, lds, s>>>(scores, vnew, vc, out, nh, nkv, cap, npos);
   }
 }
 
@@ -721,9 +718,7 @@ constexpr int kArgmaxBlocks = 128;
 __global__ void __launch_bounds__(kThreads) argmax_many(const float* __restrict__ x, int n, float* __restrict__ part_v,
                                                         int* __restrict__ part_i, unsigned* __restrict__ counter,
                                                         std::int32_t* __restrict__ out,
-                                                        std::int32_t* __restrict__ also,
-                                                        std::int32_t* __restrict__ gen = nullptr,
-                                                        int* __restrict__ advance = nullptr) {
+                                                        std::int32_t* __restrict__ also) {
   __shared__ float bv[kThreads];
   __shared__ int bi[kThreads];
   __shared__ bool last;
@@ -754,22 +749,8 @@ __global__ void __launch_bounds__(kThreads) argmax_many(const float* __restrict_
     const int idx = r.i < 0 ? 0 : r.i;
     *out = idx;
     if (also != nullptr) *also = idx;
-    if (advance != nullptr) {
-      // Recorded decode steps: advance[0] is the cache length, advance[1]
-      // the next slot of gen.
-      const int k = advance[1];
-      gen[k] = idx;
-      advance[0] = advance[0] + 1;
-      advance[1] = k + 1;
-    }
     __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
-}
-
-// The recorded-step state argmax_many advances: cache length and next slot.
-__global__ void set_advance(int* adv, int len, int slot) {
-  adv[0] = len;
-  adv[1] = slot;
 }
 
 // Standalone glue kernels (the device counterparts of kernels.hpp:13-32).
@@ -829,7 +810,6 @@ struct Workspace {
   float* am_v = nullptr;         // argmax partials and completion counter
   int* am_i = nullptr;
   unsigned* am_count = nullptr;
-  int* adv = nullptr;            // recorded decode steps: cache length, next slot of gen
 };
 
 }  // namespace llmi_hip
@@ -1061,7 +1041,7 @@ void free_workspace(Workspace& w) {
                   static_cast<void*>(w.v), static_cast<void*>(w.att), static_cast<void*>(w.g), static_cast<void*>(w.u),
                   static_cast<void*>(w.logits), static_cast<void*>(w.ids), static_cast<void*>(w.next),
                   static_cast<void*>(w.gen), static_cast<void*>(w.am_v), static_cast<void*>(w.am_i),
-                  static_cast<void*>(w.am_count), static_cast<void*>(w.adv)})
+                  static_cast<void*>(w.am_count)})
     if (p != nullptr) (void)hipFree(p);
   w = Workspace{};
 }
@@ -1090,7 +1070,6 @@ int ensure_workspace(llmi_hip_model* m, std::size_t T) {
   if (rc == LLMI_OK) rc = get(&w.am_v, kArgmaxBlocks, 4);
   if (rc == LLMI_OK) rc = get(&w.am_i, kArgmaxBlocks, 4);
   if (rc == LLMI_OK) rc = get(&w.am_count, 1, 4);
-  if (rc == LLMI_OK) rc = get(&w.adv, 2, 4);
   if (rc == LLMI_OK && hipMemsetAsync(w.am_count, 0, sizeof(unsigned), library_stream()) != hipSuccess)
     rc = fail(LLMI_ERR_HIP, "workspace: memset");
   if (rc != LLMI_OK) {
@@ -1104,7 +1083,7 @@ int ensure_workspace(llmi_hip_model* m, std::size_t T) {
 // One token (T = 1) through the fused per-layer launches built by
 // build_decode; the same arithmetic as forward_device.  Logits land in
 // ws.logits.
-int decode_step(llmi_hip_model* m, llmi_hip_cache* cache, hipStream_t s, const int* dev_len = nullptr) {
+int decode_step(llmi_hip_model* m, llmi_hip_cache* cache, hipStream_t s) {
   const auto& c = m->c;
   Workspace& w = m->ws;
   DecodeBuffers& d = m->dec;
@@ -1120,7 +1099,7 @@ int decode_step(llmi_hip_model* m, llmi_hip_cache* cache, hipStream_t s, const i
     if (int rc = l.qkv.launch(s)) return rc;
     launch_decode_attention(d.q, d.k, d.v, cache->k + li * per_layer, cache->v + li * per_layer, m->cos_t, m->sin_t,
                             cache->scores, d.att, nh, nkv, hd, static_cast<int>(cache->cap), static_cast<int>(pos + 1),
-                            dev_len, scale, s);
+                            scale, s);
     if (int rc = launch_matmul(l.wo, d.att, 1, nullptr, d.x, s, true)) return rc;
     if (int rc = l.gate_up.launch(s)) return rc;
     if (int rc = l.down_silu.launch(s)) return rc;
@@ -1129,7 +1108,7 @@ int decode_step(llmi_hip_model* m, llmi_hip_cache* cache, hipStream_t s, const i
   const DeviceMatrix& head = m->tied ? m->embed : m->lm_head;
   if (int rc = launch_matmul(head, d.h, 1, nullptr, w.logits, s)) return rc;
   LLMI_TRY_HIP(hipGetLastError());
-  if (dev_len == nullptr) cache->len = pos + 1;
+  cache->len = pos + 1;
   return LLMI_OK;
 }
 
@@ -1352,83 +1331,6 @@ int llmi_hip_model_forward_cached(llmi_hip_model* m, llmi_hip_cache* cache, cons
   return llmi_hip_model_forward_cached_trace(m, cache, tokens, n, all_positions, logits, nullptr);
 }
 
-namespace {
-
-// First index in ids[0..count) holding one of the stop ids, or count.
-std::size_t first_stop(const std::int32_t* ids, std::size_t count, const int32_t* stop_ids, std::size_t n_stop) {
-  for (std::size_t i = 0; i < count; ++i)
-    for (std::size_t k = 0; k < n_stop; ++k)
-      if (ids[i] == stop_ids[k]) return i;
-  return count;
-}
-
-// The decode steps of a greedy run after the prefill (whose logits are in
-// ws.logits), with every step recorded once as a HIP graph and replayed:
-// one graph launch per token instead of one host launch per kernel.  The
-// attention kernels read the cache length from ws.adv[0] and the argmax
-// advances it and stores the id at gen[ws.adv[1]], so the same recording
-// serves every step.  With stop ids the host checks the ids every
-// kStopChunk steps; steps run past a stop id are discarded (they cannot
-// change the ids before it).  *produced: ids in ws.gen.
-int generate_recorded(llmi_hip_model* m, llmi_hip_cache* cache, std::size_t n, std::size_t max_new,
-                      const int32_t* stop_ids, std::size_t n_stop, std::size_t* produced) {
-  constexpr std::size_t kStopChunk = 8;
-  Workspace& w = m->ws;
-  hipStream_t s = library_stream();
-  const int V = static_cast<int>(m->V);
-  argmax_many<<<kArgmaxBlocks, kThreads, 0, s>>>(w.logits, V, w.am_v, w.am_i, w.am_count, w.ids, w.gen);
-  set_advance<<<1, 1, 0, s>>>(w.adv, static_cast<int>(n), 1);
-  LLMI_TRY_HIP(hipGetLastError());
-  std::vector<std::int32_t> host(kStopChunk);
-  if (n_stop > 0) {
-    LLMI_TRY_HIP(hipMemcpyAsync(host.data(), w.gen, sizeof(std::int32_t), hipMemcpyDeviceToHost, s));
-    LLMI_TRY_HIP(hipStreamSynchronize(s));
-    if (first_stop(host.data(), 1, stop_ids, n_stop) == 0) {
-      *produced = 1;
-      return LLMI_OK;
-    }
-  }
-  LLMI_TRY_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
-  int rc = decode_step(m, cache, s, w.adv);
-  if (rc == LLMI_OK) {
-    argmax_many<<<kArgmaxBlocks, kThreads, 0, s>>>(w.logits, V, w.am_v, w.am_i, w.am_count, w.ids, nullptr, w.gen,
-                                                   w.adv);
-    if (hipGetLastError() != hipSuccess) rc = fail(LLMI_ERR_HIP, "generate: launch while recording");
-  }
-  hipGraph_t graph = nullptr;
-  const hipError_t end = hipStreamEndCapture(s, &graph);
-  if (rc == LLMI_OK && end != hipSuccess) rc = fail(LLMI_ERR_HIP, "generate: hipStreamEndCapture");
-  hipGraphExec_t exec = nullptr;
-  if (rc == LLMI_OK && hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0) != hipSuccess)
-    rc = fail(LLMI_ERR_HIP, "generate: hipGraphInstantiate");
-  std::size_t done = 1;
-  while (rc == LLMI_OK && done < max_new) {
-    const std::size_t chunk = n_stop > 0 ? std::min(kStopChunk, max_new - done) : max_new - done;
-    for (std::size_t i = 0; i < chunk && rc == LLMI_OK; ++i)
-      if (hipGraphLaunch(exec, s) != hipSuccess) rc = fail(LLMI_ERR_HIP, "generate: hipGraphLaunch");
-    if (rc == LLMI_OK && n_stop > 0) {
-      if (hipMemcpyAsync(host.data(), w.gen + done, chunk * sizeof(std::int32_t), hipMemcpyDeviceToHost, s) !=
-              hipSuccess ||
-          hipStreamSynchronize(s) != hipSuccess) {
-        rc = fail(LLMI_ERR_HIP, "generate: reading ids");
-        break;
-      }
-      const std::size_t at = first_stop(host.data(), chunk, stop_ids, n_stop);
-      if (at < chunk) {
-        done += at + 1;
-        break;
-      }
-    }
-    done += chunk;
-  }
-  if (exec != nullptr) (void)hipGraphExecDestroy(exec);
-  if (graph != nullptr) (void)hipGraphDestroy(graph);
-  *produced = done;
-  return rc;
-}
-
-}  // namespace
-
 // transformer.cpp:308-327: prefill once, then one token per step; the argmax
 // runs on the device and feeds the next step's embedding gather directly.
 // Without stop ids nothing waits for the host between steps: the ids collect
@@ -1468,12 +1370,6 @@ int llmi_hip_model_generate_greedy(llmi_hip_model* m, const int32_t* prompt, siz
   LLMI_TRY_HIP(hipEventRecord(ev[1], s));
   const int V = static_cast<int>(m->V);
   std::size_t produced = 0;
-  const int nh = static_cast<int>(m->c.num_heads), nkv = static_cast<int>(m->c.num_kv_heads);
-  if (max_new > 1 && decode_attention_fits(nh, nkv, static_cast<int>(m->hd), cache->cap)) {
-    if (int rc = generate_recorded(m, cache, n, max_new, stop_ids, n_stop, &produced)) return rc;
-    cache->len = n + produced - 1;
-    max_new = 0;  // done: skip the step-by-step loop
-  }
   for (std::size_t step = 0; step < max_new; ++step) {
     argmax_many<<<kArgmaxBlocks, kThreads, 0, s>>>(w.logits, V, w.am_v, w.am_i, w.am_count, w.ids, w.gen + step);
     LLMI_TRY_HIP(hipGetLastError());
