@@ -42,6 +42,10 @@ enum { LLMI_TYPE_F32 = 0, LLMI_TYPE_Q8_0 = 1, LLMI_TYPE_Q4_0 = 2 };
 /* Weights per quantization block (include/llmi/model/quant.hpp:15). */
 #define LLMI_BLOCK_SIZE 32
 
+/* GGUF tensor types accepted by llmi_hip_weight_from_gguf: the values of
+ * llmi::gguf::TensorType (include/llmi/model/gguf.hpp:26-34). */
+enum { LLMI_GGUF_Q4_0 = 2, LLMI_GGUF_Q8_0 = 8 };
+
 /* Model hyper-parameters: the fields of llmi::ModelConfig
  * (include/llmi/model/model.hpp:21-36) that the forward pass reads.
  * head_dim = hidden_size / num_heads (src/model/model.cpp:100-105). */
@@ -135,6 +139,19 @@ int llmi_hip_weight_upload(const uint8_t* data, const float* scales, size_t out,
 int llmi_hip_weight_quantize(const float* w, size_t out, size_t in, int type, llmi_hip_weight** weight);
 int llmi_hip_weight_quantize_dev(const float* w_dev, size_t out, size_t in, int type, llmi_hip_weight** weight);
 int llmi_hip_weight_free(llmi_hip_weight* weight);
+/* Replaces llmi::gguf::to_quantized (include/llmi/model/gguf.hpp:184,
+ * src/model/gguf.cpp:577-640) followed by the upload: `blocks` (host) is a
+ * GGUF tensor's raw data, nbytes long, out rows of in/32 ggml blocks
+ * ({fp16 d; codes}, 34 bytes for Q8_0, 18 for Q4_0).  The device converts
+ * each block into the layout llmi_hip_weight_upload produces from the
+ * reference's own QuantizedMatrix (fp16 scale -> fp32 exactly; Q4_0's
+ * halves-of-the-block nibble pairing re-packed into neighbour pairs), so
+ * downloading the result gives to_quantized's data and scales bit for bit.
+ * Fails (LLMI_ERR_ARG) where to_quantized fails: a type other than Q8_0 /
+ * Q4_0, an empty shape, in not a multiple of 32, or nbytes not matching the
+ * shape. */
+int llmi_hip_weight_from_gguf(const void* blocks, size_t nbytes, size_t out, size_t in, int gguf_type,
+                              llmi_hip_weight** weight);
 /* Copies the weight back into the reference's planar layout. */
 int llmi_hip_weight_download(const llmi_hip_weight* weight, uint8_t* data, float* scales);
 /* Shape/type queries; byte_size is QuantizedMatrix::byte_size

@@ -357,6 +357,50 @@ int llmi_hip_weight_upload(const uint8_t* data, const float* scales, size_t out,
   return LLMI_OK;
 }
 
+int llmi_hip_weight_from_gguf(const void* blocks, size_t nbytes, size_t out, size_t in, int gguf_type,
+                              llmi_hip_weight** weight) {
+  LLMI_REQUIRE_INIT();
+  LLMI_REQUIRE(weight != nullptr, "weight_from_gguf: null out-pointer");
+  *weight = nullptr;
+  int type = 0;
+  std::size_t block_bytes = 0;  // the 2-byte fp16 scale + the packed codes
+  switch (gguf_type) {
+    case LLMI_GGUF_Q8_0:
+      type = LLMI_TYPE_Q8_0;
+      block_bytes = 2 + kBlock;
+      break;
+    case LLMI_GGUF_Q4_0:
+      type = LLMI_TYPE_Q4_0;
+      block_bytes = 2 + kBlock / 2;
+      break;
+    default:
+      return fail(LLMI_ERR_ARG, "weight_from_gguf: tensor type is not Q8_0/Q4_0");
+  }
+  LLMI_REQUIRE(out > 0 && in > 0, "weight_from_gguf: out*in does not match its element count");
+  LLMI_REQUIRE(in % kBlock == 0, "weight_from_gguf: in is not a multiple of the block size (32)");
+  LLMI_REQUIRE(in <= 0x7FFFFFFFu && out <= (std::size_t{1} << 40) / in, "weight_from_gguf: shape too large");
+  LLMI_REQUIRE(nbytes == out * (in / kBlock) * block_bytes,
+               "weight_from_gguf: unexpected byte size for its declared shape");
+  LLMI_REQUIRE(blocks != nullptr, "weight_from_gguf: null blocks");
+  auto h = std::make_unique<llmi_hip_weight>();
+  if (int rc = alloc_matrix(out, in, type, &h->m)) {
+    free_matrix(&h->m);
+    return rc;
+  }
+  DevBuf raw;
+  int rc = raw.alloc(nbytes);
+  if (rc == LLMI_OK && hipMemcpyAsync(raw.p, blocks, nbytes, hipMemcpyHostToDevice, g_stream) != hipSuccess)
+    rc = fail(LLMI_ERR_HIP, "weight_from_gguf: copy");
+  if (rc == LLMI_OK) rc = launch_gguf_to_tiled(raw.p, h->m, g_stream);
+  if (rc == LLMI_OK && hipStreamSynchronize(g_stream) != hipSuccess) rc = fail(LLMI_ERR_HIP, "weight_from_gguf: sync");
+  if (rc != LLMI_OK) {
+    free_matrix(&h->m);
+    return rc;
+  }
+  *weight = h.release();
+  return LLMI_OK;
+}
+
 int llmi_hip_weight_quantize_dev(const float* w, size_t out, size_t in, int type, llmi_hip_weight** weight) {
   LLMI_REQUIRE_INIT();
   if (const int rc = check_type(type)) return rc;

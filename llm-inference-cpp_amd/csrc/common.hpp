@@ -169,6 +169,8 @@ int launch_quantize(const float* w, std::size_t out, std::size_t in, int type, s
 int launch_relayout_to_tiled(const std::uint8_t* planar_data, const float* planar_scales, const DeviceMatrix& m,
                              hipStream_t s);
 int launch_relayout_to_planar(const DeviceMatrix& m, std::uint8_t* planar_data, float* planar_scales, hipStream_t s);
+// GGUF (ggml) Q8_0 / Q4_0 blocks of m's shape (device memory) -> m.
+int launch_gguf_to_tiled(const void* raw, const DeviceMatrix& m, hipStream_t s);
 int launch_dequantize_rows(const DeviceMatrix& m, const std::int32_t* ids, std::size_t n, float* dst, hipStream_t s);
 // accumulate: y[r][o] = y[r][o] + (acc + bias) -- the reference's
 // `proj = W x; x += proj` residual update (transformer.cpp:283-284, :291-292)

@@ -132,6 +132,81 @@ __global__ void __launch_bounds__(256) planar_to_tiled(const std::uint8_t* __res
   tscales[slot * kTileRows + lane] = pscales[r * nblk + b];
 }
 
+// IEEE binary16 -> binary32, exactly, as integer operations (src/model/
+// safetensors.cpp:249-273 maps the same way: subnormals normalised, the
+// infinities and NaNs keep their payload bits unchanged).
+__device__ __forceinline__ float half_bits_to_float(std::uint32_t h) {
+  const std::uint32_t sign = (h & 0x8000u) << 16;
+  const std::uint32_t e = (h >> 10) & 0x1Fu;
+  const std::uint32_t m = h & 0x3FFu;
+  std::uint32_t bits;
+  if (e == 0) {
+    if (m == 0) {
+      bits = sign;
+    } else {
+      const int top = 31 - __builtin_clz(m);  // leading one of the mantissa, 0..9: value 2^(top - 24) * 1.f
+      bits = sign | (static_cast<std::uint32_t>(top + 103) << 23) | ((m << (23 - top)) & 0x7FFFFFu);
+    }
+  } else if (e == 0x1F) {
+    bits = sign | 0x7F800000u | (m << 13);
+  } else {
+    bits = sign | ((e + 112u) << 23) | (m << 13);
+  }
+  return __uint_as_float(bits);
+}
+
+// GGUF (ggml) blocks -> tiled device layout, one block per thread
+// (gguf.cpp:577-640, to_quantized).  A ggml block is {fp16 d; codes}:
+// Q8_0 34 bytes, its 32 signed codes in element order (copied as they are);
+// Q4_0 18 bytes, byte j holding element j in the low nibble and element
+// j + 16 in the high nibble, re-packed here into this library's pairs of
+// neighbours (byte k: element 2k low, 2k + 1 high).  Blocks start 2-byte
+// aligned (both sizes are even), so they are read as 16-bit words.
+template <int TYPE>
+__global__ void __launch_bounds__(256) gguf_to_tiled(const std::uint16_t* __restrict__ raw, std::size_t out, int nblk,
+                                                     std::uint8_t* __restrict__ tcodes,
+                                                     float* __restrict__ tscales) {
+  const std::size_t gid = static_cast<std::size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (gid >= out * static_cast<std::size_t>(nblk)) return;
+  const std::size_t r = gid / nblk;
+  const int b = static_cast<int>(gid % nblk);
+  constexpr int kHalfwords = TYPE == LLMI_TYPE_Q4_0 ? 9 : 17;
+  const std::uint16_t* src = raw + gid * kHalfwords;
+  std::uint32_t word[TYPE == LLMI_TYPE_Q4_0 ? 4 : 8];
+  if (TYPE == LLMI_TYPE_Q8_0) {
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+      word[k] = static_cast<std::uint32_t>(src[1 + 2 * k]) | (static_cast<std::uint32_t>(src[2 + 2 * k]) << 16);
+  } else {
+    std::uint8_t q[16];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      q[2 * k] = static_cast<std::uint8_t>(src[1 + k] & 0xFFu);
+      q[2 * k + 1] = static_cast<std::uint8_t>(src[1 + k] >> 8);
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) word[k] = 0u;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      const int e0 = 2 * k, e1 = 2 * k + 1;  // elements of engine byte k
+      const std::uint32_t n0 = e0 < 16 ? (q[e0] & 0xFu) : (q[e0 - 16] >> 4);
+      const std::uint32_t n1 = e1 < 16 ? (q[e1] & 0xFu) : (q[e1 - 16] >> 4);
+      word[k / 4] |= (n0 | (n1 << 4)) << (8 * (k % 4));
+    }
+  }
+  const std::size_t tile = r / kTileRows;
+  const int lane = static_cast<int>(r % kTileRows);
+  const std::size_t slot = tile * nblk + b;
+  uint4* dst = reinterpret_cast<uint4*>(tcodes);
+  if (TYPE == LLMI_TYPE_Q4_0) {
+    dst[slot * kTileRows + lane] = make_uint4(word[0], word[1], word[2], word[3]);
+  } else {
+    dst[(slot * 2 + 0) * kTileRows + lane] = make_uint4(word[0], word[1], word[2], word[3]);
+    dst[(slot * 2 + 1) * kTileRows + lane] = make_uint4(word[4], word[5], word[6], word[7]);
+  }
+  tscales[slot * kTileRows + lane] = half_bits_to_float(src[0]);
+}
+
 // Tiled device layout -> planar (reference) layout, one block per thread.
 template <int TYPE>
 __global__ void __launch_bounds__(256) tiled_to_planar(const std::uint8_t* __restrict__ tcodes,
@@ -220,6 +295,20 @@ int launch_relayout_to_tiled(const std::uint8_t* pdata, const float* pscales, co
     planar_to_tiled<LLMI_TYPE_Q8_0><<<g, 256, 0, s>>>(pdata, pscales, m.out, static_cast<int>(m.in), static_cast<int>(m.nblk), m.codes, m.scales);
   } else {
     planar_to_tiled<LLMI_TYPE_Q4_0><<<g, 256, 0, s>>>(pdata, pscales, m.out, static_cast<int>(m.in), static_cast<int>(m.nblk), m.codes, m.scales);
+  }
+  LLMI_TRY_HIP(hipGetLastError());
+  return LLMI_OK;
+}
+
+int launch_gguf_to_tiled(const void* raw, const DeviceMatrix& m, hipStream_t s) {
+  const std::size_t work = m.out * m.nblk;
+  if (work == 0) return LLMI_OK;
+  const unsigned g = grid_for(work, 256);
+  const auto* src = static_cast<const std::uint16_t*>(raw);
+  if (m.type == LLMI_TYPE_Q8_0) {
+    gguf_to_tiled<LLMI_TYPE_Q8_0><<<g, 256, 0, s>>>(src, m.out, static_cast<int>(m.nblk), m.codes, m.scales);
+  } else {
+    gguf_to_tiled<LLMI_TYPE_Q4_0><<<g, 256, 0, s>>>(src, m.out, static_cast<int>(m.nblk), m.codes, m.scales);
   }
   LLMI_TRY_HIP(hipGetLastError());
   return LLMI_OK;

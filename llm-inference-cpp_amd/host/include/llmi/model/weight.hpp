@@ -12,6 +12,7 @@
 #include <vector>
 
 #include "llmi/model/quant.hpp"
+#include "llmi/util/result.hpp"
 
 struct llmi_hip_weight;
 
@@ -24,6 +25,12 @@ class Weight {
   static Weight quantized(const std::vector<float>& w, std::size_t out, std::size_t in, quant::Type type);
   // A Weight of an already quantized matrix (e.g. from a GGUF file).
   static Weight from_quantized(const quant::QuantizedMatrix& m);
+  // gguf::to_quantized (src/model/gguf.cpp:577-640) done on the device: the
+  // raw bytes of a GGUF Q8_0 / Q4_0 tensor (gguf_type 8 / 2, the values of
+  // gguf::TensorType) of shape [out][in] go to HBM as they are and are
+  // converted there.  Fails where to_quantized fails (type, shape, size).
+  static Result<Weight> from_gguf(const void* raw, std::size_t nbytes, std::size_t out, std::size_t in,
+                                  int gguf_type);
 
   [[nodiscard]] bool empty() const;
   [[nodiscard]] std::size_t byte_size() const;

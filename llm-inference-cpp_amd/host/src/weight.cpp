@@ -55,6 +55,20 @@ Weight Weight::from_quantized(const quant::QuantizedMatrix& m) {
   return weight;
 }
 
+Result<Weight> Weight::from_gguf(const void* raw, std::size_t nbytes, std::size_t out, std::size_t in,
+                                 int gguf_type) {
+  quant::init_for_host_api();
+  llmi_hip_weight* h = nullptr;
+  if (llmi_hip_weight_from_gguf(raw, nbytes, out, in, gguf_type, &h) != LLMI_OK)
+    return fail(std::string("gguf: to_quantized: ") + llmi_hip_last_error());
+  Weight weight;
+  weight.type_ = gguf_type == LLMI_GGUF_Q8_0 ? quant::Type::Q8_0 : quant::Type::Q4_0;
+  weight.out_ = out;
+  weight.in_ = in;
+  weight.dev_ = own(h);
+  return weight;
+}
+
 bool Weight::empty() const { return dev_ == nullptr || out_ == 0 || in_ == 0; }
 
 std::size_t Weight::byte_size() const {

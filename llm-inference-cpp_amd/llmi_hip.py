@@ -17,6 +17,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libllmi_hip.so")
 
 F32, Q8_0, Q4_0 = 0, 1, 2
+GGUF_Q4_0, GGUF_Q8_0 = 2, 8  # GGUF tensor types (LLMI_GGUF_*)
 BLOCK = 32
 TYPE_NAMES = {F32: "f32", Q8_0: "q8_0", Q4_0: "q4_0"}
 
@@ -51,6 +52,7 @@ SIGNATURES = {
     "llmi_hip_weight_quantize": (_i, [_vp, _sz, _sz, _i, C.POINTER(_vp)]),
     "llmi_hip_weight_quantize_dev": (_i, [_vp, _sz, _sz, _i, C.POINTER(_vp)]),
     "llmi_hip_weight_free": (_i, [_vp]),
+    "llmi_hip_weight_from_gguf": (_i, [_vp, _sz, _sz, _sz, _i, C.POINTER(_vp)]),
     "llmi_hip_weight_download": (_i, [_vp, _vp, _vp]),
     "llmi_hip_weight_info": (_i, [_vp, C.POINTER(_sz), C.POINTER(_sz), C.POINTER(_i), C.POINTER(_sz)]),
     "llmi_hip_weight_device_bytes": (_sz, [_vp]),
@@ -194,6 +196,15 @@ class Weight:
         h = C.c_void_p()
         check(lib.llmi_hip_weight_upload(_p(np.ascontiguousarray(data)), _p(np.ascontiguousarray(scales)), out, n_in,
                                          qtype, C.byref(h)))
+        return cls(h.value, lib)
+
+    @classmethod
+    def from_gguf(cls, blocks: np.ndarray, out: int, n_in: int, gguf_type: int) -> "Weight":
+        """A GGUF Q8_0/Q4_0 tensor's raw blocks (uint8) -> device weight."""
+        lib = init()
+        h = C.c_void_p()
+        raw = np.ascontiguousarray(blocks, dtype=np.uint8)
+        check(lib.llmi_hip_weight_from_gguf(_p(raw), raw.nbytes, out, n_in, gguf_type, C.byref(h)))
         return cls(h.value, lib)
 
     @classmethod

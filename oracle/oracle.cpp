@@ -502,6 +502,89 @@ bool forward_cached(Model& m, const std::int32_t* tokens, std::size_t T, bool al
   return true;
 }
 
+// ------------------------------------------------------------ GGUF blocks
+// src/model/safetensors.cpp:249-273 (half_to_float): IEEE binary16 ->
+// binary32; zero keeps its sign, subnormals are normalised, infinities and
+// NaNs keep their payload bits.
+float half_to_float(std::uint16_t h) {
+  const std::uint32_t sign = static_cast<std::uint32_t>(h & 0x8000U) << 16U;
+  const std::uint32_t e = (h >> 10U) & 0x1FU;
+  std::uint32_t m = h & 0x3FFU;
+  std::uint32_t bits = sign;
+  if (e == 0x1FU) {
+    bits |= 0x7F800000U | (m << 13U);
+  } else if (e != 0) {
+    bits |= ((e + 112U) << 23U) | (m << 13U);
+  } else if (m != 0) {
+    // value m * 2^-24: shift the leading one up to bit 10.
+    std::uint32_t exp32 = 113;  // biased exponent of 2^-14
+    while ((m & 0x400U) == 0) {
+      m <<= 1U;
+      --exp32;
+    }
+    bits |= (exp32 << 23U) | ((m & 0x3FFU) << 13U);
+  }
+  float f;
+  std::memcpy(&f, &bits, 4);
+  return f;
+}
+
+// src/model/gguf.cpp:577-640 (to_quantized), the checks in its order, then
+// each ggml block {fp16 d; codes} into the engine layout: the scale through
+// half_to_float; Q8_0 codes in order; Q4_0 byte j of the block holds element
+// j (low nibble) and element j + 16 (high nibble), and each element's nibble
+// (code + 8) goes to the engine's neighbour pairs (even element low nibble).
+// gtype: GGUF tensor type (2 = Q4_0, 8 = Q8_0).  Returns false with a
+// message on the reference's failure cases.
+bool gguf_to_quantized(const std::uint8_t* raw, std::size_t nbytes, std::size_t out, std::size_t in, int gtype,
+                       std::uint8_t* data, float* scales, std::string* err) {
+  int type = 0;
+  std::size_t qbytes = 0;
+  if (gtype == 8) {
+    type = kQ8;
+    qbytes = kBlock;
+  } else if (gtype == 2) {
+    type = kQ4;
+    qbytes = kBlock / 2;
+  } else {
+    *err = "not Q8_0/Q4_0";
+    return false;
+  }
+  if (out == 0 || in == 0) {
+    *err = "out*in does not match its element count";
+    return false;
+  }
+  if (in % kBlock != 0) {
+    *err = "in is not a multiple of the block size";
+    return false;
+  }
+  const std::size_t bpr = in / kBlock, bb = 2 + qbytes;
+  if (nbytes != out * bpr * bb) {
+    *err = "unexpected byte size for its declared shape";
+    return false;
+  }
+  const std::size_t rb = row_bytes(in, type);
+  std::memset(data, 0, out * rb);
+  for (std::size_t r = 0; r < out; ++r) {
+    for (std::size_t b = 0; b < bpr; ++b) {
+      const std::uint8_t* blk = raw + (r * bpr + b) * bb;
+      scales[r * bpr + b] = half_to_float(static_cast<std::uint16_t>(blk[0] | (blk[1] << 8U)));
+      std::uint8_t* row = data + r * rb;
+      if (type == kQ8) {
+        std::memcpy(row + b * kBlock, blk + 2, kBlock);
+        continue;
+      }
+      for (std::size_t e = 0; e < kBlock; ++e) {
+        const std::uint8_t byte = blk[2 + (e % 16)];
+        const std::uint8_t nib = e < 16 ? (byte & 0x0FU) : static_cast<std::uint8_t>(byte >> 4U);
+        const std::size_t idx = b * kBlock + e;
+        row[idx / 2] |= static_cast<std::uint8_t>(idx % 2 == 0 ? nib : nib << 4U);
+      }
+    }
+  }
+  return true;
+}
+
 }  // namespace oracle
 
 namespace {
@@ -511,6 +594,10 @@ thread_local std::string g_err;
 extern "C" {
 
 const char* oracle_last_error() { return g_err.c_str(); }
+int oracle_gguf_to_quantized(const std::uint8_t* raw, std::size_t nbytes, std::size_t out, std::size_t in, int gtype,
+                             std::uint8_t* data, float* scales) {
+  return oracle::gguf_to_quantized(raw, nbytes, out, in, gtype, data, scales, &g_err) ? 0 : 1;
+}
 std::size_t oracle_row_bytes(std::size_t in, int type) { return oracle::row_bytes(in, type); }
 
 void oracle_quantize(const float* w, std::size_t out, std::size_t in, int type, std::uint8_t* data, float* scales) {

@@ -104,6 +104,8 @@ class Cpu:
         self._greedy.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_size_t, C.c_void_p, C.c_void_p]
         self._err = f("last_error")
         self._err.restype = C.c_char_p
+        self._gguf = f("gguf_to_quantized")
+        self._gguf.argtypes = [C.c_void_p, C.c_size_t, C.c_size_t, C.c_size_t, C.c_int, C.c_void_p, C.c_void_p]
 
     def last_error(self) -> str:
         return self._err().decode()
@@ -122,6 +124,18 @@ class Cpu:
         scales = np.zeros(out * nblocks(n_in), dtype=np.float32)
         self._quantize(_p(w), out, n_in, qtype, _p(data), _p(scales))
         return data, scales
+
+    def gguf_to_quantized(self, raw: np.ndarray, out: int, n_in: int, gguf_type: int):
+        """gguf::to_quantized on one tensor's raw ggml blocks (gguf.cpp:577-640):
+        (data, scales) in the engine layout; ValueError with the message
+        where the reference fails."""
+        raw = np.ascontiguousarray(raw, dtype=np.uint8)
+        qtype = Q8_0 if gguf_type == 8 else Q4_0
+        data = np.zeros(max(1, out * row_bytes(n_in, qtype)), dtype=np.uint8)
+        scales = np.zeros(max(1, out * nblocks(n_in)), dtype=np.float32)
+        if self._gguf(_p(raw), raw.nbytes, out, n_in, gguf_type, _p(data), _p(scales)) != 0:
+            raise ValueError(self.last_error())
+        return data[:out * row_bytes(n_in, qtype)], scales[:out * nblocks(n_in)]
 
     def dequantize_row(self, data, scales, out: int, n_in: int, qtype: int, row: int) -> np.ndarray:
         dst = np.zeros(n_in, dtype=np.float32)

@@ -18,6 +18,7 @@
 #include <vector>
 
 #include "../include/llmi_hip.h"
+#include "llmi/model/gguf.hpp"
 #include "llmi/model/kernels.hpp"
 #include "llmi/model/model.hpp"
 #include "llmi/model/quant.hpp"
@@ -228,6 +229,50 @@ int ref_generate_greedy_cached(void* m, const std::int32_t* prompt, std::size_t 
     const std::int32_t next = ids[step];
     if (ref_model_forward_cached(m, &next, 1, 0, logits.data()) != 0) return 1;
   }
+  return 0;
+}
+
+// The reference's gguf::to_quantized (gguf.cpp:577-640) on one tensor "w"
+// of type gtype and shape [out][in], given its raw blocks: a minimal GGUF v3
+// image (no metadata, one tensor at offset 0, default alignment 32) is
+// parsed with GGUFFile::parse and converted.  Returns 0, or 1 with the
+// reference's error message.
+int ref_gguf_to_quantized(const std::uint8_t* raw, std::size_t nbytes, std::size_t out, std::size_t in, int gtype,
+                          std::uint8_t* data, float* scales) {
+  std::vector<std::byte> img;
+  const auto put = [&](std::uint64_t v, int n) {
+    for (int k = 0; k < n; ++k) img.push_back(static_cast<std::byte>((v >> (8 * k)) & 0xFFU));
+  };
+  for (char c : {'G', 'G', 'U', 'F'}) img.push_back(static_cast<std::byte>(c));
+  put(3, 4);           // version
+  put(1, 8);           // tensors
+  put(0, 8);           // metadata entries
+  put(1, 8);           // name length
+  img.push_back(static_cast<std::byte>('w'));
+  put(2, 4);           // dimensions, fastest first
+  put(in, 8);
+  put(out, 8);
+  put(static_cast<std::uint64_t>(gtype), 4);
+  put(0, 8);           // offset in the data section
+  while (img.size() % 32 != 0) img.push_back(std::byte{0});
+  for (std::size_t i = 0; i < nbytes; ++i) img.push_back(static_cast<std::byte>(raw[i]));
+  auto f = llmi::gguf::GGUFFile::parse(img);
+  if (!f) {
+    g_err = f.error();
+    return 1;
+  }
+  const auto* t = f->find("w");
+  if (t == nullptr) {
+    g_err = "tensor w not found";
+    return 1;
+  }
+  auto m = llmi::gguf::to_quantized(*f, *t, out, in);
+  if (!m) {
+    g_err = m.error();
+    return 1;
+  }
+  std::memcpy(data, m->data.data(), m->data.size());
+  std::memcpy(scales, m->scales.data(), m->scales.size() * sizeof(float));
   return 0;
 }
 

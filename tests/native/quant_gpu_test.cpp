@@ -6,6 +6,7 @@
 #include "check.hpp"
 #include "llmi/model/quant.hpp"
 #include "llmi/model/weight.hpp"
+#include "llmi_hip.h"
 
 extern "C" {
 void oracle_quantize(const float* w, std::size_t out, std::size_t in, int type, std::uint8_t* data, float* scales);
@@ -161,6 +162,27 @@ TEST(Weight, QuantizedWeightMatchesTheQuantFunctionsAndSharesDeviceMemory) {
     again.matmul(x.data(), 2, in, out, nullptr, y2.data());
     EXPECT_TRUE(std::memcmp(y.data(), y2.data(), y.size() * 4) == 0);
   }
+}
+
+// gguf_test.cpp:389-416 and :418-453 through Weight::from_gguf (the device
+// does gguf::to_quantized): one Q8_0 block (scale 1.0, codes 0..31 in order)
+// and one Q4_0 block (scale 2.0, byte 0 = 0x91: element 0 nibble 1, element
+// 16 nibble 9).
+TEST(Weight, FromGgufMatchesTheReferenceKnownAnswers) {
+  std::vector<std::uint8_t> q8 = {0x00, 0x3C};
+  for (int i = 0; i < 32; ++i) q8.push_back(static_cast<std::uint8_t>(i));
+  auto w8 = llmi::Weight::from_gguf(q8.data(), q8.size(), 1, 32, LLMI_GGUF_Q8_0);
+  EXPECT_TRUE(w8.ok());
+  std::vector<float> row(32);
+  w8->row(0, 32, row.data());
+  for (int i = 0; i < 32; ++i) EXPECT_TRUE(row[static_cast<std::size_t>(i)] == static_cast<float>(i));
+  std::vector<std::uint8_t> q4 = {0x00, 0x40, 0x91};
+  for (int i = 1; i < 16; ++i) q4.push_back(0x88);
+  auto w4 = llmi::Weight::from_gguf(q4.data(), q4.size(), 1, 32, LLMI_GGUF_Q4_0);
+  EXPECT_TRUE(w4.ok());
+  w4->row(0, 32, row.data());
+  EXPECT_TRUE(row[0] == -14.0F && row[16] == 2.0F && row[1] == 0.0F && row[17] == 0.0F);
+  EXPECT_TRUE(!llmi::Weight::from_gguf(q4.data(), q4.size(), 1, 32, 0).ok());  // F32 is not Q8_0/Q4_0
 }
 
 TEST(Weight, Float32WeightsAreRejected) {
