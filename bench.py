@@ -179,6 +179,34 @@ QWEN_LAYER = [("q_proj", 896, 896), ("k_proj", 128, 896), ("v_proj", 128, 896), 
 MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense bf16
 
 
+def gguf_upload(reps=3):
+    """GGUF -> device: the raw ggml blocks of a Qwen2.5
+    lm_head-shaped tensor (151936x896) -> device weight through
+    llmi_hip_weight_from_gguf, Q4_0 and Q8_0.  Wall time of the call: the
+    host-to-device copy of the raw blocks (pageable memory) plus the
+    conversion kernel; best of `reps`."""
+    out, n_in = 151936, 896
+    nb = out * n_in // 32
+    rng = np.random.default_rng(5)
+    res = {"tensor": f"{out}x{n_in}", "timing": "wall clock of the call, PCIe copy included"}
+    for gt, name, qb in ((H.GGUF_Q4_0, "q4_0", 16), (H.GGUF_Q8_0, "q8_0", 32)):
+        raw = rng.integers(0, 256, size=(nb, 2 + qb), dtype=np.uint8)
+        sc = np.abs(rng.normal(0.0, 0.002, nb)).astype(np.float16).view(np.uint16)
+        raw[:, 0] = (sc & 0xFF).astype(np.uint8)
+        raw[:, 1] = (sc >> 8).astype(np.uint8)
+        raw = raw.reshape(-1)
+        best = float("inf")
+        for _ in range(reps):
+            H.synchronize()
+            t0 = time.perf_counter()
+            w = H.Weight.from_gguf(raw, out, n_in, gt)
+            best = min(best, time.perf_counter() - t0)
+            w.free()
+        res[name] = {"raw_bytes": int(raw.nbytes), "ms": round(best * 1e3, 2),
+                     "gbs": round(raw.nbytes / best / 1e9, 2)}
+    return res
+
+
 def prefill_gemm(steps=20, warmup=3):
     """M=512 tokens of fp32 activations against
     every Qwen2.5-0.5B linear layer (24 layers x 7 products) in Q8_0, on the
@@ -378,7 +406,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
-              "the multi-GPU design is described in DESIGN.md", file=sys.stderr)
+              "it has no multi-GPU path to measure", file=sys.stderr)
         sys.exit(2)
 
     H.init(0)
@@ -421,6 +449,7 @@ def main():
     targets = {} if args.no_targets else target_shapes()
     decode = {} if args.no_decode else decode_runs()
     gemm = {} if args.no_gemm else prefill_gemm()
+    gguf = gguf_upload()
     cpu = None if args.no_cpu else cpu_baseline()
     if decode and not args.no_cpu:
         cpu_decode(decode)
@@ -471,6 +500,7 @@ def main():
         "targets_qwen25": targets,
         "decode": decode,
         "prefill_gemm_c5": gemm,
+        "gguf_to_device": gguf,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -1,7 +1,8 @@
 """CPU test: the C++ layer builds inside the reference engine -- with the
 reference's own headers (ModelConfig, Model, SafetensorsFile, TokenId) and
 the reference's Transformer::load(const Model&, quant::Type) signature --
-as INTEGRATION.md describes.  Skipped where the reference is not present."""
+the way a maintainer adds it to the reference's build.  Skipped where the
+reference is not present."""
 
 import os
 import subprocess
