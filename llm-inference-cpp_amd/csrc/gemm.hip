@@ -10,16 +10,19 @@
 //
 // x is first converted to bf16 once (x_to_bf16: rows padded to a multiple of
 // 64 with zeros), so the GEMM reads half the activation bytes and never
-// converts them again.  One workgroup (8 wavefronts) computes a 128 (tokens)
-// x 256 (outputs) tile of y; wavefront w owns the 64 x 64 block (w / 4, w % 4)
-// as 4 x 4 MFMA tiles of 16 x 16.  Per K-step of 64 (two quantization blocks)
-// the workgroup stages 128 x 64 activations and 256 x 64 dequantized weights
-// (code * scale, rounded to bf16) in LDS, double-buffered: while the MFMAs of
-// step k read one buffer, the threads dequantize step k + 1 (already in
-// registers) into the other and issue the global loads of step k + 3, so the
-// loads have two steps to arrive; one barrier per step.  LDS rows are padded
-// by 16 bytes so that the 16-byte operand reads of 8 consecutive lanes hit
-// distinct banks.
+// converts them again.  One workgroup computes a 128 (tokens) x 256 (outputs)
+// tile of y with 12 wavefronts in two roles.  Wavefronts 0..7 run the MFMAs:
+// wavefront w owns the 64 x 64 block (w / 4, w % 4) as 4 x 4 MFMA tiles of
+// 16 x 16.  Wavefronts 8..11 produce: per K-step of 64 (two quantization
+// blocks) they stage 128 x 64 activations and 256 x 64 dequantized weights
+// (code * scale, rounded to bf16) into one of two LDS buffers while the MFMA
+// wavefronts read the other, and issue the global loads two steps ahead; one
+// barrier per step, so a step costs the longer of the two sides, not their
+// sum.  The producers' loads are unconditional (clamped addresses, the
+// scale of a block past the row's end taken as 0): a load behind a
+// per-lane branch makes the compiler wait for every load in flight.  LDS
+// rows are padded by 16 bytes so that the 16-byte operand reads of 8
+// consecutive lanes hit distinct banks.
 //
 // Products are launched as groups (one kernel for many products; a single
 // product is passed by value): workgroup w first maps to a work index so that
@@ -38,7 +41,7 @@ namespace {
 #define GMEM __attribute__((address_space(1)))
 
 constexpr int kBM = 128, kBN = 256, kBK = 64;
-constexpr int kGemmThreads = 512;
+constexpr int kGemmThreads = 768;  // 8 MFMA wavefronts + 4 producers
 constexpr int kLdsRow = kBK + 8;  // bf16 per LDS row (16 bytes of padding)
 constexpr int kXcds = 8;
 
@@ -76,14 +79,23 @@ __global__ void __launch_bounds__(256) x_to_bf16(const float* __restrict__ x, st
   }
 }
 
-// Raw data of one K-step held by one thread: 16 activations (bf16) of row
-// t/4, and the 32 codes + scale of row t/2, block t%2.
+// Raw data of one K-step held by one producer thread: 32 activations (bf16)
+// of row pt/2, columns 32*(pt%2)..+31, and the codes + scales of weight row
+// pt's two quantization blocks; live[h]: block h exists (else its scale
+// counts as 0).
 template <int TYPE>
 struct Stage {
-  u32x4 x0, x1;
-  u32x4 w[TYPE == LLMI_TYPE_Q8_0 ? 2 : 1];
-  float sc;
+  u32x4 x[4];
+  u32x4 w[TYPE == LLMI_TYPE_Q8_0 ? 4 : 2];
+  float sc[2];
+  bool live[2];
 };
+
+// Wavefronts 0..7 run the MFMAs, 8..11 produce: per K-step the producers
+// load (two steps ahead), dequantize and store the next step's tiles into
+// one LDS buffer while the MFMA wavefronts read the other; one barrier per
+// step, so a step costs the longer of the two sides rather than their sum.
+constexpr int kMfmaWaves = 8;
 
 template <int TYPE>
 __global__ void __launch_bounds__(kGemmThreads) qgemm_mfma(const GemmProblem* __restrict__ probs,
@@ -106,66 +118,82 @@ __global__ void __launch_bounds__(kGemmThreads) qgemm_mfma(const GemmProblem* __
   const int m0 = mt * kBM, n0 = nt * kBN;
   const int M = p.rows, N = p.out, nblk = p.nblk, ldx = p.ldx;
   const int nk = (p.in + kBK - 1) / kBK;
-  const GMEM u32x4* xb = (const GMEM u32x4*)p.xb;
-  const GMEM u32x4* codes = (const GMEM u32x4*)p.codes;
-  const GMEM float* scales = (const GMEM float*)p.scales;
 
   const int t = threadIdx.x;
-  const int lane = t & 63, wave = t >> 6;
-  // Staging map: activations row t/4, 16 values from column 16*(t%4);
-  // weights row t/2, quantization block t%2 of the step.
-  const int xr = t >> 2, xq = t & 3;
-  const int wr = t >> 1, lh = t & 1;
-  const int wrow = n0 + wr;
-  const int wtile = wrow / kTileRows, wlane = wrow % kTileRows;
-  const bool xrow_ok = m0 + xr < M;
-  const bool wrow_ok = wtile < p.ntiles;
-  // u32x4 index of this thread's activations at step 0.
-  const std::size_t xbase = (static_cast<std::size_t>(m0 + xr) * ldx + xq * 16) / 8;
+  const int lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
 
-  auto gload = [&](Stage<TYPE>& st, int k) {
-    if (xrow_ok) {
-      st.x0 = xb[xbase + static_cast<std::size_t>(k) * (kBK / 8)];
-      st.x1 = xb[xbase + static_cast<std::size_t>(k) * (kBK / 8) + 1];
-    } else {
-      st.x0 = st.x1 = u32x4{0, 0, 0, 0};
-    }
-    const int b = 2 * k + lh;
-    if (wrow_ok && b < nblk) {
-      const std::size_t sl = static_cast<std::size_t>(wtile) * nblk + b;
-      if (TYPE == LLMI_TYPE_Q8_0) {
-        st.w[0] = codes[(sl * 2 + 0) * kTileRows + wlane];
-        st.w[TYPE == LLMI_TYPE_Q8_0 ? 1 : 0] = codes[(sl * 2 + 1) * kTileRows + wlane];
-      } else {
-        st.w[0] = codes[sl * kTileRows + wlane];
+  if (wave >= kMfmaWaves) {
+    // ------------------------------------------------------------ producer
+    const GMEM u32x4* xb = (const GMEM u32x4*)p.xb;
+    const GMEM u32x4* codes = (const GMEM u32x4*)p.codes;
+    const GMEM float* scales = (const GMEM float*)p.scales;
+    const int pt = t - kMfmaWaves * 64;
+    const int xr = pt >> 1, xh = pt & 1;
+    // Every load is issued unconditionally from an address inside the
+    // operands (rows past M or N are clamped to the last one; their results
+    // are never stored), so no load sits behind a branch and the loads of
+    // later steps stay in flight.
+    const int wrow = min(n0 + pt, p.ntiles * kTileRows - 1);
+    const int wtile = wrow / kTileRows, wlane = wrow % kTileRows;
+    const std::size_t xbase = (static_cast<std::size_t>(min(m0 + xr, M - 1)) * ldx + xh * 32) / 8;
+    const auto gload = [&](Stage<TYPE>& st, int k) {
+      k = min(k, nk - 1);  // the ring's prefetch past the last step re-reads it
+#pragma unroll
+      for (int u = 0; u < 4; ++u) st.x[u] = xb[xbase + static_cast<std::size_t>(k) * (kBK / 8) + u];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        st.live[h] = 2 * k + h < nblk;
+        const std::size_t sl = static_cast<std::size_t>(wtile) * nblk + min(2 * k + h, nblk - 1);
+        if constexpr (TYPE == LLMI_TYPE_Q8_0) {
+          st.w[2 * h] = codes[(sl * 2 + 0) * kTileRows + wlane];
+          st.w[2 * h + 1] = codes[(sl * 2 + 1) * kTileRows + wlane];
+        } else {
+          st.w[h] = codes[sl * kTileRows + wlane];
+        }
+        st.sc[h] = scales[sl * kTileRows + wlane];
       }
-      st.sc = scales[sl * kTileRows + wlane];
-    } else {
+    };
+    const auto lstore = [&](const Stage<TYPE>& st, int buf) {
+      u32x4* xd = reinterpret_cast<u32x4*>(&xs[buf][xr * kLdsRow + xh * 32]);
 #pragma unroll
-      for (int u = 0; u < (TYPE == LLMI_TYPE_Q8_0 ? 2 : 1); ++u) st.w[u] = u32x4{0, 0, 0, 0};
-      st.sc = 0.0f;
-    }
-  };
-
-  auto lstore = [&](const Stage<TYPE>& st, int buf) {
-    u32x4* xd = reinterpret_cast<u32x4*>(&xs[buf][xr * kLdsRow + xq * 16]);
-    xd[0] = st.x0;
-    xd[1] = st.x1;
-    u32x4* wd = reinterpret_cast<u32x4*>(&ws[buf][wr * kLdsRow + lh * 32]);
+      for (int u = 0; u < 4; ++u) xd[u] = st.x[u];
+      u32x4* wd = reinterpret_cast<u32x4*>(&ws[buf][pt * kLdsRow]);
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      float c[8];
+      for (int q = 0; q < 8; ++q) {  // 8 elements each; q / 4 = the block
+        const int h = q >> 2;
+        float c[8];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int e = 8 * q + i;
-        const int code = TYPE == LLMI_TYPE_Q8_0 ? sbyte(st.w[e >> 4][(e >> 2) & 3], e & 3)
-                                                : snib(st.w[0][e >> 3], e & 7);
-        c[i] = static_cast<float>(code) * st.sc;
+        for (int i = 0; i < 8; ++i) {
+          const int e = 8 * (q & 3) + i;  // element within block h
+          int code;
+          if constexpr (TYPE == LLMI_TYPE_Q8_0) code = sbyte(st.w[2 * h + (e >> 4)][(e >> 2) & 3], e & 3);
+          else code = snib(st.w[h][e >> 3], e & 7);
+          c[i] = static_cast<float>(code) * (st.live[h] ? st.sc[h] : 0.0f);
+        }
+        wd[q] = u32x4{pack_bf16(c[0], c[1]), pack_bf16(c[2], c[3]), pack_bf16(c[4], c[5]), pack_bf16(c[6], c[7])};
       }
-      wd[q] = u32x4{pack_bf16(c[0], c[1]), pack_bf16(c[2], c[3]), pack_bf16(c[4], c[5]), pack_bf16(c[6], c[7])};
+    };
+    // Ring: step k's data is in A for even k, B for odd k.
+    Stage<TYPE> A, B;
+    gload(A, 0);
+    gload(B, 1);
+    lstore(A, 0);
+    gload(A, 2);
+    __syncthreads();
+    for (int k = 0; k < nk; k += 2) {
+      if (k + 1 < nk) lstore(B, 1);
+      gload(B, k + 3);
+      __syncthreads();
+      if (k + 1 >= nk) break;
+      if (k + 2 < nk) lstore(A, 0);
+      gload(A, k + 4);
+      __syncthreads();
     }
-  };
+    return;
+  }
 
+  // -------------------------------------------------------------- MFMA
   f32x4 acc[4][4];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
@@ -175,7 +203,7 @@ __global__ void __launch_bounds__(kGemmThreads) qgemm_mfma(const GemmProblem* __
   const int wm0 = (wave >> 2) * 64, wn0 = (wave & 3) * 64;
   const int arow = lane & 15, akoff = (lane >> 4) * 8;
 
-  auto mfma_step = [&](int buf) {
+  const auto mfma_step = [&](int buf) {
 #pragma unroll
     for (int kk = 0; kk < kBK; kk += 32) {
       bf16x8 a[4], b[4];
@@ -192,23 +220,12 @@ __global__ void __launch_bounds__(kGemmThreads) qgemm_mfma(const GemmProblem* __
     }
   };
 
-  // Ring: at step k (even), buffer 0 holds step k, registers B step k + 1
-  // and registers A the loads of step k + 2 in flight; the odd step swaps.
-  Stage<TYPE> A, B;
-  gload(A, 0);
-  if (nk > 1) gload(B, 1);
-  lstore(A, 0);
-  if (nk > 2) gload(A, 2);
-  __syncthreads();
+  __syncthreads();  // step 0 staged
   for (int k = 0; k < nk; k += 2) {
     mfma_step(0);
-    if (k + 1 < nk) lstore(B, 1);
-    if (k + 3 < nk) gload(B, k + 3);
     __syncthreads();
     if (k + 1 >= nk) break;
     mfma_step(1);
-    if (k + 2 < nk) lstore(A, 0);
-    if (k + 4 < nk) gload(A, k + 4);
     __syncthreads();
   }
 
