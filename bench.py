@@ -296,8 +296,36 @@ def decode_runs():
                         ids_match_reference=bool(np.array_equal(ids, np.array(rec["ids"], np.int32))))
         print(f"[bench] {key}: prefill {pre_ms:.1f} ms, decode {tok_s:.1f} tok/s, ids match "
               f"{res[key]['ids_match_reference']}", file=sys.stderr, flush=True)
+        if cfg["vocab_size"] > 100000:
+            res[key]["perplexity_chunk"] = perplexity_chunk(m, prompt, cfg)
         m.free()
     return res
+
+
+def perplexity_chunk(m, prompt, cfg, reps=3):
+    """llmi-perplexity's scoring of one 512-token chunk from position 256
+    (the app's default), through llmi_hip_model_chunk_nll: exact, with the
+    bf16-MFMA lm_head, and with every linear on the bf16-MFMA GEMM; wall
+    clock per chunk, scored tokens/s, and each fast mode's largest per-token
+    NLL difference from the exact one."""
+    n, first = 512, 256
+    ids = prompt[:n] if len(prompt) >= n else synth.uniform_ids(9, n, cfg["vocab_size"])
+    out = {"tokens": n, "scored": n - 1 - first}
+    nll = {}
+    for name, head in (("exact", H.SCORE_EXACT), ("mfma_head", H.SCORE_MFMA_HEAD), ("mfma", H.SCORE_MFMA)):
+        m.chunk_nll(ids, first, head)  # warm-up
+        best = float("inf")
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            nll[name] = m.chunk_nll(ids, first, head)
+            best = min(best, time.perf_counter() - t0)
+        out[name] = {"ms": round(best * 1e3, 2), "scored_tok_s": round((n - 1 - first) / best, 1),
+                     "mean_nll": round(float(nll[name].mean()), 6)}
+    for name in ("mfma_head", "mfma"):
+        out[name]["max_abs_nll_diff"] = round(float(np.abs(nll[name] - nll["exact"]).max()), 6)
+    print(f"[bench] perplexity chunk: exact {out['exact']['ms']} ms, mfma head {out['mfma_head']['ms']} ms, "
+          f"all-mfma {out['mfma']['ms']} ms", file=sys.stderr, flush=True)
+    return out
 
 
 def cpu_decode(runs, max_prompt: int = 128, steps: int = 16):

@@ -280,6 +280,24 @@ int llmi_hip_model_forward_cached_trace(llmi_hip_model* model, llmi_hip_cache* c
  * stop_ids.  Writes *n_ids ids to `ids` (room for max_new). */
 int llmi_hip_model_generate_greedy(llmi_hip_model* model, const int32_t* prompt, size_t n, size_t max_new,
                                    const int32_t* stop_ids, size_t n_stop, int32_t* ids, size_t* n_ids);
+/* The scoring loop of llmi-perplexity on one chunk
+ * (apps/llmi-perplexity/main.cpp:146-168): Transformer::forward(chunk,
+ * all_positions = true) (transformer.cpp:78-166; here through a fresh cache,
+ * bit-identical by the reference's own test), then for every position t in
+ * [t_start, n - 1): nll[t - t_start] = -(logit_t[chunk[t + 1]] - lse_t),
+ * lse_t = log(sum_v exp(double(logit_t[v] - max_t))) + max_t.  The caller
+ * sums nll in order, as the app does.  Positions before t_start are still
+ * run (they are the later positions' context) but not scored.  mode:
+ *   LLMI_SCORE_EXACT      the reference's arithmetic throughout (logits bit-
+ *                         identical; the double sum is taken as a tree, so
+ *                         nll agrees to ~1e-15 relative);
+ *   LLMI_SCORE_MFMA_HEAD  the lm_head on the bf16-MFMA GEMM (logits within
+ *                         2e-2 of max|logit|, so each nll within 4e-2 of it);
+ *   LLMI_SCORE_MFMA       every linear layer and the lm_head on the bf16-MFMA
+ *                         GEMM (the fast perplexity path; not bit-exact). */
+enum { LLMI_SCORE_EXACT = 0, LLMI_SCORE_MFMA_HEAD = 1, LLMI_SCORE_MFMA = 2 };
+int llmi_hip_model_chunk_nll(llmi_hip_model* model, const int32_t* tokens, size_t n, size_t t_start, int mode,
+                             double* nll);
 /* GPU time of the last generate_greedy call: the prompt prefill and the
  * decode loop (HIP events; the reference's llmi-generate --json reports the
  * same split as wall-clock seconds, apps/llmi-generate/main.cpp:329-345). */

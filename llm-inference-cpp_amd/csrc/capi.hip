@@ -99,6 +99,25 @@ std::size_t max_lds_per_block() { return g_max_lds; }
 
 using namespace llmi_hip;
 
+namespace llmi_hip {
+
+int launch_gemm_single(const DeviceMatrix& m, const float* x, std::size_t rows, const float* bias, float* y,
+                       hipStream_t s, bool accumulate) {
+  if (rows == 0 || m.out == 0) return LLMI_OK;
+  const GroupEntry e{&m, x, bias, y, rows, accumulate};
+  GemmPlan plan;
+  if (int rc = plan_gemm_group(&e, 1, &plan)) return rc;
+  if (int rc = g_gemm_scratch.reserve(plan.scratch_elems * sizeof(std::uint16_t), s)) return rc;
+  auto* scratch = static_cast<std::uint16_t*>(g_gemm_scratch.p);
+  bind_gemm_scratch(&plan, scratch);
+  if (int rc = launch_gemm_inputs(plan, scratch, s)) return rc;
+  for (const GemmLaunch& l : plan.launches)
+    if (int rc = launch_gemm(nullptr, nullptr, l, s, &plan.probs[l.prob_offset])) return rc;
+  return LLMI_OK;
+}
+
+}  // namespace llmi_hip
+
 struct llmi_hip_group {
   DeviceGroup g;
   ~llmi_hip_group() { g.release(); }
@@ -578,17 +597,7 @@ int llmi_hip_matmul_mfma_dev(const llmi_hip_weight* weight, const float* x, size
                              void* stream) {
   LLMI_REQUIRE_INIT();
   LLMI_REQUIRE(weight != nullptr, "gemm: null weight");
-  if (rows == 0 || weight->m.out == 0) return LLMI_OK;
-  const GroupEntry e{&weight->m, x, bias, y, rows, false};
-  GemmPlan plan;
-  if (int rc = plan_gemm_group(&e, 1, &plan)) return rc;
-  if (int rc = g_gemm_scratch.reserve(plan.scratch_elems * sizeof(std::uint16_t), pick(stream))) return rc;
-  auto* scratch = static_cast<std::uint16_t*>(g_gemm_scratch.p);
-  bind_gemm_scratch(&plan, scratch);
-  if (int rc = launch_gemm_inputs(plan, scratch, pick(stream))) return rc;
-  for (const GemmLaunch& l : plan.launches)
-    if (int rc = launch_gemm(nullptr, nullptr, l, pick(stream), &plan.probs[l.prob_offset])) return rc;
-  return LLMI_OK;
+  return llmi_hip::launch_gemm_single(weight->m, x, rows, bias, y, pick(stream));
 }
 
 }  // extern "C"

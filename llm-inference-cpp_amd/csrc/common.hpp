@@ -133,6 +133,7 @@ struct GemmProblem {
   const float* bias;
   float* y;
   int rows, in, ldx, out, nblk, ntiles, mtiles, first_wg, input;
+  int accumulate;  // y += acc + bias (the residual update), else y = acc + bias
 };
 // A distinct fp32 activation matrix of a GEMM group and where its bf16 copy
 // lives in the group's scratch (element offset).
@@ -152,6 +153,10 @@ struct GemmPlan {
   std::size_t scratch_elems = 0;  // bf16 elements of scratch the inputs need
 };
 int plan_gemm_group(const GroupEntry* entries, std::size_t count, GemmPlan* plan);
+// One product on the bf16-MFMA GEMM, with the library's bf16 staging buffer
+// (grown on demand, outside any graph capture).
+int launch_gemm_single(const DeviceMatrix& m, const float* x, std::size_t rows, const float* bias, float* y,
+                       hipStream_t s, bool accumulate = false);
 // Points every problem at its input's bf16 copy inside `scratch`.
 void bind_gemm_scratch(GemmPlan* plan, std::uint16_t* scratch);
 // Queues the fp32 -> bf16 conversion of every input into `scratch`.

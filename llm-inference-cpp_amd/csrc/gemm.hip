@@ -242,7 +242,11 @@ __global__ void __launch_bounds__(kGemmThreads) qgemm_mfma(const GemmProblem* __
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int m = m0 + wm0 + 16 * i + 4 * (lane >> 4) + q;
-        if (m < M) y[static_cast<std::size_t>(m) * N + n] = acc[i][j][q] + add;
+        if (m < M) {
+          GMEM float* dst = y + static_cast<std::size_t>(m) * N + n;
+          const float v = acc[i][j][q] + add;
+          *dst = p.accumulate ? *dst + v : v;
+        }
       }
   }
 }
@@ -301,6 +305,7 @@ int plan_gemm_group(const GroupEntry* entries, std::size_t count, GemmPlan* plan
       p.nblk = static_cast<int>(m.nblk);
       p.ntiles = static_cast<int>(m.ntiles);
       p.mtiles = static_cast<int>(ceil_div(e.rows, kBM));
+      p.accumulate = e.accumulate ? 1 : 0;
       for (std::size_t j = 0; j < plan->inputs.size(); ++j)
         if (plan->inputs[j].x == e.x) p.input = static_cast<int>(j);
       const std::size_t ntiles_n = ceil_div(m.out, kBN);

@@ -29,8 +29,9 @@
 // (one kernel per row chunk R present); each workgroup runs one tile of one
 // product with the same tile functions.
 //
-// qgemv_rows (batch > 8, the exact prefill path): one wavefront per tile
-// walks all blocks in order with the chains in registers.
+// qgemm_exact (batch > 8, the exact prefill path): 64, 32 or 16 input rows
+// x 64 outputs per workgroup, 4 x 4 / 2 x 4 / 1 x 4 chains per thread,
+// operands from LDS.
 #include <algorithm>
 #include <vector>
 
@@ -568,83 +569,140 @@ __global__ void __launch_bounds__(1024) qgemv_group_narrow(const GroupProblem* _
 }
 
 // ------------------------------------------------------------ batch > 8
-// One wavefront per tile (4 tiles per 256-thread workgroup), R input rows
-// per workgroup row (grid.y), chains in registers.
-template <int TYPE, int R, int CH>
-__global__ void __launch_bounds__(256) qgemv_rows(const uint4* __restrict__ codes, const float* __restrict__ scales,
-                                                  const float* __restrict__ x, const float* __restrict__ bias,
-                                                  float* __restrict__ y, int in, int nblk, int out, int rows,
-                                                  int ntiles, int accumulate) {
-  const int lane = threadIdx.x & (kTileRows - 1);
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const std::size_t tile = static_cast<std::size_t>(blockIdx.x) * 4 + wave;
-  if (tile >= static_cast<std::size_t>(ntiles)) return;
-  const int r0 = blockIdx.y * R;
-  const int nr = min(R, rows - r0);
-  const int nfull = in / kBlock;
-  const float* xb = x + static_cast<std::size_t>(r0) * in;
+// The exact multi-row product (the model's own prefill): one workgroup per
+// MR input rows (64, 32 or 16, chosen for parallelism) x one 64-row tile of
+// the matrix (64 outputs).  Per quantization block the workgroup stages the
+// block's activations of its MR rows and the block's codes of its 64
+// outputs, converted to fp32 once, in LDS -- transposed, [k][row] and
+// [k][output], so one read gives a thread its RT = MR/16 rows (or 4 outputs)
+// at one k -- plus the 64 scales; double-buffered: the next block's loads
+// go to registers before this block's arithmetic and to LDS after it.
+// Thread (tr, to) holds the RT x 4 chains of rows RT*tr.. and outputs
+// 4to..4to+3: part = fma(x[k], code[k], part) over the block's k in order,
+// then acc = fma(part, scale, acc) -- the reference's chains, so y is
+// bit-identical.  The final partial block runs only its len elements.
+template <int MR>
+struct RowVec;
+template <>
+struct RowVec<64> {
+  static __device__ __forceinline__ void get(const float* p, float* v) {
+    const float4 t = *reinterpret_cast<const float4*>(p);
+    v[0] = t.x; v[1] = t.y; v[2] = t.z; v[3] = t.w;
+  }
+};
+template <>
+struct RowVec<32> {
+  static __device__ __forceinline__ void get(const float* p, float* v) {
+    const float2 t = *reinterpret_cast<const float2*>(p);
+    v[0] = t.x; v[1] = t.y;
+  }
+};
+template <>
+struct RowVec<16> {
+  static __device__ __forceinline__ void get(const float* p, float* v) { v[0] = *p; }
+};
 
-  float acc[R];
+template <int TYPE, int MR>
+__global__ void __launch_bounds__(256) qgemm_exact(const uint4* __restrict__ codes, const float* __restrict__ scales,
+                                                   const float* __restrict__ x, const float* __restrict__ bias,
+                                                   float* __restrict__ y, int in, int nblk, int out, int rows,
+                                                   int accumulate) {
+  constexpr int RT = MR / 16;          // rows per thread
+  constexpr int XS = MR + 4;           // LDS floats per k of the activations
+  constexpr int CSTRIDE = kTileRows + 4;
+  constexpr int XPT = MR * kBlock / 256;  // activations staged per thread
+  __shared__ __attribute__((aligned(16))) float xs[2][kBlock * XS];
+  __shared__ __attribute__((aligned(16))) float cs[2][kBlock * CSTRIDE];
+  __shared__ float ss[2][kTileRows];
+  const std::size_t tile = blockIdx.x;
+  const int r0 = blockIdx.y * MR;
+  const int tid = threadIdx.x;
+  const int tr = tid >> 4, to = tid & 15;
+  // Staging: activations of row xr, elements XPT*xq..+XPT-1 of the block;
+  // codes of output cr (= lane of the tile), elements 8*cq..8*cq+7.
+  // Addresses are clamped into x (rows past `rows`, and elements past `in`
+  // of the final block, are never used), so no load sits behind a branch.
+  const int xr = tid / (kBlock / XPT), xq = tid % (kBlock / XPT);
+  const int cr = tid >> 2, cq = tid & 3;
+  const float* xrow = x + static_cast<std::size_t>(min(r0 + xr, rows - 1)) * in;
+  const GMEM uint4* cg = gmem(codes);
+  struct Staged {
+    float xv[XPT];
+    Block<TYPE> blk;
+    float sc;
+  };
+  const auto load = [&](Staged& st, int b) {
+    const int k0 = b * kBlock + XPT * xq;
 #pragma unroll
-  for (int r = 0; r < R; ++r) acc[r] = 0.0f;
-
-  Block<TYPE> cur[CH];
-  float cur_s[CH];
+    for (int u = 0; u < XPT; ++u) st.xv[u] = xrow[min(k0 + u, in - 1)];
+    st.blk = load_block<TYPE, false>(cg, tile * nblk + b, cr);
+    st.sc = scales[(tile * nblk + b) * kTileRows + (tid & (kTileRows - 1))];
+  };
+  const auto store = [&](const Staged& st, int buf) {
+    std::uint32_t w[8];
+    unpack_words<TYPE>(st.blk, w);
 #pragma unroll
-  for (int j = 0; j < CH; ++j) {
-    if (j < nfull) {
-      cur[j] = load_block<TYPE, false>(gmem(codes), tile * nblk + j, lane);
-      cur_s[j] = loadf<false>(gmem(scales + (tile * nblk + j) * kTileRows + lane));
+    for (int u = 0; u < XPT; ++u) xs[buf][(XPT * xq + u) * XS + xr] = st.xv[u];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) cs[buf][(8 * cq + u) * CSTRIDE + cr] = code_of<TYPE>(w, 8 * cq + u);
+    if (tid < kTileRows) ss[buf][tid] = st.sc;
+  };
+  float acc[RT][4];
+#pragma unroll
+  for (int i = 0; i < RT; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = 0.0f;
+  Staged st;
+  load(st, 0);
+  store(st, 0);
+  __syncthreads();
+  for (int b = 0; b < nblk; ++b) {
+    const int buf = b & 1;
+    if (b + 1 < nblk) load(st, b + 1);
+    const int len = min(kBlock, in - b * kBlock);
+    const float* xb = xs[buf] + RT * tr;
+    const float* cb = cs[buf] + 4 * to;
+    float part[RT][4];
+#pragma unroll
+    for (int i = 0; i < RT; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) part[i][j] = 0.0f;
+    const auto step = [&](int k) {
+      float xa[RT];
+      RowVec<MR>::get(xb + k * XS, xa);
+      const float4 cv = *reinterpret_cast<const float4*>(cb + k * CSTRIDE);
+      const float ca[4] = {cv.x, cv.y, cv.z, cv.w};
+#pragma unroll
+      for (int i = 0; i < RT; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) part[i][j] = __builtin_fmaf(xa[i], ca[j], part[i][j]);
+    };
+    if (len == kBlock) {
+#pragma unroll 8
+      for (int k = 0; k < kBlock; ++k) step(k);
+    } else {
+      for (int k = 0; k < len; ++k) step(k);
     }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float sc = ss[buf][4 * to + j];
+#pragma unroll
+      for (int i = 0; i < RT; ++i) acc[i][j] = __builtin_fmaf(part[i][j], sc, acc[i][j]);
+    }
+    if (b + 1 < nblk) store(st, buf ^ 1);
+    __syncthreads();
   }
-  for (int b = 0; b < nfull; b += CH) {
-    Block<TYPE> nxt[CH];
-    float nxt_s[CH];
 #pragma unroll
-    for (int j = 0; j < CH; ++j) {
-      if (b + CH + j < nfull) {
-        nxt[j] = load_block<TYPE, false>(gmem(codes), tile * nblk + b + CH + j, lane);
-        nxt_s[j] = loadf<false>(gmem(scales + (tile * nblk + b + CH + j) * kTileRows + lane));
-      }
-    }
-#pragma unroll
-    for (int j = 0; j < CH; ++j) {
-      if (b + j < nfull) {
-        float c[kBlock];
-        block_codes<TYPE>(cur[j], c);
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-          if (r < nr) {
-            const float p = codes_dot(c, xb + static_cast<std::size_t>(r) * in + (b + j) * kBlock);
-            acc[r] = __builtin_fmaf(p, cur_s[j], acc[r]);
-          }
-        }
-      }
-    }
-#pragma unroll
-    for (int j = 0; j < CH; ++j) {
-      cur[j] = nxt[j];
-      cur_s[j] = nxt_s[j];
-    }
-  }
-  if (nfull < nblk) {
-    const Block<TYPE> blk = load_block<TYPE, false>(gmem(codes), tile * nblk + nfull, lane);
-    const float s = loadf<false>(gmem(scales + (tile * nblk + nfull) * kTileRows + lane));
-    for (int r = 0; r < nr; ++r) {
-      const float p = tail_block_dot<TYPE>(blk, xb + static_cast<std::size_t>(r) * in + nfull * kBlock, in - nfull * kBlock);
-#pragma unroll
-      for (int rr = 0; rr < R; ++rr)
-        if (rr == r) acc[rr] = __builtin_fmaf(p, s, acc[rr]);
-    }
-  }
-  const std::size_t o = tile * kTileRows + lane;
-  if (o < static_cast<std::size_t>(out)) {
+  for (int j = 0; j < 4; ++j) {
+    const std::size_t o = tile * kTileRows + 4 * to + j;
+    if (o >= static_cast<std::size_t>(out)) continue;
     const float add = bias != nullptr ? bias[o] : 0.0f;
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-      if (r < nr) {
-        float* dst = y + static_cast<std::size_t>(r0 + r) * out + o;
-        const float v = acc[r] + add;
+    for (int i = 0; i < RT; ++i) {
+      const int r = r0 + RT * tr + i;
+      if (r < rows) {
+        float* dst = y + static_cast<std::size_t>(r) * out + o;
+        const float v = acc[i][j] + add;
         *dst = accumulate ? *dst + v : v;
       }
     }
@@ -690,7 +748,7 @@ int narrow_waves(std::size_t nblk) {
 }
 
 struct TilePlan {
-  int kind = 0;  // 0: qgemv_rows; GroupProblem::kNarrow; or the row chunk R of qgemv_tile
+  int kind = 0;  // 0: qgemm_exact; GroupProblem::kNarrow; or the row chunk R of qgemv_tile
   int waves = 1;
   int bpw = 1;
   std::size_t lds = 0;
@@ -703,7 +761,7 @@ TilePlan plan_single(const DeviceMatrix& m, std::size_t rows) {
   constexpr std::size_t kNarrowTiles = 128;
   const std::size_t nblk = std::max<std::size_t>(m.nblk, 1);
   TilePlan p;
-  if (rows > 8) return p;  // qgemv_rows
+  if (rows > 8) return p;  // qgemm_exact
   if (rows == 1 && m.ntiles < kNarrowTiles && narrow_lds(m.in, nblk) <= max_lds_per_block()) {
     p.kind = GroupProblem::kNarrow;
     p.waves = narrow_waves(nblk);
@@ -713,7 +771,7 @@ TilePlan plan_single(const DeviceMatrix& m, std::size_t rows) {
   }
   int r = pick_chunk(rows, nblk, kLdsTarget);
   if (r == 0) r = pick_chunk(1, nblk, max_lds_per_block());
-  if (r == 0) return p;  // rows too long for LDS staging: qgemv_rows
+  if (r == 0) return p;  // rows too long for LDS staging: qgemm_exact
   p.kind = r;
   p.bpw = static_cast<int>(ceil_div(nblk, wide_waves(nblk, m.type)));
   p.waves = static_cast<int>(ceil_div(nblk, p.bpw));
@@ -730,15 +788,33 @@ void launch_tile(const DeviceMatrix& m, const float* x, std::size_t rows, const 
       static_cast<int>(m.out), static_cast<int>(rows), p.bpw, acc);
 }
 
+// Row tile of the exact multi-row product: the largest MR that still gives
+// about 1024 workgroups (4 wavefronts per SIMD), else 16.
+int exact_rows_tile(std::size_t ntiles, std::size_t rows) {
+  constexpr std::size_t kWant = 1024;
+  for (int mr : {64, 32}) {
+    if (ntiles * ceil_div(rows, static_cast<std::size_t>(mr)) >= kWant) return mr;
+  }
+  return 16;
+}
+
+template <int TYPE, int MR>
+void launch_exact(const DeviceMatrix& m, const float* x, std::size_t rows, const float* bias, float* y, int acc,
+                  hipStream_t s) {
+  const dim3 grid(static_cast<unsigned>(m.ntiles), static_cast<unsigned>(ceil_div(rows, MR)));
+  qgemm_exact<TYPE, MR><<<grid, 256, 0, s>>>(reinterpret_cast<const uint4*>(m.codes), m.scales, x, bias, y,
+                                             static_cast<int>(m.in), static_cast<int>(m.nblk),
+                                             static_cast<int>(m.out), static_cast<int>(rows), acc);
+}
+
 template <int TYPE>
 void launch_rows(const DeviceMatrix& m, const float* x, std::size_t rows, const float* bias, float* y, int acc,
                  hipStream_t s) {
-  constexpr int R = 8, CH = TYPE == LLMI_TYPE_Q8_0 ? 2 : 4;
-  const dim3 grid(static_cast<unsigned>(ceil_div(m.ntiles, 4)), static_cast<unsigned>(ceil_div(rows, R)));
-  qgemv_rows<TYPE, R, CH><<<grid, 256, 0, s>>>(reinterpret_cast<const uint4*>(m.codes), m.scales, x, bias, y,
-                                               static_cast<int>(m.in), static_cast<int>(m.nblk),
-                                               static_cast<int>(m.out), static_cast<int>(rows),
-                                               static_cast<int>(m.ntiles), acc);
+  switch (exact_rows_tile(m.ntiles, rows)) {
+    case 64: launch_exact<TYPE, 64>(m, x, rows, bias, y, acc, s); break;
+    case 32: launch_exact<TYPE, 32>(m, x, rows, bias, y, acc, s); break;
+    default: launch_exact<TYPE, 16>(m, x, rows, bias, y, acc, s); break;
+  }
 }
 
 template <int TYPE>

@@ -754,6 +754,30 @@ __global__ void __launch_bounds__(kThreads) argmax_many(const float* __restrict_
 }
 
 // Standalone glue kernels (the device counterparts of kernels.hpp:13-32).
+// The scoring of llmi-perplexity (apps/llmi-perplexity/main.cpp:158-166) on
+// one logits row per workgroup: mx = the float maximum; sum_exp = sum over v
+// of exp(double(row[v] - mx)) (the float difference, widened); lse =
+// log(sum_exp) + mx; nll = -(double(row[next]) - lse).  The reference sums
+// sequentially; here the double sum is a fixed tree, so nll can differ from
+// the reference's in the last bits.
+__global__ void __launch_bounds__(kThreads) row_nll(const float* __restrict__ logits, int V,
+                                                    const std::int32_t* __restrict__ next,
+                                                    double* __restrict__ nll) {
+  __shared__ double red_d[kThreads];
+  __shared__ float red_f[kThreads];
+  const float* row = logits + static_cast<std::size_t>(blockIdx.x) * V;
+  float mx = -__builtin_inff();
+  for (int v = threadIdx.x; v < V; v += kThreads) mx = fmaxf(mx, row[v]);
+  mx = block_max_float(mx, red_f);
+  double part = 0.0;
+  for (int v = threadIdx.x; v < V; v += kThreads) part += exp(static_cast<double>(row[v] - mx));
+  const double sum = block_sum_double(part, red_d);
+  if (threadIdx.x == 0) {
+    const double lse = log(sum) + static_cast<double>(mx);
+    nll[blockIdx.x] = -(static_cast<double>(row[next[blockIdx.x]]) - lse);
+  }
+}
+
 __global__ void __launch_bounds__(kThreads) dot_many(const float* __restrict__ a, const float* __restrict__ b,
                                                      const int* __restrict__ lens, int count, float* __restrict__ out) {
   const int i = blockIdx.x * kThreads + threadIdx.x;
@@ -1112,18 +1136,19 @@ int decode_step(llmi_hip_model* m, llmi_hip_cache* cache, hipStream_t s) {
   return LLMI_OK;
 }
 
-// transformer.cpp:192-306 with the ids already on the device (ws.ids).  The
-// logits of rows first..T-1 land in ws.logits.  trace (host, optional):
-// (layers + 2) x T x H floats -- the embeddings, every layer's output and
-// the final RMSNorm, as the reference's ForwardTrace (transformer.hpp:14-19).
-int forward_device(llmi_hip_model* m, llmi_hip_cache* cache, std::size_t T, bool all_positions, hipStream_t s,
-                   float* trace = nullptr) {
+// The body of forward_device: the lm_head runs on rows [head_first,
+// head_first + head_rows) of the final normalised states (exact GEMV, or the
+// bf16-MFMA GEMM with mfma_head), logits from ws.logits row 0.
+int forward_rows(llmi_hip_model* m, llmi_hip_cache* cache, std::size_t T, std::size_t head_first,
+                 std::size_t head_rows, bool mfma_head, hipStream_t s, float* trace, bool mfma_all = false) {
+  // Every linear of the layers on the bf16-MFMA GEMM (mfma_all) or exact.
+  const auto linear = [&](const DeviceMatrix& w, const float* x, const float* bias, float* y, bool acc) {
+    return mfma_all ? launch_gemm_single(w, x, T, bias, y, s, acc) : launch_matmul(w, x, T, bias, y, s, acc);
+  };
   const auto& c = m->c;
   Workspace& w = m->ws;
   const std::size_t base = cache->len;
   const int nh = static_cast<int>(c.num_heads), nkv = static_cast<int>(c.num_kv_heads);
-  if (T == 1 && trace == nullptr && decode_attention_fits(nh, nkv, static_cast<int>(m->hd), base + 1))
-    return decode_step(m, cache, s);
   const int hd = static_cast<int>(m->hd);
   const float eps = static_cast<float>(c.rms_norm_eps);
   const float scale = 1.0F / std::sqrt(static_cast<float>(m->hd));
@@ -1138,26 +1163,26 @@ int forward_device(llmi_hip_model* m, llmi_hip_cache* cache, std::size_t T, bool
     float* kc = cache->k + li * per_layer;
     float* vc = cache->v + li * per_layer;
     rmsnorm_rows<<<tt, kThreads, 0, s>>>(w.x, l.attn_norm, w.h, static_cast<int>(m->H), eps);
-    if (int rc = launch_matmul(l.wq, w.h, T, l.bq, w.q, s)) return rc;
-    if (int rc = launch_matmul(l.wk, w.h, T, l.bk, w.k, s)) return rc;
-    if (int rc = launch_matmul(l.wv, w.h, T, l.bv, w.v, s)) return rc;
+    if (int rc = linear(l.wq, w.h, l.bq, w.q, false)) return rc;
+    if (int rc = linear(l.wk, w.h, l.bk, w.k, false)) return rc;
+    if (int rc = linear(l.wv, w.h, l.bv, w.v, false)) return rc;
     rope_and_cache<<<tt, kThreads, 0, s>>>(w.q, w.k, w.v, kc, vc, m->cos_t, m->sin_t, nh, nkv, hd,
                                            static_cast<int>(cache->cap), static_cast<int>(base));
     launch_attention(w.q, kc, vc, w.att, nh, nkv, hd, static_cast<int>(cache->cap), static_cast<int>(base),
                      static_cast<int>(T), scale, s);
-    if (int rc = launch_matmul(l.wo, w.att, T, nullptr, w.x, s, true)) return rc;
+    if (int rc = linear(l.wo, w.att, nullptr, w.x, true)) return rc;
     rmsnorm_rows<<<tt, kThreads, 0, s>>>(w.x, l.mlp_norm, w.h, static_cast<int>(m->H), eps);
-    if (int rc = launch_matmul(l.gate, w.h, T, nullptr, w.g, s)) return rc;
-    if (int rc = launch_matmul(l.up, w.h, T, nullptr, w.u, s)) return rc;
+    if (int rc = linear(l.gate, w.h, nullptr, w.g, false)) return rc;
+    if (int rc = linear(l.up, w.h, nullptr, w.u, false)) return rc;
     silu_mul<<<blocks_for(T * m->F), kThreads, 0, s>>>(w.g, w.u, T * m->F);
-    if (int rc = launch_matmul(l.down, w.g, T, nullptr, w.x, s, true)) return rc;
+    if (int rc = linear(l.down, w.g, nullptr, w.x, true)) return rc;
     if (trace != nullptr)
       LLMI_TRY_HIP(hipMemcpyAsync(trace + (li + 1) * state, w.x, state * sizeof(float), hipMemcpyDeviceToHost, s));
   }
   // The reference normalises every row (transformer.cpp:298), then applies the
   // head to the last one or to all of them.
-  const std::size_t first = all_positions ? 0 : T - 1;
-  const std::size_t rows = T - first;
+  const std::size_t first = head_first;
+  const std::size_t rows = head_rows;
   const std::size_t norm_first = trace != nullptr ? 0 : first;
   rmsnorm_rows<<<static_cast<unsigned>(T - norm_first), kThreads, 0, s>>>(
       w.x + norm_first * m->H, m->final_norm, w.h + norm_first * m->H, static_cast<int>(m->H), eps);
@@ -1165,10 +1190,27 @@ int forward_device(llmi_hip_model* m, llmi_hip_cache* cache, std::size_t T, bool
     LLMI_TRY_HIP(hipMemcpyAsync(trace + (m->layers.size() + 1) * state, w.h, state * sizeof(float),
                                 hipMemcpyDeviceToHost, s));
   const DeviceMatrix& head = m->tied ? m->embed : m->lm_head;
-  if (int rc = launch_matmul(head, w.h + first * m->H, rows, nullptr, w.logits, s)) return rc;
+  if (mfma_head) {
+    if (int rc = launch_gemm_single(head, w.h + first * m->H, rows, nullptr, w.logits, s)) return rc;
+  } else if (int rc = launch_matmul(head, w.h + first * m->H, rows, nullptr, w.logits, s)) {
+    return rc;
+  }
   LLMI_TRY_HIP(hipGetLastError());
   cache->len = base + T;
   return LLMI_OK;
+}
+
+// transformer.cpp:192-306 with the ids already on the device (ws.ids).  The
+// logits of rows first..T-1 land in ws.logits.  trace (host, optional):
+// (layers + 2) x T x H floats -- the embeddings, every layer's output and
+// the final RMSNorm, as the reference's ForwardTrace (transformer.hpp:14-19).
+int forward_device(llmi_hip_model* m, llmi_hip_cache* cache, std::size_t T, bool all_positions, hipStream_t s,
+                   float* trace = nullptr) {
+  const int nh = static_cast<int>(m->c.num_heads), nkv = static_cast<int>(m->c.num_kv_heads);
+  if (T == 1 && trace == nullptr && decode_attention_fits(nh, nkv, static_cast<int>(m->hd), cache->len + 1))
+    return decode_step(m, cache, s);
+  const std::size_t first = all_positions ? 0 : T - 1;
+  return forward_rows(m, cache, T, first, T - first, false, s, trace);
 }
 
 // Validation of transformer.cpp:204-212, with the reference's messages.
@@ -1394,6 +1436,37 @@ int llmi_hip_model_generate_greedy(llmi_hip_model* m, const int32_t* prompt, siz
   m->last_prefill_ms = pre;
   m->last_decode_ms = dec;
   *n_ids = produced;
+  return LLMI_OK;
+}
+
+int llmi_hip_model_chunk_nll(llmi_hip_model* m, const int32_t* tokens, size_t n, size_t t_start, int mode,
+                             double* nll) {
+  LLMI_REQUIRE_INIT();
+  LLMI_REQUIRE(m != nullptr, "chunk_nll: null model");
+  LLMI_REQUIRE(mode == LLMI_SCORE_EXACT || mode == LLMI_SCORE_MFMA_HEAD || mode == LLMI_SCORE_MFMA,
+               "chunk_nll: mode must be LLMI_SCORE_EXACT, _MFMA_HEAD or _MFMA");
+  llmi_hip_cache* cache = nullptr;
+  if (int rc = llmi_hip_model_new_cache(m, n, &cache)) return rc;
+  std::unique_ptr<llmi_hip_cache, int (*)(llmi_hip_cache*)> guard(cache, llmi_hip_cache_free);
+  if (int rc = validate(m, cache, tokens, n)) return rc;
+  LLMI_REQUIRE(nll != nullptr || t_start + 1 >= n, "chunk_nll: null nll");
+  if (int rc = ensure_workspace(m, n)) return rc;
+  Workspace& w = m->ws;
+  hipStream_t s = library_stream();
+  const std::size_t first = std::min(t_start, n - 1);
+  const std::size_t rows = n - 1 - first;  // the last position predicts nothing inside the chunk
+  LLMI_TRY_HIP(hipMemcpyAsync(w.ids, tokens, n * sizeof(std::int32_t), hipMemcpyHostToDevice, s));
+  if (int rc = forward_rows(m, cache, n, first, rows, mode != LLMI_SCORE_EXACT, s, nullptr, mode == LLMI_SCORE_MFMA))
+    return rc;
+  if (rows == 0) return LLMI_OK;
+  double* d = nullptr;
+  LLMI_TRY_HIP(hipMalloc(&d, rows * sizeof(double)));
+  row_nll<<<static_cast<unsigned>(rows), kThreads, 0, s>>>(w.logits, static_cast<int>(m->V), w.ids + first + 1, d);
+  hipError_t e = hipGetLastError();
+  if (e == hipSuccess) e = hipMemcpyAsync(nll, d, rows * sizeof(double), hipMemcpyDeviceToHost, s);
+  if (e == hipSuccess) e = hipStreamSynchronize(s);
+  (void)hipFree(d);
+  if (e != hipSuccess) return fail(LLMI_ERR_HIP, std::string("chunk_nll: ") + hipGetErrorString(e));
   return LLMI_OK;
 }
 

@@ -18,6 +18,7 @@ LIB_PATH = os.path.join(HERE, "libllmi_hip.so")
 
 F32, Q8_0, Q4_0 = 0, 1, 2
 GGUF_Q4_0, GGUF_Q8_0 = 2, 8  # GGUF tensor types (LLMI_GGUF_*)
+SCORE_EXACT, SCORE_MFMA_HEAD, SCORE_MFMA = 0, 1, 2  # modes of llmi_hip_model_chunk_nll
 BLOCK = 32
 TYPE_NAMES = {F32: "f32", Q8_0: "q8_0", Q4_0: "q4_0"}
 
@@ -52,6 +53,7 @@ SIGNATURES = {
     "llmi_hip_weight_quantize": (_i, [_vp, _sz, _sz, _i, C.POINTER(_vp)]),
     "llmi_hip_weight_quantize_dev": (_i, [_vp, _sz, _sz, _i, C.POINTER(_vp)]),
     "llmi_hip_weight_free": (_i, [_vp]),
+    "llmi_hip_model_chunk_nll": (_i, [_vp, _vp, _sz, _sz, _i, _vp]),
     "llmi_hip_weight_from_gguf": (_i, [_vp, _sz, _sz, _sz, _i, C.POINTER(_vp)]),
     "llmi_hip_weight_download": (_i, [_vp, _vp, _vp]),
     "llmi_hip_weight_info": (_i, [_vp, C.POINTER(_sz), C.POINTER(_sz), C.POINTER(_i), C.POINTER(_sz)]),
@@ -417,6 +419,14 @@ class Model:
         check(self.lib.llmi_hip_model_generate_greedy(self.h, _p(p), p.size, max_new, _p(stop) if stop.size else None,
                                                       stop.size, _p(ids), C.byref(n)))
         return ids[: n.value]
+
+    def chunk_nll(self, tokens, t_start: int, mode: int = SCORE_EXACT) -> np.ndarray:
+        """-log P(chunk[t+1] | chunk[..t]) for t in [t_start, n - 1) (float64)."""
+        ids = np.ascontiguousarray(tokens, dtype=np.int32)
+        rows = max(0, len(ids) - 1 - min(t_start, max(len(ids) - 1, 0)))
+        out = np.zeros(max(rows, 1), dtype=np.float64)
+        check(self.lib.llmi_hip_model_chunk_nll(self.h, _p(ids), len(ids), t_start, mode, _p(out)))
+        return out[:rows]
 
     def last_timing(self):
         """(prefill_ms, decode_ms) of the last generate_greedy call."""
