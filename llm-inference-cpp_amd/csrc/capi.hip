@@ -64,6 +64,12 @@ int alloc_matrix(std::size_t out, std::size_t in, int type, DeviceMatrix* m) {
   m->ntiles = ceil_div(out, kTileRows);
   m->code_bytes = m->ntiles * m->nblk * kTileRows * block_code_bytes(type);
   m->scale_bytes = m->ntiles * m->nblk * kTileRows * sizeof(float);
+  if (type == LLMI_TYPE_F32) {  // row-major floats, as the reference keeps them
+    m->code_bytes = out * in * sizeof(float);
+    m->scale_bytes = 0;
+    if (m->code_bytes != 0) LLMI_TRY_HIP(hipMalloc(reinterpret_cast<void**>(&m->codes), m->code_bytes));
+    return LLMI_OK;
+  }
   if (m->code_bytes == 0) return LLMI_OK;
   LLMI_TRY_HIP(hipMalloc(reinterpret_cast<void**>(&m->codes), m->code_bytes));
   const hipError_t e = hipMalloc(reinterpret_cast<void**>(&m->scales), m->scale_bytes);
@@ -422,7 +428,8 @@ int llmi_hip_weight_from_gguf(const void* blocks, size_t nbytes, size_t out, siz
 
 int llmi_hip_weight_quantize_dev(const float* w, size_t out, size_t in, int type, llmi_hip_weight** weight) {
   LLMI_REQUIRE_INIT();
-  if (const int rc = check_type(type)) return rc;
+  if (type != LLMI_TYPE_F32)
+    if (const int rc = check_type(type)) return rc;
   LLMI_REQUIRE(weight != nullptr, "weight_quantize: null out-pointer");
   LLMI_REQUIRE(in <= 0x7FFFFFFFu, "weight_quantize: in too large");
   *weight = nullptr;
@@ -432,7 +439,12 @@ int llmi_hip_weight_quantize_dev(const float* w, size_t out, size_t in, int type
     return rc;
   }
   if (out > 0 && in > 0) {
-    int rc = launch_quantize(w, out, in, type, nullptr, nullptr, &h->m, g_stream);
+    int rc = type == LLMI_TYPE_F32
+                 ? (hipMemcpyAsync(h->m.codes, w, out * in * sizeof(float), hipMemcpyDeviceToDevice, g_stream) ==
+                            hipSuccess
+                        ? LLMI_OK
+                        : fail(LLMI_ERR_HIP, "weight_quantize: copy"))
+                 : launch_quantize(w, out, in, type, nullptr, nullptr, &h->m, g_stream);
     if (rc == LLMI_OK && hipStreamSynchronize(g_stream) != hipSuccess) rc = fail(LLMI_ERR_HIP, "weight_quantize: sync");
     if (rc != LLMI_OK) {
       free_matrix(&h->m);
@@ -445,7 +457,8 @@ int llmi_hip_weight_quantize_dev(const float* w, size_t out, size_t in, int type
 
 int llmi_hip_weight_quantize(const float* w, size_t out, size_t in, int type, llmi_hip_weight** weight) {
   LLMI_REQUIRE_INIT();
-  if (const int rc = check_type(type)) return rc;
+  if (type != LLMI_TYPE_F32)
+    if (const int rc = check_type(type)) return rc;
   DevBuf dw;
   if (int rc = dw.alloc(out * in * sizeof(float))) return rc;
   if (out * in > 0) LLMI_TRY_HIP(hipMemcpyAsync(dw.p, w, out * in * sizeof(float), hipMemcpyHostToDevice, g_stream));
@@ -466,6 +479,11 @@ int llmi_hip_weight_download(const llmi_hip_weight* weight, uint8_t* data, float
   const DeviceMatrix& m = weight->m;
   const std::size_t nd = m.out * row_bytes(m.in, m.type), ns = m.out * m.nblk;
   if (nd == 0) return LLMI_OK;
+  if (m.type == LLMI_TYPE_F32) {  // the floats themselves; no scales
+    LLMI_TRY_HIP(hipMemcpyAsync(data, m.codes, nd, hipMemcpyDeviceToHost, g_stream));
+    LLMI_TRY_HIP(hipStreamSynchronize(g_stream));
+    return LLMI_OK;
+  }
   DevBuf dd, ds;
   if (int rc = dd.alloc(nd)) return rc;
   if (int rc = ds.alloc(ns * sizeof(float))) return rc;
@@ -483,7 +501,8 @@ int llmi_hip_weight_info(const llmi_hip_weight* weight, size_t* out, size_t* in,
   if (out != nullptr) *out = m.out;
   if (in != nullptr) *in = m.in;
   if (type != nullptr) *type = m.type;
-  if (byte_size != nullptr) *byte_size = m.out * row_bytes(m.in, m.type) + m.out * m.nblk * sizeof(float);
+  if (byte_size != nullptr)
+    *byte_size = m.out * row_bytes(m.in, m.type) + (m.type == LLMI_TYPE_F32 ? 0 : m.out * m.nblk * sizeof(float));
   return LLMI_OK;
 }
 

@@ -42,7 +42,9 @@ inline hipStream_t pick(void* s) { return s != nullptr ? static_cast<hipStream_t
   } while (0)
 
 inline std::size_t ceil_div(std::size_t a, std::size_t b) { return (a + b - 1) / b; }
-inline std::size_t row_bytes(std::size_t in, int type) { return type == LLMI_TYPE_Q4_0 ? (in + 1) / 2 : in; }
+inline std::size_t row_bytes(std::size_t in, int type) {
+  return type == LLMI_TYPE_Q4_0 ? (in + 1) / 2 : type == LLMI_TYPE_F32 ? 4 * in : in;
+}
 
 // Device layout of a packed matrix ("tiled"): rows are grouped in tiles of 64
 // (lane l of a wavefront owns row tile*64 + l).  For each tile and each
@@ -174,6 +176,11 @@ int launch_quantize(const float* w, std::size_t out, std::size_t in, int type, s
 int launch_relayout_to_tiled(const std::uint8_t* planar_data, const float* planar_scales, const DeviceMatrix& m,
                              hipStream_t s);
 int launch_relayout_to_planar(const DeviceMatrix& m, std::uint8_t* planar_data, float* planar_scales, hipStream_t s);
+// fp32 weights (type LLMI_TYPE_F32: codes holds the row-major [out][in]
+// floats, no scales): kernels::matmul and the row gather (f32.hip).
+int launch_matmul_f32(const DeviceMatrix& m, const float* x, std::size_t rows, const float* bias, float* y,
+                      hipStream_t s, bool accumulate);
+int launch_gather_f32(const DeviceMatrix& m, const std::int32_t* ids, std::size_t n, float* dst, hipStream_t s);
 // GGUF (ggml) Q8_0 / Q4_0 blocks of m's shape (device memory) -> m.
 int launch_gguf_to_tiled(const void* raw, const DeviceMatrix& m, hipStream_t s);
 int launch_dequantize_rows(const DeviceMatrix& m, const std::int32_t* ids, std::size_t n, float* dst, hipStream_t s);

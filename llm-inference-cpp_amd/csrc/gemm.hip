@@ -262,6 +262,7 @@ int plan_gemm_group(const GroupEntry* entries, std::size_t count, GemmPlan* plan
     const GroupEntry& e = entries[i];
     LLMI_REQUIRE(e.m != nullptr, "gemm: null weight");
     LLMI_REQUIRE(e.x != nullptr && e.y != nullptr, "gemm: null x or y");
+    LLMI_REQUIRE(e.m->type != LLMI_TYPE_F32, "gemm: fp32 weights are not part of the MFMA GEMM");
     const DeviceMatrix& m = *e.m;
     LLMI_REQUIRE(m.in > 0 && m.in <= 0x7FFFFFFFu && m.out <= 0x7FFFFFFFu, "gemm: bad shape");
     LLMI_REQUIRE(e.rows <= 0x7FFFFFFFu, "gemm: too many rows");

@@ -847,6 +847,10 @@ int check_shape(const DeviceMatrix& m, std::size_t rows) {
 int launch_matmul(const DeviceMatrix& m, const float* x, std::size_t rows, const float* bias, float* y, hipStream_t s,
                   bool accumulate) {
   if (rows == 0 || m.out == 0) return LLMI_OK;
+  if (m.type == LLMI_TYPE_F32) {
+    LLMI_REQUIRE(x != nullptr && y != nullptr, "matmul: null pointer");
+    return launch_matmul_f32(m, x, rows, bias, y, s, accumulate);
+  }
   if (int rc = check_shape(m, rows)) return rc;
   LLMI_REQUIRE(x != nullptr && y != nullptr, "matmul: null pointer");
   const int acc = accumulate ? 1 : 0;
@@ -865,6 +869,7 @@ int plan_group(const GroupEntry* entries, std::size_t count, GroupPlan* plan) {
   for (std::size_t i = 0; i < count; ++i) {
     const GroupEntry& e = entries[i];
     LLMI_REQUIRE(e.m != nullptr, "group: null weight");
+    LLMI_REQUIRE(e.m->type != LLMI_TYPE_F32, "group: fp32 weights are not part of grouped launches");
     LLMI_REQUIRE(e.rows >= 1 && e.rows <= 8, "group: each product takes 1..8 input rows");
     LLMI_REQUIRE(e.x != nullptr && e.y != nullptr, "group: null x or y");
     if (int rc = check_shape(*e.m, e.rows)) return rc;

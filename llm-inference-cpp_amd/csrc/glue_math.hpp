@@ -28,6 +28,34 @@ __device__ __forceinline__ float silu_exact(float v, const std::uint64_t* tab) {
   return v / (1.0f + exact::expf_with(-v, tab));
 }
 
+// The scalar part of kernels::dot (kernels.cpp:40-49, dot_scalar as the
+// reference's build vectorises it) on the n < 16 elements left after the
+// 16-lane chunks: 8 fused lanes over one 8-element chunk, then the leftovers
+// (when 4 or more remain, the first 4 products are rounded on their own and
+// added in order, the rest fused), the 8 lanes reduced pairwise, plus the
+// leftovers.
+__device__ __forceinline__ float ref_dot_rest(const float* __restrict__ a, const float* __restrict__ b, int n) {
+  float acc[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) acc[j] = 0.0f;
+  int i = 0;
+  for (; i + 8 <= n; i += 8) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[j] = __builtin_fmaf(a[i + j], b[i + j], acc[j]);
+  }
+  float tail = 0.0f;
+  if (n - i >= 4) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float p = a[i + j] * b[i + j];
+      tail = tail + p;
+    }
+    i += 4;
+  }
+  for (; i < n; ++i) tail = __builtin_fmaf(a[i], b[i], tail);
+  return ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7])) + tail;
+}
+
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));

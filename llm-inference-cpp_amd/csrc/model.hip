@@ -159,25 +159,7 @@ __device__ __forceinline__ float ref_dot(const float* __restrict__ a, const floa
 #pragma unroll
   for (int j = 0; j < 4; ++j) s4[j] = s8[j] + s8[j + 4];
   const float head = (s4[0] + s4[2]) + (s4[1] + s4[3]);
-  float acc[8];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) acc[j] = 0.0f;
-  for (; i + 8 <= n; i += 8) {
-#pragma unroll
-    for (int j = 0; j < 8; ++j) acc[j] = __builtin_fmaf(a[i + j], b[i + j], acc[j]);
-  }
-  float tail = 0.0f;
-  if (n - i >= 4) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const float p = a[i + j] * b[i + j];
-      tail = tail + p;
-    }
-    i += 4;
-  }
-  for (; i < n; ++i) tail = __builtin_fmaf(a[i], b[i], tail);
-  const float rest = ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7])) + tail;
-  return head + rest;
+  return head + ref_dot_rest(a + i, b + i, n - i);
 }
 
 __device__ __forceinline__ float recip_float(double s) { return static_cast<float>(1.0 / s); }
@@ -892,6 +874,15 @@ int dev_matrix(llmi_hip_model* m, const float* src, std::size_t out, std::size_t
   dm->in = in;
   dm->nblk = ceil_div(in, kBlock);
   dm->ntiles = ceil_div(out, kTileRows);
+  if (m->type == LLMI_TYPE_F32) {  // row-major floats (weight.cpp:17: kept as they are)
+    dm->code_bytes = out * in * sizeof(float);
+    dm->scale_bytes = 0;
+    if (int rc = dev_alloc(m, reinterpret_cast<void**>(&dm->codes), dm->code_bytes)) return rc;
+    LLMI_TRY_HIP(hipMemcpyAsync(dm->codes, src, dm->code_bytes,
+                                src_on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice, library_stream()));
+    LLMI_TRY_HIP(hipStreamSynchronize(library_stream()));
+    return LLMI_OK;
+  }
   dm->code_bytes = dm->ntiles * dm->nblk * kTileRows * block_code_bytes(m->type);
   dm->scale_bytes = dm->ntiles * dm->nblk * kTileRows * sizeof(float);
   if (int rc = dev_alloc(m, reinterpret_cast<void**>(&dm->codes), dm->code_bytes)) return rc;
@@ -967,8 +958,8 @@ int create_model(const llmi_model_config* cfg, const float* const* t, int type, 
                  llmi_hip_model** out) {
   LLMI_REQUIRE_INIT();
   LLMI_REQUIRE(cfg != nullptr && t != nullptr && out != nullptr, "model_create: null pointer");
-  LLMI_REQUIRE(type == LLMI_TYPE_Q8_0 || type == LLMI_TYPE_Q4_0,
-               "model_create: type must be Q8_0 or Q4_0 (the f32 path is not part of this library)");
+  LLMI_REQUIRE(type == LLMI_TYPE_Q8_0 || type == LLMI_TYPE_Q4_0 || type == LLMI_TYPE_F32,
+               "model_create: type must be Q8_0, Q4_0 or F32");
   if (int rc = check_config(*cfg)) return rc;
   *out = nullptr;
   auto m = std::make_unique<llmi_hip_model>();
@@ -1020,7 +1011,10 @@ int create_model(const llmi_model_config* cfg, const float* const* t, int type, 
     (void)hipFree(staging);
     m->allocations.erase(std::find(m->allocations.begin(), m->allocations.end(), static_cast<void*>(staging)));
   }
-  if (int rc2 = build_decode(m.get())) return cleanup(rc2);
+  // The fused one-token step (grouped quantized GEMVs) exists for Q8_0 / Q4_0;
+  // an fp32 model decodes through the per-operation path.
+  if (m->type != LLMI_TYPE_F32)
+    if (int rc2 = build_decode(m.get())) return cleanup(rc2);
   // inv_freq[i] = 1 / theta^(2i/d) in float, as transformer.cpp:59-66.
   m->inv_freq.resize(m->hd / 2);
   for (std::size_t i = 0; i < m->hd / 2; ++i) {
@@ -1207,7 +1201,8 @@ int forward_rows(llmi_hip_model* m, llmi_hip_cache* cache, std::size_t T, std::s
 int forward_device(llmi_hip_model* m, llmi_hip_cache* cache, std::size_t T, bool all_positions, hipStream_t s,
                    float* trace = nullptr) {
   const int nh = static_cast<int>(m->c.num_heads), nkv = static_cast<int>(m->c.num_kv_heads);
-  if (T == 1 && trace == nullptr && decode_attention_fits(nh, nkv, static_cast<int>(m->hd), cache->len + 1))
+  if (T == 1 && trace == nullptr && m->type != LLMI_TYPE_F32 &&
+      decode_attention_fits(nh, nkv, static_cast<int>(m->hd), cache->len + 1))
     return decode_step(m, cache, s);
   const std::size_t first = all_positions ? 0 : T - 1;
   return forward_rows(m, cache, T, first, T - first, false, s, trace);

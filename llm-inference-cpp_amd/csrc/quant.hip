@@ -328,6 +328,7 @@ int launch_relayout_to_planar(const DeviceMatrix& m, std::uint8_t* pdata, float*
 }
 
 int launch_dequantize_rows(const DeviceMatrix& m, const std::int32_t* ids, std::size_t n, float* dst, hipStream_t s) {
+  if (m.type == LLMI_TYPE_F32) return launch_gather_f32(m, ids, n, dst, s);
   if (n == 0 || m.in == 0) return LLMI_OK;
   LLMI_REQUIRE(n <= 65535, "dequantize_rows: at most 65535 rows per call");
   const dim3 g(grid_for(m.in, 256), static_cast<unsigned>(n));

@@ -3,8 +3,8 @@
 // GPU quantizer packs it straight into the device layout); copies share the
 // device matrix, which is freed with the last copy.  matmul() and row() take
 // and return host memory like the reference's and return with the result
-// complete.  Type::F32 weights are not part of this GPU path: quantized()
-// with F32, from_float(), and matmul()/row() on them throw.
+// complete.  Type::F32 weights (from_float(), quantized() with F32) run the
+// reference's kernels::matmul arithmetic on the GPU, bit for bit.
 #pragma once
 
 #include <cstddef>
@@ -43,9 +43,12 @@ class Weight {
   [[nodiscard]] const llmi_hip_weight* device() const { return dev_.get(); }
 
  private:
+  void upload_f32(std::size_t in) const;  // from_float's matrix, once its shape is known
+
   quant::Type type_ = quant::Type::F32;
-  std::size_t out_ = 0, in_ = 0;
-  std::shared_ptr<llmi_hip_weight> dev_;
+  mutable std::size_t out_ = 0, in_ = 0;
+  mutable std::shared_ptr<llmi_hip_weight> dev_;
+  mutable std::shared_ptr<const std::vector<float>> pending_;
 };
 
 }  // namespace llmi

@@ -83,8 +83,9 @@ void KVCache::reset() {
 }
 
 Result<Transformer> Transformer::load(const ModelConfig& cfg, const TensorReader& read, quant::Type weight_type) {
-  if (weight_type != quant::Type::Q8_0 && weight_type != quant::Type::Q4_0)
-    return fail("load: the GPU path runs Q8_0 and Q4_0 weights only");
+  const int abi_type = weight_type == quant::Type::Q8_0   ? LLMI_TYPE_Q8_0
+                       : weight_type == quant::Type::Q4_0 ? LLMI_TYPE_Q4_0
+                                                          : LLMI_TYPE_F32;
   if (cfg.num_heads == 0 || cfg.hidden_size % cfg.num_heads != 0) return fail("load: inconsistent head counts");
   try {
     quant::init_for_host_api();
@@ -105,8 +106,7 @@ Result<Transformer> Transformer::load(const ModelConfig& cfg, const TensorReader
   for (const auto& t : tensors) ptrs.push_back(t.data());
   const llmi_model_config abi = abi_config(cfg);
   llmi_hip_model* m = nullptr;
-  if (llmi_hip_model_create(&abi, ptrs.data(), weight_type == quant::Type::Q8_0 ? LLMI_TYPE_Q8_0 : LLMI_TYPE_Q4_0,
-                            &m) != LLMI_OK)
+  if (llmi_hip_model_create(&abi, ptrs.data(), abi_type, &m) != LLMI_OK)
     return hip_error("load");
   Transformer t;
   t.cfg_ = cfg;

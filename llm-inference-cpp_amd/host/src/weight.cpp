@@ -22,12 +22,30 @@ std::shared_ptr<llmi_hip_weight> own(llmi_hip_weight* w) {
 int abi_type(quant::Type t) {
   if (t == quant::Type::Q8_0) return LLMI_TYPE_Q8_0;
   if (t == quant::Type::Q4_0) return LLMI_TYPE_Q4_0;
-  throw std::invalid_argument("Weight: f32 weights are not part of the GPU quantized path");
+  return LLMI_TYPE_F32;
 }
 }  // namespace
 
-Weight Weight::from_float(std::vector<float> /*w*/) {
-  throw std::invalid_argument("Weight: f32 weights are not part of the GPU quantized path");
+// weight.cpp:9-14: the fp32 matrix is kept as it is.  Its shape arrives with
+// the first matmul()/row() call, which uploads it (row-major [out][in]).
+Weight Weight::from_float(std::vector<float> w) {
+  quant::init_for_host_api();
+  Weight weight;
+  weight.type_ = quant::Type::F32;
+  weight.pending_ = std::make_shared<const std::vector<float>>(std::move(w));
+  return weight;
+}
+
+void Weight::upload_f32(std::size_t in) const {
+  if (dev_ != nullptr || pending_ == nullptr) return;
+  if (in == 0 || pending_->size() % in != 0) throw std::invalid_argument("Weight: fp32 size is not a multiple of in");
+  llmi_hip_weight* h = nullptr;
+  check(llmi_hip_weight_quantize(pending_->data(), pending_->size() / in, in, LLMI_TYPE_F32, &h),
+        "llmi_hip_weight_quantize");
+  dev_ = own(h);
+  out_ = pending_->size() / in;
+  in_ = in;
+  pending_.reset();
 }
 
 Weight Weight::quantized(const std::vector<float>& w, std::size_t out, std::size_t in, quant::Type type) {
@@ -69,9 +87,13 @@ Result<Weight> Weight::from_gguf(const void* raw, std::size_t nbytes, std::size_
   return weight;
 }
 
-bool Weight::empty() const { return dev_ == nullptr || out_ == 0 || in_ == 0; }
+bool Weight::empty() const {
+  if (pending_ != nullptr) return pending_->empty();
+  return dev_ == nullptr || out_ == 0 || in_ == 0;
+}
 
 std::size_t Weight::byte_size() const {
+  if (pending_ != nullptr) return pending_->size() * sizeof(float);  // weight.cpp:26-28
   if (dev_ == nullptr) return 0;
   std::size_t bytes = 0;
   llmi_hip_weight_info(dev_.get(), nullptr, nullptr, nullptr, &bytes);
@@ -80,11 +102,13 @@ std::size_t Weight::byte_size() const {
 
 void Weight::matmul(const float* x, std::size_t rows, std::size_t in, std::size_t out, const float* bias,
                     float* y) const {
+  upload_f32(in);
   if (dev_ == nullptr) throw std::logic_error("Weight::matmul on an empty weight");
   check(llmi_hip_matmul(dev_.get(), x, rows, in, out, bias, y), "llmi_hip_matmul");
 }
 
-void Weight::row(std::size_t index, std::size_t /*in*/, float* dst) const {
+void Weight::row(std::size_t index, std::size_t in, float* dst) const {
+  upload_f32(in);
   if (dev_ == nullptr) throw std::logic_error("Weight::row on an empty weight");
   check(llmi_hip_dequantize_row(dev_.get(), index, dst), "llmi_hip_dequantize_row");
 }

@@ -185,12 +185,23 @@ TEST(Weight, FromGgufMatchesTheReferenceKnownAnswers) {
   EXPECT_TRUE(!llmi::Weight::from_gguf(q4.data(), q4.size(), 1, 32, 0).ok());  // F32 is not Q8_0/Q4_0
 }
 
-TEST(Weight, Float32WeightsAreRejected) {
-  bool threw = false;
-  try {
-    (void)llmi::Weight::quantized(std::vector<float>(4, 1.0F), 2, 2, Type::F32);
-  } catch (const std::invalid_argument&) {
-    threw = true;
+// transformer_test.cpp:30-44 (Kernels.MatmulWithBias) through fp32 Weights:
+// kernels::matmul on the GPU, from_float (shape at the first call) and
+// quantized(..., F32).
+TEST(Weight, Float32WeightsRunTheReferenceMatmul) {
+  const std::vector<float> x = {1, 2, 3, 4, 5, 6};
+  const std::vector<float> w = {1, 0, -1, 0.5F, 0.5F, 0.5F};
+  const float bias[] = {10, -1};
+  for (int how = 0; how < 2; ++how) {
+    const llmi::Weight weight = how == 0 ? llmi::Weight::from_float(w) : llmi::Weight::quantized(w, 2, 3, Type::F32);
+    float y[4];
+    weight.matmul(x.data(), 2, 3, 2, bias, y);
+    EXPECT_TRUE(y[0] == 1 - 3 + 10.0F && y[1] == 3 - 1.0F && y[2] == 4 - 6 + 10.0F && y[3] == 7.5F - 1);
+    weight.matmul(x.data(), 2, 3, 2, nullptr, y);
+    EXPECT_TRUE(y[0] == -2.0F);
+    EXPECT_TRUE(weight.byte_size() == 24);
+    float r[3];
+    weight.row(1, 3, r);
+    EXPECT_TRUE(r[0] == 0.5F && r[1] == 0.5F && r[2] == 0.5F);
   }
-  EXPECT_TRUE(threw);
 }

@@ -103,9 +103,7 @@ def test_argmax_takes_the_first_maximum():
 def test_tiny_models_match_reference(golden):
     rec, arrays = golden
     g = arrays["tiny_models"]
-    for c in rec["tiny_models"]:
-        if c["type"] == O.F32:
-            continue  # the f32 path is not part of this library
+    for c in rec["tiny_models"]:  # F32, Q8_0 and Q4_0 weights
         m = H.Model(c["cfg"], synth.make_tensors(c["cfg"], c["seed"], c["convention"]), c["type"])
         cache = m.new_cache(len(g["prompt"]) + len(g["steps"]))
         pre = m.forward_cached(cache, g["prompt"], all_positions=True)
@@ -171,7 +169,7 @@ def test_bad_input_is_reported_like_the_reference():
     with pytest.raises(H.HipError, match="max_len must be positive"):
         m.new_cache(0)
     with pytest.raises(H.HipError):
-        H.Model(cfg, synth.make_tensors(cfg, 6, "tiny"), H.F32)
+        H.Model(cfg, synth.make_tensors(cfg, 6, "tiny"), 7)  # not a weight type
 
 
 # ---------------------------------------------------- full-size models
