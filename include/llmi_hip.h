@@ -135,7 +135,10 @@ int llmi_hip_quantize_dev(const float* w_dev, size_t out, size_t in, int type, u
 int llmi_hip_weight_upload(const uint8_t* data, const float* scales, size_t out, size_t in, int type,
                            llmi_hip_weight** weight);
 /* Weight::quantized (src/model/weight.cpp:16-22): quantizes an fp32 matrix on
- * the GPU straight into the device layout.  w is a host pointer. */
+ * the GPU straight into the device layout.  w is a host pointer.  With
+ * LLMI_TYPE_F32 the matrix is kept as fp32 (Weight::from_float,
+ * weight.cpp:9-14) and products run kernels::matmul (kernels.cpp:97-113):
+ * y = dot(x_r, w_o) + bias with the reference's dot arithmetic, bit-exact. */
 int llmi_hip_weight_quantize(const float* w, size_t out, size_t in, int type, llmi_hip_weight** weight);
 int llmi_hip_weight_quantize_dev(const float* w_dev, size_t out, size_t in, int type, llmi_hip_weight** weight);
 int llmi_hip_weight_free(llmi_hip_weight* weight);
@@ -152,7 +155,8 @@ int llmi_hip_weight_free(llmi_hip_weight* weight);
  * shape. */
 int llmi_hip_weight_from_gguf(const void* blocks, size_t nbytes, size_t out, size_t in, int gguf_type,
                               llmi_hip_weight** weight);
-/* Copies the weight back into the reference's planar layout. */
+/* Copies the weight back into the reference's planar layout (an fp32 weight:
+ * its out x in floats into data, scales untouched). */
 int llmi_hip_weight_download(const llmi_hip_weight* weight, uint8_t* data, float* scales);
 /* Shape/type queries; byte_size is QuantizedMatrix::byte_size
  * (quant.hpp:47): packed code bytes + 4 * number of scales. */
@@ -236,10 +240,11 @@ int llmi_hip_argmax_dev(const float* x, size_t n, int32_t* out, void* stream);
 typedef struct llmi_hip_model llmi_hip_model; /* device-resident quantized decoder */
 typedef struct llmi_hip_cache llmi_hip_cache; /* device KV cache of one sequence */
 
-/* Replaces llmi::Transformer::load(model, Q8_0 | Q4_0)
+/* Replaces llmi::Transformer::load(model, F32 | Q8_0 | Q4_0)
  * (include/llmi/model/transformer.hpp:58, src/model/transformer.cpp:26-67):
  * quantizes every matrix (embedding, q/k/v/o, gate/up/down, untied lm_head)
- * on the GPU; RMSNorm weights and q/k/v biases stay fp32.  `tensors` holds
+ * on the GPU, or keeps them fp32 with LLMI_TYPE_F32; RMSNorm weights and
+ * q/k/v biases stay fp32.  `tensors` holds
  * one fp32 array per tensor in the reference's expected_tensors() order
  * (src/model/model.cpp:135-162): embed; per layer input_layernorm, q, k, v,
  * [q_bias, k_bias, v_bias], o, post_attention_layernorm, gate, up, down;

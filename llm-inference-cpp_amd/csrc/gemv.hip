@@ -32,6 +32,8 @@
 // qgemm_exact (batch > 8, the exact prefill path): 64, 32 or 16 input rows
 // x 64 outputs per workgroup, 4 x 4 / 2 x 4 / 1 x 4 chains per thread,
 // operands from LDS.
+//
+// fp32 weights take kernels::matmul instead (f32.hip).
 #include <algorithm>
 #include <vector>
 
