@@ -303,8 +303,55 @@ int llmi_hip_model_generate_greedy(llmi_hip_model* model, const int32_t* prompt,
 enum { LLMI_SCORE_EXACT = 0, LLMI_SCORE_MFMA_HEAD = 1, LLMI_SCORE_MFMA = 2 };
 int llmi_hip_model_chunk_nll(llmi_hip_model* model, const int32_t* tokens, size_t n, size_t t_start, int mode,
                              double* nll);
-/* GPU time of the last generate_greedy call: the prompt prefill and the
- * decode loop (HIP events; the reference's llmi-generate --json reports the
+/* ---------------------------------------------------------- token sampling */
+
+/* SamplingConfig (include/llmi/model/sampling.hpp:20-24). */
+typedef struct llmi_hip_sampling {
+  float temperature; /* <= 0: the first maximum, nothing drawn (sampling.cpp:61) */
+  size_t top_k;      /* 0 (or > n): no top-k filter */
+  float top_p;       /* >= 1: no nucleus filter */
+} llmi_hip_sampling;
+
+/* llmi::sample (include/llmi/model/sampling.hpp:39, src/model/sampling.cpp:
+ * 60-77) with its random number given: `target` is the number sample() draws
+ * from the caller's generator, std::uniform_real_distribution<double>(0, 1)
+ * on std::mt19937_64, once per call when temperature > 0 (no draw, and
+ * `target` unused, otherwise).  *id is the reference's index for the same
+ * logits, configuration and draw, bit for bit.  Logits may be -inf (masked
+ * entries); NaN, or +inf after the division by temperature, are rejected
+ * (LLMI_ERR_ARG: the reference's ranking is undefined there); every entry
+ * -inf gives index 0, as the reference's fallback to argmax does.
+ * _dev: logits in device memory, queued on `stream` (NULL = the library's),
+ * synchronous (the index returns to the host).  n >= 1. */
+int llmi_hip_sample(const float* logits, size_t n, const llmi_hip_sampling* cfg, double target, int32_t* id);
+int llmi_hip_sample_dev(const float* logits, size_t n, const llmi_hip_sampling* cfg, double target, int32_t* id,
+                        void* stream);
+/* llmi::sampling_probabilities (sampling.hpp:32, sampling.cpp:11-58): the
+ * filtered, renormalised distribution (host pointers), bit for bit. */
+int llmi_hip_sampling_probabilities(const float* logits, size_t n, const llmi_hip_sampling* cfg, float* probs);
+/* Testing aids, no counterpart in the reference: force every double sum of a
+ * sample call onto its sequential pass (same results, slower), and report
+ * which sums of the last call took the sequential pass (bit 0 softmax sum,
+ * 1 top-p sum, 2 running sum of the draw, 3 renormalisation sum). */
+int llmi_hip_sampling_set_exact_only(int on);
+int llmi_hip_sampling_last_paths(int* paths);
+
+/* One serving step on the device: forward_cached of `tokens` (transformer.cpp:
+ * 192-306) and sample() on the last position's logits, which never leave HBM
+ * (the loop of src/server/server.cpp:109-195 and llmi-chat, one call per
+ * token).  `target` as for llmi_hip_sample. */
+int llmi_hip_model_forward_sample(llmi_hip_model* model, llmi_hip_cache* cache, const int32_t* tokens, size_t n,
+                                  const llmi_hip_sampling* cfg, double target, int32_t* id);
+/* generate_greedy_cached with sample() in place of argmax: prefill, then up to
+ * max_new sampled tokens, targets[i] being the draw of step i (room for
+ * max_new; the caller draws them from its generator in order), stopping after
+ * a token in stop_ids.  Timing as for generate_greedy (last_timing). */
+int llmi_hip_model_generate_sampled(llmi_hip_model* model, const int32_t* prompt, size_t n, size_t max_new,
+                                    const llmi_hip_sampling* cfg, const double* targets, const int32_t* stop_ids,
+                                    size_t n_stop, int32_t* ids, size_t* n_ids);
+
+/* GPU time of the last generate_greedy / generate_sampled call: the prompt
+ * prefill and the decode loop (HIP events; the reference's llmi-generate --json reports the
  * same split as wall-clock seconds, apps/llmi-generate/main.cpp:329-345). */
 int llmi_hip_model_last_timing(const llmi_hip_model* model, double* prefill_ms, double* decode_ms);
 

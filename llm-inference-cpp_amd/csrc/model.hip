@@ -1434,6 +1434,73 @@ int llmi_hip_model_generate_greedy(llmi_hip_model* m, const int32_t* prompt, siz
   return LLMI_OK;
 }
 
+// One serving step: forward_cached, then sample() on the last position's
+// logits in HBM (sampling.hip).
+int llmi_hip_model_forward_sample(llmi_hip_model* m, llmi_hip_cache* cache, const int32_t* tokens, size_t n,
+                                  const llmi_hip_sampling* cfg, double target, int32_t* id) {
+  LLMI_REQUIRE_INIT();
+  LLMI_REQUIRE(m != nullptr && cfg != nullptr && id != nullptr, "forward_sample: null pointer");
+  if (int rc = validate(m, cache, tokens, n)) return rc;
+  if (int rc = ensure_workspace(m, n)) return rc;
+  hipStream_t s = library_stream();
+  LLMI_TRY_HIP(hipMemcpyAsync(m->ws.ids, tokens, n * sizeof(std::int32_t), hipMemcpyHostToDevice, s));
+  if (int rc = forward_device(m, cache, n, false, s)) return rc;
+  return sample_device(m->ws.logits, m->V, *cfg, target, id, nullptr, s);
+}
+
+// generate_greedy with sample() per step: the drawn index also lands in the
+// next step's token slot on the device, so the host only reads it (to stop).
+int llmi_hip_model_generate_sampled(llmi_hip_model* m, const int32_t* prompt, size_t n, size_t max_new,
+                                    const llmi_hip_sampling* cfg, const double* targets, const int32_t* stop_ids,
+                                    size_t n_stop, int32_t* ids, size_t* n_ids) {
+  LLMI_REQUIRE_INIT();
+  LLMI_REQUIRE(m != nullptr && cfg != nullptr && ids != nullptr && n_ids != nullptr, "generate_sampled: null pointer");
+  LLMI_REQUIRE(targets != nullptr || max_new == 0 || cfg->temperature <= 0.0f, "generate_sampled: null targets");
+  *n_ids = 0;
+  llmi_hip_cache* cache = nullptr;
+  if (int rc = llmi_hip_model_new_cache(m, n + max_new, &cache)) return rc;
+  std::unique_ptr<llmi_hip_cache, int (*)(llmi_hip_cache*)> guard(cache, llmi_hip_cache_free);
+  if (int rc = validate(m, cache, prompt, n)) return rc;
+  if (max_new == 0) return LLMI_OK;
+  if (int rc = ensure_workspace(m, n)) return rc;
+  Workspace& w = m->ws;
+  hipStream_t s = library_stream();
+  hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
+  for (auto& e : ev) LLMI_TRY_HIP(hipEventCreate(&e));
+  struct EvGuard {
+    hipEvent_t* e;
+    ~EvGuard() {
+      for (int i = 0; i < 3; ++i)
+        if (e[i] != nullptr) (void)hipEventDestroy(e[i]);
+    }
+  } ev_guard{ev};
+  LLMI_TRY_HIP(hipMemcpyAsync(w.ids, prompt, n * sizeof(std::int32_t), hipMemcpyHostToDevice, s));
+  LLMI_TRY_HIP(hipEventRecord(ev[0], s));
+  if (int rc = forward_device(m, cache, n, false, s)) return rc;
+  LLMI_TRY_HIP(hipEventRecord(ev[1], s));
+  std::size_t produced = 0;
+  for (std::size_t step = 0; step < max_new; ++step) {
+    std::int32_t next = 0;
+    const double target = cfg->temperature > 0.0f ? targets[step] : 0.0;
+    if (int rc = sample_device(w.logits, m->V, *cfg, target, &next, w.ids, s)) return rc;
+    ids[step] = next;
+    produced = step + 1;
+    bool stop = false;
+    for (std::size_t k = 0; k < n_stop; ++k) stop = stop || stop_ids[k] == next;
+    if (stop || step + 1 == max_new) break;
+    if (int rc = forward_device(m, cache, 1, false, s)) return rc;
+  }
+  LLMI_TRY_HIP(hipEventRecord(ev[2], s));
+  LLMI_TRY_HIP(hipStreamSynchronize(s));
+  float pre = 0.0f, dec = 0.0f;
+  LLMI_TRY_HIP(hipEventElapsedTime(&pre, ev[0], ev[1]));
+  LLMI_TRY_HIP(hipEventElapsedTime(&dec, ev[1], ev[2]));
+  m->last_prefill_ms = pre;
+  m->last_decode_ms = dec;
+  *n_ids = produced;
+  return LLMI_OK;
+}
+
 int llmi_hip_model_chunk_nll(llmi_hip_model* m, const int32_t* tokens, size_t n, size_t t_start, int mode,
                              double* nll) {
   LLMI_REQUIRE_INIT();

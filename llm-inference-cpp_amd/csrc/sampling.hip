@@ -1,0 +1,818 @@
+// Token sampling on the GPU: the reference's sampling_probabilities and
+// sample() (src/model/sampling.cpp:11-77) on logits in HBM, with the
+// reference's results bit for bit.  The random number stays the caller's:
+// sample() draws one std::uniform_real_distribution<double>(0, 1) number from
+// its std::mt19937_64 per call (temperature > 0), and the device entry points
+// take that number (`target`).
+//
+// The reference's arithmetic is elementwise except for four sequential double
+// sums: the softmax denominator (index order), the top-p running sum and the
+// renormalisation sum (both in ranking order), and the running sum that
+// sample() compares with its draw (index order).  Each is taken here as a
+// parallel sum P with a bound on its distance from the sequential sum S: for
+// m non-negative terms both lie within (m-1)u of the exact sum (u = 2^-53,
+// whatever the summation tree), so |S - P| <= sigma*P with
+// sigma = 4u*(m + 65536) (the 65536 covers the empty slots of the reduction
+// trees).  A decision is taken from P only when every S in
+// [P(1-sigma), P(1+sigma)] gives the same decision -- the same float
+// reciprocal, the same first index whose running sum reaches a threshold --
+// and the sum is otherwise recomputed sequentially in the reference's order
+// (by one thread, the block staging the terms through LDS).  The sequential
+// passes are rare (a threshold within ~1e-11 relative of a running sum).
+//
+// Kernels of one sampling call (temperature > 0), all on one stream:
+//   smp_max    max of logits / temperature (float division), NaN / +inf flags
+//   smp_exp    e = expf(x / T - max) (the exact expf), sum -> inv = float(1/sum)
+//   smp_scale  p = e * inv; ranking keys (float bits, index) when needed
+//   [rocprim radix sort, descending, stable: std::stable_sort's order]
+//   smp_keep   top-k, top-p, bounds on the renormalisation sum
+//   smp_draw   the filtered probabilities (bounded) and the first index whose
+//              running sum reaches target
+// When the renormalisation sum's bound leaves the drawn index open (rare),
+// the host runs smp_seq_sum2 (the exact sum, ranking order) and smp_draw
+// again.  sampling_probabilities always takes the exact sum.
+
+#include <hip/hip_runtime.h>
+
+#include <cstring>  // rocprim's headers use memset on the host
+#include <rocprim/device/device_radix_sort.hpp>
+
+#include <cstdint>
+#include <vector>
+
+#include "common.hpp"
+#include "exact_math.hpp"
+#include "glue_math.hpp"
+
+namespace llmi_hip {
+namespace {
+
+constexpr int kSmpThreads = 256;
+constexpr int kSmpWaves = kSmpThreads / 64;
+constexpr int kSmpBlocks = 128;               // slices of the vocabulary, one workgroup each
+constexpr int kSeqChunk = kSmpThreads * 8;    // terms per LDS stage of the sequential sums
+
+enum : int { kFlagNaN = 1, kFlagPosInf = 2, kFlagAllNegInf = 4 };
+constexpr int kFlagBad = kFlagNaN | kFlagPosInf | kFlagAllNegInf;
+enum : int { kSeqSoftmax = 1, kSeqTopP = 2, kSeqDraw = 4, kSeqSum2 = 8 };
+
+struct SmpState {
+  float mx;         // max of logits / temperature
+  int flags;        // kFlag*
+  float inv;        // float(1 / softmax sum)
+  int keep;         // kept entries (top-k, top-p)
+  double s2_lo;     // the renormalisation sum lies in [s2_lo, s2_hi]; equal when exact
+  double s2_hi;
+  float p_thr;      // kept: p > p_thr, or p == p_thr and index <= idx_last
+  int idx_last;
+  int id;           // the drawn index
+  int decided;      // 1 when id is the reference's
+  int seq_paths;    // kSeq*: which sums needed the sequential pass (diagnostics)
+  unsigned counter; // last-block handshake, reset by each kernel's last block
+};
+
+struct SmpWork {
+  float* p;                  // e, then p = e * inv
+  std::uint32_t* keys;       // ranking keys: bits of p (p >= +0)
+  std::uint32_t* keys_sorted;
+  std::int32_t* idx;
+  std::int32_t* idx_sorted;
+  double* part_d;            // per-block partials
+  int* part_i;
+  float* part_f;
+  SmpState* st;
+};
+
+__device__ __forceinline__ float recip_float(double s) { return static_cast<float>(1.0 / s); }
+__device__ __forceinline__ double smp_sigma(int m) { return 4.0 * (static_cast<double>(m) + 65536.0) * 0x1p-53; }
+
+struct Slice {
+  int lo, hi;
+};
+__device__ __forceinline__ Slice slice_of(int m, int b, int blocks) {
+  const int per = (m + blocks - 1) / blocks;
+  const int lo = min(m, b * per);
+  return Slice{lo, min(m, lo + per)};
+}
+
+__device__ __forceinline__ float block_max_f(float v, float* red) {
+  v = wave_max(v);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  float r = red[0];
+  for (int w = 1; w < kSmpWaves; ++w) r = fmaxf(r, red[w]);
+  __syncthreads();
+  return r;
+}
+__device__ __forceinline__ int block_or(int v, int* red) {
+  for (int o = 32; o > 0; o >>= 1) v |= __shfl_xor(v, o, 64);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  int r = 0;
+  for (int w = 0; w < kSmpWaves; ++w) r |= red[w];
+  __syncthreads();
+  return r;
+}
+__device__ __forceinline__ int block_min_i(int v, int* red) {
+  for (int o = 32; o > 0; o >>= 1) v = min(v, __shfl_xor(v, o, 64));
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  int r = red[0];
+  for (int w = 1; w < kSmpWaves; ++w) r = min(r, red[w]);
+  __syncthreads();
+  return r;
+}
+__device__ __forceinline__ int block_max_i(int v, int* red) {
+  for (int o = 32; o > 0; o >>= 1) v = max(v, __shfl_xor(v, o, 64));
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  int r = red[0];
+  for (int w = 1; w < kSmpWaves; ++w) r = max(r, red[w]);
+  __syncthreads();
+  return r;
+}
+__device__ __forceinline__ double block_sum_d(double v, double* red) {
+  v = wave_sum(v);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  double r = red[0];
+  for (int w = 1; w < kSmpWaves; ++w) r = r + red[w];
+  __syncthreads();
+  return r;
+}
+
+// Exclusive prefix of v over the block's threads in thread order (an
+// inclusive Hillis-Steele scan in LDS, read one slot back); *total = the sum.
+__device__ __forceinline__ double block_exclusive_scan(double v, double* sh, double* total) {
+  const int t = threadIdx.x;
+  sh[t] = v;
+  __syncthreads();
+  for (int off = 1; off < kSmpThreads; off <<= 1) {
+    const double add = t >= off ? sh[t - off] : 0.0;
+    __syncthreads();
+    sh[t] = sh[t] + add;
+    __syncthreads();
+  }
+  const double excl = t > 0 ? sh[t - 1] : 0.0;
+  *total = sh[kSmpThreads - 1];
+  __syncthreads();
+  return excl;
+}
+
+// Thread 0 publishes the block's partials (already stored) and learns whether
+// it is the last block of the grid to do so.
+__device__ __forceinline__ bool arrive_last(unsigned* counter) {
+  __threadfence();
+  const unsigned done = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+  return done == gridDim.x - 1;
+}
+__device__ __forceinline__ void reset_counter(unsigned* counter) {
+  __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <typename T>
+__device__ __forceinline__ T load_relaxed(const T* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// First j in [lo, hi) with (base + v(lo) + ... + v(j)) * factor >= t, or hi.
+// Every thread of the block takes part; the running sums are a tree over the
+// terms (a contiguous run per thread, then the block scan).
+template <typename F>
+__device__ int slice_first_reach(F v, int lo, int hi, double base, double factor, double t, double* sh, int* red_i) {
+  const int len = hi - lo;
+  const int per = (len + kSmpThreads - 1) / kSmpThreads;
+  const int a = lo + min(len, static_cast<int>(threadIdx.x) * per);
+  const int e = min(hi, a + per);
+  double cs = 0.0;
+  for (int j = a; j < e; ++j) cs = cs + static_cast<double>(v(j));
+  double total;
+  const double excl = block_exclusive_scan(cs, sh, &total);
+  double run = base + excl;
+  int found = hi;
+  for (int j = a; j < e; ++j) {
+    run = run + static_cast<double>(v(j));
+    if (run * factor >= t) {
+      found = j;
+      break;
+    }
+  }
+  return block_min_i(found, red_i);
+}
+
+// base + v(lo) + ... + v(hi - 1), a tree as above.
+template <typename F>
+__device__ double slice_sum(F v, int lo, int hi, double* red) {
+  double s = 0.0;
+  for (int j = lo + static_cast<int>(threadIdx.x); j < hi; j += kSmpThreads) s = s + static_cast<double>(v(j));
+  return block_sum_d(s, red);
+}
+
+// The reference's own sequential double running sum of v(0), v(1), ...,
+// v(m-1): thread 0 adds while waves 1..3 stage the next kSeqChunk terms into
+// the other half of `stage` (2 * kSeqChunk floats).  With `has_stop`, stops at
+// the first j whose running sum reaches stop_at and returns j; else returns m.
+// *sum = the running sum where it stopped.  Every thread must call it.  The
+// stop index goes through two LDS slots used in alternate rounds, so thread 0
+// never overwrites a slot another wave has yet to read.
+template <typename F>
+__device__ int block_sequential_sum(F v, int m, bool has_stop, double stop_at, double* sum, float* stage,
+                                    int* stop_slots) {
+  const int t = threadIdx.x;
+  for (int k = t; k < kSeqChunk; k += kSmpThreads) stage[k] = k < m ? v(k) : 0.0f;
+  if (t == 0) {
+    stop_slots[0] = -1;
+    stop_slots[1] = -1;
+  }
+  __syncthreads();
+  double run = 0.0;
+  int buf = 0, stop = -1;
+  for (int c0 = 0; c0 < m; c0 += kSeqChunk) {
+    if (t >= 64) {
+      float* nxt = stage + (buf ^ 1) * kSeqChunk;
+      for (int k = t - 64; k < kSeqChunk; k += kSmpThreads - 64) {
+        const int j = c0 + kSeqChunk + k;
+        nxt[k] = j < m ? v(j) : 0.0f;
+      }
+    }
+    if (t == 0) {
+      const float* cur = stage + buf * kSeqChunk;
+      const int len = min(kSeqChunk, m - c0);
+      for (int k = 0; k < len; ++k) {
+        run = run + static_cast<double>(cur[k]);
+        if (has_stop && run >= stop_at) {
+          stop_slots[buf] = c0 + k;
+          break;
+        }
+      }
+    }
+    __syncthreads();
+    stop = stop_slots[buf];
+    if (stop >= 0) break;
+    buf ^= 1;
+  }
+  if (t == 0) *sum = run;
+  __syncthreads();
+  return stop >= 0 ? stop : m;
+}
+
+// ------------------------------------------------------------------ kernels
+__global__ void __launch_bounds__(kSmpThreads) smp_max(const float* __restrict__ logits, int n, float temp, SmpWork w) {
+  __shared__ float red_f[kSmpWaves];
+  __shared__ int red_i[kSmpWaves];
+  __shared__ bool last;
+  const Slice sl = slice_of(n, blockIdx.x, gridDim.x);
+  float m = -__builtin_inff();
+  int fl = 0;
+  for (int i = sl.lo + static_cast<int>(threadIdx.x); i < sl.hi; i += kSmpThreads) {
+    const float v = logits[i] / temp;
+    if (v != v) fl |= kFlagNaN;
+    if (v == __builtin_inff()) fl |= kFlagPosInf;
+    m = fmaxf(m, v);
+  }
+  m = block_max_f(m, red_f);
+  fl = block_or(fl, red_i);
+  if (threadIdx.x == 0) {
+    w.part_f[blockIdx.x] = m;
+    w.part_i[blockIdx.x] = fl;
+    last = arrive_last(&w.st->counter);
+  }
+  __syncthreads();
+  if (!last) return;
+  __threadfence();
+  float mm = -__builtin_inff();
+  int ff = 0;
+  for (int b = threadIdx.x; b < static_cast<int>(gridDim.x); b += kSmpThreads) {
+    mm = fmaxf(mm, load_relaxed(w.part_f + b));
+    ff |= load_relaxed(w.part_i + b);
+  }
+  mm = block_max_f(mm, red_f);
+  ff = block_or(ff, red_i);
+  if (threadIdx.x == 0) {
+    if (ff == 0 && mm == -__builtin_inff()) ff = kFlagAllNegInf;
+    w.st->mx = mm;
+    w.st->flags = ff;
+    w.st->seq_paths = 0;
+    w.st->decided = 0;
+    reset_counter(&w.st->counter);
+  }
+}
+
+// kernels.cpp:136-146 on x / temperature.
+__global__ void __launch_bounds__(kSmpThreads) smp_exp(const float* __restrict__ logits, int n, float temp, SmpWork w) {
+  __shared__ std::uint64_t tab[32];
+  __shared__ double red_d[kSmpWaves];
+  __shared__ float stage[2 * kSeqChunk];
+  __shared__ int stop[2];
+  __shared__ double seq;
+  __shared__ bool last;
+  if (w.st->flags & kFlagBad) return;
+  if (threadIdx.x < 32) tab[threadIdx.x] = exact::kExp2Tab[threadIdx.x];
+  __syncthreads();
+  const float mx = w.st->mx;
+  const Slice sl = slice_of(n, blockIdx.x, gridDim.x);
+  double part = 0.0;
+  for (int i = sl.lo + static_cast<int>(threadIdx.x); i < sl.hi; i += kSmpThreads) {
+    const float e = exact::expf_with(logits[i] / temp - mx, tab);
+    w.p[i] = e;
+    part = part + static_cast<double>(e);
+  }
+  __threadfence();  // every wave's e: the last block may read them all
+  part = block_sum_d(part, red_d);
+  if (threadIdx.x == 0) {
+    w.part_d[blockIdx.x] = part;
+    last = arrive_last(&w.st->counter);
+  }
+  __syncthreads();
+  if (!last) return;
+  __threadfence();
+  __shared__ float inv_s;
+  if (threadIdx.x == 0) {
+    double sum = 0.0;
+    for (int b = 0; b < static_cast<int>(gridDim.x); ++b) sum = sum + load_relaxed(w.part_d + b);
+    const double slack = smp_sigma(n) * sum;
+    inv_s = recip_float(sum - slack) == recip_float(sum + slack) ? recip_float(sum) : -1.0f;
+  }
+  __syncthreads();
+  float inv = inv_s;
+  if (inv < 0.0f) {  // the bound leaves float(1/sum) open: the sequential sum
+    const float* p = w.p;
+    block_sequential_sum([p](int j) { return p[j]; }, n, false, 0.0, &seq, stage, stop);
+    inv = recip_float(seq);
+    if (threadIdx.x == 0) w.st->seq_paths |= kSeqSoftmax;
+  }
+  if (threadIdx.x == 0) {
+    w.st->inv = inv;
+    reset_counter(&w.st->counter);
+  }
+}
+
+__global__ void __launch_bounds__(kSmpThreads) smp_scale(int n, SmpWork w, int write_keys) {
+  if (w.st->flags & kFlagBad) return;
+  const int i = blockIdx.x * kSmpThreads + threadIdx.x;
+  if (i >= n) return;
+  const float p = w.p[i] * w.st->inv;
+  w.p[i] = p;
+  if (write_keys) {
+    w.keys[i] = __builtin_bit_cast(std::uint32_t, p);
+    w.idx[i] = i;
+  }
+}
+
+// Ranking keys of the already-scaled p (the exact path of an unfiltered draw).
+__global__ void __launch_bounds__(kSmpThreads) smp_keys(int n, SmpWork w) {
+  const int i = blockIdx.x * kSmpThreads + threadIdx.x;
+  if (i >= n) return;
+  w.keys[i] = __builtin_bit_cast(std::uint32_t, w.p[i]);
+  w.idx[i] = i;
+}
+
+// Top-k and top-p (sampling.cpp:28-51) over the first m ranked values
+// (m = k; `vals` is the ranking, or the unranked p when nothing is
+// filtered: then m = n and every entry is kept), and the bounds on the
+// renormalisation sum of the kept ones (:53-57).
+__global__ void __launch_bounds__(kSmpThreads) smp_keep(const float* __restrict__ vals,
+                                                        const std::int32_t* __restrict__ idx_sorted, int m, int n,
+                                                        float top_p, SmpWork w) {
+  __shared__ double red_d[kSmpWaves];
+  __shared__ int red_i[kSmpWaves];
+  __shared__ double sh[kSmpThreads];
+  __shared__ double pre[kSmpBlocks + 1];
+  __shared__ float stage[2 * kSeqChunk];
+  __shared__ int stop[2];
+  __shared__ double seq;
+  __shared__ bool last;
+  if (w.st->flags & kFlagBad) return;
+  auto v = [vals](int j) { return vals[j]; };
+  const Slice sl = slice_of(m, blockIdx.x, gridDim.x);
+  const double part = slice_sum(v, sl.lo, sl.hi, red_d);
+  if (threadIdx.x == 0) {
+    w.part_d[blockIdx.x] = part;
+    last = arrive_last(&w.st->counter);
+  }
+  __syncthreads();
+  if (!last) return;
+  __threadfence();
+  const int nb = gridDim.x;
+  if (threadIdx.x == 0) {
+    pre[0] = 0.0;
+    for (int b = 0; b < nb; ++b) pre[b + 1] = pre[b] + load_relaxed(w.part_d + b);
+  }
+  __syncthreads();
+  const double sigma = smp_sigma(m);
+  int keep = m;
+  bool exact = false;
+  double s2 = 0.0;
+  if (top_p < 1.0f) {
+    const double t = static_cast<double>(top_p);
+    int b_e = nb, b_l = nb;
+    for (int b = nb - 1; b >= 0; --b) {
+      if (pre[b + 1] * (1.0 + sigma) >= t) b_e = b;
+      if (pre[b + 1] * (1.0 - sigma) >= t) b_l = b;
+    }
+    bool decided = false;
+    if (b_e == nb) {
+      decided = true;  // the running sum certainly stays below top_p: keep = m
+    } else if (b_l < nb) {
+      const Slice se = slice_of(m, b_e, nb), sl2 = slice_of(m, b_l, nb);
+      const int j_e = slice_first_reach(v, se.lo, se.hi, pre[b_e], 1.0 + sigma, t, sh, red_i);
+      const int j_l = slice_first_reach(v, sl2.lo, sl2.hi, pre[b_l], 1.0 - sigma, t, sh, red_i);
+      if (j_l < sl2.hi && j_e == j_l) {
+        keep = j_e + 1;
+        decided = true;
+      }
+    }
+    if (!decided) {
+      const int j = block_sequential_sum(v, m, true, t, &seq, stage, stop);
+      keep = j < m ? j + 1 : m;
+      s2 = seq;
+      exact = true;
+      if (threadIdx.x == 0) w.st->seq_paths |= kSeqTopP;
+    }
+  }
+  if (!exact) {
+    // P = running sum through keep - 1.
+    int b_k = 0;
+    while (b_k + 1 < nb && slice_of(m, b_k, nb).hi < keep) ++b_k;
+    const Slice sk = slice_of(m, b_k, nb);
+    const double within = slice_sum(v, sk.lo, keep, red_d);
+    s2 = pre[b_k] + within;
+  }
+  if (threadIdx.x == 0) {
+    const double sg = smp_sigma(keep);
+    w.st->keep = keep;
+    w.st->s2_lo = exact ? s2 : s2 * (1.0 - sg);
+    w.st->s2_hi = exact ? s2 : s2 * (1.0 + sg);
+    if (idx_sorted != nullptr) {
+      w.st->p_thr = vals[keep - 1];
+      w.st->idx_last = idx_sorted[keep - 1];
+    } else {
+      w.st->p_thr = -__builtin_inff();
+      w.st->idx_last = n;
+    }
+    reset_counter(&w.st->counter);
+  }
+}
+
+// The exact renormalisation sum (sampling.cpp:53-56): the kept ranked values
+// in ranking order, sequentially.  One workgroup; nothing to do when the
+// bound already pinned it.
+__global__ void __launch_bounds__(kSmpThreads) smp_seq_sum2(const float* __restrict__ ranked, SmpWork w) {
+  __shared__ float stage[2 * kSeqChunk];
+  __shared__ int stop[2];
+  __shared__ double seq;
+  if (w.st->flags & kFlagBad) return;
+  if (w.st->s2_lo == w.st->s2_hi) return;
+  const int keep = w.st->keep;
+  block_sequential_sum([ranked](int j) { return ranked[j]; }, keep, false, 0.0, &seq, stage, stop);
+  if (threadIdx.x == 0) {
+    w.st->s2_lo = seq;
+    w.st->s2_hi = seq;
+    w.st->seq_paths |= kSeqSum2;
+  }
+}
+
+__device__ __forceinline__ bool kept(float p, int i, float p_thr, int idx_last) {
+  return p > p_thr || (p == p_thr && i <= idx_last);
+}
+__device__ __forceinline__ float renorm(float p, double s) {
+  return static_cast<float>(static_cast<double>(p) / s);
+}
+
+// sample() (sampling.cpp:60-77) given its draw: the filtered probabilities
+// f = float(double(p) / s2) lie in [f(s2_hi), f(s2_lo)]; the first index
+// whose running sum reaches target, or else the last nonzero entry.
+__global__ void __launch_bounds__(kSmpThreads) smp_draw(int n, double target, SmpWork w,
+                                                        std::int32_t* __restrict__ also) {
+  __shared__ double red_d[kSmpWaves];
+  __shared__ int red_i[kSmpWaves];
+  __shared__ double sh[kSmpThreads];
+  __shared__ double pre_lo[kSmpBlocks + 1], pre_hi[kSmpBlocks + 1];
+  __shared__ float stage[2 * kSeqChunk];
+  __shared__ int stop[2];
+  __shared__ double seq;
+  __shared__ bool last;
+  if (w.st->flags & kFlagBad) return;
+  const float* p = w.p;
+  const float p_thr = w.st->p_thr;
+  const int idx_last = w.st->idx_last;
+  const double s2_lo = w.st->s2_lo, s2_hi = w.st->s2_hi;
+  auto f_lo = [=](int i) {
+    const float x = p[i];
+    return kept(x, i, p_thr, idx_last) ? renorm(x, s2_hi) : 0.0f;
+  };
+  auto f_hi = [=](int i) {
+    const float x = p[i];
+    return kept(x, i, p_thr, idx_last) ? renorm(x, s2_lo) : 0.0f;
+  };
+  const Slice sl = slice_of(n, blockIdx.x, gridDim.x);
+  double sum_lo = 0.0, sum_hi = 0.0;
+  int nz_lo = -1, nz_hi = -1;
+  for (int i = sl.lo + static_cast<int>(threadIdx.x); i < sl.hi; i += kSmpThreads) {
+    const float a = f_lo(i), b = f_hi(i);
+    sum_lo = sum_lo + static_cast<double>(a);
+    sum_hi = sum_hi + static_cast<double>(b);
+    if (a > 0.0f) nz_lo = i;
+    if (b > 0.0f) nz_hi = i;
+  }
+  sum_lo = block_sum_d(sum_lo, red_d);
+  sum_hi = block_sum_d(sum_hi, red_d);
+  nz_lo = block_max_i(nz_lo, red_i);
+  nz_hi = block_max_i(nz_hi, red_i);
+  if (threadIdx.x == 0) {
+    w.part_d[2 * blockIdx.x] = sum_lo;
+    w.part_d[2 * blockIdx.x + 1] = sum_hi;
+    w.part_i[2 * blockIdx.x] = nz_lo;
+    w.part_i[2 * blockIdx.x + 1] = nz_hi;
+    last = arrive_last(&w.st->counter);
+  }
+  __syncthreads();
+  if (!last) return;
+  __threadfence();
+  const int nb = gridDim.x;
+  if (threadIdx.x == 0) {
+    pre_lo[0] = 0.0;
+    pre_hi[0] = 0.0;
+    for (int b = 0; b < nb; ++b) {
+      pre_lo[b + 1] = pre_lo[b] + load_relaxed(w.part_d + 2 * b);
+      pre_hi[b + 1] = pre_hi[b] + load_relaxed(w.part_d + 2 * b + 1);
+    }
+  }
+  int last_lo = -1, last_hi = -1;
+  for (int b = threadIdx.x; b < nb; b += kSmpThreads) {
+    last_lo = max(last_lo, load_relaxed(w.part_i + 2 * b));
+    last_hi = max(last_hi, load_relaxed(w.part_i + 2 * b + 1));
+  }
+  last_lo = block_max_i(last_lo, red_i);
+  last_hi = block_max_i(last_hi, red_i);  // (its barriers also publish pre_lo / pre_hi)
+  const double sigma = smp_sigma(n);
+  int b_e = nb, b_l = nb;
+  for (int b = nb - 1; b >= 0; --b) {
+    if (pre_hi[b + 1] * (1.0 + sigma) >= target) b_e = b;
+    if (pre_lo[b + 1] * (1.0 - sigma) >= target) b_l = b;
+  }
+  int id = -1;
+  if (b_e == nb) {
+    // The running sum certainly stays below target: the last nonzero entry.
+    if (last_lo == last_hi) id = last_lo < 0 ? 0 : last_lo;  // (never empty: the top entry is kept and > 0)
+  } else if (b_l < nb) {
+    const Slice se = slice_of(n, b_e, nb), sl2 = slice_of(n, b_l, nb);
+    const int j_e = slice_first_reach(f_hi, se.lo, se.hi, pre_hi[b_e], 1.0 + sigma, target, sh, red_i);
+    const int j_l = slice_first_reach(f_lo, sl2.lo, sl2.hi, pre_lo[b_l], 1.0 - sigma, target, sh, red_i);
+    if (j_l < sl2.hi && j_e == j_l) id = j_e;
+  }
+  if (id < 0 && s2_lo == s2_hi) {
+    // Exact probabilities, the running sum's bound leaves the index open:
+    // the sequential running sum.
+    const int j = block_sequential_sum(f_lo, n, true, target, &seq, stage, stop);
+    id = j < n ? j : (last_lo < 0 ? 0 : last_lo);
+    if (threadIdx.x == 0) w.st->seq_paths |= kSeqDraw;
+  }
+  if (threadIdx.x == 0) {
+    w.st->id = id;
+    w.st->decided = id >= 0 ? 1 : 0;
+    if (id >= 0 && also != nullptr) *also = id;
+    reset_counter(&w.st->counter);
+  }
+}
+
+// sampling_probabilities' result, with the exact renormalisation sum.
+__global__ void __launch_bounds__(kSmpThreads) smp_write(int n, SmpWork w, float* __restrict__ out) {
+  const int i = blockIdx.x * kSmpThreads + threadIdx.x;
+  if (i >= n) return;
+  const float x = w.p[i];
+  out[i] = kept(x, i, w.st->p_thr, w.st->idx_last) ? renorm(x, w.st->s2_lo) : 0.0f;
+}
+
+// ------------------------------------------------------------------- host
+struct SmpBuffers {
+  std::size_t cap = 0;
+  void* base = nullptr;
+  void* sort_tmp = nullptr;
+  std::size_t sort_bytes = 0;
+  float* host_io = nullptr;  // staging for the host-pointer entry points (device)
+  std::int32_t* id_dev = nullptr;
+  SmpWork w{};
+};
+SmpBuffers g_smp;
+bool g_exact_only = false;
+
+int smp_reserve(std::size_t n, hipStream_t s) {
+  if (n <= g_smp.cap) return LLMI_OK;
+  LLMI_TRY_HIP(hipStreamSynchronize(s));
+  if (g_smp.base != nullptr) LLMI_TRY_HIP(hipFree(g_smp.base));
+  if (g_smp.sort_tmp != nullptr) LLMI_TRY_HIP(hipFree(g_smp.sort_tmp));
+  g_smp = SmpBuffers{};
+  std::size_t sort_bytes = 0;
+  LLMI_TRY_HIP(rocprim::radix_sort_pairs_desc(nullptr, sort_bytes, static_cast<const std::uint32_t*>(nullptr),
+                                              static_cast<std::uint32_t*>(nullptr),
+                                              static_cast<const std::int32_t*>(nullptr),
+                                              static_cast<std::int32_t*>(nullptr), static_cast<unsigned>(n), 0, 32, s));
+  auto al = [](std::size_t b) { return (b + 255) & ~static_cast<std::size_t>(255); };
+  const std::size_t vec = al(n * 4);
+  const std::size_t bytes = 7 * vec + al(sizeof(double) * 2 * kSmpBlocks) + al(sizeof(int) * 2 * kSmpBlocks) +
+                            al(sizeof(float) * kSmpBlocks) + al(sizeof(SmpState)) + al(sizeof(std::int32_t));
+  LLMI_TRY_HIP(hipMalloc(&g_smp.base, bytes));
+  const hipError_t e = hipMalloc(&g_smp.sort_tmp, sort_bytes == 0 ? 1 : sort_bytes);
+  if (e != hipSuccess) {
+    (void)hipFree(g_smp.base);
+    g_smp.base = nullptr;
+    return fail(LLMI_ERR_HIP, std::string("sampling workspace: ") + hipGetErrorString(e));
+  }
+  char* c = static_cast<char*>(g_smp.base);
+  auto take = [&c, &al](std::size_t b) {
+    void* r = c;
+    c += al(b);
+    return r;
+  };
+  SmpWork& w = g_smp.w;
+  w.p = static_cast<float*>(take(n * 4));
+  w.keys = static_cast<std::uint32_t*>(take(n * 4));
+  w.keys_sorted = static_cast<std::uint32_t*>(take(n * 4));
+  w.idx = static_cast<std::int32_t*>(take(n * 4));
+  w.idx_sorted = static_cast<std::int32_t*>(take(n * 4));
+  g_smp.host_io = static_cast<float*>(take(n * 4));
+  (void)take(n * 4);  // spare
+  w.part_d = static_cast<double*>(take(sizeof(double) * 2 * kSmpBlocks));
+  w.part_i = static_cast<int*>(take(sizeof(int) * 2 * kSmpBlocks));
+  w.part_f = static_cast<float*>(take(sizeof(float) * kSmpBlocks));
+  w.st = static_cast<SmpState*>(take(sizeof(SmpState)));
+  g_smp.id_dev = static_cast<std::int32_t*>(take(sizeof(std::int32_t)));
+  LLMI_TRY_HIP(hipMemsetAsync(w.st, 0, sizeof(SmpState), s));
+  g_smp.sort_bytes = sort_bytes;
+  g_smp.cap = n;
+  return LLMI_OK;
+}
+
+int smp_check_cfg(const llmi_hip_sampling* cfg, std::size_t n) {
+  LLMI_REQUIRE(cfg != nullptr, "sampling: null config");
+  LLMI_REQUIRE(n >= 1 && n <= (std::size_t{1} << 28), "sampling: need 1 <= n <= 2^28 logits");
+  return LLMI_OK;
+}
+
+int smp_sort(std::size_t n, hipStream_t s) {
+  std::size_t bytes = g_smp.sort_bytes;
+  LLMI_TRY_HIP(rocprim::radix_sort_pairs_desc(g_smp.sort_tmp, bytes, g_smp.w.keys, g_smp.w.keys_sorted, g_smp.w.idx,
+                                              g_smp.w.idx_sorted, static_cast<unsigned>(n), 0, 32, s));
+  return LLMI_OK;
+}
+
+// Everything up to and including smp_keep.  *ranked: whether the ranking
+// (keys_sorted / idx_sorted) was built.
+int smp_front(const float* logits, std::size_t n, const llmi_hip_sampling& cfg, bool need_ranking, hipStream_t s,
+              bool* ranked) {
+  const int ni = static_cast<int>(n);
+  const std::size_t k = cfg.top_k == 0 || cfg.top_k > n ? n : cfg.top_k;
+  const bool filtering = k < n || cfg.top_p < 1.0f;
+  *ranked = filtering || need_ranking;
+  SmpWork& w = g_smp.w;
+  smp_max<<<kSmpBlocks, kSmpThreads, 0, s>>>(logits, ni, cfg.temperature, w);
+  smp_exp<<<kSmpBlocks, kSmpThreads, 0, s>>>(logits, ni, cfg.temperature, w);
+  smp_scale<<<static_cast<unsigned>(ceil_div(n, kSmpThreads)), kSmpThreads, 0, s>>>(ni, w, *ranked ? 1 : 0);
+  LLMI_TRY_HIP(hipGetLastError());
+  if (*ranked) {
+    if (int rc = smp_sort(n, s)) return rc;
+    smp_keep<<<kSmpBlocks, kSmpThreads, 0, s>>>(reinterpret_cast<const float*>(w.keys_sorted), w.idx_sorted,
+                                                static_cast<int>(k), ni, cfg.top_p, w);
+  } else {
+    smp_keep<<<kSmpBlocks, kSmpThreads, 0, s>>>(w.p, nullptr, ni, ni, 2.0f, w);
+  }
+  LLMI_TRY_HIP(hipGetLastError());
+  return LLMI_OK;
+}
+
+int smp_read_state(SmpState* st, hipStream_t s) {
+  LLMI_TRY_HIP(hipMemcpyAsync(st, g_smp.w.st, sizeof(SmpState), hipMemcpyDeviceToHost, s));
+  LLMI_TRY_HIP(hipStreamSynchronize(s));
+  return LLMI_OK;
+}
+
+int smp_bad_input(const SmpState& st) {
+  if (st.flags & kFlagNaN) return fail(LLMI_ERR_ARG, "sampling: logits / temperature has a NaN entry");
+  return fail(LLMI_ERR_ARG, "sampling: logits / temperature has a +inf entry");
+}
+
+}  // namespace
+
+// Draws one index on the device; *id_host receives it.  `also` (device, may
+// be null) receives it too, on the stream, before the host learns it.
+int sample_device(const float* logits, std::size_t n, const llmi_hip_sampling& cfg, double target,
+                  std::int32_t* id_host, std::int32_t* also, hipStream_t s) {
+  if (int rc = smp_check_cfg(&cfg, n)) return rc;
+  if (int rc = smp_reserve(n, s)) return rc;
+  if (cfg.temperature <= 0.0f) {  // sampling.cpp:61: the first maximum, nothing drawn
+    std::int32_t* dst = also != nullptr ? also : g_smp.id_dev;
+    if (int rc = llmi_hip_argmax_dev(logits, n, dst, s)) return rc;
+    LLMI_TRY_HIP(hipMemcpyAsync(id_host, dst, sizeof(std::int32_t), hipMemcpyDeviceToHost, s));
+    LLMI_TRY_HIP(hipStreamSynchronize(s));
+    return LLMI_OK;
+  }
+  bool ranked = false;
+  if (int rc = smp_front(logits, n, cfg, g_exact_only, s, &ranked)) return rc;
+  SmpWork& w = g_smp.w;
+  const int ni = static_cast<int>(n);
+  if (g_exact_only) smp_seq_sum2<<<1, kSmpThreads, 0, s>>>(reinterpret_cast<const float*>(w.keys_sorted), w);
+  smp_draw<<<kSmpBlocks, kSmpThreads, 0, s>>>(ni, target, w, also);
+  LLMI_TRY_HIP(hipGetLastError());
+  SmpState st{};
+  if (int rc = smp_read_state(&st, s)) return rc;
+  if (st.flags & kFlagAllNegInf) {
+    // Every logit is -inf: the reference's probabilities are NaN and its
+    // draw falls through to argmax(logits), the first entry.
+    *id_host = 0;
+    if (also != nullptr) LLMI_TRY_HIP(hipMemcpyAsync(also, id_host, sizeof(std::int32_t), hipMemcpyHostToDevice, s));
+    LLMI_TRY_HIP(hipStreamSynchronize(s));
+    return LLMI_OK;
+  }
+  if (st.flags & kFlagBad) return smp_bad_input(st);
+  if (!st.decided) {
+    // The exact renormalisation sum, which needs the ranking.
+    if (!ranked) {
+      smp_keys<<<static_cast<unsigned>(ceil_div(n, kSmpThreads)), kSmpThreads, 0, s>>>(ni, w);
+      LLMI_TRY_HIP(hipGetLastError());
+      if (int rc = smp_sort(n, s)) return rc;
+    }
+    smp_seq_sum2<<<1, kSmpThreads, 0, s>>>(reinterpret_cast<const float*>(w.keys_sorted), w);
+    smp_draw<<<kSmpBlocks, kSmpThreads, 0, s>>>(ni, target, w, also);
+    LLMI_TRY_HIP(hipGetLastError());
+    if (int rc = smp_read_state(&st, s)) return rc;
+    if (!st.decided) return fail(LLMI_ERR_STATE, "sampling: the exact draw did not decide (internal error)");
+  }
+  *id_host = st.id;
+  return LLMI_OK;
+}
+
+}  // namespace llmi_hip
+
+using namespace llmi_hip;
+
+int llmi_hip_sample_dev(const float* logits, size_t n, const llmi_hip_sampling* cfg, double target, int32_t* id,
+                        void* stream) {
+  LLMI_REQUIRE_INIT();
+  LLMI_REQUIRE(logits != nullptr && id != nullptr, "sample: null pointer");
+  if (int rc = smp_check_cfg(cfg, n)) return rc;
+  return sample_device(logits, n, *cfg, target, id, nullptr, pick(stream));
+}
+
+int llmi_hip_sample(const float* logits, size_t n, const llmi_hip_sampling* cfg, double target, int32_t* id) {
+  LLMI_REQUIRE_INIT();
+  LLMI_REQUIRE(logits != nullptr && id != nullptr, "sample: null pointer");
+  if (int rc = smp_check_cfg(cfg, n)) return rc;
+  hipStream_t s = library_stream();
+  if (int rc = smp_reserve(n, s)) return rc;
+  LLMI_TRY_HIP(hipMemcpyAsync(g_smp.host_io, logits, n * sizeof(float), hipMemcpyHostToDevice, s));
+  return sample_device(g_smp.host_io, n, *cfg, target, id, nullptr, s);
+}
+
+int llmi_hip_sampling_probabilities(const float* logits, size_t n, const llmi_hip_sampling* cfg, float* probs) {
+  LLMI_REQUIRE_INIT();
+  LLMI_REQUIRE(logits != nullptr && probs != nullptr, "sampling_probabilities: null pointer");
+  if (int rc = smp_check_cfg(cfg, n)) return rc;
+  hipStream_t s = library_stream();
+  if (int rc = smp_reserve(n, s)) return rc;
+  const std::size_t k = cfg->top_k == 0 || cfg->top_k > n ? n : cfg->top_k;
+  float* dev_in = g_smp.host_io;
+  LLMI_TRY_HIP(hipMemcpyAsync(dev_in, logits, n * sizeof(float), hipMemcpyHostToDevice, s));
+  if (cfg->temperature <= 0.0f) {  // sampling.cpp:13-19: all mass on the first maximum
+    std::int32_t best = 0;
+    if (int rc = llmi_hip_argmax_dev(dev_in, n, g_smp.id_dev, s)) return rc;
+    LLMI_TRY_HIP(hipMemcpyAsync(&best, g_smp.id_dev, sizeof(best), hipMemcpyDeviceToHost, s));
+    LLMI_TRY_HIP(hipStreamSynchronize(s));
+    std::fill(probs, probs + n, 0.0f);
+    probs[best] = 1.0f;
+    return LLMI_OK;
+  }
+  bool ranked = false;
+  if (int rc = smp_front(dev_in, n, *cfg, true, s, &ranked)) return rc;
+  SmpWork& w = g_smp.w;
+  smp_seq_sum2<<<1, kSmpThreads, 0, s>>>(reinterpret_cast<const float*>(w.keys_sorted), w);
+  float* out = reinterpret_cast<float*>(w.keys);  // the keys are no longer needed
+  smp_write<<<static_cast<unsigned>(ceil_div(n, kSmpThreads)), kSmpThreads, 0, s>>>(static_cast<int>(n), w, out);
+  LLMI_TRY_HIP(hipGetLastError());
+  SmpState st{};
+  if (int rc = smp_read_state(&st, s)) return rc;
+  if (st.flags & kFlagAllNegInf) {
+    // Every logit is -inf: the reference's softmax gives NaN everywhere, its
+    // ranking keeps index order and nothing is renormalised (sum > 0 fails).
+    for (std::size_t i = 0; i < n; ++i) probs[i] = i < k ? __builtin_nanf("") : 0.0f;
+    return LLMI_OK;
+  }
+  if (st.flags & kFlagBad) return smp_bad_input(st);
+  LLMI_TRY_HIP(hipMemcpy(probs, out, n * sizeof(float), hipMemcpyDeviceToHost));
+  return LLMI_OK;
+}
+
+int llmi_hip_sampling_set_exact_only(int on) {
+  g_exact_only = on != 0;
+  return LLMI_OK;
+}
+
+int llmi_hip_sampling_last_paths(int* paths) {
+  LLMI_REQUIRE_INIT();
+  LLMI_REQUIRE(paths != nullptr, "sampling_last_paths: null pointer");
+  *paths = 0;
+  if (g_smp.w.st == nullptr) return LLMI_OK;
+  SmpState st{};
+  if (int rc = smp_read_state(&st, library_stream())) return rc;
+  *paths = st.seq_paths;
+  return LLMI_OK;
+}

@@ -87,7 +87,23 @@ SIGNATURES = {
     "llmi_hip_model_forward_cached_trace": (_i, [_vp, _vp, _vp, _sz, _i, _vp, _vp]),
     "llmi_hip_model_generate_greedy": (_i, [_vp, _vp, _sz, _sz, _vp, _sz, _vp, C.POINTER(_sz)]),
     "llmi_hip_model_last_timing": (_i, [_vp, C.POINTER(_d), C.POINTER(_d)]),
+    "llmi_hip_sample": (_i, [_vp, _sz, _vp, _d, C.POINTER(C.c_int32)]),
+    "llmi_hip_sample_dev": (_i, [_vp, _sz, _vp, _d, C.POINTER(C.c_int32), _vp]),
+    "llmi_hip_sampling_probabilities": (_i, [_vp, _sz, _vp, _vp]),
+    "llmi_hip_sampling_set_exact_only": (_i, [_i]),
+    "llmi_hip_sampling_last_paths": (_i, [C.POINTER(_i)]),
+    "llmi_hip_model_forward_sample": (_i, [_vp, _vp, _vp, _sz, _vp, _d, C.POINTER(C.c_int32)]),
+    "llmi_hip_model_generate_sampled": (_i, [_vp, _vp, _sz, _sz, _vp, _vp, _vp, _sz, _vp, C.POINTER(_sz)]),
 }
+
+
+class Sampling(C.Structure):
+    """llmi_hip_sampling: SamplingConfig (include/llmi/model/sampling.hpp:20-24)."""
+
+    _fields_ = [("temperature", C.c_float), ("top_k", C.c_size_t), ("top_p", C.c_float)]
+
+    def __init__(self, temperature: float = 1.0, top_k: int = 0, top_p: float = 1.0):
+        super().__init__(float(temperature), int(top_k), float(top_p))
 
 
 class HipError(RuntimeError):
@@ -428,8 +444,27 @@ class Model:
         check(self.lib.llmi_hip_model_chunk_nll(self.h, _p(ids), len(ids), t_start, mode, _p(out)))
         return out[:rows]
 
+    def forward_sample(self, cache: Cache, tokens, cfg: "Sampling", target: float) -> int:
+        """forward_cached + sample() on the device; `target` is sample()'s draw."""
+        toks = np.ascontiguousarray(tokens, dtype=np.int32)
+        out = C.c_int32()
+        check(self.lib.llmi_hip_model_forward_sample(self.h, cache.h, _p(toks), toks.size, C.byref(cfg),
+                                                     float(target), C.byref(out)))
+        return out.value
+
+    def generate_sampled(self, prompt, max_new: int, cfg: "Sampling", targets, stop_ids=()) -> np.ndarray:
+        p = np.ascontiguousarray(prompt, dtype=np.int32)
+        t = np.ascontiguousarray(targets, dtype=np.float64)
+        stop = np.ascontiguousarray(list(stop_ids), dtype=np.int32)
+        ids = np.zeros(max(max_new, 1), dtype=np.int32)
+        n = _sz()
+        check(self.lib.llmi_hip_model_generate_sampled(self.h, _p(p), p.size, max_new, C.byref(cfg),
+                                                       _p(t) if t.size else None, _p(stop) if stop.size else None,
+                                                       stop.size, _p(ids), C.byref(n)))
+        return ids[: n.value]
+
     def last_timing(self):
-        """(prefill_ms, decode_ms) of the last generate_greedy call."""
+        """(prefill_ms, decode_ms) of the last generate_greedy / generate_sampled call."""
         a, b = _d(), _d()
         check(self.lib.llmi_hip_model_last_timing(self.h, C.byref(a), C.byref(b)))
         return a.value, b.value
@@ -444,6 +479,37 @@ class Model:
             self.free()
         except Exception:
             pass
+
+
+def sample(logits, cfg: Sampling, target: float) -> int:
+    """llmi::sample with its draw given (host logits)."""
+    x = np.ascontiguousarray(logits, dtype=np.float32)
+    out = C.c_int32()
+    check(init().llmi_hip_sample(_p(x), x.size, C.byref(cfg), float(target), C.byref(out)))
+    return out.value
+
+
+def sample_dev(logits: "DeviceBuffer", n: int, cfg: Sampling, target: float) -> int:
+    out = C.c_int32()
+    check(init().llmi_hip_sample_dev(logits.ptr, n, C.byref(cfg), float(target), C.byref(out), None))
+    return out.value
+
+
+def sampling_probabilities(logits, cfg: Sampling) -> np.ndarray:
+    x = np.ascontiguousarray(logits, dtype=np.float32)
+    out = np.empty_like(x)
+    check(init().llmi_hip_sampling_probabilities(_p(x), x.size, C.byref(cfg), _p(out)))
+    return out
+
+
+def sampling_set_exact_only(on: bool) -> None:
+    check(init().llmi_hip_sampling_set_exact_only(int(on)))
+
+
+def sampling_last_paths() -> int:
+    v = C.c_int()
+    check(init().llmi_hip_sampling_last_paths(C.byref(v)))
+    return v.value
 
 
 def synthetic_model_dev(cfg: dict, base_seed: int, qtype: int, convention: str = "bench") -> "Model":

@@ -23,6 +23,11 @@
 //     (transformer_test.cpp:15-144).
 //   forward_cached / generate_greedy_cached: golden logits and greedy ids of
 //     the compiled reference on synthetic models.
+//   sampling_probabilities / sample_with_target / draw_uniform: the compiled
+//     reference's sampling_probabilities and sample() (same generator seed),
+//     its own sampling tests (sampling_test.cpp), a plain double softmax, the
+//     standard's mt19937_64 known answer and the uniform mapping's closed form
+//     (tests/test_oracle_sampling.py).
 // ============================================================================
 
 #include <algorithm>
@@ -33,6 +38,7 @@
 #include <functional>
 #include <memory>
 #include <mutex>
+#include <random>
 #include <string>
 #include <thread>
 #include <vector>
@@ -314,6 +320,69 @@ std::size_t argmax(const float* x, std::size_t n) {  // transformer.cpp:22-24: f
   for (std::size_t i = 1; i < n; ++i)
     if (x[best] < x[i]) best = i;
   return best;
+}
+
+// ---------------------------------------------------------------- sampling
+// src/model/sampling.cpp:11-58 (sampling_probabilities).  temperature <= 0:
+// all mass on the first maximum.  Otherwise: each logit divided by the
+// temperature in float, kernels::softmax, the entries ranked by probability
+// (descending; equal probabilities keep index order, as std::stable_sort
+// does), top-k, then the top-p nucleus -- the shortest prefix of the ranking
+// whose double running sum reaches double(top_p), at least one entry -- and
+// the kept entries divided by their double sum taken in ranking order.
+std::vector<float> sampling_probabilities(const float* logits, std::size_t n, float temperature, std::size_t top_k,
+                                          float top_p) {
+  std::vector<float> out(n, 0.0F);
+  if (temperature <= 0.0F) {
+    out[argmax(logits, n)] = 1.0F;
+    return out;
+  }
+  std::vector<float> p(n);
+  for (std::size_t i = 0; i < n; ++i) p[i] = logits[i] / temperature;
+  softmax(p.data(), n);
+  std::vector<std::size_t> rank(n);
+  for (std::size_t i = 0; i < n; ++i) rank[i] = i;
+  std::stable_sort(rank.begin(), rank.end(), [&p](std::size_t a, std::size_t b) { return p[a] > p[b]; });
+  const std::size_t k = top_k == 0 || top_k > n ? n : top_k;
+  std::size_t keep = k;
+  if (top_p < 1.0F) {
+    double run = 0.0;
+    for (std::size_t j = 0; j < k; ++j) {
+      run += static_cast<double>(p[rank[j]]);
+      if (run >= static_cast<double>(top_p)) {
+        keep = j + 1;
+        break;
+      }
+    }
+    if (keep == 0) keep = 1;
+  }
+  double total = 0.0;
+  for (std::size_t j = 0; j < keep; ++j) {
+    out[rank[j]] = p[rank[j]];
+    total += static_cast<double>(p[rank[j]]);
+  }
+  if (total > 0.0)
+    for (float& v : out) v = static_cast<float>(static_cast<double>(v) / total);
+  return out;
+}
+
+// sampling.cpp:60-77 (sample) with its random number given: target is what
+// std::uniform_real_distribution<double>(0, 1) drew from the caller's
+// generator.  The first index whose double running sum (in index order) of
+// the filtered probabilities reaches target; else the last nonzero entry;
+// else the first maximum.  temperature <= 0 draws nothing: the first maximum.
+std::size_t sample_with_target(const float* logits, std::size_t n, float temperature, std::size_t top_k, float top_p,
+                               double target) {
+  if (temperature <= 0.0F) return argmax(logits, n);
+  const std::vector<float> f = sampling_probabilities(logits, n, temperature, top_k, top_p);
+  double run = 0.0;
+  for (std::size_t i = 0; i < n; ++i) {
+    run += static_cast<double>(f[i]);
+    if (run >= target) return i;
+  }
+  for (std::size_t i = n; i-- > 0;)
+    if (f[i] > 0.0F) return i;
+  return argmax(logits, n);
 }
 
 // ------------------------------------------------------------------- model
@@ -625,6 +694,26 @@ void oracle_rope(float* v, std::size_t hd, std::size_t pos, const float* inv_fre
 void oracle_softmax(float* x, std::size_t n) { oracle::softmax(x, n); }
 float oracle_silu(float v) { return oracle::silu(v); }
 std::size_t oracle_argmax(const float* x, std::size_t n) { return oracle::argmax(x, n); }
+
+// n >= 1 (the reference indexes an empty vector otherwise).
+void oracle_sampling_probabilities(const float* logits, std::size_t n, float temperature, std::size_t top_k,
+                                   float top_p, float* out) {
+  const std::vector<float> f = oracle::sampling_probabilities(logits, n, temperature, top_k, top_p);
+  std::memcpy(out, f.data(), n * sizeof(float));
+}
+std::size_t oracle_sample_target(const float* logits, std::size_t n, float temperature, std::size_t top_k, float top_p,
+                                 double target) {
+  return oracle::sample_with_target(logits, n, temperature, top_k, top_p, target);
+}
+// The numbers sample() draws (sampling.cpp:64-65): `count` successive
+// std::uniform_real_distribution<double>(0, 1) draws from
+// std::mt19937_64(seed) -- the standard library's generator and mapping, as
+// the reference's build uses them.
+void oracle_draw_uniform(std::uint64_t seed, std::size_t count, double* out) {
+  std::mt19937_64 rng(seed);
+  std::uniform_real_distribution<double> u(0.0, 1.0);
+  for (std::size_t i = 0; i < count; ++i) out[i] = u(rng);
+}
 
 void* oracle_model_create(const llmi_model_config* cfg, const float* const* tensors, int type) {
   return oracle::create(cfg, tensors, type);

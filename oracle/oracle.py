@@ -191,6 +191,46 @@ class Cpu:
         x = np.ascontiguousarray(x, np.float32)
         return int(self._argmax(_p(x), x.size))
 
+    # -- sampling (sampling.cpp) ----------------------------------------------
+    def sampling_probabilities(self, logits, temperature: float, top_k: int = 0, top_p: float = 1.0) -> np.ndarray:
+        x = np.ascontiguousarray(logits, np.float32)
+        if x.size == 0:
+            raise ValueError("sampling_probabilities: empty logits")
+        out = np.empty_like(x)
+        fn = getattr(self.lib, self.prefix + "sampling_probabilities")
+        fn.argtypes = [C.c_void_p, C.c_size_t, C.c_float, C.c_size_t, C.c_float, C.c_void_p]
+        fn(_p(x), x.size, float(temperature), int(top_k), float(top_p), _p(out))
+        return out
+
+    def sample_target(self, logits, temperature: float, top_k: int, top_p: float, target: float) -> int:
+        """Oracle only: sample() with the uniform draw given."""
+        x = np.ascontiguousarray(logits, np.float32)
+        fn = self.lib.oracle_sample_target
+        fn.restype = C.c_size_t
+        fn.argtypes = [C.c_void_p, C.c_size_t, C.c_float, C.c_size_t, C.c_float, C.c_double]
+        return int(fn(_p(x), x.size, float(temperature), int(top_k), float(top_p), float(target)))
+
+    def draw_uniform(self, seed: int, count: int) -> np.ndarray:
+        """Oracle only: the numbers successive sample() calls draw from
+        std::mt19937_64(seed)."""
+        out = np.empty(count, np.float64)
+        fn = self.lib.oracle_draw_uniform
+        fn.argtypes = [C.c_uint64, C.c_size_t, C.c_void_p]
+        fn(int(seed), int(count), _p(out))
+        return out
+
+    def sample_sequence(self, logits, temperature: float, top_k: int, top_p: float, seed: int, count: int):
+        """Reference only: `count` sample() calls on std::mt19937_64(seed) ->
+        (ids, the number each call drew, -1 when it drew none)."""
+        x = np.ascontiguousarray(logits, np.float32)
+        ids = np.empty(count, np.int32)
+        targets = np.empty(count, np.float64)
+        fn = self.lib.ref_sample_sequence
+        fn.argtypes = [C.c_void_p, C.c_size_t, C.c_float, C.c_size_t, C.c_float, C.c_uint64, C.c_size_t, C.c_void_p,
+                       C.c_void_p]
+        fn(_p(x), x.size, float(temperature), int(top_k), float(top_p), int(seed), int(count), _p(ids), _p(targets))
+        return ids, targets
+
     # -- model -------------------------------------------------------------
     def model(self, cfg: dict, tensors: list, qtype: int) -> "CpuModel":
         return CpuModel(self, cfg, tensors, qtype)

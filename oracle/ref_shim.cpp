@@ -23,6 +23,7 @@
 #include "llmi/model/model.hpp"
 #include "llmi/model/quant.hpp"
 #include "llmi/model/safetensors.hpp"
+#include "llmi/model/sampling.hpp"
 #include "llmi/model/transformer.hpp"
 #include "llmi/util/thread_pool.hpp"
 
@@ -108,6 +109,28 @@ void ref_rope(float* v, std::size_t hd, std::size_t pos, const float* inv_freq) 
 void ref_softmax(float* x, std::size_t n) { llmi::kernels::softmax(x, n); }
 float ref_silu(float v) { return llmi::kernels::silu(v); }
 std::size_t ref_argmax(const float* x, std::size_t n) { return llmi::argmax(x, n); }
+
+// sampling.cpp: the reference's own filtering, and `count` successive sample()
+// calls on one std::mt19937_64(seed).  targets[c] receives the number call c
+// draws (read from a copy of the generator taken just before the call), or
+// -1 where temperature <= 0 draws nothing.
+void ref_sampling_probabilities(const float* logits, std::size_t n, float temperature, std::size_t top_k, float top_p,
+                                float* out) {
+  const llmi::SamplingConfig cfg{temperature, top_k, top_p};
+  const std::vector<float> p = llmi::sampling_probabilities(logits, n, cfg);
+  std::memcpy(out, p.data(), n * sizeof(float));
+}
+void ref_sample_sequence(const float* logits, std::size_t n, float temperature, std::size_t top_k, float top_p,
+                         std::uint64_t seed, std::size_t count, std::int32_t* ids, double* targets) {
+  const llmi::SamplingConfig cfg{temperature, top_k, top_p};
+  std::mt19937_64 rng(seed);
+  for (std::size_t c = 0; c < count; ++c) {
+    std::mt19937_64 peek = rng;
+    std::uniform_real_distribution<double> u(0.0, 1.0);
+    targets[c] = temperature <= 0.0F ? -1.0 : u(peek);
+    ids[c] = llmi::sample(logits, n, cfg, rng);
+  }
+}
 
 // tensors: fp32 arrays in expected_tensors() order.
 void* ref_model_create(const llmi_model_config* cfg, const float* const* tensors, int type) {
