@@ -296,10 +296,57 @@ def decode_runs():
                         ids_match_reference=bool(np.array_equal(ids, np.array(rec["ids"], np.int32))))
         print(f"[bench] {key}: prefill {pre_ms:.1f} ms, decode {tok_s:.1f} tok/s, ids match "
               f"{res[key]['ids_match_reference']}", file=sys.stderr, flush=True)
+        res[key]["sampled"] = sampled_decode(m, prompt, rec, cfg)
         if cfg["vocab_size"] > 100000:
             res[key]["perplexity_chunk"] = perplexity_chunk(m, prompt, cfg)
         m.free()
     return res
+
+
+SAMPLING_CFG = (0.8, 40, 0.9)  # llmi-chat's documented sampling example (docs/sampling.md)
+
+
+def sampling_targets(n: int) -> np.ndarray:
+    """Uniform [0, 1) doubles standing in for sample()'s draws (the CPU leg
+    replays the same numbers)."""
+    return np.random.default_rng(2024).random(n)
+
+
+def sampled_decode(m, prompt, rec, cfg):
+    """The same decode with sample() per step on the device
+    (llmi_hip_model_generate_sampled): temperature 0.8, top-k 40, top-p 0.9,
+    and unfiltered temperature 1.0; plus the cost of one sampling call alone
+    on device-resident logits of this vocabulary (greedy / unfiltered /
+    filtered), each call synchronous as in the serving loop."""
+    n = rec["n_steps"]
+    targets = sampling_targets(n)
+    out = {}
+    for name, sc in (("t0.8_k40_p0.9", SAMPLING_CFG), ("t1.0", (1.0, 0, 1.0))):
+        m.generate_sampled(prompt[:8], 4, H.Sampling(*sc), targets[:4])  # warm-up
+        ids = m.generate_sampled(prompt, n, H.Sampling(*sc), targets)
+        _, dec_ms = m.last_timing()
+        out[name] = {"decode_tok_s": round(len(ids) / (dec_ms * 1e-3), 1), "steps": int(len(ids))}
+        if name == "t0.8_k40_p0.9":
+            out["ids_first16"] = [int(i) for i in ids[:16]]
+    V = cfg["vocab_size"]
+    buf = H.DeviceBuffer(V * 4)
+    H.synth_normal_dev(buf, V, 77, 0.0, 3.0)
+    H.synchronize()
+    calls = {}
+    for name, sc in (("greedy", (0.0, 0, 1.0)), ("t1.0", (1.0, 0, 1.0)), ("t0.8_k40_p0.9", SAMPLING_CFG)):
+        c = H.Sampling(*sc)
+        for t in targets[:3]:
+            H.sample_dev(buf, V, c, t)
+        reps = 50
+        t0 = time.perf_counter()
+        for t in targets[:reps]:
+            H.sample_dev(buf, V, c, t)
+        calls[name] = round((time.perf_counter() - t0) / reps * 1e6, 1)
+    buf.free()
+    out["call_us"] = calls
+    print(f"[bench] sampled decode {out['t0.8_k40_p0.9']['decode_tok_s']} tok/s (t0.8 k40 p0.9), "
+          f"{out['t1.0']['decode_tok_s']} tok/s (t1.0); one call {calls} us", file=sys.stderr, flush=True)
+    return out
 
 
 def perplexity_chunk(m, prompt, cfg, reps=3):
@@ -361,12 +408,27 @@ def cpu_decode(runs, max_prompt: int = 128, steps: int = 16):
             ids.append(nxt)
             logits = cm.forward_cached(np.array([nxt], np.int32))
         t2 = time.perf_counter()
-        cm.close()
         same = ids == list(rec["ids"][:steps]) if prompt_len == rec["n_prompt"] else None
+        sampled_same = None
+        want = runs[key].get("sampled", {}).get("ids_first16")
+        if prompt_len == rec["n_prompt"] and want is not None:
+            # The same 16 sampled steps on the CPU: forward_cached, then the
+            # restated sample() with the GPU run's draws.
+            cm.new_cache(prompt_len + steps + 1)
+            targets = sampling_targets(rec["n_steps"])
+            logits = cm.forward_cached(prompt)
+            got = []
+            for i in range(min(steps, len(want))):
+                nxt = O.oracle().sample_target(logits, *SAMPLING_CFG, targets[i])
+                got.append(nxt)
+                logits = cm.forward_cached(np.array([nxt], np.int32))
+            sampled_same = got == want[: len(got)]
+        cm.close()
         runs[key].update(cpu_kind="reference" if use_ref else "port", cpu_threads=cpu.pool_workers() + 1,
                          cpu_sample=f"prompt {prompt_len} ids, {steps} greedy steps (load/quantize {load_s:.1f} s)",
                          cpu_prefill_tok_s=round(prompt_len / (t1 - t0), 1),
-                         cpu_decode_tok_s=round(steps / (t2 - t1), 2), cpu_ids_match=same)
+                         cpu_decode_tok_s=round(steps / (t2 - t1), 2), cpu_ids_match=same,
+                         cpu_sampled_ids_match=sampled_same)
         print(f"[bench] {key} CPU: decode {steps / (t2 - t1):.2f} tok/s", file=sys.stderr, flush=True)
 
 

@@ -23,7 +23,8 @@
 // Kernels of one sampling call (temperature > 0), all on one stream:
 //   smp_max    max of logits / temperature (float division), NaN / +inf flags
 //   smp_exp    e = expf(x / T - max) (the exact expf), sum -> inv = float(1/sum)
-//   smp_scale  p = e * inv; ranking keys (float bits, index) when needed
+//   smp_scale  p = e * inv and the ranking keys (float bits, index), when
+//              something is filtered (else the later kernels scale e on the fly)
 //   [rocprim radix sort, descending, stable: std::stable_sort's order]
 //   smp_keep   top-k, top-p, bounds on the renormalisation sum
 //   smp_draw   the filtered probabilities (bounded) and the first index whose
@@ -159,10 +160,14 @@ __device__ __forceinline__ double block_exclusive_scan(double v, double* sh, dou
   return excl;
 }
 
-// Thread 0 publishes the block's partials (already stored) and learns whether
-// it is the last block of the grid to do so.
+// Thread 0 publishes the block's partials (already stored; the release half
+// of the counter update makes them visible at agent scope) and learns whether
+// it is the last block of the grid to do so (the acquire half).  The last
+// block's other threads read the partials after a barrier with agent-scope
+// atomic loads (load_relaxed); data written by earlier kernels needs nothing.
+// No other fence: an agent-scope fence writes back or invalidates the whole
+// L2 of the XCD, which costs microseconds per wavefront.
 __device__ __forceinline__ bool arrive_last(unsigned* counter) {
-  __threadfence();
   const unsigned done = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
   return done == gridDim.x - 1;
 }
@@ -172,6 +177,27 @@ __device__ __forceinline__ void reset_counter(unsigned* counter) {
 template <typename T>
 __device__ __forceinline__ T load_relaxed(const T* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// The grid's per-block partials src[0..nb) (written by other workgroups of
+// this launch) into LDS, every thread loading its share, then the running
+// prefix pre[0..nb] (pre[0] = 0) by thread 0 in block order.
+__device__ __forceinline__ void partial_prefix(const double* src, int stride, int nb, double* tmp, double* pre) {
+  for (int b = threadIdx.x; b < nb; b += kSmpThreads) tmp[b] = load_relaxed(src + static_cast<std::size_t>(b) * stride);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    pre[0] = 0.0;
+    for (int b = 0; b < nb; ++b) pre[b + 1] = pre[b] + tmp[b];
+  }
+  __syncthreads();
+}
+
+// First b in [0, nb) with pre[b + 1] * factor >= t, or nb (pre in LDS).
+__device__ __forceinline__ int first_block_reaching(const double* pre, int nb, double factor, double t, int* red_i) {
+  int c = nb;
+  for (int b = threadIdx.x; b < nb; b += kSmpThreads)
+    if (pre[b + 1] * factor >= t) c = min(c, b);
+  return block_min_i(c, red_i);
 }
 
 // First j in [lo, hi) with (base + v(lo) + ... + v(j)) * factor >= t, or hi.
@@ -278,7 +304,6 @@ __global__ void __launch_bounds__(kSmpThreads) smp_max(const float* __restrict__
   }
   __syncthreads();
   if (!last) return;
-  __threadfence();
   float mm = -__builtin_inff();
   int ff = 0;
   for (int b = threadIdx.x; b < static_cast<int>(gridDim.x); b += kSmpThreads) {
@@ -316,7 +341,6 @@ __global__ void __launch_bounds__(kSmpThreads) smp_exp(const float* __restrict__
     w.p[i] = e;
     part = part + static_cast<double>(e);
   }
-  __threadfence();  // every wave's e: the last block may read them all
   part = block_sum_d(part, red_d);
   if (threadIdx.x == 0) {
     w.part_d[blockIdx.x] = part;
@@ -324,19 +348,21 @@ __global__ void __launch_bounds__(kSmpThreads) smp_exp(const float* __restrict__
   }
   __syncthreads();
   if (!last) return;
-  __threadfence();
   __shared__ float inv_s;
+  __shared__ double tmp[kSmpBlocks], pre[kSmpBlocks + 1];
+  partial_prefix(w.part_d, 1, gridDim.x, tmp, pre);
   if (threadIdx.x == 0) {
-    double sum = 0.0;
-    for (int b = 0; b < static_cast<int>(gridDim.x); ++b) sum = sum + load_relaxed(w.part_d + b);
+    const double sum = pre[gridDim.x];
     const double slack = smp_sigma(n) * sum;
     inv_s = recip_float(sum - slack) == recip_float(sum + slack) ? recip_float(sum) : -1.0f;
   }
   __syncthreads();
   float inv = inv_s;
-  if (inv < 0.0f) {  // the bound leaves float(1/sum) open: the sequential sum
-    const float* p = w.p;
-    block_sequential_sum([p](int j) { return p[j]; }, n, false, 0.0, &seq, stage, stop);
+  if (inv < 0.0f) {
+    // The bound leaves float(1/sum) open: the sequential sum, its terms
+    // recomputed from the logits (other workgroups' e need not be visible).
+    block_sequential_sum([=](int j) { return exact::expf_with(logits[j] / temp - mx, tab); }, n, false, 0.0, &seq,
+                         stage, stop);
     inv = recip_float(seq);
     if (threadIdx.x == 0) w.st->seq_paths |= kSeqSoftmax;
   }
@@ -358,12 +384,66 @@ __global__ void __launch_bounds__(kSmpThreads) smp_scale(int n, SmpWork w, int w
   }
 }
 
-// Ranking keys of the already-scaled p (the exact path of an unfiltered draw).
+// Ranking keys of p = e * inv, p left unscaled (the exact path of an
+// unfiltered draw, which skipped smp_scale).
 __global__ void __launch_bounds__(kSmpThreads) smp_keys(int n, SmpWork w) {
   const int i = blockIdx.x * kSmpThreads + threadIdx.x;
   if (i >= n) return;
-  w.keys[i] = __builtin_bit_cast(std::uint32_t, w.p[i]);
+  w.keys[i] = __builtin_bit_cast(std::uint32_t, w.p[i] * w.st->inv);
   w.idx[i] = i;
+}
+
+// First maximum of x (transformer.cpp:22-24) for temperature <= 0: slices,
+// then the last workgroup combines (lowest index among equal maxima).
+__device__ __forceinline__ void better_of(float& v, int& i, float v2, int i2) {
+  if (i2 < 0) return;
+  if (i < 0 || v2 > v || (v2 == v && i2 < i)) {
+    v = v2;
+    i = i2;
+  }
+}
+__device__ __forceinline__ void block_best(float& v, int& i, float* sv, int* si) {
+  for (int o = 32; o > 0; o >>= 1) {
+    const float v2 = __shfl_xor(v, o, 64);
+    const int i2 = __shfl_xor(i, o, 64);
+    better_of(v, i, v2, i2);
+  }
+  if ((threadIdx.x & 63) == 0) {
+    sv[threadIdx.x >> 6] = v;
+    si[threadIdx.x >> 6] = i;
+  }
+  __syncthreads();
+  v = sv[0];
+  i = si[0];
+  for (int w = 1; w < kSmpWaves; ++w) better_of(v, i, sv[w], si[w]);
+  __syncthreads();
+}
+__global__ void __launch_bounds__(kSmpThreads) smp_argmax(const float* __restrict__ x, int n, SmpWork w,
+                                                          std::int32_t* __restrict__ out) {
+  __shared__ float sv[kSmpWaves];
+  __shared__ int si[kSmpWaves];
+  __shared__ bool last;
+  const Slice sl = slice_of(n, blockIdx.x, gridDim.x);
+  float v = 0.0f;
+  int i = -1;
+  for (int j = sl.lo + static_cast<int>(threadIdx.x); j < sl.hi; j += kSmpThreads) better_of(v, i, x[j], j);
+  block_best(v, i, sv, si);
+  if (threadIdx.x == 0) {
+    w.part_f[blockIdx.x] = v;
+    w.part_i[blockIdx.x] = i;
+    last = arrive_last(&w.st->counter);
+  }
+  __syncthreads();
+  if (!last) return;
+  v = 0.0f;
+  i = -1;
+  for (int b = threadIdx.x; b < static_cast<int>(gridDim.x); b += kSmpThreads)
+    better_of(v, i, load_relaxed(w.part_f + b), load_relaxed(w.part_i + b));
+  block_best(v, i, sv, si);
+  if (threadIdx.x == 0) {
+    *out = i < 0 ? 0 : i;
+    reset_counter(&w.st->counter);
+  }
 }
 
 // Top-k and top-p (sampling.cpp:28-51) over the first m ranked values
@@ -372,7 +452,7 @@ __global__ void __launch_bounds__(kSmpThreads) smp_keys(int n, SmpWork w) {
 // renormalisation sum of the kept ones (:53-57).
 __global__ void __launch_bounds__(kSmpThreads) smp_keep(const float* __restrict__ vals,
                                                         const std::int32_t* __restrict__ idx_sorted, int m, int n,
-                                                        float top_p, SmpWork w) {
+                                                        float top_p, int scaled, SmpWork w) {
   __shared__ double red_d[kSmpWaves];
   __shared__ int red_i[kSmpWaves];
   __shared__ double sh[kSmpThreads];
@@ -382,7 +462,8 @@ __global__ void __launch_bounds__(kSmpThreads) smp_keep(const float* __restrict_
   __shared__ double seq;
   __shared__ bool last;
   if (w.st->flags & kFlagBad) return;
-  auto v = [vals](int j) { return vals[j]; };
+  const float mult = scaled ? 1.0f : w.st->inv;  // unscaled: vals holds e, p = e * inv
+  auto v = [vals, mult](int j) { return vals[j] * mult; };
   const Slice sl = slice_of(m, blockIdx.x, gridDim.x);
   const double part = slice_sum(v, sl.lo, sl.hi, red_d);
   if (threadIdx.x == 0) {
@@ -391,24 +472,16 @@ __global__ void __launch_bounds__(kSmpThreads) smp_keep(const float* __restrict_
   }
   __syncthreads();
   if (!last) return;
-  __threadfence();
   const int nb = gridDim.x;
-  if (threadIdx.x == 0) {
-    pre[0] = 0.0;
-    for (int b = 0; b < nb; ++b) pre[b + 1] = pre[b] + load_relaxed(w.part_d + b);
-  }
-  __syncthreads();
+  partial_prefix(w.part_d, 1, nb, sh, pre);
   const double sigma = smp_sigma(m);
   int keep = m;
   bool exact = false;
   double s2 = 0.0;
   if (top_p < 1.0f) {
     const double t = static_cast<double>(top_p);
-    int b_e = nb, b_l = nb;
-    for (int b = nb - 1; b >= 0; --b) {
-      if (pre[b + 1] * (1.0 + sigma) >= t) b_e = b;
-      if (pre[b + 1] * (1.0 - sigma) >= t) b_l = b;
-    }
+    const int b_e = first_block_reaching(pre, nb, 1.0 + sigma, t, red_i);
+    const int b_l = first_block_reaching(pre, nb, 1.0 - sigma, t, red_i);
     bool decided = false;
     if (b_e == nb) {
       decided = true;  // the running sum certainly stays below top_p: keep = m
@@ -431,8 +504,8 @@ __global__ void __launch_bounds__(kSmpThreads) smp_keep(const float* __restrict_
   }
   if (!exact) {
     // P = running sum through keep - 1.
-    int b_k = 0;
-    while (b_k + 1 < nb && slice_of(m, b_k, nb).hi < keep) ++b_k;
+    const int per = (m + nb - 1) / nb;
+    const int b_k = (keep - 1) / per;  // the slice holding index keep - 1
     const Slice sk = slice_of(m, b_k, nb);
     const double within = slice_sum(v, sk.lo, keep, red_d);
     s2 = pre[b_k] + within;
@@ -443,7 +516,7 @@ __global__ void __launch_bounds__(kSmpThreads) smp_keep(const float* __restrict_
     w.st->s2_lo = exact ? s2 : s2 * (1.0 - sg);
     w.st->s2_hi = exact ? s2 : s2 * (1.0 + sg);
     if (idx_sorted != nullptr) {
-      w.st->p_thr = vals[keep - 1];
+      w.st->p_thr = v(keep - 1);
       w.st->idx_last = idx_sorted[keep - 1];
     } else {
       w.st->p_thr = -__builtin_inff();
@@ -481,7 +554,7 @@ __device__ __forceinline__ float renorm(float p, double s) {
 // sample() (sampling.cpp:60-77) given its draw: the filtered probabilities
 // f = float(double(p) / s2) lie in [f(s2_hi), f(s2_lo)]; the first index
 // whose running sum reaches target, or else the last nonzero entry.
-__global__ void __launch_bounds__(kSmpThreads) smp_draw(int n, double target, SmpWork w,
+__global__ void __launch_bounds__(kSmpThreads) smp_draw(int n, double target, int scaled, SmpWork w,
                                                         std::int32_t* __restrict__ also) {
   __shared__ double red_d[kSmpWaves];
   __shared__ int red_i[kSmpWaves];
@@ -493,15 +566,16 @@ __global__ void __launch_bounds__(kSmpThreads) smp_draw(int n, double target, Sm
   __shared__ bool last;
   if (w.st->flags & kFlagBad) return;
   const float* p = w.p;
+  const float mult = scaled ? 1.0f : w.st->inv;
   const float p_thr = w.st->p_thr;
   const int idx_last = w.st->idx_last;
   const double s2_lo = w.st->s2_lo, s2_hi = w.st->s2_hi;
   auto f_lo = [=](int i) {
-    const float x = p[i];
+    const float x = p[i] * mult;
     return kept(x, i, p_thr, idx_last) ? renorm(x, s2_hi) : 0.0f;
   };
   auto f_hi = [=](int i) {
-    const float x = p[i];
+    const float x = p[i] * mult;
     return kept(x, i, p_thr, idx_last) ? renorm(x, s2_lo) : 0.0f;
   };
   const Slice sl = slice_of(n, blockIdx.x, gridDim.x);
@@ -527,29 +601,19 @@ __global__ void __launch_bounds__(kSmpThreads) smp_draw(int n, double target, Sm
   }
   __syncthreads();
   if (!last) return;
-  __threadfence();
   const int nb = gridDim.x;
-  if (threadIdx.x == 0) {
-    pre_lo[0] = 0.0;
-    pre_hi[0] = 0.0;
-    for (int b = 0; b < nb; ++b) {
-      pre_lo[b + 1] = pre_lo[b] + load_relaxed(w.part_d + 2 * b);
-      pre_hi[b + 1] = pre_hi[b] + load_relaxed(w.part_d + 2 * b + 1);
-    }
-  }
+  partial_prefix(w.part_d, 2, nb, sh, pre_lo);
+  partial_prefix(w.part_d + 1, 2, nb, sh, pre_hi);
   int last_lo = -1, last_hi = -1;
   for (int b = threadIdx.x; b < nb; b += kSmpThreads) {
     last_lo = max(last_lo, load_relaxed(w.part_i + 2 * b));
     last_hi = max(last_hi, load_relaxed(w.part_i + 2 * b + 1));
   }
   last_lo = block_max_i(last_lo, red_i);
-  last_hi = block_max_i(last_hi, red_i);  // (its barriers also publish pre_lo / pre_hi)
+  last_hi = block_max_i(last_hi, red_i);
   const double sigma = smp_sigma(n);
-  int b_e = nb, b_l = nb;
-  for (int b = nb - 1; b >= 0; --b) {
-    if (pre_hi[b + 1] * (1.0 + sigma) >= target) b_e = b;
-    if (pre_lo[b + 1] * (1.0 - sigma) >= target) b_l = b;
-  }
+  const int b_e = first_block_reaching(pre_hi, nb, 1.0 + sigma, target, red_i);
+  const int b_l = first_block_reaching(pre_lo, nb, 1.0 - sigma, target, red_i);
   int id = -1;
   if (b_e == nb) {
     // The running sum certainly stays below target: the last nonzero entry.
@@ -667,14 +731,14 @@ int smp_front(const float* logits, std::size_t n, const llmi_hip_sampling& cfg, 
   SmpWork& w = g_smp.w;
   smp_max<<<kSmpBlocks, kSmpThreads, 0, s>>>(logits, ni, cfg.temperature, w);
   smp_exp<<<kSmpBlocks, kSmpThreads, 0, s>>>(logits, ni, cfg.temperature, w);
-  smp_scale<<<static_cast<unsigned>(ceil_div(n, kSmpThreads)), kSmpThreads, 0, s>>>(ni, w, *ranked ? 1 : 0);
   LLMI_TRY_HIP(hipGetLastError());
   if (*ranked) {
+    smp_scale<<<static_cast<unsigned>(ceil_div(n, kSmpThreads)), kSmpThreads, 0, s>>>(ni, w, 1);
     if (int rc = smp_sort(n, s)) return rc;
     smp_keep<<<kSmpBlocks, kSmpThreads, 0, s>>>(reinterpret_cast<const float*>(w.keys_sorted), w.idx_sorted,
-                                                static_cast<int>(k), ni, cfg.top_p, w);
+                                                static_cast<int>(k), ni, cfg.top_p, 1, w);
   } else {
-    smp_keep<<<kSmpBlocks, kSmpThreads, 0, s>>>(w.p, nullptr, ni, ni, 2.0f, w);
+    smp_keep<<<kSmpBlocks, kSmpThreads, 0, s>>>(w.p, nullptr, ni, ni, 2.0f, 0, w);
   }
   LLMI_TRY_HIP(hipGetLastError());
   return LLMI_OK;
@@ -701,7 +765,8 @@ int sample_device(const float* logits, std::size_t n, const llmi_hip_sampling& c
   if (int rc = smp_reserve(n, s)) return rc;
   if (cfg.temperature <= 0.0f) {  // sampling.cpp:61: the first maximum, nothing drawn
     std::int32_t* dst = also != nullptr ? also : g_smp.id_dev;
-    if (int rc = llmi_hip_argmax_dev(logits, n, dst, s)) return rc;
+    smp_argmax<<<kSmpBlocks, kSmpThreads, 0, s>>>(logits, static_cast<int>(n), g_smp.w, dst);
+    LLMI_TRY_HIP(hipGetLastError());
     LLMI_TRY_HIP(hipMemcpyAsync(id_host, dst, sizeof(std::int32_t), hipMemcpyDeviceToHost, s));
     LLMI_TRY_HIP(hipStreamSynchronize(s));
     return LLMI_OK;
@@ -711,7 +776,7 @@ int sample_device(const float* logits, std::size_t n, const llmi_hip_sampling& c
   SmpWork& w = g_smp.w;
   const int ni = static_cast<int>(n);
   if (g_exact_only) smp_seq_sum2<<<1, kSmpThreads, 0, s>>>(reinterpret_cast<const float*>(w.keys_sorted), w);
-  smp_draw<<<kSmpBlocks, kSmpThreads, 0, s>>>(ni, target, w, also);
+  smp_draw<<<kSmpBlocks, kSmpThreads, 0, s>>>(ni, target, ranked ? 1 : 0, w, also);
   LLMI_TRY_HIP(hipGetLastError());
   SmpState st{};
   if (int rc = smp_read_state(&st, s)) return rc;
@@ -732,7 +797,7 @@ int sample_device(const float* logits, std::size_t n, const llmi_hip_sampling& c
       if (int rc = smp_sort(n, s)) return rc;
     }
     smp_seq_sum2<<<1, kSmpThreads, 0, s>>>(reinterpret_cast<const float*>(w.keys_sorted), w);
-    smp_draw<<<kSmpBlocks, kSmpThreads, 0, s>>>(ni, target, w, also);
+    smp_draw<<<kSmpBlocks, kSmpThreads, 0, s>>>(ni, target, ranked ? 1 : 0, w, also);
     LLMI_TRY_HIP(hipGetLastError());
     if (int rc = smp_read_state(&st, s)) return rc;
     if (!st.decided) return fail(LLMI_ERR_STATE, "sampling: the exact draw did not decide (internal error)");

@@ -20,6 +20,7 @@
 #include <vector>
 
 #include "llmi/model/quant.hpp"
+#include "llmi/model/sampling.hpp"
 #include "llmi/util/result.hpp"
 
 struct llmi_hip_model;
@@ -99,6 +100,13 @@ class Transformer {
   [[nodiscard]] Result<std::vector<TokenId>> generate_greedy_cached(const std::vector<TokenId>& prompt,
                                                                     std::size_t max_new,
                                                                     const std::vector<TokenId>& stop_ids) const;
+
+  // One serving step without the logits leaving the GPU: forward_cached(tokens,
+  // cache) followed by sample(logits, cfg, rng), as the loop of
+  // src/server/server.cpp:109-195 does, with the same draws from rng and the
+  // same token.  (No counterpart in the reference's class.)
+  [[nodiscard]] Result<TokenId> forward_sample(const std::vector<TokenId>& tokens, KVCache& cache,
+                                               const SamplingConfig& cfg, std::mt19937_64& rng) const;
 
  private:
   ModelConfig cfg_;

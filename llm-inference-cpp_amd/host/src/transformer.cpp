@@ -144,6 +144,17 @@ Result<std::vector<float>> Transformer::forward_cached(const std::vector<TokenId
   return logits;
 }
 
+Result<TokenId> Transformer::forward_sample(const std::vector<TokenId>& tokens, KVCache& cache,
+                                            const SamplingConfig& cfg, std::mt19937_64& rng) const {
+  const double target = detail::sample_draw(cfg, rng);
+  const llmi_hip_sampling c{cfg.temperature, cfg.top_k, cfg.top_p};
+  std::int32_t id = 0;
+  if (llmi_hip_model_forward_sample(dev_.get(), cache.dev_.get(), tokens.data(), tokens.size(), &c, target, &id) !=
+      LLMI_OK)
+    return fail(llmi_hip_last_error());
+  return static_cast<TokenId>(id);
+}
+
 // forward() recomputes the whole sequence; the reference's own tests hold it
 // bit-identical to forward_cached on a fresh cache (transformer_test.cpp:322-339).
 Result<std::vector<float>> Transformer::forward(const std::vector<TokenId>& tokens, bool all_positions,

@@ -3,6 +3,7 @@
 // reference's 2-layer test architecture, plus bit-exact logits against the
 // CPU oracle (oracle/liboracle.so).
 #include <map>
+#include <random>
 
 #include "check.hpp"
 #include "llmi/model/transformer.hpp"
@@ -274,4 +275,36 @@ TEST(Transformer, GreedyIsDeterministic) {
   auto stopped = tf.generate_greedy({1, 2}, 10, {(*a)[0]});
   ASSERT_TRUE(stopped);
   EXPECT_EQ(stopped->size(), 1U);
+}
+
+// The serving loop (server.cpp:109-195): forward_cached, sample(), feed the
+// token back -- and forward_sample doing both on the device, with the same
+// generator: the same tokens and the same generator state after.
+TEST(Transformer, ForwardSampleMatchesForwardCachedThenSample) {
+  for (quant::Type type : {quant::Type::Q8_0, quant::Type::Q4_0}) {
+    auto tiny = make_tiny(Arch::Qwen2, true, 21);
+    auto tf = load(tiny, type);
+    const SamplingConfig cfg{0.9F, 8, 0.95F};
+    auto c1 = tf.new_cache(40);
+    auto c2 = tf.new_cache(40);
+    ASSERT_TRUE(c1 && c2);
+    std::mt19937_64 r1(99), r2(99);
+    std::vector<TokenId> in = {1, 2, 3, 4};
+    auto logits = tf.forward_cached(in, *c1);
+    ASSERT_TRUE(logits);
+    TokenId want = sample(logits->data(), logits->size(), cfg, r1);
+    auto got = tf.forward_sample(in, *c2, cfg, r2);
+    ASSERT_TRUE(got);
+    EXPECT_EQ(*got, want);
+    for (int step = 0; step < 20; ++step) {
+      logits = tf.forward_cached({want}, *c1);
+      ASSERT_TRUE(logits);
+      want = sample(logits->data(), logits->size(), cfg, r1);
+      got = tf.forward_sample({*got}, *c2, cfg, r2);
+      ASSERT_TRUE(got);
+      EXPECT_EQ(*got, want);
+    }
+    EXPECT_TRUE(r1 == r2);
+    EXPECT_EQ(c1->length(), c2->length());
+  }
 }

@@ -1,7 +1,7 @@
 """The C++ host layer (llm-inference-cpp_amd/host: llmi::quant, llmi::Weight,
-llmi::Transformer with the reference's interface): the tests of
-tests/native/*_gpu_test.cpp mirror the reference's quant_test.cpp and
-transformer_test.cpp against it.  Building them needs no GPU; running them
+llmi::Transformer, llmi::sample with the reference's interface): the tests
+of tests/native/*_gpu_test.cpp mirror the reference's quant_test.cpp,
+transformer_test.cpp and sampling_test.cpp against it.  Building them needs no GPU; running them
 does."""
 
 import os
@@ -12,7 +12,7 @@ import pytest
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 PKG = os.path.join(ROOT, "llm-inference-cpp_amd")
 NATIVE = os.path.join(ROOT, "tests", "native")
-TESTS = ["quant_gpu_test", "transformer_gpu_test"]
+TESTS = ["quant_gpu_test", "transformer_gpu_test", "sampling_gpu_test"]
 
 
 def build(name, out_dir):
