@@ -171,6 +171,28 @@ def target_shapes():
             w.free()
     if stage is not None:
         stage.free()
+    res.update(grouped_mlp_targets())
+    return res
+
+
+def grouped_mlp_targets(steps=50):
+    """The Qwen2.5-0.5B MLP matrices at streaming scale: all 24 layers' gate,
+    up (4864x896) and down (896x4864) as one grouped launch per step, batch 1,
+    rotating copies (>= 1 GiB).  A single launch of one of these 2.7 MB
+    matrices is bound by launch latency, not bandwidth."""
+    res = {}
+    shapes = [s for _ in range(24) for s in (("gate_proj", 4864, 896), ("up_proj", 4864, 896), ("down_proj", 896, 4864))]
+    for qt in (H.Q4_0, H.Q8_0):
+        wb = sum(o * H.row_bytes(i, qt) + 4 * o * H.nblocks(i) for _, o, i in shapes)
+        wset = WeightSet(shapes, qt, max(2, -(-ROTATE_BYTES // wb)), 31)
+        ms = time_steps(wset, 1, steps, 5, mode="group")
+        wset.free()
+        us = ms / steps * 1e3
+        gbs = sum(algo_bytes(o, i, qt, 1) for _, o, i in shapes) / (us * 1e-6) / 1e9
+        res[f"qwen_mlp_24_layers_grouped_{H.TYPE_NAMES[qt]}"] = dict(
+            us=round(us, 2), gbs=round(gbs, 1), pct_hbm_peak=round(100 * gbs / HBM_PEAK_GBS, 1))
+        print(f"[bench] Qwen MLP x24 grouped {H.TYPE_NAMES[qt]}: {us:.1f} us, {gbs:.0f} GB/s", file=sys.stderr,
+              flush=True)
     return res
 
 

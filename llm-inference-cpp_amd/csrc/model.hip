@@ -713,13 +713,15 @@ __global__ void __launch_bounds__(kThreads) argmax_many(const float* __restrict_
   if (threadIdx.x == 0) {
     part_v[blockIdx.x] = b.v;
     part_i[blockIdx.x] = b.i;
-    __threadfence();
+    // The release half of the update publishes this block's partials; the
+    // last block reads them with agent-scope atomic loads after its barrier.
+    // (An extra agent-scope fence would write back or invalidate the XCD's
+    // whole L2 per wavefront.)
     const unsigned done = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
     last = done == gridDim.x - 1;
   }
   __syncthreads();
   if (!last) return;
-  __threadfence();
   Best r{-__builtin_inff(), -1};
   for (int k = threadIdx.x; k < static_cast<int>(gridDim.x); k += kThreads) {
     const float v = __hip_atomic_load(part_v + k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

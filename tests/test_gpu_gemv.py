@@ -95,6 +95,56 @@ def test_extreme_activations_match_oracle(qt):
         assert np.array_equal(bits(got), bits(want)), (out, n_in, rows)
 
 
+@pytest.mark.parametrize("case", ["tiny", "edges", "one_bad_block", "huge"])
+def test_q4_batch1_extreme_magnitudes(case):
+    """Batch-1 Q4_0 products (f16 code operands of v_fma_mix_f32) on
+    activations of extreme magnitude: all near 2^-100 (block sums that cancel
+    down to a few units of 2^-123), values on both sides of 2^-100 and 2^101,
+    one tiny value among ordinary ones, and values near 2^120 (sums that
+    overflow).  The oracle's bits in the single-product kernels and in
+    grouped launches (both tile sizes)."""
+    orc = O.oracle()
+    rng = np.random.default_rng({"tiny": 1, "edges": 2, "one_bad_block": 3, "huge": 4}[case])
+    lo, hi_ok = np.float32(2.0 ** -100), np.nextafter(np.float32(2.0 ** 101), np.float32(0))
+    shapes = ((200, 576), (4000, 96), (1536, 576), (65, 33))
+    for out, n_in in shapes:
+        w = synth.normal(out + n_in, out * n_in, 0.0, 0.02)
+        data, scales = orc.quantize(w, out, n_in, O.Q4_0)
+        dev = H.Weight.upload(data, scales, out, n_in, O.Q4_0)
+        sign = np.where(rng.random(n_in) < 0.5, -1.0, 1.0).astype(np.float32)
+        if case == "tiny":  # every |x| a little above 2^-100: sums cancel towards the 2^-123 grid
+            x = (sign * lo * (1 + rng.integers(0, 4, n_in))).astype(np.float32)
+        elif case == "edges":
+            pick = rng.integers(0, 5, n_in)
+            vals = np.array([lo, np.nextafter(lo, np.float32(0)), hi_ok, np.float32(2.0 ** 101), 0.0], np.float32)
+            x = (sign * vals[pick]).astype(np.float32)
+        elif case == "one_bad_block":  # ordinary values, one below the range
+            x = synth.normal(n_in, n_in, 0.0, 1.0)
+            x[rng.integers(0, n_in)] = np.float32(1e-35)
+        else:
+            x = (synth.normal(n_in, n_in, 0.0, 1.0) * np.float32(2.0 ** 120)).astype(np.float32)
+        want = orc.matmul(x, 1, n_in, data, scales, O.Q4_0, out, None)
+        got = dev.matmul(x, 1, None)
+        assert np.array_equal(bits(got), bits(want)), (case, out, n_in)
+        for spread in (False, True):  # grouped: alone (16-row tiles) or beside a big product (64-row tiles)
+            xd, yd = H.DeviceBuffer.from_array(x), H.DeviceBuffer(out * 4)
+            items = [(dev, xd.ptr, yd.ptr, 1, None)]
+            extra = []
+            if spread:
+                big = H.Weight.quantize(synth.normal(5, 70000 * 96, 0.0, 0.02), 70000, 96, H.Q4_0)
+                bx, by = H.DeviceBuffer.from_array(synth.normal(6, 96, 0.0, 1.0)), H.DeviceBuffer(70000 * 4)
+                items.append((big, bx.ptr, by.ptr, 1, None))
+                extra = [big, bx, by]
+            g = H.Group(items)
+            g.launch()
+            H.synchronize()
+            assert np.array_equal(bits(yd.download(np.float32)), bits(want)), (case, out, n_in, spread)
+            g.free()
+            for e in extra + [xd, yd]:
+                e.free()
+        dev.free()
+
+
 def test_device_pointer_entry_point_and_determinism():
     orc = O.oracle()
     out, n_in, qt = 4864, 896, O.Q4_0
