@@ -864,12 +864,15 @@ int launch_matmul(const DeviceMatrix& m, const float* x, std::size_t rows, const
 
 int plan_group(const GroupEntry* entries, std::size_t count, GroupPlan* plan) {
   // Narrow 16-row tiles for batch-1 products only when the 64-row tiles would
-  // leave the GPU mostly idle (fewer than ~4 workgroups per CU), and not for
-  // long rows (more than kNarrowMaxBlocks blocks), which stream about twice
-  // as fast on 64-row tiles (measured on MI355X: 24 Qwen2.5 down_proj
-  // matrices, 896 x 4864, in one launch) -- unless a prologue needs them.
+  // leave the GPU mostly idle (fewer than ~4 workgroups per CU), and for long
+  // rows (more than kNarrowMaxBlocks blocks) only below one 64-row workgroup
+  // per CU: 24 Qwen2.5 down_proj matrices (896 x 4864, 336 64-row tiles) in
+  // one launch stream about twice as fast on 64-row tiles, one alone (14
+  // tiles) about 1.6x faster on 16-row tiles (measured on MI355X).  A
+  // prologue always needs them.
   constexpr std::size_t kNarrowBelow = 1024;
   constexpr std::size_t kNarrowMaxBlocks = 64;
+  constexpr std::size_t kLongRowsNarrowBelow = 256;
   *plan = GroupPlan{};
   std::size_t wide_total = 0;
   for (std::size_t i = 0; i < count; ++i) {
@@ -893,8 +896,10 @@ int plan_group(const GroupEntry* entries, std::size_t count, GroupPlan* plan) {
       const DeviceMatrix& m = *e.m;
       if (m.out == 0) continue;
       const bool fits = narrow_lds(m.in, m.nblk) <= max_lds_per_block();
-      const bool narrow = e.rows == 1 && fits &&
-                          (e.prologue != kPlain || (wide_total < kNarrowBelow && m.nblk <= kNarrowMaxBlocks));
+      const bool narrow =
+          e.rows == 1 && fits &&
+          (e.prologue != kPlain ||
+           (wide_total < kNarrowBelow && (m.nblk <= kNarrowMaxBlocks || wide_total < kLongRowsNarrowBelow)));
       LLMI_REQUIRE(e.prologue == kPlain || narrow, "group: a prologue needs batch 1 and in <= ~20k");
       int r = narrow ? int{GroupProblem::kNarrow} : pick_chunk(e.rows, m.nblk, kLdsTarget);
       if (r == 0) r = pick_chunk(1, m.nblk, max_lds_per_block());
