@@ -38,7 +38,7 @@ HBM_PEAK_GBS = 8000.0
 # HBM bytes per qgemv_group launch of the batch-1 step, from the two
 # rocprofv3 --pmc passes (FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0, the factors a
 # 256 MiB copy kernel reads) recorded in profiles/qgemv_group_smollm2_q4_b1.md.
-GROUP_B1_HBM_BYTES = 85_161_245
+GROUP_B1_HBM_BYTES = 85_093_182
 ROTATE_BYTES = 1 << 30
 
 SMOL_LAYER = [("q_proj", 576, 576), ("k_proj", 192, 576), ("v_proj", 192, 576), ("o_proj", 576, 576),
