@@ -202,6 +202,11 @@ int llmi_hip_shutdown(void) {
     LLMI_TRY_HIP(hipStreamSynchronize(g_stream));
     LLMI_TRY_HIP(hipStreamDestroy(g_stream));
   }
+  // The library's own workspaces (model, weight and group handles belong to
+  // their callers).
+  release_sampling_workspace();
+  if (g_gemm_scratch.p != nullptr) (void)hipFree(g_gemm_scratch.p);
+  g_gemm_scratch = Scratch{};
   g_stream = nullptr;
   g_device = -1;
   return LLMI_OK;

@@ -189,6 +189,9 @@ int launch_dequantize_rows(const DeviceMatrix& m, const std::int32_t* ids, std::
 // done in the GEMV's epilogue with the same two roundings.
 int launch_matmul(const DeviceMatrix& m, const float* x, std::size_t rows, const float* bias, float* y, hipStream_t s,
                   bool accumulate = false);
+// Frees the sampling workspace (llmi_hip_shutdown; the stream is idle).
+void release_sampling_workspace();
+
 // sample() on device logits (sampling.hip); *id_host receives the index and
 // `also` (device, may be null) too, on the stream.
 int sample_device(const float* logits, std::size_t n, const llmi_hip_sampling& cfg, double target,

@@ -757,6 +757,12 @@ int smp_bad_input(const SmpState& st) {
 
 }  // namespace
 
+void release_sampling_workspace() {
+  if (g_smp.base != nullptr) (void)hipFree(g_smp.base);
+  if (g_smp.sort_tmp != nullptr) (void)hipFree(g_smp.sort_tmp);
+  g_smp = SmpBuffers{};
+}
+
 // Draws one index on the device; *id_host receives it.  `also` (device, may
 // be null) receives it too, on the stream, before the host learns it.
 int sample_device(const float* logits, std::size_t n, const llmi_hip_sampling& cfg, double target,

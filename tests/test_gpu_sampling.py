@@ -209,3 +209,16 @@ def test_model_steps_sample_like_the_reference_loop(qt):
     ids = gm.generate_sampled(prompt, steps, H.Sampling(*sc), targets, stop_ids=[stop])
     assert list(ids) == want[: want.index(stop) + 1]
     gm.free()
+
+
+def test_shutdown_releases_and_reinit_works():
+    """llmi_hip_shutdown frees the library's sampling and GEMM workspaces;
+    a later llmi_hip_init starts clean and sampling still gives the oracle's
+    index."""
+    lib = H.init()
+    lg = logits_case("normal", 5000, 21)
+    want = O.oracle().sample_target(lg, 0.9, 20, 0.9, 0.37)
+    assert H.sample(lg, H.Sampling(0.9, 20, 0.9), 0.37) == want
+    H.check(lib.llmi_hip_shutdown())
+    H.check(lib.llmi_hip_init(0))
+    assert H.sample(lg, H.Sampling(0.9, 20, 0.9), 0.37) == want
