@@ -654,13 +654,19 @@ __global__ void __launch_bounds__(256) qgemm_exact(const uint4* __restrict__ cod
   for (int i = 0; i < RT; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = 0.0f;
-  Staged st;
-  load(st, 0);
-  store(st, 0);
+  // Two register sets carry the staged blocks two iterations ahead: set A
+  // the odd blocks, set B the even ones past block 0.  Iteration b computes
+  // block b from LDS, stores block b + 1 (loaded two iterations earlier)
+  // into the other LDS buffer and loads block b + 3 into the set it freed,
+  // so a block's global loads have two blocks of arithmetic to arrive.
+  Staged A, B;
+  load(B, 0);
+  store(B, 0);
+  if (nblk > 1) load(A, 1);
+  if (nblk > 2) load(B, 2);
   __syncthreads();
-  for (int b = 0; b < nblk; ++b) {
+  const auto iteration = [&](int b, Staged& next) {
     const int buf = b & 1;
-    if (b + 1 < nblk) load(st, b + 1);
     const int len = min(kBlock, in - b * kBlock);
     const float* xb = xs[buf] + RT * tr;
     const float* cb = cs[buf] + 4 * to;
@@ -691,8 +697,15 @@ __global__ void __launch_bounds__(256) qgemm_exact(const uint4* __restrict__ cod
 #pragma unroll
       for (int i = 0; i < RT; ++i) acc[i][j] = __builtin_fmaf(part[i][j], sc, acc[i][j]);
     }
-    if (b + 1 < nblk) store(st, buf ^ 1);
+    if (b + 1 < nblk) {
+      store(next, buf ^ 1);
+      if (b + 3 < nblk) load(next, b + 3);
+    }
     __syncthreads();
+  };
+  for (int b = 0; b < nblk; b += 2) {
+    iteration(b, A);
+    if (b + 1 < nblk) iteration(b + 1, B);
   }
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
