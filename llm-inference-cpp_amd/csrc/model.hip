@@ -314,6 +314,248 @@ __global__ void __launch_bounds__(kThreads) attention_hd16(const float* __restri
   }
 }
 
+// ------------------------------------------------ prefill attention, hd 64
+// The same arithmetic as attention_hd16 with one workgroup per (KV head,
+// tile of tq tokens).  Its rows are the G = nh / nkv query heads of that KV
+// head for each token of the tile (row = tt * G + g, at most kAttnRows), and
+// they share every K and V row the workgroup stages.  Phases:
+//  scores  64-position K tiles in LDS (double buffered through registers);
+//          thread (rg, pg) computes rows rg + 8r (r < 4) x positions pg,
+//          pg + 32: each score is 16 fused lanes (lane j over elements j,
+//          j+16, j+32, j+48), lanes j and j+8 added, then j and j+4, then
+//          (0 + 2) + (1 + 3) -- kernels::dot's order -- plus 0.0f, times
+//          scale.  Scores go to LDS sc[position][row].
+//  softmax thread (row, phase): float max, exact expf and double partial
+//          sums over positions phase, phase + 8, ...; the 8 partials are
+//          added in a fixed order and the float reciprocal is taken from that
+//          sum when the order bound proves the sequential sum gives the same
+//          float, otherwise one thread re-adds the row in order.
+//  P.V     64-position V tiles in LDS; thread (rp, dq) runs the chains of
+//          rows 2rp, 2rp + 1 x dims 4dq..4dq+3 in position order:
+//          out = fma(p_s, v_s[i], out).  Positions every row of the
+//          workgroup attends to run unchecked; the diagonal ones are checked
+//          per row.
+constexpr int kAttnRows = 32;
+constexpr int kAttnTile = 64;
+constexpr int kAttnStride = 68;  // LDS floats per staged row: 16-byte aligned, consecutive rows 4 banks apart
+constexpr int kAttnPhases = kThreads / kAttnRows;
+constexpr std::size_t kAttnStaticLds =
+    (kAttnRows * kAttnStride + 2 * kAttnTile * kAttnStride + kAttnPhases * kAttnRows + kAttnRows) * sizeof(float) +
+    kAttnPhases * kAttnRows * sizeof(double) + 256;
+
+// One thread's share (4 float4) of a 64 x 64 tile of the cache starting at
+// position s0; positions at or past npos are not read.
+__device__ __forceinline__ void attn_load_tile(const float* __restrict__ src, int s0, int npos, float4 (&r)[4]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int f = threadIdx.x + kThreads * i;
+    const int p = s0 + (f >> 4);
+    if (p < npos) r[i] = *reinterpret_cast<const float4*>(src + static_cast<std::size_t>(p) * 64 + 4 * (f & 15));
+  }
+}
+__device__ __forceinline__ void attn_store_tile(float* dst, const float4 (&r)[4]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int f = threadIdx.x + kThreads * i;
+    *reinterpret_cast<float4*>(dst + (f >> 4) * kAttnStride + 4 * (f & 15)) = r[i];
+  }
+}
+
+// Lanes j0..j0+3 of the 16-lane dot for 4 rows x 2 positions.
+__device__ __forceinline__ void attn_quad(const float* q0, const float* k0, int j0, float (&L)[4][2][4]) {
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+#pragma unroll
+    for (int p = 0; p < 2; ++p)
+#pragma unroll
+      for (int u = 0; u < 4; ++u) L[r][p][u] = 0.0f;
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    float4 qv[4], kv[2];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) qv[r] = *reinterpret_cast<const float4*>(q0 + 8 * r * kAttnStride + 16 * c + j0);
+#pragma unroll
+    for (int p = 0; p < 2; ++p) kv[p] = *reinterpret_cast<const float4*>(k0 + 32 * p * kAttnStride + 16 * c + j0);
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+      for (int p = 0; p < 2; ++p) {
+        L[r][p][0] = __builtin_fmaf(qv[r].x, kv[p].x, L[r][p][0]);
+        L[r][p][1] = __builtin_fmaf(qv[r].y, kv[p].y, L[r][p][1]);
+        L[r][p][2] = __builtin_fmaf(qv[r].z, kv[p].z, L[r][p][2]);
+        L[r][p][3] = __builtin_fmaf(qv[r].w, kv[p].w, L[r][p][3]);
+      }
+  }
+}
+
+__global__ void __launch_bounds__(kThreads) attention_rows64(const float* __restrict__ q, const float* __restrict__ kc,
+                                                             const float* __restrict__ vc, float* __restrict__ out,
+                                                             int nh, int nkv, int cap, int base, int T, int tq,
+                                                             float scale) {
+  extern __shared__ float sc[];  // [position][kAttnRows]
+  __shared__ __attribute__((aligned(16))) float qs[kAttnRows * kAttnStride];
+  __shared__ __attribute__((aligned(16))) float tile[2][kAttnTile * kAttnStride];
+  __shared__ double red_d[kAttnPhases][kAttnRows];
+  __shared__ float red_f[kAttnPhases][kAttnRows];
+  __shared__ float inv_s[kAttnRows];
+  const int G = nh / nkv;
+  const int kvh = blockIdx.y;
+  const int t0 = (static_cast<int>(gridDim.x) - 1 - static_cast<int>(blockIdx.x)) * tq;  // longest rows first
+  const int ntok = min(tq, T - t0);
+  const int nrows = ntok * G;
+  const int npos_max = base + t0 + ntok;  // positions of the tile's last token
+  const int npos_min = base + t0 + 1;     // positions every row attends to
+  const float* kh = kc + static_cast<std::size_t>(kvh) * cap * 64;
+  const float* vh = vc + static_cast<std::size_t>(kvh) * cap * 64;
+  const int tid = threadIdx.x;
+
+  for (int f = tid; f < kAttnRows * 16; f += kThreads) {
+    const int row = f >> 4, e4 = f & 15;
+    float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (row < nrows) {
+      const int tt = row / G, g = row - tt * G;
+      v = *reinterpret_cast<const float4*>(q + (static_cast<std::size_t>(t0 + tt) * nh + kvh * G + g) * 64 + 4 * e4);
+    }
+    *reinterpret_cast<float4*>(qs + row * kAttnStride + 4 * e4) = v;
+  }
+
+  // ---- scores
+  const int ntile = (npos_max + kAttnTile - 1) / kAttnTile;
+  float4 st[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) st[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  attn_load_tile(kh, 0, npos_max, st);
+  attn_store_tile(tile[0], st);
+  if (ntile > 1) attn_load_tile(kh, kAttnTile, npos_max, st);
+  __syncthreads();
+  {
+    const int rg = tid & 7, pg = tid >> 3;
+    const float* q0 = qs + rg * kAttnStride;
+    for (int k = 0; k < ntile; ++k) {
+      const float* k0 = tile[k & 1] + pg * kAttnStride;
+      float A[4][2][4], B[4][2][4], C[4][2][4];
+      attn_quad(q0, k0, 0, A);
+      attn_quad(q0, k0, 8, B);
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int p = 0; p < 2; ++p)
+#pragma unroll
+          for (int u = 0; u < 4; ++u) A[r][p][u] = A[r][p][u] + B[r][p][u];  // lanes j + (j + 8), j < 4
+      attn_quad(q0, k0, 4, B);
+      attn_quad(q0, k0, 12, C);
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+          float s4[4];
+#pragma unroll
+          for (int u = 0; u < 4; ++u) s4[u] = A[r][p][u] + (B[r][p][u] + C[r][p][u]);  // + lanes (j+4) + (j+12)
+          const float head = (s4[0] + s4[2]) + (s4[1] + s4[3]);
+          sc[(k * kAttnTile + pg + 32 * p) * kAttnRows + rg + 8 * r] = (head + 0.0f) * scale;
+        }
+      if (k + 1 < ntile) {
+        attn_store_tile(tile[(k + 1) & 1], st);
+        if (k + 2 < ntile) attn_load_tile(kh, (k + 2) * kAttnTile, npos_max, st);
+      }
+      __syncthreads();
+    }
+  }
+  attn_load_tile(vh, 0, npos_max, st);  // in flight during the softmax
+
+  // ---- softmax
+  {
+    const int row = tid & (kAttnRows - 1), ph = tid / kAttnRows;
+    const int np = row < nrows ? base + t0 + row / G + 1 : 0;
+    float m = -__builtin_inff();
+    for (int s = ph; s < np; s += kAttnPhases) m = fmaxf(m, sc[s * kAttnRows + row]);
+    red_f[ph][row] = m;
+    __syncthreads();
+    float mx = red_f[0][row];
+#pragma unroll
+    for (int i = 1; i < kAttnPhases; ++i) mx = fmaxf(mx, red_f[i][row]);
+    double part = 0.0;
+    for (int s = ph; s < np; s += kAttnPhases) {
+      const float e = exact::expf(sc[s * kAttnRows + row] - mx);
+      sc[s * kAttnRows + row] = e;
+      part += static_cast<double>(e);
+    }
+    red_d[ph][row] = part;
+    __syncthreads();
+    if (ph == 0 && row < nrows) {
+      double sum = red_d[0][row];
+#pragma unroll
+      for (int i = 1; i < kAttnPhases; ++i) sum = sum + red_d[i][row];
+      const double slack = sum_slack(np) * sum;
+      float inv = recip_float(sum);
+      if (recip_float(sum - slack) != recip_float(sum + slack)) {
+        double seq = 0.0;
+        for (int s = 0; s < np; ++s) seq += static_cast<double>(sc[s * kAttnRows + row]);
+        inv = recip_float(seq);
+      }
+      inv_s[row] = inv;
+    }
+    __syncthreads();
+    if (np > 0) {
+      const float inv = inv_s[row];
+      for (int s = ph; s < np; s += kAttnPhases) sc[s * kAttnRows + row] = sc[s * kAttnRows + row] * inv;
+    }
+  }
+
+  // ---- P.V
+  attn_store_tile(tile[0], st);
+  if (ntile > 1) attn_load_tile(vh, kAttnTile, npos_max, st);
+  __syncthreads();
+  const int rp = tid >> 4, dq = tid & 15;
+  const int ra = 2 * rp;
+  const int np_a = ra < nrows ? base + t0 + ra / G + 1 : npos_max;
+  const int np_b = ra + 1 < nrows ? base + t0 + (ra + 1) / G + 1 : npos_max;
+  float acc[2][4] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
+  const auto step = [&](const float* vt, int s, int u, bool checked) {
+    const float2 p = *reinterpret_cast<const float2*>(sc + s * kAttnRows + ra);
+    const float4 v = *reinterpret_cast<const float4*>(vt + u * kAttnStride + 4 * dq);
+    if (!checked || s < np_a) {
+      acc[0][0] = __builtin_fmaf(p.x, v.x, acc[0][0]);
+      acc[0][1] = __builtin_fmaf(p.x, v.y, acc[0][1]);
+      acc[0][2] = __builtin_fmaf(p.x, v.z, acc[0][2]);
+      acc[0][3] = __builtin_fmaf(p.x, v.w, acc[0][3]);
+    }
+    if (!checked || s < np_b) {
+      acc[1][0] = __builtin_fmaf(p.y, v.x, acc[1][0]);
+      acc[1][1] = __builtin_fmaf(p.y, v.y, acc[1][1]);
+      acc[1][2] = __builtin_fmaf(p.y, v.z, acc[1][2]);
+      acc[1][3] = __builtin_fmaf(p.y, v.w, acc[1][3]);
+    }
+  };
+  for (int k = 0; k < ntile; ++k) {
+    const float* vt = tile[k & 1];
+    const int s0 = k * kAttnTile;
+    const int cnt = min(kAttnTile, npos_max - s0);
+    const int full = max(0, min(cnt, npos_min - s0));
+    int u = 0;
+    for (; u + 8 <= full; u += 8) {
+#pragma unroll
+      for (int w = 0; w < 8; ++w) step(vt, s0 + u + w, u + w, false);
+    }
+    for (; u < full; ++u) step(vt, s0 + u, u, false);
+    for (; u < cnt; ++u) step(vt, s0 + u, u, true);
+    if (k + 1 < ntile) {
+      attn_store_tile(tile[(k + 1) & 1], st);
+      if (k + 2 < ntile) attn_load_tile(vh, (k + 2) * kAttnTile, npos_max, st);
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int row = ra + i;
+    if (row < nrows) {
+      const int tt = row / G, g = row - tt * G;
+      *reinterpret_cast<float4*>(out + (static_cast<std::size_t>(t0 + tt) * nh + kvh * G + g) * 64 + 4 * dq) =
+          make_float4(acc[i][0], acc[i][1], acc[i][2], acc[i][3]);
+    }
+  }
+}
+
 // ------------------------------------------------- decode attention (T = 1)
 // The same arithmetic as attention_hd16 for one new token, restructured for
 // latency: the one-workgroup-per-head kernel spends ~140 ns per cached
@@ -623,9 +865,27 @@ std::size_t attention_dyn_lds(std::size_t npos, std::size_t hd) {
   return hd % 16 == 0 && hd <= 256 ? (npos + 2 * kVTile * hd) * sizeof(float) : npos * sizeof(float);
 }
 
+// Scores LDS of attention_rows64 when its longest row attends to npos
+// positions (whole 64-position tiles).
+std::size_t attention_rows_lds(std::size_t npos) {
+  return ceil_div(npos, static_cast<std::size_t>(kAttnTile)) * kAttnTile * kAttnRows * sizeof(float);
+}
+
+bool attention_rows_fits(int nh, int nkv, int hd, std::size_t npos) {
+  return hd == 64 && nkv >= 1 && nh % nkv == 0 && nh / nkv <= kAttnRows &&
+         attention_rows_lds(npos) + kAttnStaticLds <= max_lds_per_block();
+}
+
 void launch_attention(const float* q, const float* kc, const float* vc, float* out, int nh, int nkv, int hd, int cap,
                       int base, int T, float scale, hipStream_t s) {
   const std::size_t npos = static_cast<std::size_t>(base) + T;
+  if (attention_rows_fits(nh, nkv, hd, npos)) {
+    const int tq = kAttnRows / (nh / nkv);
+    const dim3 grid(static_cast<unsigned>(ceil_div(T, tq)), static_cast<unsigned>(nkv));
+    attention_rows64<<<grid, kThreads, attention_rows_lds(npos), s>>>(q, kc, vc, out, nh, nkv, cap, base, T, tq,
+                                                                      scale);
+    return;
+  }
   const dim3 grid(static_cast<unsigned>(nh), static_cast<unsigned>(T));
   if (hd % 16 == 0 && hd <= 256) {
     attention_hd16<<<grid, kThreads, attention_dyn_lds(npos, hd), s>>>(q, kc, vc, out, nh, nkv, hd, cap, base, scale,

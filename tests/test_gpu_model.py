@@ -241,3 +241,57 @@ def test_decode_attention_matches_reference(hidden, heads, kv):
     cache.free()
     gm.free()
     cm.close()
+
+
+# ----------------------------------------------- prefill attention shapes
+@pytest.mark.parametrize("hidden,heads,kv", [(64, 1, 1), (256, 4, 2), (192, 3, 1), (448, 7, 1), (576, 9, 3),
+                                             (2048, 32, 1), (256, 2, 1)])
+def test_prefill_attention_matches_reference(hidden, heads, kv):
+    """Multi-token forward passes after earlier ones (base > 0): head size 64
+    with GQA groups of 1 to 32 takes the workgroup-per-(KV head, token tile)
+    prefill attention, head size 128 the per-(head, token) kernel.  Chunk
+    lengths leave ragged token tiles and end on and off the 64-position K/V
+    tiles; every position's logits equal the reference's bit for bit."""
+    cpu = O.reference() or O.oracle()
+    cfg = dict(arch=1, vocab_size=64, hidden_size=hidden, intermediate_size=2 * hidden, num_layers=2,
+               num_heads=heads, num_kv_heads=kv, max_position_embeddings=512, rms_norm_eps=1e-6,
+               rope_theta=10000.0, tie_word_embeddings=1, qkv_bias=1)
+    tensors = synth.make_tensors(cfg, hidden + 3 * heads, "bench")
+    gm = H.Model(cfg, tensors, H.Q8_0)
+    cm = O.CpuModel(cpu, cfg, tensors, O.Q8_0)
+    chunks = [37, 1, 90, 64, 128, 23]
+    ids = synth.uniform_ids(hidden + 1, sum(chunks), cfg["vocab_size"])
+    cache = gm.new_cache(sum(chunks))
+    assert cm.new_cache(sum(chunks))
+    at = 0
+    for n in chunks:
+        got = gm.forward_cached(cache, ids[at:at + n], all_positions=True)
+        want = cm.forward_cached(ids[at:at + n], all_positions=True)
+        assert np.array_equal(bits(got), bits(want)), (hidden, heads, kv, at, n)
+        at += n
+    cache.free()
+    gm.free()
+    cm.close()
+
+
+def test_prefill_attention_past_the_lds_scores():
+    """A prompt longer than the workgroup-per-tile kernel's LDS holds (about
+    900 positions) takes the per-(head, token) kernel; logits still equal the
+    reference's."""
+    cpu = O.reference() or O.oracle()
+    cfg = dict(arch=0, vocab_size=64, hidden_size=128, intermediate_size=256, num_layers=1, num_heads=2,
+               num_kv_heads=1, max_position_embeddings=1100, rms_norm_eps=1e-5, rope_theta=10000.0,
+               tie_word_embeddings=1, qkv_bias=0)
+    tensors = synth.make_tensors(cfg, 5, "bench")
+    gm = H.Model(cfg, tensors, H.Q4_0)
+    cm = O.CpuModel(cpu, cfg, tensors, O.Q4_0)
+    ids = synth.uniform_ids(6, 1100, cfg["vocab_size"])
+    cache = gm.new_cache(1100)
+    assert cm.new_cache(1100)
+    for a, b in ((0, 700), (700, 1100)):
+        got = gm.forward_cached(cache, ids[a:b], all_positions=True)
+        want = cm.forward_cached(ids[a:b], all_positions=True)
+        assert np.array_equal(bits(got), bits(want)), (a, b)
+    cache.free()
+    gm.free()
+    cm.close()
