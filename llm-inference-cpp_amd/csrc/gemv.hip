@@ -724,6 +724,99 @@ __global__ void __launch_bounds__(256) qgemm_exact(const uint4* __restrict__ cod
   }
 }
 
+// qgemm_split (batch > 8, matrices with few 64-row tiles): one workgroup per
+// (tile, chunk of kSplitRows input rows) whose kSplitWaves wavefronts take
+// the tile's blocks round-robin.  In each round wavefront w decodes block
+// round * kSplitWaves + w once (lane l: output tile*64 + l) and forms its
+// block sums for every row of the chunk, with the activations read by
+// scalar loads; the sums and scales go to LDS (two buffers, one barrier per
+// round), and wavefront w then advances the chains of rows w, w +
+// kSplitWaves over the round's blocks in order: acc = fma(part, scale, acc).
+// The block sums are the reference's per-block chains and the chain over
+// blocks runs in block order, so y is bit-identical; splitting the blocks
+// fills the GPU where a 64-row tile per row chunk gives too few workgroups.
+constexpr int kSplitRows = 16;
+constexpr int kSplitWaves = 8;
+
+template <int TYPE>
+__global__ void __launch_bounds__(kSplitWaves * 64) qgemm_split(const uint4* __restrict__ codes,
+                                                                const float* __restrict__ scales,
+                                                                const float* __restrict__ x,
+                                                                const float* __restrict__ bias, float* __restrict__ y,
+                                                                int in, int nblk, int out, int rows, int accumulate) {
+  constexpr int RW = kSplitRows / kSplitWaves;  // chains per lane
+  __shared__ float part[2][kSplitRows][kSplitWaves][kTileRows];
+  __shared__ float scl[2][kSplitWaves][kTileRows];
+  const std::size_t tile = blockIdx.x;
+  const int r0 = blockIdx.y * kSplitRows;
+  const int nr = min(kSplitRows, rows - r0);
+  const int lane = threadIdx.x & (kTileRows - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const GMEM uint4* cg = gmem(codes);
+  const GMEM float* sg = gmem(scales);
+  const GMEM float* xg = gmem(x) + static_cast<std::size_t>(r0) * in;
+  const int nfull = in / kBlock;
+  const std::size_t base = tile * nblk;
+  float acc[RW];
+#pragma unroll
+  for (int i = 0; i < RW; ++i) acc[i] = 0.0f;
+  const int nround = (nblk + kSplitWaves - 1) / kSplitWaves;
+  Block<TYPE> cur{};
+  float cur_s = 0.0f;
+  if (wave < nblk) {
+    cur = load_block<TYPE, false>(cg, base + wave, lane);
+    cur_s = sg[(base + wave) * kTileRows + lane];
+  }
+  for (int rd = 0; rd < nround; ++rd) {
+    const int buf = rd & 1;
+    const int b = rd * kSplitWaves + wave;
+    Block<TYPE> nxt{};
+    float nxt_s = 0.0f;
+    if (b + kSplitWaves < nblk) {
+      nxt = load_block<TYPE, false>(cg, base + b + kSplitWaves, lane);
+      nxt_s = sg[(base + b + kSplitWaves) * kTileRows + lane];
+    }
+    if (b < nfull) {
+      float c[kBlock];
+      block_codes<TYPE>(cur, c);
+#pragma unroll
+      for (int r = 0; r < kSplitRows; ++r)
+        if (r < nr) part[buf][r][wave][lane] = codes_dot(c, xg + static_cast<std::size_t>(r) * in + b * kBlock);
+    } else if (b < nblk) {
+      for (int r = 0; r < nr; ++r)
+        part[buf][r][wave][lane] =
+            tail_block_dot<TYPE>(cur, xg + static_cast<std::size_t>(r) * in + b * kBlock, in - b * kBlock);
+    }
+    if (b < nblk) scl[buf][wave][lane] = cur_s;
+    __syncthreads();
+    const int nb = min(kSplitWaves, nblk - rd * kSplitWaves);
+#pragma unroll
+    for (int i = 0; i < RW; ++i) {
+      const int r = wave + kSplitWaves * i;
+      if (r < nr) {
+        float a = acc[i];
+        for (int j = 0; j < nb; ++j) a = __builtin_fmaf(part[buf][r][j][lane], scl[buf][j][lane], a);
+        acc[i] = a;
+      }
+    }
+    cur = nxt;
+    cur_s = nxt_s;
+  }
+  const std::size_t o = tile * kTileRows + lane;
+  if (o < static_cast<std::size_t>(out)) {
+    const float add = bias != nullptr ? bias[o] : 0.0f;
+#pragma unroll
+    for (int i = 0; i < RW; ++i) {
+      const int r = wave + kSplitWaves * i;
+      if (r < nr) {
+        float* dst = y + static_cast<std::size_t>(r0 + r) * out + o;
+        const float v = acc[i] + add;
+        *dst = accumulate ? *dst + v : v;
+      }
+    }
+  }
+}
+
 // ------------------------------------------------------------ planning
 // LDS bytes of one workgroup of each kind.
 std::size_t wide_lds(std::size_t nblk, std::size_t nr) { return (nr + 1) * nblk * kTileRows * sizeof(float); }
@@ -822,9 +915,30 @@ void launch_exact(const DeviceMatrix& m, const float* x, std::size_t rows, const
                                              static_cast<int>(m.out), static_cast<int>(rows), acc);
 }
 
+// Multi-row products on few 64-row tiles take qgemm_split: qgemm_exact runs
+// each tile's blocks in one workgroup, and below about 1024 workgroups of
+// 32-row chunks the GPU is mostly idle.
+bool use_split(std::size_t ntiles, std::size_t rows) {
+  constexpr std::size_t kExactMin = 1024;
+  return ntiles * ceil_div(rows, 32) < kExactMin;
+}
+
+template <int TYPE>
+void launch_split(const DeviceMatrix& m, const float* x, std::size_t rows, const float* bias, float* y, int acc,
+                  hipStream_t s) {
+  const dim3 grid(static_cast<unsigned>(m.ntiles), static_cast<unsigned>(ceil_div(rows, kSplitRows)));
+  qgemm_split<TYPE><<<grid, kSplitWaves * 64, 0, s>>>(reinterpret_cast<const uint4*>(m.codes), m.scales, x, bias, y,
+                                                      static_cast<int>(m.in), static_cast<int>(m.nblk),
+                                                      static_cast<int>(m.out), static_cast<int>(rows), acc);
+}
+
 template <int TYPE>
 void launch_rows(const DeviceMatrix& m, const float* x, std::size_t rows, const float* bias, float* y, int acc,
                  hipStream_t s) {
+  if (use_split(m.ntiles, rows)) {
+    launch_split<TYPE>(m, x, rows, bias, y, acc, s);
+    return;
+  }
   switch (exact_rows_tile(m.ntiles, rows)) {
     case 64: launch_exact<TYPE, 64>(m, x, rows, bias, y, acc, s); break;
     case 32: launch_exact<TYPE, 32>(m, x, rows, bias, y, acc, s); break;

@@ -57,8 +57,11 @@ def test_baseline_shapes_match_reference(golden):
 @pytest.mark.parametrize("qt", [O.Q8_0, O.Q4_0])
 @pytest.mark.parametrize("rows", [1, 2, 3, 4, 5, 7, 8, 9, 17, 64])
 @pytest.mark.parametrize("out,n_in", [(1, 1), (63, 33), (65, 100), (200, 576), (130, 4864), (96, 8192),
-                                      (40, 20000)])
+                                      (40, 20000), (40000, 100)])
 def test_batches_and_ragged_shapes_match_oracle(qt, rows, out, n_in):
+    """Every kernel shape: batch 1-8 GEMVs; above 8 rows the split-block
+    product on few tiles and the per-tile product on many (40000 outputs at
+    64 rows)."""
     orc = O.oracle()
     w = synth.normal(out * 7 + n_in, out * n_in, 0.0, 0.02)
     x = synth.normal(rows * 13 + n_in, rows * n_in, 0.0, 1.0)
