@@ -29,9 +29,13 @@
 // (one kernel per row chunk R present); each workgroup runs one tile of one
 // product with the same tile functions.
 //
-// qgemm_exact (batch > 8, the exact prefill path): 64, 32 or 16 input rows
-// x 64 outputs per workgroup, 4 x 4 / 2 x 4 / 1 x 4 chains per thread,
-// operands from LDS.
+// qgemm_exact (batch > 8 on matrices with many tiles, e.g. an lm_head over
+// every position): 64 input rows x 64 outputs per workgroup, 4 x 4 chains
+// per thread, operands from LDS.
+//
+// qgemm_split (batch > 8 on matrices with few tiles, the prefill's
+// projections): a tile's blocks spread over the workgroup's wavefronts,
+// activations from scalar loads, block sums and scales through LDS.
 //
 // fp32 weights take kernels::matmul instead (f32.hip).
 #include <algorithm>
@@ -571,44 +575,25 @@ __global__ void __launch_bounds__(1024) qgemv_group_narrow(const GroupProblem* _
 }
 
 // ------------------------------------------------------------ batch > 8
-// The exact multi-row product (the model's own prefill): one workgroup per
-// MR input rows (64, 32 or 16, chosen for parallelism) x one 64-row tile of
-// the matrix (64 outputs).  Per quantization block the workgroup stages the
-// block's activations of its MR rows and the block's codes of its 64
-// outputs, converted to fp32 once, in LDS -- transposed, [k][row] and
-// [k][output], so one read gives a thread its RT = MR/16 rows (or 4 outputs)
-// at one k -- plus the 64 scales; double-buffered: the next block's loads
-// go to registers before this block's arithmetic and to LDS after it.
-// Thread (tr, to) holds the RT x 4 chains of rows RT*tr.. and outputs
-// 4to..4to+3: part = fma(x[k], code[k], part) over the block's k in order,
-// then acc = fma(part, scale, acc) -- the reference's chains, so y is
+// The exact multi-row product on many tiles: one workgroup per MR = 64
+// input rows x one 64-row tile of the matrix (64 outputs).  Per quantization
+// block the workgroup stages the block's activations of its MR rows and the
+// block's codes of its 64 outputs, converted to fp32 once, in LDS --
+// transposed, [k][row] and [k][output], so one read gives a thread its 4
+// rows (or 4 outputs) at one k -- plus the 64 scales; double-buffered: the
+// next block's loads go to registers before this block's arithmetic and to
+// LDS after it.  Thread (tr, to) holds the 4 x 4 chains of rows 4tr.. and
+// outputs 4to..4to+3: part = fma(x[k], code[k], part) over the block's k in
+// order, then acc = fma(part, scale, acc) -- the reference's chains, so y is
 // bit-identical.  The final partial block runs only its len elements.
-template <int MR>
-struct RowVec;
-template <>
-struct RowVec<64> {
-  static __device__ __forceinline__ void get(const float* p, float* v) {
-    const float4 t = *reinterpret_cast<const float4*>(p);
-    v[0] = t.x; v[1] = t.y; v[2] = t.z; v[3] = t.w;
-  }
-};
-template <>
-struct RowVec<32> {
-  static __device__ __forceinline__ void get(const float* p, float* v) {
-    const float2 t = *reinterpret_cast<const float2*>(p);
-    v[0] = t.x; v[1] = t.y;
-  }
-};
-template <>
-struct RowVec<16> {
-  static __device__ __forceinline__ void get(const float* p, float* v) { v[0] = *p; }
-};
+constexpr int kExactRows = 64;
 
-template <int TYPE, int MR>
+template <int TYPE>
 __global__ void __launch_bounds__(256) qgemm_exact(const uint4* __restrict__ codes, const float* __restrict__ scales,
                                                    const float* __restrict__ x, const float* __restrict__ bias,
                                                    float* __restrict__ y, int in, int nblk, int out, int rows,
                                                    int accumulate) {
+  constexpr int MR = kExactRows;
   constexpr int RT = MR / 16;          // rows per thread
   constexpr int XS = MR + 4;           // LDS floats per k of the activations
   constexpr int CSTRIDE = kTileRows + 4;
@@ -676,8 +661,8 @@ __global__ void __launch_bounds__(256) qgemm_exact(const uint4* __restrict__ cod
 #pragma unroll
       for (int j = 0; j < 4; ++j) part[i][j] = 0.0f;
     const auto step = [&](int k) {
-      float xa[RT];
-      RowVec<MR>::get(xb + k * XS, xa);
+      const float4 xv = *reinterpret_cast<const float4*>(xb + k * XS);
+      const float xa[RT] = {xv.x, xv.y, xv.z, xv.w};
       const float4 cv = *reinterpret_cast<const float4*>(cb + k * CSTRIDE);
       const float ca[4] = {cv.x, cv.y, cv.z, cv.w};
 #pragma unroll
@@ -735,16 +720,15 @@ __global__ void __launch_bounds__(256) qgemm_exact(const uint4* __restrict__ cod
 // The block sums are the reference's per-block chains and the chain over
 // blocks runs in block order, so y is bit-identical; splitting the blocks
 // fills the GPU where a 64-row tile per row chunk gives too few workgroups.
-constexpr int kSplitRows = 16;
-constexpr int kSplitWaves = 8;
-
-template <int TYPE>
+// Small row chunks (2 or 4 rows) measured fastest: the chunk's activations
+// are scalar loads per block and row, and more workgroups hide them.
+template <int TYPE, int kSplitRows, int kSplitWaves>
 __global__ void __launch_bounds__(kSplitWaves * 64) qgemm_split(const uint4* __restrict__ codes,
                                                                 const float* __restrict__ scales,
                                                                 const float* __restrict__ x,
                                                                 const float* __restrict__ bias, float* __restrict__ y,
                                                                 int in, int nblk, int out, int rows, int accumulate) {
-  constexpr int RW = kSplitRows / kSplitWaves;  // chains per lane
+  constexpr int RW = (kSplitRows + kSplitWaves - 1) / kSplitWaves;  // chains per lane
   __shared__ float part[2][kSplitRows][kSplitWaves][kTileRows];
   __shared__ float scl[2][kSplitWaves][kTileRows];
   const std::size_t tile = blockIdx.x;
@@ -793,7 +777,7 @@ __global__ void __launch_bounds__(kSplitWaves * 64) qgemm_split(const uint4* __r
 #pragma unroll
     for (int i = 0; i < RW; ++i) {
       const int r = wave + kSplitWaves * i;
-      if (r < nr) {
+      if (r < kSplitRows && r < nr) {
         float a = acc[i];
         for (int j = 0; j < nb; ++j) a = __builtin_fmaf(part[buf][r][j][lane], scl[buf][j][lane], a);
         acc[i] = a;
@@ -808,7 +792,7 @@ __global__ void __launch_bounds__(kSplitWaves * 64) qgemm_split(const uint4* __r
 #pragma unroll
     for (int i = 0; i < RW; ++i) {
       const int r = wave + kSplitWaves * i;
-      if (r < nr) {
+      if (r < kSplitRows && r < nr) {
         float* dst = y + static_cast<std::size_t>(r0 + r) * out + o;
         const float v = acc[i] + add;
         *dst = accumulate ? *dst + v : v;
@@ -896,54 +880,37 @@ void launch_tile(const DeviceMatrix& m, const float* x, std::size_t rows, const 
       static_cast<int>(m.out), static_cast<int>(rows), p.bpw, acc);
 }
 
-// Row tile of the exact multi-row product: the largest MR that still gives
-// about 1024 workgroups (4 wavefronts per SIMD), else 16.
-int exact_rows_tile(std::size_t ntiles, std::size_t rows) {
-  constexpr std::size_t kWant = 1024;
-  for (int mr : {64, 32}) {
-    if (ntiles * ceil_div(rows, static_cast<std::size_t>(mr)) >= kWant) return mr;
-  }
-  return 16;
-}
-
-template <int TYPE, int MR>
-void launch_exact(const DeviceMatrix& m, const float* x, std::size_t rows, const float* bias, float* y, int acc,
-                  hipStream_t s) {
-  const dim3 grid(static_cast<unsigned>(m.ntiles), static_cast<unsigned>(ceil_div(rows, MR)));
-  qgemm_exact<TYPE, MR><<<grid, 256, 0, s>>>(reinterpret_cast<const uint4*>(m.codes), m.scales, x, bias, y,
-                                             static_cast<int>(m.in), static_cast<int>(m.nblk),
-                                             static_cast<int>(m.out), static_cast<int>(rows), acc);
-}
-
-// Multi-row products on few 64-row tiles take qgemm_split: qgemm_exact runs
-// each tile's blocks in one workgroup, and below about 1024 workgroups of
-// 32-row chunks the GPU is mostly idle.
-bool use_split(std::size_t ntiles, std::size_t rows) {
-  constexpr std::size_t kExactMin = 1024;
-  return ntiles * ceil_div(rows, 32) < kExactMin;
-}
-
-template <int TYPE>
+template <int TYPE, int R, int W>
 void launch_split(const DeviceMatrix& m, const float* x, std::size_t rows, const float* bias, float* y, int acc,
                   hipStream_t s) {
-  const dim3 grid(static_cast<unsigned>(m.ntiles), static_cast<unsigned>(ceil_div(rows, kSplitRows)));
-  qgemm_split<TYPE><<<grid, kSplitWaves * 64, 0, s>>>(reinterpret_cast<const uint4*>(m.codes), m.scales, x, bias, y,
-                                                      static_cast<int>(m.in), static_cast<int>(m.nblk),
-                                                      static_cast<int>(m.out), static_cast<int>(rows), acc);
+  const dim3 grid(static_cast<unsigned>(m.ntiles), static_cast<unsigned>(ceil_div(rows, R)));
+  qgemm_split<TYPE, R, W><<<grid, W * 64, 0, s>>>(reinterpret_cast<const uint4*>(m.codes), m.scales, x, bias, y,
+                                                  static_cast<int>(m.in), static_cast<int>(m.nblk),
+                                                  static_cast<int>(m.out), static_cast<int>(rows), acc);
 }
 
+// Multi-row products.  qgemm_exact when its 64-row chunks alone give about
+// 1024 workgroups (an lm_head over every position); otherwise qgemm_split
+// with the row chunk and wavefront count measured fastest on MI355X for the
+// launch's size: 4 rows x 4 wavefronts from ~6K wavefronts up, 4 x 8 from
+// ~4K, else 2 x 8 (SmolLM2-135M and Qwen2.5-0.5B projections at 128 and 512
+// rows; Qwen2.5's gate/up 92 us split against 109 on qgemm_exact, its
+// 151936-row lm_head 2.46 ms split against 2.14).
 template <int TYPE>
 void launch_rows(const DeviceMatrix& m, const float* x, std::size_t rows, const float* bias, float* y, int acc,
                  hipStream_t s) {
-  if (use_split(m.ntiles, rows)) {
-    launch_split<TYPE>(m, x, rows, bias, y, acc, s);
+  constexpr std::size_t kExactMin = 1024;
+  if (m.ntiles * ceil_div(rows, kExactRows) >= kExactMin) {
+    const dim3 grid(static_cast<unsigned>(m.ntiles), static_cast<unsigned>(ceil_div(rows, kExactRows)));
+    qgemm_exact<TYPE><<<grid, 256, 0, s>>>(reinterpret_cast<const uint4*>(m.codes), m.scales, x, bias, y,
+                                           static_cast<int>(m.in), static_cast<int>(m.nblk), static_cast<int>(m.out),
+                                           static_cast<int>(rows), acc);
     return;
   }
-  switch (exact_rows_tile(m.ntiles, rows)) {
-    case 64: launch_exact<TYPE, 64>(m, x, rows, bias, y, acc, s); break;
-    case 32: launch_exact<TYPE, 32>(m, x, rows, bias, y, acc, s); break;
-    default: launch_exact<TYPE, 16>(m, x, rows, bias, y, acc, s); break;
-  }
+  const auto waves = [&](std::size_t r, std::size_t w) { return m.ntiles * ceil_div(rows, r) * w; };
+  if (waves(4, 4) >= 6144) launch_split<TYPE, 4, 4>(m, x, rows, bias, y, acc, s);
+  else if (waves(4, 8) >= 4096) launch_split<TYPE, 4, 8>(m, x, rows, bias, y, acc, s);
+  else launch_split<TYPE, 2, 8>(m, x, rows, bias, y, acc, s);
 }
 
 template <int TYPE>

@@ -57,11 +57,10 @@ def test_baseline_shapes_match_reference(golden):
 @pytest.mark.parametrize("qt", [O.Q8_0, O.Q4_0])
 @pytest.mark.parametrize("rows", [1, 2, 3, 4, 5, 7, 8, 9, 17, 64])
 @pytest.mark.parametrize("out,n_in", [(1, 1), (63, 33), (65, 100), (200, 576), (130, 4864), (96, 8192),
-                                      (40, 20000), (40000, 100)])
+                                      (40, 20000)])
 def test_batches_and_ragged_shapes_match_oracle(qt, rows, out, n_in):
-    """Every kernel shape: batch 1-8 GEMVs; above 8 rows the split-block
-    product on few tiles and the per-tile product on many (40000 outputs at
-    64 rows)."""
+    """Batch 1-8 GEMVs and, above 8 rows, the multi-row products on ragged
+    shapes."""
     orc = O.oracle()
     w = synth.normal(out * 7 + n_in, out * n_in, 0.0, 0.02)
     x = synth.normal(rows * 13 + n_in, rows * n_in, 0.0, 1.0)
@@ -72,6 +71,24 @@ def test_batches_and_ragged_shapes_match_oracle(qt, rows, out, n_in):
         got = dev.matmul(x, rows, b)
         want = orc.matmul(x, rows, n_in, data, scales, qt, out, b)
         assert np.array_equal(bits(got), bits(want)), (rows, out, n_in, b is None)
+
+
+@pytest.mark.parametrize("qt", [O.Q8_0, O.Q4_0])
+@pytest.mark.parametrize("out,n_in,rows", [(40000, 100, 100), (40000, 100, 64), (4000, 200, 64), (200, 576, 64),
+                                           (130, 4864, 33)])
+def test_multi_row_launch_shapes_match_oracle(qt, out, n_in, rows):
+    """Each multi-row launch shape with a partial final block: the per-tile
+    product (64-row chunks giving >= 1024 workgroups) and the split-block
+    product at 4 rows x 4 wavefronts, 4 x 8 and 2 x 8."""
+    orc = O.oracle()
+    w = synth.normal(out + 3 * n_in, out * n_in, 0.0, 0.02)
+    x = synth.normal(rows + 7 * n_in, rows * n_in, 0.0, 1.0)
+    bias = synth.normal(9, out, 0.0, 0.5)
+    data, scales = orc.quantize(w, out, n_in, qt)
+    dev = H.Weight.upload(data, scales, out, n_in, qt)
+    got = dev.matmul(x, rows, bias)
+    want = orc.matmul(x, rows, n_in, data, scales, qt, out, bias)
+    assert np.array_equal(bits(got), bits(want))
 
 
 @pytest.mark.parametrize("qt", [O.Q8_0, O.Q4_0])
