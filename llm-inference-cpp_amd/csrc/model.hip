@@ -317,31 +317,32 @@ __global__ void __launch_bounds__(kThreads) attention_hd16(const float* __restri
 // ------------------------------------------------ prefill attention, hd 64
 // The same arithmetic as attention_hd16 with one workgroup per (KV head,
 // tile of tq tokens).  Its rows are the G = nh / nkv query heads of that KV
-// head for each token of the tile (row = tt * G + g, at most kAttnRows), and
-// they share every K and V row the workgroup stages.  Phases:
+// head for each token of the tile (row = tt * G + g, at most ROWS = 16 or
+// 32), and they share every K and V row the workgroup stages.  Phases:
 //  scores  64-position K tiles in LDS (double buffered through registers);
-//          thread (rg, pg) computes rows rg + 8r (r < 4) x positions pg,
-//          pg + 32: each score is 16 fused lanes (lane j over elements j,
-//          j+16, j+32, j+48), lanes j and j+8 added, then j and j+4, then
-//          (0 + 2) + (1 + 3) -- kernels::dot's order -- plus 0.0f, times
-//          scale.  Scores go to LDS sc[position][row].
+//          thread (rg, pg) computes rows rg + RG*r (r < 4, RG = ROWS / 4) x
+//          positions pg + (64 / P)*p (p < P = RG / 4): each score is 16 fused
+//          lanes (lane j over elements j, j+16, j+32, j+48), lanes j and j+8
+//          added, then j and j+4, then (0 + 2) + (1 + 3) -- kernels::dot's
+//          order -- plus 0.0f, times scale.  Scores go to LDS
+//          sc[position][row].
 //  softmax thread (row, phase): float max, exact expf and double partial
-//          sums over positions phase, phase + 8, ...; the 8 partials are
+//          sums over positions phase, phase + 256/ROWS, ...; the partials are
 //          added in a fixed order and the float reciprocal is taken from that
 //          sum when the order bound proves the sequential sum gives the same
 //          float, otherwise one thread re-adds the row in order.
 //  P.V     64-position V tiles in LDS; thread (rp, dq) runs the chains of
-//          rows 2rp, 2rp + 1 x dims 4dq..4dq+3 in position order:
+//          rows RP*rp.. (RP = ROWS / 16) x dims 4dq..4dq+3 in position order:
 //          out = fma(p_s, v_s[i], out).  Positions every row of the
 //          workgroup attends to run unchecked; the diagonal ones are checked
 //          per row.
-constexpr int kAttnRows = 32;
 constexpr int kAttnTile = 64;
 constexpr int kAttnStride = 68;  // LDS floats per staged row: 16-byte aligned, consecutive rows 4 banks apart
-constexpr int kAttnPhases = kThreads / kAttnRows;
-constexpr std::size_t kAttnStaticLds =
-    (kAttnRows * kAttnStride + 2 * kAttnTile * kAttnStride + kAttnPhases * kAttnRows + kAttnRows) * sizeof(float) +
-    kAttnPhases * kAttnRows * sizeof(double) + 256;
+template <int ROWS>
+constexpr std::size_t attn_static_lds() {
+  return (ROWS * kAttnStride + 2 * kAttnTile * kAttnStride + (kThreads / ROWS) * ROWS + ROWS) * sizeof(float) +
+         (kThreads / ROWS) * ROWS * sizeof(double) + 256;
+}
 
 // One thread's share (4 float4) of a 64 x 64 tile of the cache starting at
 // position s0; positions at or past npos are not read.
@@ -361,25 +362,27 @@ __device__ __forceinline__ void attn_store_tile(float* dst, const float4 (&r)[4]
   }
 }
 
-// Lanes j0..j0+3 of the 16-lane dot for 4 rows x 2 positions.
-__device__ __forceinline__ void attn_quad(const float* q0, const float* k0, int j0, float (&L)[4][2][4]) {
+// Lanes j0..j0+3 of the 16-lane dot for 4 rows (RG apart) x P positions
+// (PS apart).
+template <int RG, int P, int PS>
+__device__ __forceinline__ void attn_quad(const float* q0, const float* k0, int j0, float (&L)[4][P][4]) {
 #pragma unroll
   for (int r = 0; r < 4; ++r)
 #pragma unroll
-    for (int p = 0; p < 2; ++p)
+    for (int p = 0; p < P; ++p)
 #pragma unroll
       for (int u = 0; u < 4; ++u) L[r][p][u] = 0.0f;
 #pragma unroll
   for (int c = 0; c < 4; ++c) {
-    float4 qv[4], kv[2];
+    float4 qv[4], kv[P];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) qv[r] = *reinterpret_cast<const float4*>(q0 + 8 * r * kAttnStride + 16 * c + j0);
+    for (int r = 0; r < 4; ++r) qv[r] = *reinterpret_cast<const float4*>(q0 + RG * r * kAttnStride + 16 * c + j0);
 #pragma unroll
-    for (int p = 0; p < 2; ++p) kv[p] = *reinterpret_cast<const float4*>(k0 + 32 * p * kAttnStride + 16 * c + j0);
+    for (int p = 0; p < P; ++p) kv[p] = *reinterpret_cast<const float4*>(k0 + PS * p * kAttnStride + 16 * c + j0);
 #pragma unroll
     for (int r = 0; r < 4; ++r)
 #pragma unroll
-      for (int p = 0; p < 2; ++p) {
+      for (int p = 0; p < P; ++p) {
         L[r][p][0] = __builtin_fmaf(qv[r].x, kv[p].x, L[r][p][0]);
         L[r][p][1] = __builtin_fmaf(qv[r].y, kv[p].y, L[r][p][1]);
         L[r][p][2] = __builtin_fmaf(qv[r].z, kv[p].z, L[r][p][2]);
@@ -388,16 +391,23 @@ __device__ __forceinline__ void attn_quad(const float* q0, const float* k0, int 
   }
 }
 
+template <int ROWS>
 __global__ void __launch_bounds__(kThreads) attention_rows64(const float* __restrict__ q, const float* __restrict__ kc,
                                                              const float* __restrict__ vc, float* __restrict__ out,
                                                              int nh, int nkv, int cap, int base, int T, int tq,
                                                              float scale) {
-  extern __shared__ float sc[];  // [position][kAttnRows]
-  __shared__ __attribute__((aligned(16))) float qs[kAttnRows * kAttnStride];
+  constexpr int RG = ROWS / 4;            // row groups of the scores phase
+  constexpr int PG = kThreads / RG;       // position groups
+  constexpr int P = kAttnTile / PG;       // positions per thread
+  constexpr int PH = kThreads / ROWS;     // softmax phases per row
+  constexpr int RP = ROWS / 16;           // P.V rows per thread
+  static_assert(P >= 1 && RP >= 1 && P * PG == kAttnTile, "attention_rows64: ROWS must be 16 or 32");
+  extern __shared__ float sc[];  // [position][ROWS]
+  __shared__ __attribute__((aligned(16))) float qs[ROWS * kAttnStride];
   __shared__ __attribute__((aligned(16))) float tile[2][kAttnTile * kAttnStride];
-  __shared__ double red_d[kAttnPhases][kAttnRows];
-  __shared__ float red_f[kAttnPhases][kAttnRows];
-  __shared__ float inv_s[kAttnRows];
+  __shared__ double red_d[PH][ROWS];
+  __shared__ float red_f[PH][ROWS];
+  __shared__ float inv_s[ROWS];
   const int G = nh / nkv;
   const int kvh = blockIdx.y;
   const int t0 = (static_cast<int>(gridDim.x) - 1 - static_cast<int>(blockIdx.x)) * tq;  // longest rows first
@@ -409,7 +419,7 @@ __global__ void __launch_bounds__(kThreads) attention_rows64(const float* __rest
   const float* vh = vc + static_cast<std::size_t>(kvh) * cap * 64;
   const int tid = threadIdx.x;
 
-  for (int f = tid; f < kAttnRows * 16; f += kThreads) {
+  for (int f = tid; f < ROWS * 16; f += kThreads) {
     const int row = f >> 4, e4 = f & 15;
     float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     if (row < nrows) {
@@ -429,30 +439,30 @@ __global__ void __launch_bounds__(kThreads) attention_rows64(const float* __rest
   if (ntile > 1) attn_load_tile(kh, kAttnTile, npos_max, st);
   __syncthreads();
   {
-    const int rg = tid & 7, pg = tid >> 3;
+    const int rg = tid % RG, pg = tid / RG;
     const float* q0 = qs + rg * kAttnStride;
     for (int k = 0; k < ntile; ++k) {
       const float* k0 = tile[k & 1] + pg * kAttnStride;
-      float A[4][2][4], B[4][2][4], C[4][2][4];
-      attn_quad(q0, k0, 0, A);
-      attn_quad(q0, k0, 8, B);
+      float A[4][P][4], B[4][P][4], C[4][P][4];
+      attn_quad<RG, P, PG>(q0, k0, 0, A);
+      attn_quad<RG, P, PG>(q0, k0, 8, B);
 #pragma unroll
       for (int r = 0; r < 4; ++r)
 #pragma unroll
-        for (int p = 0; p < 2; ++p)
+        for (int p = 0; p < P; ++p)
 #pragma unroll
           for (int u = 0; u < 4; ++u) A[r][p][u] = A[r][p][u] + B[r][p][u];  // lanes j + (j + 8), j < 4
-      attn_quad(q0, k0, 4, B);
-      attn_quad(q0, k0, 12, C);
+      attn_quad<RG, P, PG>(q0, k0, 4, B);
+      attn_quad<RG, P, PG>(q0, k0, 12, C);
 #pragma unroll
       for (int r = 0; r < 4; ++r)
 #pragma unroll
-        for (int p = 0; p < 2; ++p) {
+        for (int p = 0; p < P; ++p) {
           float s4[4];
 #pragma unroll
           for (int u = 0; u < 4; ++u) s4[u] = A[r][p][u] + (B[r][p][u] + C[r][p][u]);  // + lanes (j+4) + (j+12)
           const float head = (s4[0] + s4[2]) + (s4[1] + s4[3]);
-          sc[(k * kAttnTile + pg + 32 * p) * kAttnRows + rg + 8 * r] = (head + 0.0f) * scale;
+          sc[(k * kAttnTile + pg + PG * p) * ROWS + rg + RG * r] = (head + 0.0f) * scale;
         }
       if (k + 1 < ntile) {
         attn_store_tile(tile[(k + 1) & 1], st);
@@ -465,19 +475,19 @@ __global__ void __launch_bounds__(kThreads) attention_rows64(const float* __rest
 
   // ---- softmax
   {
-    const int row = tid & (kAttnRows - 1), ph = tid / kAttnRows;
+    const int row = tid % ROWS, ph = tid / ROWS;
     const int np = row < nrows ? base + t0 + row / G + 1 : 0;
     float m = -__builtin_inff();
-    for (int s = ph; s < np; s += kAttnPhases) m = fmaxf(m, sc[s * kAttnRows + row]);
+    for (int s = ph; s < np; s += PH) m = fmaxf(m, sc[s * ROWS + row]);
     red_f[ph][row] = m;
     __syncthreads();
     float mx = red_f[0][row];
 #pragma unroll
-    for (int i = 1; i < kAttnPhases; ++i) mx = fmaxf(mx, red_f[i][row]);
+    for (int i = 1; i < PH; ++i) mx = fmaxf(mx, red_f[i][row]);
     double part = 0.0;
-    for (int s = ph; s < np; s += kAttnPhases) {
-      const float e = exact::expf(sc[s * kAttnRows + row] - mx);
-      sc[s * kAttnRows + row] = e;
+    for (int s = ph; s < np; s += PH) {
+      const float e = exact::expf(sc[s * ROWS + row] - mx);
+      sc[s * ROWS + row] = e;
       part += static_cast<double>(e);
     }
     red_d[ph][row] = part;
@@ -485,12 +495,12 @@ __global__ void __launch_bounds__(kThreads) attention_rows64(const float* __rest
     if (ph == 0 && row < nrows) {
       double sum = red_d[0][row];
 #pragma unroll
-      for (int i = 1; i < kAttnPhases; ++i) sum = sum + red_d[i][row];
+      for (int i = 1; i < PH; ++i) sum = sum + red_d[i][row];
       const double slack = sum_slack(np) * sum;
       float inv = recip_float(sum);
       if (recip_float(sum - slack) != recip_float(sum + slack)) {
         double seq = 0.0;
-        for (int s = 0; s < np; ++s) seq += static_cast<double>(sc[s * kAttnRows + row]);
+        for (int s = 0; s < np; ++s) seq += static_cast<double>(sc[s * ROWS + row]);
         inv = recip_float(seq);
       }
       inv_s[row] = inv;
@@ -498,7 +508,7 @@ __global__ void __launch_bounds__(kThreads) attention_rows64(const float* __rest
     __syncthreads();
     if (np > 0) {
       const float inv = inv_s[row];
-      for (int s = ph; s < np; s += kAttnPhases) sc[s * kAttnRows + row] = sc[s * kAttnRows + row] * inv;
+      for (int s = ph; s < np; s += PH) sc[s * ROWS + row] = sc[s * ROWS + row] * inv;
     }
   }
 
@@ -507,24 +517,33 @@ __global__ void __launch_bounds__(kThreads) attention_rows64(const float* __rest
   if (ntile > 1) attn_load_tile(vh, kAttnTile, npos_max, st);
   __syncthreads();
   const int rp = tid >> 4, dq = tid & 15;
-  const int ra = 2 * rp;
-  const int np_a = ra < nrows ? base + t0 + ra / G + 1 : npos_max;
-  const int np_b = ra + 1 < nrows ? base + t0 + (ra + 1) / G + 1 : npos_max;
-  float acc[2][4] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
+  const int ra = RP * rp;
+  int np_r[RP];
+#pragma unroll
+  for (int i = 0; i < RP; ++i) np_r[i] = ra + i < nrows ? base + t0 + (ra + i) / G + 1 : npos_max;
+  float acc[RP][4];
+#pragma unroll
+  for (int i = 0; i < RP; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = 0.0f;
   const auto step = [&](const float* vt, int s, int u, bool checked) {
-    const float2 p = *reinterpret_cast<const float2*>(sc + s * kAttnRows + ra);
-    const float4 v = *reinterpret_cast<const float4*>(vt + u * kAttnStride + 4 * dq);
-    if (!checked || s < np_a) {
-      acc[0][0] = __builtin_fmaf(p.x, v.x, acc[0][0]);
-      acc[0][1] = __builtin_fmaf(p.x, v.y, acc[0][1]);
-      acc[0][2] = __builtin_fmaf(p.x, v.z, acc[0][2]);
-      acc[0][3] = __builtin_fmaf(p.x, v.w, acc[0][3]);
+    float p[RP];
+    if constexpr (RP == 2) {
+      const float2 p2 = *reinterpret_cast<const float2*>(sc + s * ROWS + ra);
+      p[0] = p2.x;
+      p[1] = p2.y;
+    } else {
+      p[0] = sc[s * ROWS + ra];
     }
-    if (!checked || s < np_b) {
-      acc[1][0] = __builtin_fmaf(p.y, v.x, acc[1][0]);
-      acc[1][1] = __builtin_fmaf(p.y, v.y, acc[1][1]);
-      acc[1][2] = __builtin_fmaf(p.y, v.z, acc[1][2]);
-      acc[1][3] = __builtin_fmaf(p.y, v.w, acc[1][3]);
+    const float4 v = *reinterpret_cast<const float4*>(vt + u * kAttnStride + 4 * dq);
+#pragma unroll
+    for (int i = 0; i < RP; ++i) {
+      if (!checked || s < np_r[i]) {
+        acc[i][0] = __builtin_fmaf(p[i], v.x, acc[i][0]);
+        acc[i][1] = __builtin_fmaf(p[i], v.y, acc[i][1]);
+        acc[i][2] = __builtin_fmaf(p[i], v.z, acc[i][2]);
+        acc[i][3] = __builtin_fmaf(p[i], v.w, acc[i][3]);
+      }
     }
   };
   for (int k = 0; k < ntile; ++k) {
@@ -546,7 +565,7 @@ __global__ void __launch_bounds__(kThreads) attention_rows64(const float* __rest
     __syncthreads();
   }
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
+  for (int i = 0; i < RP; ++i) {
     const int row = ra + i;
     if (row < nrows) {
       const int tt = row / G, g = row - tt * G;
@@ -865,25 +884,37 @@ std::size_t attention_dyn_lds(std::size_t npos, std::size_t hd) {
   return hd % 16 == 0 && hd <= 256 ? (npos + 2 * kVTile * hd) * sizeof(float) : npos * sizeof(float);
 }
 
-// Scores LDS of attention_rows64 when its longest row attends to npos
-// positions (whole 64-position tiles).
-std::size_t attention_rows_lds(std::size_t npos) {
-  return ceil_div(npos, static_cast<std::size_t>(kAttnTile)) * kAttnTile * kAttnRows * sizeof(float);
+// Rows per workgroup of the prefill attention: 16 when the GQA group fits
+// (measured faster on MI355X than 32: twice the workgroups, half the LDS),
+// else 32.
+int attention_rows(int nh, int nkv) { return nh / nkv <= 16 ? 16 : 32; }
+
+// Scores LDS of attention_rows64 with `rows` rows when its longest row
+// attends to npos positions (whole 64-position tiles).
+std::size_t attention_rows_lds(std::size_t npos, int rows) {
+  return ceil_div(npos, static_cast<std::size_t>(kAttnTile)) * kAttnTile * rows * sizeof(float);
 }
 
 bool attention_rows_fits(int nh, int nkv, int hd, std::size_t npos) {
-  return hd == 64 && nkv >= 1 && nh % nkv == 0 && nh / nkv <= kAttnRows &&
-         attention_rows_lds(npos) + kAttnStaticLds <= max_lds_per_block();
+  if (hd != 64 || nkv < 1 || nh % nkv != 0 || nh / nkv > 32) return false;
+  const int rows = attention_rows(nh, nkv);
+  const std::size_t stat = rows == 16 ? attn_static_lds<16>() : attn_static_lds<32>();
+  return attention_rows_lds(npos, rows) + stat <= max_lds_per_block();
 }
 
 void launch_attention(const float* q, const float* kc, const float* vc, float* out, int nh, int nkv, int hd, int cap,
                       int base, int T, float scale, hipStream_t s) {
   const std::size_t npos = static_cast<std::size_t>(base) + T;
   if (attention_rows_fits(nh, nkv, hd, npos)) {
-    const int tq = kAttnRows / (nh / nkv);
+    const int rows = attention_rows(nh, nkv);
+    const int tq = rows / (nh / nkv);
     const dim3 grid(static_cast<unsigned>(ceil_div(T, tq)), static_cast<unsigned>(nkv));
-    attention_rows64<<<grid, kThreads, attention_rows_lds(npos), s>>>(q, kc, vc, out, nh, nkv, cap, base, T, tq,
-                                                                      scale);
+    const std::size_t lds = attention_rows_lds(npos, rows);
+    if (rows == 16) {
+      attention_rows64<16><<<grid, kThreads, lds, s>>>(q, kc, vc, out, nh, nkv, cap, base, T, tq, scale);
+    } else {
+      attention_rows64<32><<<grid, kThreads, lds, s>>>(q, kc, vc, out, nh, nkv, cap, base, T, tq, scale);
+    }
     return;
   }
   const dim3 grid(static_cast<unsigned>(nh), static_cast<unsigned>(T));
