@@ -230,6 +230,8 @@ __global__ void __launch_bounds__(kGemmThreads) qgemm_mfma(const GemmProblem* __
   }
 
   // acc[i][j][q]: token m0 + wm0 + 16i + 4*(lane/16) + q, output n0 + wn0 + 16j + lane%16.
+  // With accumulate, a column's 16 old values are loaded together (clamped
+  // rows, no branch) before any is used, so their latencies overlap.
   GMEM float* y = (GMEM float*)p.y;
   const GMEM float* bias = (const GMEM float*)p.bias;
 #pragma unroll
@@ -237,15 +239,24 @@ __global__ void __launch_bounds__(kGemmThreads) qgemm_mfma(const GemmProblem* __
     const int n = n0 + wn0 + 16 * j + (lane & 15);
     if (n >= N) continue;
     const float add = bias != nullptr ? bias[n] : 0.0f;
+    float old[4][4];
+    if (p.accumulate) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int m = min(m0 + wm0 + 16 * i + 4 * (lane >> 4) + q, M - 1);
+          old[i][q] = y[static_cast<std::size_t>(m) * N + n];
+        }
+    }
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int m = m0 + wm0 + 16 * i + 4 * (lane >> 4) + q;
         if (m < M) {
-          GMEM float* dst = y + static_cast<std::size_t>(m) * N + n;
           const float v = acc[i][j][q] + add;
-          *dst = p.accumulate ? *dst + v : v;
+          y[static_cast<std::size_t>(m) * N + n] = p.accumulate ? old[i][q] + v : v;
         }
       }
   }
