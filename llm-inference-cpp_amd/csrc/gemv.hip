@@ -907,6 +907,8 @@ void launch_rows(const DeviceMatrix& m, const float* x, std::size_t rows, const 
                                            static_cast<int>(rows), acc);
     return;
   }
+  // Here ntiles * ceil(rows / 64) < 1024, so rows < 65536 and every split
+  // launch's grid y (ceil(rows / R), R >= 2) stays below 32768.
   const auto waves = [&](std::size_t r, std::size_t w) { return m.ntiles * ceil_div(rows, r) * w; };
   if (waves(4, 4) >= 6144) launch_split<TYPE, 4, 4>(m, x, rows, bias, y, acc, s);
   else if (waves(4, 8) >= 4096) launch_split<TYPE, 4, 8>(m, x, rows, bias, y, acc, s);
