@@ -276,20 +276,21 @@ def test_prefill_attention_matches_reference(hidden, heads, kv):
 
 
 def test_prefill_attention_past_the_lds_scores():
-    """A prompt longer than the workgroup-per-tile kernel's LDS holds (about
-    900 positions) takes the per-(head, token) kernel; logits still equal the
-    reference's."""
+    """The workgroup-per-tile kernel holds a 16-row tile's scores in LDS up to
+    about 1850 positions: a first chunk of 1200 positions takes it, a second
+    one reaching 2000 positions the per-(head, token) kernel; logits still
+    equal the reference's."""
     cpu = O.reference() or O.oracle()
     cfg = dict(arch=0, vocab_size=64, hidden_size=128, intermediate_size=256, num_layers=1, num_heads=2,
-               num_kv_heads=1, max_position_embeddings=1100, rms_norm_eps=1e-5, rope_theta=10000.0,
+               num_kv_heads=1, max_position_embeddings=2000, rms_norm_eps=1e-5, rope_theta=10000.0,
                tie_word_embeddings=1, qkv_bias=0)
     tensors = synth.make_tensors(cfg, 5, "bench")
     gm = H.Model(cfg, tensors, H.Q4_0)
     cm = O.CpuModel(cpu, cfg, tensors, O.Q4_0)
-    ids = synth.uniform_ids(6, 1100, cfg["vocab_size"])
-    cache = gm.new_cache(1100)
-    assert cm.new_cache(1100)
-    for a, b in ((0, 700), (700, 1100)):
+    ids = synth.uniform_ids(6, 2000, cfg["vocab_size"])
+    cache = gm.new_cache(2000)
+    assert cm.new_cache(2000)
+    for a, b in ((0, 1200), (1200, 2000)):
         got = gm.forward_cached(cache, ids[a:b], all_positions=True)
         want = cm.forward_cached(ids[a:b], all_positions=True)
         assert np.array_equal(bits(got), bits(want)), (a, b)
