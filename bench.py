@@ -199,6 +199,7 @@ def grouped_mlp_targets(steps=50):
 QWEN_LAYER = [("q_proj", 896, 896), ("k_proj", 128, 896), ("v_proj", 128, 896), ("o_proj", 896, 896),
               ("gate_proj", 4864, 896), ("up_proj", 4864, 896), ("down_proj", 896, 4864)]
 MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense bf16
+FP32_PEAK_TFLOPS = 157.3  # MI355X fp32 vector (packed); this build issues non-packed FMAs only
 
 
 def gguf_upload(reps=3):
@@ -291,6 +292,18 @@ DECODE_RUNS = [  # (key, golden fixture, model config, weight type): BASELINE.js
 ]
 
 
+def prefill_flops(cfg, T):
+    """Floating-point operations of the exact prefill of T tokens: every
+    projection at T rows, the lm_head on the last row, and causal attention
+    (scores and P.V, 2 flops per multiply-add each)."""
+    H, L, nh = cfg["hidden_size"], cfg["num_layers"], cfg["num_heads"]
+    hd = H // nh
+    kv = cfg["num_kv_heads"] * hd
+    per_layer = H * H + 2 * kv * H + H * H + 3 * cfg["intermediate_size"] * H
+    attn = L * nh * hd * 4 * T * (T + 1) // 2
+    return 2 * T * L * per_layer + 2 * cfg["vocab_size"] * H + attn
+
+
 def decode_runs():
     """Full-model greedy decode on the synthetic models: prefill the prompt,
     then the configured number of greedy steps; ids are checked against the
@@ -309,9 +322,11 @@ def decode_runs():
         mean_ctx = rec["n_prompt"] + rec["n_steps"] / 2.0
         bytes_per_token = wb + n_kv * mean_ctx
         tok_s = rec["n_steps"] / (dec_ms * 1e-3)
+        pre_tf = prefill_flops(cfg, rec["n_prompt"]) / (pre_ms * 1e-3) / 1e12
         roof = HBM_PEAK_GBS * 1e9 / bytes_per_token
         res[key] = dict(prompt=rec["n_prompt"], steps=rec["n_steps"], weights=H.TYPE_NAMES[qt],
                         prefill_ms=round(pre_ms, 2), prefill_tok_s=round(rec["n_prompt"] / (pre_ms * 1e-3), 1),
+                        prefill_tflops=round(pre_tf, 2), prefill_frac_of_fp32_peak=round(pre_tf / FP32_PEAK_TFLOPS, 4),
                         decode_ms=round(dec_ms, 2), decode_tok_s=round(tok_s, 1),
                         bytes_per_token=int(bytes_per_token), roofline_tok_s=round(roof, 1),
                         frac_of_roofline=round(tok_s / roof, 4),
