@@ -189,6 +189,11 @@ int launch_dequantize_rows(const DeviceMatrix& m, const std::int32_t* ids, std::
 // done in the GEMV's epilogue with the same two roundings.
 int launch_matmul(const DeviceMatrix& m, const float* x, std::size_t rows, const float* bias, float* y, hipStream_t s,
                   bool accumulate = false);
+// Products of one weight type and input size sharing x and rows (the
+// prefill's q/k/v, gate/up): one split-block launch over all their tiles
+// when each would take the split-block product, else one launch each.
+int launch_matmul_shared(const DeviceMatrix* const* ms, const float* const* biases, float* const* ys, int count,
+                         const float* x, std::size_t rows, hipStream_t s);
 // Frees the sampling workspace (llmi_hip_shutdown; the stream is idle).
 void release_sampling_workspace();
 

@@ -723,16 +723,14 @@ __global__ void __launch_bounds__(256) qgemm_exact(const uint4* __restrict__ cod
 // Small row chunks (2 or 4 rows) measured fastest: the chunk's activations
 // are scalar loads per block and row, and more workgroups hide them.
 template <int TYPE, int kSplitRows, int kSplitWaves>
-__global__ void __launch_bounds__(kSplitWaves * 64) qgemm_split(const uint4* __restrict__ codes,
-                                                                const float* __restrict__ scales,
-                                                                const float* __restrict__ x,
-                                                                const float* __restrict__ bias, float* __restrict__ y,
-                                                                int in, int nblk, int out, int rows, int accumulate) {
+__device__ __forceinline__ void split_tile(const uint4* __restrict__ codes, const float* __restrict__ scales,
+                                           const float* __restrict__ x, const float* __restrict__ bias,
+                                           float* __restrict__ y, int in, int nblk, int out, int rows, int accumulate,
+                                           std::size_t tile, int chunk) {
   constexpr int RW = (kSplitRows + kSplitWaves - 1) / kSplitWaves;  // chains per lane
   __shared__ float part[2][kSplitRows][kSplitWaves][kTileRows];
   __shared__ float scl[2][kSplitWaves][kTileRows];
-  const std::size_t tile = blockIdx.x;
-  const int r0 = blockIdx.y * kSplitRows;
+  const int r0 = chunk * kSplitRows;
   const int nr = min(kSplitRows, rows - r0);
   const int lane = threadIdx.x & (kTileRows - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -799,6 +797,40 @@ __global__ void __launch_bounds__(kSplitWaves * 64) qgemm_split(const uint4* __r
       }
     }
   }
+}
+
+template <int TYPE, int R, int W>
+__global__ void __launch_bounds__(W * 64) qgemm_split(const uint4* __restrict__ codes, const float* __restrict__ scales,
+                                                      const float* __restrict__ x, const float* __restrict__ bias,
+                                                      float* __restrict__ y, int in, int nblk, int out, int rows,
+                                                      int accumulate) {
+  split_tile<TYPE, R, W>(codes, scales, x, bias, y, in, nblk, out, rows, accumulate, blockIdx.x, blockIdx.y);
+}
+
+// Up to kMaxShared products of one weight type and input size that share x
+// and rows (the prefill's q/k/v, gate/up) in one launch: workgroup column
+// blockIdx.x is tile blockIdx.x - tile_end[p - 1] of the product p whose
+// tile range holds it.
+constexpr int kMaxShared = 3;
+struct SplitGroup {
+  const uint4* codes[kMaxShared];
+  const float* scales[kMaxShared];
+  const float* bias[kMaxShared];
+  float* y[kMaxShared];
+  int out[kMaxShared];
+  int tile_end[kMaxShared];
+  int count;
+};
+
+template <int TYPE, int R, int W>
+__global__ void __launch_bounds__(W * 64) qgemm_split_group(SplitGroup g, const float* __restrict__ x, int in,
+                                                            int nblk, int rows) {
+  const int t = static_cast<int>(blockIdx.x);
+  int p = 0;
+  while (p + 1 < g.count && t >= g.tile_end[p]) ++p;
+  const int t0 = p == 0 ? 0 : g.tile_end[p - 1];
+  split_tile<TYPE, R, W>(g.codes[p], g.scales[p], x, g.bias[p], g.y[p], in, nblk, g.out[p], rows, 0,
+                         static_cast<std::size_t>(t - t0), blockIdx.y);
 }
 
 // ------------------------------------------------------------ planning
@@ -915,6 +947,25 @@ void launch_rows(const DeviceMatrix& m, const float* x, std::size_t rows, const 
   else launch_split<TYPE, 2, 8>(m, x, rows, bias, y, acc, s);
 }
 
+template <int TYPE, int R, int W>
+void launch_split_group(const SplitGroup& g, std::size_t tiles, const float* x, std::size_t in, std::size_t nblk,
+                        std::size_t rows, hipStream_t s) {
+  const dim3 grid(static_cast<unsigned>(tiles), static_cast<unsigned>(ceil_div(rows, R)));
+  qgemm_split_group<TYPE, R, W><<<grid, W * 64, 0, s>>>(g, x, static_cast<int>(in), static_cast<int>(nblk),
+                                                        static_cast<int>(rows));
+}
+
+// The grouped split launch of launch_matmul_shared: the row chunk and
+// wavefront count by the launch's total size, as for one product.
+template <int TYPE>
+void launch_group_rows(const SplitGroup& g, std::size_t tiles, const float* x, std::size_t in, std::size_t nblk,
+                       std::size_t rows, hipStream_t s) {
+  const auto waves = [&](std::size_t r, std::size_t w) { return tiles * ceil_div(rows, r) * w; };
+  if (waves(4, 4) >= 6144) launch_split_group<TYPE, 4, 4>(g, tiles, x, in, nblk, rows, s);
+  else if (waves(4, 8) >= 4096) launch_split_group<TYPE, 4, 8>(g, tiles, x, in, nblk, rows, s);
+  else launch_split_group<TYPE, 2, 8>(g, tiles, x, in, nblk, rows, s);
+}
+
 template <int TYPE>
 void launch_typed(const DeviceMatrix& m, const float* x, std::size_t rows, const float* bias, float* y, int acc,
                   hipStream_t s) {
@@ -954,6 +1005,45 @@ int launch_matmul(const DeviceMatrix& m, const float* x, std::size_t rows, const
   const int acc = accumulate ? 1 : 0;
   if (m.type == LLMI_TYPE_Q8_0) launch_typed<LLMI_TYPE_Q8_0>(m, x, rows, bias, y, acc, s);
   else launch_typed<LLMI_TYPE_Q4_0>(m, x, rows, bias, y, acc, s);
+  LLMI_TRY_HIP(hipGetLastError());
+  return LLMI_OK;
+}
+
+int launch_matmul_shared(const DeviceMatrix* const* ms, const float* const* biases, float* const* ys, int count,
+                         const float* x, std::size_t rows, hipStream_t s) {
+  LLMI_REQUIRE(count >= 1 && count <= kMaxShared, "matmul_shared: 1..3 products");
+  std::size_t tiles = 0;
+  bool grouped = count > 1 && rows > 8;
+  for (int i = 0; i < count && grouped; ++i) {
+    const DeviceMatrix& m = *ms[i];
+    // One launch only where each product alone would take qgemm_split.
+    grouped = m.type != LLMI_TYPE_F32 && m.type == ms[0]->type && m.in == ms[0]->in && m.out > 0 &&
+              m.ntiles * ceil_div(rows, kExactRows) < 1024;
+    tiles += m.ntiles;
+  }
+  if (!grouped) {
+    for (int i = 0; i < count; ++i)
+      if (int rc = launch_matmul(*ms[i], x, rows, biases[i], ys[i], s)) return rc;
+    return LLMI_OK;
+  }
+  if (int rc = check_shape(*ms[0], rows)) return rc;
+  LLMI_REQUIRE(x != nullptr, "matmul_shared: null x");
+  SplitGroup g{};
+  int end = 0;
+  for (int i = 0; i < count; ++i) {
+    LLMI_REQUIRE(ys[i] != nullptr, "matmul_shared: null y");
+    g.codes[i] = reinterpret_cast<const uint4*>(ms[i]->codes);
+    g.scales[i] = ms[i]->scales;
+    g.bias[i] = biases[i];
+    g.y[i] = ys[i];
+    g.out[i] = static_cast<int>(ms[i]->out);
+    end += static_cast<int>(ms[i]->ntiles);
+    g.tile_end[i] = end;
+  }
+  g.count = count;
+  const DeviceMatrix& m0 = *ms[0];
+  if (m0.type == LLMI_TYPE_Q8_0) launch_group_rows<LLMI_TYPE_Q8_0>(g, tiles, x, m0.in, m0.nblk, rows, s);
+  else launch_group_rows<LLMI_TYPE_Q4_0>(g, tiles, x, m0.in, m0.nblk, rows, s);
   LLMI_TRY_HIP(hipGetLastError());
   return LLMI_OK;
 }

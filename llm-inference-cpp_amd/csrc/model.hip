@@ -1450,17 +1450,31 @@ int forward_rows(llmi_hip_model* m, llmi_hip_cache* cache, std::size_t T, std::s
     float* kc = cache->k + li * per_layer;
     float* vc = cache->v + li * per_layer;
     rmsnorm_rows<<<tt, kThreads, 0, s>>>(w.x, l.attn_norm, w.h, static_cast<int>(m->H), eps);
-    if (int rc = linear(l.wq, w.h, l.bq, w.q, false)) return rc;
-    if (int rc = linear(l.wk, w.h, l.bk, w.k, false)) return rc;
-    if (int rc = linear(l.wv, w.h, l.bv, w.v, false)) return rc;
+    if (mfma_all) {
+      if (int rc = linear(l.wq, w.h, l.bq, w.q, false)) return rc;
+      if (int rc = linear(l.wk, w.h, l.bk, w.k, false)) return rc;
+      if (int rc = linear(l.wv, w.h, l.bv, w.v, false)) return rc;
+    } else {
+      const DeviceMatrix* qkv[3] = {&l.wq, &l.wk, &l.wv};
+      const float* qkv_bias[3] = {l.bq, l.bk, l.bv};
+      float* qkv_out[3] = {w.q, w.k, w.v};
+      if (int rc = launch_matmul_shared(qkv, qkv_bias, qkv_out, 3, w.h, T, s)) return rc;
+    }
     rope_and_cache<<<tt, kThreads, 0, s>>>(w.q, w.k, w.v, kc, vc, m->cos_t, m->sin_t, nh, nkv, hd,
                                            static_cast<int>(cache->cap), static_cast<int>(base));
     launch_attention(w.q, kc, vc, w.att, nh, nkv, hd, static_cast<int>(cache->cap), static_cast<int>(base),
                      static_cast<int>(T), scale, s);
     if (int rc = linear(l.wo, w.att, nullptr, w.x, true)) return rc;
     rmsnorm_rows<<<tt, kThreads, 0, s>>>(w.x, l.mlp_norm, w.h, static_cast<int>(m->H), eps);
-    if (int rc = linear(l.gate, w.h, nullptr, w.g, false)) return rc;
-    if (int rc = linear(l.up, w.h, nullptr, w.u, false)) return rc;
+    if (mfma_all) {
+      if (int rc = linear(l.gate, w.h, nullptr, w.g, false)) return rc;
+      if (int rc = linear(l.up, w.h, nullptr, w.u, false)) return rc;
+    } else {
+      const DeviceMatrix* gu[2] = {&l.gate, &l.up};
+      const float* gu_bias[2] = {nullptr, nullptr};
+      float* gu_out[2] = {w.g, w.u};
+      if (int rc = launch_matmul_shared(gu, gu_bias, gu_out, 2, w.h, T, s)) return rc;
+    }
     silu_mul<<<blocks_for(T * m->F), kThreads, 0, s>>>(w.g, w.u, T * m->F);
     if (int rc = linear(l.down, w.g, nullptr, w.x, true)) return rc;
     if (trace != nullptr)
