@@ -194,6 +194,12 @@ int launch_matmul(const DeviceMatrix& m, const float* x, std::size_t rows, const
 // when each would take the split-block product, else one launch each.
 int launch_matmul_shared(const DeviceMatrix* const* ms, const float* const* biases, float* const* ys, int count,
                          const float* x, std::size_t rows, hipStream_t s);
+// The prefill's MLP gate and up projections fused with silu(gate) * up into
+// y, when both would take the split-block product (rows > 8, few tiles, one
+// quantized type and shape); *fused reports whether it ran (else nothing was
+// launched and the caller takes the unfused path).
+int launch_gate_up_silu(const DeviceMatrix& gate, const DeviceMatrix& up, const float* x, std::size_t rows,
+                        float* y, hipStream_t s, bool* fused);
 // Frees the sampling workspace (llmi_hip_shutdown; the stream is idle).
 void release_sampling_workspace();
 

@@ -39,6 +39,7 @@
 //
 // fp32 weights take kernels::matmul instead (f32.hip).
 #include <algorithm>
+#include <type_traits>
 #include <vector>
 
 #include "common.hpp"
@@ -807,6 +808,119 @@ __global__ void __launch_bounds__(W * 64) qgemm_split(const uint4* __restrict__ 
   split_tile<TYPE, R, W>(codes, scales, x, bias, y, in, nblk, out, rows, accumulate, blockIdx.x, blockIdx.y);
 }
 
+// The gate and up projections of an MLP in one split-block tile: each round
+// a wavefront decodes block b of the gate matrix and forms its block sums for
+// every input row, then the same for the up matrix, the chains run side by
+// side, and the epilogue writes
+// silu(gate) * up as the reference's MLP does after its two matmuls
+// (kernels.cpp:148, transformer.cpp:288-290): v = gate + 0.0f (the matmul's
+// absent bias), v / (1 + expf(-v)) * (up + 0.0f), with the exact expf.
+template <int TYPE, int kSplitRows, int kSplitWaves>
+__global__ void __launch_bounds__(kSplitWaves * 64) qgemm_split_gate_up(
+    const uint4* __restrict__ codes_g, const float* __restrict__ scales_g, const uint4* __restrict__ codes_u,
+    const float* __restrict__ scales_u, const float* __restrict__ x, float* __restrict__ y, int in, int nblk, int out,
+    int rows) {
+  constexpr int RW = (kSplitRows + kSplitWaves - 1) / kSplitWaves;  // chains per lane and product
+  __shared__ float part[2][2][kSplitRows][kSplitWaves][kTileRows];  // [buffer][gate, up]
+  __shared__ float scl[2][2][kSplitWaves][kTileRows];
+  const std::size_t tile = blockIdx.x;
+  const int r0 = blockIdx.y * kSplitRows;
+  const int nr = min(kSplitRows, rows - r0);
+  const int lane = threadIdx.x & (kTileRows - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const GMEM uint4* cgg = gmem(codes_g);
+  const GMEM uint4* cgu = gmem(codes_u);
+  const GMEM float* sgg = gmem(scales_g);
+  const GMEM float* sgu = gmem(scales_u);
+  const GMEM float* xg = gmem(x) + static_cast<std::size_t>(r0) * in;
+  const int nfull = in / kBlock;
+  const std::size_t base = tile * nblk;
+  float acc_g[RW], acc_u[RW];
+#pragma unroll
+  for (int i = 0; i < RW; ++i) acc_g[i] = acc_u[i] = 0.0f;
+  const int nround = (nblk + kSplitWaves - 1) / kSplitWaves;
+  Block<TYPE> cur_g{}, cur_u{};
+  float sc_g = 0.0f, sc_u = 0.0f;
+  if (wave < nblk) {
+    cur_g = load_block<TYPE, false>(cgg, base + wave, lane);
+    cur_u = load_block<TYPE, false>(cgu, base + wave, lane);
+    sc_g = sgg[(base + wave) * kTileRows + lane];
+    sc_u = sgu[(base + wave) * kTileRows + lane];
+  }
+  for (int rd = 0; rd < nround; ++rd) {
+    const int buf = rd & 1;
+    const int b = rd * kSplitWaves + wave;
+    Block<TYPE> nxt_g{}, nxt_u{};
+    float nsc_g = 0.0f, nsc_u = 0.0f;
+    if (b + kSplitWaves < nblk) {
+      nxt_g = load_block<TYPE, false>(cgg, base + b + kSplitWaves, lane);
+      nxt_u = load_block<TYPE, false>(cgu, base + b + kSplitWaves, lane);
+      nsc_g = sgg[(base + b + kSplitWaves) * kTileRows + lane];
+      nsc_u = sgu[(base + b + kSplitWaves) * kTileRows + lane];
+    }
+    if (b < nfull) {
+      // One product's block at a time: a single set of 32 decoded codes
+      // stays live, which keeps the kernel at the split kernel's occupancy.
+      {
+        float c[kBlock];
+        block_codes<TYPE>(cur_g, c);
+#pragma unroll
+        for (int r = 0; r < kSplitRows; ++r)
+          if (r < nr) part[buf][0][r][wave][lane] = codes_dot(c, xg + static_cast<std::size_t>(r) * in + b * kBlock);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      {
+        float c[kBlock];
+        block_codes<TYPE>(cur_u, c);
+#pragma unroll
+        for (int r = 0; r < kSplitRows; ++r)
+          if (r < nr) part[buf][1][r][wave][lane] = codes_dot(c, xg + static_cast<std::size_t>(r) * in + b * kBlock);
+      }
+    } else if (b < nblk) {
+      for (int r = 0; r < nr; ++r) {
+        const GMEM float* xr = xg + static_cast<std::size_t>(r) * in + b * kBlock;
+        part[buf][0][r][wave][lane] = tail_block_dot<TYPE>(cur_g, xr, in - b * kBlock);
+        part[buf][1][r][wave][lane] = tail_block_dot<TYPE>(cur_u, xr, in - b * kBlock);
+      }
+    }
+    if (b < nblk) {
+      scl[buf][0][wave][lane] = sc_g;
+      scl[buf][1][wave][lane] = sc_u;
+    }
+    __syncthreads();
+    const int nb = min(kSplitWaves, nblk - rd * kSplitWaves);
+#pragma unroll
+    for (int i = 0; i < RW; ++i) {
+      const int r = wave + kSplitWaves * i;
+      if (r < kSplitRows && r < nr) {
+        float ag = acc_g[i], au = acc_u[i];
+        for (int j = 0; j < nb; ++j) {
+          ag = __builtin_fmaf(part[buf][0][r][j][lane], scl[buf][0][j][lane], ag);
+          au = __builtin_fmaf(part[buf][1][r][j][lane], scl[buf][1][j][lane], au);
+        }
+        acc_g[i] = ag;
+        acc_u[i] = au;
+      }
+    }
+    cur_g = nxt_g;
+    cur_u = nxt_u;
+    sc_g = nsc_g;
+    sc_u = nsc_u;
+  }
+  const std::size_t o = tile * kTileRows + lane;
+  if (o < static_cast<std::size_t>(out)) {
+#pragma unroll
+    for (int i = 0; i < RW; ++i) {
+      const int r = wave + kSplitWaves * i;
+      if (r < kSplitRows && r < nr) {
+        const float v = acc_g[i] + 0.0f;
+        const float u = acc_u[i] + 0.0f;
+        y[static_cast<std::size_t>(r0 + r) * out + o] = v / (1.0f + exact::expf(-v)) * u;
+      }
+    }
+  }
+}
+
 // Up to kMaxShared products of one weight type and input size that share x
 // and rows (the prefill's q/k/v, gate/up) in one launch: workgroup column
 // blockIdx.x is tile blockIdx.x - tile_end[p - 1] of the product p whose
@@ -1006,6 +1120,40 @@ int launch_matmul(const DeviceMatrix& m, const float* x, std::size_t rows, const
   if (m.type == LLMI_TYPE_Q8_0) launch_typed<LLMI_TYPE_Q8_0>(m, x, rows, bias, y, acc, s);
   else launch_typed<LLMI_TYPE_Q4_0>(m, x, rows, bias, y, acc, s);
   LLMI_TRY_HIP(hipGetLastError());
+  return LLMI_OK;
+}
+
+int launch_gate_up_silu(const DeviceMatrix& gate, const DeviceMatrix& up, const float* x, std::size_t rows,
+                        float* y, hipStream_t s, bool* fused) {
+  *fused = false;
+  if (rows <= 8 || gate.type == LLMI_TYPE_F32 || gate.type != up.type || gate.in != up.in || gate.out != up.out ||
+      gate.out == 0 || gate.ntiles * ceil_div(rows, kExactRows) >= 1024)
+    return LLMI_OK;
+  if (int rc = check_shape(gate, rows)) return rc;
+  LLMI_REQUIRE(x != nullptr && y != nullptr, "gate_up: null pointer");
+  const auto waves = [&](std::size_t r, std::size_t w) { return gate.ntiles * ceil_div(rows, r) * w; };
+  const auto launch = [&](auto tag_r, auto tag_w) {
+    constexpr int R = decltype(tag_r)::value, W = decltype(tag_w)::value;
+    const dim3 grid(static_cast<unsigned>(gate.ntiles), static_cast<unsigned>(ceil_div(rows, R)));
+    const int in = static_cast<int>(gate.in), nblk = static_cast<int>(gate.nblk), out = static_cast<int>(gate.out);
+    const int nr = static_cast<int>(rows);
+    const auto* cg = reinterpret_cast<const uint4*>(gate.codes);
+    const auto* cu = reinterpret_cast<const uint4*>(up.codes);
+    if (gate.type == LLMI_TYPE_Q8_0)
+      qgemm_split_gate_up<LLMI_TYPE_Q8_0, R, W><<<grid, W * 64, 0, s>>>(cg, gate.scales, cu, up.scales, x, y, in, nblk,
+                                                                        out, nr);
+    else
+      qgemm_split_gate_up<LLMI_TYPE_Q4_0, R, W><<<grid, W * 64, 0, s>>>(cg, gate.scales, cu, up.scales, x, y, in, nblk,
+                                                                        out, nr);
+  };
+  using I2 = std::integral_constant<int, 2>;
+  using I4 = std::integral_constant<int, 4>;
+  using I8 = std::integral_constant<int, 8>;
+  if (waves(4, 4) >= 6144) launch(I4{}, I4{});
+  else if (waves(4, 8) >= 4096) launch(I4{}, I8{});
+  else launch(I2{}, I8{});
+  LLMI_TRY_HIP(hipGetLastError());
+  *fused = true;
   return LLMI_OK;
 }
 

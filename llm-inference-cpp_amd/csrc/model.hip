@@ -1466,16 +1466,22 @@ int forward_rows(llmi_hip_model* m, llmi_hip_cache* cache, std::size_t T, std::s
                      static_cast<int>(T), scale, s);
     if (int rc = linear(l.wo, w.att, nullptr, w.x, true)) return rc;
     rmsnorm_rows<<<tt, kThreads, 0, s>>>(w.x, l.mlp_norm, w.h, static_cast<int>(m->H), eps);
-    if (mfma_all) {
-      if (int rc = linear(l.gate, w.h, nullptr, w.g, false)) return rc;
-      if (int rc = linear(l.up, w.h, nullptr, w.u, false)) return rc;
-    } else {
-      const DeviceMatrix* gu[2] = {&l.gate, &l.up};
-      const float* gu_bias[2] = {nullptr, nullptr};
-      float* gu_out[2] = {w.g, w.u};
-      if (int rc = launch_matmul_shared(gu, gu_bias, gu_out, 2, w.h, T, s)) return rc;
+    bool fused = false;
+    if (!mfma_all) {
+      if (int rc = launch_gate_up_silu(l.gate, l.up, w.h, T, w.g, s, &fused)) return rc;
     }
-    silu_mul<<<blocks_for(T * m->F), kThreads, 0, s>>>(w.g, w.u, T * m->F);
+    if (!fused) {
+      if (mfma_all) {
+        if (int rc = linear(l.gate, w.h, nullptr, w.g, false)) return rc;
+        if (int rc = linear(l.up, w.h, nullptr, w.u, false)) return rc;
+      } else {
+        const DeviceMatrix* gu[2] = {&l.gate, &l.up};
+        const float* gu_bias[2] = {nullptr, nullptr};
+        float* gu_out[2] = {w.g, w.u};
+        if (int rc = launch_matmul_shared(gu, gu_bias, gu_out, 2, w.h, T, s)) return rc;
+      }
+      silu_mul<<<blocks_for(T * m->F), kThreads, 0, s>>>(w.g, w.u, T * m->F);
+    }
     if (int rc = linear(l.down, w.g, nullptr, w.x, true)) return rc;
     if (trace != nullptr)
       LLMI_TRY_HIP(hipMemcpyAsync(trace + (li + 1) * state, w.x, state * sizeof(float), hipMemcpyDeviceToHost, s));
