@@ -907,7 +907,9 @@ void launch_attention(const float* q, const float* kc, const float* vc, float* o
   const std::size_t npos = static_cast<std::size_t>(base) + T;
   if (attention_rows_fits(nh, nkv, hd, npos)) {
     const int rows = attention_rows(nh, nkv);
-    const int tq = rows / (nh / nkv);
+    // Tokens per workgroup: the tile's full G x tq rows, fewer when that
+    // would leave fewer than ~256 workgroups (short prompts, few KV heads).
+    const int tq = std::clamp(static_cast<int>(ceil_div(static_cast<std::size_t>(T) * nkv, 256)), 1, rows / (nh / nkv));
     const dim3 grid(static_cast<unsigned>(ceil_div(T, tq)), static_cast<unsigned>(nkv));
     const std::size_t lds = attention_rows_lds(npos, rows);
     if (rows == 16) {
