@@ -192,8 +192,22 @@ int launch_matmul(const DeviceMatrix& m, const float* x, std::size_t rows, const
 // Products of one weight type and input size sharing x and rows (the
 // prefill's q/k/v, gate/up): one split-block launch over all their tiles
 // when each would take the split-block product, else one launch each.
+// RoPE tables (cos_t / sin_t: [position][32], head size 64), the first
+// position of the launch's rows, and one layer's K / V cache ([head][cap][64]).
+struct RopeCache {
+  const float* cos_t = nullptr;
+  const float* sin_t = nullptr;
+  float* kc = nullptr;
+  float* vc = nullptr;
+  int base = 0, cap = 0;
+};
+enum SharedEpilogue { kStorePlain = 0, kStoreRope = 1, kStoreRopeCache = 2, kStoreCache = 3 };
+// With rope (and roped) given and three products of head size 64 grouped,
+// q is RoPE'd in place, k RoPE'd into rope->kc and v copied into rope->vc at
+// positions base + row, and *roped is set; otherwise the caller applies RoPE.
 int launch_matmul_shared(const DeviceMatrix* const* ms, const float* const* biases, float* const* ys, int count,
-                         const float* x, std::size_t rows, hipStream_t s);
+                         const float* x, std::size_t rows, hipStream_t s, const RopeCache* rope = nullptr,
+                         bool* roped = nullptr);
 // The prefill's MLP gate and up projections fused with silu(gate) * up into
 // y, when both would take the split-block product (rows > 8, few tiles, one
 // quantized type and shape); *fused reports whether it ran (else nothing was

@@ -723,11 +723,10 @@ __global__ void __launch_bounds__(256) qgemm_exact(const uint4* __restrict__ cod
 // fills the GPU where a 64-row tile per row chunk gives too few workgroups.
 // Small row chunks (2 or 4 rows) measured fastest: the chunk's activations
 // are scalar loads per block and row, and more workgroups hide them.
-template <int TYPE, int kSplitRows, int kSplitWaves>
+template <int TYPE, int kSplitRows, int kSplitWaves, class Epi>
 __device__ __forceinline__ void split_tile(const uint4* __restrict__ codes, const float* __restrict__ scales,
-                                           const float* __restrict__ x, const float* __restrict__ bias,
-                                           float* __restrict__ y, int in, int nblk, int out, int rows, int accumulate,
-                                           std::size_t tile, int chunk) {
+                                           const float* __restrict__ x, const float* __restrict__ bias, int in,
+                                           int nblk, int out, int rows, std::size_t tile, int chunk, const Epi& epi) {
   constexpr int RW = (kSplitRows + kSplitWaves - 1) / kSplitWaves;  // chains per lane
   __shared__ float part[2][kSplitRows][kSplitWaves][kTileRows];
   __shared__ float scl[2][kSplitWaves][kTileRows];
@@ -785,27 +784,36 @@ __device__ __forceinline__ void split_tile(const uint4* __restrict__ codes, cons
     cur = nxt;
     cur_s = nxt_s;
   }
+  // The epilogue runs on whole wavefronts (row conditions are per wavefront),
+  // so it may exchange values between the lanes of a row.
   const std::size_t o = tile * kTileRows + lane;
-  if (o < static_cast<std::size_t>(out)) {
-    const float add = bias != nullptr ? bias[o] : 0.0f;
+  const bool o_ok = o < static_cast<std::size_t>(out);
+  const float add = bias != nullptr && o_ok ? bias[o] : 0.0f;
 #pragma unroll
-    for (int i = 0; i < RW; ++i) {
-      const int r = wave + kSplitWaves * i;
-      if (r < kSplitRows && r < nr) {
-        float* dst = y + static_cast<std::size_t>(r0 + r) * out + o;
-        const float v = acc[i] + add;
-        *dst = accumulate ? *dst + v : v;
-      }
-    }
+  for (int i = 0; i < RW; ++i) {
+    const int r = wave + kSplitWaves * i;
+    if (r < kSplitRows && r < nr) epi(r0 + r, o, o_ok, acc[i] + add);
   }
 }
+
+// y[row][o] = v (or += v).
+struct StoreOut {
+  float* y;
+  int out, accumulate;
+  __device__ __forceinline__ void operator()(int row, std::size_t o, bool o_ok, float v) const {
+    if (!o_ok) return;
+    float* dst = y + static_cast<std::size_t>(row) * out + o;
+    *dst = accumulate ? *dst + v : v;
+  }
+};
 
 template <int TYPE, int R, int W>
 __global__ void __launch_bounds__(W * 64) qgemm_split(const uint4* __restrict__ codes, const float* __restrict__ scales,
                                                       const float* __restrict__ x, const float* __restrict__ bias,
                                                       float* __restrict__ y, int in, int nblk, int out, int rows,
                                                       int accumulate) {
-  split_tile<TYPE, R, W>(codes, scales, x, bias, y, in, nblk, out, rows, accumulate, blockIdx.x, blockIdx.y);
+  split_tile<TYPE, R, W>(codes, scales, x, bias, in, nblk, out, rows, blockIdx.x, blockIdx.y,
+                         StoreOut{y, out, accumulate});
 }
 
 // The gate and up projections of an MLP in one split-block tile: each round
@@ -933,7 +941,41 @@ struct SplitGroup {
   float* y[kMaxShared];
   int out[kMaxShared];
   int tile_end[kMaxShared];
+  int mode[kMaxShared];  // a SharedEpilogue
   int count;
+  RopeCache rope;
+};
+
+// A product's output in a grouped launch: y as computed, RoPE'd in place (q),
+// RoPE'd into the KV cache (k), or copied into it (v).  The RoPE modes take a
+// head size of 64, one head per 64-output tile, and rotate elements (i, i+32)
+// of a head with the host tables: v[i] = fma(a, c, -(b * s)),
+// v[i + 32] = fma(b, c, a * s) (kernels.cpp:122-134).
+struct GroupStore {
+  const SplitGroup& g;
+  int p;
+  __device__ __forceinline__ void operator()(int row, std::size_t o, bool o_ok, float v) const {
+    const int mode = g.mode[p];
+    if (mode == kStorePlain) {
+      if (o_ok) g.y[p][static_cast<std::size_t>(row) * g.out[p] + o] = v;
+      return;
+    }
+    const int lane = static_cast<int>(o & 63);
+    const int pos = g.rope.base + row;
+    if (mode != kStoreCache) {
+      const float partner = __shfl_xor(v, 32, 64);
+      const float c = g.rope.cos_t[static_cast<std::size_t>(pos) * 32 + (lane & 31)];
+      const float sn = g.rope.sin_t[static_cast<std::size_t>(pos) * 32 + (lane & 31)];
+      v = lane < 32 ? __builtin_fmaf(v, c, -(partner * sn)) : __builtin_fmaf(v, c, partner * sn);
+    }
+    if (!o_ok) return;
+    if (mode == kStoreRope) {
+      g.y[p][static_cast<std::size_t>(row) * g.out[p] + o] = v;
+    } else {
+      const std::size_t head = o >> 6;
+      g.y[p][(head * g.rope.cap + pos) * 64 + lane] = v;
+    }
+  }
 };
 
 template <int TYPE, int R, int W>
@@ -943,8 +985,8 @@ __global__ void __launch_bounds__(W * 64) qgemm_split_group(SplitGroup g, const 
   int p = 0;
   while (p + 1 < g.count && t >= g.tile_end[p]) ++p;
   const int t0 = p == 0 ? 0 : g.tile_end[p - 1];
-  split_tile<TYPE, R, W>(g.codes[p], g.scales[p], x, g.bias[p], g.y[p], in, nblk, g.out[p], rows, 0,
-                         static_cast<std::size_t>(t - t0), blockIdx.y);
+  split_tile<TYPE, R, W>(g.codes[p], g.scales[p], x, g.bias[p], in, nblk, g.out[p], rows,
+                         static_cast<std::size_t>(t - t0), blockIdx.y, GroupStore{g, p});
 }
 
 // ------------------------------------------------------------ planning
@@ -1158,7 +1200,8 @@ int launch_gate_up_silu(const DeviceMatrix& gate, const DeviceMatrix& up, const 
 }
 
 int launch_matmul_shared(const DeviceMatrix* const* ms, const float* const* biases, float* const* ys, int count,
-                         const float* x, std::size_t rows, hipStream_t s) {
+                         const float* x, std::size_t rows, hipStream_t s, const RopeCache* rope, bool* roped) {
+  if (roped != nullptr) *roped = false;
   LLMI_REQUIRE(count >= 1 && count <= kMaxShared, "matmul_shared: 1..3 products");
   std::size_t tiles = 0;
   bool grouped = count > 1 && rows > 8;
@@ -1187,8 +1230,20 @@ int launch_matmul_shared(const DeviceMatrix* const* ms, const float* const* bias
     g.out[i] = static_cast<int>(ms[i]->out);
     end += static_cast<int>(ms[i]->ntiles);
     g.tile_end[i] = end;
+    g.mode[i] = kStorePlain;
   }
   g.count = count;
+  // RoPE and the cache writes ride along for q, k, v of head size 64.
+  if (rope != nullptr && roped != nullptr && count == 3 && ms[0]->out % 64 == 0 && ms[1]->out % 64 == 0 &&
+      ms[2]->out % 64 == 0) {
+    g.rope = *rope;
+    g.mode[0] = kStoreRope;
+    g.mode[1] = kStoreRopeCache;
+    g.mode[2] = kStoreCache;
+    g.y[1] = rope->kc;
+    g.y[2] = rope->vc;
+    *roped = true;
+  }
   const DeviceMatrix& m0 = *ms[0];
   if (m0.type == LLMI_TYPE_Q8_0) launch_group_rows<LLMI_TYPE_Q8_0>(g, tiles, x, m0.in, m0.nblk, rows, s);
   else launch_group_rows<LLMI_TYPE_Q4_0>(g, tiles, x, m0.in, m0.nblk, rows, s);

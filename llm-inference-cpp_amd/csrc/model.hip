@@ -1452,6 +1452,7 @@ int forward_rows(llmi_hip_model* m, llmi_hip_cache* cache, std::size_t T, std::s
     float* kc = cache->k + li * per_layer;
     float* vc = cache->v + li * per_layer;
     rmsnorm_rows<<<tt, kThreads, 0, s>>>(w.x, l.attn_norm, w.h, static_cast<int>(m->H), eps);
+    bool roped = false;
     if (mfma_all) {
       if (int rc = linear(l.wq, w.h, l.bq, w.q, false)) return rc;
       if (int rc = linear(l.wk, w.h, l.bk, w.k, false)) return rc;
@@ -1460,10 +1461,19 @@ int forward_rows(llmi_hip_model* m, llmi_hip_cache* cache, std::size_t T, std::s
       const DeviceMatrix* qkv[3] = {&l.wq, &l.wk, &l.wv};
       const float* qkv_bias[3] = {l.bq, l.bk, l.bv};
       float* qkv_out[3] = {w.q, w.k, w.v};
-      if (int rc = launch_matmul_shared(qkv, qkv_bias, qkv_out, 3, w.h, T, s)) return rc;
+      RopeCache rc_args;
+      rc_args.cos_t = m->cos_t;
+      rc_args.sin_t = m->sin_t;
+      rc_args.kc = kc;
+      rc_args.vc = vc;
+      rc_args.base = static_cast<int>(base);
+      rc_args.cap = static_cast<int>(cache->cap);
+      if (int rc = launch_matmul_shared(qkv, qkv_bias, qkv_out, 3, w.h, T, s, hd == 64 ? &rc_args : nullptr, &roped))
+        return rc;
     }
-    rope_and_cache<<<tt, kThreads, 0, s>>>(w.q, w.k, w.v, kc, vc, m->cos_t, m->sin_t, nh, nkv, hd,
-                                           static_cast<int>(cache->cap), static_cast<int>(base));
+    if (!roped)
+      rope_and_cache<<<tt, kThreads, 0, s>>>(w.q, w.k, w.v, kc, vc, m->cos_t, m->sin_t, nh, nkv, hd,
+                                             static_cast<int>(cache->cap), static_cast<int>(base));
     launch_attention(w.q, kc, vc, w.att, nh, nkv, hd, static_cast<int>(cache->cap), static_cast<int>(base),
                      static_cast<int>(T), scale, s);
     if (int rc = linear(l.wo, w.att, nullptr, w.x, true)) return rc;
