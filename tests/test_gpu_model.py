@@ -245,12 +245,14 @@ def test_decode_attention_matches_reference(hidden, heads, kv):
 
 # ----------------------------------------------- prefill attention shapes
 @pytest.mark.parametrize("hidden,heads,kv", [(64, 1, 1), (256, 4, 2), (192, 3, 1), (448, 7, 1), (576, 9, 3),
-                                             (2048, 32, 1), (1024, 16, 1), (256, 2, 1)])
+                                             (2048, 32, 1), (1024, 16, 1), (256, 2, 1), (80, 1, 1)])
 def test_prefill_attention_matches_reference(hidden, heads, kv):
     """Multi-token forward passes after earlier ones (base > 0): head size 64
     with GQA groups of 1 to 32 takes the workgroup-per-(KV head, token tile)
     prefill attention (16 rows per workgroup up to groups of 16, 32 above),
-    head size 128 the per-(head, token) kernel.  Chunk
+    head sizes 128 and 80 the per-(head, token) kernel (80 also leaves a
+    partial final quantization block in the q/k/v and fused gate/up
+    products).  Chunk
     lengths leave ragged token tiles and end on and off the 64-position K/V
     tiles; every position's logits equal the reference's bit for bit."""
     cpu = O.reference() or O.oracle()
