@@ -314,7 +314,7 @@ def decode_runs():
             rec = json.load(f)
         m = H.synthetic_model_dev(cfg, rec["seed"], qt, rec["convention"])
         prompt = synth.uniform_ids(rec["prompt_seed"], rec["n_prompt"], cfg["vocab_size"])
-        m.generate_greedy(prompt[:8], 4)  # warm-up (code objects, workspace)
+        m.generate_greedy(prompt, 4)  # warm-up at the real prompt length (code objects, workspace)
         ids = m.generate_greedy(prompt, rec["n_steps"])
         pre_ms, dec_ms = m.last_timing()
         wb = m.weight_bytes()
