@@ -712,12 +712,14 @@ __global__ void __launch_bounds__(256) qgemm_exact(const uint4* __restrict__ cod
 
 // qgemm_split (batch > 8, matrices with few 64-row tiles): one workgroup per
 // (tile, chunk of kSplitRows input rows) whose kSplitWaves wavefronts take
-// the tile's blocks round-robin.  In each round wavefront w decodes block
-// round * kSplitWaves + w once (lane l: output tile*64 + l) and forms its
-// block sums for every row of the chunk, with the activations read by
-// scalar loads; the sums and scales go to LDS (two buffers, one barrier per
-// round), and wavefront w then advances the chains of rows w, w +
-// kSplitWaves over the round's blocks in order: acc = fma(part, scale, acc).
+// the tile's blocks round-robin, two per round each (W = kSplitWaves).  In
+// each round wavefront w decodes blocks 2W * round + w and 2W * round + W + w
+// once each (lane l: output tile*64 + l) and forms their block sums for
+// every row of the chunk, with the activations read by scalar loads; the
+// sums and scales go to LDS (two buffers, one barrier per round), and
+// wavefront w then advances the chains of rows w, w + W over the round's 2W
+// blocks in order: acc = fma(part, scale, acc).  (Two blocks per round
+// halve the barriers: Qwen2.5's down_proj at 512 rows 109 -> 102 us.)
 // The block sums are the reference's per-block chains and the chain over
 // blocks runs in block order, so y is bit-identical; splitting the blocks
 // fills the GPU where a 64-row tile per row chunk gives too few workgroups.
@@ -728,8 +730,8 @@ __device__ __forceinline__ void split_tile(const uint4* __restrict__ codes, cons
                                            const float* __restrict__ x, const float* __restrict__ bias, int in,
                                            int nblk, int out, int rows, std::size_t tile, int chunk, const Epi& epi) {
   constexpr int RW = (kSplitRows + kSplitWaves - 1) / kSplitWaves;  // chains per lane
-  __shared__ float part[2][kSplitRows][kSplitWaves][kTileRows];
-  __shared__ float scl[2][kSplitWaves][kTileRows];
+  __shared__ float part[2][kSplitRows][2 * kSplitWaves][kTileRows];
+  __shared__ float scl[2][2 * kSplitWaves][kTileRows];
   const int r0 = chunk * kSplitRows;
   const int nr = min(kSplitRows, rows - r0);
   const int lane = threadIdx.x & (kTileRows - 1);
@@ -742,36 +744,48 @@ __device__ __forceinline__ void split_tile(const uint4* __restrict__ codes, cons
   float acc[RW];
 #pragma unroll
   for (int i = 0; i < RW; ++i) acc[i] = 0.0f;
-  const int nround = (nblk + kSplitWaves - 1) / kSplitWaves;
-  Block<TYPE> cur{};
-  float cur_s = 0.0f;
-  if (wave < nblk) {
-    cur = load_block<TYPE, false>(cg, base + wave, lane);
-    cur_s = sg[(base + wave) * kTileRows + lane];
+  const int nround = (nblk + 2 * kSplitWaves - 1) / (2 * kSplitWaves);
+  Block<TYPE> cur[2]{};
+  float cur_s[2] = {0.0f, 0.0f};
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int bb = h * kSplitWaves + wave;
+    if (bb < nblk) {
+      cur[h] = load_block<TYPE, false>(cg, base + bb, lane);
+      cur_s[h] = sg[(base + bb) * kTileRows + lane];
+    }
   }
   for (int rd = 0; rd < nround; ++rd) {
     const int buf = rd & 1;
-    const int b = rd * kSplitWaves + wave;
-    Block<TYPE> nxt{};
-    float nxt_s = 0.0f;
-    if (b + kSplitWaves < nblk) {
-      nxt = load_block<TYPE, false>(cg, base + b + kSplitWaves, lane);
-      nxt_s = sg[(base + b + kSplitWaves) * kTileRows + lane];
-    }
-    if (b < nfull) {
-      float c[kBlock];
-      block_codes<TYPE>(cur, c);
+    Block<TYPE> nxt[2]{};
+    float nxt_s[2] = {0.0f, 0.0f};
 #pragma unroll
-      for (int r = 0; r < kSplitRows; ++r)
-        if (r < nr) part[buf][r][wave][lane] = codes_dot(c, xg + static_cast<std::size_t>(r) * in + b * kBlock);
-    } else if (b < nblk) {
-      for (int r = 0; r < nr; ++r)
-        part[buf][r][wave][lane] =
-            tail_block_dot<TYPE>(cur, xg + static_cast<std::size_t>(r) * in + b * kBlock, in - b * kBlock);
+    for (int h = 0; h < 2; ++h) {
+      const int bn = (rd + 1) * 2 * kSplitWaves + h * kSplitWaves + wave;
+      if (bn < nblk) {
+        nxt[h] = load_block<TYPE, false>(cg, base + bn, lane);
+        nxt_s[h] = sg[(base + bn) * kTileRows + lane];
+      }
     }
-    if (b < nblk) scl[buf][wave][lane] = cur_s;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int b = rd * 2 * kSplitWaves + h * kSplitWaves + wave;
+      const int j = h * kSplitWaves + wave;
+      if (b < nfull) {
+        float c[kBlock];
+        block_codes<TYPE>(cur[h], c);
+#pragma unroll
+        for (int r = 0; r < kSplitRows; ++r)
+          if (r < nr) part[buf][r][j][lane] = codes_dot(c, xg + static_cast<std::size_t>(r) * in + b * kBlock);
+      } else if (b < nblk) {
+        for (int r = 0; r < nr; ++r)
+          part[buf][r][j][lane] =
+              tail_block_dot<TYPE>(cur[h], xg + static_cast<std::size_t>(r) * in + b * kBlock, in - b * kBlock);
+      }
+      if (b < nblk) scl[buf][j][lane] = cur_s[h];
+    }
     __syncthreads();
-    const int nb = min(kSplitWaves, nblk - rd * kSplitWaves);
+    const int nb = min(2 * kSplitWaves, nblk - rd * 2 * kSplitWaves);
 #pragma unroll
     for (int i = 0; i < RW; ++i) {
       const int r = wave + kSplitWaves * i;
@@ -781,8 +795,10 @@ __device__ __forceinline__ void split_tile(const uint4* __restrict__ codes, cons
         acc[i] = a;
       }
     }
-    cur = nxt;
-    cur_s = nxt_s;
+    cur[0] = nxt[0];
+    cur[1] = nxt[1];
+    cur_s[0] = nxt_s[0];
+    cur_s[1] = nxt_s[1];
   }
   // The epilogue runs on whole wavefronts (row conditions are per wavefront),
   // so it may exchange values between the lanes of a row.
