@@ -32,6 +32,7 @@ sys.path.insert(0, os.path.join(ROOT, "llm-inference-cpp_amd"))
 
 import llmi_hip as H  # noqa: E402
 import synth  # noqa: E402
+import workloads as W  # noqa: E402
 
 METRIC = "Q4_0/Q8_0 GEMV achieved HBM GB/s (% of peak); decode tokens/s, 1 GPU"
 HBM_PEAK_GBS = 8000.0
@@ -41,17 +42,14 @@ HBM_PEAK_GBS = 8000.0
 GROUP_B1_HBM_BYTES = 85_093_182
 ROTATE_BYTES = 1 << 30
 
-SMOL_LAYER = [("q_proj", 576, 576), ("k_proj", 192, 576), ("v_proj", 192, 576), ("o_proj", 576, 576),
-              ("gate_proj", 1536, 576), ("up_proj", 1536, 576), ("down_proj", 576, 1536)]
-SMOL_HEAD = ("lm_head", 49152, 576)
+SMOL_LAYER = W.SMOL_LAYER
+SMOL_HEAD = W.SMOL_HEAD
 N_LAYERS = 30
 QWEN_TARGETS = [("lm_head", 151936, 896, H.Q4_0), ("lm_head", 151936, 896, H.Q8_0),
                 ("gate_proj", 4864, 896, H.Q4_0), ("down_proj", 896, 4864, H.Q4_0)]
 
 
-def algo_bytes(out: int, n_in: int, qt: int, batch: int) -> int:
-    """Packed codes + fp32 scales + x + y, each counted once."""
-    return out * H.row_bytes(n_in, qt) + 4 * out * H.nblocks(n_in) + 4 * batch * (n_in + out)
+algo_bytes = W.algo_bytes
 
 
 def step_shapes():
@@ -196,8 +194,7 @@ def grouped_mlp_targets(steps=50):
     return res
 
 
-QWEN_LAYER = [("q_proj", 896, 896), ("k_proj", 128, 896), ("v_proj", 128, 896), ("o_proj", 896, 896),
-              ("gate_proj", 4864, 896), ("up_proj", 4864, 896), ("down_proj", 896, 4864)]
+QWEN_LAYER = W.QWEN_LAYER
 MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense bf16
 FP32_PEAK_TFLOPS = 157.3  # MI355X fp32 vector (packed); this build issues non-packed FMAs only
 
@@ -233,32 +230,18 @@ def gguf_upload(reps=3):
 def prefill_gemm(steps=20, warmup=3):
     """M=512 tokens of fp32 activations against
     every Qwen2.5-0.5B linear layer (24 layers x 7 products) in Q8_0, on the
-    bf16-MFMA GEMM.  All 168 products run as one grouped launch per step
-    (llmi_hip_gemm_group); a second figure runs them as 24 per-layer groups."""
-    M, L = 512, 24
-    xs = {}
-    for n_in in sorted({i for _, _, i in QWEN_LAYER}):
-        xb = H.DeviceBuffer(M * n_in * 4)
-        H.synth_normal_dev(xb, M * n_in, 300 + n_in, 0.0, 1.0)
-        xs[n_in] = xb
-    stage = H.DeviceBuffer(4864 * 896 * 4)
-    ws, ys, items, layers = [], [], [], []
-    for layer in range(L):
-        li = []
-        for j, (_, out, n_in) in enumerate(QWEN_LAYER):
-            H.synth_normal_dev(stage, out * n_in, 7000 + 16 * layer + j, 0.0, 0.02)
-            w = H.Weight.quantize_dev(stage.ptr, out, n_in, H.Q8_0)
-            y = H.DeviceBuffer(M * out * 4)
-            ws.append(w)
-            ys.append(y)
-            li.append((w, xs[n_in].ptr, y.ptr, M))
-        items += li
-        layers.append(li)
-    stage.free()
-    flops = 2.0 * M * sum(o * i for _, o, i in QWEN_LAYER) * L
-    wbytes = sum(w.byte_size for w in ws)
+    bf16-MFMA GEMM, each layer with its own activations
+    (workloads.PrefillProducts, the same products
+    tests/test_gpu_gemm.py checks).  "per_layer" runs them as 24 launches of
+    one layer's 7 products -- the realistic schedule, since a layer's input
+    is the previous layer's output; "one_launch" runs all 168 in one grouped
+    launch (independent products, an upper bound on the kernel)."""
+    prods = W.PrefillProducts(M=512, layers=24, qt=H.Q8_0)
+    flops = prods.flops()
+    wbytes = sum(w.byte_size for w in prods.weights)
     res = {}
-    for mode, groups in (("one_launch", [H.GemmGroup(items)]), ("per_layer", [H.GemmGroup(li) for li in layers])):
+    for mode, groups in (("per_layer", [H.GemmGroup(li) for li in prods.per_layer]),
+                         ("one_launch", [H.GemmGroup(prods.items)])):
         for _ in range(warmup):
             for g in groups:
                 g.launch()
@@ -275,14 +258,12 @@ def prefill_gemm(steps=20, warmup=3):
                          launches=len(groups))
         for g in groups:
             g.free()
-    for b in list(xs.values()) + ys:
-        b.free()
-    for w in ws:
-        w.free()
-    res.update(workload="24 layers x {q,k,v,o 896/128 x 896; gate,up 4864x896; down 896x4864} Q8_0, M=512, fp32 in/out",
+    prods.free()
+    res.update(workload="24 layers x {q,k,v,o 896/128 x 896; gate,up 4864x896; down 896x4864} Q8_0, M=512, fp32 "
+                        "in/out, distinct activations per layer",
                gflop=round(flops / 1e9, 2), weight_bytes=wbytes, precision="bf16 operands, fp32 accumulate (tolerance 2e-2)")
-    print(f"[bench] c5 prefill GEMM: {res['one_launch']['tflops']} TFLOP/s one launch, "
-          f"{res['per_layer']['tflops']} per-layer", file=sys.stderr, flush=True)
+    print(f"[bench] c5 prefill GEMM: {res['per_layer']['tflops']} TFLOP/s per-layer, "
+          f"{res['one_launch']['tflops']} one launch", file=sys.stderr, flush=True)
     return res
 
 

@@ -280,6 +280,15 @@ int llmi_hip_model_forward_cached(llmi_hip_model* model, llmi_hip_cache* cache, 
 int llmi_hip_model_forward_cached_trace(llmi_hip_model* model, llmi_hip_cache* cache, const int32_t* tokens,
                                         size_t n, int all_positions, float* logits, float* states);
 
+/* Transformer::forward (transformer.cpp:78-166): the whole sequence without a
+ * caller's cache (the model's own is reused and reset), logits of the last
+ * token or of every token; states as for forward_cached_trace (NULL to
+ * skip).  Bit-identical to forward_cached on a fresh cache, as the
+ * reference's own test holds (tests/transformer_test.cpp:322-339); errors
+ * carry forward's messages ("forward: ..."). */
+int llmi_hip_model_forward(llmi_hip_model* model, const int32_t* tokens, size_t n, int all_positions, float* logits,
+                           float* states);
+
 /* Transformer::generate_greedy_cached (transformer.cpp:308-327): prefill,
  * then up to max_new greedy tokens (first maximum), stopping after a token in
  * stop_ids.  Writes *n_ids ids to `ids` (room for max_new). */

@@ -1108,6 +1108,8 @@ struct Workspace {
   std::int32_t* next = nullptr;  // argmax result
   std::int32_t* gen = nullptr;   // generated ids of the current greedy run
   std::size_t gen_cap = 0;
+  double* nll = nullptr;         // per-position NLL of chunk_nll
+  std::size_t nll_cap = 0;
   float* am_v = nullptr;         // argmax partials and completion counter
   int* am_i = nullptr;
   unsigned* am_count = nullptr;
@@ -1129,6 +1131,10 @@ struct llmi_hip_model {
   std::size_t table_len = 0;
   llmi_hip::Workspace ws;
   llmi_hip::DecodeBuffers dec;
+  // The cache of the calls that need one only for their own duration
+  // (forward without a cache, generate_*, chunk_nll): kept and reused while
+  // its allocation is large enough, reset on every use.
+  llmi_hip_cache* scratch = nullptr;
   std::vector<void*> allocations;
   double last_prefill_ms = 0.0, last_decode_ms = 0.0;  // of the last greedy run
 };
@@ -1139,6 +1145,7 @@ struct llmi_hip_cache {
   float* k = nullptr;  // [layer][kv_head][cap][hd]
   float* v = nullptr;
   float* scores = nullptr;  // [head][cap], decode attention scratch
+  std::size_t kv_elems = 0, score_elems = 0;  // allocated floats of k (= v) and scores
 };
 
 namespace llmi_hip {
@@ -1353,7 +1360,8 @@ void free_workspace(Workspace& w) {
   for (void* p : {static_cast<void*>(w.x), static_cast<void*>(w.h), static_cast<void*>(w.q), static_cast<void*>(w.k),
                   static_cast<void*>(w.v), static_cast<void*>(w.att), static_cast<void*>(w.g), static_cast<void*>(w.u),
                   static_cast<void*>(w.logits), static_cast<void*>(w.ids), static_cast<void*>(w.next),
-                  static_cast<void*>(w.gen), static_cast<void*>(w.am_v), static_cast<void*>(w.am_i),
+                  static_cast<void*>(w.gen), static_cast<void*>(w.nll), static_cast<void*>(w.am_v),
+                  static_cast<void*>(w.am_i),
                   static_cast<void*>(w.am_count)})
     if (p != nullptr) (void)hipFree(p);
   w = Workspace{};
@@ -1401,6 +1409,7 @@ int decode_step(llmi_hip_model* m, llmi_hip_cache* cache, hipStream_t s) {
   Workspace& w = m->ws;
   DecodeBuffers& d = m->dec;
   const std::size_t pos = cache->len;
+  if (pos + 1 > cache->cap || pos + 1 > m->table_len) return fail(LLMI_ERR_STATE, "forward_cached: cache is full");
   const int nh = static_cast<int>(c.num_heads), nkv = static_cast<int>(c.num_kv_heads);
   const int hd = static_cast<int>(m->hd);
   const float eps = static_cast<float>(c.rms_norm_eps);
@@ -1437,6 +1446,7 @@ int forward_rows(llmi_hip_model* m, llmi_hip_cache* cache, std::size_t T, std::s
   const auto& c = m->c;
   Workspace& w = m->ws;
   const std::size_t base = cache->len;
+  if (base + T > cache->cap || base + T > m->table_len) return fail(LLMI_ERR_STATE, "forward_cached: cache is full");
   const int nh = static_cast<int>(c.num_heads), nkv = static_cast<int>(c.num_kv_heads);
   const int hd = static_cast<int>(m->hd);
   const float eps = static_cast<float>(c.rms_norm_eps);
@@ -1525,12 +1535,71 @@ int forward_rows(llmi_hip_model* m, llmi_hip_cache* cache, std::size_t T, std::s
 // the final RMSNorm, as the reference's ForwardTrace (transformer.hpp:14-19).
 int forward_device(llmi_hip_model* m, llmi_hip_cache* cache, std::size_t T, bool all_positions, hipStream_t s,
                    float* trace = nullptr) {
+  // The capacity and context checks of transformer.cpp:209-210, repeated
+  // here because the generate loops call this once per step without going
+  // through validate(): a step past the cache would write K/V and read RoPE
+  // tables out of bounds.
+  if (cache->len + T > cache->cap) return fail(LLMI_ERR_STATE, "forward_cached: cache is full");
+  if (cache->len + T > m->c.max_position_embeddings)
+    return fail(LLMI_ERR_STATE, "forward_cached: sequence longer than the model's context");
   const int nh = static_cast<int>(m->c.num_heads), nkv = static_cast<int>(m->c.num_kv_heads);
   if (T == 1 && trace == nullptr && m->type != LLMI_TYPE_F32 &&
       decode_attention_fits(nh, nkv, static_cast<int>(m->hd), cache->len + 1))
     return decode_step(m, cache, s);
   const std::size_t first = all_positions ? 0 : T - 1;
   return forward_rows(m, cache, T, first, T - first, false, s, trace);
+}
+
+// A cache of `cap` positions (the caller has clamped cap to the context):
+// new_cache's allocation (transformer.cpp:182-190), or -- reuse != nullptr --
+// that cache re-shaped to cap positions when its allocation holds them.
+// The layout [layer][kv_head][cap][hd] changes with cap, so a reused cache
+// starts empty.
+int alloc_cache(llmi_hip_model* m, std::size_t cap, llmi_hip_cache* reuse, llmi_hip_cache** out) {
+  *out = nullptr;
+  if (cap == 0) return fail(LLMI_ERR_ARG, "new_cache: max_len must be positive");
+  LLMI_REQUIRE(attention_dyn_lds(cap, m->hd) + attention_static_lds() <= max_lds_per_block(),
+               "new_cache: capacity exceeds the attention kernel's LDS");
+  if (int rc = ensure_tables(m, cap)) return rc;
+  const std::size_t kv = m->layers.size() * m->c.num_kv_heads * cap * m->hd;
+  const std::size_t sc = static_cast<std::size_t>(m->c.num_heads) * cap;
+  if (reuse != nullptr && reuse->kv_elems >= kv && reuse->score_elems >= sc) {
+    reuse->cap = cap;
+    reuse->len = 0;
+    *out = reuse;
+    return LLMI_OK;
+  }
+  auto c = std::make_unique<llmi_hip_cache>();
+  c->model = m;
+  c->cap = cap;
+  LLMI_TRY_HIP(hipMalloc(&c->k, kv * sizeof(float)));
+  if (hipMalloc(&c->v, kv * sizeof(float)) != hipSuccess) {
+    (void)hipFree(c->k);
+    return fail(LLMI_ERR_HIP, "new_cache: hipMalloc");
+  }
+  if (hipMalloc(&c->scores, sc * sizeof(float)) != hipSuccess) {
+    (void)hipFree(c->k);
+    (void)hipFree(c->v);
+    return fail(LLMI_ERR_HIP, "new_cache: hipMalloc");
+  }
+  c->kv_elems = kv;
+  c->score_elems = sc;
+  *out = c.release();
+  return LLMI_OK;
+}
+
+// The model's own cache for calls that need one only while they run,
+// sized for min(max_len, context) positions and empty.
+int scratch_cache(llmi_hip_model* m, std::size_t max_len, llmi_hip_cache** out) {
+  const std::size_t cap = std::min<std::size_t>(max_len, m->c.max_position_embeddings);
+  llmi_hip_cache* c = nullptr;
+  if (int rc = alloc_cache(m, cap, m->scratch, &c)) return rc;
+  if (c != m->scratch) {
+    (void)llmi_hip_cache_free(m->scratch);  // synchronises the stream first
+    m->scratch = c;
+  }
+  *out = c;
+  return LLMI_OK;
 }
 
 // Validation of transformer.cpp:204-212, with the reference's messages.
@@ -1608,6 +1677,7 @@ int llmi_hip_model_free(llmi_hip_model* m) {
   if (m == nullptr) return LLMI_OK;
   if (library_stream() != nullptr) (void)hipStreamSynchronize(library_stream());
   release_decode(m);
+  (void)llmi_hip_cache_free(m->scratch);
   for (void* p : m->allocations) (void)hipFree(p);
   if (m->cos_t != nullptr) (void)hipFree(m->cos_t);
   if (m->sin_t != nullptr) (void)hipFree(m->sin_t);
@@ -1631,27 +1701,7 @@ int llmi_hip_model_new_cache(llmi_hip_model* m, size_t max_len, llmi_hip_cache**
   LLMI_REQUIRE_INIT();
   LLMI_REQUIRE(m != nullptr && cache != nullptr, "new_cache: null pointer");
   *cache = nullptr;
-  const std::size_t cap = std::min<std::size_t>(max_len, m->c.max_position_embeddings);
-  if (cap == 0) return fail(LLMI_ERR_ARG, "new_cache: max_len must be positive");
-  LLMI_REQUIRE(attention_dyn_lds(cap, m->hd) + attention_static_lds() <= max_lds_per_block(),
-               "new_cache: capacity exceeds the attention kernel's LDS");
-  if (int rc = ensure_tables(m, cap)) return rc;
-  auto c = std::make_unique<llmi_hip_cache>();
-  c->model = m;
-  c->cap = cap;
-  const std::size_t n = m->layers.size() * m->c.num_kv_heads * cap * m->hd;
-  LLMI_TRY_HIP(hipMalloc(&c->k, n * sizeof(float)));
-  if (hipMalloc(&c->v, n * sizeof(float)) != hipSuccess) {
-    (void)hipFree(c->k);
-    return fail(LLMI_ERR_HIP, "new_cache: hipMalloc");
-  }
-  if (hipMalloc(&c->scores, m->c.num_heads * cap * sizeof(float)) != hipSuccess) {
-    (void)hipFree(c->k);
-    (void)hipFree(c->v);
-    return fail(LLMI_ERR_HIP, "new_cache: hipMalloc");
-  }
-  *cache = c.release();
-  return LLMI_OK;
+  return alloc_cache(m, std::min<std::size_t>(max_len, m->c.max_position_embeddings), nullptr, cache);
 }
 
 int llmi_hip_cache_free(llmi_hip_cache* c) {
@@ -1688,6 +1738,24 @@ int llmi_hip_model_forward_cached_trace(llmi_hip_model* m, llmi_hip_cache* cache
   return LLMI_OK;
 }
 
+// Transformer::forward (transformer.cpp:78-166): the whole sequence through
+// the model's own scratch cache, reset first -- bit-identical to
+// forward_cached on a fresh cache (transformer_test.cpp:322-339).
+int llmi_hip_model_forward(llmi_hip_model* m, const int32_t* tokens, size_t n, int all_positions, float* logits,
+                           float* states) {
+  LLMI_REQUIRE_INIT();
+  LLMI_REQUIRE(m != nullptr, "forward: null model");
+  if (n == 0) return fail(LLMI_ERR_ARG, "forward: no tokens");
+  if (n > m->c.max_position_embeddings)
+    return fail(LLMI_ERR_STATE, "forward: sequence longer than the model's context");
+  for (std::size_t t = 0; t < n; ++t)
+    if (tokens[t] < 0 || static_cast<std::size_t>(tokens[t]) >= m->V)
+      return fail(LLMI_ERR_ARG, "forward: token id " + std::to_string(tokens[t]) + " out of range");
+  llmi_hip_cache* cache = nullptr;
+  if (int rc = scratch_cache(m, n, &cache)) return rc;
+  return llmi_hip_model_forward_cached_trace(m, cache, tokens, n, all_positions, logits, states);
+}
+
 int llmi_hip_model_forward_cached(llmi_hip_model* m, llmi_hip_cache* cache, const int32_t* tokens, size_t n,
                                   int all_positions, float* logits) {
   return llmi_hip_model_forward_cached_trace(m, cache, tokens, n, all_positions, logits, nullptr);
@@ -1703,8 +1771,7 @@ int llmi_hip_model_generate_greedy(llmi_hip_model* m, const int32_t* prompt, siz
   LLMI_REQUIRE(m != nullptr && ids != nullptr && n_ids != nullptr, "generate_greedy: null pointer");
   *n_ids = 0;
   llmi_hip_cache* cache = nullptr;
-  if (int rc = llmi_hip_model_new_cache(m, n + max_new, &cache)) return rc;
-  std::unique_ptr<llmi_hip_cache, int (*)(llmi_hip_cache*)> guard(cache, llmi_hip_cache_free);
+  if (int rc = scratch_cache(m, n + max_new, &cache)) return rc;
   if (int rc = validate(m, cache, prompt, n)) return rc;
   if (max_new == 0) return LLMI_OK;
   if (int rc = ensure_workspace(m, n)) return rc;
@@ -1783,8 +1850,7 @@ int llmi_hip_model_generate_sampled(llmi_hip_model* m, const int32_t* prompt, si
   LLMI_REQUIRE(targets != nullptr || max_new == 0 || cfg->temperature <= 0.0f, "generate_sampled: null targets");
   *n_ids = 0;
   llmi_hip_cache* cache = nullptr;
-  if (int rc = llmi_hip_model_new_cache(m, n + max_new, &cache)) return rc;
-  std::unique_ptr<llmi_hip_cache, int (*)(llmi_hip_cache*)> guard(cache, llmi_hip_cache_free);
+  if (int rc = scratch_cache(m, n + max_new, &cache)) return rc;
   if (int rc = validate(m, cache, prompt, n)) return rc;
   if (max_new == 0) return LLMI_OK;
   if (int rc = ensure_workspace(m, n)) return rc;
@@ -1833,8 +1899,7 @@ int llmi_hip_model_chunk_nll(llmi_hip_model* m, const int32_t* tokens, size_t n,
   LLMI_REQUIRE(mode == LLMI_SCORE_EXACT || mode == LLMI_SCORE_MFMA_HEAD || mode == LLMI_SCORE_MFMA,
                "chunk_nll: mode must be LLMI_SCORE_EXACT, _MFMA_HEAD or _MFMA");
   llmi_hip_cache* cache = nullptr;
-  if (int rc = llmi_hip_model_new_cache(m, n, &cache)) return rc;
-  std::unique_ptr<llmi_hip_cache, int (*)(llmi_hip_cache*)> guard(cache, llmi_hip_cache_free);
+  if (int rc = scratch_cache(m, n, &cache)) return rc;
   if (int rc = validate(m, cache, tokens, n)) return rc;
   LLMI_REQUIRE(nll != nullptr || t_start + 1 >= n, "chunk_nll: null nll");
   if (int rc = ensure_workspace(m, n)) return rc;
@@ -1846,14 +1911,18 @@ int llmi_hip_model_chunk_nll(llmi_hip_model* m, const int32_t* tokens, size_t n,
   if (int rc = forward_rows(m, cache, n, first, rows, mode != LLMI_SCORE_EXACT, s, nullptr, mode == LLMI_SCORE_MFMA))
     return rc;
   if (rows == 0) return LLMI_OK;
-  double* d = nullptr;
-  LLMI_TRY_HIP(hipMalloc(&d, rows * sizeof(double)));
-  row_nll<<<static_cast<unsigned>(rows), kThreads, 0, s>>>(w.logits, static_cast<int>(m->V), w.ids + first + 1, d);
-  hipError_t e = hipGetLastError();
-  if (e == hipSuccess) e = hipMemcpyAsync(nll, d, rows * sizeof(double), hipMemcpyDeviceToHost, s);
-  if (e == hipSuccess) e = hipStreamSynchronize(s);
-  (void)hipFree(d);
-  if (e != hipSuccess) return fail(LLMI_ERR_HIP, std::string("chunk_nll: ") + hipGetErrorString(e));
+  if (w.nll_cap < rows) {
+    LLMI_TRY_HIP(hipStreamSynchronize(s));
+    if (w.nll != nullptr) (void)hipFree(w.nll);
+    w.nll = nullptr;
+    w.nll_cap = 0;
+    LLMI_TRY_HIP(hipMalloc(&w.nll, w.tokens * sizeof(double)));  // rows < n <= w.tokens
+    w.nll_cap = w.tokens;
+  }
+  row_nll<<<static_cast<unsigned>(rows), kThreads, 0, s>>>(w.logits, static_cast<int>(m->V), w.ids + first + 1, w.nll);
+  LLMI_TRY_HIP(hipGetLastError());
+  LLMI_TRY_HIP(hipMemcpyAsync(nll, w.nll, rows * sizeof(double), hipMemcpyDeviceToHost, s));
+  LLMI_TRY_HIP(hipStreamSynchronize(s));
   return LLMI_OK;
 }
 

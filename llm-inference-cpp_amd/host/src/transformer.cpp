@@ -155,21 +155,27 @@ Result<TokenId> Transformer::forward_sample(const std::vector<TokenId>& tokens, 
   return static_cast<TokenId>(id);
 }
 
-// forward() recomputes the whole sequence; the reference's own tests hold it
-// bit-identical to forward_cached on a fresh cache (transformer_test.cpp:322-339).
+// forward() recomputes the whole sequence (transformer.cpp:78-166) through the
+// model's own device cache, which the library reuses across calls; the
+// reference's own tests hold it bit-identical to forward_cached on a fresh
+// cache (transformer_test.cpp:322-339).
 Result<std::vector<float>> Transformer::forward(const std::vector<TokenId>& tokens, bool all_positions,
                                                 ForwardTrace* trace) const {
-  if (tokens.empty()) return fail("forward: no tokens");
-  if (tokens.size() > cfg_.max_position_embeddings) return fail("forward: sequence longer than the model's context");
-  auto cache = new_cache(tokens.size());
-  if (!cache) return fail(cache.error());
-  auto r = forward_cached(tokens, *cache, all_positions, trace);
-  if (!r) {
-    std::string msg = r.error();
-    if (msg.rfind("forward_cached: ", 0) == 0) msg = "forward: " + msg.substr(16);
-    return fail(msg);
+  const std::size_t T = tokens.size();
+  std::vector<float> logits((all_positions ? std::max<std::size_t>(T, 1) : 1) * cfg_.vocab_size);
+  std::vector<float> states;
+  if (trace != nullptr) states.resize((cfg_.num_layers + 2) * T * cfg_.hidden_size);
+  if (llmi_hip_model_forward(dev_.get(), tokens.data(), T, all_positions ? 1 : 0, logits.data(),
+                             trace != nullptr ? states.data() : nullptr) != LLMI_OK)
+    return fail(llmi_hip_last_error());
+  if (trace != nullptr) {
+    const std::size_t n = T * cfg_.hidden_size;
+    trace->states.clear();
+    for (std::size_t k = 0; k < cfg_.num_layers + 2; ++k)
+      trace->states.emplace_back(states.begin() + static_cast<std::ptrdiff_t>(k * n),
+                                 states.begin() + static_cast<std::ptrdiff_t>((k + 1) * n));
   }
-  return r;
+  return logits;
 }
 
 Result<std::vector<TokenId>> Transformer::generate_greedy_cached(const std::vector<TokenId>& prompt,

@@ -85,6 +85,7 @@ SIGNATURES = {
     "llmi_hip_cache_reset": (_i, [_vp]),
     "llmi_hip_model_forward_cached": (_i, [_vp, _vp, _vp, _sz, _i, _vp]),
     "llmi_hip_model_forward_cached_trace": (_i, [_vp, _vp, _vp, _sz, _i, _vp, _vp]),
+    "llmi_hip_model_forward": (_i, [_vp, _vp, _sz, _i, _vp, _vp]),
     "llmi_hip_model_generate_greedy": (_i, [_vp, _vp, _sz, _sz, _vp, _sz, _vp, C.POINTER(_sz)]),
     "llmi_hip_model_last_timing": (_i, [_vp, C.POINTER(_d), C.POINTER(_d)]),
     "llmi_hip_sample": (_i, [_vp, _sz, _vp, _d, C.POINTER(C.c_int32)]),
@@ -426,6 +427,14 @@ class Model:
         check(self.lib.llmi_hip_model_forward_cached_trace(self.h, cache.h, _p(toks), toks.size, int(all_positions),
                                                            _p(logits), _p(states)))
         return logits, states
+
+    def forward(self, tokens, all_positions: bool = False) -> np.ndarray:
+        """Transformer::forward: the whole sequence, no caller's cache."""
+        toks = np.ascontiguousarray(tokens, dtype=np.int32)
+        rows = toks.size if all_positions else 1
+        logits = np.zeros(max(rows, 1) * self.cfg["vocab_size"], dtype=np.float32)
+        check(self.lib.llmi_hip_model_forward(self.h, _p(toks), toks.size, int(all_positions), _p(logits), None))
+        return logits
 
     def generate_greedy(self, prompt, max_new: int, stop_ids=()) -> np.ndarray:
         p = np.ascontiguousarray(prompt, dtype=np.int32)

@@ -16,6 +16,7 @@ import pytest
 import llmi_hip as H
 import oracle as O
 import synth
+import workloads
 
 pytestmark = pytest.mark.gpu
 
@@ -78,8 +79,9 @@ def test_dequantized_restatement_matches_oracle():
 
 
 @pytest.mark.parametrize("qt", [O.Q8_0, O.Q4_0])
-@pytest.mark.parametrize("out,n_in,rows", [(896, 896, 512), (128, 896, 512), (200, 100, 130), (65, 33, 1),
-                                           (300, 99, 77), (1, 64, 129), (257, 4864, 64)])
+@pytest.mark.parametrize("out,n_in,rows", [(896, 896, 512), (128, 896, 512), (4864, 896, 512), (896, 4864, 512),
+                                           (200, 100, 130), (65, 33, 1), (300, 99, 77), (1, 64, 129),
+                                           (257, 4864, 64)])
 def test_mfma_gemm_within_tolerance(qt, out, n_in, rows):
     orc, data, scales, x, bias = case(out, n_in, rows, qt, out + 3 * n_in + rows, with_bias=(out % 2 == 0))
     dev = H.Weight.upload(data, scales, out, n_in, qt)
@@ -112,3 +114,34 @@ def test_gemm_group_matches_single_launches():
             assert np.array_equal(got.view(np.uint32), singles[i].view(np.uint32)), (rep, specs[i])
     check(keep[0][2].download(np.float32), *keep[0][4:])
     g.free()
+
+
+def test_c5_grouped_launch_at_its_own_size():
+    """BASELINE.json configs[4] as bench.py times it: the 168 Q8_0 products of
+    24 Qwen2.5-0.5B layers at M = 512 in ONE grouped launch, every layer with
+    its own activations (workloads.PrefillProducts).  Every product equals
+    its own single launch bit for bit; three whole layers (first, middle,
+    last: all seven shapes, incl. gate/up 4864x896 and down 896x4864) are
+    checked against the oracle at 2e-2 and against the bf16 bound."""
+    prods = workloads.PrefillProducts(M=512, layers=24, qt=H.Q8_0)
+    g = H.GemmGroup(prods.items)
+    for y in prods.ys:
+        H.check(H.init().llmi_hip_memset_dev(y.ptr, 0xFF, y.nbytes))  # NaN: every output must be written
+    g.launch()
+    H.synchronize()
+    orc = O.oracle()
+    one = H.DeviceBuffer(max(y.nbytes for y in prods.ys))
+    for i, (w, xp, _, rows) in enumerate(prods.items):
+        got = prods.output(i)
+        w.matmul_mfma_dev(xp, rows, None, one.ptr)
+        H.synchronize()
+        single = one.download(np.float32)[: got.size]
+        assert np.array_equal(got.view(np.uint32), single.view(np.uint32)), prods.spec[i]
+        layer, name, out, n_in, x_seed, w_seed = prods.spec[i]
+        if layer in (0, 11, 23):
+            data, scales = orc.quantize(synth.normal(w_seed, out * n_in, 0.0, 0.02), out, n_in, O.Q8_0)
+            x = synth.normal(x_seed, rows * n_in, 0.0, 1.0)
+            check(got, orc, data, scales, x, None, out, n_in, rows, O.Q8_0)
+    one.free()
+    g.free()
+    prods.free()

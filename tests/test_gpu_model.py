@@ -126,6 +126,13 @@ def test_kv_cache_invariants_and_causality():
             ids = np.array([2, 17, 4, 9, 21, 0, 13], np.int32)
             c1 = m.new_cache(len(ids))
             allpos = m.forward_cached(c1, ids, all_positions=True).reshape(len(ids), -1)
+            # forward() without a cache (the model's own, reused and reset
+            # between calls, also by a longer call in between) gives the same
+            # logits, every time.
+            for rep in range(2):
+                assert np.array_equal(bits(m.forward(ids, all_positions=True)), bits(allpos.reshape(-1))), (arch, rep)
+                assert np.array_equal(bits(m.forward(ids[:4])), bits(allpos[3])), (arch, rep)
+                m.forward(np.arange(40, dtype=np.int32) % cfg["vocab_size"])
             c2 = m.new_cache(len(ids))
             for t, tok in enumerate(ids):
                 assert np.array_equal(bits(m.forward_cached(c2, [tok])), bits(allpos[t])), (arch, qt, t)
@@ -168,8 +175,42 @@ def test_bad_input_is_reported_like_the_reference():
     m.forward_cached(c, [1, 2, 3])
     with pytest.raises(H.HipError, match="max_len must be positive"):
         m.new_cache(0)
+    for bad, msg in (([], "forward: no tokens"), ([32], "forward: token id 32 out of range"),
+                     (list(range(65)), "forward: sequence longer than the model's context")):
+        with pytest.raises(H.HipError, match=msg):
+            m.forward([t % 32 for t in bad] if len(bad) > 1 else bad)
     with pytest.raises(H.HipError):
         H.Model(cfg, synth.make_tensors(cfg, 6, "tiny"), 7)  # not a weight type
+
+
+def test_generation_past_the_context_fails_like_the_reference():
+    """generate_greedy_cached (transformer.cpp:308-327) sizes its cache as
+    min(prompt + max_new, max_position_embeddings) and fails with 'cache is
+    full' at the first step that does not fit.  The tiny model's context is
+    64: a 60-token prompt with 10 new tokens needs 69 positions and must
+    fail (greedy and sampled, with and without stop ids); 5 new tokens need
+    exactly 64 and must succeed, with the same ids as a run that stops
+    early."""
+    cfg = synth.tiny(1, True)
+    assert cfg["max_position_embeddings"] == 64
+    m = H.Model(cfg, synth.make_tensors(cfg, 8, "tiny"), H.Q4_0)
+    prompt = synth.uniform_ids(3, 60, cfg["vocab_size"])
+    with pytest.raises(H.HipError, match="cache is full"):
+        m.generate_greedy(prompt, 10)
+    with pytest.raises(H.HipError, match="cache is full"):
+        m.generate_greedy(prompt, 10, stop_ids=[cfg["vocab_size"] + 5])  # never produced: the host-synced loop
+    targets = np.linspace(0.05, 0.95, 10)
+    with pytest.raises(H.HipError, match="cache is full"):
+        m.generate_sampled(prompt, 10, H.Sampling(0.8, 0, 1.0), targets)
+    ids5 = m.generate_greedy(prompt, 5)
+    assert len(ids5) == 5
+    assert np.array_equal(m.generate_greedy(prompt, 3), ids5[:3])
+    # The model is still usable after the failed calls.
+    c = m.new_cache(64)
+    logits = m.forward_cached(c, prompt)
+    assert int(np.argmax(logits)) == int(ids5[0])
+    c.free()
+    m.free()
 
 
 # ---------------------------------------------------- full-size models

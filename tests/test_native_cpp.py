@@ -1,8 +1,8 @@
 """The C++ host layer (llm-inference-cpp_amd/host: llmi::quant, llmi::Weight,
-llmi::Transformer, llmi::sample with the reference's interface): the tests
-of tests/native/*_gpu_test.cpp mirror the reference's quant_test.cpp,
-transformer_test.cpp and sampling_test.cpp against it.  Building them needs no GPU; running them
-does."""
+llmi::Transformer, llmi::sample with the reference's interface): the
+programs tests/native/host_*_diff.cpp drive it through tables of cases and
+compare every output with the CPU oracle bit for bit.  Building them needs
+no GPU; running them does."""
 
 import os
 import subprocess
@@ -12,7 +12,7 @@ import pytest
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 PKG = os.path.join(ROOT, "llm-inference-cpp_amd")
 NATIVE = os.path.join(ROOT, "tests", "native")
-TESTS = ["quant_gpu_test", "transformer_gpu_test", "sampling_gpu_test"]
+TESTS = ["host_quant_diff", "host_model_diff", "host_sampling_diff"]
 
 
 def build(name, out_dir):
