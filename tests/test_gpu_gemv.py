@@ -92,13 +92,66 @@ def test_multi_row_launch_shapes_match_oracle(qt, out, n_in, rows):
 
 
 @pytest.mark.parametrize("qt", [O.Q8_0, O.Q4_0])
+@pytest.mark.parametrize("out,n_in", [(1, 1536), (15, 1537), (17, 1550), (64, 4864), (100, 4870), (576, 1536),
+                                      (896, 4864), (2000, 3000), (33, 15000)])
+def test_long_row_products_match_oracle(qt, out, n_in):
+    """Batch-1 products on long rows (48 to 469 blocks: the 16-row tiles
+    with many lane groups, or the 64-row tiles with the blocks spread over
+    up to 16 wavefronts): ragged rows and partial final blocks, with and
+    without bias, three calls in a row on different activations."""
+    orc = O.oracle()
+    w = synth.normal(out * 3 + n_in, out * n_in, 0.0, 0.02)
+    data, scales = orc.quantize(w, out, n_in, qt)
+    dev = H.Weight.upload(data, scales, out, n_in, qt)
+    bias = synth.normal(out + 1, out, 0.0, 0.5)
+    for call in range(3):
+        x = synth.normal(call * 101 + n_in, n_in, 0.0, 1.0)
+        b = bias if call != 1 else None
+        got = dev.matmul(x, 1, b)
+        want = orc.matmul(x, 1, n_in, data, scales, qt, out, b)
+        assert np.array_equal(bits(got), bits(want)), (out, n_in, call)
+    dev.free()
+
+
+def test_long_row_products_in_one_group_match_oracle():
+    """A grouped launch holding long-row products next to short-row and
+    multi-row ones: every output equals the oracle's, on two launches of the
+    group."""
+    orc = O.oracle()
+    specs = [(896, 4864, 1, O.Q4_0), (576, 1536, 1, O.Q8_0), (4864, 896, 1, O.Q4_0), (100, 2000, 1, O.Q4_0),
+             (300, 4864, 4, O.Q8_0), (65, 33, 1, O.Q8_0)]
+    keep, items = [], []
+    for i, (out, n_in, rows, qt) in enumerate(specs):
+        w = synth.normal(60 + i, out * n_in, 0.0, 0.02)
+        data, scales = orc.quantize(w, out, n_in, qt)
+        dev = H.Weight.upload(data, scales, out, n_in, qt)
+        xd = H.DeviceBuffer(rows * n_in * 4)
+        yd = H.DeviceBuffer(rows * out * 4)
+        keep.append((dev, xd, yd, rows, n_in, out, data, scales, qt))
+        items.append((dev, xd.ptr, yd.ptr, rows))
+    g = H.Group(items)
+    for rep in range(2):
+        for i, (dev, xd, yd, rows, n_in, out, data, scales, qt) in enumerate(keep):
+            xd.upload(synth.normal(700 + 10 * rep + i, rows * n_in, 0.0, 1.0))
+            yd.upload(np.full(rows * out, np.nan, np.float32))
+        g.launch()
+        H.synchronize()
+        for i, (dev, xd, yd, rows, n_in, out, data, scales, qt) in enumerate(keep):
+            x = synth.normal(700 + 10 * rep + i, rows * n_in, 0.0, 1.0)
+            want = orc.matmul(x, rows, n_in, data, scales, qt, out, None)
+            assert np.array_equal(bits(yd.download(np.float32)), bits(want)), (rep, specs[i])
+    g.free()
+
+
+@pytest.mark.parametrize("qt", [O.Q8_0, O.Q4_0])
 def test_extreme_activations_match_oracle(qt):
     """Subnormal, zero, negative-zero and very large activations: the f16
     code operands of the Q4_0 fused multiply-adds and the Q8_0 conversions
     give the oracle's fp32 results bit for bit in every kernel shape."""
     orc = O.oracle()
     rng = np.random.default_rng(11)
-    for out, n_in, rows in ((200, 576, 1), (4000, 96, 1), (200, 576, 3), (130, 100, 9), (65, 33, 1)):
+    for out, n_in, rows in ((200, 576, 1), (4000, 96, 1), (200, 576, 3), (130, 100, 9), (65, 33, 1),
+                             (130, 4864, 1)):
         w = synth.normal(out + n_in, out * n_in, 0.0, 0.02)
         data, scales = orc.quantize(w, out, n_in, qt)
         dev = H.Weight.upload(data, scales, out, n_in, qt)

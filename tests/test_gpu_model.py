@@ -284,6 +284,33 @@ def test_decode_attention_matches_reference(hidden, heads, kv):
     cm.close()
 
 
+@pytest.mark.parametrize("qt", [H.Q8_0, H.Q4_0])
+@pytest.mark.parametrize("inter", [1536, 1560, 4864])
+def test_decode_long_down_proj_matches_reference(qt, inter):
+    """The one-token step's down_proj on rows of 48 to 152 blocks with
+    SiLU(gate) * up staged by every workgroup (1560: a partial final block
+    of 24 elements); every step's logits equal the reference's bit for
+    bit."""
+    cpu = O.reference() or O.oracle()
+    cfg = dict(arch=1, vocab_size=80, hidden_size=128, intermediate_size=inter, num_layers=2, num_heads=2,
+               num_kv_heads=1, max_position_embeddings=64, rms_norm_eps=1e-6, rope_theta=1e6,
+               tie_word_embeddings=1, qkv_bias=1)
+    tensors = synth.make_tensors(cfg, inter + qt, "bench")
+    gm = H.Model(cfg, tensors, qt)
+    cm = O.CpuModel(cpu, cfg, tensors, qt)
+    ids = synth.uniform_ids(inter, 24, cfg["vocab_size"])
+    cache = gm.new_cache(24)
+    assert cm.new_cache(24)
+    assert np.array_equal(bits(gm.forward_cached(cache, ids[:4])), bits(cm.forward_cached(ids[:4])))
+    for t in range(4, 24):
+        got = gm.forward_cached(cache, ids[t:t + 1])
+        want = cm.forward_cached(ids[t:t + 1])
+        assert np.array_equal(bits(got), bits(want)), (inter, qt, t)
+    cache.free()
+    gm.free()
+    cm.close()
+
+
 # ----------------------------------------------- prefill attention shapes
 @pytest.mark.parametrize("hidden,heads,kv", [(64, 1, 1), (256, 4, 2), (192, 3, 1), (448, 7, 1), (576, 9, 3),
                                              (2048, 32, 1), (1024, 16, 1), (256, 2, 1), (80, 1, 1)])
