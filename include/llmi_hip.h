@@ -211,6 +211,17 @@ void llmi_hip_group_free(llmi_hip_group* group);
  * weight type), e.g. the q/k/v or gate/up products of a layer. */
 int llmi_hip_matmul_mfma_dev(const llmi_hip_weight* weight, const float* x_dev, size_t rows, const float* bias_dev,
                              float* y_dev, void* stream);
+/* llmi_hip_matmul_mfma_dev for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  No counterpart in the reference.  Same kernels and results,
+ * bit for bit; the bf16 copy of x lives in a fixed per-GPU array set up by
+ * llmi_hip_init instead of a buffer the library grows, so the call makes no
+ * allocation.  Limit: rows * (in rounded up to 64) <=
+ * LLMI_MFMA_NOALLOC_MAX_ELEMS (LLMI_ERR_ARG beyond).  Calls that overlap on
+ * one GPU (e.g. on two streams) share that array and race. */
+#define LLMI_MFMA_NOALLOC_MAX_ELEMS 4194304
+int llmi_hip_matmul_mfma_noalloc_dev(const llmi_hip_weight* weight, const float* x_dev, size_t rows,
+                                     const float* bias_dev, float* y_dev, void* stream);
 typedef struct llmi_hip_gemm_group llmi_hip_gemm_group;
 int llmi_hip_gemm_group_create(const llmi_hip_weight* const* w, const float* const* x_dev, const size_t* rows,
                                const float* const* bias_dev, float* const* y_dev, size_t count,

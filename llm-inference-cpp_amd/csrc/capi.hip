@@ -193,6 +193,7 @@ int llmi_hip_init(int device) {
   hipDeviceProp_t prop{};
   LLMI_TRY_HIP(hipGetDeviceProperties(&prop, device));
   g_max_lds = prop.sharedMemPerBlock;
+  if (int rc = noalloc_setup(device)) return rc;
   g_device = device;
   return LLMI_OK;
 }
@@ -622,6 +623,13 @@ int llmi_hip_matmul_mfma_dev(const llmi_hip_weight* weight, const float* x, size
   LLMI_REQUIRE_INIT();
   LLMI_REQUIRE(weight != nullptr, "gemm: null weight");
   return llmi_hip::launch_gemm_single(weight->m, x, rows, bias, y, pick(stream));
+}
+
+int llmi_hip_matmul_mfma_noalloc_dev(const llmi_hip_weight* weight, const float* x, size_t rows, const float* bias,
+                                     float* y, void* stream) {
+  LLMI_REQUIRE_INIT();
+  LLMI_REQUIRE(weight != nullptr, "matmul_mfma_noalloc: null weight");
+  return llmi_hip::launch_gemm_noalloc(g_device, weight->m, x, rows, bias, y, pick(stream));
 }
 
 }  // extern "C"

@@ -159,6 +159,14 @@ int plan_gemm_group(const GroupEntry* entries, std::size_t count, GemmPlan* plan
 // (grown on demand, outside any graph capture).
 int launch_gemm_single(const DeviceMatrix& m, const float* x, std::size_t rows, const float* bias, float* y,
                        hipStream_t s, bool accumulate = false);
+// The allocation-free single-product GEMM (llmi_hip_matmul_mfma_noalloc_dev):
+// noalloc_setup records, with `device` current, the device address of its
+// file-scope scratch array (once per device, from llmi_hip_init);
+// launch_gemm_noalloc runs launch_gemm_single's kernels with x's bf16 copy
+// in that array.
+int noalloc_setup(int device);
+int launch_gemm_noalloc(int device, const DeviceMatrix& m, const float* x, std::size_t rows, const float* bias,
+                        float* y, hipStream_t s);
 // Points every problem at its input's bf16 copy inside `scratch`.
 void bind_gemm_scratch(GemmPlan* plan, std::uint16_t* scratch);
 // Queues the fp32 -> bf16 conversion of every input into `scratch`.

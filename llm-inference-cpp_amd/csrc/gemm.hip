@@ -30,6 +30,7 @@
 // the same XCD (workgroups are dealt to the 8 XCDs round-robin), then finds
 // its product through a work -> product map.
 #include <algorithm>
+#include <string>
 #include <vector>
 
 #include "common.hpp"
@@ -349,6 +350,73 @@ int launch_gemm_inputs(const GemmPlan& plan, std::uint16_t* scratch, hipStream_t
   }
   LLMI_TRY_HIP(hipGetLastError());
   return LLMI_OK;
+}
+
+// ------------------------------------------------- allocation-free launch
+// llmi_hip_matmul_mfma_noalloc_dev keeps the bf16 copy of x in this
+// file-scope device array instead of a buffer the library allocates: every
+// GPU the library runs on holds its own copy until the process ends.  In
+// host code `scratch` is only a symbol; its device address (per GPU) comes
+// from hipGetSymbolAddress at llmi_hip_init and is what kernels are given.
+// Nothing in it needs clearing: x_to_bf16 writes every element a launch
+// reads (rows x ldx, the padding columns as zeros; the GEMM clamps token
+// rows to rows - 1).  Calls that overlap on one GPU share it and race.
+constexpr std::size_t kNoAllocElems = LLMI_MFMA_NOALLOC_MAX_ELEMS;
+static __device__ __align__(256) std::uint16_t scratch[kNoAllocElems];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::uint16_t* g_scratch_dev[kMaxDevices] = {};  // scratch's address on each GPU
+}  // namespace
+
+int noalloc_setup(int device) {
+  LLMI_REQUIRE(device >= 0 && device < kMaxDevices, "llmi_hip_init: device ordinal above the library's limit");
+  if (g_scratch_dev[device] != nullptr) return LLMI_OK;
+  void* ptr = nullptr;
+  LLMI_TRY_HIP(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+  g_scratch_dev[device] = static_cast<std::uint16_t*>(ptr);
+  return LLMI_OK;
+}
+
+int launch_gemm_noalloc(int device, const DeviceMatrix& m, const float* x, std::size_t rows, const float* bias,
+                        float* y, hipStream_t s) {
+  LLMI_REQUIRE(m.type == LLMI_TYPE_Q8_0 || m.type == LLMI_TYPE_Q4_0,
+               "matmul_mfma_noalloc: weight must be Q8_0 or Q4_0");
+  LLMI_REQUIRE(m.in > 0 && m.in <= 0x7FFFFFFFu && m.out <= 0x7FFFFFFFu, "matmul_mfma_noalloc: bad shape");
+  if (rows == 0 || m.out == 0) return LLMI_OK;
+  LLMI_REQUIRE(x != nullptr && y != nullptr, "matmul_mfma_noalloc: null x or y");
+  const std::size_t ldx = gemm_ldx(m.in);
+  LLMI_REQUIRE(rows <= kNoAllocElems / ldx,
+               "matmul_mfma_noalloc: rows x in (rounded up to 64) exceeds the " +
+                   std::to_string(kNoAllocElems) + "-element scratch");
+  LLMI_REQUIRE(device >= 0 && device < kMaxDevices && g_scratch_dev[device] != nullptr,
+               "matmul_mfma_noalloc: scratch not set up on this device");
+  std::uint16_t* xb = g_scratch_dev[device];
+  // The single-product launch of launch_gemm_single, planned on the stack.
+  GemmProblem p{};
+  p.codes = m.codes;
+  p.scales = m.scales;
+  p.xb = xb;
+  p.bias = bias;
+  p.y = y;
+  p.rows = static_cast<int>(rows);
+  p.in = static_cast<int>(m.in);
+  p.ldx = static_cast<int>(ldx);
+  p.out = static_cast<int>(m.out);
+  p.nblk = static_cast<int>(m.nblk);
+  p.ntiles = static_cast<int>(m.ntiles);
+  p.mtiles = static_cast<int>(ceil_div(rows, kBM));
+  p.first_wg = 0;
+  p.input = 0;
+  p.accumulate = 0;
+  GemmLaunch l;
+  l.type = m.type;
+  l.total_wgs = static_cast<int>(static_cast<std::size_t>(p.mtiles) * ceil_div(m.out, kBN));
+  const std::size_t quads = rows * (ldx / 4);
+  const unsigned blocks = static_cast<unsigned>(std::min<std::size_t>(ceil_div(quads, 256), 4096));
+  x_to_bf16<<<blocks, 256, 0, s>>>(x, xb, static_cast<int>(rows), static_cast<int>(m.in), static_cast<int>(ldx));
+  LLMI_TRY_HIP(hipGetLastError());
+  return launch_gemm(nullptr, nullptr, l, s, &p);
 }
 
 int launch_gemm(const GemmProblem* probs_dev, const std::uint32_t* map_dev, const GemmLaunch& l, hipStream_t s,

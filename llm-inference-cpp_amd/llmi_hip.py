@@ -86,6 +86,7 @@ SIGNATURES = {
     "llmi_hip_model_forward_cached": (_i, [_vp, _vp, _vp, _sz, _i, _vp]),
     "llmi_hip_model_forward_cached_trace": (_i, [_vp, _vp, _vp, _sz, _i, _vp, _vp]),
     "llmi_hip_model_forward": (_i, [_vp, _vp, _sz, _i, _vp, _vp]),
+    "llmi_hip_matmul_mfma_noalloc_dev": (_i, [_vp, _vp, _sz, _vp, _vp, _vp]),
     "llmi_hip_model_generate_greedy": (_i, [_vp, _vp, _sz, _sz, _vp, _sz, _vp, C.POINTER(_sz)]),
     "llmi_hip_model_last_timing": (_i, [_vp, C.POINTER(_d), C.POINTER(_d)]),
     "llmi_hip_sample": (_i, [_vp, _sz, _vp, _d, C.POINTER(C.c_int32)]),
