@@ -281,21 +281,35 @@ __device__ __forceinline__ void block_sums(const GMEM uint4* __restrict__ codes,
 }
 
 // The sequential chain over all blocks of one row of a tile, from LDS
-// (stride `stride` floats between blocks).
+// (stride `stride` floats between blocks).  The reads run a round ahead of
+// the fused multiply-adds (kChainRound blocks per round; indices past the
+// last block are clamped to it and their values unused), so the LDS latency
+// is paid once, not once per block.
+constexpr int kChainRound = 8;
 __device__ __forceinline__ float chain_lds(const float* part, const float* scl, int nblk, int lane, int stride) {
   float acc = 0.0f;
-  int b = 0;
-  for (; b + 4 <= nblk; b += 4) {
-    const float p0 = part[(b + 0) * stride + lane], s0 = scl[(b + 0) * stride + lane];
-    const float p1 = part[(b + 1) * stride + lane], s1 = scl[(b + 1) * stride + lane];
-    const float p2 = part[(b + 2) * stride + lane], s2 = scl[(b + 2) * stride + lane];
-    const float p3 = part[(b + 3) * stride + lane], s3 = scl[(b + 3) * stride + lane];
-    acc = __builtin_fmaf(p0, s0, acc);
-    acc = __builtin_fmaf(p1, s1, acc);
-    acc = __builtin_fmaf(p2, s2, acc);
-    acc = __builtin_fmaf(p3, s3, acc);
+  float p[kChainRound], s[kChainRound];
+  const auto read = [&](int b0, float* pp, float* ss) {
+#pragma unroll
+    for (int u = 0; u < kChainRound; ++u) {
+      const int b = min(b0 + u, nblk - 1);
+      pp[u] = part[b * stride + lane];
+      ss[u] = scl[b * stride + lane];
+    }
+  };
+  read(0, p, s);
+  for (int b = 0; b < nblk; b += kChainRound) {
+    float pn[kChainRound], sn[kChainRound];
+    read(b + kChainRound < nblk ? b + kChainRound : b, pn, sn);
+#pragma unroll
+    for (int u = 0; u < kChainRound; ++u)
+      if (b + u < nblk) acc = __builtin_fmaf(p[u], s[u], acc);
+#pragma unroll
+    for (int u = 0; u < kChainRound; ++u) {
+      p[u] = pn[u];
+      s[u] = sn[u];
+    }
   }
-  for (; b < nblk; ++b) acc = __builtin_fmaf(part[b * stride + lane], scl[b * stride + lane], acc);
   return acc;
 }
 
@@ -389,11 +403,18 @@ __device__ __forceinline__ void stage_x(const GMEM float* __restrict__ x, int in
   part = row_sum16_f64(part);
   if ((tid & 15) == 15) red[tid >> 4] = part;
   __syncthreads();
-  double ss = 0.0;
-  for (int r = 0; r < (nthreads >> 4); ++r) ss += red[r];
+  // Every wave sums the (up to 64) row partials with its lanes, as a tree,
+  // and evaluates the three scales of the bound check -- at ss - slack, ss
+  // and ss + slack -- on lanes 0, 1 and 2 at once (one double division and
+  // square root deep, not three).
+  const int lane = tid & 63;
+  double rs = lane < (nthreads >> 4) ? red[lane] : 0.0;
+  rs = row_sum16_f64(rs);
+  const double ss = (readlane_f64(rs, 15) + readlane_f64(rs, 31)) + (readlane_f64(rs, 47) + readlane_f64(rs, 63));
   const double slack = sum_slack(in) * ss;
-  float sc = rms_scale(ss, in, eps);
-  if (rms_scale(ss - slack, in, eps) != rms_scale(ss + slack, in, eps)) {
+  const float mine = rms_scale(lane == 0 ? ss - slack : lane == 2 ? ss + slack : ss, in, eps);
+  float sc = readlane_f32(mine, 1);
+  if (readlane_f32(mine, 0) != readlane_f32(mine, 2)) {
     double seq = 0.0;  // every x is in LDS (the barrier above)
     for (int i = 0; i < in; ++i) {
       const double d = static_cast<double>(xs[i]);
@@ -421,22 +442,29 @@ __device__ __forceinline__ void stage_x(const GMEM float* __restrict__ x, int in
 __host__ __device__ __forceinline__ int pair_stride(int nblk) { return 2 * ((nblk + 15) & ~15) + 4; }
 
 // The sequential chain over the (block sum, scale) pairs of one row, two
-// blocks per 16-byte LDS read, eight reads issued per round.
+// blocks per 16-byte LDS read, eight reads (16 blocks) per round, the next
+// round's reads issued before this round's fused multiply-adds.  The row
+// holds nblk rounded up to 16 pairs (pair_stride), so a round's reads stay
+// inside it; pairs past nblk are read but not used.
 __device__ __forceinline__ float chain_pairs(const float* row, int nblk) {
   const float4* pr = reinterpret_cast<const float4*>(row);
   float acc = 0.0f;
-  int b = 0;
-  for (; b + 16 <= nblk; b += 16) {
-    float4 a[8];
+  float4 a[8];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) a[u] = pr[b / 2 + u];
+  for (int u = 0; u < 8; ++u) a[u] = pr[u];
+  for (int b = 0; b < nblk; b += 16) {
+    float4 n[8];
+    const int q = b + 16 < nblk ? (b + 16) / 2 : b / 2;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) n[u] = pr[q + u];
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
-      acc = __builtin_fmaf(a[u].x, a[u].y, acc);
-      acc = __builtin_fmaf(a[u].z, a[u].w, acc);
+      if (b + 2 * u < nblk) acc = __builtin_fmaf(a[u].x, a[u].y, acc);
+      if (b + 2 * u + 1 < nblk) acc = __builtin_fmaf(a[u].z, a[u].w, acc);
     }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) a[u] = n[u];
   }
-  for (; b < nblk; ++b) acc = __builtin_fmaf(row[2 * b], row[2 * b + 1], acc);
   return acc;
 }
 

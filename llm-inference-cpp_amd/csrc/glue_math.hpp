@@ -56,6 +56,17 @@ __device__ __forceinline__ float ref_dot_rest(const float* __restrict__ a, const
   return ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7])) + tail;
 }
 
+// The value of lane l of the wavefront (l uniform), broadcast to every lane.
+__device__ __forceinline__ float readlane_f32(float v, int l) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+__device__ __forceinline__ double readlane_f64(double v, int l) {
+  const std::uint64_t u = __builtin_bit_cast(std::uint64_t, v);
+  const std::uint32_t lo = static_cast<std::uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(u), l));
+  const std::uint32_t hi = static_cast<std::uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(u >> 32), l));
+  return __builtin_bit_cast(double, (static_cast<std::uint64_t>(hi) << 32) | lo);
+}
+
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));

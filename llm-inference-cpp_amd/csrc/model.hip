@@ -782,12 +782,17 @@ __global__ void __launch_bounds__(kThreads) attn_pv_1(const float* __restrict__ 
   part = row_sum16_f64(part);
   if ((tid & 15) == 15) red_d[tid >> 4] = part;
   __syncthreads();  // red_d and every e in p
-  double sum = red_d[0];
-#pragma unroll
-  for (int r = 1; r < kRows; ++r) sum = sum + red_d[r];
+  // The row partials summed by each wave's lanes as a tree, and the three
+  // reciprocals of the bound check (sum - slack, sum, sum + slack) on lanes
+  // 0, 1, 2 at once.
+  const int lane = tid & 63;
+  double rs = lane < kRows ? red_d[lane] : 0.0;
+  rs = row_sum16_f64(rs);
+  const double sum = readlane_f64(rs, 15);
   const double slack = sum_slack(npos) * sum;
-  float inv = recip_float(sum);
-  if (recip_float(sum - slack) != recip_float(sum + slack)) {
+  const float mine = recip_float(lane == 0 ? sum - slack : lane == 2 ? sum + slack : sum);
+  float inv = readlane_f32(mine, 1);
+  if (readlane_f32(mine, 0) != readlane_f32(mine, 2)) {
     double seq = 0.0;
     for (int sp = 0; sp < npos; ++sp) seq += static_cast<double>(p[sp]);
     inv = recip_float(seq);
