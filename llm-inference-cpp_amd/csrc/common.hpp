@@ -104,7 +104,7 @@ struct GroupEntry {
 // chunk `rchunk` (GroupProblem::kNarrow: the 16-row tiles), at
 // probs[prob_offset...], workgroup w running product wg_prob[map_offset + w].
 struct GroupLaunch {
-  int type = 0, rchunk = 1, waves = 1, total_wgs = 0;
+  int type = 0, rchunk = 1, waves = 1, total_wgs = 0, nprob = 0;
   std::size_t lds = 0, prob_offset = 0, map_offset = 0;
 };
 struct GroupPlan {
@@ -121,6 +121,7 @@ struct DeviceGroup {
   const GroupProblem* probs = nullptr;
   const std::uint32_t* map = nullptr;
   std::vector<GroupLaunch> launches;
+  std::vector<GroupProblem> host_probs;  // the table's host copy (few-product launches pass them by value)
   int build(const GroupEntry* entries, std::size_t count);
   int launch(hipStream_t s) const;
   void release();

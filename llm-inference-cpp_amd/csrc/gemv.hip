@@ -603,6 +603,31 @@ __global__ void __launch_bounds__(1024) qgemv_group_narrow(const GroupProblem* _
                     reinterpret_cast<float*>(lds4), p.prologue, gmem(p.pw), p.eps);
 }
 
+// The same 16-row tiles for a launch of at most kFewProblems products whose
+// descriptors travel as kernel arguments: the kernel starts without the two
+// dependent memory reads (workgroup -> product, then the product) of the
+// table-driven launch, which sit in front of every load of the one-token
+// step's short kernels.
+constexpr int kFewProblems = 3;
+struct FewProblems {
+  GroupProblem p[kFewProblems];
+  int count;
+};
+template <int TYPE>
+__global__ void __launch_bounds__(1024) qgemv_few_narrow(FewProblems f) {
+  extern __shared__ float4 lds4[];
+  const int wg = blockIdx.x;
+  // The product by comparisons (uniform), each field by selects, so the
+  // argument block is never indexed dynamically.
+  const int i = (f.count > 2 && wg >= f.p[2].first_wg) ? 2 : (f.count > 1 && wg >= f.p[1].first_wg) ? 1 : 0;
+#define LLMI_PICK(fld) (i == 2 ? f.p[2].fld : i == 1 ? f.p[1].fld : f.p[0].fld)
+  narrow_tile<TYPE>(gmem(reinterpret_cast<const uint4*>(LLMI_PICK(codes))), gmem(LLMI_PICK(scales)), gmem(LLMI_PICK(x)),
+                    gmem(LLMI_PICK(bias)), gmem_out(LLMI_PICK(y)), LLMI_PICK(in), LLMI_PICK(nblk), LLMI_PICK(out),
+                    LLMI_PICK(bpw), LLMI_PICK(accumulate), wg - LLMI_PICK(first_wg), reinterpret_cast<float*>(lds4),
+                    LLMI_PICK(prologue), gmem(LLMI_PICK(pw)), LLMI_PICK(eps));
+#undef LLMI_PICK
+}
+
 // ------------------------------------------------------------ batch > 8
 // The exact multi-row product on many tiles: one workgroup per MR = 64
 // input rows x one 64-row tile of the matrix (64 outputs).  Per quantization
@@ -1400,6 +1425,7 @@ int plan_group(const GroupEntry* entries, std::size_t count, GroupPlan* plan) {
     }
     LLMI_REQUIRE(l.lds <= max_lds_per_block(), "group: a product needs more LDS than one workgroup may use");
     l.total_wgs = static_cast<int>(wg);
+    l.nprob = static_cast<int>(probs.size());
     plan->probs.insert(plan->probs.end(), probs.begin(), probs.end());
     plan->launches.push_back(l);
   }
@@ -1438,6 +1464,7 @@ int DeviceGroup::build(const GroupEntry* entries, std::size_t count) {
   GroupPlan plan;
   if (int rc = plan_group(entries, count, &plan)) return rc;
   launches = plan.launches;
+  host_probs = plan.probs;
   const std::size_t pbytes = plan.probs.size() * sizeof(GroupProblem);
   const std::size_t mbytes = plan.wg_prob.size() * sizeof(std::uint32_t);
   if (pbytes + mbytes == 0) return LLMI_OK;
@@ -1451,8 +1478,20 @@ int DeviceGroup::build(const GroupEntry* entries, std::size_t count) {
 }
 
 int DeviceGroup::launch(hipStream_t s) const {
-  for (const GroupLaunch& l : launches)
+  for (const GroupLaunch& l : launches) {
+    if (l.rchunk == GroupProblem::kNarrow && l.nprob >= 1 && l.nprob <= kFewProblems && l.total_wgs > 0) {
+      // Few products: descriptors by value (qgemv_few_narrow).
+      FewProblems f{};
+      f.count = l.nprob;
+      for (int k = 0; k < l.nprob; ++k) f.p[k] = host_probs[l.prob_offset + static_cast<std::size_t>(k)];
+      const dim3 grid(static_cast<unsigned>(l.total_wgs)), block(static_cast<unsigned>(l.waves * 64));
+      if (l.type == LLMI_TYPE_Q8_0) qgemv_few_narrow<LLMI_TYPE_Q8_0><<<grid, block, l.lds, s>>>(f);
+      else qgemv_few_narrow<LLMI_TYPE_Q4_0><<<grid, block, l.lds, s>>>(f);
+      LLMI_TRY_HIP(hipGetLastError());
+      continue;
+    }
     if (int rc = launch_group(probs, map, l, s)) return rc;
+  }
   return LLMI_OK;
 }
 
@@ -1462,6 +1501,7 @@ void DeviceGroup::release() {
   probs = nullptr;
   map = nullptr;
   launches.clear();
+  host_probs.clear();
 }
 
 }  // namespace llmi_hip
