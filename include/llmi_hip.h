@@ -208,18 +208,27 @@ void llmi_hip_group_free(llmi_hip_group* group);
  * (typically ~1e-3).  Use llmi_hip_matmul_dev where the reference's exact
  * results are needed.  Any rows >= 1; efficient for rows >= 64.
  * llmi_hip_gemm_group_* run a list of such products as one launch (per
- * weight type), e.g. the q/k/v or gate/up products of a layer. */
+ * weight type), e.g. the q/k/v or gate/up products of a layer.  A launch of
+ * fewer than 256 output tiles (128 x 256) splits the K of products with
+ * more than 1536 inputs over several workgroups and sums their fp32 partials
+ * in a second kernel, so a product's results can differ in the last bits
+ * between a launch that splits it and one that does not. */
 int llmi_hip_matmul_mfma_dev(const llmi_hip_weight* weight, const float* x_dev, size_t rows, const float* bias_dev,
                              float* y_dev, void* stream);
 /* llmi_hip_matmul_mfma_dev for callers that cannot allocate device memory
  * (code under HIP graph capture, tight serving loops, harnesses that forbid
  * hipMalloc).  No counterpart in the reference.  Same kernels and results,
- * bit for bit; the bf16 copy of x lives in a fixed per-GPU array set up by
- * llmi_hip_init instead of a buffer the library grows, so the call makes no
- * allocation.  Limit: rows * (in rounded up to 64) <=
- * LLMI_MFMA_NOALLOC_MAX_ELEMS (LLMI_ERR_ARG beyond).  Calls that overlap on
- * one GPU (e.g. on two streams) share that array and race. */
-#define LLMI_MFMA_NOALLOC_MAX_ELEMS 4194304
+ * bit for bit; the GEMM's scratch -- the bf16 copy of x and, for a product
+ * whose K is split over several workgroups (more than 1536 inputs on fewer
+ * than 256 output tiles of 128 x 256, as llmi_hip_matmul_mfma_dev splits
+ * it), its fp32 partial sums -- lives in a
+ * fixed per-GPU array set up by llmi_hip_init instead of a buffer the
+ * library grows, so the call makes no allocation.  Limit: 2 * rows * (in
+ * rounded up to 64), rounded up to 256, plus 4 * rows * out * ceil(ceil(in /
+ * 64) / 16) when K is split, at most LLMI_MFMA_NOALLOC_SCRATCH_BYTES
+ * (LLMI_ERR_ARG beyond; e.g. 512 rows of 896 x 4864 need 14.1 MB).  Calls
+ * that overlap on one GPU (e.g. on two streams) share that array and race. */
+#define LLMI_MFMA_NOALLOC_SCRATCH_BYTES 33554432
 int llmi_hip_matmul_mfma_noalloc_dev(const llmi_hip_weight* weight, const float* x_dev, size_t rows,
                                      const float* bias_dev, float* y_dev, void* stream);
 typedef struct llmi_hip_gemm_group llmi_hip_gemm_group;

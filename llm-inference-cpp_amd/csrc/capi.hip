@@ -113,13 +113,13 @@ int launch_gemm_single(const DeviceMatrix& m, const float* x, std::size_t rows, 
   const GroupEntry e{&m, x, bias, y, rows, accumulate};
   GemmPlan plan;
   if (int rc = plan_gemm_group(&e, 1, &plan)) return rc;
-  if (int rc = g_gemm_scratch.reserve(plan.scratch_elems * sizeof(std::uint16_t), s)) return rc;
+  if (int rc = g_gemm_scratch.reserve(gemm_scratch_bytes(plan), s)) return rc;
   auto* scratch = static_cast<std::uint16_t*>(g_gemm_scratch.p);
   bind_gemm_scratch(&plan, scratch);
   if (int rc = launch_gemm_inputs(plan, scratch, s)) return rc;
   for (const GemmLaunch& l : plan.launches)
     if (int rc = launch_gemm(nullptr, nullptr, l, s, &plan.probs[l.prob_offset])) return rc;
-  return LLMI_OK;
+  return launch_gemm_reduces(plan, s);
 }
 
 }  // namespace llmi_hip
@@ -598,8 +598,8 @@ int llmi_hip_gemm_group_create(const llmi_hip_weight* const* w, const float* con
   if (int rc = group_entries(w, x, rows, bias, y, count, 0, &entries)) return rc;
   auto g = std::make_unique<llmi_hip_gemm_group>();
   if (int rc = plan_gemm_group(entries.data(), count, &g->plan)) return rc;
-  if (g->plan.scratch_elems > 0) {
-    LLMI_TRY_HIP(hipMalloc(reinterpret_cast<void**>(&g->scratch), g->plan.scratch_elems * sizeof(std::uint16_t)));
+  if (gemm_scratch_bytes(g->plan) > 0) {
+    LLMI_TRY_HIP(hipMalloc(reinterpret_cast<void**>(&g->scratch), gemm_scratch_bytes(g->plan)));
     bind_gemm_scratch(&g->plan, g->scratch);
   }
   if (int rc = upload_plan(g->plan, g->plan.probs, g->plan.work_prob, g.get())) return rc;
@@ -613,7 +613,7 @@ int llmi_hip_gemm_group_launch(const llmi_hip_gemm_group* g, void* stream) {
   if (int rc = launch_gemm_inputs(g->plan, g->scratch, pick(stream))) return rc;
   for (const GemmLaunch& l : g->plan.launches)
     if (int rc = launch_gemm(g->probs, g->map, l, pick(stream))) return rc;
-  return LLMI_OK;
+  return launch_gemm_reduces(g->plan, pick(stream));
 }
 
 void llmi_hip_gemm_group_free(llmi_hip_gemm_group* g) { delete g; }

@@ -137,7 +137,25 @@ struct GemmProblem {
   float* y;
   int rows, in, ldx, out, nblk, ntiles, mtiles, first_wg, input;
   int accumulate;  // y += acc + bias (the residual update), else y = acc + bias
+  // Split K: kchunks workgroups per output tile, each over kpc K-steps of 64,
+  // write fp32 partial tiles to part ([kchunks][rows][out]); gemm_reduce then
+  // sums them in chunk order and applies bias / accumulate.  kchunks == 1:
+  // the workgroup writes y itself.
+  int kchunks, kpc;
+  float* part;
 };
+// K chunks of a product with `in` inputs on a GEMM launch of `launch_tiles`
+// output tiles (128 x 256): long K (more than 24 steps of 64) on a launch of
+// fewer than 256 tiles -- fewer than one workgroup per CU -- is split into
+// chunks of about 16 steps, so one long product does not leave the K loop
+// of a few workgroups as the launch's critical path; launches with enough
+// tiles are not split (the partial sums would only add traffic).  The split
+// changes the fp32 summation order, so a product's bits depend on whether
+// its launch splits it.
+int gemm_kchunks(std::size_t in, std::size_t launch_tiles);
+std::size_t gemm_tiles(std::size_t rows, std::size_t out);
+// fp32 partials a split product needs (0 when it is not split).
+std::size_t gemm_part_floats(std::size_t rows, std::size_t in, std::size_t out, std::size_t launch_tiles);
 // A distinct fp32 activation matrix of a GEMM group and where its bf16 copy
 // lives in the group's scratch (element offset).
 struct GemmInput {
@@ -154,7 +172,12 @@ struct GemmPlan {
   std::vector<GemmLaunch> launches;
   std::vector<GemmInput> inputs;
   std::size_t scratch_elems = 0;  // bf16 elements of scratch the inputs need
+  std::vector<std::size_t> part_off;  // per problem: float offset of its partials (split problems)
+  std::size_t part_floats = 0;        // fp32 partials the split problems need
 };
+// Bytes of a plan's scratch: the bf16 inputs, then (256-byte aligned) the
+// fp32 partials.
+std::size_t gemm_scratch_bytes(const GemmPlan& plan);
 int plan_gemm_group(const GroupEntry* entries, std::size_t count, GemmPlan* plan);
 // One product on the bf16-MFMA GEMM, with the library's bf16 staging buffer
 // (grown on demand, outside any graph capture).
@@ -168,8 +191,11 @@ int launch_gemm_single(const DeviceMatrix& m, const float* x, std::size_t rows, 
 int noalloc_setup(int device);
 int launch_gemm_noalloc(int device, const DeviceMatrix& m, const float* x, std::size_t rows, const float* bias,
                         float* y, hipStream_t s);
-// Points every problem at its input's bf16 copy inside `scratch`.
+// Points every problem at its input's bf16 copy inside `scratch` and its
+// partials after them (gemm_scratch_bytes bytes in all).
 void bind_gemm_scratch(GemmPlan* plan, std::uint16_t* scratch);
+// The reduction of every split problem of a plan (after its GEMM launches).
+int launch_gemm_reduces(const GemmPlan& plan, hipStream_t s);
 // Queues the fp32 -> bf16 conversion of every input into `scratch`.
 int launch_gemm_inputs(const GemmPlan& plan, std::uint16_t* scratch, hipStream_t s);
 // one != nullptr: launch the single product *one (plan of one entry) without

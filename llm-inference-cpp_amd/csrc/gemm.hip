@@ -80,6 +80,48 @@ __global__ void __launch_bounds__(256) x_to_bf16(const float* __restrict__ x, st
   }
 }
 
+// Up to kConvBatch activation matrices converted by one x_to_bf16_batch
+// launch: input i covers quads [qend[i-1], qend[i]) of the launch's range.
+constexpr int kConvBatch = 8;
+struct ConvBatch {
+  const float* x[kConvBatch];
+  std::uint16_t* xb[kConvBatch];
+  int in[kConvBatch], ldx[kConvBatch];
+  unsigned long long qend[kConvBatch];
+  int n;
+};
+__global__ void __launch_bounds__(256) x_to_bf16_batch(ConvBatch c) {
+  const unsigned long long total = c.qend[c.n - 1];
+  for (unsigned long long q = static_cast<unsigned long long>(blockIdx.x) * blockDim.x + threadIdx.x; q < total;
+       q += static_cast<unsigned long long>(gridDim.x) * blockDim.x) {
+    int i = 0;
+#pragma unroll
+    for (int k = 0; k < kConvBatch - 1; ++k)
+      if (k < c.n - 1 && q >= c.qend[k]) i = k + 1;
+    const unsigned long long q0 = i == 0 ? 0ull : c.qend[i - 1];
+    // Select this input's fields without indexing the argument block.
+    const float* x = c.x[0];
+    std::uint16_t* xb = c.xb[0];
+    int in = c.in[0], ldx = c.ldx[0];
+#pragma unroll
+    for (int k = 1; k < kConvBatch; ++k)
+      if (i == k) {
+        x = c.x[k];
+        xb = c.xb[k];
+        in = c.in[k];
+        ldx = c.ldx[k];
+      }
+    const unsigned long long lq = q - q0;
+    const std::size_t r = lq / (ldx / 4);
+    const int k0 = static_cast<int>(lq % (ldx / 4)) * 4;
+    const float* src = x + r * in + k0;
+    float v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) v[u] = k0 + u < in ? src[u] : 0.0f;
+    *reinterpret_cast<uint2*>(xb + r * ldx + k0) = make_uint2(pack_bf16(v[0], v[1]), pack_bf16(v[2], v[3]));
+  }
+}
+
 // Raw data of one K-step held by one producer thread: 32 activations (bf16)
 // of row pt/2, columns 32*(pt%2)..+31, and the codes + scales of weight row
 // pt's two quantization blocks; live[h]: block h exists (else its scale
@@ -115,10 +157,15 @@ __global__ void __launch_bounds__(kGemmThreads) qgemm_mfma(const GemmProblem* __
   GemmProblem p = one;
   if (probs != nullptr) p = probs[__builtin_amdgcn_readfirstlane(static_cast<int>(work_prob[work]))];
   const int local = work - p.first_wg;
-  const int mt = local % p.mtiles, nt = local / p.mtiles;
+  // Consecutive work items: the token tiles of one (weight tile, K chunk).
+  const int mt = local % p.mtiles, rest = local / p.mtiles;
+  const int kc = rest % p.kchunks, nt = rest / p.kchunks;
   const int m0 = mt * kBM, n0 = nt * kBN;
   const int M = p.rows, N = p.out, nblk = p.nblk, ldx = p.ldx;
-  const int nk = (p.in + kBK - 1) / kBK;
+  // This workgroup's K-steps of 64: [kb, kb + nk) of the product's.
+  const int nk_all = (p.in + kBK - 1) / kBK;
+  const int kb = kc * p.kpc;
+  const int nk = min(p.kpc, nk_all - kb);
 
   const int t = threadIdx.x;
   const int lane = t & 63;
@@ -138,8 +185,8 @@ __global__ void __launch_bounds__(kGemmThreads) qgemm_mfma(const GemmProblem* __
     const int wrow = min(n0 + pt, p.ntiles * kTileRows - 1);
     const int wtile = wrow / kTileRows, wlane = wrow % kTileRows;
     const std::size_t xbase = (static_cast<std::size_t>(min(m0 + xr, M - 1)) * ldx + xh * 32) / 8;
-    const auto gload = [&](Stage<TYPE>& st, int k) {
-      k = min(k, nk - 1);  // the ring's prefetch past the last step re-reads it
+    const auto gload = [&](Stage<TYPE>& st, int j) {
+      const int k = kb + min(j, nk - 1);  // the ring's prefetch past the last step re-reads it
 #pragma unroll
       for (int u = 0; u < 4; ++u) st.x[u] = xb[xbase + static_cast<std::size_t>(k) * (kBK / 8) + u];
 #pragma unroll
@@ -231,6 +278,23 @@ __global__ void __launch_bounds__(kGemmThreads) qgemm_mfma(const GemmProblem* __
   }
 
   // acc[i][j][q]: token m0 + wm0 + 16i + 4*(lane/16) + q, output n0 + wn0 + 16j + lane%16.
+  if (p.kchunks > 1) {
+    // A K chunk: the partial tile as it is (gemm_reduce adds the rest).
+    GMEM float* part = (GMEM float*)(p.part + static_cast<std::size_t>(kc) * M * N);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int n = n0 + wn0 + 16 * j + (lane & 15);
+      if (n >= N) continue;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int m = m0 + wm0 + 16 * i + 4 * (lane >> 4) + q;
+          if (m < M) part[static_cast<std::size_t>(m) * N + n] = acc[i][j][q];
+        }
+    }
+    return;
+  }
   // With accumulate, a column's 16 old values are loaded together (clamped
   // rows, no branch) before any is used, so their latencies overlap.
   GMEM float* y = (GMEM float*)p.y;
@@ -263,7 +327,45 @@ __global__ void __launch_bounds__(kGemmThreads) qgemm_mfma(const GemmProblem* __
   }
 }
 
+// y = (part_0 + part_1 + ... in chunk order) + bias (+ the old y with
+// accumulate): the epilogue of a split product, one thread per output.
+__global__ void __launch_bounds__(256) gemm_reduce(const float* __restrict__ part, int kchunks, int rows, int out,
+                                                   const float* __restrict__ bias, float* __restrict__ y,
+                                                   int accumulate) {
+  const std::size_t n_all = static_cast<std::size_t>(rows) * out;
+  const std::size_t stride = n_all;
+  for (std::size_t i = static_cast<std::size_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n_all;
+       i += static_cast<std::size_t>(gridDim.x) * blockDim.x) {
+    float v[16];
+    const int kc = min(kchunks, 16);
+#pragma unroll
+    for (int c = 0; c < 16; ++c)
+      if (c < kc) v[c] = part[c * stride + i];
+    float sum = v[0];
+#pragma unroll
+    for (int c = 1; c < 16; ++c)
+      if (c < kc) sum = sum + v[c];
+    for (int c = 16; c < kchunks; ++c) sum = sum + part[c * stride + i];
+    const float add = bias != nullptr ? bias[i % out] : 0.0f;
+    const float val = sum + add;
+    y[i] = accumulate ? y[i] + val : val;
+  }
+}
+
 }  // namespace
+
+int gemm_kchunks(std::size_t in, std::size_t launch_tiles) {
+  const std::size_t nk = (in + kBK - 1) / kBK;
+  if (nk <= 24 || launch_tiles >= 256) return 1;
+  return static_cast<int>(ceil_div(nk, 16));
+}
+
+std::size_t gemm_tiles(std::size_t rows, std::size_t out) { return ceil_div(rows, kBM) * ceil_div(out, kBN); }
+
+std::size_t gemm_part_floats(std::size_t rows, std::size_t in, std::size_t out, std::size_t launch_tiles) {
+  const int kc = gemm_kchunks(in, launch_tiles);
+  return kc > 1 ? static_cast<std::size_t>(kc) * rows * out : 0;
+}
 
 std::size_t gemm_ldx(std::size_t in) { return (in + kBK - 1) / kBK * kBK; }
 
@@ -296,6 +398,11 @@ int plan_gemm_group(const GroupEntry* entries, std::size_t count, GemmPlan* plan
       plan->inputs.push_back(in);
     }
   }
+  // Output tiles of each launch (one per weight type), for the K split.
+  std::size_t launch_tiles[3] = {0, 0, 0};
+  for (std::size_t i = 0; i < count; ++i)
+    if (entries[i].rows > 0 && entries[i].m->out > 0)
+      launch_tiles[entries[i].m->type] += gemm_tiles(entries[i].rows, entries[i].m->out);
   for (int type : {LLMI_TYPE_Q8_0, LLMI_TYPE_Q4_0}) {
     GemmLaunch l;
     l.type = type;
@@ -319,11 +426,16 @@ int plan_gemm_group(const GroupEntry* entries, std::size_t count, GemmPlan* plan
       p.ntiles = static_cast<int>(m.ntiles);
       p.mtiles = static_cast<int>(ceil_div(e.rows, kBM));
       p.accumulate = e.accumulate ? 1 : 0;
+      p.kchunks = gemm_kchunks(m.in, launch_tiles[type]);
+      p.kpc = static_cast<int>(ceil_div(ceil_div(m.in, kBK), static_cast<std::size_t>(p.kchunks)));
+      p.part = nullptr;
+      plan->part_off.push_back(plan->part_floats);
+      plan->part_floats += gemm_part_floats(e.rows, m.in, m.out, launch_tiles[type]);
       for (std::size_t j = 0; j < plan->inputs.size(); ++j)
         if (plan->inputs[j].x == e.x) p.input = static_cast<int>(j);
       const std::size_t ntiles_n = ceil_div(m.out, kBN);
       p.first_wg = static_cast<int>(wg);
-      const std::size_t wgs = static_cast<std::size_t>(p.mtiles) * ntiles_n;
+      const std::size_t wgs = static_cast<std::size_t>(p.mtiles) * ntiles_n * static_cast<std::size_t>(p.kchunks);
       wg += wgs;
       LLMI_REQUIRE(wg <= 0x7FFFFFFFu, "gemm: too many workgroups");
       plan->work_prob.insert(plan->work_prob.end(), wgs, static_cast<std::uint32_t>(nprob));
@@ -337,16 +449,50 @@ int plan_gemm_group(const GroupEntry* entries, std::size_t count, GemmPlan* plan
   return LLMI_OK;
 }
 
+std::size_t gemm_scratch_bytes(const GemmPlan& plan) {
+  const std::size_t xbytes = (plan.scratch_elems * sizeof(std::uint16_t) + 255) / 256 * 256;
+  return xbytes + plan.part_floats * sizeof(float);
+}
+
 void bind_gemm_scratch(GemmPlan* plan, std::uint16_t* scratch) {
-  for (GemmProblem& p : plan->probs) p.xb = scratch + plan->inputs[p.input].offset;
+  const std::size_t xbytes = (plan->scratch_elems * sizeof(std::uint16_t) + 255) / 256 * 256;
+  float* parts = reinterpret_cast<float*>(reinterpret_cast<std::uint8_t*>(scratch) + xbytes);
+  for (std::size_t i = 0; i < plan->probs.size(); ++i) {
+    GemmProblem& p = plan->probs[i];
+    p.xb = scratch + plan->inputs[p.input].offset;
+    p.part = p.kchunks > 1 ? parts + plan->part_off[i] : nullptr;
+  }
+}
+
+int launch_gemm_reduces(const GemmPlan& plan, hipStream_t s) {
+  for (const GemmProblem& p : plan.probs) {
+    if (p.kchunks <= 1) continue;
+    const std::size_t n = static_cast<std::size_t>(p.rows) * p.out;
+    const unsigned blocks = static_cast<unsigned>(std::min<std::size_t>(ceil_div(n, 256), 8192));
+    gemm_reduce<<<blocks, 256, 0, s>>>(p.part, p.kchunks, p.rows, p.out, p.bias, p.y, p.accumulate);
+  }
+  LLMI_TRY_HIP(hipGetLastError());
+  return LLMI_OK;
 }
 
 int launch_gemm_inputs(const GemmPlan& plan, std::uint16_t* scratch, hipStream_t s) {
-  for (const GemmInput& in : plan.inputs) {
-    const std::size_t quads = in.rows * (in.ldx / 4);
-    const unsigned blocks = static_cast<unsigned>(std::min<std::size_t>(ceil_div(quads, 256), 4096));
-    x_to_bf16<<<blocks, 256, 0, s>>>(in.x, scratch + in.offset, static_cast<int>(in.rows), static_cast<int>(in.in),
-                                     static_cast<int>(in.ldx));
+  // The inputs in batches of kConvBatch per launch.
+  for (std::size_t i0 = 0; i0 < plan.inputs.size(); i0 += kConvBatch) {
+    ConvBatch c{};
+    unsigned long long q = 0;
+    c.n = static_cast<int>(std::min<std::size_t>(kConvBatch, plan.inputs.size() - i0));
+    for (int k = 0; k < c.n; ++k) {
+      const GemmInput& in = plan.inputs[i0 + static_cast<std::size_t>(k)];
+      c.x[k] = in.x;
+      c.xb[k] = scratch + in.offset;
+      c.in[k] = static_cast<int>(in.in);
+      c.ldx[k] = static_cast<int>(in.ldx);
+      q += static_cast<unsigned long long>(in.rows) * (in.ldx / 4);
+      c.qend[k] = q;
+    }
+    if (q == 0) continue;
+    const unsigned blocks = static_cast<unsigned>(std::min<unsigned long long>((q + 255) / 256, 8192));
+    x_to_bf16_batch<<<blocks, 256, 0, s>>>(c);
   }
   LLMI_TRY_HIP(hipGetLastError());
   return LLMI_OK;
@@ -361,8 +507,8 @@ int launch_gemm_inputs(const GemmPlan& plan, std::uint16_t* scratch, hipStream_t
 // Nothing in it needs clearing: x_to_bf16 writes every element a launch
 // reads (rows x ldx, the padding columns as zeros; the GEMM clamps token
 // rows to rows - 1).  Calls that overlap on one GPU share it and race.
-constexpr std::size_t kNoAllocElems = LLMI_MFMA_NOALLOC_MAX_ELEMS;
-static __device__ __align__(256) std::uint16_t scratch[kNoAllocElems];
+constexpr std::size_t kNoAllocBytes = LLMI_MFMA_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) std::uint16_t scratch[kNoAllocBytes / sizeof(std::uint16_t)];
 
 namespace {
 constexpr int kMaxDevices = 64;
@@ -386,9 +532,15 @@ int launch_gemm_noalloc(int device, const DeviceMatrix& m, const float* x, std::
   if (rows == 0 || m.out == 0) return LLMI_OK;
   LLMI_REQUIRE(x != nullptr && y != nullptr, "matmul_mfma_noalloc: null x or y");
   const std::size_t ldx = gemm_ldx(m.in);
-  LLMI_REQUIRE(rows <= kNoAllocElems / ldx,
-               "matmul_mfma_noalloc: rows x in (rounded up to 64) exceeds the " +
-                   std::to_string(kNoAllocElems) + "-element scratch");
+  // The bf16 copy of x (rounded up to 256 bytes), then a split product's
+  // fp32 partials: the layout gemm_scratch_bytes / bind_gemm_scratch use.
+  LLMI_REQUIRE(rows <= 0x7FFFFFFFu && rows <= kNoAllocBytes / (2 * ldx),
+               "matmul_mfma_noalloc: the product exceeds the " + std::to_string(kNoAllocBytes) + "-byte scratch");
+  const std::size_t xbytes = (rows * ldx * sizeof(std::uint16_t) + 255) / 256 * 256;
+  const std::size_t tiles = gemm_tiles(rows, m.out);
+  const std::size_t pbytes = gemm_part_floats(rows, m.in, m.out, tiles) * sizeof(float);
+  LLMI_REQUIRE(xbytes + pbytes <= kNoAllocBytes,
+               "matmul_mfma_noalloc: the product exceeds the " + std::to_string(kNoAllocBytes) + "-byte scratch");
   LLMI_REQUIRE(device >= 0 && device < kMaxDevices && g_scratch_dev[device] != nullptr,
                "matmul_mfma_noalloc: scratch not set up on this device");
   std::uint16_t* xb = g_scratch_dev[device];
@@ -409,14 +561,25 @@ int launch_gemm_noalloc(int device, const DeviceMatrix& m, const float* x, std::
   p.first_wg = 0;
   p.input = 0;
   p.accumulate = 0;
+  p.kchunks = gemm_kchunks(m.in, tiles);
+  p.kpc = static_cast<int>(ceil_div(ceil_div(m.in, kBK), static_cast<std::size_t>(p.kchunks)));
+  p.part = p.kchunks > 1 ? reinterpret_cast<float*>(reinterpret_cast<std::uint8_t*>(xb) + xbytes) : nullptr;
   GemmLaunch l;
   l.type = m.type;
-  l.total_wgs = static_cast<int>(static_cast<std::size_t>(p.mtiles) * ceil_div(m.out, kBN));
+  l.total_wgs = static_cast<int>(static_cast<std::size_t>(p.mtiles) * ceil_div(m.out, kBN) *
+                                 static_cast<std::size_t>(p.kchunks));
   const std::size_t quads = rows * (ldx / 4);
   const unsigned blocks = static_cast<unsigned>(std::min<std::size_t>(ceil_div(quads, 256), 4096));
   x_to_bf16<<<blocks, 256, 0, s>>>(x, xb, static_cast<int>(rows), static_cast<int>(m.in), static_cast<int>(ldx));
   LLMI_TRY_HIP(hipGetLastError());
-  return launch_gemm(nullptr, nullptr, l, s, &p);
+  if (int rc = launch_gemm(nullptr, nullptr, l, s, &p)) return rc;
+  if (p.kchunks > 1) {
+    const std::size_t n = rows * m.out;
+    const unsigned rblocks = static_cast<unsigned>(std::min<std::size_t>(ceil_div(n, 256), 8192));
+    gemm_reduce<<<rblocks, 256, 0, s>>>(p.part, p.kchunks, p.rows, p.out, p.bias, p.y, p.accumulate);
+    LLMI_TRY_HIP(hipGetLastError());
+  }
+  return LLMI_OK;
 }
 
 int launch_gemm(const GemmProblem* probs_dev, const std::uint32_t* map_dev, const GemmLaunch& l, hipStream_t s,

@@ -120,9 +120,12 @@ def test_c5_grouped_launch_at_its_own_size():
     """BASELINE.json configs[4] as bench.py times it: the 168 Q8_0 products of
     24 Qwen2.5-0.5B layers at M = 512 in ONE grouped launch, every layer with
     its own activations (workloads.PrefillProducts).  Every product equals
-    its own single launch bit for bit; three whole layers (first, middle,
-    last: all seven shapes, incl. gate/up 4864x896 and down 896x4864) are
-    checked against the oracle at 2e-2 and against the bf16 bound."""
+    its own single launch bit for bit, except down_proj, whose single launch
+    (16 output tiles) splits K=4864 over five workgroups while the grouped
+    one (4992 tiles) does not: there the two agree to fp32 summation order
+    (1e-5 of max|y|).  Three whole layers (first, middle, last: all seven
+    shapes, incl. gate/up 4864x896 and down 896x4864) are checked against
+    the oracle at 2e-2 and against the bf16 bound."""
     prods = workloads.PrefillProducts(M=512, layers=24, qt=H.Q8_0)
     g = H.GemmGroup(prods.items)
     for y in prods.ys:
@@ -136,8 +139,12 @@ def test_c5_grouped_launch_at_its_own_size():
         w.matmul_mfma_dev(xp, rows, None, one.ptr)
         H.synchronize()
         single = one.download(np.float32)[: got.size]
-        assert np.array_equal(got.view(np.uint32), single.view(np.uint32)), prods.spec[i]
         layer, name, out, n_in, x_seed, w_seed = prods.spec[i]
+        if n_in > 1536:
+            scale = float(np.max(np.abs(single)))
+            assert float(np.max(np.abs(got.astype(np.float64) - single))) <= 1e-5 * scale, prods.spec[i]
+        else:
+            assert np.array_equal(got.view(np.uint32), single.view(np.uint32)), prods.spec[i]
         if layer in (0, 11, 23):
             data, scales = orc.quantize(synth.normal(w_seed, out * n_in, 0.0, 0.02), out, n_in, O.Q8_0)
             x = synth.normal(x_seed, rows * n_in, 0.0, 1.0)

@@ -14,7 +14,20 @@ import synth
 
 pytestmark = pytest.mark.gpu
 
-MAX_ELEMS = 4194304  # LLMI_MFMA_NOALLOC_MAX_ELEMS (include/llmi_hip.h)
+SCRATCH_BYTES = 33554432  # LLMI_MFMA_NOALLOC_SCRATCH_BYTES (include/llmi_hip.h)
+
+
+def scratch_need(rows, n_in, out):
+    """The header's formula: the bf16 copy of x rounded up to 256 bytes, plus
+    fp32 partials when K is split (more than 24 K-steps of 64 on fewer than
+    256 output tiles of 128 x 256)."""
+    ldx = -(-n_in // 64) * 64
+    need = -(-(2 * rows * ldx) // 256) * 256
+    nk = -(-n_in // 64)
+    tiles = -(-rows // 128) * -(-out // 256)
+    if nk > 24 and tiles < 256:
+        need += 4 * rows * out * -(-nk // 16)
+    return need
 
 
 def product(fn, w, x, rows, bias):
@@ -52,13 +65,17 @@ def test_noalloc_equals_the_allocating_entry_point(qt, out, n_in, calls):
 
 
 def test_noalloc_limit():
-    """rows * ldx (in rounded up to 64) up to the array's size is accepted and
-    exact; one row more is rejected before anything runs."""
+    """The largest product that fits the array (here with K split, so x's copy
+    and the partials share it) is accepted and exact; one row more is
+    rejected before anything runs."""
     orc = O.oracle()
-    out, n_in = 128, 4864  # ldx = 4864
+    out, n_in = 128, 4864  # ldx = 4864, 76 K-steps: split into 5 chunks
     data, scales = orc.quantize(synth.normal(9, out * n_in, 0.0, 0.02), out, n_in, O.Q8_0)
     w = H.Weight.upload(data, scales, out, n_in, O.Q8_0)
-    rows = MAX_ELEMS // n_in
+    rows = 1
+    while scratch_need(rows + 1, n_in, out) <= SCRATCH_BYTES:
+        rows += 1
+    assert scratch_need(rows, n_in, out) > 2 * rows * n_in  # the partials are part of it
     x = synth.normal(10, rows * n_in, 0.0, 1.0)
     want = product("llmi_hip_matmul_mfma_dev", w, x, rows, None)
     got = product("llmi_hip_matmul_mfma_noalloc_dev", w, x, rows, None)
