@@ -224,9 +224,12 @@ int llmi_hip_matmul_mfma_dev(const llmi_hip_weight* weight, const float* x_dev, 
  * it), its fp32 partial sums -- lives in a
  * fixed per-GPU array set up by llmi_hip_init instead of a buffer the
  * library grows, so the call makes no allocation.  Limit: 2 * rows * (in
- * rounded up to 64), rounded up to 256, plus 4 * rows * out * ceil(ceil(in /
- * 64) / 16) when K is split, at most LLMI_MFMA_NOALLOC_SCRATCH_BYTES
- * (LLMI_ERR_ARG beyond; e.g. 512 rows of 896 x 4864 need 14.1 MB).  Calls
+ * rounded up to 64), rounded up to 256, plus 4 * rows * out * kchunks when K
+ * is split, at most LLMI_MFMA_NOALLOC_SCRATCH_BYTES (LLMI_ERR_ARG beyond).
+ * With nk = ceil(in / 64) and tiles = ceil(rows / 128) * ceil(out / 256), K
+ * is split when nk > 24, tiles < 256 and k = min(256 / tiles, nk / 8)
+ * (integer quotients) is at least 2, into kchunks = ceil(nk / ceil(nk / k))
+ * chunks; e.g. 512 rows of 896 x 4864 take 9 chunks and need 21.5 MB.  Calls
  * that overlap on one GPU (e.g. on two streams) share that array and race. */
 #define LLMI_MFMA_NOALLOC_SCRATCH_BYTES 33554432
 int llmi_hip_matmul_mfma_noalloc_dev(const llmi_hip_weight* weight, const float* x_dev, size_t rows,

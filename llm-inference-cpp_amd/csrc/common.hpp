@@ -145,17 +145,20 @@ struct GemmProblem {
   float* part;
 };
 // K chunks of a product with `in` inputs on a GEMM launch of `launch_tiles`
-// output tiles (128 x 256): long K (more than 24 steps of 64) on a launch of
-// fewer than 256 tiles -- fewer than one workgroup per CU -- is split into
-// chunks of about 16 steps, so one long product does not leave the K loop
-// of a few workgroups as the launch's critical path; launches with enough
-// tiles are not split (the partial sums would only add traffic).  The split
-// changes the fp32 summation order, so a product's bits depend on whether
-// its launch splits it.
-int gemm_kchunks(std::size_t in, std::size_t launch_tiles);
+// output tiles (128 x 256), `split_tiles` of them belonging to products of
+// more than 24 K-steps of 64.  A launch of fewer tiles than the 256 CUs
+// splits the K of those long products over as many workgroups (chunks of at
+// least 8 steps) as the CUs its short products leave free, so the long K
+// loops of a few workgroups are not the launch's critical path; launches
+// with enough tiles are not split (partial sums would only add traffic).
+// The split changes the fp32 summation order, so a product's bits depend on
+// whether and how its launch splits it.
+int gemm_kchunks(std::size_t in, std::size_t launch_tiles, std::size_t split_tiles);
+// K-steps per chunk for kchunks chunks (every chunk non-empty).
+int gemm_kpc(std::size_t in, int kchunks);
 std::size_t gemm_tiles(std::size_t rows, std::size_t out);
-// fp32 partials a split product needs (0 when it is not split).
-std::size_t gemm_part_floats(std::size_t rows, std::size_t in, std::size_t out, std::size_t launch_tiles);
+// Tiles of a product that the K split may apply to (0 for short K).
+std::size_t gemm_split_tiles(std::size_t rows, std::size_t in, std::size_t out);
 // A distinct fp32 activation matrix of a GEMM group and where its bf16 copy
 // lives in the group's scratch (element offset).
 struct GemmInput {

@@ -42,6 +42,9 @@ namespace {
 #define GMEM __attribute__((address_space(1)))
 
 constexpr int kBM = 128, kBN = 256, kBK = 64;
+// K of more than kSplitMinSteps steps of kBK may be split over workgroups;
+// kCus is MI355X's CU count.
+constexpr std::size_t kSplitMinSteps = 24, kCus = 256;
 constexpr int kGemmThreads = 768;  // 8 MFMA wavefronts + 4 producers
 constexpr int kLdsRow = kBK + 8;  // bf16 per LDS row (16 bytes of padding)
 constexpr int kXcds = 8;
@@ -63,62 +66,58 @@ __device__ __forceinline__ int snib(std::uint32_t w, int i) {
   return static_cast<int>(__builtin_amdgcn_sbfe(w ^ 0x88888888u, i * 4, 4));
 }
 
-// xb[r][k] = bf16(x[r][k]) for k < in, 0 for in <= k < ldx.  One thread per 4
-// elements of a row.
-__global__ void __launch_bounds__(256) x_to_bf16(const float* __restrict__ x, std::uint16_t* __restrict__ xb,
-                                                 int rows, int in, int ldx) {
-  const std::size_t quads = static_cast<std::size_t>(rows) * (ldx / 4);
-  for (std::size_t q = static_cast<std::size_t>(blockIdx.x) * blockDim.x + threadIdx.x; q < quads;
-       q += static_cast<std::size_t>(gridDim.x) * blockDim.x) {
-    const std::size_t r = q / (ldx / 4);
-    const int k = static_cast<int>(q % (ldx / 4)) * 4;
-    const float* src = x + r * in + k;
-    float v[4];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) v[u] = k + u < in ? src[u] : 0.0f;
-    *reinterpret_cast<uint2*>(xb + r * ldx + k) = make_uint2(pack_bf16(v[0], v[1]), pack_bf16(v[2], v[3]));
-  }
-}
-
+// xb[r][k] = bf16(x[r][k]) for k < in, 0 for in <= k < ldx.
 // Up to kConvBatch activation matrices converted by one x_to_bf16_batch
-// launch: input i covers quads [qend[i-1], qend[i]) of the launch's range.
-constexpr int kConvBatch = 8;
+// launch, in octets (8 consecutive elements of a row, ldx being a multiple
+// of 64): input i covers octets [oend[i-1], oend[i]) of the launch's range,
+// cpr[i] = ldx[i] / 8 per row; vec[i]: x rows are 16-byte aligned (in % 4 ==
+// 0 and an aligned base), so whole octets load as two 16-byte vectors.
+constexpr int kConvBatch = 16;
 struct ConvBatch {
   const float* x[kConvBatch];
   std::uint16_t* xb[kConvBatch];
   int in[kConvBatch], ldx[kConvBatch];
-  unsigned long long qend[kConvBatch];
+  unsigned oend[kConvBatch];
+  unsigned char vec[kConvBatch];
   int n;
 };
 __global__ void __launch_bounds__(256) x_to_bf16_batch(ConvBatch c) {
-  const unsigned long long total = c.qend[c.n - 1];
-  for (unsigned long long q = static_cast<unsigned long long>(blockIdx.x) * blockDim.x + threadIdx.x; q < total;
-       q += static_cast<unsigned long long>(gridDim.x) * blockDim.x) {
-    int i = 0;
-#pragma unroll
-    for (int k = 0; k < kConvBatch - 1; ++k)
-      if (k < c.n - 1 && q >= c.qend[k]) i = k + 1;
-    const unsigned long long q0 = i == 0 ? 0ull : c.qend[i - 1];
-    // Select this input's fields without indexing the argument block.
+  const unsigned total = c.oend[c.n - 1];
+  for (unsigned o = blockIdx.x * blockDim.x + threadIdx.x; o < total; o += gridDim.x * blockDim.x) {
+    // Select this octet's input without indexing the argument block.
     const float* x = c.x[0];
     std::uint16_t* xb = c.xb[0];
     int in = c.in[0], ldx = c.ldx[0];
+    unsigned o0 = 0;
+    bool vec = c.vec[0] != 0;
 #pragma unroll
     for (int k = 1; k < kConvBatch; ++k)
-      if (i == k) {
+      if (k < c.n && o >= c.oend[k - 1]) {
         x = c.x[k];
         xb = c.xb[k];
         in = c.in[k];
         ldx = c.ldx[k];
+        o0 = c.oend[k - 1];
+        vec = c.vec[k] != 0;
       }
-    const unsigned long long lq = q - q0;
-    const std::size_t r = lq / (ldx / 4);
-    const int k0 = static_cast<int>(lq % (ldx / 4)) * 4;
-    const float* src = x + r * in + k0;
-    float v[4];
+    const unsigned lo = o - o0, cpr = static_cast<unsigned>(ldx) >> 3;
+    const unsigned r = lo / cpr;
+    const int k0 = static_cast<int>(lo - r * cpr) * 8;
+    const float* src = x + static_cast<std::size_t>(r) * in + k0;
+    float v[8];
+    if (vec && k0 + 8 <= in) {
+      const f32x4 lo4 = *reinterpret_cast<const f32x4*>(src), hi4 = *reinterpret_cast<const f32x4*>(src + 4);
 #pragma unroll
-    for (int u = 0; u < 4; ++u) v[u] = k0 + u < in ? src[u] : 0.0f;
-    *reinterpret_cast<uint2*>(xb + r * ldx + k0) = make_uint2(pack_bf16(v[0], v[1]), pack_bf16(v[2], v[3]));
+      for (int u = 0; u < 4; ++u) {
+        v[u] = lo4[u];
+        v[u + 4] = hi4[u];
+      }
+    } else {
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = k0 + u < in ? src[u] : 0.0f;
+    }
+    *reinterpret_cast<u32x4*>(xb + static_cast<std::size_t>(r) * ldx + k0) =
+        u32x4{pack_bf16(v[0], v[1]), pack_bf16(v[2], v[3]), pack_bf16(v[4], v[5]), pack_bf16(v[6], v[7])};
   }
 }
 
@@ -251,79 +250,112 @@ __global__ void __launch_bounds__(kGemmThreads) qgemm_mfma(const GemmProblem* __
   const int wm0 = (wave >> 2) * 64, wn0 = (wave & 3) * 64;
   const int arow = lane & 15, akoff = (lane >> 4) * 8;
 
-  const auto mfma_step = [&](int buf) {
+  // A K-step is two K-slices of 32, each 4 A and 4 B fragments (one register
+  // set).  The reads of a slice are in flight while the previous slice's 16
+  // MFMAs run: slice 1 of step k loads during slice 0's MFMAs, then (after
+  // the step's barrier, which its reads complete and which makes step k+1's
+  // buffer valid) slice 0 of step k+1 loads during slice 1's MFMAs.  The
+  // product is W x^T: acc[i][j][q] holds token m0 + wm0 + 16i + lane%16 and
+  // output n0 + wn0 + 16j + 4*(lane/16) + q, so a lane's four values are
+  // consecutive outputs of one token.
+  bf16x8 fa[2][4], fb[2][4];
+  const auto load_slice = [&](int set, int buf, int s) {
 #pragma unroll
-    for (int kk = 0; kk < kBK; kk += 32) {
-      bf16x8 a[4], b[4];
+    for (int i = 0; i < 4; ++i)
+      fa[set][i] = *reinterpret_cast<const bf16x8*>(&xs[buf][(wm0 + 16 * i + arow) * kLdsRow + 32 * s + akoff]);
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        a[i] = *reinterpret_cast<const bf16x8*>(&xs[buf][(wm0 + 16 * i + arow) * kLdsRow + kk + akoff]);
+    for (int j = 0; j < 4; ++j)
+      fb[set][j] = *reinterpret_cast<const bf16x8*>(&ws[buf][(wn0 + 16 * j + arow) * kLdsRow + 32 * s + akoff]);
+  };
+  const auto mfma_slice = [&](int set) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
 #pragma unroll
       for (int j = 0; j < 4; ++j)
-        b[j] = *reinterpret_cast<const bf16x8*>(&ws[buf][(wn0 + 16 * j + arow) * kLdsRow + kk + akoff]);
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
-    }
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fb[set][j], fa[set][i], acc[i][j], 0, 0, 0);
   };
 
   __syncthreads();  // step 0 staged
-  for (int k = 0; k < nk; k += 2) {
-    mfma_step(0);
+  load_slice(0, 0, 0);
+  for (int k = 0; k < nk; ++k) {
+    const int buf = k & 1;
+    load_slice(1, buf, 1);
+    mfma_slice(0);
+    // Nothing is scheduled across the barrier.
+    __builtin_amdgcn_sched_barrier(0);
     __syncthreads();
-    if (k + 1 >= nk) break;
-    mfma_step(1);
-    __syncthreads();
+    __builtin_amdgcn_sched_barrier(0);
+    if (k + 1 < nk) load_slice(0, buf ^ 1, 0);
+    mfma_slice(1);
   }
 
-  // acc[i][j][q]: token m0 + wm0 + 16i + 4*(lane/16) + q, output n0 + wn0 + 16j + lane%16.
+  // Rows of y / part are 16-byte aligned when N is a multiple of 4: a lane's
+  // four outputs then go out as one 16-byte store (the only case in which
+  // n < N implies n + 3 < N, since n is a multiple of 4).
+  const bool vec = (N & 3) == 0;
+  const int mrow = m0 + wm0 + (lane & 15), ncol = n0 + wn0 + 4 * (lane >> 4);
+  const auto store4 = [&](GMEM float* dst, const f32x4& v, int n) {
+    if (vec) {
+      *(GMEM f32x4*)dst = v;
+    } else {
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        if (n + q < N) dst[q] = v[q];
+    }
+  };
   if (p.kchunks > 1) {
     // A K chunk: the partial tile as it is (gemm_reduce adds the rest).
     GMEM float* part = (GMEM float*)(p.part + static_cast<std::size_t>(kc) * M * N);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int n = n0 + wn0 + 16 * j + (lane & 15);
-      if (n >= N) continue;
+    for (int i = 0; i < 4; ++i) {
+      const int m = mrow + 16 * i;
+      if (m >= M) continue;
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int m = m0 + wm0 + 16 * i + 4 * (lane >> 4) + q;
-          if (m < M) part[static_cast<std::size_t>(m) * N + n] = acc[i][j][q];
-        }
+      for (int j = 0; j < 4; ++j) {
+        const int n = ncol + 16 * j;
+        if (n < N) store4(part + static_cast<std::size_t>(m) * N + n, acc[i][j], n);
+      }
     }
     return;
   }
-  // With accumulate, a column's 16 old values are loaded together (clamped
-  // rows, no branch) before any is used, so their latencies overlap.
   GMEM float* y = (GMEM float*)p.y;
   const GMEM float* bias = (const GMEM float*)p.bias;
+  f32x4 add[4];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int n = n0 + wn0 + 16 * j + (lane & 15);
-    if (n >= N) continue;
-    const float add = bias != nullptr ? bias[n] : 0.0f;
-    float old[4][4];
-    if (p.accumulate) {
+  for (int j = 0; j < 4; ++j)
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int m = min(m0 + wm0 + 16 * i + 4 * (lane >> 4) + q, M - 1);
-          old[i][q] = y[static_cast<std::size_t>(m) * N + n];
-        }
+    for (int q = 0; q < 4; ++q) {
+      const int n = ncol + 16 * j + q;
+      add[j][q] = bias != nullptr && n < N ? bias[n] : 0.0f;
     }
+  // With accumulate, a token row's four old vectors are loaded (clamped to
+  // a row and column inside y) before any is used, so their latencies
+  // overlap.
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < 4; ++i) {
+    const int m = mrow + 16 * i;
+    f32x4 old[4];
+    if (p.accumulate) {
+      const std::size_t row = static_cast<std::size_t>(min(m, M - 1)) * N;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int m = m0 + wm0 + 16 * i + 4 * (lane >> 4) + q;
-        if (m < M) {
-          const float v = acc[i][j][q] + add;
-          y[static_cast<std::size_t>(m) * N + n] = p.accumulate ? old[i][q] + v : v;
+      for (int j = 0; j < 4; ++j) {
+        const int n = ncol + 16 * j;
+        if (vec) {
+          old[j] = *(const GMEM f32x4*)(y + row + min(n, N - 4));
+        } else {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) old[j][q] = y[row + min(n + q, N - 1)];
         }
       }
+    }
+    if (m >= M) continue;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int n = ncol + 16 * j;
+      if (n >= N) continue;
+      const f32x4 v = acc[i][j] + add[j];
+      store4(y + static_cast<std::size_t>(m) * N + n, p.accumulate ? old[j] + v : v, n);
+    }
   }
 }
 
@@ -354,17 +386,27 @@ __global__ void __launch_bounds__(256) gemm_reduce(const float* __restrict__ par
 
 }  // namespace
 
-int gemm_kchunks(std::size_t in, std::size_t launch_tiles) {
-  const std::size_t nk = (in + kBK - 1) / kBK;
-  if (nk <= 24 || launch_tiles >= 256) return 1;
-  return static_cast<int>(ceil_div(nk, 16));
+int gemm_kchunks(std::size_t in, std::size_t launch_tiles, std::size_t split_tiles) {
+  // One workgroup of qgemm_mfma fills a CU (110.6 KB of LDS, 12 waves of
+  // 166 VGPRs), so a launch of fewer tiles than CUs leaves CUs idle: a long
+  // product takes as many K chunks (of at least 8 K-steps) as the CUs the
+  // launch's other tiles leave over allow.
+  const std::size_t nk = ceil_div(in, static_cast<std::size_t>(kBK));
+  if (nk <= kSplitMinSteps || launch_tiles >= kCus || split_tiles == 0 || split_tiles > launch_tiles) return 1;
+  const std::size_t k = std::min((kCus - (launch_tiles - split_tiles)) / split_tiles, nk / 8);
+  if (k < 2) return 1;
+  // No empty chunk: as many chunks as ceil(nk / k) K-steps need.
+  return static_cast<int>(ceil_div(nk, ceil_div(nk, k)));
+}
+
+int gemm_kpc(std::size_t in, int kchunks) {
+  return static_cast<int>(ceil_div(ceil_div(in, static_cast<std::size_t>(kBK)), static_cast<std::size_t>(kchunks)));
 }
 
 std::size_t gemm_tiles(std::size_t rows, std::size_t out) { return ceil_div(rows, kBM) * ceil_div(out, kBN); }
 
-std::size_t gemm_part_floats(std::size_t rows, std::size_t in, std::size_t out, std::size_t launch_tiles) {
-  const int kc = gemm_kchunks(in, launch_tiles);
-  return kc > 1 ? static_cast<std::size_t>(kc) * rows * out : 0;
+std::size_t gemm_split_tiles(std::size_t rows, std::size_t in, std::size_t out) {
+  return ceil_div(in, static_cast<std::size_t>(kBK)) > kSplitMinSteps ? gemm_tiles(rows, out) : 0;
 }
 
 std::size_t gemm_ldx(std::size_t in) { return (in + kBK - 1) / kBK * kBK; }
@@ -399,10 +441,12 @@ int plan_gemm_group(const GroupEntry* entries, std::size_t count, GemmPlan* plan
     }
   }
   // Output tiles of each launch (one per weight type), for the K split.
-  std::size_t launch_tiles[3] = {0, 0, 0};
+  std::size_t launch_tiles[3] = {0, 0, 0}, split_tiles[3] = {0, 0, 0};
   for (std::size_t i = 0; i < count; ++i)
-    if (entries[i].rows > 0 && entries[i].m->out > 0)
+    if (entries[i].rows > 0 && entries[i].m->out > 0) {
       launch_tiles[entries[i].m->type] += gemm_tiles(entries[i].rows, entries[i].m->out);
+      split_tiles[entries[i].m->type] += gemm_split_tiles(entries[i].rows, entries[i].m->in, entries[i].m->out);
+    }
   for (int type : {LLMI_TYPE_Q8_0, LLMI_TYPE_Q4_0}) {
     GemmLaunch l;
     l.type = type;
@@ -426,11 +470,11 @@ int plan_gemm_group(const GroupEntry* entries, std::size_t count, GemmPlan* plan
       p.ntiles = static_cast<int>(m.ntiles);
       p.mtiles = static_cast<int>(ceil_div(e.rows, kBM));
       p.accumulate = e.accumulate ? 1 : 0;
-      p.kchunks = gemm_kchunks(m.in, launch_tiles[type]);
-      p.kpc = static_cast<int>(ceil_div(ceil_div(m.in, kBK), static_cast<std::size_t>(p.kchunks)));
+      p.kchunks = gemm_kchunks(m.in, launch_tiles[type], split_tiles[type]);
+      p.kpc = gemm_kpc(m.in, p.kchunks);
       p.part = nullptr;
       plan->part_off.push_back(plan->part_floats);
-      plan->part_floats += gemm_part_floats(e.rows, m.in, m.out, launch_tiles[type]);
+      plan->part_floats += p.kchunks > 1 ? static_cast<std::size_t>(p.kchunks) * e.rows * m.out : 0;
       for (std::size_t j = 0; j < plan->inputs.size(); ++j)
         if (plan->inputs[j].x == e.x) p.input = static_cast<int>(j);
       const std::size_t ntiles_n = ceil_div(m.out, kBN);
@@ -476,22 +520,31 @@ int launch_gemm_reduces(const GemmPlan& plan, hipStream_t s) {
 }
 
 int launch_gemm_inputs(const GemmPlan& plan, std::uint16_t* scratch, hipStream_t s) {
-  // The inputs in batches of kConvBatch per launch.
-  for (std::size_t i0 = 0; i0 < plan.inputs.size(); i0 += kConvBatch) {
+  // The inputs in batches of kConvBatch per launch, each batch's octets
+  // counted in 32 bits (a batch is cut short before it would overflow).
+  std::size_t i0 = 0;
+  while (i0 < plan.inputs.size()) {
     ConvBatch c{};
-    unsigned long long q = 0;
-    c.n = static_cast<int>(std::min<std::size_t>(kConvBatch, plan.inputs.size() - i0));
-    for (int k = 0; k < c.n; ++k) {
-      const GemmInput& in = plan.inputs[i0 + static_cast<std::size_t>(k)];
-      c.x[k] = in.x;
-      c.xb[k] = scratch + in.offset;
-      c.in[k] = static_cast<int>(in.in);
-      c.ldx[k] = static_cast<int>(in.ldx);
-      q += static_cast<unsigned long long>(in.rows) * (in.ldx / 4);
-      c.qend[k] = q;
+    std::size_t o = 0;
+    int n = 0;
+    while (n < kConvBatch && i0 + static_cast<std::size_t>(n) < plan.inputs.size()) {
+      const GemmInput& in = plan.inputs[i0 + static_cast<std::size_t>(n)];
+      const std::size_t octets = in.rows * (in.ldx / 8);
+      LLMI_REQUIRE(octets < 0x80000000u, "gemm: activation matrix too large");
+      if (o + octets > 0xFFFFFFFFu) break;
+      o += octets;
+      c.x[n] = in.x;
+      c.xb[n] = scratch + in.offset;
+      c.in[n] = static_cast<int>(in.in);
+      c.ldx[n] = static_cast<int>(in.ldx);
+      c.oend[n] = static_cast<unsigned>(o);
+      c.vec[n] = in.in % 4 == 0 && reinterpret_cast<std::uintptr_t>(in.x) % 16 == 0 ? 1 : 0;
+      ++n;
     }
-    if (q == 0) continue;
-    const unsigned blocks = static_cast<unsigned>(std::min<unsigned long long>((q + 255) / 256, 8192));
+    c.n = n;
+    i0 += static_cast<std::size_t>(n);
+    if (o == 0) continue;
+    const unsigned blocks = static_cast<unsigned>(std::min<std::size_t>((o + 255) / 256, 16384));
     x_to_bf16_batch<<<blocks, 256, 0, s>>>(c);
   }
   LLMI_TRY_HIP(hipGetLastError());
@@ -538,7 +591,8 @@ int launch_gemm_noalloc(int device, const DeviceMatrix& m, const float* x, std::
                "matmul_mfma_noalloc: the product exceeds the " + std::to_string(kNoAllocBytes) + "-byte scratch");
   const std::size_t xbytes = (rows * ldx * sizeof(std::uint16_t) + 255) / 256 * 256;
   const std::size_t tiles = gemm_tiles(rows, m.out);
-  const std::size_t pbytes = gemm_part_floats(rows, m.in, m.out, tiles) * sizeof(float);
+  const int kchunks = gemm_kchunks(m.in, tiles, tiles);
+  const std::size_t pbytes = kchunks > 1 ? static_cast<std::size_t>(kchunks) * rows * m.out * sizeof(float) : 0;
   LLMI_REQUIRE(xbytes + pbytes <= kNoAllocBytes,
                "matmul_mfma_noalloc: the product exceeds the " + std::to_string(kNoAllocBytes) + "-byte scratch");
   LLMI_REQUIRE(device >= 0 && device < kMaxDevices && g_scratch_dev[device] != nullptr,
@@ -561,16 +615,25 @@ int launch_gemm_noalloc(int device, const DeviceMatrix& m, const float* x, std::
   p.first_wg = 0;
   p.input = 0;
   p.accumulate = 0;
-  p.kchunks = gemm_kchunks(m.in, tiles);
-  p.kpc = static_cast<int>(ceil_div(ceil_div(m.in, kBK), static_cast<std::size_t>(p.kchunks)));
+  p.kchunks = kchunks;
+  p.kpc = gemm_kpc(m.in, kchunks);
   p.part = p.kchunks > 1 ? reinterpret_cast<float*>(reinterpret_cast<std::uint8_t*>(xb) + xbytes) : nullptr;
   GemmLaunch l;
   l.type = m.type;
   l.total_wgs = static_cast<int>(static_cast<std::size_t>(p.mtiles) * ceil_div(m.out, kBN) *
                                  static_cast<std::size_t>(p.kchunks));
-  const std::size_t quads = rows * (ldx / 4);
-  const unsigned blocks = static_cast<unsigned>(std::min<std::size_t>(ceil_div(quads, 256), 4096));
-  x_to_bf16<<<blocks, 256, 0, s>>>(x, xb, static_cast<int>(rows), static_cast<int>(m.in), static_cast<int>(ldx));
+  // x's bf16 copy: one input of the batched conversion, planned on the stack.
+  ConvBatch c{};
+  const std::size_t octets = rows * (ldx / 8);
+  LLMI_REQUIRE(octets < 0x80000000u, "matmul_mfma_noalloc: activation matrix too large");
+  c.n = 1;
+  c.x[0] = x;
+  c.xb[0] = xb;
+  c.in[0] = static_cast<int>(m.in);
+  c.ldx[0] = static_cast<int>(ldx);
+  c.oend[0] = static_cast<unsigned>(octets);
+  c.vec[0] = m.in % 4 == 0 && reinterpret_cast<std::uintptr_t>(x) % 16 == 0 ? 1 : 0;
+  x_to_bf16_batch<<<static_cast<unsigned>(std::min<std::size_t>(ceil_div(octets, 256), 16384)), 256, 0, s>>>(c);
   LLMI_TRY_HIP(hipGetLastError());
   if (int rc = launch_gemm(nullptr, nullptr, l, s, &p)) return rc;
   if (p.kchunks > 1) {

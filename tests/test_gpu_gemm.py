@@ -121,7 +121,7 @@ def test_c5_grouped_launch_at_its_own_size():
     24 Qwen2.5-0.5B layers at M = 512 in ONE grouped launch, every layer with
     its own activations (workloads.PrefillProducts).  Every product equals
     its own single launch bit for bit, except down_proj, whose single launch
-    (16 output tiles) splits K=4864 over five workgroups while the grouped
+    (16 output tiles) splits K=4864 over nine workgroups while the grouped
     one (4992 tiles) does not: there the two agree to fp32 summation order
     (1e-5 of max|y|).  Three whole layers (first, middle, last: all seven
     shapes, incl. gate/up 4864x896 and down 896x4864) are checked against

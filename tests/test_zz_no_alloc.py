@@ -20,13 +20,16 @@ SCRATCH_BYTES = 33554432  # LLMI_MFMA_NOALLOC_SCRATCH_BYTES (include/llmi_hip.h)
 def scratch_need(rows, n_in, out):
     """The header's formula: the bf16 copy of x rounded up to 256 bytes, plus
     fp32 partials when K is split (more than 24 K-steps of 64 on fewer than
-    256 output tiles of 128 x 256)."""
+    256 output tiles of 128 x 256, into as many chunks of at least 8 steps as
+    256 // tiles allows)."""
     ldx = -(-n_in // 64) * 64
     need = -(-(2 * rows * ldx) // 256) * 256
     nk = -(-n_in // 64)
     tiles = -(-rows // 128) * -(-out // 256)
     if nk > 24 and tiles < 256:
-        need += 4 * rows * out * -(-nk // 16)
+        k = min(256 // tiles, nk // 8)
+        if k >= 2:
+            need += 4 * rows * out * -(-nk // -(-nk // k))
     return need
 
 
@@ -69,7 +72,7 @@ def test_noalloc_limit():
     and the partials share it) is accepted and exact; one row more is
     rejected before anything runs."""
     orc = O.oracle()
-    out, n_in = 128, 4864  # ldx = 4864, 76 K-steps: split into 5 chunks
+    out, n_in = 128, 4864  # ldx = 4864, 76 K-steps: split into 9 chunks
     data, scales = orc.quantize(synth.normal(9, out * n_in, 0.0, 0.02), out, n_in, O.Q8_0)
     w = H.Weight.upload(data, scales, out, n_in, O.Q8_0)
     rows = 1
