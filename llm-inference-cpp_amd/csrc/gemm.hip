@@ -31,6 +31,7 @@
 // its product through a work -> product map.
 #include <algorithm>
 #include <string>
+#include <type_traits>
 #include <vector>
 
 #include "common.hpp"
@@ -45,7 +46,7 @@ constexpr int kBM = 128, kBN = 256, kBK = 64;
 // K of more than kSplitMinSteps steps of kBK may be split over workgroups;
 // kCus is MI355X's CU count.
 constexpr std::size_t kSplitMinSteps = 24, kCus = 256;
-constexpr int kGemmThreads = 768;  // 8 MFMA wavefronts + 4 producers
+constexpr int kGemmThreads = 512;  // 8 wavefronts
 constexpr int kLdsRow = kBK + 8;  // bf16 per LDS row (16 bytes of padding)
 constexpr int kXcds = 8;
 
@@ -53,6 +54,7 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ std::uint32_t pack_bf16(float a, float b) {
   const bf16x2 v = {static_cast<__bf16>(a), static_cast<__bf16>(b)};
@@ -121,30 +123,36 @@ __global__ void __launch_bounds__(256) x_to_bf16_batch(ConvBatch c) {
   }
 }
 
-// Raw data of one K-step held by one producer thread: 32 activations (bf16)
-// of row pt/2, columns 32*(pt%2)..+31, and the codes + scales of weight row
-// pt's two quantization blocks; live[h]: block h exists (else its scale
-// counts as 0).
+// One K-step (64) of a wavefront's weights as loaded: for each K-slice s (a
+// quantization block) and column group j, the 8 codes a lane feeds the MFMA
+// (Q8_0: 8 bytes, Q4_0: 8 nibbles in one word) and the row's block scale;
+// live[s]: block s exists (else its scale counts as 0).
 template <int TYPE>
-struct Stage {
-  u32x4 x[4];
-  u32x4 w[TYPE == LLMI_TYPE_Q8_0 ? 4 : 2];
-  float sc[2];
+struct WStage {
+  using Code = std::conditional_t<TYPE == LLMI_TYPE_Q8_0, u32x2, std::uint32_t>;
+  Code c[2][2];
+  float sc[2][2];
   bool live[2];
 };
+// One K-step of the activation tile held by one thread: chunks t and t+512
+// (16 bytes each) of the 128 x 64 bf16 tile.
+struct XStage {
+  u32x4 v[2];
+};
 
-// Wavefronts 0..7 run the MFMAs, 8..11 produce: per K-step the producers
-// load (two steps ahead), dequantize and store the next step's tiles into
-// one LDS buffer while the MFMA wavefronts read the other; one barrier per
-// step, so a step costs the longer of the two sides rather than their sum.
-constexpr int kMfmaWaves = 8;
-
+// qgemm_mfma: a workgroup computes a 128-token x 256-output tile of y = x W^T
+// (or one K chunk of it) with 8 wavefronts.  Wavefront w owns outputs
+// 32w..32w+31 of the tile and all 128 tokens: it loads its own weight codes
+// (two K-steps ahead), dequantizes them to bf16 in registers for the next
+// step while the current step's MFMAs run, and reads the activations from a
+// double-buffered LDS tile that all wavefronts fill together (also two steps
+// ahead through registers).  One barrier per K-step publishes the next
+// activation tile and frees the one just read.
 template <int TYPE>
 __global__ void __launch_bounds__(kGemmThreads) qgemm_mfma(const GemmProblem* __restrict__ probs,
                                                            const std::uint32_t* __restrict__ work_prob, int total,
                                                            GemmProblem one) {
   __shared__ __attribute__((aligned(16))) std::uint16_t xs[2][kBM * kLdsRow];
-  __shared__ __attribute__((aligned(16))) std::uint16_t ws[2][kBN * kLdsRow];
 
   // Work index: workgroup w runs on XCD w % 8; give each XCD a contiguous
   // range of work items.
@@ -169,149 +177,164 @@ __global__ void __launch_bounds__(kGemmThreads) qgemm_mfma(const GemmProblem* __
   const int t = threadIdx.x;
   const int lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int wn0 = wave * 32;
+  const int arow = lane & 15, q = lane >> 4;
 
-  if (wave >= kMfmaWaves) {
-    // ------------------------------------------------------------ producer
-    const GMEM u32x4* xb = (const GMEM u32x4*)p.xb;
-    const GMEM u32x4* codes = (const GMEM u32x4*)p.codes;
-    const GMEM float* scales = (const GMEM float*)p.scales;
-    const int pt = t - kMfmaWaves * 64;
-    const int xr = pt >> 1, xh = pt & 1;
-    // Every load is issued unconditionally from an address inside the
-    // operands (rows past M or N are clamped to the last one; their results
-    // are never stored), so no load sits behind a branch and the loads of
-    // later steps stay in flight.
-    const int wrow = min(n0 + pt, p.ntiles * kTileRows - 1);
-    const int wtile = wrow / kTileRows, wlane = wrow % kTileRows;
-    const std::size_t xbase = (static_cast<std::size_t>(min(m0 + xr, M - 1)) * ldx + xh * 32) / 8;
-    const auto gload = [&](Stage<TYPE>& st, int j) {
-      const int k = kb + min(j, nk - 1);  // the ring's prefetch past the last step re-reads it
+  // Every load is issued unconditionally from an address inside the
+  // operands (rows past M or N are clamped to the last one; their results
+  // are never stored; steps past the last re-read it), so no load sits
+  // behind a branch.
+  const GMEM u32x4* xb = (const GMEM u32x4*)p.xb;
+  std::size_t xoff[2];
+  int xlds[2];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) st.x[u] = xb[xbase + static_cast<std::size_t>(k) * (kBK / 8) + u];
+  for (int u = 0; u < 2; ++u) {
+    const int c = t + 512 * u, row = c >> 3, col = c & 7;
+    xoff[u] = (static_cast<std::size_t>(min(m0 + row, M - 1)) * ldx + col * 8) / 8;
+    xlds[u] = row * kLdsRow + col * 8;
+  }
+  const auto xload = [&](XStage& st, int j) {
+    const int k = kb + min(j, nk - 1);
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        st.live[h] = 2 * k + h < nblk;
-        const std::size_t sl = static_cast<std::size_t>(wtile) * nblk + min(2 * k + h, nblk - 1);
+    for (int u = 0; u < 2; ++u) st.v[u] = xb[xoff[u] + static_cast<std::size_t>(k) * (kBK / 8)];
+  };
+  const auto xstore = [&](const XStage& st, int buf) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) *reinterpret_cast<u32x4*>(&xs[buf][xlds[u]]) = st.v[u];
+  };
+
+  // This lane's weight rows (columns of the tile): n0 + wn0 + 16j + lane%16,
+  // clamped into the padded matrix; the wavefront's 32 rows lie in one
+  // 64-row tile.
+  const int wrow0 = min(n0 + wn0 + arow, p.ntiles * kTileRows - 1);
+  const int wrow1 = min(n0 + wn0 + 16 + arow, p.ntiles * kTileRows - 1);
+  const std::size_t wt0 = static_cast<std::size_t>(wrow0 / kTileRows) * nblk,
+                    wt1 = static_cast<std::size_t>(wrow1 / kTileRows) * nblk;
+  const int wl0 = wrow0 % kTileRows, wl1 = wrow1 % kTileRows;
+  const GMEM float* scales = (const GMEM float*)p.scales;
+  const auto wload = [&](WStage<TYPE>& st, int j) {
+    const int k = kb + min(j, nk - 1);
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const int blk = 2 * k + s;
+      st.live[s] = blk < nblk;
+      const int bc = min(blk, nblk - 1);
+#pragma unroll
+      for (int jj = 0; jj < 2; ++jj) {
+        const std::size_t sl = (jj == 0 ? wt0 : wt1) + bc;
+        const int wl = jj == 0 ? wl0 : wl1;
         if constexpr (TYPE == LLMI_TYPE_Q8_0) {
-          st.w[2 * h] = codes[(sl * 2 + 0) * kTileRows + wlane];
-          st.w[2 * h + 1] = codes[(sl * 2 + 1) * kTileRows + wlane];
+          // Block = two 16-byte halves of 64 rows; codes 8q..8q+7.
+          const GMEM u32x2* codes = (const GMEM u32x2*)p.codes;
+          st.c[s][jj] = codes[((sl * 2 + (q >> 1)) * kTileRows + wl) * 2 + (q & 1)];
         } else {
-          st.w[h] = codes[sl * kTileRows + wlane];
+          // Block = 16 bytes per row; codes 8q..8q+7 are word q.
+          const GMEM std::uint32_t* codes = (const GMEM std::uint32_t*)p.codes;
+          st.c[s][jj] = codes[(sl * kTileRows + wl) * 4 + q];
         }
-        st.sc[h] = scales[sl * kTileRows + wlane];
+        st.sc[s][jj] = scales[sl * kTileRows + wl];
       }
-    };
-    const auto lstore = [&](const Stage<TYPE>& st, int buf) {
-      u32x4* xd = reinterpret_cast<u32x4*>(&xs[buf][xr * kLdsRow + xh * 32]);
+    }
+  };
+  // bf16(code * scale), the operand of the fp32 restatement rounded once.
+  const auto dequant = [&](const WStage<TYPE>& st, bf16x8 (&bf)[2][2]) {
 #pragma unroll
-      for (int u = 0; u < 4; ++u) xd[u] = st.x[u];
-      u32x4* wd = reinterpret_cast<u32x4*>(&ws[buf][pt * kLdsRow]);
+    for (int s = 0; s < 2; ++s)
 #pragma unroll
-      for (int q = 0; q < 8; ++q) {  // 8 elements each; q / 4 = the block
-        const int h = q >> 2;
+      for (int jj = 0; jj < 2; ++jj) {
+        const float sc = st.live[s] ? st.sc[s][jj] : 0.0f;
         float c[8];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const int e = 8 * (q & 3) + i;  // element within block h
+        for (int e = 0; e < 8; ++e) {
           int code;
-          if constexpr (TYPE == LLMI_TYPE_Q8_0) code = sbyte(st.w[2 * h + (e >> 4)][(e >> 2) & 3], e & 3);
-          else code = snib(st.w[h][e >> 3], e & 7);
-          c[i] = static_cast<float>(code) * (st.live[h] ? st.sc[h] : 0.0f);
+          if constexpr (TYPE == LLMI_TYPE_Q8_0) code = sbyte(st.c[s][jj][e >> 2], e & 3);
+          else code = snib(st.c[s][jj], e);
+          c[e] = static_cast<float>(code) * sc;
         }
-        wd[q] = u32x4{pack_bf16(c[0], c[1]), pack_bf16(c[2], c[3]), pack_bf16(c[4], c[5]), pack_bf16(c[6], c[7])};
+        const u32x4 pk{pack_bf16(c[0], c[1]), pack_bf16(c[2], c[3]), pack_bf16(c[4], c[5]), pack_bf16(c[6], c[7])};
+        bf[s][jj] = __builtin_bit_cast(bf16x8, pk);
       }
-    };
-    // Ring: step k's data is in A for even k, B for odd k.
-    Stage<TYPE> A, B;
-    gload(A, 0);
-    gload(B, 1);
-    lstore(A, 0);
-    gload(A, 2);
-    __syncthreads();
-    for (int k = 0; k < nk; k += 2) {
-      if (k + 1 < nk) lstore(B, 1);
-      gload(B, k + 3);
-      __syncthreads();
-      if (k + 1 >= nk) break;
-      if (k + 2 < nk) lstore(A, 0);
-      gload(A, k + 4);
-      __syncthreads();
-    }
-    return;
-  }
-
-  // -------------------------------------------------------------- MFMA
-  f32x4 acc[4][4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-
-  const int wm0 = (wave >> 2) * 64, wn0 = (wave & 3) * 64;
-  const int arow = lane & 15, akoff = (lane >> 4) * 8;
-
-  // A K-step is two K-slices of 32, each 4 A and 4 B fragments (one register
-  // set).  The reads of a slice are in flight while the previous slice's 16
-  // MFMAs run: slice 1 of step k loads during slice 0's MFMAs, then (after
-  // the step's barrier, which its reads complete and which makes step k+1's
-  // buffer valid) slice 0 of step k+1 loads during slice 1's MFMAs.  The
-  // product is W x^T: acc[i][j][q] holds token m0 + wm0 + 16i + lane%16 and
-  // output n0 + wn0 + 16j + 4*(lane/16) + q, so a lane's four values are
-  // consecutive outputs of one token.
-  bf16x8 fa[2][4], fb[2][4];
-  const auto load_slice = [&](int set, int buf, int s) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      fa[set][i] = *reinterpret_cast<const bf16x8*>(&xs[buf][(wm0 + 16 * i + arow) * kLdsRow + 32 * s + akoff]);
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      fb[set][j] = *reinterpret_cast<const bf16x8*>(&ws[buf][(wn0 + 16 * j + arow) * kLdsRow + 32 * s + akoff]);
-  };
-  const auto mfma_slice = [&](int set) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fb[set][j], fa[set][i], acc[i][j], 0, 0, 0);
   };
 
-  __syncthreads();  // step 0 staged
-  load_slice(0, 0, 0);
-  for (int k = 0; k < nk; ++k) {
-    const int buf = k & 1;
-    load_slice(1, buf, 1);
-    mfma_slice(0);
-    // Nothing is scheduled across the barrier.
-    __builtin_amdgcn_sched_barrier(0);
+  f32x4 acc[8][2];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  // One K-step: the 16 activation fragments of the step (two K-slices of
+  // 32), then 32 MFMAs.  The product is W x^T: acc[i][j][e] holds token
+  // m0 + 16i + lane%16 and output n0 + wn0 + 16j + 4*(lane/16) + e, so a
+  // lane's four values are consecutive outputs of one token.
+  const auto step = [&](int buf, const bf16x8 (&bf)[2][2]) {
+    bf16x8 a[2][8];
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        a[s][i] = *reinterpret_cast<const bf16x8*>(&xs[buf][(16 * i + arow) * kLdsRow + 32 * s + 8 * q]);
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bf[s][j], a[s][i], acc[i][j], 0, 0, 0);
+  };
+
+  // Rings: activations of step k in XA (even k) / XB (odd), raw weights in
+  // WA / WB likewise, dequantized weights of step k in BA / BB.
+  XStage XA, XB;
+  WStage<TYPE> WA, WB;
+  bf16x8 BA[2][2], BB[2][2];
+  xload(XA, 0);
+  xload(XB, 1);
+  wload(WA, 0);
+  wload(WB, 1);
+  xstore(XA, 0);
+  xload(XA, 2);
+  dequant(WA, BA);
+  wload(WA, 2);
+  __syncthreads();  // step 0's activations staged
+  for (int k = 0; k < nk; k += 2) {
+    if (k + 1 < nk) xstore(XB, 1);
+    xload(XB, k + 3);
+    dequant(WB, BB);
+    wload(WB, k + 3);
+    step(0, BA);
     __syncthreads();
-    __builtin_amdgcn_sched_barrier(0);
-    if (k + 1 < nk) load_slice(0, buf ^ 1, 0);
-    mfma_slice(1);
+    if (k + 1 >= nk) break;
+    if (k + 2 < nk) xstore(XA, 0);
+    xload(XA, k + 4);
+    dequant(WA, BA);
+    wload(WA, k + 4);
+    step(1, BB);
+    __syncthreads();
   }
 
   // Rows of y / part are 16-byte aligned when N is a multiple of 4: a lane's
   // four outputs then go out as one 16-byte store (the only case in which
   // n < N implies n + 3 < N, since n is a multiple of 4).
   const bool vec = (N & 3) == 0;
-  const int mrow = m0 + wm0 + (lane & 15), ncol = n0 + wn0 + 4 * (lane >> 4);
+  const int mrow = m0 + arow, ncol = n0 + wn0 + 4 * q;
   const auto store4 = [&](GMEM float* dst, const f32x4& v, int n) {
     if (vec) {
       *(GMEM f32x4*)dst = v;
     } else {
 #pragma unroll
-      for (int q = 0; q < 4; ++q)
-        if (n + q < N) dst[q] = v[q];
+      for (int e = 0; e < 4; ++e)
+        if (n + e < N) dst[e] = v[e];
     }
   };
   if (p.kchunks > 1) {
     // A K chunk: the partial tile as it is (gemm_reduce adds the rest).
     GMEM float* part = (GMEM float*)(p.part + static_cast<std::size_t>(kc) * M * N);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < 8; ++i) {
       const int m = mrow + 16 * i;
       if (m >= M) continue;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
+      for (int j = 0; j < 2; ++j) {
         const int n = ncol + 16 * j;
         if (n < N) store4(part + static_cast<std::size_t>(m) * N + n, acc[i][j], n);
       }
@@ -320,37 +343,36 @@ __global__ void __launch_bounds__(kGemmThreads) qgemm_mfma(const GemmProblem* __
   }
   GMEM float* y = (GMEM float*)p.y;
   const GMEM float* bias = (const GMEM float*)p.bias;
-  f32x4 add[4];
+  f32x4 add[2];
 #pragma unroll
-  for (int j = 0; j < 4; ++j)
+  for (int j = 0; j < 2; ++j)
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int n = ncol + 16 * j + q;
-      add[j][q] = bias != nullptr && n < N ? bias[n] : 0.0f;
+    for (int e = 0; e < 4; ++e) {
+      const int n = ncol + 16 * j + e;
+      add[j][e] = bias != nullptr && n < N ? bias[n] : 0.0f;
     }
-  // With accumulate, a token row's four old vectors are loaded (clamped to
-  // a row and column inside y) before any is used, so their latencies
-  // overlap.
+  // With accumulate, a token row's old vectors are loaded (clamped to a row
+  // and column inside y) before any is used, so their latencies overlap.
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < 8; ++i) {
     const int m = mrow + 16 * i;
-    f32x4 old[4];
+    f32x4 old[2];
     if (p.accumulate) {
       const std::size_t row = static_cast<std::size_t>(min(m, M - 1)) * N;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
+      for (int j = 0; j < 2; ++j) {
         const int n = ncol + 16 * j;
         if (vec) {
           old[j] = *(const GMEM f32x4*)(y + row + min(n, N - 4));
         } else {
 #pragma unroll
-          for (int q = 0; q < 4; ++q) old[j][q] = y[row + min(n + q, N - 1)];
+          for (int e = 0; e < 4; ++e) old[j][e] = y[row + min(n + e, N - 1)];
         }
       }
     }
     if (m >= M) continue;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < 2; ++j) {
       const int n = ncol + 16 * j;
       if (n >= N) continue;
       const f32x4 v = acc[i][j] + add[j];
