@@ -36,11 +36,37 @@ import workloads as W  # noqa: E402
 
 METRIC = "Q4_0/Q8_0 GEMV achieved HBM GB/s (% of peak); decode tokens/s, 1 GPU"
 HBM_PEAK_GBS = 8000.0
-# HBM bytes per qgemv_group launch of the batch-1 step, from the two
-# rocprofv3 --pmc passes (FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0, the factors a
-# 256 MiB copy kernel reads) recorded in profiles/qgemv_group_smollm2_q4_b1.md.
-GROUP_B1_HBM_BYTES = 85_093_182
 ROTATE_BYTES = 1 << 30
+# The rocprofv3 summary that holds the measured HBM traffic of the headline
+# kernel (FETCH_SIZE and WRITE_SIZE passes over this script, scaled by a
+# plain copy kernel's readings).
+TRAFFIC_PROFILE = os.path.join("profiles", "qgemv_group_smollm2_q4_b1.md")
+HEADLINE_KERNEL = "qgemv_group<2, 1>"
+
+
+def profiled_traffic(kernel: str = HEADLINE_KERNEL, path: str = TRAFFIC_PROFILE):
+    """HBM bytes per launch of `kernel` from the traffic table of a committed
+    rocprofv3 summary: the row whose first cell is the kernel's name, the
+    column headed "HBM bytes (scaled)".  None when the summary has no such
+    row."""
+    try:
+        with open(os.path.join(ROOT, path)) as f:
+            lines = f.read().splitlines()
+    except OSError:
+        return None
+    header = None
+    for line in lines:
+        cells = [c.strip() for c in line.strip().strip("|").split("|")]
+        if "HBM bytes (scaled)" in cells:
+            header = cells
+            continue
+        if header is not None and cells and cells[0].strip("`") == kernel and len(cells) == len(header):
+            try:
+                return int(cells[header.index("HBM bytes (scaled)")].replace(",", ""))
+            except ValueError:
+                return None
+    return None
+
 
 SMOL_LAYER = W.SMOL_LAYER
 SMOL_HEAD = W.SMOL_HEAD
@@ -194,6 +220,56 @@ def grouped_mlp_targets(steps=50):
     return res
 
 
+# The reference's per-shape decode table (tools/bench_apple_silicon.cpp:96-146):
+# each SmolLM2-135M shape alone at rows = 1, (name, out, in).
+REF_SHAPES = [("attn_qkv_o", 576, 576), ("mlp_up_gate", 1536, 576), ("mlp_down", 576, 1536), ("lm_head", 49152, 576)]
+PER_SHAPE_ROTATE = 512 << 20
+
+
+def weight_bytes_of(out: int, n_in: int, qt: int) -> int:
+    """Device bytes of one matrix: fp32 values, or packed codes + fp32 scales."""
+    if qt == H.F32:
+        return 4 * out * n_in
+    return out * H.row_bytes(n_in, qt) + 4 * out * H.nblocks(n_in)
+
+
+def per_shape_gpu():
+    """Each of the reference's per-shape rows on the GPU: F32, Q8_0 and Q4_0,
+    batch 1 and 8, as back-to-back single launches (llmi_hip_matmul_dev)
+    cycling over rotating copies of >= 512 MB (more than the 256 MB Infinity
+    Cache) or 2000 copies.  us = mean per launch between one pair of HIP
+    events (includes the ~2 us dispatch gap); gbs = algorithmic bytes
+    (weights + x + y) / us; weight_gbs = weight bytes / us, the reference
+    table's GB/s."""
+    res = {}
+    stage = H.DeviceBuffer(max(o * i for _, o, i in REF_SHAPES) * 4)
+    for name, out, n_in in REF_SHAPES:
+        row = {}
+        for qt in (H.F32, H.Q8_0, H.Q4_0):
+            wb = weight_bytes_of(out, n_in, qt)
+            copies = max(2, min(2000, -(-PER_SHAPE_ROTATE // wb)))
+            ws = []
+            for c in range(copies):
+                H.synth_normal_dev(stage, out * n_in, 700 + c, 0.0, 0.02)
+                ws.append(H.Weight.quantize_dev(stage.ptr, out, n_in, qt))
+            entry = {"copies": copies, "weight_bytes": wb}
+            for batch in (1, 8):
+                us = time_launches(ws, batch, max(200, min(4000, 2 * copies))) * 1e3
+                algo = wb + 4 * batch * (n_in + out)
+                gbs = algo / (us * 1e-6) / 1e9
+                entry[f"b{batch}"] = dict(us=round(us, 3), gbs=round(gbs, 1),
+                                          weight_gbs=round(wb / (us * 1e-6) / 1e9, 1),
+                                          pct_hbm_peak=round(100 * gbs / HBM_PEAK_GBS, 1))
+            for w in ws:
+                w.free()
+            row[H.TYPE_NAMES[qt]] = entry
+        res[f"{name}_{out}x{n_in}"] = row
+    stage.free()
+    b1 = res["mlp_up_gate_1536x576"]["q8_0"]["b1"]
+    print(f"[bench] per-shape: C1 q8_0 1536x576 b1 {b1['us']} us {b1['gbs']} GB/s", file=sys.stderr, flush=True)
+    return res
+
+
 QWEN_LAYER = W.QWEN_LAYER
 MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense bf16
 FP32_PEAK_TFLOPS = 157.3  # MI355X fp32 vector (packed); this build issues non-packed FMAs only
@@ -285,18 +361,27 @@ def prefill_flops(cfg, T):
     return 2 * T * L * per_layer + 2 * cfg["vocab_size"] * H + attn
 
 
-def decode_runs():
+def decode_runs(max_steps: int | None = None):
     """Full-model greedy decode on the synthetic models: prefill the prompt,
-    then the configured number of greedy steps; ids are checked against the
-    reference's (tests/golden)."""
+    then the configured number of greedy steps (at most max_steps, for
+    profiling runs); ids are checked against the reference's (tests/golden),
+    a shortened run against their prefix."""
     res = {}
     for key, golden, cfg, qt in DECODE_RUNS:
         with open(os.path.join(ROOT, "tests", "golden", golden + ".json")) as f:
             rec = json.load(f)
+        if max_steps is not None and max_steps < rec["n_steps"]:
+            rec = dict(rec, n_steps=max_steps, ids=rec["ids"][:max_steps])
+        H.synchronize()
+        t0 = time.perf_counter()
         m = H.synthetic_model_dev(cfg, rec["seed"], qt, rec["convention"])
+        H.synchronize()
+        load_s = time.perf_counter() - t0
         prompt = synth.uniform_ids(rec["prompt_seed"], rec["n_prompt"], cfg["vocab_size"])
         m.generate_greedy(prompt, 4)  # warm-up at the real prompt length (code objects, workspace)
+        t0 = time.perf_counter()
         ids = m.generate_greedy(prompt, rec["n_steps"])
+        gen_s = time.perf_counter() - t0
         pre_ms, dec_ms = m.last_timing()
         wb = m.weight_bytes()
         n_kv = cfg["num_layers"] * cfg["num_kv_heads"] * (cfg["hidden_size"] // cfg["num_heads"]) * 4 * 2
@@ -312,6 +397,11 @@ def decode_runs():
                         bytes_per_token=int(bytes_per_token), roofline_tok_s=round(roof, 1),
                         frac_of_roofline=round(tok_s / roof, 4),
                         ids_match_reference=bool(np.array_equal(ids, np.array(rec["ids"], np.int32))))
+        # llmi-generate --json's record (apps/llmi-generate/main.cpp:339-345); load = synthesising the
+        # fp32 weights on the device and quantizing them there (no checkpoint file exists here).
+        res[key]["generate_json"] = dict(prompt_ids=[int(i) for i in prompt], generated_ids=[int(i) for i in ids],
+                                         load_seconds=round(load_s, 3), generate_seconds=round(gen_s, 3),
+                                         weight_bytes=int(wb))
         print(f"[bench] {key}: prefill {pre_ms:.1f} ms, decode {tok_s:.1f} tok/s, ids match "
               f"{res[key]['ids_match_reference']}", file=sys.stderr, flush=True)
         res[key]["sampled"] = sampled_decode(m, prompt, rec, cfg)
@@ -450,36 +540,114 @@ def cpu_decode(runs, max_prompt: int = 128, steps: int = 16):
         print(f"[bench] {key} CPU: decode {steps / (t2 - t1):.2f} tok/s", file=sys.stderr, flush=True)
 
 
-def cpu_baseline(seconds_budget: float = 12.0):
-    """The reference's threaded CPU quant::matmul (oracle/_ref, built from the
-    reference sources) -- or, where its pool would exceed the 16 host cores
-    granted to one GPU, the oracle's restatement with a 16-thread pool -- on
-    full passes over the same SmolLM2 Q4_0 linear layers at batch 1."""
+def pick_cpu(max_threads: int = 16):
+    """The CPU implementation timed beside the GPU: the reference compiled
+    from its sources (oracle/_ref) when its pool (hardware_concurrency() - 1
+    workers, thread_pool.cpp) stays within `max_threads`, else the oracle's
+    restatement with a pool of max_threads - 1 workers."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as O
 
     ref = O.reference()
-    use_ref = ref is not None and ref.pool_workers() + 1 <= 16
-    cpu = ref if use_ref else O.oracle()
-    if not use_ref:
-        cpu.set_pool_workers(15)
-    kind = "reference" if use_ref else "port"
+    if ref is not None and ref.pool_workers() + 1 <= max_threads:
+        return O, ref, "reference"
+    cpu = O.oracle()
+    cpu.set_pool_workers(max_threads - 1)
+    return O, cpu, "port"
+
+
+def host_info():
+    """The CPU the baselines ran on: model string, os.cpu_count(), the CPUs
+    this process may run on, and std::thread::hardware_concurrency() (the
+    reference's pool size + 1)."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    ref = O.reference()
+    return dict(cpu_model=model, os_cpu_count=os.cpu_count(), affinity_cpus=len(os.sched_getaffinity(0)),
+                hardware_concurrency=None if ref is None else ref.pool_workers() + 1,
+                omp_num_threads=os.environ.get("OMP_NUM_THREADS"))
+
+
+def timed_calls(fn, seconds: float, min_calls: int = 3) -> float:
+    """Seconds per call of fn() over at least `seconds` and `min_calls`."""
+    fn()
+    n, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        n += 1
+        dt = time.perf_counter() - t0
+        if dt >= seconds and n >= min_calls:
+            return dt / n
+
+
+def cpu_per_shape(seconds_per_leg: float = 0.25):
+    """The reference's quant::matmul (a QuantizedMatrix kept alive between
+    calls) on each per-shape row, Q8_0 and Q4_0, batch 1 and 8; and C5's
+    dominant shape, gate_proj 4864x896 Q8_0 at M = 512."""
+    O, cpu, kind = pick_cpu()
+    res = {"kind": kind, "threads": cpu.pool_workers() + 1}
+    for name, out, n_in in REF_SHAPES:
+        row = {}
+        for qt in (H.Q8_0, H.Q4_0):
+            data, scales = cpu.quantize(synth.normal(600 + out, out * n_in, 0.0, 0.02), out, n_in, qt)
+            qm = cpu.qmatrix(data, scales, out, n_in, qt)
+            wb = weight_bytes_of(out, n_in, qt)
+            entry = {}
+            for batch in (1, 8):
+                x = synth.normal(601 + batch, batch * n_in, 0.0, 1.0)
+                y = np.zeros(batch * out, np.float32)
+                sec = timed_calls(lambda: qm.matmul(x, batch, y), seconds_per_leg)
+                entry[f"b{batch}"] = dict(us=round(sec * 1e6, 2),
+                                          gbs=round((wb + 4 * batch * (n_in + out)) / sec / 1e9, 2),
+                                          weight_gbs=round(wb / sec / 1e9, 2))
+            qm.close()
+            row[H.TYPE_NAMES[qt]] = entry
+        res[f"{name}_{out}x{n_in}"] = row
+    out, n_in, M = 4864, 896, 512
+    data, scales = cpu.quantize(synth.normal(602, out * n_in, 0.0, 0.02), out, n_in, H.Q8_0)
+    qm = cpu.qmatrix(data, scales, out, n_in, H.Q8_0)
+    x = synth.normal(603, M * n_in, 0.0, 1.0)
+    y = np.zeros(M * out, np.float32)
+    sec = timed_calls(lambda: qm.matmul(x, M, y), 1.0, min_calls=2)
+    qm.close()
+    res["c5_gate_proj_4864x896_q8_0_m512"] = dict(ms=round(sec * 1e3, 2),
+                                                  gflops=round(2.0 * M * out * n_in / sec / 1e9, 2))
+    return res
+
+
+def cpu_baseline(seconds_budget: float = 12.0, max_threads: int = 16):
+    """The reference's threaded CPU quant::matmul (oracle/_ref, built from the
+    reference sources) -- or, where its pool would exceed `max_threads`, the
+    oracle's restatement with a pool of that size -- on full passes over the
+    same SmolLM2 Q4_0 linear layers at batch 1, each matrix wrapped once
+    (a QuantizedMatrix kept alive) so a pass times quant::matmul alone."""
+    O, cpu, kind = pick_cpu(max_threads)
     shapes = SMOL_LAYER + [SMOL_HEAD]
     mats = []
     for j, (_, out, n_in) in enumerate(shapes):
         w = synth.normal(4000 + j, out * n_in, 0.0, 0.02)
         data, scales = cpu.quantize(w, out, n_in, O.Q4_0)
         x = synth.normal(5000 + j, n_in, 0.0, 1.0)
-        mats.append((out, n_in, data, scales, x))
+        mats.append((cpu.qmatrix(data, scales, out, n_in, O.Q4_0), x, np.zeros(out, np.float32)))
     layer_bytes = sum(algo_bytes(o, i, H.Q4_0, 1) for _, o, i in SMOL_LAYER)
     head_bytes = algo_bytes(SMOL_HEAD[1], SMOL_HEAD[2], H.Q4_0, 1)
 
     def one_pass():
         for _ in range(N_LAYERS):
-            for out, n_in, data, scales, x in mats[:-1]:
-                cpu.matmul(x, 1, n_in, data, scales, O.Q4_0, out)
-        out, n_in, data, scales, x = mats[-1]
-        cpu.matmul(x, 1, n_in, data, scales, O.Q4_0, out)
+            for qm, x, y in mats[:-1]:
+                qm.matmul(x, 1, y)
+        qm, x, y = mats[-1]
+        qm.matmul(x, 1, y)
 
     one_pass()  # warm-up
     t0 = time.perf_counter()
@@ -490,11 +658,45 @@ def cpu_baseline(seconds_budget: float = 12.0):
         if time.perf_counter() - t0 >= seconds_budget:
             break
     dt = time.perf_counter() - t0
+    for qm, _, _ in mats:
+        qm.close()
     step_bytes = N_LAYERS * layer_bytes + head_bytes
     threads = cpu.pool_workers() + 1
     return dict(value=round(passes * step_bytes / dt / 1e9, 3), unit="GB/s", cores=threads, kind=kind,
                 sample=f"{passes} full passes of the 211 SmolLM2 Q4_0 matvecs (batch 1), {dt:.1f} s",
                 ms_per_step=round(1e3 * dt / passes, 2))
+
+
+def cpu_leg_8():
+    """The cpu_baseline workload on CPUs 0-7 only (as `taskset -c 0-7`), 8
+    threads: comparable with the 8-CPU container the reference's fixtures
+    were recorded in.  Runs in a child process started before this process
+    touches the GPU."""
+    cpus = {c for c in range(8) if c in os.sched_getaffinity(0)}
+    os.sched_setaffinity(0, cpus)
+    r = cpu_baseline(seconds_budget=6.0, max_threads=8)
+    r["affinity"] = sorted(cpus)
+    print(json.dumps(r), flush=True)
+
+
+def cpu_legs_before_gpu():
+    """Every CPU leg that needs no GPU result, run before this process
+    initialises the GPU (the 8-CPU leg is a child process)."""
+    import subprocess
+
+    res = {"host": host_info()}
+    try:
+        child = subprocess.run([sys.executable, os.path.abspath(__file__), "--cpu-leg-8"], capture_output=True,
+                               text=True, timeout=300)
+        res["taskset_0_7"] = json.loads(child.stdout.strip().splitlines()[-1]) if child.returncode == 0 else {
+            "error": child.stderr[-300:]}
+    except (subprocess.SubprocessError, ValueError, IndexError) as e:
+        res["taskset_0_7"] = {"error": str(e)}
+    res["per_shape"] = cpu_per_shape()
+    res["baseline"] = cpu_baseline()
+    print(f"[bench] CPU: {res['baseline']['value']} GB/s ({res['baseline']['cores']} threads), 8 CPUs "
+          f"{res['taskset_0_7'].get('value')} GB/s", file=sys.stderr, flush=True)
+    return res
 
 
 def main():
@@ -511,12 +713,20 @@ def main():
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE readings")
     ap.add_argument("--no-graphs", action="store_true",
                     help="time the linear pass with plain launches only (for profilers that do not follow graphs)")
+    ap.add_argument("--no-shapes", action="store_true", help="skip the per-shape table (C1, C2 shapes)")
+    ap.add_argument("--decode-steps", type=int, default=None,
+                    help="cap the greedy decode runs at this many steps (profiling; ids checked as a prefix)")
+    ap.add_argument("--cpu-leg-8", action="store_true", help=argparse.SUPPRESS)
     args = ap.parse_args()
+    if args.cpu_leg_8:
+        cpu_leg_8()
+        return
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
               "it has no multi-GPU path to measure", file=sys.stderr)
         sys.exit(2)
 
+    cpu_early = None if args.no_cpu else cpu_legs_before_gpu()
     H.init(0)
     shapes = step_shapes()
     bytes_b1 = sum(algo_bytes(o, i, H.Q4_0, 1) for _, o, i in shapes)
@@ -554,13 +764,25 @@ def main():
         src.free()
         dst.free()
 
+    per_shape = {} if args.no_shapes else per_shape_gpu()
     targets = {} if args.no_targets else target_shapes()
-    decode = {} if args.no_decode else decode_runs()
+    decode = {} if args.no_decode else decode_runs(args.decode_steps)
     gemm = {} if args.no_gemm else prefill_gemm()
     gguf = gguf_upload()
-    cpu = None if args.no_cpu else cpu_baseline()
+    cpu = None
+    if cpu_early is not None:
+        cpu = dict(cpu_early["baseline"], host=cpu_early["host"], taskset_0_7=cpu_early["taskset_0_7"])
+        for key, row in cpu_early["per_shape"].items():
+            if key in per_shape:
+                for t, entry in row.items():
+                    per_shape[key].setdefault(t, {})["cpu"] = entry
+        per_shape["cpu_kind"] = cpu_early["per_shape"]["kind"]
+        per_shape["cpu_threads"] = cpu_early["per_shape"]["threads"]
+        if gemm:
+            gemm["cpu_gate_proj_m512"] = cpu_early["per_shape"]["c5_gate_proj_4864x896_q8_0_m512"]
     if decode and not args.no_cpu:
         cpu_decode(decode)
+    c1 = per_shape.get("mlp_up_gate_1536x576", {}).get("q8_0")
 
     line = {
         "metric": METRIC,
@@ -593,6 +815,10 @@ def main():
             "lm_head_single_launch": {"us": round(head_ms * 1e3, 3),
                                       "gbs": round(head_bytes / (head_ms * 1e-3) / 1e9, 1)},
         },
+        "c1_q8_0_1536x576": None if c1 is None else dict(
+            c1, workload="BASELINE.json configs[0]: one Q8_0 1536x576 matvec (SmolLM2 up/gate), batch 1; "
+                         "b8 = the same at batch 8"),
+        "per_shape": per_shape,
         "roofline": {
             "kernel": "qgemv_group (one launch = the 211 SmolLM2 Q4_0 matvecs of a step), batch 1",
             "bound": "hbm",
@@ -600,8 +826,8 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(value / HBM_PEAK_GBS, 4),
-            "traffic": GROUP_B1_HBM_BYTES,
-            "traffic_source": "rocprofv3 --pmc FETCH_SIZE/WRITE_SIZE, profiles/qgemv_group_smollm2_q4_b1.md",
+            "traffic": profiled_traffic(),
+            "traffic_source": f"rocprofv3 --pmc FETCH_SIZE/WRITE_SIZE of {HEADLINE_KERNEL}, {TRAFFIC_PROFILE}",
             "algorithmic_bytes_per_launch": bytes_b1,
             "mean_launch_us": round(step_ms * 1e3, 3),
         },

@@ -160,6 +160,12 @@ class Cpu:
             self._matmul(_p(x), rows, n_in, _p(data), _p(scales), qtype, out, _p(bias), _p(y), threads)
         return y
 
+    def qmatrix(self, data, scales, out: int, n_in: int, qtype: int) -> "QMatrix":
+        """A packed matrix held across calls, so that a timing loop measures
+        quant::matmul alone (the reference's QuantizedMatrix kept alive,
+        ref_shim.cpp; the restatement reads the arrays in place)."""
+        return QMatrix(self, data, scales, out, n_in, qtype)
+
     # -- glue kernels ------------------------------------------------------
     def dot(self, a, b) -> float:
         a = np.ascontiguousarray(a, np.float32)
@@ -281,6 +287,41 @@ class CpuModel:
 
 
 _cache: dict = {}
+
+
+class QMatrix:
+    """Cpu.qmatrix: y = x W^T on a matrix that stays wrapped between calls."""
+
+    def __init__(self, cpu: Cpu, data, scales, out: int, n_in: int, qtype: int):
+        self.cpu, self.out, self.n_in, self.qtype = cpu, out, n_in, qtype
+        self.data = np.ascontiguousarray(data, dtype=np.uint8)
+        self.scales = np.ascontiguousarray(scales, dtype=np.float32)
+        self.h = None
+        if cpu.prefix == "ref_":
+            L = cpu.lib
+            L.ref_qmatrix_create.restype = C.c_void_p
+            L.ref_qmatrix_create.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_size_t, C.c_int]
+            L.ref_qmatrix_matmul.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p, C.c_void_p]
+            L.ref_qmatrix_free.argtypes = [C.c_void_p]
+            self.h = L.ref_qmatrix_create(_p(self.data), _p(self.scales), out, n_in, qtype)
+
+    def matmul(self, x: np.ndarray, rows: int, y: np.ndarray) -> np.ndarray:
+        if self.h is not None:
+            self.cpu.lib.ref_qmatrix_matmul(self.h, _p(x), rows, None, _p(y))
+        else:
+            self.cpu._matmul.argtypes = [C.c_void_p, C.c_size_t, C.c_size_t, C.c_void_p, C.c_void_p, C.c_int,
+                                         C.c_size_t, C.c_void_p, C.c_void_p, C.c_int]
+            self.cpu._matmul(_p(x), rows, self.n_in, _p(self.data), _p(self.scales), self.qtype, self.out, None,
+                             _p(y), 0)
+        return y
+
+    def close(self) -> None:
+        if self.h is not None:
+            self.cpu.lib.ref_qmatrix_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
 
 
 def oracle() -> Cpu:
