@@ -1,0 +1,42 @@
+"""CPU checks of bench.py's host logic: the roofline traffic it reads from
+the committed rocprofv3 summary, and the one-GPU refusal."""
+
+import os
+import subprocess
+import sys
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+sys.path.insert(0, ROOT)
+
+import bench  # noqa: E402
+
+
+def test_traffic_comes_from_the_committed_profile():
+    t = bench.profiled_traffic()
+    assert isinstance(t, int)
+    shapes = bench.step_shapes()
+    algo = sum(bench.algo_bytes(o, i, bench.H.Q4_0, 1) for _, o, i in shapes)
+    # The counters read the packed weights once: within a few percent of the algorithmic bytes.
+    assert 0.9 * algo <= t <= 1.1 * algo
+
+
+def test_traffic_parser_reads_the_named_row(tmp_path):
+    p = tmp_path / "t.md"
+    p.write_text("| kernel | dispatches | HBM bytes (scaled) |\n|---|---|---|\n| `k<1>` | 3 | 1,234 |\n"
+                 "| `k<2>` | 3 | 99 |\n")
+    assert bench.profiled_traffic("k<2>", str(p)) == 99
+    assert bench.profiled_traffic("k<3>", str(p)) is None
+    assert bench.profiled_traffic("k<1>", str(tmp_path / "missing.md")) is None
+
+
+def test_more_than_one_gpu_is_refused():
+    r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"], capture_output=True, text=True,
+                       timeout=120)
+    assert r.returncode == 2
+    assert "one GPU" in r.stderr
+
+
+def test_weight_bytes_of_each_type():
+    assert bench.weight_bytes_of(4, 64, bench.H.F32) == 4 * 4 * 64
+    assert bench.weight_bytes_of(4, 64, bench.H.Q8_0) == 4 * 64 + 4 * 4 * 2
+    assert bench.weight_bytes_of(4, 64, bench.H.Q4_0) == 4 * 32 + 4 * 4 * 2
