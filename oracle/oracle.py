@@ -16,8 +16,11 @@ import os
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-ORACLE_SO = os.path.join(HERE, "liboracle.so")
-REF_SO = os.path.join(HERE, "_ref", "libllmi_ref.so")
+# LLMI_ORACLE_SANITIZED=1 loads the AddressSanitizer/UBSan builds
+# (make -C oracle sanitize) instead; the process must have libasan preloaded.
+_SAN = os.environ.get("LLMI_ORACLE_SANITIZED") == "1"
+ORACLE_SO = os.path.join(HERE, "_asan" if _SAN else "", "liboracle.so")
+REF_SO = os.path.join(HERE, "_ref", "asan" if _SAN else "", "libllmi_ref.so")
 
 F32, Q8_0, Q4_0 = 0, 1, 2
 BLOCK = 32
