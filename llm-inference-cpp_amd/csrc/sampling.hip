@@ -23,9 +23,13 @@
 // Kernels of one sampling call (temperature > 0), all on one stream:
 //   smp_max    max of logits / temperature (float division), NaN / +inf flags
 //   smp_exp    e = expf(x / T - max) (the exact expf), sum -> inv = float(1/sum)
-//   smp_scale  p = e * inv and the ranking keys (float bits, index), when
-//              something is filtered (else the later kernels scale e on the fly)
-//   [rocprim radix sort, descending, stable: std::stable_sort's order]
+//   when 0 < top_k <= kSelectMax (the ranking's first k):
+//     smp_sel_local  p = e * inv; each slice's first k, in index order
+//     smp_sel_merge  the first k among those, ranked
+//   else, when something is filtered (the whole ranking):
+//     smp_scale  p = e * inv and the ranking keys (float bits, index)
+//     [rocprim radix sort, descending, stable: std::stable_sort's order]
+//   (nothing filtered: the later kernels scale e on the fly)
 //   smp_keep   top-k, top-p, bounds on the renormalisation sum
 //   smp_draw   the filtered probabilities (bounded) and the first index whose
 //              running sum reaches target
@@ -142,24 +146,6 @@ __device__ __forceinline__ double block_sum_d(double v, double* red) {
   return r;
 }
 
-// Exclusive prefix of v over the block's threads in thread order (an
-// inclusive Hillis-Steele scan in LDS, read one slot back); *total = the sum.
-__device__ __forceinline__ double block_exclusive_scan(double v, double* sh, double* total) {
-  const int t = threadIdx.x;
-  sh[t] = v;
-  __syncthreads();
-  for (int off = 1; off < kSmpThreads; off <<= 1) {
-    const double add = t >= off ? sh[t - off] : 0.0;
-    __syncthreads();
-    sh[t] = sh[t] + add;
-    __syncthreads();
-  }
-  const double excl = t > 0 ? sh[t - 1] : 0.0;
-  *total = sh[kSmpThreads - 1];
-  __syncthreads();
-  return excl;
-}
-
 // Thread 0 publishes the block's partials (already stored; the release half
 // of the counter update makes them visible at agent scope) and learns whether
 // it is the last block of the grid to do so (the acquire half).  The last
@@ -200,21 +186,67 @@ __device__ __forceinline__ int first_block_reaching(const double* pre, int nb, d
   return block_min_i(c, red_i);
 }
 
+// Exclusive prefix of v over the block in thread order, as sums (wave
+// shuffles, then the wave totals: no subtraction, so every prefix is a tree
+// of the terms); *total = the sum.  wave_tot holds kSmpWaves doubles.
+__device__ __forceinline__ double block_exclusive_scan_w(double v, double* wave_tot, double* total) {
+  const int l = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  double incl = v;
+  for (int o = 1; o < 64; o <<= 1) {
+    const double u = __shfl_up(incl, o, 64);
+    if (l >= o) incl = incl + u;
+  }
+  double excl = __shfl_up(incl, 1, 64);
+  if (l == 0) excl = 0.0;
+  if (l == 63) wave_tot[wv] = incl;
+  __syncthreads();
+  double before = 0.0, tot = 0.0;
+  for (int q = 0; q < kSmpWaves; ++q) {
+    if (q < wv) before = before + wave_tot[q];
+    tot = tot + wave_tot[q];
+  }
+  __syncthreads();
+  *total = tot;
+  return before + excl;
+}
+
 // First j in [lo, hi) with (base + v(lo) + ... + v(j)) * factor >= t, or hi.
 // Every thread of the block takes part; the running sums are a tree over the
-// terms (a contiguous run per thread, then the block scan).
+// terms (a contiguous run per thread, then the block scan).  Runs of up to
+// kHeld terms are read once, every load issued before the first use (the
+// slice was written on another XCD: each dependent read would wait for HBM).
 template <typename F>
 __device__ int slice_first_reach(F v, int lo, int hi, double base, double factor, double t, double* sh, int* red_i) {
+  constexpr int kHeld = 8;
   const int len = hi - lo;
+  if (len <= 0) return hi;
   const int per = (len + kSmpThreads - 1) / kSmpThreads;
   const int a = lo + min(len, static_cast<int>(threadIdx.x) * per);
   const int e = min(hi, a + per);
+  int found = hi;
+  if (per <= kHeld) {
+    float x[kHeld];
+#pragma unroll
+    for (int q = 0; q < kHeld; ++q) {
+      const float val = v(min(a + q, hi - 1));
+      x[q] = a + q < e ? val : 0.0f;
+    }
+    double cs = 0.0;
+#pragma unroll
+    for (int q = 0; q < kHeld; ++q) cs = cs + static_cast<double>(x[q]);
+    double total;
+    double run = base + block_exclusive_scan_w(cs, sh, &total);
+#pragma unroll
+    for (int q = 0; q < kHeld; ++q) {
+      run = run + static_cast<double>(x[q]);
+      if (found == hi && a + q < e && run * factor >= t) found = a + q;
+    }
+    return block_min_i(found, red_i);
+  }
   double cs = 0.0;
   for (int j = a; j < e; ++j) cs = cs + static_cast<double>(v(j));
   double total;
-  const double excl = block_exclusive_scan(cs, sh, &total);
-  double run = base + excl;
-  int found = hi;
+  double run = base + block_exclusive_scan_w(cs, sh, &total);
   for (int j = a; j < e; ++j) {
     run = run + static_cast<double>(v(j));
     if (run * factor >= t) {
@@ -446,6 +478,210 @@ __global__ void __launch_bounds__(kSmpThreads) smp_argmax(const float* __restric
   }
 }
 
+// ------------------------------------------------------------ top-k selection
+// The first k entries of the ranking (p descending, equal p by index, the
+// order std::stable_sort gives sampling.cpp:30-34) without sorting all n, for
+// 0 < top_k <= kSelectMax.  Keys are the bits of p = e * inv (p >= +0, so
+// their unsigned order is p's order); a select finds the k-th largest key K
+// by four 8-bit radix passes over LDS histograms (integer counts: every
+// decision is exact) and keeps every key above K and the lowest-index entries
+// equal to it.  smp_sel_local does that per slice, writing the slice's first
+// k in index order; the ranking's first k are among those candidates, which
+// are then in index order overall, and smp_sel_merge selects again over them
+// and ranks the k it keeps.
+constexpr int kSelectMax = 64;
+constexpr int kCandMax = kSmpBlocks * kSelectMax;
+static_assert(kSmpThreads == 256, "one histogram bin per thread");
+
+__device__ __forceinline__ std::uint32_t key_bits(float p) { return __builtin_bit_cast(std::uint32_t, p); }
+
+// One radix step of a select.  hist[0..256) holds the counts of the next
+// digit among the keys under the prefix sel[0]; sel[1] keys are known to be
+// above that prefix.  Wave 0 finds the digit where the count from the top
+// first reaches `want` and appends it (lane l owns digits 255-4l .. 252-4l).
+// Call between barriers.
+__device__ __forceinline__ void radix_pick(const int* hist, int want, unsigned* sel) {
+  if (threadIdx.x >= 64) return;
+  const int l = threadIdx.x;
+  const unsigned prefix = sel[0];
+  const int above = static_cast<int>(sel[1]);
+  int c[4], s = 0;
+  for (int j = 0; j < 4; ++j) {
+    c[j] = hist[255 - 4 * l - j];
+    s += c[j];
+  }
+  int incl = s;
+  for (int o = 1; o < 64; o <<= 1) {
+    const int u = __shfl_up(incl, o, 64);
+    if (l >= o) incl += u;
+  }
+  int run = above + incl - s;
+  for (int j = 0; j < 4; ++j) {
+    if (run < want && run + c[j] >= want) {
+      sel[0] = (prefix << 8) | static_cast<unsigned>(255 - 4 * l - j);
+      sel[1] = static_cast<unsigned>(run);
+    }
+    run += c[j];
+  }
+}
+
+// Exclusive prefix over the block (kWaves wavefronts) of one count per
+// thread, in thread order; *total = the sum.  wave_tot holds kWaves ints.
+template <int kWaves>
+__device__ __forceinline__ int block_count_prefix(int v, int* wave_tot, int* total) {
+  const int l = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  int incl = v;
+  for (int o = 1; o < 64; o <<= 1) {
+    const int u = __shfl_up(incl, o, 64);
+    if (l >= o) incl += u;
+  }
+  if (l == 63) wave_tot[wv] = incl;
+  __syncthreads();
+  int r = incl - v, tot = 0;
+  for (int q = 0; q < kWaves; ++q) {
+    const int c = wave_tot[q];
+    if (q < wv) r += c;
+    tot += c;
+  }
+  __syncthreads();
+  *total = tot;
+  return r;
+}
+
+// Scales the slice (p = e * inv, the work of smp_scale) and writes its first
+// min(k, slice) entries of the ranking, in index order, to
+// keys / idx [b * kSelectMax, ...); their count to part_i[b].
+__global__ void __launch_bounds__(kSmpThreads) smp_sel_local(int n, int k, SmpWork w) {
+  __shared__ int hist[256];
+  __shared__ unsigned sel[2];
+  __shared__ int wave_tot[kSmpWaves];
+  if (w.st->flags & kFlagBad) return;
+  const Slice sl = slice_of(n, blockIdx.x, gridDim.x);
+  const int want = min(k, sl.hi - sl.lo);
+  const int t = threadIdx.x;
+  const float inv = w.st->inv;
+  if (t == 0) {
+    sel[0] = 0u;
+    sel[1] = 0u;
+  }
+  for (int pass = 0; pass < 4; ++pass) {
+    const int shift = 24 - 8 * pass;
+    hist[t] = 0;
+    __syncthreads();
+    const unsigned prefix = sel[0];
+    for (int i = sl.lo + t; i < sl.hi; i += kSmpThreads) {
+      std::uint32_t key;
+      if (pass == 0) {
+        const float p = w.p[i] * inv;
+        w.p[i] = p;
+        key = key_bits(p);
+      } else {
+        key = key_bits(w.p[i]);
+      }
+      if (pass == 0 || (key >> (shift + 8)) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1);
+    }
+    __syncthreads();
+    if (want > 0) radix_pick(hist, want, sel);
+    __syncthreads();
+  }
+  const std::uint32_t K = sel[0];
+  const int need = want - static_cast<int>(sel[1]);  // keys equal to K that are kept
+  std::uint32_t* keys = w.keys + blockIdx.x * kSelectMax;
+  std::int32_t* idx = w.idx + blockIdx.x * kSelectMax;
+  int above_done = 0, ties_done = 0;
+  for (int c0 = sl.lo; c0 < sl.hi; c0 += kSmpThreads) {
+    const int i = c0 + t;
+    const bool in = want > 0 && i < sl.hi;
+    const std::uint32_t key = in ? key_bits(w.p[i]) : 0u;
+    const bool above = in && key > K, tie = in && key == K;
+    // One exchange carries both counts: above in the high half, ties low.
+    int tot = 0;
+    const int before = block_count_prefix<kSmpWaves>((above ? 1 << 16 : 0) + (tie ? 1 : 0), wave_tot, &tot);
+    const int a_before = above_done + (before >> 16), t_before = ties_done + (before & 0xffff);
+    if (above || (tie && t_before < need)) {
+      const int pos = a_before + min(t_before, need);
+      keys[pos] = key;
+      idx[pos] = i;
+    }
+    above_done += tot >> 16;
+    ties_done += tot & 0xffff;
+  }
+  if (t == 0) w.part_i[blockIdx.x] = want;
+}
+
+// One workgroup: the select over every slice's candidates, each thread
+// holding a run of kRun slots in registers (vector loads, all issued at
+// once: the candidates come from other XCDs' workgroups), then the k kept,
+// ranked, into keys_sorted / idx_sorted.
+constexpr int kMergeThreads = 1024;
+__global__ void __launch_bounds__(kMergeThreads) smp_sel_merge(int k, SmpWork w) {
+  constexpr int kRun = kCandMax / kMergeThreads;
+  constexpr int kWaves = kMergeThreads / 64;
+  static_assert(kRun == 8 && kSelectMax % kRun == 0, "a thread's run is two 16-byte loads inside one slice");
+  __shared__ int hist[256];
+  __shared__ unsigned sel[2];
+  __shared__ int wave_tot[kWaves];
+  __shared__ std::uint32_t sk[kSelectMax];
+  __shared__ std::int32_t si[kSelectMax];
+  __shared__ int slot;
+  if (w.st->flags & kFlagBad) return;
+  const int t = threadIdx.x;
+  const int c_lo = t * kRun;
+  // Slots past a slice's count hold stale values and are never used.
+  const int valid = min(kRun, max(0, w.part_i[c_lo / kSelectMax] - c_lo % kSelectMax));
+  const auto* kp = reinterpret_cast<const uint4*>(w.keys + c_lo);
+  const auto* ip = reinterpret_cast<const uint4*>(w.idx + c_lo);
+  const uint4 k0 = kp[0], k1 = kp[1], i0 = ip[0], i1 = ip[1];
+  const std::uint32_t key[kRun] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
+  const std::int32_t id[kRun] = {static_cast<std::int32_t>(i0.x), static_cast<std::int32_t>(i0.y),
+                                 static_cast<std::int32_t>(i0.z), static_cast<std::int32_t>(i0.w),
+                                 static_cast<std::int32_t>(i1.x), static_cast<std::int32_t>(i1.y),
+                                 static_cast<std::int32_t>(i1.z), static_cast<std::int32_t>(i1.w)};
+  if (t == 0) {
+    sel[0] = 0u;
+    sel[1] = 0u;
+    slot = 0;
+  }
+  for (int pass = 0; pass < 4; ++pass) {
+    const int shift = 24 - 8 * pass;
+    if (t < 256) hist[t] = 0;
+    __syncthreads();
+    const unsigned prefix = sel[0];
+#pragma unroll
+    for (int j = 0; j < kRun; ++j)
+      if (j < valid && (pass == 0 || (key[j] >> (shift + 8)) == prefix)) atomicAdd(&hist[(key[j] >> shift) & 255u], 1);
+    __syncthreads();
+    radix_pick(hist, k, sel);
+    __syncthreads();
+  }
+  const std::uint32_t K = sel[0];
+  const int need = k - static_cast<int>(sel[1]);
+  int my_ties = 0;
+#pragma unroll
+  for (int j = 0; j < kRun; ++j) my_ties += (j < valid && key[j] == K) ? 1 : 0;
+  int tot = 0;
+  int tie_rank = block_count_prefix<kWaves>(my_ties, wave_tot, &tot);  // the candidates are in index order
+#pragma unroll
+  for (int j = 0; j < kRun; ++j) {
+    bool keep = j < valid && key[j] > K;
+    if (j < valid && key[j] == K) keep = tie_rank++ < need;
+    if (keep) {
+      const int q = atomicAdd(&slot, 1);
+      sk[q] = key[j];
+      si[q] = id[j];
+    }
+  }
+  __syncthreads();
+  if (t < k) {
+    const std::uint32_t kt = sk[t];
+    const std::int32_t it = si[t];
+    int r = 0;
+    for (int q = 0; q < k; ++q) r += (sk[q] > kt || (sk[q] == kt && si[q] < it)) ? 1 : 0;
+    w.keys_sorted[r] = kt;
+    w.idx_sorted[r] = it;
+  }
+}
+
 // Top-k and top-p (sampling.cpp:28-51) over the first m ranked values
 // (m = k; `vals` is the ranking, or the unranked p when nothing is
 // filtered: then m = n and every entry is kept), and the bounds on the
@@ -672,7 +908,9 @@ int smp_reserve(std::size_t n, hipStream_t s) {
                                               static_cast<const std::int32_t*>(nullptr),
                                               static_cast<std::int32_t*>(nullptr), static_cast<unsigned>(n), 0, 32, s));
   auto al = [](std::size_t b) { return (b + 255) & ~static_cast<std::size_t>(255); };
-  const std::size_t vec = al(n * 4);
+  // The top-k selection writes up to kCandMax candidates into keys / idx.
+  const std::size_t vn = n > static_cast<std::size_t>(kCandMax) ? n : static_cast<std::size_t>(kCandMax);
+  const std::size_t vec = al(vn * 4);
   const std::size_t bytes = 7 * vec + al(sizeof(double) * 2 * kSmpBlocks) + al(sizeof(int) * 2 * kSmpBlocks) +
                             al(sizeof(float) * kSmpBlocks) + al(sizeof(SmpState)) + al(sizeof(std::int32_t));
   LLMI_TRY_HIP(hipMalloc(&g_smp.base, bytes));
@@ -689,13 +927,13 @@ int smp_reserve(std::size_t n, hipStream_t s) {
     return r;
   };
   SmpWork& w = g_smp.w;
-  w.p = static_cast<float*>(take(n * 4));
-  w.keys = static_cast<std::uint32_t*>(take(n * 4));
-  w.keys_sorted = static_cast<std::uint32_t*>(take(n * 4));
-  w.idx = static_cast<std::int32_t*>(take(n * 4));
-  w.idx_sorted = static_cast<std::int32_t*>(take(n * 4));
-  g_smp.host_io = static_cast<float*>(take(n * 4));
-  (void)take(n * 4);  // spare
+  w.p = static_cast<float*>(take(vn * 4));
+  w.keys = static_cast<std::uint32_t*>(take(vn * 4));
+  w.keys_sorted = static_cast<std::uint32_t*>(take(vn * 4));
+  w.idx = static_cast<std::int32_t*>(take(vn * 4));
+  w.idx_sorted = static_cast<std::int32_t*>(take(vn * 4));
+  g_smp.host_io = static_cast<float*>(take(vn * 4));
+  (void)take(vn * 4);  // spare
   w.part_d = static_cast<double*>(take(sizeof(double) * 2 * kSmpBlocks));
   w.part_i = static_cast<int*>(take(sizeof(int) * 2 * kSmpBlocks));
   w.part_f = static_cast<float*>(take(sizeof(float) * kSmpBlocks));
@@ -732,7 +970,14 @@ int smp_front(const float* logits, std::size_t n, const llmi_hip_sampling& cfg, 
   smp_max<<<kSmpBlocks, kSmpThreads, 0, s>>>(logits, ni, cfg.temperature, w);
   smp_exp<<<kSmpBlocks, kSmpThreads, 0, s>>>(logits, ni, cfg.temperature, w);
   LLMI_TRY_HIP(hipGetLastError());
-  if (*ranked) {
+  if (*ranked && k < n && k <= static_cast<std::size_t>(kSelectMax)) {
+    // Only the first k of the ranking are read: select them.
+    const int ki = static_cast<int>(k);
+    smp_sel_local<<<kSmpBlocks, kSmpThreads, 0, s>>>(ni, ki, w);
+    smp_sel_merge<<<1, kMergeThreads, 0, s>>>(ki, w);
+    smp_keep<<<kSmpBlocks, kSmpThreads, 0, s>>>(reinterpret_cast<const float*>(w.keys_sorted), w.idx_sorted, ki, ni,
+                                                cfg.top_p, 1, w);
+  } else if (*ranked) {
     smp_scale<<<static_cast<unsigned>(ceil_div(n, kSmpThreads)), kSmpThreads, 0, s>>>(ni, w, 1);
     if (int rc = smp_sort(n, s)) return rc;
     smp_keep<<<kSmpBlocks, kSmpThreads, 0, s>>>(reinterpret_cast<const float*>(w.keys_sorted), w.idx_sorted,

@@ -80,6 +80,22 @@ def test_probabilities_and_draws_match_oracle(kind, n):
             assert H.sample(lg, cfg, t) == o.sample_target(lg, temp, top_k, top_p, t), (temp, top_k, top_p, t)
 
 
+@pytest.mark.parametrize("kind", ["normal", "masked", "ties"])
+@pytest.mark.parametrize("n", [70, 4100, 8193, 151936])
+def test_top_k_around_the_selection_limit(kind, n):
+    """top_k up to 64 takes the per-slice selection, 65 and above the full
+    sort; ties and zero probabilities straddle the k-th entry, and slices
+    hold fewer entries than k when n is small."""
+    o = O.oracle()
+    for k in (2, 63, 64, 65):
+        lg = logits_case(kind, n, 7 * n + k)
+        want = o.sampling_probabilities(lg, 1.0, k, 1.0)
+        assert np.array_equal(bits(H.sampling_probabilities(lg, H.Sampling(1.0, k, 1.0))), bits(want)), k
+        assert np.count_nonzero(want) <= k
+        for t in o.draw_uniform(k, 4):
+            assert H.sample(lg, H.Sampling(1.0, k, 0.9), t) == o.sample_target(lg, 1.0, k, 0.9, t), (k, t)
+
+
 @pytest.mark.parametrize("cfg", [(1.0, 0, 1.0), (0.8, 40, 0.9), (0.6, 0, 0.95), (1.0, 1000, 1.0)])
 def test_qwen_vocabulary(cfg):
     """151936 entries (Qwen2.5's vocabulary), device-resident logits."""
