@@ -128,12 +128,15 @@ def time_steps(wset, batch, steps, warmup, mode="group"):
     """GPU time of `steps` passes over the rotating weight copies.
 
     mode "group": each pass is ONE llmi_hip_group launch holding its copy's
-    211 products; "graph": one HIP graph replay of 211 single-matrix
-    launches; "plain": 211 single-matrix launches from Python."""
+    211 products; "tol": the same products as one tolerance-mode group
+    (llmi_hip_tol_group: the activation split kernel + one product launch);
+    "graph": one HIP graph replay of 211 single-matrix launches; "plain": 211
+    single-matrix launches from Python."""
     xs, ys, keep = activations(wset.shapes, batch, 77)
     n = len(wset.copies)
-    if mode == "group":
-        gs = [H.Group([(w, x.ptr, y.ptr, batch) for w, x, y in zip(ws, xs, ys)]) for ws in wset.copies]
+    if mode in ("group", "tol"):
+        kind = H.Group if mode == "group" else H.TolGroup
+        gs = [kind([(w, x.ptr, y.ptr, batch) for w, x, y in zip(ws, xs, ys)]) for ws in wset.copies]
         run = lambda i: gs[i % n].launch()  # noqa: E731
     elif mode == "graph":
         gs = [H.Graph(lambda ws=ws: run_step(ws, xs, ys, batch)) for ws in wset.copies]
@@ -153,7 +156,7 @@ def time_steps(wset, batch, steps, warmup, mode="group"):
     return ms
 
 
-def time_launches(weights, batch, launches):
+def time_launches(weights, batch, launches, tol=False):
     """Mean GPU time per launch of `launches` back-to-back launches (cycling
     through the rotating weight copies) between one pair of HIP events on
     the library stream.  Includes the ~2 us stream dispatch gap between
@@ -162,12 +165,14 @@ def time_launches(weights, batch, launches):
     xb = H.DeviceBuffer(batch * n_in * 4)
     H.synth_normal_dev(xb, batch * n_in, 5, 0.0, 1.0)
     yb = H.DeviceBuffer(batch * out * 4)
-    weights[0].matmul_dev(xb.ptr, batch, None, yb.ptr)  # warm-up (code load)
+    call = (lambda w: w.matmul_tol_dev(xb.ptr, batch, None, yb.ptr)) if tol else \
+        (lambda w: w.matmul_dev(xb.ptr, batch, None, yb.ptr))
+    call(weights[0])  # warm-up (code load)
     H.synchronize()
     t = H.Timer()
     t.start()
     for i in range(launches):
-        weights[(i + 1) % len(weights)].matmul_dev(xb.ptr, batch, None, yb.ptr)
+        call(weights[(i + 1) % len(weights)])
     ms = t.stop()
     H.synchronize()
     return ms / launches

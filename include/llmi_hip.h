@@ -201,6 +201,26 @@ int llmi_hip_group_create(const llmi_hip_weight* const* w, const float* const* x
 int llmi_hip_group_launch(const llmi_hip_group* group, void* stream);
 void llmi_hip_group_free(llmi_hip_group* group);
 
+/* Tolerance mode, Q4_0: quant::matmul (quant.cpp:119-153) for batch 1..8
+ * with the products summed on the matrix cores in another order than the
+ * reference's chains.  NOT bit-exact: |y - y_ref| <= 1e-4 * max|y_ref| (the
+ * fp32-accumulate tolerance of the path's contract; measured ~1e-6), with
+ * finite x below ~3e38.  The codes enter as exact bf16 values, x as two bf16
+ * parts (16 significant bits), sums in fp32.  Same arguments and meaning as
+ * llmi_hip_matmul_dev (rows 1..8, in <= ~14k); llmi_hip_tol_group_* run a
+ * list of such products as one launch, as llmi_hip_group_* do for the exact
+ * kernel.  The exact
+ * entry points stay the default everywhere: the model's decode and the
+ * reference-signature layer never take this one. */
+typedef struct llmi_hip_tol_group llmi_hip_tol_group;
+int llmi_hip_matmul_tol_dev(const llmi_hip_weight* weight, const float* x_dev, size_t rows, const float* bias_dev,
+                            float* y_dev, void* stream);
+int llmi_hip_tol_group_create(const llmi_hip_weight* const* w, const float* const* x_dev, const size_t* rows,
+                              const float* const* bias_dev, float* const* y_dev, size_t count,
+                              llmi_hip_tol_group** out);
+int llmi_hip_tol_group_launch(const llmi_hip_tol_group* group, void* stream);
+void llmi_hip_tol_group_free(llmi_hip_tol_group* group);
+
 /* Prefill GEMM on the matrix cores: quant::matmul (quant.cpp:119-153) as the
  * reference's prefill calls it with rows = T tokens (transformer.cpp:245-291),
  * computed with x and the dequantized weights rounded to bf16 and fp32

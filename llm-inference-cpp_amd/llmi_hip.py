@@ -69,6 +69,10 @@ SIGNATURES = {
     "llmi_hip_gemm_group_create": (_i, [_vp, _vp, _vp, _vp, _vp, _sz, C.POINTER(_vp)]),
     "llmi_hip_gemm_group_launch": (_i, [_vp, _vp]),
     "llmi_hip_gemm_group_free": (None, [_vp]),
+    "llmi_hip_matmul_tol_dev": (_i, [_vp, _vp, _sz, _vp, _vp, _vp]),
+    "llmi_hip_tol_group_create": (_i, [_vp, _vp, _vp, _vp, _vp, _sz, C.POINTER(_vp)]),
+    "llmi_hip_tol_group_launch": (_i, [_vp, _vp]),
+    "llmi_hip_tol_group_free": (None, [_vp]),
     "llmi_hip_dot_dev": (_i, [_vp, _vp, _vp, _sz, _vp, _vp]),
     "llmi_hip_rmsnorm_dev": (_i, [_vp, _vp, _sz, _sz, _f, _vp, _vp]),
     "llmi_hip_softmax_dev": (_i, [_vp, _sz, _sz, _vp]),
@@ -267,6 +271,22 @@ class Weight:
 
     def matmul_mfma_dev(self, x_dev: int, rows: int, bias_dev: int | None, y_dev: int, stream=None) -> None:
         check(self.lib.llmi_hip_matmul_mfma_dev(self.h, x_dev, rows, bias_dev, y_dev, stream))
+
+    def matmul_tol_dev(self, x_dev: int, rows: int, bias_dev: int | None, y_dev: int, stream=None) -> None:
+        check(self.lib.llmi_hip_matmul_tol_dev(self.h, x_dev, rows, bias_dev, y_dev, stream))
+
+    def matmul_tol(self, x: np.ndarray, rows: int, bias: np.ndarray | None = None) -> np.ndarray:
+        """The tolerance-mode Q4_0 product (matrix cores) on host arrays."""
+        xd = DeviceBuffer.from_array(np.ascontiguousarray(x, dtype=np.float32))
+        yd = DeviceBuffer(max(1, rows * self.out) * 4)
+        bd = None if bias is None else DeviceBuffer.from_array(np.ascontiguousarray(bias, dtype=np.float32))
+        self.matmul_tol_dev(xd.ptr, rows, None if bd is None else bd.ptr, yd.ptr)
+        synchronize()
+        y = yd.download(np.float32, rows * self.out)
+        for b in (xd, yd, bd):
+            if b is not None:
+                b.free()
+        return y
 
     def matmul_mfma(self, x: np.ndarray, rows: int, bias: np.ndarray | None = None) -> np.ndarray:
         """The bf16-MFMA prefill product on host arrays (tolerance, not exact)."""
@@ -581,6 +601,13 @@ class GemmGroup(Group):
     launched together (llmi_hip_gemm_group_*)."""
 
     _create, _launch, _free = "llmi_hip_gemm_group_create", "llmi_hip_gemm_group_launch", "llmi_hip_gemm_group_free"
+
+
+class TolGroup(Group):
+    """A list of tolerance-mode Q4_0 products (Weight, x, y, rows, bias)
+    launched together (llmi_hip_tol_group_*)."""
+
+    _create, _launch, _free = "llmi_hip_tol_group_create", "llmi_hip_tol_group_launch", "llmi_hip_tol_group_free"
 
 
 class Graph:
