@@ -156,6 +156,34 @@ def time_steps(wset, batch, steps, warmup, mode="group"):
     return ms
 
 
+def tolerance_check(wset):
+    """Largest |y_tol - y_exact| / max|y_exact| over the 211 products of one
+    copy, batch 1 and 8 (the exact kernel's outputs equal the reference's)."""
+    worst = 0.0
+    ws = wset.copies[0]
+    for batch in (1, 8):
+        xs, ys, keep = activations(wset.shapes, batch, 77)
+        yt = {id(w): H.DeviceBuffer(batch * out * 4) for (_, out, _), w in zip(wset.shapes, ws)}
+        gt = H.TolGroup([(w, x.ptr, yt[id(w)].ptr, batch) for w, x in zip(ws, xs)])
+        gt.launch()
+        H.synchronize()
+        # The exact group's products of one shape share a y buffer, so each
+        # product's exact output comes from a launch of its own.
+        for (_, out, _), w, x in zip(wset.shapes, ws, xs):
+            ye = H.DeviceBuffer(batch * out * 4)
+            w.matmul_dev(x.ptr, batch, None, ye.ptr)
+            H.synchronize()
+            a = ye.download(np.float32, batch * out).astype(np.float64)
+            b = yt[id(w)].download(np.float32, batch * out).astype(np.float64)
+            worst = max(worst, float(np.abs(a - b).max() / max(np.abs(a).max(), 1e-30)))
+            ye.free()
+        gt.free()
+        for b in yt.values():
+            b.free()
+        del keep
+    return worst
+
+
 def time_launches(weights, batch, launches, tol=False):
     """Mean GPU time per launch of `launches` back-to-back launches (cycling
     through the rotating weight copies) between one pair of HIP events on
@@ -196,6 +224,11 @@ def target_shapes():
         gbs = algo_bytes(out, n_in, qt, 1) / (ms * 1e-3) / 1e9
         res[f"qwen_{name}_{H.TYPE_NAMES[qt]}_{out}x{n_in}"] = dict(us=round(ms * 1e3, 2), gbs=round(gbs, 1),
                                                                   pct_hbm_peak=round(100 * gbs / HBM_PEAK_GBS, 1))
+        if qt == H.Q4_0:
+            ms = time_launches(ws, 1, min(200, 2 * copies), tol=True)
+            gbs = algo_bytes(out, n_in, qt, 1) / (ms * 1e-3) / 1e9
+            res[f"qwen_{name}_{H.TYPE_NAMES[qt]}_{out}x{n_in}_tolerance_mode"] = dict(
+                us=round(ms * 1e3, 2), gbs=round(gbs, 1), pct_hbm_peak=round(100 * gbs / HBM_PEAK_GBS, 1))
         for w in ws:
             w.free()
     if stage is not None:
@@ -214,14 +247,15 @@ def grouped_mlp_targets(steps=50):
     for qt in (H.Q4_0, H.Q8_0):
         wb = sum(o * H.row_bytes(i, qt) + 4 * o * H.nblocks(i) for _, o, i in shapes)
         wset = WeightSet(shapes, qt, max(2, -(-ROTATE_BYTES // wb)), 31)
-        ms = time_steps(wset, 1, steps, 5, mode="group")
+        for mode in ("group", "tol") if qt == H.Q4_0 else ("group",):
+            ms = time_steps(wset, 1, steps, 5, mode=mode)
+            us = ms / steps * 1e3
+            gbs = sum(algo_bytes(o, i, qt, 1) for _, o, i in shapes) / (us * 1e-6) / 1e9
+            key = f"qwen_mlp_24_layers_grouped_{H.TYPE_NAMES[qt]}" + ("_tolerance_mode" if mode == "tol" else "")
+            res[key] = dict(us=round(us, 2), gbs=round(gbs, 1), pct_hbm_peak=round(100 * gbs / HBM_PEAK_GBS, 1))
+            print(f"[bench] Qwen MLP x24 grouped {H.TYPE_NAMES[qt]} {mode}: {us:.1f} us, {gbs:.0f} GB/s",
+                  file=sys.stderr, flush=True)
         wset.free()
-        us = ms / steps * 1e3
-        gbs = sum(algo_bytes(o, i, qt, 1) for _, o, i in shapes) / (us * 1e-6) / 1e9
-        res[f"qwen_mlp_24_layers_grouped_{H.TYPE_NAMES[qt]}"] = dict(
-            us=round(us, 2), gbs=round(gbs, 1), pct_hbm_peak=round(100 * gbs / HBM_PEAK_GBS, 1))
-        print(f"[bench] Qwen MLP x24 grouped {H.TYPE_NAMES[qt]}: {us:.1f} us, {gbs:.0f} GB/s", file=sys.stderr,
-              flush=True)
     return res
 
 
@@ -744,6 +778,8 @@ def main():
 
     ms_b1 = time_steps(wset, 1, args.steps, args.warmup, mode="group")
     ms_b8 = time_steps(wset, 8, max(1, args.steps // 4), args.warmup, mode="group")
+    ms_b1_tol = time_steps(wset, 1, args.steps, args.warmup, mode="tol")
+    ms_b8_tol = time_steps(wset, 8, max(1, args.steps // 4), args.warmup, mode="tol")
     n_single = max(1, args.steps // 10)
     ms_b1_graph = None if args.no_graphs else time_steps(wset, 1, n_single, 2, mode="graph")
     ms_b1_plain = time_steps(wset, 1, n_single, 2, mode="plain")
@@ -752,6 +788,11 @@ def main():
     b8_step_ms = ms_b8 / max(1, args.steps // 4)
     print(f"[bench] grouped b1 {step_ms * 1e3:.1f} us/step {value:.1f} GB/s; b8 {b8_step_ms * 1e3:.1f} us/step",
           file=sys.stderr, flush=True)
+
+    tol_b1_us = ms_b1_tol / args.steps * 1e3
+    tol_b8_us = ms_b8_tol / max(1, args.steps // 4) * 1e3
+    print(f"[bench] tolerance mode b1 {tol_b1_us:.1f} us/step; b8 {tol_b8_us:.1f} us/step", file=sys.stderr, flush=True)
+    tol_err = tolerance_check(wset)
 
     heads = [ws[-1] for ws in wset.copies]
     head_ms = time_launches(heads, 1, 2 * len(heads) * 4)
@@ -835,6 +876,19 @@ def main():
             "traffic_source": f"rocprofv3 --pmc FETCH_SIZE/WRITE_SIZE of {HEADLINE_KERNEL}, {TRAFFIC_PROFILE}",
             "algorithmic_bytes_per_launch": bytes_b1,
             "mean_launch_us": round(step_ms * 1e3, 3),
+        },
+        "tolerance_mode": {
+            "what": "the same products through llmi_hip_tol_group (Q4_0 on the matrix cores, another summation "
+                    "order): the fp32-accumulate contract max|y - y_ref| <= 1e-4 * max|y_ref|, not bit-exact; the "
+                    "exact path above stays the default and the value of this line",
+            "c2_b1": {"us_per_step": round(tol_b1_us, 2), "gbs": round(bytes_b1 / tol_b1_us / 1e3, 1),
+                      "pct_hbm_peak": round(100 * bytes_b1 / tol_b1_us / 1e3 / HBM_PEAK_GBS, 1)},
+            "c2_b8": {"us_per_step": round(tol_b8_us, 2), "gbs": round(bytes_b8 / tol_b8_us / 1e3, 1),
+                      "pct_hbm_peak": round(100 * bytes_b8 / tol_b8_us / 1e3 / HBM_PEAK_GBS, 1)},
+            "max_rel_error_vs_exact": tol_err,
+            "roofline": {"kernel": "qgemv_tol_small<1> (the 211 products of a step), batch 1", "bound": "hbm",
+                         "achieved": round(bytes_b1 / tol_b1_us / 1e3, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(bytes_b1 / tol_b1_us / 1e3 / HBM_PEAK_GBS, 4)},
         },
         "targets_qwen25": targets,
         "decode": decode,

@@ -206,6 +206,7 @@ int llmi_hip_shutdown(void) {
   // The library's own workspaces (model, weight and group handles belong to
   // their callers).
   release_sampling_workspace();
+  release_tol_workspace();
   if (g_gemm_scratch.p != nullptr) (void)hipFree(g_gemm_scratch.p);
   g_gemm_scratch = Scratch{};
   g_stream = nullptr;

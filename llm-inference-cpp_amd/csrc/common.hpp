@@ -254,6 +254,8 @@ int launch_gate_up_silu(const DeviceMatrix& gate, const DeviceMatrix& up, const 
                         float* y, hipStream_t s, bool* fused);
 // Frees the sampling workspace (llmi_hip_shutdown; the stream is idle).
 void release_sampling_workspace();
+// Frees the tolerance-mode product's split activations (likewise).
+void release_tol_workspace();
 
 // sample() on device logits (sampling.hip); *id_host receives the index and
 // `also` (device, may be null) too, on the stream.

@@ -39,6 +39,7 @@
 // not wait for HBM.  Lanes outside the active pattern read zero slots.
 #include <algorithm>
 #include <memory>
+#include <utility>
 #include <vector>
 
 #include "common.hpp"
@@ -50,6 +51,7 @@ namespace {
 typedef unsigned int tu32x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 tbf16x8 __attribute__((ext_vector_type(8)));
 typedef float tf32x4 __attribute__((ext_vector_type(4)));
+typedef float tf32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kSlotsPerBlock = 8;  // 16-byte slots per row and block: 4 words x 2 parts
 constexpr int kTolChunk = 4;       // blocks whose code loads are in flight per wavefront
@@ -62,6 +64,22 @@ struct TolProblem {
   float* y;
   const float* x;
   int in, nblk, out, rows, ntiles, bpw, accumulate, first_wg;
+};
+
+// The split activations a batch of three to eight rows reads (tol_split's
+// output for the product's input), kept apart from TolProblem so that the
+// small batches' kernel carries no unused fields.
+struct TolSplit {
+  const tu32x4* xs;  // [row][block][word][part]
+  const float* sx;   // 24 * block sums of the split activations, [row][block]
+};
+
+// One distinct activation matrix of a launch, split once by tol_split.
+struct TolInput {
+  const float* x;
+  tu32x4* xs;
+  float* sx;
+  int rows, in, nblk;
 };
 
 __device__ __forceinline__ std::uint32_t bf16_bits_rne(float f) {
@@ -103,15 +121,49 @@ __device__ __forceinline__ tbf16x8 decode_word(std::uint32_t w, const TolMagic& 
   return __builtin_bit_cast(tbf16x8, r);
 }
 
-// One 64-row tile of one product for input rows [r0, r0 + nr), nr <= R.
-// The workgroup's wavefronts split the tile's blocks, bpw each; each
+// tol_split: one workgroup per input (inputs[blockIdx.x], or `single` when
+// inputs is null) writes, for every row and block, the two bf16 parts of the
+// 32 activations in the MFMA's k order ([row][block][word][part] 16-byte
+// slots) and 24 * the sum of the block's x' = hi + lo (elements past `in`
+// are zero).  Used by the batches of three to eight rows, whose workgroups
+// would otherwise each split eight rows again.
+__global__ void __launch_bounds__(256) tol_split(const TolInput* __restrict__ inputs, TolInput single) {
+  const TolInput t = inputs != nullptr ? inputs[blockIdx.x] : single;
+  const int total = t.rows * t.nblk;
+  for (int rb = threadIdx.x; rb < total; rb += blockDim.x) {
+    const int r = rb / t.nblk, b = rb - r * t.nblk;
+    const float* xr = t.x + static_cast<std::size_t>(r) * t.in + static_cast<std::size_t>(b) * kBlock;
+    const int len = min(kBlock, t.in - b * kBlock);
+    float sum = 0.0f;
+    tu32x4* dst = t.xs + static_cast<std::size_t>(rb) * kSlotsPerBlock;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      std::uint32_t hi[8], lo[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int i = 8 * q + (e >> 1) + 4 * (e & 1);
+        const float v = i < len ? xr[i] : 0.0f;
+        hi[e] = bf16_bits_rne(v);
+        lo[e] = bf16_bits_rne(v - bf16_value(hi[e]));
+        sum += bf16_value(hi[e]) + bf16_value(lo[e]);
+      }
+      dst[2 * q] = tu32x4{hi[0] | (hi[1] << 16), hi[2] | (hi[3] << 16), hi[4] | (hi[5] << 16), hi[6] | (hi[7] << 16)};
+      dst[2 * q + 1] = tu32x4{lo[0] | (lo[1] << 16), lo[2] | (lo[3] << 16), lo[4] | (lo[5] << 16), lo[6] | (lo[7] << 16)};
+    }
+    t.sx[rb] = 24.0f * sum;
+  }
+}
+
+// qgemv_tol_small (batches of one or two rows, v_mfma_f32_16x16x32_bf16): one
+// 64-row tile of one product for input rows [r0, r0 + nr), nr <= R.  The
+// workgroup's wavefronts split the tile's blocks, bpw each; each
 // wavefront splits the activations of its own blocks into its own LDS region
 // (no workgroup barrier before the products; LDS operations of one wavefront
 // complete in order).  Region of wavefront w: kZeroSlots zero slots (the A
 // operand of inactive lanes; every wavefront writes the same zeros), then
 // [row][block][word][part] 16-byte slots, then 24 * sx per row and block.
 template <int R>
-__global__ void __launch_bounds__(1024) qgemv_tol(const TolProblem* __restrict__ probs,
+__global__ void __launch_bounds__(1024) qgemv_tol_small(const TolProblem* __restrict__ probs,
                                                   const std::uint32_t* __restrict__ wg_prob, TolProblem single) {
   constexpr int kSets = (R + 1) / 2;
   extern __shared__ tu32x4 lds[];
@@ -291,30 +343,213 @@ __global__ void __launch_bounds__(1024) qgemv_tol(const TolProblem* __restrict__
     }
   }
 }
+// The MFMA shapes.  Batches of one or two rows take v_mfma_f32_16x16x32_bf16
+// (rows of the tile in groups of 16, the four m of a group = two input rows x
+// two activation parts); batches of three to eight take
+// v_mfma_f32_32x32x16_bf16 (groups of 32 rows, the sixteen m of a group =
+// eight input rows x two parts), half the A reads and MFMAs per row.
+//   16x16x32: A[m][k] at lane m + 16(k/8); B[k][n] at lane n + 16(k/8);
+//             D[m][n] at lane n + 16(m/4), register m%4.
+//   32x32x16: A[m][k] at lane m + 32(k/8); B[k][n] at lane n + 32(k/8);
+//             D[m][n] at lane n + 32((m/4)%2), register 4(m/8) + m%4.
+// With B = the codes of word q of lane l's own row, k-slice g = l/16 (l/32)
+// carries row 16g + n (32g + n) and A[m][k] is nonzero only for k in the
+// slice of m's group, so every lane receives its own row's sums.
+// This lane's A-operand role: active, its activation part and input row.
+template <bool K32>
+__device__ __forceinline__ void a_role(int lane, bool* active, int* part, int* row) {
+  if (K32) {
+    const int m = lane & 31;
+    *active = ((m >> 2) & 1) == (lane >> 5);
+    *part = (m >> 3) & 1;
+    *row = 4 * (m >> 4) + (m & 3);
+  } else {
+    const int m = lane & 15;
+    *active = (m >> 2) == (lane >> 4);
+    *part = m & 1;
+    *row = (m >> 1) & 1;
+  }
+}
+
+constexpr int wide_chunk(int R) { return R == 8 ? 2 : kTolChunk; }
+
+// qgemv_tol_wide (batches of three to eight rows, v_mfma_f32_32x32x16_bf16):
+// one 64-row tile of one product for input rows [r0, r0 + nr), nr <= R.  The
+// workgroup's wavefronts split the tile's blocks, bpw each, and walk them in
+// chunks of kTolChunk.  Each wavefront copies the current chunk's split
+// activations (tol_split's) into its own LDS region -- no workgroup barrier
+// before the products; LDS operations of one wavefront complete in order --
+// and loads the next chunk's activations and codes while it computes this
+// one.  Region of a wavefront: kZeroSlots zero slots (the A operand of
+// inactive lanes; every wavefront writes the same zeros), the chunk's
+// [row][block][word][part] 16-byte slots, then 24 * sx per row and block of
+// the chunk.
+template <int R>
+__global__ void __launch_bounds__(1024) qgemv_tol_wide(const TolProblem* __restrict__ probs,
+                                                       const TolSplit* __restrict__ splits,
+                                                       const std::uint32_t* __restrict__ wg_prob, TolProblem single,
+                                                       TolSplit single_split) {
+  static_assert(R == 4 || R == 8, "batches of three to eight rows");
+  constexpr int kC = wide_chunk(R);  // blocks per chunk (registers: eight rows keep fewer in flight)
+  constexpr int kRegionSlots = kZeroSlots + R * kC * kSlotsPerBlock;
+  extern __shared__ tu32x4 lds[];
+  const int wg = blockIdx.x;
+  TolProblem p = single;
+  TolSplit sp = single_split;
+  if (probs != nullptr) {
+    const int idx = __builtin_amdgcn_readfirstlane(static_cast<int>(wg_prob[wg]));
+    p = probs[idx];
+    sp = splits[idx];
+  }
+  const int local = wg - p.first_wg;
+  const int tile = local % p.ntiles;
+  const int r0 = (local / p.ntiles) * R;
+  const int nr = min(R, p.rows - r0);
+  const int nblk = p.nblk, bpw = p.bpw;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  const int nwaves = blockDim.x >> 6;
+  const int b_begin = wave * bpw, b_end = min(nblk, b_begin + bpw);
+
+  const std::size_t tbase = static_cast<std::size_t>(tile) * nblk * kTileRows + lane;
+  const TGMEM tu32x4* codes = (const TGMEM tu32x4*)p.codes + tbase;
+  const TGMEM float* scales = (const TGMEM float*)p.scales + tbase;
+  const TGMEM tu32x4* xsrc = (const TGMEM tu32x4*)sp.xs + static_cast<std::size_t>(r0) * nblk * kSlotsPerBlock;
+  const TGMEM float* sxsrc = (const TGMEM float*)sp.sx + static_cast<std::size_t>(r0) * nblk;
+
+  tu32x4* wl = lds + static_cast<std::size_t>(wave) * kRegionSlots;
+  float* wsx = reinterpret_cast<float*>(lds + static_cast<std::size_t>(nwaves) * kRegionSlots) + wave * R * kC;
+  float* red = reinterpret_cast<float*>(lds + static_cast<std::size_t>(nwaves) * kRegionSlots) + nwaves * R * kC;
+
+  // Copy of a chunk starting at block c: slot i (of R rows x kC blocks
+  // x 8) = row i / 32, slot i % 32 of the row's chunk (contiguous in
+  // tol_split's layout); lane l copies slots l + 64 k, and lane l < 4R one
+  // block sum.  Blocks past the wavefront's range are not read (their slots
+  // are never used).
+  constexpr int kCopy = R * kC * kSlotsPerBlock / 64;
+  tu32x4 xs[kCopy];
+  float sxv;
+  const auto load_chunk_x = [&](int c) {
+#pragma unroll
+    for (int k = 0; k < kCopy; ++k) {
+      const int i = lane + 64 * k, r = i / (kC * kSlotsPerBlock), off = i % (kC * kSlotsPerBlock);
+      const bool ok = r < nr && c + (off >> 3) < b_end;
+      xs[k] = ok ? xsrc[(static_cast<std::size_t>(r) * nblk + c) * kSlotsPerBlock + off] : tu32x4{0u, 0u, 0u, 0u};
+    }
+    const int r = lane / kC, jb = lane % kC;
+    sxv = (lane < kC * R && r < nr && c + jb < b_end) ? sxsrc[static_cast<std::size_t>(r) * nblk + c + jb] : 0.0f;
+  };
+  const auto stage_chunk = [&]() {
+#pragma unroll
+    for (int k = 0; k < kCopy; ++k) wl[kZeroSlots + lane + 64 * k] = xs[k];
+    if (lane < kC * R) wsx[lane] = sxv;
+  };
+
+  // This lane's A operand: slot base + jb * step + 2q of the chunk's block
+  // jb, word q (inactive lanes: step 0, base 0 -- a zero slot).
+  bool active;
+  int part, arow;
+  a_role<true>(lane, &active, &part, &arow);
+  const bool on = active && arow < nr;
+  const int base = on ? kZeroSlots + arow * kC * kSlotsPerBlock + part : 0;
+  const int step = on ? kSlotsPerBlock : 0;
+  const TolMagic mk = tol_magic();
+
+  float acc[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) acc[r] = 0.0f;
+
+  if (b_begin < b_end) {
+    // The first chunk: activations first, then codes (loads complete in
+    // order, so waiting for the activations does not wait for HBM).
+    load_chunk_x(b_begin);
+    tu32x4 cur_c[kC];
+    float cur_s[kC];
+#pragma unroll
+    for (int j = 0; j < kC; ++j) {
+      const std::size_t bc = static_cast<std::size_t>(min(b_begin + j, b_end - 1));
+      cur_c[j] = __builtin_nontemporal_load(codes + bc * kTileRows);
+      cur_s[j] = __builtin_nontemporal_load(scales + bc * kTileRows);
+    }
+    if (lane < kZeroSlots) wl[lane] = tu32x4{0u, 0u, 0u, 0u};
+    for (int b = b_begin; b < b_end; b += kC) {
+      stage_chunk();
+      // The next chunk's activations, then its codes.
+      const int bn = b + kC;
+      tu32x4 nxt_c[kC];
+      float nxt_s[kC];
+      if (bn < b_end) {
+        load_chunk_x(bn);
+#pragma unroll
+        for (int j = 0; j < kC; ++j) {
+          const std::size_t bc = static_cast<std::size_t>(min(bn + j, b_end - 1));
+          nxt_c[j] = __builtin_nontemporal_load(codes + bc * kTileRows);
+          nxt_s[j] = __builtin_nontemporal_load(scales + bc * kTileRows);
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < kC; ++j) {
+        if (b + j >= b_end) break;
+        tf32x16 d{};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const tbf16x8 bq = decode_word(cur_c[j][q], mk);
+          const tbf16x8 aq = __builtin_bit_cast(tbf16x8, wl[base + j * step + 2 * q]);
+          d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(aq, bq, d, 0, 0, 0);
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+          if (r < nr) {
+            const int rh = 8 * (r >> 2) + (r & 3);
+            const float blk = __builtin_fmaf(16.0f, d[rh] + d[rh + 4], -wsx[r * kC + j]);
+            acc[r] = __builtin_fmaf(blk, cur_s[j], acc[r]);
+          }
+      }
+      if (bn < b_end) {
+#pragma unroll
+        for (int j = 0; j < kC; ++j) {
+          cur_c[j] = nxt_c[j];
+          cur_s[j] = nxt_s[j];
+        }
+      }
+    }
+  }
+
+  // The wavefronts' partial sums of each row, added in wavefront order.
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+    if (r < nr) red[(wave * R + r) * kTileRows + lane] = acc[r];
+  __syncthreads();
+  const std::size_t o = static_cast<std::size_t>(tile) * kTileRows + lane;
+  for (int r = wave; r < nr; r += nwaves) {
+    float v = red[r * kTileRows + lane];
+    for (int w2 = 1; w2 < nwaves; ++w2) v += red[(w2 * R + r) * kTileRows + lane];
+    if (o < static_cast<std::size_t>(p.out)) {
+      TGMEM float* y = (TGMEM float*)p.y + static_cast<std::size_t>(r0 + r) * p.out;
+      const float bias = p.bias != nullptr ? p.bias[o] : 0.0f;
+      y[o] = p.accumulate ? y[o] + (v + bias) : v + bias;
+    }
+  }
+}
 
 // ------------------------------------------------------------ planning
-
-constexpr std::size_t kTolLdsBudget = 32 * 1024;
 
 // Wavefronts per tile: about kTolChunk blocks each, at most 16.
 int tol_waves(std::size_t nblk) {
   return static_cast<int>(std::clamp<std::size_t>(ceil_div(nblk, kTolChunk), 1, 16));
 }
-// LDS of one workgroup: per wavefront its zero slots, split activations and
-// block sums (R rows x bpw blocks), then the reduction area.
+// LDS of one workgroup.  qgemv_tol_small: per wavefront its zero slots and
+// the split activations and block sums of its bpw blocks; qgemv_tol_wide: per
+// wavefront its zero slots and one chunk's (kTolChunk blocks); both then the
+// reduction area.
 std::size_t tol_lds(int waves, int R, int bpw) {
+  const std::size_t blocks = R <= 2 ? static_cast<std::size_t>(bpw) : static_cast<std::size_t>(wide_chunk(R));
   return static_cast<std::size_t>(waves) *
-             ((kZeroSlots + static_cast<std::size_t>(R) * bpw * kSlotsPerBlock) * sizeof(tu32x4) +
-              static_cast<std::size_t>(R) * bpw * sizeof(float)) +
-         static_cast<std::size_t>(waves) * R * kTileRows * sizeof(float);
+         ((kZeroSlots + static_cast<std::size_t>(R) * blocks * kSlotsPerBlock) * sizeof(tu32x4) +
+          static_cast<std::size_t>(R) * blocks * sizeof(float) + static_cast<std::size_t>(R) * kTileRows * sizeof(float));
 }
-// Row chunk R (1, 2, 4, 8): the smallest covering `rows`, halved while the
-// staged activations exceed the budget.
-int tol_chunk(std::size_t rows, std::size_t nblk) {
-  int r = rows <= 1 ? 1 : rows <= 2 ? 2 : rows <= 4 ? 4 : 8;
-  while (r > 1 && std::min<std::size_t>(rows, r) * nblk * kSlotsPerBlock * sizeof(tu32x4) > kTolLdsBudget) r /= 2;
-  return r;
-}
+// Row chunk R (1, 2, 4, 8): the smallest covering `rows`.
+int tol_chunk(std::size_t rows) { return rows <= 1 ? 1 : rows <= 2 ? 2 : rows <= 4 ? 4 : 8; }
 
 struct TolLaunch {
   int rchunk = 1, waves = 1, total_wgs = 0;
@@ -322,9 +557,12 @@ struct TolLaunch {
 };
 
 struct TolPlan {
+  std::vector<TolInput> inputs;  // inputs of the batches of 3..8 (xs / sx: scratch offsets until bound)
   std::vector<TolProblem> probs;
+  std::vector<TolSplit> splits;  // parallel to probs
   std::vector<std::uint32_t> wg_prob;
   std::vector<TolLaunch> launches;
+  std::size_t scratch_bytes = 0;
 };
 
 int plan_tol(const GroupEntry* entries, std::size_t count, TolPlan* plan) {
@@ -337,30 +575,59 @@ int plan_tol(const GroupEntry* entries, std::size_t count, TolPlan* plan) {
     LLMI_REQUIRE(e.rows >= 1 && e.rows <= 8, "tolerance matmul: each product takes 1..8 input rows");
     const DeviceMatrix& m = *e.m;
     LLMI_REQUIRE(m.in > 0 && m.in <= (1u << 20) && m.out <= 0x7FFFFFFFu, "tolerance matmul: bad shape");
-    LLMI_REQUIRE(tol_lds(16, 1, static_cast<int>(ceil_div(m.nblk, 16))) <= max_lds_per_block(),
+    LLMI_REQUIRE(tol_lds(16, 2, static_cast<int>(ceil_div(m.nblk, 16))) <= max_lds_per_block(),
                  "tolerance matmul: rows too long");
   }
+  // Distinct inputs of the batches of three to eight rows, split once.
+  std::vector<std::size_t> input_of(count, 0);
+  for (std::size_t i = 0; i < count; ++i) {
+    const GroupEntry& e = entries[i];
+    if (tol_chunk(e.rows) <= 2 || e.m->out == 0) continue;
+    std::size_t k = plan->inputs.size();
+    for (std::size_t j = 0; j < plan->inputs.size(); ++j)
+      if (plan->inputs[j].x == e.x) {
+        LLMI_REQUIRE(plan->inputs[j].rows == static_cast<int>(e.rows) && plan->inputs[j].in == static_cast<int>(e.m->in),
+                     "tolerance matmul: one x used with two shapes");
+        k = j;
+      }
+    if (k == plan->inputs.size()) {
+      TolInput t{};
+      t.x = e.x;
+      t.rows = static_cast<int>(e.rows);
+      t.in = static_cast<int>(e.m->in);
+      t.nblk = static_cast<int>(e.m->nblk);
+      const std::size_t slots = e.rows * e.m->nblk;
+      t.xs = reinterpret_cast<tu32x4*>(plan->scratch_bytes);
+      plan->scratch_bytes += slots * kSlotsPerBlock * sizeof(tu32x4);
+      t.sx = reinterpret_cast<float*>(plan->scratch_bytes);
+      plan->scratch_bytes += (slots * sizeof(float) + 255) & ~std::size_t{255};
+      plan->inputs.push_back(t);
+    }
+    input_of[i] = k;
+  }
   for (int R : {1, 2, 4, 8}) {
-    std::vector<TolProblem> probs;
+    std::vector<std::pair<TolProblem, TolSplit>> probs;
     int waves = 1;
     std::size_t biggest = 0, lds = 0;
     for (std::size_t i = 0; i < count; ++i) {
       const GroupEntry& e = entries[i];
       const DeviceMatrix& m = *e.m;
-      if (m.out == 0 || tol_chunk(e.rows, m.nblk) != R) continue;
+      if (m.out == 0 || tol_chunk(e.rows) != R) continue;
       TolProblem p{};
       p.codes = m.codes;
       p.scales = m.scales;
       p.bias = e.bias;
       p.y = e.y;
       p.x = e.x;
+      TolSplit sp{};
+      if (R > 2) sp = TolSplit{plan->inputs[input_of[i]].xs, plan->inputs[input_of[i]].sx};
       p.in = static_cast<int>(m.in);
       p.nblk = static_cast<int>(m.nblk);
       p.out = static_cast<int>(m.out);
       p.rows = static_cast<int>(e.rows);
       p.ntiles = static_cast<int>(m.ntiles);
       p.accumulate = e.accumulate ? 1 : 0;
-      probs.push_back(p);
+      probs.emplace_back(p, sp);
       const std::size_t bytes = m.code_bytes + m.scale_bytes;
       if (bytes > biggest) {
         biggest = bytes;
@@ -369,7 +636,8 @@ int plan_tol(const GroupEntry* entries, std::size_t count, TolPlan* plan) {
     }
     if (probs.empty()) continue;
     // Longest workgroups first, as in the exact grouped launch.
-    std::stable_sort(probs.begin(), probs.end(), [](const TolProblem& a, const TolProblem& b) { return a.nblk > b.nblk; });
+    std::stable_sort(probs.begin(), probs.end(),
+                     [](const auto& a, const auto& b) { return a.first.nblk > b.first.nblk; });
     TolLaunch l;
     l.rchunk = R;
     l.waves = waves;
@@ -377,7 +645,7 @@ int plan_tol(const GroupEntry* entries, std::size_t count, TolPlan* plan) {
     l.map_offset = plan->wg_prob.size();
     std::size_t wg = 0;
     for (std::size_t j = 0; j < probs.size(); ++j) {
-      TolProblem& p = probs[j];
+      TolProblem& p = probs[j].first;
       p.bpw = static_cast<int>(ceil_div(p.nblk, waves));
       p.first_wg = static_cast<int>(wg);
       const std::size_t wgs = static_cast<std::size_t>(p.ntiles) * ceil_div(p.rows, R);
@@ -389,21 +657,39 @@ int plan_tol(const GroupEntry* entries, std::size_t count, TolPlan* plan) {
     LLMI_REQUIRE(lds <= max_lds_per_block(), "tolerance matmul: a product needs more LDS than one workgroup may use");
     l.lds = lds;
     l.total_wgs = static_cast<int>(wg);
-    plan->probs.insert(plan->probs.end(), probs.begin(), probs.end());
+    for (const auto& [p, sp] : probs) {
+      plan->probs.push_back(p);
+      plan->splits.push_back(sp);
+    }
     plan->launches.push_back(l);
   }
   return LLMI_OK;
 }
 
-int launch_tol_kernel(const TolLaunch& l, const TolProblem* probs, const std::uint32_t* map, const TolProblem& single,
-                      hipStream_t s) {
+// Scratch offsets -> device addresses.
+void bind_tol(TolPlan* plan, std::uint8_t* scratch) {
+  const auto at = [scratch](const void* off) { return scratch + reinterpret_cast<std::size_t>(off); };
+  for (TolInput& t : plan->inputs) {
+    t.xs = reinterpret_cast<tu32x4*>(at(t.xs));
+    t.sx = reinterpret_cast<float*>(at(t.sx));
+  }
+  for (std::size_t i = 0; i < plan->splits.size(); ++i)
+    if (plan->probs[i].rows > 2) {  // tol_chunk > 2: the split is read
+      TolSplit& sp = plan->splits[i];
+      sp.xs = reinterpret_cast<const tu32x4*>(at(sp.xs));
+      sp.sx = reinterpret_cast<const float*>(at(sp.sx));
+    }
+}
+
+int launch_tol_kernel(const TolLaunch& l, const TolProblem* probs, const TolSplit* splits, const std::uint32_t* map,
+                      const TolProblem& single, const TolSplit& single_split, hipStream_t s) {
   if (l.total_wgs == 0) return LLMI_OK;
   const dim3 grid(static_cast<unsigned>(l.total_wgs)), block(static_cast<unsigned>(l.waves * 64));
   switch (l.rchunk) {
-    case 1: qgemv_tol<1><<<grid, block, l.lds, s>>>(probs, map, single); break;
-    case 2: qgemv_tol<2><<<grid, block, l.lds, s>>>(probs, map, single); break;
-    case 4: qgemv_tol<4><<<grid, block, l.lds, s>>>(probs, map, single); break;
-    default: qgemv_tol<8><<<grid, block, l.lds, s>>>(probs, map, single); break;
+    case 1: qgemv_tol_small<1><<<grid, block, l.lds, s>>>(probs, map, single); break;
+    case 2: qgemv_tol_small<2><<<grid, block, l.lds, s>>>(probs, map, single); break;
+    case 4: qgemv_tol_wide<4><<<grid, block, l.lds, s>>>(probs, splits, map, single, single_split); break;
+    default: qgemv_tol_wide<8><<<grid, block, l.lds, s>>>(probs, splits, map, single, single_split); break;
   }
   LLMI_TRY_HIP(hipGetLastError());
   return LLMI_OK;
@@ -418,11 +704,15 @@ using namespace llmi_hip;
 // workgroup map.
 struct llmi_hip_tol_group {
   void* table = nullptr;
+  std::uint8_t* scratch = nullptr;  // split activations of the batches of 3..8
+  const TolInput* inputs = nullptr;
   const TolProblem* probs = nullptr;
+  const TolSplit* splits = nullptr;
   const std::uint32_t* map = nullptr;
   TolPlan plan;
   ~llmi_hip_tol_group() {
     if (table != nullptr) (void)hipFree(table);
+    if (scratch != nullptr) (void)hipFree(scratch);
   }
 };
 
@@ -439,7 +729,21 @@ int tol_entries(const llmi_hip_weight* const* w, const float* const* x, const si
   return LLMI_OK;
 }
 
+// The single-product entry keeps its split activations here (grow-only).
+struct TolWorkspace {
+  std::uint8_t* scratch = nullptr;
+  std::size_t bytes = 0;
+};
+TolWorkspace g_tol_ws;
+
 }  // namespace
+
+namespace llmi_hip {
+void release_tol_workspace() {
+  if (g_tol_ws.scratch != nullptr) (void)hipFree(g_tol_ws.scratch);
+  g_tol_ws = TolWorkspace{};
+}
+}  // namespace llmi_hip
 
 extern "C" {
 
@@ -453,15 +757,25 @@ int llmi_hip_tol_group_create(const llmi_hip_weight* const* w, const float* cons
   if (int rc = tol_entries(w, x_dev, rows, bias_dev, y_dev, count, &entries)) return rc;
   auto g = std::make_unique<llmi_hip_tol_group>();
   if (int rc = plan_tol(entries.data(), count, &g->plan)) return rc;
+  if (g->plan.scratch_bytes > 0) {
+    LLMI_TRY_HIP(hipMalloc(reinterpret_cast<void**>(&g->scratch), g->plan.scratch_bytes));
+    bind_tol(&g->plan, g->scratch);
+  }
+  const std::size_t ib = g->plan.inputs.size() * sizeof(TolInput);
   const std::size_t pb = g->plan.probs.size() * sizeof(TolProblem);
+  const std::size_t sb = g->plan.splits.size() * sizeof(TolSplit);
   const std::size_t mb = g->plan.wg_prob.size() * sizeof(std::uint32_t);
-  if (pb + mb > 0) {
-    LLMI_TRY_HIP(hipMalloc(&g->table, pb + mb));
+  if (ib + pb + sb + mb > 0) {
+    LLMI_TRY_HIP(hipMalloc(&g->table, ib + pb + sb + mb));
     auto* base = static_cast<std::uint8_t*>(g->table);
-    if (pb > 0) LLMI_TRY_HIP(hipMemcpy(base, g->plan.probs.data(), pb, hipMemcpyHostToDevice));
-    if (mb > 0) LLMI_TRY_HIP(hipMemcpy(base + pb, g->plan.wg_prob.data(), mb, hipMemcpyHostToDevice));
-    g->probs = reinterpret_cast<const TolProblem*>(base);
-    g->map = reinterpret_cast<const std::uint32_t*>(base + pb);
+    if (ib > 0) LLMI_TRY_HIP(hipMemcpy(base, g->plan.inputs.data(), ib, hipMemcpyHostToDevice));
+    if (pb > 0) LLMI_TRY_HIP(hipMemcpy(base + ib, g->plan.probs.data(), pb, hipMemcpyHostToDevice));
+    if (sb > 0) LLMI_TRY_HIP(hipMemcpy(base + ib + pb, g->plan.splits.data(), sb, hipMemcpyHostToDevice));
+    if (mb > 0) LLMI_TRY_HIP(hipMemcpy(base + ib + pb + sb, g->plan.wg_prob.data(), mb, hipMemcpyHostToDevice));
+    g->inputs = reinterpret_cast<const TolInput*>(base);
+    g->probs = reinterpret_cast<const TolProblem*>(base + ib);
+    g->splits = reinterpret_cast<const TolSplit*>(base + ib + pb);
+    g->map = reinterpret_cast<const std::uint32_t*>(base + ib + pb + sb);
   }
   *out = g.release();
   return LLMI_OK;
@@ -470,8 +784,13 @@ int llmi_hip_tol_group_create(const llmi_hip_weight* const* w, const float* cons
 int llmi_hip_tol_group_launch(const llmi_hip_tol_group* g, void* stream) {
   LLMI_REQUIRE_INIT();
   LLMI_REQUIRE(g != nullptr, "tolerance matmul: null group");
+  if (!g->plan.inputs.empty()) {
+    tol_split<<<static_cast<unsigned>(g->plan.inputs.size()), 256, 0, pick(stream)>>>(g->inputs, TolInput{});
+    LLMI_TRY_HIP(hipGetLastError());
+  }
   for (const TolLaunch& l : g->plan.launches)
-    if (int rc = launch_tol_kernel(l, g->probs + l.prob_offset, g->map + l.map_offset, TolProblem{}, pick(stream)))
+    if (int rc = launch_tol_kernel(l, g->probs + l.prob_offset, g->splits + l.prob_offset, g->map + l.map_offset,
+                                   TolProblem{}, TolSplit{}, pick(stream)))
       return rc;
   return LLMI_OK;
 }
@@ -486,10 +805,22 @@ int llmi_hip_matmul_tol_dev(const llmi_hip_weight* weight, const float* x_dev, s
   TolPlan plan;
   if (int rc = plan_tol(&e, 1, &plan)) return rc;
   if (plan.launches.empty()) return LLMI_OK;
-  // One product: its descriptor travels as a kernel argument.
+  // One product: its descriptor (and the split's) travel as kernel arguments.
+  const hipStream_t s = pick(stream);
+  if (plan.scratch_bytes > 0) {
+    if (plan.scratch_bytes > g_tol_ws.bytes) {
+      LLMI_TRY_HIP(hipStreamSynchronize(s));
+      release_tol_workspace();
+      LLMI_TRY_HIP(hipMalloc(reinterpret_cast<void**>(&g_tol_ws.scratch), plan.scratch_bytes));
+      g_tol_ws.bytes = plan.scratch_bytes;
+    }
+    bind_tol(&plan, g_tol_ws.scratch);
+    tol_split<<<1, 256, 0, s>>>(nullptr, plan.inputs[0]);
+    LLMI_TRY_HIP(hipGetLastError());
+  }
   TolProblem p = plan.probs[0];
   p.first_wg = 0;
-  return launch_tol_kernel(plan.launches[0], nullptr, nullptr, p, pick(stream));
+  return launch_tol_kernel(plan.launches[0], nullptr, nullptr, nullptr, p, plan.splits[0], s);
 }
 
 }  // extern "C"
