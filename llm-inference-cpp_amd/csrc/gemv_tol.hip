@@ -371,7 +371,11 @@ __device__ __forceinline__ void a_role(int lane, bool* active, int* part, int* r
   }
 }
 
-constexpr int wide_chunk(int R) { return R == 8 ? 2 : kTolChunk; }
+// Blocks per chunk of qgemv_tol_wide: one -- each block's MFMAs, sixteen
+// accumulators and a batch's partial sums fill the registers, and fewer
+// blocks in flight per wavefront buy more wavefronts per SIMD (batch 8 on
+// MI355X: 43.4 us per SmolLM2 step with two, 35.5 with one).
+constexpr int wide_chunk(int) { return 1; }
 
 // qgemv_tol_wide (batches of three to eight rows, v_mfma_f32_32x32x16_bf16):
 // one 64-row tile of one product for input rows [r0, r0 + nr), nr <= R.  The
@@ -426,14 +430,15 @@ __global__ void __launch_bounds__(1024) qgemv_tol_wide(const TolProblem* __restr
   // tol_split's layout); lane l copies slots l + 64 k, and lane l < 4R one
   // block sum.  Blocks past the wavefront's range are not read (their slots
   // are never used).
-  constexpr int kCopy = R * kC * kSlotsPerBlock / 64;
+  constexpr int kChunkSlots = R * kC * kSlotsPerBlock;
+  constexpr int kCopy = (kChunkSlots + 63) / 64;
   tu32x4 xs[kCopy];
   float sxv;
   const auto load_chunk_x = [&](int c) {
 #pragma unroll
     for (int k = 0; k < kCopy; ++k) {
       const int i = lane + 64 * k, r = i / (kC * kSlotsPerBlock), off = i % (kC * kSlotsPerBlock);
-      const bool ok = r < nr && c + (off >> 3) < b_end;
+      const bool ok = i < kChunkSlots && r < nr && c + (off >> 3) < b_end;
       xs[k] = ok ? xsrc[(static_cast<std::size_t>(r) * nblk + c) * kSlotsPerBlock + off] : tu32x4{0u, 0u, 0u, 0u};
     }
     const int r = lane / kC, jb = lane % kC;
@@ -441,7 +446,8 @@ __global__ void __launch_bounds__(1024) qgemv_tol_wide(const TolProblem* __restr
   };
   const auto stage_chunk = [&]() {
 #pragma unroll
-    for (int k = 0; k < kCopy; ++k) wl[kZeroSlots + lane + 64 * k] = xs[k];
+    for (int k = 0; k < kCopy; ++k)
+      if (lane + 64 * k < kChunkSlots) wl[kZeroSlots + lane + 64 * k] = xs[k];
     if (lane < kC * R) wsx[lane] = sxv;
   };
 
