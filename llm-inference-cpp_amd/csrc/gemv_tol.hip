@@ -79,7 +79,7 @@ struct TolInput {
   const float* x;
   tu32x4* xs;
   float* sx;
-  int rows, in, nblk;
+  int rows, in, nblk, first_word;  // first_word: this input's first word in tol_split's grid
 };
 
 __device__ __forceinline__ std::uint32_t bf16_bits_rne(float f) {
@@ -121,37 +121,49 @@ __device__ __forceinline__ tbf16x8 decode_word(std::uint32_t w, const TolMagic& 
   return __builtin_bit_cast(tbf16x8, r);
 }
 
-// tol_split: one workgroup per input (inputs[blockIdx.x], or `single` when
-// inputs is null) writes, for every row and block, the two bf16 parts of the
-// 32 activations in the MFMA's k order ([row][block][word][part] 16-byte
-// slots) and 24 * the sum of the block's x' = hi + lo (elements past `in`
-// are zero).  Used by the batches of three to eight rows, whose workgroups
-// would otherwise each split eight rows again.
-__global__ void __launch_bounds__(256) tol_split(const TolInput* __restrict__ inputs, TolInput single) {
-  const TolInput t = inputs != nullptr ? inputs[blockIdx.x] : single;
-  const int total = t.rows * t.nblk;
-  for (int rb = threadIdx.x; rb < total; rb += blockDim.x) {
-    const int r = rb / t.nblk, b = rb - r * t.nblk;
-    const float* xr = t.x + static_cast<std::size_t>(r) * t.in + static_cast<std::size_t>(b) * kBlock;
-    const int len = min(kBlock, t.in - b * kBlock);
-    float sum = 0.0f;
-    tu32x4* dst = t.xs + static_cast<std::size_t>(rb) * kSlotsPerBlock;
+// tol_split: for every row and block of each input, the two bf16 parts of
+// the 32 activations in the MFMA's k order ([row][block][word][part]
+// 16-byte slots) and 24 * the sum of the block's x' = hi + lo (elements past
+// `in` are zero).  Used by the batches of three to eight rows, whose
+// workgroups would otherwise each split eight rows again.  One thread per
+// word (8 activations); a quad of lanes adds its block's four word sums in a
+// fixed order.  Grid: the inputs laid end to end, each starting at a
+// multiple of 256 words (inputs[i].first_word), so workgroup g splits words
+// of input wg_input[g] only; `single` stands for the tables when inputs is
+// null.
+__global__ void __launch_bounds__(256) tol_split(const TolInput* __restrict__ inputs,
+                                                 const std::uint32_t* __restrict__ wg_input, TolInput single) {
+  const int gw = blockIdx.x * blockDim.x + threadIdx.x;
+  const TolInput t =
+      inputs != nullptr ? inputs[__builtin_amdgcn_readfirstlane(static_cast<int>(wg_input[blockIdx.x]))] : single;
+  const int w = gw - t.first_word;
+  const int words = t.rows * t.nblk * 4;
+  const bool live = w >= 0 && w < words;
+  const int rb = live ? w >> 2 : 0, q = w & 3;
+  const int r = live ? rb / t.nblk : 0, b = rb - r * t.nblk;
+  float sum = 0.0f;
+  if (live) {
+    const float* xr = t.x + static_cast<std::size_t>(r) * t.in + static_cast<std::size_t>(b) * kBlock + 8 * q;
+    const int len = t.in - (b * kBlock + 8 * q);
+    float v[8];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      std::uint32_t hi[8], lo[8];
+    for (int i = 0; i < 8; ++i) v[i] = i < len ? xr[i] : 0.0f;
+    std::uint32_t hi[8], lo[8];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int i = 8 * q + (e >> 1) + 4 * (e & 1);
-        const float v = i < len ? xr[i] : 0.0f;
-        hi[e] = bf16_bits_rne(v);
-        lo[e] = bf16_bits_rne(v - bf16_value(hi[e]));
-        sum += bf16_value(hi[e]) + bf16_value(lo[e]);
-      }
-      dst[2 * q] = tu32x4{hi[0] | (hi[1] << 16), hi[2] | (hi[3] << 16), hi[4] | (hi[5] << 16), hi[6] | (hi[7] << 16)};
-      dst[2 * q + 1] = tu32x4{lo[0] | (lo[1] << 16), lo[2] | (lo[3] << 16), lo[4] | (lo[5] << 16), lo[6] | (lo[7] << 16)};
+    for (int e = 0; e < 8; ++e) {
+      const float x = v[(e >> 1) + 4 * (e & 1)];
+      hi[e] = bf16_bits_rne(x);
+      lo[e] = bf16_bits_rne(x - bf16_value(hi[e]));
+      sum += bf16_value(hi[e]) + bf16_value(lo[e]);
     }
-    t.sx[rb] = 24.0f * sum;
+    tu32x4* dst = t.xs + static_cast<std::size_t>(rb) * kSlotsPerBlock + 2 * q;
+    dst[0] = tu32x4{hi[0] | (hi[1] << 16), hi[2] | (hi[3] << 16), hi[4] | (hi[5] << 16), hi[6] | (hi[7] << 16)};
+    dst[1] = tu32x4{lo[0] | (lo[1] << 16), lo[2] | (lo[3] << 16), lo[4] | (lo[5] << 16), lo[6] | (lo[7] << 16)};
   }
+  // Inputs start at multiples of four words, so a quad is one block.
+  sum += __shfl_xor(sum, 1, 64);
+  sum += __shfl_xor(sum, 2, 64);
+  if (live && q == 0) t.sx[rb] = 24.0f * sum;
 }
 
 // qgemv_tol_small (batches of one or two rows, v_mfma_f32_16x16x32_bf16): one
@@ -569,6 +581,8 @@ struct TolPlan {
   std::vector<std::uint32_t> wg_prob;
   std::vector<TolLaunch> launches;
   std::size_t scratch_bytes = 0;
+  std::size_t split_words = 0;            // tol_split's grid, in words
+  std::vector<std::uint32_t> split_wg;     // tol_split's workgroup -> input
 };
 
 int plan_tol(const GroupEntry* entries, std::size_t count, TolPlan* plan) {
@@ -602,6 +616,11 @@ int plan_tol(const GroupEntry* entries, std::size_t count, TolPlan* plan) {
       t.rows = static_cast<int>(e.rows);
       t.in = static_cast<int>(e.m->in);
       t.nblk = static_cast<int>(e.m->nblk);
+      t.first_word = static_cast<int>(plan->split_words);
+      plan->split_words += ceil_div(e.rows * e.m->nblk * 4, 256) * 256;
+      LLMI_REQUIRE(plan->split_words <= 0x7FFFFFFFu, "tolerance matmul: activations too large");
+      plan->split_wg.insert(plan->split_wg.end(), (plan->split_words - t.first_word) / 256,
+                            static_cast<std::uint32_t>(plan->inputs.size()));
       const std::size_t slots = e.rows * e.m->nblk;
       t.xs = reinterpret_cast<tu32x4*>(plan->scratch_bytes);
       plan->scratch_bytes += slots * kSlotsPerBlock * sizeof(tu32x4);
@@ -715,6 +734,7 @@ struct llmi_hip_tol_group {
   const TolProblem* probs = nullptr;
   const TolSplit* splits = nullptr;
   const std::uint32_t* map = nullptr;
+  const std::uint32_t* split_wg = nullptr;
   TolPlan plan;
   ~llmi_hip_tol_group() {
     if (table != nullptr) (void)hipFree(table);
@@ -771,8 +791,9 @@ int llmi_hip_tol_group_create(const llmi_hip_weight* const* w, const float* cons
   const std::size_t pb = g->plan.probs.size() * sizeof(TolProblem);
   const std::size_t sb = g->plan.splits.size() * sizeof(TolSplit);
   const std::size_t mb = g->plan.wg_prob.size() * sizeof(std::uint32_t);
-  if (ib + pb + sb + mb > 0) {
-    LLMI_TRY_HIP(hipMalloc(&g->table, ib + pb + sb + mb));
+  const std::size_t xb = g->plan.split_wg.size() * sizeof(std::uint32_t);
+  if (ib + pb + sb + mb + xb > 0) {
+    LLMI_TRY_HIP(hipMalloc(&g->table, ib + pb + sb + mb + xb));
     auto* base = static_cast<std::uint8_t*>(g->table);
     if (ib > 0) LLMI_TRY_HIP(hipMemcpy(base, g->plan.inputs.data(), ib, hipMemcpyHostToDevice));
     if (pb > 0) LLMI_TRY_HIP(hipMemcpy(base + ib, g->plan.probs.data(), pb, hipMemcpyHostToDevice));
@@ -782,6 +803,9 @@ int llmi_hip_tol_group_create(const llmi_hip_weight* const* w, const float* cons
     g->probs = reinterpret_cast<const TolProblem*>(base + ib);
     g->splits = reinterpret_cast<const TolSplit*>(base + ib + pb);
     g->map = reinterpret_cast<const std::uint32_t*>(base + ib + pb + sb);
+    if (xb > 0)
+      LLMI_TRY_HIP(hipMemcpy(base + ib + pb + sb + mb, g->plan.split_wg.data(), xb, hipMemcpyHostToDevice));
+    g->split_wg = reinterpret_cast<const std::uint32_t*>(base + ib + pb + sb + mb);
   }
   *out = g.release();
   return LLMI_OK;
@@ -791,7 +815,8 @@ int llmi_hip_tol_group_launch(const llmi_hip_tol_group* g, void* stream) {
   LLMI_REQUIRE_INIT();
   LLMI_REQUIRE(g != nullptr, "tolerance matmul: null group");
   if (!g->plan.inputs.empty()) {
-    tol_split<<<static_cast<unsigned>(g->plan.inputs.size()), 256, 0, pick(stream)>>>(g->inputs, TolInput{});
+    tol_split<<<static_cast<unsigned>(g->plan.split_words / 256), 256, 0, pick(stream)>>>(g->inputs, g->split_wg,
+                                                                                          TolInput{});
     LLMI_TRY_HIP(hipGetLastError());
   }
   for (const TolLaunch& l : g->plan.launches)
@@ -821,7 +846,7 @@ int llmi_hip_matmul_tol_dev(const llmi_hip_weight* weight, const float* x_dev, s
       g_tol_ws.bytes = plan.scratch_bytes;
     }
     bind_tol(&plan, g_tol_ws.scratch);
-    tol_split<<<1, 256, 0, s>>>(nullptr, plan.inputs[0]);
+    tol_split<<<static_cast<unsigned>(plan.split_words / 256), 256, 0, s>>>(nullptr, nullptr, plan.inputs[0]);
     LLMI_TRY_HIP(hipGetLastError());
   }
   TolProblem p = plan.probs[0];
