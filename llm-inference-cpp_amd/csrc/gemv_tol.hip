@@ -82,13 +82,23 @@ struct TolInput {
   int rows, in, nblk, first_word;  // first_word: this input's first word in tol_split's grid
 };
 
-__device__ __forceinline__ std::uint32_t bf16_bits_rne(float f) {
-  // Round to nearest even; the inputs are finite (inf/NaN pass through with
-  // their payload's top bits, which the caller's check excludes anyway).
-  const std::uint32_t u = __builtin_bit_cast(std::uint32_t, f);
-  return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+// Two floats as a bf16 pair, rounded to nearest even (v_cvt_pk_bf16_f32).
+typedef __bf16 tbf16x2 __attribute__((ext_vector_type(2)));
+typedef float tf32x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ std::uint32_t bf16_pair(float a, float b) {
+  return __builtin_bit_cast(std::uint32_t, __builtin_convertvector(tf32x2{a, b}, tbf16x2));
 }
-__device__ __forceinline__ float bf16_value(std::uint32_t b) { return __builtin_bit_cast(float, b << 16); }
+// The split of two activations: *hi = bf16 pair of (a, b), *lo = bf16 pair
+// of the remainders; returns (hi_a + lo_a) + (hi_b + lo_b).
+__device__ __forceinline__ float split_pair(float a, float b, std::uint32_t* hi, std::uint32_t* lo) {
+  const std::uint32_t h = bf16_pair(a, b);
+  const float ha = __builtin_bit_cast(float, h << 16), hb = __builtin_bit_cast(float, h & 0xFFFF0000u);
+  const std::uint32_t l = bf16_pair(a - ha, b - hb);
+  const float la = __builtin_bit_cast(float, l << 16), lb = __builtin_bit_cast(float, l & 0xFFFF0000u);
+  *hi = h;
+  *lo = l;
+  return (ha + la) + (hb + lb);
+}
 
 // v of lane (i + n) % 16 of this lane's row of 16 (DPP row_ror:n).
 template <int N>
@@ -148,17 +158,13 @@ __global__ void __launch_bounds__(256) tol_split(const TolInput* __restrict__ in
     float v[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) v[i] = i < len ? xr[i] : 0.0f;
-    std::uint32_t hi[8], lo[8];
+    // k-order pair p of the word holds elements p and p + 4.
+    std::uint32_t hi[4], lo[4];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float x = v[(e >> 1) + 4 * (e & 1)];
-      hi[e] = bf16_bits_rne(x);
-      lo[e] = bf16_bits_rne(x - bf16_value(hi[e]));
-      sum += bf16_value(hi[e]) + bf16_value(lo[e]);
-    }
+    for (int pr = 0; pr < 4; ++pr) sum += split_pair(v[pr], v[pr + 4], &hi[pr], &lo[pr]);
     tu32x4* dst = t.xs + static_cast<std::size_t>(rb) * kSlotsPerBlock + 2 * q;
-    dst[0] = tu32x4{hi[0] | (hi[1] << 16), hi[2] | (hi[3] << 16), hi[4] | (hi[5] << 16), hi[6] | (hi[7] << 16)};
-    dst[1] = tu32x4{lo[0] | (lo[1] << 16), lo[2] | (lo[3] << 16), lo[4] | (lo[5] << 16), lo[6] | (lo[7] << 16)};
+    dst[0] = tu32x4{hi[0], hi[1], hi[2], hi[3]};
+    dst[1] = tu32x4{lo[0], lo[1], lo[2], lo[3]};
   }
   // Inputs start at multiples of four words, so a quad is one block.
   sum += __shfl_xor(sum, 1, 64);
@@ -249,14 +255,13 @@ __global__ void __launch_bounds__(1024) qgemv_tol_small(const TolProblem* __rest
     for (int k = 0; k < kStage; ++k) {
       if (r + k >= rounds) break;
       const int it = lane + 64 * (r + k);
-      const std::uint32_t h0 = bf16_bits_rne(xs[k][0]), h1 = bf16_bits_rne(xs[k][1]);
-      const std::uint32_t l0 = bf16_bits_rne(xs[k][0] - bf16_value(h0)), l1 = bf16_bits_rne(xs[k][1] - bf16_value(h1));
-      float sum = (bf16_value(h0) + bf16_value(l0)) + (bf16_value(h1) + bf16_value(l1));
+      std::uint32_t hp, lp;
+      float sum = split_pair(xs[k][0], xs[k][1], &hp, &lp);
       const int pr = it & 15, rb = it >> 4;
       if (it < items) {
         std::uint32_t* slot = reinterpret_cast<std::uint32_t*>(wl + kZeroSlots + rb * kSlotsPerBlock + 2 * (pr >> 2));
-        slot[pr & 3] = h0 | (h1 << 16);
-        slot[4 + (pr & 3)] = l0 | (l1 << 16);
+        slot[pr & 3] = hp;
+        slot[4 + (pr & 3)] = lp;
       }
       // The row-block's 16 pair sums (one row of 16 lanes) by rotations within
       // the row; lane 0 of the row writes its total (a fixed order).
