@@ -13,30 +13,30 @@
 //                    (a shift and one v_and_or_b32 per two codes);
 //   A (activations)  x split into two bf16 parts, x' = hi + lo (hi = bf16(x),
 //                    lo = bf16(x - hi): 16 significant bits);
-//   D                v_mfma_f32_16x16x32_bf16: sum_i x'_i (1 + n_i/16) in
-//                    fp32, so T = sum_i x'_i c_i = 16 D - 24 sx with
-//                    sx = sum_i x'_i of the block (computed once per input).
+//   D                the MFMA: sum_i x'_i (1 + n_i/16) in fp32, so
+//                    T = sum_i x'_i c_i = 16 D - 24 sx with sx = sum_i x'_i
+//                    of the block (computed with the split).
 // Then acc = fma(T, scale, acc) over a wavefront's blocks, and the
 // wavefronts' partial sums of a tile are added in wavefront order, so the
 // result does not depend on timing.
 //
 // Operand layout.  Lane l holds tile row l's 16 code bytes (the tiled layout:
-// one 16-byte load), row 16g + n with g = l/16, n = l%16.  For code word q
-// (elements 8q..8q+7) the lane's four decoded registers are the MFMA's B
-// operand B[k = 8g + e][n]: k-slice g carries row 16g + n.  A[m][k] is
-// nonzero only for k in slice m/4, so D[m][n] is word q's dot product of row
-// 16(m/4) + n, and D[m][n] sits at lane 16(m/4) + n, register m%4: every lane
-// receives its own row's sums.  Of the four m = 4g + j of a row group, j&1 is
-// the activation part (hi, lo) and j/2 picks one of two input rows, so one
-// MFMA set covers two input rows; the four words accumulate in D (its C
-// operand), four MFMAs per block and set.  Inside a word, register v of B
-// holds nibbles v and v + 4, so A holds x in the order 0,4,1,5,2,6,3,7.
+// one 16-byte load).  For code word q (elements 8q..8q+7) the lane's four
+// decoded registers are the MFMA's B operand at the lane's own k-slice and
+// column, so the slice carries the lane's row; A[m][k] is nonzero only for k
+// in the slice of m's row group, so every lane receives its own row's sums
+// (lane maps: the MFMA-shape notes before a_role).  The four words
+// accumulate in D (its C operand).  Inside a word, register v of B holds
+// nibbles v and v + 4, so A holds x in the order 0,4,1,5,2,6,3,7.
 //
-// Each wavefront splits the activations of its own blocks into its own LDS
-// region (two elements per lane, the block sums by DPP rotations within rows
-// of 16 lanes), so no workgroup barrier precedes the products; the loads of
-// the activations are issued before the code loads, so waiting for them does
-// not wait for HBM.  Lanes outside the active pattern read zero slots.
+// Kernels: qgemv_tol_small (batches 1-2, v_mfma_f32_16x16x32_bf16) -- each
+// wavefront splits the activations of its own blocks into its own LDS region
+// (two elements per lane, the block sums by DPP rotations within rows of 16
+// lanes), so no workgroup barrier precedes the products, and loads the
+// activations before the codes, so waiting for them does not wait for HBM;
+// qgemv_tol_wide (batches 3-8, v_mfma_f32_32x32x16_bf16) -- tol_split splits
+// each input once per launch and each wavefront copies one block at a time
+// into its LDS region.  Lanes outside the active pattern read zero slots.
 #include <algorithm>
 #include <memory>
 #include <utility>
