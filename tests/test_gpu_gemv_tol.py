@@ -128,3 +128,27 @@ def test_rejects_what_it_does_not_cover():
         q4.matmul_tol(x, 9)
     q8.free()
     q4.free()
+
+
+@pytest.mark.parametrize("rows", [1, 8])
+def test_qwen_lm_head_shape(rows):
+    """The 151936 x 896 lm_head (2374 tiles): every output within the
+    contract of the exact kernel's (= the reference's) output, and a sample
+    of 1500 rows within the per-output bound."""
+    o = O.oracle()
+    out, n_in = 151936, 896
+    buf = H.DeviceBuffer(out * n_in * 4)
+    H.synth_normal_dev(buf, out * n_in, 4242, 0.0, 0.02)
+    w = H.Weight.quantize_dev(buf.ptr, out, n_in, O.Q4_0)
+    buf.free()
+    x = synth.normal(4243, rows * n_in, 0.0, 1.0)
+    exact = w.matmul(x, rows).astype(np.float64)
+    tol = w.matmul_tol(x, rows).astype(np.float64)
+    assert np.abs(tol - exact).max() <= TOL_CONTRACT * np.abs(exact).max()
+    data, scales = w.download()
+    sample = np.random.default_rng(1).choice(out, 1500, replace=False)
+    wabs = np.abs(np.stack([o.dequantize_row(data, scales, out, n_in, O.Q4_0, int(r)) for r in sample]).astype(np.float64))
+    mag = np.abs(x.reshape(rows, n_in).astype(np.float64)) @ wabs.T
+    err = np.abs(tol.reshape(rows, out)[:, sample] - exact.reshape(rows, out)[:, sample])
+    assert np.all(err <= TOL_TERMS * mag), float((err / mag).max())
+    w.free()
