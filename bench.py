@@ -472,7 +472,8 @@ def sampled_decode(m, prompt, rec, cfg):
         m.generate_sampled(prompt[:8], 4, H.Sampling(*sc), targets[:4])  # warm-up
         ids = m.generate_sampled(prompt, n, H.Sampling(*sc), targets)
         _, dec_ms = m.last_timing()
-        out[name] = {"decode_tok_s": round(len(ids) / (dec_ms * 1e-3), 1), "steps": int(len(ids))}
+        out[name] = {"decode_tok_s": round(len(ids) / (dec_ms * 1e-3), 1), "steps": int(len(ids)),
+                     "redrawn_steps": m.last_redraws()}
         if name == "t0.8_k40_p0.9":
             out["ids_first16"] = [int(i) for i in ids[:16]]
     V = cfg["vocab_size"]

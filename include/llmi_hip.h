@@ -384,7 +384,9 @@ int llmi_hip_sampling_probabilities(const float* logits, size_t n, const llmi_hi
 /* Testing aids, no counterpart in the reference: force every double sum of a
  * sample call onto its sequential pass (same results, slower), and report
  * which sums of the last call took the sequential pass (bit 0 softmax sum,
- * 1 top-p sum, 2 running sum of the draw, 3 renormalisation sum). */
+ * 1 top-p sum, 2 running sum of the draw, 3 renormalisation sum, 4 all of
+ * the top-p sum, renormalisation sum and draw over the top-k select's
+ * k <= 64 ranked values, which always run sequentially). */
 int llmi_hip_sampling_set_exact_only(int on);
 int llmi_hip_sampling_last_paths(int* paths);
 
@@ -406,6 +408,14 @@ int llmi_hip_model_generate_sampled(llmi_hip_model* model, const int32_t* prompt
  * prefill and the decode loop (HIP events; the reference's llmi-generate --json reports the
  * same split as wall-clock seconds, apps/llmi-generate/main.cpp:329-345). */
 int llmi_hip_model_last_timing(const llmi_hip_model* model, double* prefill_ms, double* decode_ms);
+
+/* Of the last generate_sampled call: how many of its steps were redrawn with
+ * a host read-back of their own.  With temperature > 0 the steps are queued
+ * on the device in windows and read back once per window; a queued draw that
+ * its bounds leave undecided (a target on a running sum) sends the run back
+ * to that step, which is redrawn exactly before queueing resumes.  0 when
+ * every step ran queued.  Diagnostic: no counterpart in the reference. */
+int llmi_hip_model_last_redraws(const llmi_hip_model* model, size_t* steps);
 
 #ifdef __cplusplus
 } /* extern "C" */

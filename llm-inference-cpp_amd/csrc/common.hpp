@@ -261,6 +261,16 @@ void release_tol_workspace();
 // `also` (device, may be null) too, on the stream.
 int sample_device(const float* logits, std::size_t n, const llmi_hip_sampling& cfg, double target,
                   std::int32_t* id_host, std::int32_t* also, hipStream_t s);
+// One draw's outcome, written on the device: id (-1 when undecided) and
+// state (bit 0: decided; bits 1..: the logits' NaN / +inf / all -inf flags).
+struct SampleLog {
+  std::int32_t id;
+  std::int32_t state;
+};
+// sample_device without the host read-back (temperature > 0): the index goes
+// to `also` and *log; an undecided log entry must be redrawn by sample_device.
+int sample_device_async(const float* logits, std::size_t n, const llmi_hip_sampling& cfg, double target,
+                        std::int32_t* also, SampleLog* log, hipStream_t s);
 
 int launch_synth_normal(float* dst, std::size_t n, std::uint64_t seed, std::uint64_t offset, double mean, double stdev,
                         hipStream_t s);

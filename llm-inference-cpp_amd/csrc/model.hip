@@ -1105,6 +1105,9 @@ struct DecodeBuffers {
         *u = nullptr;
 };
 
+// Sampled steps queued per host read-back in generate_sampled.
+constexpr std::size_t kSampleWindow = 32;
+
 struct Workspace {
   std::size_t tokens = 0;  // capacity in tokens
   float *x = nullptr, *h = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *att = nullptr, *g = nullptr,
@@ -1113,6 +1116,7 @@ struct Workspace {
   std::int32_t* next = nullptr;  // argmax result
   std::int32_t* gen = nullptr;   // generated ids of the current greedy run
   std::size_t gen_cap = 0;
+  SampleLog* slog = nullptr;     // the sampled loop's per-step draws (kSampleWindow)
   double* nll = nullptr;         // per-position NLL of chunk_nll
   std::size_t nll_cap = 0;
   float* am_v = nullptr;         // argmax partials and completion counter
@@ -1142,6 +1146,7 @@ struct llmi_hip_model {
   llmi_hip_cache* scratch = nullptr;
   std::vector<void*> allocations;
   double last_prefill_ms = 0.0, last_decode_ms = 0.0;  // of the last greedy run
+  std::size_t last_redraws = 0;  // generate_sampled: queued draws redrawn step by step
 };
 
 struct llmi_hip_cache {
@@ -1365,7 +1370,8 @@ void free_workspace(Workspace& w) {
   for (void* p : {static_cast<void*>(w.x), static_cast<void*>(w.h), static_cast<void*>(w.q), static_cast<void*>(w.k),
                   static_cast<void*>(w.v), static_cast<void*>(w.att), static_cast<void*>(w.g), static_cast<void*>(w.u),
                   static_cast<void*>(w.logits), static_cast<void*>(w.ids), static_cast<void*>(w.next),
-                  static_cast<void*>(w.gen), static_cast<void*>(w.nll), static_cast<void*>(w.am_v),
+                  static_cast<void*>(w.gen), static_cast<void*>(w.slog), static_cast<void*>(w.nll),
+                  static_cast<void*>(w.am_v),
                   static_cast<void*>(w.am_i),
                   static_cast<void*>(w.am_count)})
     if (p != nullptr) (void)hipFree(p);
@@ -1854,6 +1860,7 @@ int llmi_hip_model_generate_sampled(llmi_hip_model* m, const int32_t* prompt, si
   LLMI_REQUIRE(m != nullptr && cfg != nullptr && ids != nullptr && n_ids != nullptr, "generate_sampled: null pointer");
   LLMI_REQUIRE(targets != nullptr || max_new == 0 || cfg->temperature <= 0.0f, "generate_sampled: null targets");
   *n_ids = 0;
+  m->last_redraws = 0;
   llmi_hip_cache* cache = nullptr;
   if (int rc = scratch_cache(m, n + max_new, &cache)) return rc;
   if (int rc = validate(m, cache, prompt, n)) return rc;
@@ -1875,7 +1882,69 @@ int llmi_hip_model_generate_sampled(llmi_hip_model* m, const int32_t* prompt, si
   if (int rc = forward_device(m, cache, n, false, s)) return rc;
   LLMI_TRY_HIP(hipEventRecord(ev[1], s));
   std::size_t produced = 0;
-  for (std::size_t step = 0; step < max_new; ++step) {
+  std::size_t step = 0;
+  bool done = false;
+  if (cfg->temperature > 0.0f) {
+    // Windows of steps queued without a host round trip: each draw writes its
+    // index where the next step's forward reads it, and its outcome to the
+    // window's log; the host reads the log once per window.  Stop ids end the
+    // run at the first one (the window's later steps are discarded).  At the
+    // first undecided draw of a window (a bound left the index open, or bad
+    // logits) the cache is rolled back to that step and its logits
+    // recomputed; sample_device settles the draw exactly (or reports the bad
+    // logits), and queueing resumes after it.  Only steps whose following
+    // forward fits the cache are queued: a run that reaches the end of the
+    // cache does so step by step below, so a stop id drawn first still ends
+    // it without the "cache is full" failure.
+    if (w.slog == nullptr) LLMI_TRY_HIP(hipMalloc(&w.slog, kSampleWindow * sizeof(SampleLog)));
+    SampleLog hlog[kSampleWindow];
+    const std::size_t queued_end = std::min(max_new, cache->cap - n);
+    auto is_stop = [&](std::int32_t id) {
+      for (std::size_t k = 0; k < n_stop; ++k)
+        if (stop_ids[k] == id) return true;
+      return false;
+    };
+    while (step < queued_end && !done) {
+      const std::size_t end = std::min(queued_end, step + kSampleWindow);
+      for (std::size_t t = step; t < end; ++t) {
+        if (int rc = sample_device_async(w.logits, m->V, *cfg, targets[t], w.ids, w.slog + (t - step), s)) return rc;
+        if (t + 1 < max_new)
+          if (int rc = forward_device(m, cache, 1, false, s)) return rc;
+      }
+      LLMI_TRY_HIP(hipMemcpyAsync(hlog, w.slog, (end - step) * sizeof(SampleLog), hipMemcpyDeviceToHost, s));
+      LLMI_TRY_HIP(hipStreamSynchronize(s));
+      std::size_t t = step;
+      for (; t < end && !done; ++t) {
+        if ((hlog[t - step].state & 1) == 0) break;
+        ids[t] = hlog[t - step].id;
+        produced = t + 1;
+        done = is_stop(ids[t]);
+      }
+      step = t;
+      if (done || t == end) continue;
+      // Undecided draw at step t: its logits come from the prompt (t = 0) or
+      // from token t - 1 at position n + t - 1.
+      ++m->last_redraws;
+      if (t == 0) {
+        cache->len = 0;
+        LLMI_TRY_HIP(hipMemcpyAsync(w.ids, prompt, n * sizeof(std::int32_t), hipMemcpyHostToDevice, s));
+        if (int rc = forward_device(m, cache, n, false, s)) return rc;
+      } else {
+        cache->len = n + t - 1;
+        LLMI_TRY_HIP(hipMemcpyAsync(w.ids, &ids[t - 1], sizeof(std::int32_t), hipMemcpyHostToDevice, s));
+        if (int rc = forward_device(m, cache, 1, false, s)) return rc;
+      }
+      if (int rc = sample_device(w.logits, m->V, *cfg, targets[t], &ids[t], w.ids, s)) return rc;
+      produced = t + 1;
+      done = is_stop(ids[t]);
+      step = t + 1;
+      if (!done && step < max_new)
+        if (int rc = forward_device(m, cache, 1, false, s)) return rc;
+    }
+  }
+  // Step by step: temperature <= 0, and the steps whose forward would not
+  // fit the cache.
+  for (; step < max_new && !done; ++step) {
     std::int32_t next = 0;
     const double target = cfg->temperature > 0.0f ? targets[step] : 0.0;
     if (int rc = sample_device(w.logits, m->V, *cfg, target, &next, w.ids, s)) return rc;
@@ -1935,6 +2004,12 @@ int llmi_hip_model_last_timing(const llmi_hip_model* m, double* prefill_ms, doub
   LLMI_REQUIRE(m != nullptr, "last_timing: null model");
   if (prefill_ms != nullptr) *prefill_ms = m->last_prefill_ms;
   if (decode_ms != nullptr) *decode_ms = m->last_decode_ms;
+  return LLMI_OK;
+}
+
+int llmi_hip_model_last_redraws(const llmi_hip_model* m, size_t* steps) {
+  LLMI_REQUIRE(m != nullptr && steps != nullptr, "last_redraws: null pointer");
+  *steps = m->last_redraws;
   return LLMI_OK;
 }
 

@@ -59,7 +59,7 @@ constexpr int kSeqChunk = kSmpThreads * 8;    // terms per LDS stage of the sequ
 
 enum : int { kFlagNaN = 1, kFlagPosInf = 2, kFlagAllNegInf = 4 };
 constexpr int kFlagBad = kFlagNaN | kFlagPosInf | kFlagAllNegInf;
-enum : int { kSeqSoftmax = 1, kSeqTopP = 2, kSeqDraw = 4, kSeqSum2 = 8 };
+enum : int { kSeqSoftmax = 1, kSeqTopP = 2, kSeqDraw = 4, kSeqSum2 = 8, kSeqSelect = 16 };
 
 struct SmpState {
   float mx;         // max of logits / temperature
@@ -314,7 +314,8 @@ __device__ int block_sequential_sum(F v, int m, bool has_stop, double stop_at, d
 }
 
 // ------------------------------------------------------------------ kernels
-__global__ void __launch_bounds__(kSmpThreads) smp_max(const float* __restrict__ logits, int n, float temp, SmpWork w) {
+__global__ void __launch_bounds__(kSmpThreads) smp_max(const float* __restrict__ logits, int n, float temp, SmpWork w,
+                                                       SampleLog* __restrict__ log) {
   __shared__ float red_f[kSmpWaves];
   __shared__ int red_i[kSmpWaves];
   __shared__ bool last;
@@ -350,6 +351,7 @@ __global__ void __launch_bounds__(kSmpThreads) smp_max(const float* __restrict__
     w.st->flags = ff;
     w.st->seq_paths = 0;
     w.st->decided = 0;
+    if (log != nullptr) *log = SampleLog{-1, ff << 1};  // smp_draw overwrites it when it decides
     reset_counter(&w.st->counter);
   }
 }
@@ -476,6 +478,15 @@ __global__ void __launch_bounds__(kSmpThreads) smp_argmax(const float* __restric
     *out = i < 0 ? 0 : i;
     reset_counter(&w.st->counter);
   }
+}
+
+// Kept by the filters: above the last kept value, or equal to it at an index
+// up to the last kept one's (the ranking breaks ties by index).
+__device__ __forceinline__ bool kept(float p, int i, float p_thr, int idx_last) {
+  return p > p_thr || (p == p_thr && i <= idx_last);
+}
+__device__ __forceinline__ float renorm(float p, double s) {
+  return static_cast<float>(static_cast<double>(p) / s);
 }
 
 // ------------------------------------------------------------ top-k selection
@@ -612,9 +623,17 @@ __global__ void __launch_bounds__(kSmpThreads) smp_sel_local(int n, int k, SmpWo
 // One workgroup: the select over every slice's candidates, each thread
 // holding a run of kRun slots in registers (vector loads, all issued at
 // once: the candidates come from other XCDs' workgroups), then the k kept,
-// ranked, into keys_sorted / idx_sorted.
+// ranked, into keys_sorted / idx_sorted.  With at most kSelectMax ranked
+// values the rest of sampling_probabilities and sample() (sampling.cpp:36-77)
+// is short enough for one lane to run exactly as the reference does: the
+// top-p cumulative and the renormalisation sum are the same left fold over
+// the ranking, and the draw's running sum over index order adds only the
+// kept entries (the others are +0, which leaves a double sum unchanged).  So
+// the state is written with the exact sum, and with draw set the index too.
 constexpr int kMergeThreads = 1024;
-__global__ void __launch_bounds__(kMergeThreads) smp_sel_merge(int k, SmpWork w) {
+__global__ void __launch_bounds__(kMergeThreads) smp_sel_merge(int k, float top_p, double target, int draw, SmpWork w,
+                                                               std::int32_t* __restrict__ also,
+                                                               SampleLog* __restrict__ log) {
   constexpr int kRun = kCandMax / kMergeThreads;
   constexpr int kWaves = kMergeThreads / 64;
   static_assert(kRun == 8 && kSelectMax % kRun == 0, "a thread's run is two 16-byte loads inside one slice");
@@ -672,6 +691,12 @@ __global__ void __launch_bounds__(kMergeThreads) smp_sel_merge(int k, SmpWork w)
     }
   }
   __syncthreads();
+  __shared__ float rv[kSelectMax];        // the ranking's values
+  __shared__ std::int32_t ri[kSelectMax]; // and indices
+  __shared__ float fo[kSelectMax];        // the kept f in index order
+  __shared__ std::int32_t io[kSelectMax];
+  __shared__ int keep_s;
+  __shared__ double s2_s;
   if (t < k) {
     const std::uint32_t kt = sk[t];
     const std::int32_t it = si[t];
@@ -679,6 +704,60 @@ __global__ void __launch_bounds__(kMergeThreads) smp_sel_merge(int k, SmpWork w)
     for (int q = 0; q < k; ++q) r += (sk[q] > kt || (sk[q] == kt && si[q] < it)) ? 1 : 0;
     w.keys_sorted[r] = kt;
     w.idx_sorted[r] = it;
+    rv[r] = __builtin_bit_cast(float, kt);
+    ri[r] = it;
+  }
+  __syncthreads();
+  if (t == 0) {
+    // sampling.cpp:36-45 and :50-53: the cumulative stops at keep - 1, where
+    // it equals the sum of the kept.
+    double cum = 0.0;
+    int keep = k;
+    for (int i = 0; i < k; ++i) {
+      cum += static_cast<double>(rv[i]);
+      if (top_p < 1.0f && cum >= static_cast<double>(top_p)) {
+        keep = i + 1;
+        break;
+      }
+    }
+    keep_s = keep;
+    s2_s = cum;
+  }
+  __syncthreads();
+  const int keep = keep_s;
+  const double s2 = s2_s;
+  if (t < keep) {
+    const std::int32_t it = ri[t];
+    int pos = 0;
+    for (int q = 0; q < keep; ++q) pos += ri[q] < it ? 1 : 0;
+    fo[pos] = renorm(rv[t], s2);
+    io[pos] = it;
+  }
+  __syncthreads();
+  if (t == 0) {
+    SmpState* st = w.st;
+    st->keep = keep;
+    st->s2_lo = s2;
+    st->s2_hi = s2;
+    st->p_thr = rv[keep - 1];
+    st->idx_last = ri[keep - 1];
+    st->seq_paths |= kSeqSelect;
+    if (draw) {
+      // sampling.cpp:66-76.  target <= 0 is reached at index 0 whatever p[0].
+      int id = target <= 0.0 ? 0 : -1;
+      double cum = 0.0;
+      for (int j = 0; j < keep && id < 0; ++j) {
+        cum += static_cast<double>(fo[j]);
+        if (cum >= target) id = io[j];
+      }
+      for (int j = keep - 1; j >= 0 && id < 0; --j)
+        if (fo[j] > 0.0f) id = io[j];
+      if (id < 0) id = 0;  // (never: the top entry's f is at least 1 / keep)
+      st->id = id;
+      st->decided = 1;
+      if (also != nullptr) *also = id;
+      if (log != nullptr) *log = SampleLog{id, 1};
+    }
   }
 }
 
@@ -780,18 +859,11 @@ __global__ void __launch_bounds__(kSmpThreads) smp_seq_sum2(const float* __restr
   }
 }
 
-__device__ __forceinline__ bool kept(float p, int i, float p_thr, int idx_last) {
-  return p > p_thr || (p == p_thr && i <= idx_last);
-}
-__device__ __forceinline__ float renorm(float p, double s) {
-  return static_cast<float>(static_cast<double>(p) / s);
-}
-
 // sample() (sampling.cpp:60-77) given its draw: the filtered probabilities
 // f = float(double(p) / s2) lie in [f(s2_hi), f(s2_lo)]; the first index
 // whose running sum reaches target, or else the last nonzero entry.
 __global__ void __launch_bounds__(kSmpThreads) smp_draw(int n, double target, int scaled, SmpWork w,
-                                                        std::int32_t* __restrict__ also) {
+                                                        std::int32_t* __restrict__ also, SampleLog* __restrict__ log) {
   __shared__ double red_d[kSmpWaves];
   __shared__ int red_i[kSmpWaves];
   __shared__ double sh[kSmpThreads];
@@ -871,6 +943,7 @@ __global__ void __launch_bounds__(kSmpThreads) smp_draw(int n, double target, in
     w.st->id = id;
     w.st->decided = id >= 0 ? 1 : 0;
     if (id >= 0 && also != nullptr) *also = id;
+    if (log != nullptr) *log = SampleLog{id, id >= 0 ? 1 : 0};
     reset_counter(&w.st->counter);
   }
 }
@@ -958,25 +1031,35 @@ int smp_sort(std::size_t n, hipStream_t s) {
   return LLMI_OK;
 }
 
+// What smp_front passes to the merge kernel's draw: with the top-k select
+// (top_k <= kSelectMax) the draw is exact there and smp_draw is not needed.
+struct FrontDraw {
+  double target;
+  std::int32_t* also;
+  SampleLog* log;
+};
+
 // Everything up to and including smp_keep.  *ranked: whether the ranking
-// (keys_sorted / idx_sorted) was built.
+// (keys_sorted / idx_sorted) was built.  *drawn: whether the select path
+// already drew the index for `draw` (null: no draw wanted).
 int smp_front(const float* logits, std::size_t n, const llmi_hip_sampling& cfg, bool need_ranking, hipStream_t s,
-              bool* ranked) {
+              bool* ranked, bool* drawn, const FrontDraw* draw = nullptr, SampleLog* log = nullptr) {
   const int ni = static_cast<int>(n);
   const std::size_t k = cfg.top_k == 0 || cfg.top_k > n ? n : cfg.top_k;
   const bool filtering = k < n || cfg.top_p < 1.0f;
   *ranked = filtering || need_ranking;
+  *drawn = false;
   SmpWork& w = g_smp.w;
-  smp_max<<<kSmpBlocks, kSmpThreads, 0, s>>>(logits, ni, cfg.temperature, w);
+  smp_max<<<kSmpBlocks, kSmpThreads, 0, s>>>(logits, ni, cfg.temperature, w, log);
   smp_exp<<<kSmpBlocks, kSmpThreads, 0, s>>>(logits, ni, cfg.temperature, w);
   LLMI_TRY_HIP(hipGetLastError());
   if (*ranked && k < n && k <= static_cast<std::size_t>(kSelectMax)) {
     // Only the first k of the ranking are read: select them.
     const int ki = static_cast<int>(k);
     smp_sel_local<<<kSmpBlocks, kSmpThreads, 0, s>>>(ni, ki, w);
-    smp_sel_merge<<<1, kMergeThreads, 0, s>>>(ki, w);
-    smp_keep<<<kSmpBlocks, kSmpThreads, 0, s>>>(reinterpret_cast<const float*>(w.keys_sorted), w.idx_sorted, ki, ni,
-                                                cfg.top_p, 1, w);
+    smp_sel_merge<<<1, kMergeThreads, 0, s>>>(ki, cfg.top_p, draw != nullptr ? draw->target : 0.0,
+                                              draw != nullptr ? 1 : 0, w, draw != nullptr ? draw->also : nullptr, log);
+    *drawn = draw != nullptr;
   } else if (*ranked) {
     smp_scale<<<static_cast<unsigned>(ceil_div(n, kSmpThreads)), kSmpThreads, 0, s>>>(ni, w, 1);
     if (int rc = smp_sort(n, s)) return rc;
@@ -1022,12 +1105,15 @@ int sample_device(const float* logits, std::size_t n, const llmi_hip_sampling& c
     LLMI_TRY_HIP(hipStreamSynchronize(s));
     return LLMI_OK;
   }
-  bool ranked = false;
-  if (int rc = smp_front(logits, n, cfg, g_exact_only, s, &ranked)) return rc;
+  bool ranked = false, drawn = false;
+  const FrontDraw fd{target, also, nullptr};
+  if (int rc = smp_front(logits, n, cfg, g_exact_only, s, &ranked, &drawn, &fd)) return rc;
   SmpWork& w = g_smp.w;
   const int ni = static_cast<int>(n);
-  if (g_exact_only) smp_seq_sum2<<<1, kSmpThreads, 0, s>>>(reinterpret_cast<const float*>(w.keys_sorted), w);
-  smp_draw<<<kSmpBlocks, kSmpThreads, 0, s>>>(ni, target, ranked ? 1 : 0, w, also);
+  if (!drawn) {
+    if (g_exact_only) smp_seq_sum2<<<1, kSmpThreads, 0, s>>>(reinterpret_cast<const float*>(w.keys_sorted), w);
+    smp_draw<<<kSmpBlocks, kSmpThreads, 0, s>>>(ni, target, ranked ? 1 : 0, w, also, nullptr);
+  }
   LLMI_TRY_HIP(hipGetLastError());
   SmpState st{};
   if (int rc = smp_read_state(&st, s)) return rc;
@@ -1048,12 +1134,34 @@ int sample_device(const float* logits, std::size_t n, const llmi_hip_sampling& c
       if (int rc = smp_sort(n, s)) return rc;
     }
     smp_seq_sum2<<<1, kSmpThreads, 0, s>>>(reinterpret_cast<const float*>(w.keys_sorted), w);
-    smp_draw<<<kSmpBlocks, kSmpThreads, 0, s>>>(ni, target, ranked ? 1 : 0, w, also);
+    smp_draw<<<kSmpBlocks, kSmpThreads, 0, s>>>(ni, target, ranked ? 1 : 0, w, also, nullptr);
     LLMI_TRY_HIP(hipGetLastError());
     if (int rc = smp_read_state(&st, s)) return rc;
     if (!st.decided) return fail(LLMI_ERR_STATE, "sampling: the exact draw did not decide (internal error)");
   }
   *id_host = st.id;
+  return LLMI_OK;
+}
+
+// sample_device's kernels without the read-back: the drawn index goes to
+// `also` (device) and, with the state, to *log; a step whose log says
+// undecided (state bit 0 clear: a bound left the index open, or the logits
+// were bad) must be redrawn through sample_device.  temperature > 0 only.
+int sample_device_async(const float* logits, std::size_t n, const llmi_hip_sampling& cfg, double target,
+                        std::int32_t* also, SampleLog* log, hipStream_t s) {
+  if (int rc = smp_check_cfg(&cfg, n)) return rc;
+  LLMI_REQUIRE(cfg.temperature > 0.0f, "sampling: the asynchronous draw needs temperature > 0");
+  if (int rc = smp_reserve(n, s)) return rc;
+  bool ranked = false, drawn = false;
+  const FrontDraw fd{target, also, log};
+  if (int rc = smp_front(logits, n, cfg, g_exact_only, s, &ranked, &drawn, &fd, log)) return rc;
+  SmpWork& w = g_smp.w;
+  const int ni = static_cast<int>(n);
+  if (!drawn) {
+    if (g_exact_only) smp_seq_sum2<<<1, kSmpThreads, 0, s>>>(reinterpret_cast<const float*>(w.keys_sorted), w);
+    smp_draw<<<kSmpBlocks, kSmpThreads, 0, s>>>(ni, target, ranked ? 1 : 0, w, also, log);
+  }
+  LLMI_TRY_HIP(hipGetLastError());
   return LLMI_OK;
 }
 
@@ -1097,8 +1205,8 @@ int llmi_hip_sampling_probabilities(const float* logits, size_t n, const llmi_hi
     probs[best] = 1.0f;
     return LLMI_OK;
   }
-  bool ranked = false;
-  if (int rc = smp_front(dev_in, n, *cfg, true, s, &ranked)) return rc;
+  bool ranked = false, drawn = false;
+  if (int rc = smp_front(dev_in, n, *cfg, true, s, &ranked, &drawn)) return rc;
   SmpWork& w = g_smp.w;
   smp_seq_sum2<<<1, kSmpThreads, 0, s>>>(reinterpret_cast<const float*>(w.keys_sorted), w);
   float* out = reinterpret_cast<float*>(w.keys);  // the keys are no longer needed

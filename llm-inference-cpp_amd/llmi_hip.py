@@ -93,6 +93,7 @@ SIGNATURES = {
     "llmi_hip_matmul_mfma_noalloc_dev": (_i, [_vp, _vp, _sz, _vp, _vp, _vp]),
     "llmi_hip_model_generate_greedy": (_i, [_vp, _vp, _sz, _sz, _vp, _sz, _vp, C.POINTER(_sz)]),
     "llmi_hip_model_last_timing": (_i, [_vp, C.POINTER(_d), C.POINTER(_d)]),
+    "llmi_hip_model_last_redraws": (_i, [_vp, C.POINTER(_sz)]),
     "llmi_hip_sample": (_i, [_vp, _sz, _vp, _d, C.POINTER(C.c_int32)]),
     "llmi_hip_sample_dev": (_i, [_vp, _sz, _vp, _d, C.POINTER(C.c_int32), _vp]),
     "llmi_hip_sampling_probabilities": (_i, [_vp, _sz, _vp, _vp]),
@@ -498,6 +499,13 @@ class Model:
         a, b = _d(), _d()
         check(self.lib.llmi_hip_model_last_timing(self.h, C.byref(a), C.byref(b)))
         return a.value, b.value
+
+    def last_redraws(self) -> int:
+        """How many steps of the last generate_sampled call were redrawn with
+        a host read-back of their own (0 when every step ran queued)."""
+        v = _sz()
+        check(self.lib.llmi_hip_model_last_redraws(self.h, C.byref(v)))
+        return v.value
 
     def free(self) -> None:
         if self.h:

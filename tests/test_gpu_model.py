@@ -205,6 +205,16 @@ def test_generation_past_the_context_fails_like_the_reference():
     ids5 = m.generate_greedy(prompt, 5)
     assert len(ids5) == 5
     assert np.array_equal(m.generate_greedy(prompt, 3), ids5[:3])
+    # Sampled: the steps whose forward fits are queued on the device, the
+    # rest run step by step, so a stop id drawn before the cache runs out
+    # ends the run without the failure -- at a queued step (2) and at the
+    # first step-by-step one (4).
+    sc = H.Sampling(0.8, 0, 1.0)
+    s5 = m.generate_sampled(prompt, 5, sc, targets)
+    assert len(s5) == 5
+    for at in (2, 4):
+        got = m.generate_sampled(prompt, 10, sc, targets, stop_ids=[int(s5[at])])
+        assert list(got) == list(s5[: list(s5).index(s5[at]) + 1])
     # The model is still usable after the failed calls.
     c = m.new_cache(64)
     logits = m.forward_cached(c, prompt)

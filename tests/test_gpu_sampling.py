@@ -133,7 +133,9 @@ def test_draws_on_a_running_sum_take_the_sequential_pass(cfg):
             got = H.sample(lg, c, t)
             assert got == o.sample_target(lg, *cfg, t), (j, t)
             seen |= H.sampling_last_paths()
-    assert seen & (4 | 8)  # the draw's running sum and/or the renormalisation sum went sequential
+    # The draw's running sum and/or the renormalisation sum went sequential
+    # (with top_k <= 64 they always do, over the select's ranked values).
+    assert seen & (4 | 8 | 16)
 
 
 def test_top_p_on_a_running_sum():
@@ -146,6 +148,27 @@ def test_top_p_on_a_running_sum():
         assert np.count_nonzero(p) == keep, top_p
         assert np.array_equal(bits(p), bits(o.sampling_probabilities(lg, 1.0, 0, top_p)))
         assert H.sampling_last_paths() & 2 or keep == 4
+
+
+@pytest.mark.parametrize("n", [16, 5000])
+def test_select_path_on_exact_boundaries(n):
+    """top_k <= 64 takes the select path, whose top-p cumulative,
+    renormalisation sum and draw run sequentially over the ranked values.
+    Equal logits make every one of them a binary fraction: top_p and the
+    draw's targets land exactly on running sums (and one ulp either side)."""
+    o = O.oracle()
+    lg = np.zeros(n, np.float32)
+    lg[n // 2:] = -1.0  # a second level: the kept come from the first half, ties by index
+    for top_k, top_p in ((8, 1.0), (8, 0.0), (8, 2.0**-20), (40, 1.0), (64, 1.0)):
+        cfg = (1.0, top_k, top_p)
+        p = H.sampling_probabilities(lg, H.Sampling(*cfg))
+        assert np.array_equal(bits(p), bits(o.sampling_probabilities(lg, *cfg))), cfg
+        run = running_sums(p)
+        nz = np.flatnonzero(p)
+        for j in sorted({nz[0], nz[min(1, len(nz) - 1)], nz[-2 if len(nz) > 1 else 0], nz[-1]}):
+            for t in (run[j], np.nextafter(run[j], 0.0), np.nextafter(run[j], 2.0), 0.0):
+                assert H.sample(lg, H.Sampling(*cfg), t) == o.sample_target(lg, *cfg, t), (cfg, j, t)
+        assert bool(H.sampling_last_paths() & 16) == (top_k < n)
 
 
 @pytest.mark.parametrize("n", [5, 3000])
@@ -221,9 +244,53 @@ def test_model_steps_sample_like_the_reference_loop(qt):
     assert got == want
     ids = gm.generate_sampled(prompt, steps, H.Sampling(*sc), targets)
     assert list(ids) == want
+    assert gm.last_redraws() == 0  # every step ran queued on the device
     stop = want[5]
     ids = gm.generate_sampled(prompt, steps, H.Sampling(*sc), targets, stop_ids=[stop])
     assert list(ids) == want[: want.index(stop) + 1]
+    gm.free()
+
+
+@pytest.mark.parametrize("crafted", [(0, 37), (6, 37)])
+@pytest.mark.parametrize("sc", [(1.0, 0, 1.0), (0.9, 100, 0.8), (0.9, 50, 0.8)])
+def test_generate_sampled_redraws_an_undecided_queued_step(sc, crafted):
+    """generate_sampled queues its steps on the device in windows of 32.  A
+    draw whose target sits on the reference's running sum (the bounds cannot
+    decide it on the device) sends the run back to that step: the cache is
+    rolled back (to the prompt for step 0), the step's logits recomputed and
+    the draw settled exactly, and queueing resumes after it.  The ids must
+    still be the reference loop's, with at least one crafted step redrawn
+    (a bound may happen to decide one; 37 lies in the second window) --
+    except with top_k <= 64, whose draw is exact on the device: none."""
+    cfg = toy_cfg()
+    tensors = synth.make_tensors(cfg, 70, "bench")
+    cpu = O.reference() or O.oracle()
+    o = O.oracle()
+    cm = O.CpuModel(cpu, cfg, tensors, H.Q4_0)
+    prompt = synth.uniform_ids(71, 9, cfg["vocab_size"])
+    steps = 45
+    targets = o.draw_uniform(72, steps).astype(np.float64)
+    assert cm.new_cache(64)
+    want = []
+    logits = cm.forward_cached(prompt)
+    for s in range(steps):
+        if s in crafted:
+            f = o.sampling_probabilities(logits, *sc)
+            nz = np.flatnonzero(f)
+            targets[s] = running_sums(f)[nz[len(nz) // 2]]
+        want.append(o.sample_target(logits, *sc, targets[s]))
+        logits = cm.forward_cached([want[-1]])
+    cm.close()
+    gm = H.Model(cfg, tensors, H.Q4_0)
+    ids = gm.generate_sampled(prompt, steps, H.Sampling(*sc), targets)
+    assert list(ids) == want
+    if sc[1] == 50:
+        assert gm.last_redraws() == 0
+    else:
+        assert 1 <= gm.last_redraws() <= len(crafted)
+    for stop in (want[crafted[0]], want[40]):  # a stop drawn at a crafted step, and after one
+        ids = gm.generate_sampled(prompt, steps, H.Sampling(*sc), targets, stop_ids=[stop])
+        assert list(ids) == want[: want.index(stop) + 1]
     gm.free()
 
 
