@@ -8,21 +8,20 @@
 // the tested bound is max|dy| <= 2e-2 * max|y|).  The exact path for the
 // same shapes is llmi_hip_matmul_dev.
 //
-// x is first converted to bf16 once (x_to_bf16: rows padded to a multiple of
-// 64 with zeros), so the GEMM reads half the activation bytes and never
-// converts them again.  One workgroup computes a 128 (tokens) x 256 (outputs)
-// tile of y with 12 wavefronts in two roles.  Wavefronts 0..7 run the MFMAs:
-// wavefront w owns the 64 x 64 block (w / 4, w % 4) as 4 x 4 MFMA tiles of
-// 16 x 16.  Wavefronts 8..11 produce: per K-step of 64 (two quantization
-// blocks) they stage 128 x 64 activations and 256 x 64 dequantized weights
-// (code * scale, rounded to bf16) into one of two LDS buffers while the MFMA
-// wavefronts read the other, and issue the global loads two steps ahead; one
-// barrier per step, so a step costs the longer of the two sides, not their
-// sum.  The producers' loads are unconditional (clamped addresses, the
-// scale of a block past the row's end taken as 0): a load behind a
-// per-lane branch makes the compiler wait for every load in flight.  LDS
-// rows are padded by 16 bytes so that the 16-byte operand reads of 8
-// consecutive lanes hit distinct banks.
+// x is first converted to bf16 once (x_to_bf16: row stride padded to a
+// multiple of 64 with zeros), so the GEMM reads half the activation bytes
+// and never converts them again.  One workgroup computes a 128 (tokens) x
+// 256 (outputs) tile of y with 8 wavefronts (qgemm_mfma below): wavefront w
+// owns outputs 32w..32w+31 and all 128 tokens.  Per K-step of 64 (two
+// quantization blocks) each wavefront loads its own weight codes and scales
+// two steps ahead and dequantizes them (code * scale, rounded to bf16) in
+// registers while the current step's MFMAs run; the 128 x 64 activation
+// tile is staged by all wavefronts into one of two LDS buffers (also two
+// steps ahead through registers), one barrier per step.  The loads are
+// unconditional (clamped addresses, the scale of a block past the row's end
+// taken as 0): a load behind a per-lane branch makes the compiler wait for
+// every load in flight.  LDS rows are padded by 16 bytes so that the 16-byte
+// operand reads of 8 consecutive lanes hit distinct banks.
 //
 // Products are launched as groups (one kernel for many products; a single
 // product is passed by value): workgroup w first maps to a work index so that
@@ -409,8 +408,8 @@ __global__ void __launch_bounds__(256) gemm_reduce(const float* __restrict__ par
 }  // namespace
 
 int gemm_kchunks(std::size_t in, std::size_t launch_tiles, std::size_t split_tiles) {
-  // One workgroup of qgemm_mfma fills a CU (110.6 KB of LDS, 12 waves of
-  // 166 VGPRs), so a launch of fewer tiles than CUs leaves CUs idle: a long
+  // One workgroup of qgemm_mfma fills a CU (8 wavefronts of ~250 VGPRs,
+  // two per SIMD), so a launch of fewer tiles than CUs leaves CUs idle: a long
   // product takes as many K chunks (of at least 8 K-steps) as the CUs the
   // launch's other tiles leave over allow.
   const std::size_t nk = ceil_div(in, static_cast<std::size_t>(kBK));
