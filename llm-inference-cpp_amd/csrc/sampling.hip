@@ -708,55 +708,80 @@ __global__ void __launch_bounds__(kMergeThreads) smp_sel_merge(int k, float top_
     ri[r] = it;
   }
   __syncthreads();
-  if (t == 0) {
+  // Wave 0 runs the sequential folds with lane i holding ranked value i,
+  // read in order with v_readlane (no LDS round trip per term).
+  if (t < 64) {
+    const float v = t < k ? rv[t] : 0.0f;
+    const std::int32_t vi = t < k ? ri[t] : 0;
     // sampling.cpp:36-45 and :50-53: the cumulative stops at keep - 1, where
     // it equals the sum of the kept.
     double cum = 0.0;
     int keep = k;
-    for (int i = 0; i < k; ++i) {
-      cum += static_cast<double>(rv[i]);
-      if (top_p < 1.0f && cum >= static_cast<double>(top_p)) {
-        keep = i + 1;
-        break;
+    bool cut = false;
+#pragma unroll
+    for (int i = 0; i < kSelectMax; ++i) {
+      if (i < k && !cut) {
+        cum += static_cast<double>(readlane_f32(v, i));
+        if (top_p < 1.0f && cum >= static_cast<double>(top_p)) {
+          keep = i + 1;
+          cut = true;
+        }
       }
     }
-    keep_s = keep;
-    s2_s = cum;
+    const double s2 = cum;
+    // The kept values renormalised, placed in index order.
+    if (t < keep) {
+      int pos = 0;
+#pragma unroll
+      for (int q = 0; q < kSelectMax; ++q)
+        if (q < keep) pos += __builtin_amdgcn_readlane(vi, q) < vi ? 1 : 0;
+      fo[pos] = renorm(v, s2);
+      io[pos] = vi;
+    }
+    if (t == 0) {
+      keep_s = keep;
+      s2_s = s2;
+    }
   }
   __syncthreads();
-  const int keep = keep_s;
-  const double s2 = s2_s;
-  if (t < keep) {
-    const std::int32_t it = ri[t];
-    int pos = 0;
-    for (int q = 0; q < keep; ++q) pos += ri[q] < it ? 1 : 0;
-    fo[pos] = renorm(rv[t], s2);
-    io[pos] = it;
-  }
-  __syncthreads();
-  if (t == 0) {
-    SmpState* st = w.st;
-    st->keep = keep;
-    st->s2_lo = s2;
-    st->s2_hi = s2;
-    st->p_thr = rv[keep - 1];
-    st->idx_last = ri[keep - 1];
-    st->seq_paths |= kSeqSelect;
+  if (t < 64) {
+    const int keep = keep_s;
+    const double s2 = s2_s;
+    const float f = t < keep ? fo[t] : 0.0f;
+    const std::int32_t fi = t < keep ? io[t] : 0;
+    int id = -1;
     if (draw) {
-      // sampling.cpp:66-76.  target <= 0 is reached at index 0 whatever p[0].
-      int id = target <= 0.0 ? 0 : -1;
+      // sampling.cpp:66-76.  target <= 0 is reached at index 0 whatever p[0];
+      // the filtered entries add +0 to the running sum.
+      id = target <= 0.0 ? 0 : -1;
       double cum = 0.0;
-      for (int j = 0; j < keep && id < 0; ++j) {
-        cum += static_cast<double>(fo[j]);
-        if (cum >= target) id = io[j];
+#pragma unroll
+      for (int j = 0; j < kSelectMax; ++j) {
+        if (j < keep && id < 0) {
+          cum += static_cast<double>(readlane_f32(f, j));
+          if (cum >= target) id = __builtin_amdgcn_readlane(fi, j);
+        }
       }
-      for (int j = keep - 1; j >= 0 && id < 0; --j)
-        if (fo[j] > 0.0f) id = io[j];
-      if (id < 0) id = 0;  // (never: the top entry's f is at least 1 / keep)
-      st->id = id;
-      st->decided = 1;
-      if (also != nullptr) *also = id;
-      if (log != nullptr) *log = SampleLog{id, 1};
+      // Else the last nonzero entry (never absent: the top entry's f is at
+      // least 1 / keep).
+      const unsigned long long nz = __builtin_amdgcn_ballot_w64(t < keep && f > 0.0f);
+      if (id < 0 && nz != 0) id = __builtin_amdgcn_readlane(fi, 63 - __builtin_clzll(nz));
+      if (id < 0) id = 0;
+    }
+    if (t == 0) {
+      SmpState* st = w.st;
+      st->keep = keep;
+      st->s2_lo = s2;
+      st->s2_hi = s2;
+      st->p_thr = rv[keep - 1];
+      st->idx_last = ri[keep - 1];
+      st->seq_paths |= kSeqSelect;
+      if (draw) {
+        st->id = id;
+        st->decided = 1;
+        if (also != nullptr) *also = id;
+        if (log != nullptr) *log = SampleLog{id, 1};
+      }
     }
   }
 }
