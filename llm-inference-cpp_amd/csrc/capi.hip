@@ -107,19 +107,29 @@ using namespace llmi_hip;
 
 namespace llmi_hip {
 
-int launch_gemm_single(const DeviceMatrix& m, const float* x, std::size_t rows, const float* bias, float* y,
-                       hipStream_t s, bool accumulate) {
-  if (rows == 0 || m.out == 0) return LLMI_OK;
-  const GroupEntry e{&m, x, bias, y, rows, accumulate};
+int launch_gemm_entries(const GroupEntry* e, std::size_t n, hipStream_t s) {
+  LLMI_REQUIRE(n >= 1 && n <= static_cast<std::size_t>(kGemmFew), "gemm: 1..3 products");
   GemmPlan plan;
-  if (int rc = plan_gemm_group(&e, 1, &plan)) return rc;
+  if (int rc = plan_gemm_group(e, n, &plan)) return rc;
+  if (plan.launches.empty()) return LLMI_OK;
   if (int rc = g_gemm_scratch.reserve(gemm_scratch_bytes(plan), s)) return rc;
   auto* scratch = static_cast<std::uint16_t*>(g_gemm_scratch.p);
   bind_gemm_scratch(&plan, scratch);
   if (int rc = launch_gemm_inputs(plan, scratch, s)) return rc;
-  for (const GemmLaunch& l : plan.launches)
-    if (int rc = launch_gemm(nullptr, nullptr, l, s, &plan.probs[l.prob_offset])) return rc;
+  for (std::size_t i = 0; i < plan.launches.size(); ++i) {
+    const GemmLaunch& l = plan.launches[i];
+    const std::size_t end = i + 1 < plan.launches.size() ? plan.launches[i + 1].prob_offset : plan.probs.size();
+    if (int rc = launch_gemm(nullptr, nullptr, l, s, &plan.probs[l.prob_offset], static_cast<int>(end - l.prob_offset)))
+      return rc;
+  }
   return launch_gemm_reduces(plan, s);
+}
+
+int launch_gemm_single(const DeviceMatrix& m, const float* x, std::size_t rows, const float* bias, float* y,
+                       hipStream_t s, bool accumulate) {
+  if (rows == 0 || m.out == 0) return LLMI_OK;
+  const GroupEntry e{&m, x, bias, y, rows, accumulate};
+  return launch_gemm_entries(&e, 1, s);
 }
 
 }  // namespace llmi_hip

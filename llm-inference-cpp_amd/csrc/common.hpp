@@ -184,6 +184,11 @@ std::size_t gemm_scratch_bytes(const GemmPlan& plan);
 int plan_gemm_group(const GroupEntry* entries, std::size_t count, GemmPlan* plan);
 // One product on the bf16-MFMA GEMM, with the library's bf16 staging buffer
 // (grown on demand, outside any graph capture).
+// Up to kGemmFew products (GroupEntry, batch rows each) on the bf16-MFMA
+// GEMM as one conversion launch, one GEMM launch per weight type (products
+// by value) and the split products' reductions; scratch from the library's
+// grow-only GEMM workspace.
+int launch_gemm_entries(const GroupEntry* e, std::size_t n, hipStream_t s);
 int launch_gemm_single(const DeviceMatrix& m, const float* x, std::size_t rows, const float* bias, float* y,
                        hipStream_t s, bool accumulate = false);
 // The allocation-free single-product GEMM (llmi_hip_matmul_mfma_noalloc_dev):
@@ -203,8 +208,16 @@ int launch_gemm_reduces(const GemmPlan& plan, hipStream_t s);
 int launch_gemm_inputs(const GemmPlan& plan, std::uint16_t* scratch, hipStream_t s);
 // one != nullptr: launch the single product *one (plan of one entry) without
 // a device table.
+// Up to kGemmFew products of one launch passed by value (no device table).
+constexpr int kGemmFew = 3;
+struct GemmFew {
+  GemmProblem p[kGemmFew];
+  int count;
+};
+// probs_dev / map_dev: a launch's device tables; or one != nullptr: the
+// launch's nfew (1..kGemmFew) products by value.
 int launch_gemm(const GemmProblem* probs_dev, const std::uint32_t* map_dev, const GemmLaunch& l, hipStream_t s,
-                const GemmProblem* one = nullptr);
+                const GemmProblem* one = nullptr, int nfew = 1);
 
 inline std::size_t block_code_bytes(int type) { return type == LLMI_TYPE_Q4_0 ? 16 : 32; }
 

@@ -150,7 +150,7 @@ struct XStage {
 template <int TYPE>
 __global__ void __launch_bounds__(kGemmThreads) qgemm_mfma(const GemmProblem* __restrict__ probs,
                                                            const std::uint32_t* __restrict__ work_prob, int total,
-                                                           GemmProblem one) {
+                                                           GemmFew few) {
   __shared__ __attribute__((aligned(16))) std::uint16_t xs[2][kBM * kLdsRow];
 
   // Work index: workgroup w runs on XCD w % 8; give each XCD a contiguous
@@ -159,8 +159,11 @@ __global__ void __launch_bounds__(kGemmThreads) qgemm_mfma(const GemmProblem* __
   const int per = total / kXcds, extra = total % kXcds;
   const int xcd = wgi % kXcds, slot = wgi / kXcds;
   const int work = xcd * per + min(xcd, extra) + slot;
-  // A single product comes by value (no table); a group through the map.
-  GemmProblem p = one;
+  // Up to kGemmFew products come by value (no table; the product by
+  // comparisons and selects, so the argument block is never indexed
+  // dynamically); a group through the map.
+  const int fi = (few.count > 2 && work >= few.p[2].first_wg) ? 2 : (few.count > 1 && work >= few.p[1].first_wg) ? 1 : 0;
+  GemmProblem p = fi == 2 ? few.p[2] : fi == 1 ? few.p[1] : few.p[0];
   if (probs != nullptr) p = probs[__builtin_amdgcn_readfirstlane(static_cast<int>(work_prob[work]))];
   const int local = work - p.first_wg;
   // Consecutive work items: the token tiles of one (weight tile, K chunk).
@@ -667,15 +670,20 @@ int launch_gemm_noalloc(int device, const DeviceMatrix& m, const float* x, std::
 }
 
 int launch_gemm(const GemmProblem* probs_dev, const std::uint32_t* map_dev, const GemmLaunch& l, hipStream_t s,
-                const GemmProblem* one) {
+                const GemmProblem* one, int nfew) {
   if (l.total_wgs == 0) return LLMI_OK;
+  LLMI_REQUIRE(one == nullptr || (nfew >= 1 && nfew <= kGemmFew), "gemm: 1..3 products by value");
   const GemmProblem* probs = one != nullptr ? nullptr : probs_dev + l.prob_offset;
   const std::uint32_t* map = one != nullptr ? nullptr : map_dev + l.map_offset;
-  const GemmProblem single = one != nullptr ? *one : GemmProblem{};
+  GemmFew few{};
+  if (one != nullptr) {
+    for (int i = 0; i < nfew; ++i) few.p[i] = one[i];
+    few.count = nfew;
+  }
   if (l.type == LLMI_TYPE_Q8_0)
-    qgemm_mfma<LLMI_TYPE_Q8_0><<<l.total_wgs, kGemmThreads, 0, s>>>(probs, map, l.total_wgs, single);
+    qgemm_mfma<LLMI_TYPE_Q8_0><<<l.total_wgs, kGemmThreads, 0, s>>>(probs, map, l.total_wgs, few);
   else
-    qgemm_mfma<LLMI_TYPE_Q4_0><<<l.total_wgs, kGemmThreads, 0, s>>>(probs, map, l.total_wgs, single);
+    qgemm_mfma<LLMI_TYPE_Q4_0><<<l.total_wgs, kGemmThreads, 0, s>>>(probs, map, l.total_wgs, few);
   LLMI_TRY_HIP(hipGetLastError());
   return LLMI_OK;
 }

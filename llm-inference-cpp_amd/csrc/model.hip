@@ -1475,9 +1475,11 @@ int forward_rows(llmi_hip_model* m, llmi_hip_cache* cache, std::size_t T, std::s
     rmsnorm_rows<<<tt, kThreads, 0, s>>>(w.x, l.attn_norm, w.h, static_cast<int>(m->H), eps);
     bool roped = false;
     if (mfma_all) {
-      if (int rc = linear(l.wq, w.h, l.bq, w.q, false)) return rc;
-      if (int rc = linear(l.wk, w.h, l.bk, w.k, false)) return rc;
-      if (int rc = linear(l.wv, w.h, l.bv, w.v, false)) return rc;
+      // q, k and v share h: one conversion and one GEMM launch.
+      const GroupEntry qkv[3] = {{&l.wq, w.h, l.bq, w.q, T, false},
+                                 {&l.wk, w.h, l.bk, w.k, T, false},
+                                 {&l.wv, w.h, l.bv, w.v, T, false}};
+      if (int rc = launch_gemm_entries(qkv, 3, s)) return rc;
     } else {
       const DeviceMatrix* qkv[3] = {&l.wq, &l.wk, &l.wv};
       const float* qkv_bias[3] = {l.bq, l.bk, l.bv};
@@ -1505,8 +1507,8 @@ int forward_rows(llmi_hip_model* m, llmi_hip_cache* cache, std::size_t T, std::s
     }
     if (!fused) {
       if (mfma_all) {
-        if (int rc = linear(l.gate, w.h, nullptr, w.g, false)) return rc;
-        if (int rc = linear(l.up, w.h, nullptr, w.u, false)) return rc;
+        const GroupEntry gu[2] = {{&l.gate, w.h, nullptr, w.g, T, false}, {&l.up, w.h, nullptr, w.u, T, false}};
+        if (int rc = launch_gemm_entries(gu, 2, s)) return rc;
       } else {
         const DeviceMatrix* gu[2] = {&l.gate, &l.up};
         const float* gu_bias[2] = {nullptr, nullptr};
