@@ -294,6 +294,38 @@ def test_generate_sampled_redraws_an_undecided_queued_step(sc, crafted):
     gm.free()
 
 
+@pytest.mark.parametrize("steps", [1, 31, 32, 33, 64])
+def test_generate_sampled_at_window_boundaries(steps):
+    """generate_sampled queues 32 steps per host read-back: runs of one step,
+    a window less one, exactly one and two windows, and one step past a
+    window give the reference loop's ids, as does a stop id drawn at the last
+    step; temperature 0 redraws nothing."""
+    cfg = toy_cfg()
+    tensors = synth.make_tensors(cfg, 80, "bench")
+    cpu = O.reference() or O.oracle()
+    o = O.oracle()
+    cm = O.CpuModel(cpu, cfg, tensors, H.Q8_0)
+    prompt = synth.uniform_ids(81, 7, cfg["vocab_size"])
+    sc = (1.1, 0, 1.0)
+    targets = o.draw_uniform(82, steps)
+    assert cm.new_cache(96)
+    want = []
+    logits = cm.forward_cached(prompt)
+    for s in range(steps):
+        want.append(o.sample_target(logits, *sc, targets[s]))
+        logits = cm.forward_cached([want[-1]])
+    cm.close()
+    gm = H.Model(cfg, tensors, H.Q8_0)
+    assert list(gm.generate_sampled(prompt, steps, H.Sampling(*sc), targets)) == want
+    stop = want[-1]
+    assert list(gm.generate_sampled(prompt, steps, H.Sampling(*sc), targets, stop_ids=[stop])) == \
+        want[: want.index(stop) + 1]
+    greedy = gm.generate_greedy(prompt, steps)
+    assert list(gm.generate_sampled(prompt, steps, H.Sampling(0.0), [])) == list(greedy)
+    assert gm.last_redraws() == 0
+    gm.free()
+
+
 def test_shutdown_releases_and_reinit_works():
     """llmi_hip_shutdown frees the library's sampling and GEMM workspaces;
     a later llmi_hip_init starts clean and sampling still gives the oracle's
