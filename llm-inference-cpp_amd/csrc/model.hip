@@ -814,15 +814,19 @@ __global__ void __launch_bounds__(kThreads) attn_pv_1(const float* __restrict__ 
   if (tid < kPvCols) {
     const float4* pr = reinterpret_cast<const float4*>(p);
     const float4* vr = reinterpret_cast<const float4*>(vt + static_cast<std::size_t>(tid) * stride);
-    const int nq = npad / 4;  // a multiple of kPvChain
+    const int nq = npad / 4;  // a multiple of 2 * kPvChain
     // Two register sets, A and B: the reads of one round are issued before
-    // the chain steps of the other, so LDS latency overlaps the chain.
+    // the chain steps of the other, so LDS latency overlaps the chain.  The
+    // reads walk two pointers with constant offsets (a clamped index would
+    // put the next address in a register an outstanding read still
+    // targets, and every round would wait for all reads in flight); the last
+    // round's look-ahead reads the padding attn_pv_lds adds (unused).
     float4 pa[kPvChain], va[kPvChain], pb[kPvChain], vb[kPvChain];
-    const auto read = [&](float4* pp, float4* vv, int q) {
+    const auto read = [&](float4* pp, float4* vv, const float4* ps, const float4* vs) {
 #pragma unroll
       for (int u = 0; u < kPvChain; ++u) {
-        pp[u] = pr[q + u];
-        vv[u] = vr[q + u];
+        pp[u] = ps[u];
+        vv[u] = vs[u];
       }
     };
     float acc = 0.0f;
@@ -835,19 +839,16 @@ __global__ void __launch_bounds__(kThreads) attn_pv_1(const float* __restrict__ 
         acc = __builtin_fmaf(pp[u].w, vv[u].w, acc);
       }
     };
-    // Every round issues its reads unconditionally (re-reading the last
-    // round when there is no next one), so the number of reads in flight is
-    // the same on every path and the waits before each chain round only
-    // cover that round's own reads.
-    read(pa, va, 0);
+    read(pa, va, pr, vr);
     for (int q4 = 0; q4 < nq; q4 += 2 * kPvChain) {
-      read(pb, vb, q4 + kPvChain < nq ? q4 + kPvChain : q4);
+      read(pb, vb, pr + kPvChain, vr + kPvChain);
       __builtin_amdgcn_sched_barrier(0);
       steps(pa, va);
-      if (q4 + kPvChain >= nq) break;
-      read(pa, va, q4 + 2 * kPvChain < nq ? q4 + 2 * kPvChain : q4);
+      read(pa, va, pr + 2 * kPvChain, vr + 2 * kPvChain);
       __builtin_amdgcn_sched_barrier(0);
       steps(pb, vb);
+      pr += 2 * kPvChain;
+      vr += 2 * kPvChain;
     }
     out[static_cast<std::size_t>(h) * hd + i0 + tid] = acc;
   }
@@ -855,7 +856,8 @@ __global__ void __launch_bounds__(kThreads) attn_pv_1(const float* __restrict__ 
 
 std::size_t attn_pv_lds(std::size_t npos) {
   const std::size_t npad = static_cast<std::size_t>(pv_pad(static_cast<int>(npos)));
-  return (npad + kPvCols * (npad + 4)) * sizeof(float);
+  // + one look-ahead round of reads past the last row (4 * kPvChain floats)
+  return (npad + kPvCols * (npad + 4) + 4 * kPvChain) * sizeof(float);
 }
 
 // The two-kernel decode path applies to one token with head_dim 64 or 128,
