@@ -281,35 +281,49 @@ __device__ __forceinline__ void block_sums(const GMEM uint4* __restrict__ codes,
 }
 
 // The sequential chain over all blocks of one row of a tile, from LDS
-// (stride `stride` floats between blocks).  The reads run a round ahead of
-// the fused multiply-adds (kChainRound blocks per round; indices past the
-// last block are clamped to it and their values unused), so the LDS latency
-// is paid once, not once per block.
-constexpr int kChainRound = 8;
+// (stride `stride` floats between blocks).  Two register sets of
+// kChainRound blocks: the reads of one are issued before the fused
+// multiply-adds of the other, so LDS latency overlaps the chain.  The reads
+// walk two pointers with constant offsets (an index clamped to the last
+// block puts the next address in a register an outstanding read still
+// targets, and every round then waits for all reads in flight).  A round's
+// look-ahead may read up to kChainRound blocks past the row: inside the
+// next row or the scales, or in the padding wide_lds adds after them; those
+// values are never used.
+constexpr int kChainRound = 4;
 __device__ __forceinline__ float chain_lds(const float* part, const float* scl, int nblk, int lane, int stride) {
-  float acc = 0.0f;
-  float p[kChainRound], s[kChainRound];
-  const auto read = [&](int b0, float* pp, float* ss) {
+  const float* pp = part + lane;
+  const float* sp = scl + lane;
+  float pa[kChainRound], sa[kChainRound], pb[kChainRound], sb[kChainRound];
+  const auto read = [&](float* p, float* q, const float* ps, const float* ss) {
 #pragma unroll
     for (int u = 0; u < kChainRound; ++u) {
-      const int b = min(b0 + u, nblk - 1);
-      pp[u] = part[b * stride + lane];
-      ss[u] = scl[b * stride + lane];
+      p[u] = ps[u * stride];
+      q[u] = ss[u * stride];
     }
   };
-  read(0, p, s);
-  for (int b = 0; b < nblk; b += kChainRound) {
-    float pn[kChainRound], sn[kChainRound];
-    read(b + kChainRound < nblk ? b + kChainRound : b, pn, sn);
+  float acc = 0.0f;
+  const auto steps = [&](const float* p, const float* q) {
 #pragma unroll
-    for (int u = 0; u < kChainRound; ++u)
-      if (b + u < nblk) acc = __builtin_fmaf(p[u], s[u], acc);
-#pragma unroll
-    for (int u = 0; u < kChainRound; ++u) {
-      p[u] = pn[u];
-      s[u] = sn[u];
-    }
+    for (int u = 0; u < kChainRound; ++u) acc = __builtin_fmaf(p[u], q[u], acc);
+  };
+  read(pa, sa, pp, sp);
+  int b = 0;
+  for (; b + 2 * kChainRound <= nblk; b += 2 * kChainRound) {
+    read(pb, sb, pp + kChainRound * stride, sp + kChainRound * stride);
+    __builtin_amdgcn_sched_barrier(0);
+    steps(pa, sa);
+    read(pa, sa, pp + 2 * kChainRound * stride, sp + 2 * kChainRound * stride);
+    __builtin_amdgcn_sched_barrier(0);
+    steps(pb, sb);
+    pp += 2 * kChainRound * stride;
+    sp += 2 * kChainRound * stride;
   }
+  // pa holds blocks b .. b + 3 (those below nblk); the rest one by one.
+#pragma unroll
+  for (int u = 0; u < kChainRound; ++u)
+    if (b + u < nblk) acc = __builtin_fmaf(pa[u], sa[u], acc);
+  for (int c = b + kChainRound; c < nblk; ++c) acc = __builtin_fmaf(part[c * stride + lane], scl[c * stride + lane], acc);
   return acc;
 }
 
@@ -442,28 +456,53 @@ __device__ __forceinline__ void stage_x(const GMEM float* __restrict__ x, int in
 __host__ __device__ __forceinline__ int pair_stride(int nblk) { return 2 * ((nblk + 15) & ~15) + 4; }
 
 // The sequential chain over the (block sum, scale) pairs of one row, two
-// blocks per 16-byte LDS read, eight reads (16 blocks) per round, the next
-// round's reads issued before this round's fused multiply-adds.  The row
-// holds nblk rounded up to 16 pairs (pair_stride), so a round's reads stay
-// inside it; pairs past nblk are read but not used.
+// blocks per 16-byte LDS read, eight reads (16 blocks) per round.  Two
+// register sets: the reads of one round are issued before the fused
+// multiply-adds of the other, and whole rounds run without per-block
+// conditions (only the last, partial round has them).  The reads walk one
+// pointer with constant offsets; a look-ahead may read up to 15 pairs past
+// nblk -- inside the next row, or in the padding narrow_lds adds after the
+// last row -- and those values are never used.
+constexpr int kPairPad = 32;  // floats of look-ahead padding after the last row
 __device__ __forceinline__ float chain_pairs(const float* row, int nblk) {
   const float4* pr = reinterpret_cast<const float4*>(row);
+  float4 a[8], c[8];
+  const auto read = [&](float4* v, const float4* src) {
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = src[u];
+  };
   float acc = 0.0f;
-  float4 a[8];
-#pragma unroll
-  for (int u = 0; u < 8; ++u) a[u] = pr[u];
-  for (int b = 0; b < nblk; b += 16) {
-    float4 n[8];
-    const int q = b + 16 < nblk ? (b + 16) / 2 : b / 2;
-#pragma unroll
-    for (int u = 0; u < 8; ++u) n[u] = pr[q + u];
+  const auto steps = [&](const float4* v) {
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
-      if (b + 2 * u < nblk) acc = __builtin_fmaf(a[u].x, a[u].y, acc);
-      if (b + 2 * u + 1 < nblk) acc = __builtin_fmaf(a[u].z, a[u].w, acc);
+      acc = __builtin_fmaf(v[u].x, v[u].y, acc);
+      acc = __builtin_fmaf(v[u].z, v[u].w, acc);
     }
+  };
+  read(a, pr);
+  int b = 0;
+  for (; b + 32 <= nblk; b += 32) {
+    read(c, pr + 8);
+    __builtin_amdgcn_sched_barrier(0);
+    steps(a);
+    read(a, pr + 16);
+    __builtin_amdgcn_sched_barrier(0);
+    steps(c);
+    pr += 16;
+  }
+  // a holds pairs b .. b + 15; fewer than 32 remain.
+  if (b + 16 <= nblk) {
+    read(c, pr + 8);
+    __builtin_amdgcn_sched_barrier(0);
+    steps(a);
 #pragma unroll
-    for (int u = 0; u < 8; ++u) a[u] = n[u];
+    for (int u = 0; u < 8; ++u) a[u] = c[u];
+    b += 16;
+  }
+#pragma unroll
+  for (int u = 0; u < 8; ++u) {
+    if (b + 2 * u < nblk) acc = __builtin_fmaf(a[u].x, a[u].y, acc);
+    if (b + 2 * u + 1 < nblk) acc = __builtin_fmaf(a[u].z, a[u].w, acc);
   }
   return acc;
 }
@@ -1060,9 +1099,14 @@ __global__ void __launch_bounds__(W * 64) qgemm_split_group(SplitGroup g, const 
 
 // ------------------------------------------------------------ planning
 // LDS bytes of one workgroup of each kind.
-std::size_t wide_lds(std::size_t nblk, std::size_t nr) { return (nr + 1) * nblk * kTileRows * sizeof(float); }
+// part[nr][nblk][64], scale[nblk][64], then the chain's look-ahead padding.
+std::size_t wide_lds(std::size_t nblk, std::size_t nr) {
+  return ((nr + 1) * nblk + 2 * kChainRound) * kTileRows * sizeof(float);
+}
+// x[in (padded to 4)], 16 rows of pairs, then chain_pairs' look-ahead padding.
 std::size_t narrow_lds(std::size_t in, std::size_t nblk) {
-  return (((in + 3) & ~std::size_t{3}) + 16 * static_cast<std::size_t>(pair_stride(static_cast<int>(nblk)))) *
+  return (((in + 3) & ~std::size_t{3}) + 16 * static_cast<std::size_t>(pair_stride(static_cast<int>(nblk))) +
+          kPairPad) *
          sizeof(float);
 }
 
