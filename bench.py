@@ -400,11 +400,12 @@ def prefill_flops(cfg, T):
     return 2 * T * L * per_layer + 2 * cfg["vocab_size"] * H + attn
 
 
-def decode_runs(max_steps: int | None = None):
+def decode_runs(max_steps: int | None = None, greedy_only: bool = False):
     """Full-model greedy decode on the synthetic models: prefill the prompt,
     then the configured number of greedy steps (at most max_steps, for
     profiling runs); ids are checked against the reference's (tests/golden),
-    a shortened run against their prefix."""
+    a shortened run against their prefix.  Then the sampled decode and the
+    perplexity chunk, unless greedy_only (profiling passes)."""
     res = {}
     for key, golden, cfg, qt in DECODE_RUNS:
         with open(os.path.join(ROOT, "tests", "golden", golden + ".json")) as f:
@@ -443,8 +444,9 @@ def decode_runs(max_steps: int | None = None):
                                          weight_bytes=int(wb))
         print(f"[bench] {key}: prefill {pre_ms:.1f} ms, decode {tok_s:.1f} tok/s, ids match "
               f"{res[key]['ids_match_reference']}", file=sys.stderr, flush=True)
-        res[key]["sampled"] = sampled_decode(m, prompt, rec, cfg)
-        if cfg["vocab_size"] > 100000:
+        if not greedy_only:
+            res[key]["sampled"] = sampled_decode(m, prompt, rec, cfg)
+        if cfg["vocab_size"] > 100000 and not greedy_only:
             res[key]["perplexity_chunk"] = perplexity_chunk(m, prompt, cfg)
         m.free()
     return res
@@ -756,6 +758,8 @@ def main():
     ap.add_argument("--no-shapes", action="store_true", help="skip the per-shape table (C1, C2 shapes)")
     ap.add_argument("--decode-steps", type=int, default=None,
                     help="cap the greedy decode runs at this many steps (profiling; ids checked as a prefix)")
+    ap.add_argument("--greedy-only", action="store_true",
+                    help="decode runs without the sampled decode and the perplexity chunk (profiling)")
     ap.add_argument("--cpu-leg-8", action="store_true", help=argparse.SUPPRESS)
     args = ap.parse_args()
     if args.cpu_leg_8:
@@ -813,7 +817,7 @@ def main():
 
     per_shape = {} if args.no_shapes else per_shape_gpu()
     targets = {} if args.no_targets else target_shapes()
-    decode = {} if args.no_decode else decode_runs(args.decode_steps)
+    decode = {} if args.no_decode else decode_runs(args.decode_steps, args.greedy_only)
     gemm = {} if args.no_gemm else prefill_gemm()
     gguf = gguf_upload()
     cpu = None

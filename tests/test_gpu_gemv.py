@@ -113,6 +113,30 @@ def test_long_row_products_match_oracle(qt, out, n_in):
     dev.free()
 
 
+@pytest.mark.parametrize("qt", [O.Q8_0, O.Q4_0])
+@pytest.mark.parametrize("out,rows", [(40, 1), (8200, 1), (8200, 3)])
+def test_block_chain_round_boundaries_match_oracle(qt, out, rows):
+    """Rows of 3 to 65 blocks around the block chains' rounds (4 and 8
+    blocks on the 64-row tiles, 16 and 32 pairs on the 16-row tiles, whose
+    look-ahead reads past the last block; up to 33 blocks on the 64-row
+    tiles, where the rounds are shorter): 40 outputs take the 16-row tiles,
+    8200 (129 tiles, the last one partial) the 64-row tiles, 3 input rows
+    the multi-row chains."""
+    orc = O.oracle()
+    wide = (3, 4, 5, 7, 8, 9, 12, 15, 16, 17, 24, 33)
+    narrow = (3, 4, 5, 7, 8, 9, 15, 16, 17, 24, 31, 32, 33, 40, 47, 48, 63, 64, 65)
+    for nblk in narrow if out < 64 else wide:
+        n_in = 32 * nblk - (5 if nblk % 2 else 0)  # odd block counts end on a partial block
+        w = synth.normal(nblk * 11 + out, out * n_in, 0.0, 0.02)
+        data, scales = orc.quantize(w, out, n_in, qt)
+        dev = H.Weight.upload(data, scales, out, n_in, qt)
+        x = synth.normal(nblk + 3 * rows, rows * n_in, 0.0, 1.0)
+        got = dev.matmul(x, rows, None)
+        want = orc.matmul(x, rows, n_in, data, scales, qt, out, None)
+        dev.free()
+        assert np.array_equal(bits(got), bits(want)), (nblk, n_in)
+
+
 def test_long_row_products_in_one_group_match_oracle():
     """A grouped launch holding long-row products next to short-row and
     multi-row ones: every output equals the oracle's, on two launches of the
