@@ -677,14 +677,14 @@ __global__ void __launch_bounds__(kThreads) attn_scores_1(const float* __restric
 // like the sequential sum, else summed sequentially); then it parks p and
 // the transposed V slice in LDS and lanes 0-15 run the P.V chains of the 16
 // columns.  Dynamic LDS: p[npad] then vt[16][npad + 4] (npad = npos rounded
-// up to 32, zero-padded; rows start 4 banks apart).  The padding adds
+// up to 64, zero-padded; rows start 4 banks apart).  The padding adds
 // fma(0, 0, acc) = acc: acc starts at +0 and never becomes -0.
 constexpr int kPvCols = 16;
 constexpr int kPvBatch = 16;   // V float4 loads per thread per round (1024 positions)
 constexpr int kPvScores = 10;  // score registers per thread: npos <= 2560
-constexpr int kPvChain = 4;    // float4 reads per operand per chain round (8 LDS reads in flight)
+constexpr int kPvChain = 8;    // float4 reads per operand per chain round (16 LDS reads in flight)
 
-__host__ __device__ __forceinline__ int pv_pad(int npos) { return (npos + 31) & ~31; }
+__host__ __device__ __forceinline__ int pv_pad(int npos) { return (npos + 63) & ~63; }
 
 __device__ __forceinline__ float row_max16(float v) {
   // Lanes whose source is outside the row keep their own value.
