@@ -232,15 +232,57 @@ def gen_big_model(ref, out_dir, name, cfg, qt, seed, prompt_seed, n_prompt, n_st
     print(f"{name}: {t3 - t0:.1f}s, min margin {min(margins):.3g}", flush=True)
 
 
+STEP_LOGIT_STEPS = (0, 63, 127)  # plus the last step of each run
+
+
+def gen_step_logits(ref, out_dir, name, cfg, qt):
+    """Per-step logits of a big-model run, fed the recorded greedy ids one
+    token at a time through forward_cached: SHA-256 of the logits that
+    choose ids[s] for s in STEP_LOGIT_STEPS and the last step (s = 0 is the
+    prefill's), plus the argmax of every step checked against the recorded
+    ids.  Adds `step_logits_sha256` to the run's record."""
+    path = os.path.join(out_dir, f"{name}.json")
+    with open(path) as f:
+        rec = json.load(f)
+    t0 = time.time()
+    tensors = synth.make_tensors(cfg, rec["seed"], rec["convention"])
+    m = ref.model(cfg, tensors, qt)
+    del tensors
+    prompt = synth.uniform_ids(rec["prompt_seed"], rec["n_prompt"], cfg["vocab_size"])
+    n = rec["n_steps"]
+    want = set(STEP_LOGIT_STEPS) | {n - 1}
+    assert m.new_cache(rec["n_prompt"] + n)
+    logits = m.forward_cached(prompt)
+    shas = {}
+    for s in range(n):
+        if s in want:
+            shas[str(s)] = sha(logits)
+        top = int(np.argmax(logits))
+        assert top == rec["ids"][s], (name, s, top, rec["ids"][s])
+        if s + 1 < n:
+            logits = m.forward_cached(np.array([rec["ids"][s]], np.int32))
+    m.close()
+    rec["step_logits_sha256"] = shas
+    with open(path, "w") as f:
+        json.dump(rec, f, indent=1)
+    print(f"{name}: step logits at {sorted(int(k) for k in shas)} in {time.time() - t0:.1f}s", flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--models", action="store_true", help="also run the full-size synthetic models (minutes)")
     ap.add_argument("--only-models", action="store_true")
+    ap.add_argument("--step-logits", action="store_true",
+                    help="add per-step logits digests to the recorded big-model runs (minutes)")
     args = ap.parse_args()
     ref = O.reference()
     if ref is None:
         sys.exit("oracle/_ref/libllmi_ref.so is not built (needs /root/reference)")
     out_dir = HERE
+    if args.step_logits:
+        gen_step_logits(ref, out_dir, "c3_smollm2_q8", synth.SMOLLM2_135M, Q8)
+        gen_step_logits(ref, out_dir, "c4_qwen25_q4", synth.QWEN25_05B, Q4)
+        return
     if not args.only_models:
         record = dict(meta=meta(ref))
         record["quant_small"] = gen_quant_small(ref, out_dir)

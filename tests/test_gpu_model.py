@@ -245,6 +245,36 @@ def test_synthetic_model_greedy_ids_match_reference(name):
     m.free()
 
 
+@pytest.mark.parametrize("name", ["c3_smollm2_q8", "c4_qwen25_q4"])
+def test_synthetic_model_step_logits_match_reference(name):
+    """Per-step logits of the full-size synthetic models past the prefill
+    (the reference pins per-step equality, tests/transformer_test.cpp:
+    322-398): the one-token step fed the reference's greedy ids, its logits
+    bit-identical (SHA-256) to the compiled reference's at the recorded
+    steps (0 = the prefill's, 63, 127 and the last), and every step's argmax
+    equal to the recorded id."""
+    with open(os.path.join(GOLDEN, name + ".json")) as f:
+        rec = json.load(f)
+    want = rec["step_logits_sha256"]
+    cfg = rec["cfg"]
+    m = H.synthetic_model_dev(cfg, rec["seed"], rec["type"], rec["convention"])
+    prompt = synth.uniform_ids(rec["prompt_seed"], rec["n_prompt"], cfg["vocab_size"])
+    n = rec["n_steps"]
+    cache = m.new_cache(rec["n_prompt"] + n)
+    logits = m.forward_cached(cache, prompt)
+    checked = 0
+    for s in range(n):
+        if str(s) in want:
+            assert sha(logits) == want[str(s)], (name, s, np.argsort(-logits)[:4])
+            checked += 1
+        assert int(np.argmax(logits)) == rec["ids"][s], (name, s)
+        if s + 1 < n:
+            logits = m.forward_cached(cache, [rec["ids"][s]])
+    assert checked == len(want) >= 4
+    cache.free()
+    m.free()
+
+
 def test_forward_trace_states():
     """ForwardTrace (transformer.hpp:14-19): embeddings, each layer, final
     norm; the embeddings are the dequantized rows and the head applied to
