@@ -1703,7 +1703,9 @@ int llmi_hip_model_free(llmi_hip_model* m) {
 
 size_t llmi_hip_model_weight_bytes(const llmi_hip_model* m) {
   if (m == nullptr) return 0;
+  // Weight::byte_size (weight.cpp:26-28): fp32 values, or packed codes + scales.
   auto qbytes = [&](std::size_t out, std::size_t in) {
+    if (m->type == LLMI_TYPE_F32) return out * in * sizeof(float);
     return out * row_bytes(in, m->type) + out * ceil_div(in, kBlock) * sizeof(float);
   };
   std::size_t total = qbytes(m->V, m->H) + (m->tied ? 0 : qbytes(m->V, m->H));
