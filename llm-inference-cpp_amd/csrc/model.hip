@@ -860,12 +860,18 @@ std::size_t attn_pv_lds(std::size_t npos) {
   return (npad + kPvCols * (npad + 4) + 4 * kPvChain) * sizeof(float);
 }
 
+// Static LDS of attn_pv_1: the expf table and the two reduction arrays.
+constexpr std::size_t kPvStaticLds = 32 * sizeof(std::uint64_t) + (kThreads / 16) * (sizeof(float) + sizeof(double));
+
 // The two-kernel decode path applies to one token with head_dim 64 or 128,
-// at most 16 query heads per KV head and a V slice that fits in LDS.
+// at most 16 query heads per KV head and p plus a V slice that fit in LDS
+// beside attn_pv_1's static arrays.
+
 bool decode_attention_fits(int nh, int nkv, int hd, std::size_t npos) {
   const int G = nh / nkv;
   return (hd == 64 || hd == 128) && G >= 1 && G <= 16 && nh % nkv == 0 &&
-         npos <= static_cast<std::size_t>(kPvScores) * kThreads && attn_pv_lds(npos) <= max_lds_per_block();
+         npos <= static_cast<std::size_t>(kPvScores) * kThreads &&
+         attn_pv_lds(npos) + kPvStaticLds <= max_lds_per_block();
 }
 
 // npos positions, the new token at npos - 1.
