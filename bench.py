@@ -453,6 +453,24 @@ def decode_runs(max_steps: int | None = None, greedy_only: bool = False):
                                          weight_bytes=int(wb))
         print(f"[bench] {key}: prefill {pre_ms:.1f} ms, decode {tok_s:.1f} tok/s, ids match "
               f"{res[key]['ids_match_reference']}", file=sys.stderr, flush=True)
+        # The same greedy run with the tolerance-mode decode step
+        # (llmi_hip_model_set_decode_mode): position-chunked attention merged
+        # in o_proj; logits within the fp32 tolerance, not bit-identical.
+        m.set_decode_mode(H.DECODE_TOLERANCE)
+        m.generate_greedy(prompt, 4)
+        ids_t = m.generate_greedy(prompt, rec["n_steps"])
+        _, dec_t = m.last_timing()
+        m.set_decode_mode(H.DECODE_EXACT)
+        tok_t = rec["n_steps"] / (dec_t * 1e-3)
+        want = np.array(rec["ids"], np.int32)
+        res[key]["tolerance_mode"] = dict(
+            decode_tok_s=round(tok_t, 1), frac_of_roofline=round(tok_t / roof, 4),
+            ids_match_first64=bool(np.array_equal(ids_t[:64], want[:64])),
+            ids_match_reference=bool(np.array_equal(ids_t, want)),
+            what="attention split over position chunks (softmax per chunk, merged in the o_proj launch); the "
+                 "quantized matmuls exact; logits within 1e-4 * max|logit| of the exact step (tests)")
+        print(f"[bench] {key}: tolerance-mode decode {tok_t:.1f} tok/s, first 64 ids match "
+              f"{res[key]['tolerance_mode']['ids_match_first64']}", file=sys.stderr, flush=True)
         if not greedy_only:
             res[key]["sampled"] = sampled_decode(m, prompt, rec, cfg)
         if cfg["vocab_size"] > 100000 and not greedy_only:
@@ -921,7 +939,7 @@ def main():
     per_shape = {} if args.no_shapes else per_shape_gpu()
     targets = {} if args.no_targets else target_shapes()
     decode = {} if args.no_decode else decode_runs(args.decode_steps, args.greedy_only)
-    decode_tol = {}
+    decode_tol = {k: r.pop("tolerance_mode") for k, r in decode.items() if "tolerance_mode" in r}
     gemm = {} if args.no_gemm else prefill_gemm()
     gguf = gguf_upload()
     cpu = None

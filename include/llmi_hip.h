@@ -417,6 +417,22 @@ int llmi_hip_model_last_timing(const llmi_hip_model* model, double* prefill_ms, 
  * every step ran queued.  Diagnostic: no counterpart in the reference. */
 int llmi_hip_model_last_redraws(const llmi_hip_model* model, size_t* steps);
 
+/* The arithmetic of the model's one-token decode steps (forward_cached with
+ * one token, generate_greedy / generate_sampled after the prompt).
+ * LLMI_DECODE_EXACT (the default): the reference's operations in its order,
+ * logits bit-identical to transformer.cpp:192-306.  LLMI_DECODE_TOLERANCE:
+ * the same quantized matmuls (still exact), but attention split over
+ * position chunks (at most 16 per head), each chunk's softmax taken against
+ * its own maximum with the hardware exponential, and the chunks merged in
+ * the o_proj launch's staging -- one launch per layer fewer; logits within
+ * the path's floating-point tolerance of the exact ones, not bit-identical.
+ * Applies to head_dim 64 / 128 with at most 16 query heads per KV head (other
+ * models keep the exact step); the prompt's prefill is exact in both modes.
+ * No counterpart in the reference (whose decode is exact by construction):
+ * a speed option for callers that accept the tolerance. */
+enum { LLMI_DECODE_EXACT = 0, LLMI_DECODE_TOLERANCE = 1 };
+int llmi_hip_model_set_decode_mode(llmi_hip_model* model, int mode);
+
 #ifdef __cplusplus
 } /* extern "C" */
 #endif

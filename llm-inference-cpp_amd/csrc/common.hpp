@@ -72,7 +72,17 @@ struct DeviceMatrix {
 // (kernels.cpp:115-120) with pw = w; kSiluUp silu(x) * pw, the reference's
 // SiLU times up (transformer.cpp:290, kernels.cpp:148).  Either one is the
 // same arithmetic as the separate glue kernel it replaces.
-enum { kPlain = 0, kRmsNorm = 1, kSiluUp = 2 };
+// kAttnCombine (tolerance-mode decode only): the attention output assembled
+// from per-chunk partial softmax states (attn_part_1): pw points to the
+// partials (layout at kAttnMaxChunks); GroupEntry::pa = head_dim.
+enum { kPlain = 0, kRmsNorm = 1, kSiluUp = 2, kAttnCombine = 3 };
+
+// Partial attention states of the tolerance-mode decode, per query head h
+// and position chunk c < kAttnMaxChunks, in one buffer of
+// kAttnMaxChunks * nh * (hd + 2) floats: o[h][c][hd] (the chunk's
+// unnormalised P.V), then m[h][c] (the chunk's score maximum), then
+// l[h][c] (its sum of exp(score - m)).
+constexpr int kAttnMaxChunks = 16;
 
 // One product of a grouped launch (qgemv_group), as the kernel reads it.
 struct GroupProblem {
@@ -82,7 +92,7 @@ struct GroupProblem {
   const float* x;
   const float* bias;
   float* y;
-  const float* pw;  // prologue operand (RMSNorm weight or the up vector)
+  const float* pw;  // prologue operand (RMSNorm weight, the up vector or the attention partials)
   float eps;        // RMSNorm epsilon
   int type, kind, in, nblk, out, rows, ntiles, bpw, accumulate, first_wg, prologue;
 };
@@ -99,6 +109,7 @@ struct GroupEntry {
   int prologue = kPlain;
   const float* pw = nullptr;
   float eps = 0.0f;
+  int pa = 0;  // kAttnCombine: head_dim
 };
 // One kernel launch of a group: the products of weight type `type` and row
 // chunk `rchunk` (GroupProblem::kNarrow: the 16-row tiles), at
@@ -122,8 +133,11 @@ struct DeviceGroup {
   const std::uint32_t* map = nullptr;
   std::vector<GroupLaunch> launches;
   std::vector<GroupProblem> host_probs;  // the table's host copy (few-product launches pass them by value)
+  int comb_hd = 0;                       // head_dim of a kAttnCombine product (0: none)
   int build(const GroupEntry* entries, std::size_t count);
-  int launch(hipStream_t s) const;
+  // chunks >= 0: the number of attention chunks for the kAttnCombine
+  // products (set per launch; such products run on the by-value path).
+  int launch(hipStream_t s, int chunks = -1) const;
   void release();
 };
 

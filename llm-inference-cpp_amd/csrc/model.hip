@@ -890,6 +890,212 @@ void launch_decode_attention(const float* q, const float* knew, const float* vne
   }
 }
 
+// ------------------------------- tolerance-mode decode attention (T = 1)
+// The one-token attention with the positions split into chunks (flash
+// decoding): not the reference's summation order -- the softmax is taken
+// per chunk against the chunk's own maximum and the chunks are merged by the
+// consumer (the o_proj launch's kAttnCombine staging) -- so it is used only
+// by the tolerance-mode decode step (llmi_hip_model_set_decode_mode).
+// grid (chunks, KV heads, head groups of kAttnHeads), one wavefront per
+// query head: a workgroup takes `chunk` positions of one KV head,
+// kAttnSub = 64 at a time staged in LDS by all its threads (K rows padded
+// by one float against bank conflicts); then each wavefront works on its own
+// head without further barriers -- lane r scores position r, a wavefront
+// max and sum update the head's running softmax, and lane d accumulates
+// output column d (and d + 64) over the sub-block's positions.  Each thread
+// loads its share of the next sub-block's K and V into registers before the
+// current one is used, and the first sub-block's loads are in flight while
+// q is read and rotated.  It writes o, m and l of each of its heads (the
+// layout at kAttnMaxChunks, common.hpp).  q and the new k are rotated (RoPE,
+// the same arithmetic as rope_and_cache); the workgroups holding position
+// npos - 1 take the new k and v in place of that cache row, and the first
+// head group writes them there (no workgroup reads that row).
+constexpr int kAttnSub = 64;    // positions per staged sub-block = lanes of a wavefront
+constexpr int kAttnHeads = 4;   // query heads (wavefronts) per workgroup
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+  return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
+template <int NCH>
+__global__ void __launch_bounds__(kAttnHeads * 64) attn_part_1(const float* __restrict__ q,
+                                                               const float* __restrict__ knew,
+                                                               const float* __restrict__ vnew, float* __restrict__ kc,
+                                                               float* __restrict__ vc, const float* __restrict__ cos_t,
+                                                               const float* __restrict__ sin_t,
+                                                               float* __restrict__ part, int nh, int nkv, int cap,
+                                                               int npos, int chunk, float scale) {
+  constexpr int hd = 16 * NCH, half = hd / 2;
+  constexpr int kT = kAttnHeads * 64;
+  constexpr int kLd = kAttnSub * hd / 4 / kT;  // float4 of K (and of V) per thread per sub-block
+  constexpr int kCols = hd / 64;               // output columns per lane
+  __shared__ float qs[kAttnHeads * hd];
+  __shared__ float kt[kAttnSub * (hd + 1)];
+  __shared__ float vt[kAttnSub * hd];
+  __shared__ float ps[kAttnHeads * kAttnSub];
+  __shared__ float kn[hd];
+  const int c = blockIdx.x, kvh = blockIdx.y;
+  const int G = nh / nkv;
+  const int g0 = blockIdx.z * kAttnHeads;
+  const int ng = min(kAttnHeads, G - g0);
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int pos = npos - 1;
+  const int s_begin = c * chunk, s_end = min(npos, s_begin + chunk);
+  const float* kh = kc + static_cast<std::size_t>(kvh) * cap * hd;
+  const float* vh = vc + static_cast<std::size_t>(kvh) * cap * hd;
+  const float* vn = vnew + static_cast<std::size_t>(kvh) * hd;
+
+  // Element e of a sub-block: row e / (hd / 4), columns 4 * (e % (hd / 4)) ..
+  float4 kr[kLd], vr[kLd];
+  const auto load_sub = [&](int sb) {
+#pragma unroll
+    for (int u = 0; u < kLd; ++u) {
+      const int e = u * kT + tid;
+      const int r = e / (hd / 4), c4 = 4 * (e - r * (hd / 4));
+      const int sp = sb + r;
+      const bool cached = sp < s_end && sp != pos;
+      kr[u] = cached ? *reinterpret_cast<const float4*>(kh + static_cast<std::size_t>(sp) * hd + c4)
+                     : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      vr[u] = cached ? *reinterpret_cast<const float4*>(vh + static_cast<std::size_t>(sp) * hd + c4)
+                     : sp == pos ? *reinterpret_cast<const float4*>(vn + c4) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+  };
+  const auto store_sub = [&](int sb) {
+#pragma unroll
+    for (int u = 0; u < kLd; ++u) {
+      const int e = u * kT + tid;
+      const int r = e / (hd / 4), c4 = 4 * (e - r * (hd / 4));
+      float4 kv = kr[u];
+      if (sb + r == pos) kv = make_float4(kn[c4], kn[c4 + 1], kn[c4 + 2], kn[c4 + 3]);
+      float* kd = kt + r * (hd + 1) + c4;
+      kd[0] = kv.x;
+      kd[1] = kv.y;
+      kd[2] = kv.z;
+      kd[3] = kv.w;
+      *reinterpret_cast<float4*>(vt + r * hd + c4) = vr[u];
+    }
+  };
+  load_sub(s_begin);
+
+  const float* cr = cos_t + static_cast<std::size_t>(pos) * half;
+  const float* sr = sin_t + static_cast<std::size_t>(pos) * half;
+  for (int e = tid; e < ng * half; e += kT) {
+    const int g = e / half, i = e - g * half;
+    const float* qh = q + static_cast<std::size_t>(kvh * G + g0 + g) * hd;
+    const float a = qh[i], b = qh[i + half], cs = cr[i], sn = sr[i];
+    qs[g * hd + i] = __builtin_fmaf(a, cs, -(b * sn));
+    qs[g * hd + i + half] = __builtin_fmaf(b, cs, a * sn);
+  }
+  const bool has_new = pos >= s_begin && pos < s_end;
+  if (has_new && tid < half) {
+    const float* kq = knew + static_cast<std::size_t>(kvh) * hd;
+    const float a = kq[tid], b = kq[tid + half], cs = cr[tid], sn = sr[tid];
+    kn[tid] = __builtin_fmaf(a, cs, -(b * sn));
+    kn[tid + half] = __builtin_fmaf(b, cs, a * sn);
+  }
+  __syncthreads();  // qs, kn
+  if (has_new && blockIdx.z == 0 && tid < hd) {
+    kc[(static_cast<std::size_t>(kvh) * cap + pos) * hd + tid] = kn[tid];
+    vc[(static_cast<std::size_t>(kvh) * cap + pos) * hd + tid] = vn[tid];
+  }
+  const bool active = w < ng;
+  const float* qg = qs + w * hd;
+  float* pw = ps + w * kAttnSub;
+  float mrun = -__builtin_inff(), lrun = 0.0f;
+  float acc[kCols];
+#pragma unroll
+  for (int k = 0; k < kCols; ++k) acc[k] = 0.0f;
+  for (int sb = s_begin; sb < s_end; sb += kAttnSub) {
+    const int n = min(kAttnSub, s_end - sb);
+    if (sb != s_begin) __syncthreads();  // every wavefront is done with the previous sub-block
+    store_sub(sb);
+    if (sb + kAttnSub < s_end) load_sub(sb + kAttnSub);
+    __syncthreads();  // the sub-block in LDS
+    if (active) {
+      // Score of position `lane`.
+      const float* kq = kt + lane * (hd + 1);
+      float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+#pragma unroll
+      for (int i = 0; i < hd; i += 4) {
+        a0 = __builtin_fmaf(qg[i], kq[i], a0);
+        a1 = __builtin_fmaf(qg[i + 1], kq[i + 1], a1);
+        a2 = __builtin_fmaf(qg[i + 2], kq[i + 2], a2);
+        a3 = __builtin_fmaf(qg[i + 3], kq[i + 3], a3);
+      }
+      const float sc = lane < n ? ((a0 + a1) + (a2 + a3)) * scale : -__builtin_inff();
+      const float mnew = fmaxf(mrun, wave_max(sc));
+      const float e = lane < n ? __expf(sc - mnew) : 0.0f;
+      const float f = __expf(mrun - mnew);  // 0 on the first sub-block (mrun = -inf)
+      lrun = __builtin_fmaf(lrun, f, wave_sum(e));
+      mrun = mnew;
+      pw[lane] = e;
+      __builtin_amdgcn_wave_barrier();
+      // Column lane (+ 64): the sub-block's P.V.
+#pragma unroll
+      for (int k = 0; k < kCols; ++k) {
+        const int d = lane + 64 * k;
+        float b0 = acc[k] * f, b1 = 0.0f;
+        int r = 0;
+        for (; r + 1 < n; r += 2) {
+          b0 = __builtin_fmaf(pw[r], vt[r * hd + d], b0);
+          b1 = __builtin_fmaf(pw[r + 1], vt[(r + 1) * hd + d], b1);
+        }
+        if (r < n) b0 = __builtin_fmaf(pw[r], vt[r * hd + d], b0);
+        acc[k] = b0 + b1;
+      }
+    }
+  }
+  // Partials: o[h][c][d], m[h][c], l[h][c].
+  if (active) {
+    const int h = kvh * G + g0 + w;
+    float* po = part + (static_cast<std::size_t>(h) * kAttnMaxChunks + c) * hd;
+#pragma unroll
+    for (int k = 0; k < kCols; ++k) po[lane + 64 * k] = acc[k];
+    if (lane == 0) {
+      float* pm = part + static_cast<std::size_t>(kAttnMaxChunks) * nh * hd;
+      pm[h * kAttnMaxChunks + c] = mrun;
+      pm[kAttnMaxChunks * nh + h * kAttnMaxChunks + c] = lrun;
+    }
+  }
+}
+
+// Positions per chunk of the tolerance-mode attention for npos positions:
+// a multiple of kAttnSub giving at most kAttnMaxChunks chunks.
+int attn_chunk(int npos) {
+  const int subs = (npos + kAttnSub - 1) / kAttnSub;
+  return kAttnSub * ((subs + kAttnMaxChunks - 1) / kAttnMaxChunks);
+}
+
+// The tolerance-mode decode path applies to head_dim 64 or 128 and at most
+// 16 query heads per KV head (any number of positions).
+bool tol_attention_fits(int nh, int nkv, int hd) {
+  const int G = nh / nkv;
+  return (hd == 64 || hd == 128) && G >= 1 && G <= 16 && nh % nkv == 0;
+}
+
+// Returns the number of chunks written.
+int launch_tol_attention(const float* q, const float* knew, const float* vnew, float* kc, float* vc,
+                         const float* cos_t, const float* sin_t, float* part, int nh, int nkv, int hd, int cap,
+                         int npos, float scale, hipStream_t s) {
+  const int chunk = attn_chunk(npos);
+  const int nch = (npos + chunk - 1) / chunk;
+  const int G = nh / nkv;
+  const dim3 grid(static_cast<unsigned>(nch), static_cast<unsigned>(nkv),
+                  static_cast<unsigned>((G + kAttnHeads - 1) / kAttnHeads));
+  if (hd == 64)
+    attn_part_1<4><<<grid, kAttnHeads * 64, 0, s>>>(q, knew, vnew, kc, vc, cos_t, sin_t, part, nh, nkv, cap, npos, chunk, scale);
+  else
+    attn_part_1<8><<<grid, kAttnHeads * 64, 0, s>>>(q, knew, vnew, kc, vc, cos_t, sin_t, part, nh, nkv, cap, npos, chunk, scale);
+  return nch;
+}
+
 std::size_t attention_static_lds() { return kThreads * (sizeof(double) + sizeof(float)) + 16; }
 
 // Dynamic LDS of the attention launch for npos positions.
@@ -1103,14 +1309,17 @@ unsigned blocks_for(std::size_t n) { return static_cast<unsigned>(ceil_div(n, kT
 struct DeviceLayer {
   float *attn_norm = nullptr, *mlp_norm = nullptr, *bq = nullptr, *bk = nullptr, *bv = nullptr;
   DeviceMatrix wq, wk, wv, wo, gate, up, down;
-  // The fused one-token step's launches (see decode_step).
-  DeviceGroup qkv, gate_up, down_silu;
+  // The fused one-token step's launches (see decode_step); o_comb is the
+  // tolerance-mode step's o_proj, which stages the attention output from
+  // the chunk partials (kAttnCombine).
+  DeviceGroup qkv, gate_up, down_silu, o_comb;
 };
 
 // Fixed one-token buffers of the fused decode step.
 struct DecodeBuffers {
   float *x = nullptr, *h = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *att = nullptr, *g = nullptr,
         *u = nullptr;
+  float* part = nullptr;  // the tolerance-mode attention's chunk partials
 };
 
 // Sampled steps queued per host read-back in generate_sampled.
@@ -1154,6 +1363,8 @@ struct llmi_hip_model {
   llmi_hip_cache* scratch = nullptr;
   std::vector<void*> allocations;
   double last_prefill_ms = 0.0, last_decode_ms = 0.0;  // of the last greedy run
+  int decode_mode = LLMI_DECODE_EXACT;  // llmi_hip_model_set_decode_mode
+  bool tol_ready = false;               // build_decode made the tolerance-mode step
   std::size_t last_redraws = 0;  // generate_sampled: queued draws redrawn step by step
 };
 
@@ -1251,7 +1462,13 @@ int build_decode(llmi_hip_model* m) {
   if (int rc = get(&d.att, m->Q)) return rc;
   if (int rc = get(&d.g, m->F)) return rc;
   if (int rc = get(&d.u, m->F)) return rc;
+  if (int rc = get(&d.part, static_cast<std::size_t>(kAttnMaxChunks) * m->c.num_heads * (m->hd + 2))) return rc;
   const float eps = static_cast<float>(m->c.rms_norm_eps);
+  // The tolerance-mode step: head sizes of attn_part_1, and an o_proj whose
+  // combine staging fits one workgroup of up to 512 threads (in <= 2048).
+  const bool tol = tol_attention_fits(static_cast<int>(m->c.num_heads), static_cast<int>(m->c.num_kv_heads),
+                                      static_cast<int>(m->hd)) &&
+                   m->Q <= 2048;
   for (DeviceLayer& l : m->layers) {
     const GroupEntry qkv[3] = {{&l.wq, d.x, l.bq, d.q, 1, false, kRmsNorm, l.attn_norm, eps},
                                {&l.wk, d.x, l.bk, d.k, 1, false, kRmsNorm, l.attn_norm, eps},
@@ -1262,7 +1479,13 @@ int build_decode(llmi_hip_model* m) {
     if (int rc = l.qkv.build(qkv, 3)) return rc;
     if (int rc = l.gate_up.build(gu, 2)) return rc;
     if (int rc = l.down_silu.build(dn, 1)) return rc;
+    if (tol) {
+      GroupEntry oc{&l.wo, d.part, nullptr, d.x, 1, true, kAttnCombine, d.part, 0.0f};
+      oc.pa = static_cast<int>(m->hd);
+      if (int rc = l.o_comb.build(&oc, 1)) return rc;
+    }
   }
+  m->tol_ready = tol;
   return LLMI_OK;
 }
 
@@ -1271,6 +1494,7 @@ void release_decode(llmi_hip_model* m) {
     l.qkv.release();
     l.gate_up.release();
     l.down_silu.release();
+    l.o_comb.release();
   }
 }
 
@@ -1423,7 +1647,10 @@ int ensure_workspace(llmi_hip_model* m, std::size_t T) {
 // One token (T = 1) through the fused per-layer launches built by
 // build_decode; the same arithmetic as forward_device.  Logits land in
 // ws.logits.
-int decode_step(llmi_hip_model* m, llmi_hip_cache* cache, hipStream_t s) {
+// tolerance: the attention of llmi_hip_model_set_decode_mode's tolerance
+// mode (position chunks merged in o_proj's staging); everything else is the
+// exact step.
+int decode_step(llmi_hip_model* m, llmi_hip_cache* cache, hipStream_t s, bool tolerance = false) {
   const auto& c = m->c;
   Workspace& w = m->ws;
   DecodeBuffers& d = m->dec;
@@ -1438,10 +1665,17 @@ int decode_step(llmi_hip_model* m, llmi_hip_cache* cache, hipStream_t s) {
   for (std::size_t li = 0; li < m->layers.size(); ++li) {
     const DeviceLayer& l = m->layers[li];
     if (int rc = l.qkv.launch(s)) return rc;
-    launch_decode_attention(d.q, d.k, d.v, cache->k + li * per_layer, cache->v + li * per_layer, m->cos_t, m->sin_t,
-                            cache->scores, d.att, nh, nkv, hd, static_cast<int>(cache->cap), static_cast<int>(pos + 1),
-                            scale, s);
-    if (int rc = launch_matmul(l.wo, d.att, 1, nullptr, d.x, s, true)) return rc;
+    if (tolerance) {
+      const int nch = launch_tol_attention(d.q, d.k, d.v, cache->k + li * per_layer, cache->v + li * per_layer,
+                                           m->cos_t, m->sin_t, d.part, nh, nkv, hd, static_cast<int>(cache->cap),
+                                           static_cast<int>(pos + 1), scale, s);
+      if (int rc = l.o_comb.launch(s, nch)) return rc;
+    } else {
+      launch_decode_attention(d.q, d.k, d.v, cache->k + li * per_layer, cache->v + li * per_layer, m->cos_t,
+                              m->sin_t, cache->scores, d.att, nh, nkv, hd, static_cast<int>(cache->cap),
+                              static_cast<int>(pos + 1), scale, s);
+      if (int rc = launch_matmul(l.wo, d.att, 1, nullptr, d.x, s, true)) return rc;
+    }
     if (int rc = l.gate_up.launch(s)) return rc;
     if (int rc = l.down_silu.launch(s)) return rc;
   }
@@ -1564,9 +1798,10 @@ int forward_device(llmi_hip_model* m, llmi_hip_cache* cache, std::size_t T, bool
   if (cache->len + T > m->c.max_position_embeddings)
     return fail(LLMI_ERR_STATE, "forward_cached: sequence longer than the model's context");
   const int nh = static_cast<int>(m->c.num_heads), nkv = static_cast<int>(m->c.num_kv_heads);
-  if (T == 1 && trace == nullptr && m->type != LLMI_TYPE_F32 &&
-      decode_attention_fits(nh, nkv, static_cast<int>(m->hd), cache->len + 1))
-    return decode_step(m, cache, s);
+  if (T == 1 && trace == nullptr && m->type != LLMI_TYPE_F32) {
+    if (m->decode_mode == LLMI_DECODE_TOLERANCE && m->tol_ready) return decode_step(m, cache, s, true);
+    if (decode_attention_fits(nh, nkv, static_cast<int>(m->hd), cache->len + 1)) return decode_step(m, cache, s);
+  }
   const std::size_t first = all_positions ? 0 : T - 1;
   return forward_rows(m, cache, T, first, T - first, false, s, trace);
 }
@@ -2022,6 +2257,13 @@ int llmi_hip_model_last_timing(const llmi_hip_model* m, double* prefill_ms, doub
 int llmi_hip_model_last_redraws(const llmi_hip_model* m, size_t* steps) {
   LLMI_REQUIRE(m != nullptr && steps != nullptr, "last_redraws: null pointer");
   *steps = m->last_redraws;
+  return LLMI_OK;
+}
+
+int llmi_hip_model_set_decode_mode(llmi_hip_model* m, int mode) {
+  LLMI_REQUIRE(m != nullptr, "set_decode_mode: null model");
+  LLMI_REQUIRE(mode == LLMI_DECODE_EXACT || mode == LLMI_DECODE_TOLERANCE, "set_decode_mode: unknown mode");
+  m->decode_mode = mode;
   return LLMI_OK;
 }
 

@@ -94,6 +94,7 @@ SIGNATURES = {
     "llmi_hip_model_generate_greedy": (_i, [_vp, _vp, _sz, _sz, _vp, _sz, _vp, C.POINTER(_sz)]),
     "llmi_hip_model_last_timing": (_i, [_vp, C.POINTER(_d), C.POINTER(_d)]),
     "llmi_hip_model_last_redraws": (_i, [_vp, C.POINTER(_sz)]),
+    "llmi_hip_model_set_decode_mode": (_i, [_vp, _i]),
     "llmi_hip_sample": (_i, [_vp, _sz, _vp, _d, C.POINTER(C.c_int32)]),
     "llmi_hip_sample_dev": (_i, [_vp, _sz, _vp, _d, C.POINTER(C.c_int32), _vp]),
     "llmi_hip_sampling_probabilities": (_i, [_vp, _sz, _vp, _vp]),
@@ -111,6 +112,9 @@ class Sampling(C.Structure):
 
     def __init__(self, temperature: float = 1.0, top_k: int = 0, top_p: float = 1.0):
         super().__init__(float(temperature), int(top_k), float(top_p))
+
+
+DECODE_EXACT, DECODE_TOLERANCE = 0, 1
 
 
 class HipError(RuntimeError):
@@ -506,6 +510,11 @@ class Model:
         v = _sz()
         check(self.lib.llmi_hip_model_last_redraws(self.h, C.byref(v)))
         return v.value
+
+    def set_decode_mode(self, mode: int) -> None:
+        """DECODE_EXACT (bit-identical, the default) or DECODE_TOLERANCE
+        (position-chunked attention merged in o_proj; llmi_hip.h)."""
+        check(self.lib.llmi_hip_model_set_decode_mode(self.h, int(mode)))
 
     def free(self) -> None:
         if self.h:

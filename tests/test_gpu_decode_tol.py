@@ -1,0 +1,128 @@
+"""The tolerance-mode decode step (llmi_hip_model_set_decode_mode): attention
+split over position chunks, merged in the o_proj launch's staging.  Its
+logits are held to the path's floating-point contract against the exact
+step, whose logits equal the reference's bit for bit (tests/test_gpu_model.py
+pins them at the full-size models' recorded steps):
+
+* per step, max|logits_tol - logits_exact| <= 1e-4 * max|logits_exact|
+  (the relative-error bar the north star states for fp32-accumulate paths),
+  fed the same tokens, on small models with head sizes 64 and 128, GQA groups
+  1, 3 and 7, and contexts from 1 to past 2048 positions (one chunk of 64 up
+  to sixteen chunks of 192);
+* on the synthetic SmolLM2-135M and Qwen2.5-0.5B:
+  the greedy ids of the first 64 steps equal the compiled reference's, and
+  every step's logits, fed the reference's ids, are within the bar.
+"""
+
+import json
+import os
+
+import numpy as np
+import pytest
+
+import llmi_hip as H
+import synth
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+TOL = 1e-4
+
+
+def rel_err(a, b):
+    a64, b64 = a.astype(np.float64), b.astype(np.float64)
+    return float(np.abs(a64 - b64).max() / max(np.abs(b64).max(), 1e-30))
+
+
+def cfg_of(hidden, heads, kv, arch=1, ctx=4096, layers=2, vocab=512):
+    return dict(arch=arch, vocab_size=vocab, hidden_size=hidden, intermediate_size=2 * hidden, num_layers=layers,
+                num_heads=heads, num_kv_heads=kv, max_position_embeddings=ctx, rms_norm_eps=1e-6,
+                rope_theta=10000.0, tie_word_embeddings=1, qkv_bias=int(arch == 1))
+
+
+@pytest.mark.parametrize("hidden,heads,kv,qt", [(128, 2, 2, H.Q8_0), (448, 7, 1, H.Q4_0), (576, 9, 3, H.Q8_0),
+                                                (256, 2, 1, H.Q4_0)])
+def test_tolerance_steps_match_exact_steps(hidden, heads, kv, qt):
+    """Steps at positions 1..80 after a one-token prompt, then steps at
+    positions ~1000-1100 and ~2100 after longer prompts (chunks of 64, 128 and
+    192 positions); both modes fed the same tokens."""
+    cfg = cfg_of(hidden, heads, kv)
+    m = H.Model(cfg, synth.make_tensors(cfg, 500 + hidden + heads, "bench"), qt)
+    worst = 0.0
+    for n_prompt, n_steps in ((1, 80), (1000, 100), (2100, 20)):
+        prompt = synth.uniform_ids(n_prompt + hidden, n_prompt, cfg["vocab_size"])
+        steps = synth.uniform_ids(n_steps + 7, n_steps, cfg["vocab_size"])
+        ce, ct = m.new_cache(n_prompt + n_steps), m.new_cache(n_prompt + n_steps)
+        m.set_decode_mode(H.DECODE_EXACT)
+        le = m.forward_cached(ce, prompt)
+        m.set_decode_mode(H.DECODE_TOLERANCE)
+        lt = m.forward_cached(ct, prompt)
+        if n_prompt > 1:
+            assert np.array_equal(le, lt)  # the prompt's prefill is exact in both modes
+        for i, tok in enumerate(steps):
+            m.set_decode_mode(H.DECODE_EXACT)
+            le = m.forward_cached(ce, [tok])
+            m.set_decode_mode(H.DECODE_TOLERANCE)
+            lt = m.forward_cached(ct, [tok])
+            err = rel_err(lt, le)
+            assert err <= TOL, (n_prompt, i, err)
+            worst = max(worst, err)
+        ce.free()
+        ct.free()
+    m.free()
+    print(f"hidden {hidden} heads {heads}/{kv}: worst relative logit error {worst:.3e}")
+
+
+def test_tolerance_mode_is_rejected_when_unknown():
+    cfg = cfg_of(128, 2, 2)
+    m = H.Model(cfg, synth.make_tensors(cfg, 3, "bench"), H.Q8_0)
+    with pytest.raises(H.HipError, match="unknown mode"):
+        m.set_decode_mode(7)
+    m.free()
+
+
+def test_head_size_without_a_tolerance_kernel_keeps_the_exact_step():
+    """head_dim 16 (the reference's tiny test models): the tolerance mode
+    falls back to the exact step, so its logits stay bit-identical."""
+    cfg = synth.tiny(1, True)
+    m = H.Model(cfg, synth.make_tensors(cfg, 8, "tiny"), H.Q4_0)
+    ce, ct = m.new_cache(16), m.new_cache(16)
+    for tok in [3, 9, 1, 30]:
+        m.set_decode_mode(H.DECODE_EXACT)
+        le = m.forward_cached(ce, [tok])
+        m.set_decode_mode(H.DECODE_TOLERANCE)
+        lt = m.forward_cached(ct, [tok])
+        assert np.array_equal(le, lt)
+    m.free()
+
+
+@pytest.mark.parametrize("name", ["c3_smollm2_q8", "c4_qwen25_q4"])
+def test_full_size_tolerance_decode(name):
+    with open(os.path.join(GOLDEN, name + ".json")) as f:
+        rec = json.load(f)
+    cfg = rec["cfg"]
+    m = H.synthetic_model_dev(cfg, rec["seed"], rec["type"], rec["convention"])
+    prompt = synth.uniform_ids(rec["prompt_seed"], rec["n_prompt"], cfg["vocab_size"])
+    m.set_decode_mode(H.DECODE_TOLERANCE)
+    ids = m.generate_greedy(prompt, 64)
+    assert list(ids) == rec["ids"][:64]
+    # Every step fed the reference's ids: tolerance against exact.
+    n = rec["n_steps"]
+    ce, ct = m.new_cache(rec["n_prompt"] + n), m.new_cache(rec["n_prompt"] + n)
+    m.set_decode_mode(H.DECODE_EXACT)
+    le = m.forward_cached(ce, prompt)
+    lt = m.forward_cached(ct, prompt)
+    worst = 0.0
+    for s in range(n - 1):
+        tok = [rec["ids"][s]]
+        m.set_decode_mode(H.DECODE_EXACT)
+        le = m.forward_cached(ce, tok)
+        m.set_decode_mode(H.DECODE_TOLERANCE)
+        lt = m.forward_cached(ct, tok)
+        err = rel_err(lt, le)
+        assert err <= TOL, (name, s, err)
+        worst = max(worst, err)
+    ce.free()
+    ct.free()
+    m.free()
+    print(f"{name}: worst relative logit error over {n - 1} steps {worst:.3e}")
