@@ -743,6 +743,23 @@ __global__ void __launch_bounds__(COMBINE ? kCombineMaxThreads : 1024) qgemv_few
 #undef LLMI_PICK
 }
 
+// One 16-row-tile product with its descriptor as scalar arguments, ordered
+// so that what the first loads need (the weight pointers and shape, x and
+// the prologue operand) is among the first 14 dwords, which arrive
+// preloaded in SGPRs (-amdgpu-kernarg-preload-count); the one-token step's
+// launches of one product take it.
+template <int TYPE, bool COMBINE = false>
+__global__ void __launch_bounds__(COMBINE ? kCombineMaxThreads : 1024)
+    qgemv_one_narrow(const uint4* __restrict__ codes, const float* __restrict__ scales, const float* __restrict__ x,
+                     const float* __restrict__ pw, int nblk, int bpw, int in, int prologue, float eps, int out,
+                     const float* __restrict__ bias, float* __restrict__ y, int accumulate, int comb_hd,
+                     int comb_nch) {
+  extern __shared__ float4 lds4[];
+  narrow_tile<TYPE, COMBINE>(gmem(codes), gmem(scales), gmem(x), gmem(bias), gmem_out(y), in, nblk, out, bpw,
+                             accumulate, blockIdx.x, reinterpret_cast<float*>(lds4), prologue, gmem(pw), eps, comb_hd,
+                             comb_nch);
+}
+
 // ------------------------------------------------------------ batch > 8
 // The exact multi-row product on many tiles: one workgroup per MR = 64
 // input rows x one 64-row tile of the matrix (64 outputs).  Per quantization
@@ -1623,6 +1640,25 @@ int DeviceGroup::launch(hipStream_t s, int chunks) const {
         f.comb_nch = chunks;
       }
       const dim3 grid(static_cast<unsigned>(l.total_wgs)), block(static_cast<unsigned>(l.waves * 64));
+      if (l.nprob == 1) {
+        // One product: scalar arguments (preloaded), qgemv_one_narrow.
+        const GroupProblem& p = f.p[0];
+        const auto* codes = reinterpret_cast<const uint4*>(p.codes);
+#define LLMI_ONE_ARGS                                                                                    \
+  codes, p.scales, p.x, p.pw, p.nblk, p.bpw, p.in, p.prologue, p.eps, p.out, p.bias, p.y, p.accumulate, \
+      f.comb_hd, f.comb_nch
+        if (comb) {
+          if (l.type == LLMI_TYPE_Q8_0) qgemv_one_narrow<LLMI_TYPE_Q8_0, true><<<grid, block, l.lds, s>>>(LLMI_ONE_ARGS);
+          else qgemv_one_narrow<LLMI_TYPE_Q4_0, true><<<grid, block, l.lds, s>>>(LLMI_ONE_ARGS);
+        } else if (l.type == LLMI_TYPE_Q8_0) {
+          qgemv_one_narrow<LLMI_TYPE_Q8_0><<<grid, block, l.lds, s>>>(LLMI_ONE_ARGS);
+        } else {
+          qgemv_one_narrow<LLMI_TYPE_Q4_0><<<grid, block, l.lds, s>>>(LLMI_ONE_ARGS);
+        }
+#undef LLMI_ONE_ARGS
+        LLMI_TRY_HIP(hipGetLastError());
+        continue;
+      }
       if (comb) {
         if (l.type == LLMI_TYPE_Q8_0) qgemv_few_narrow<LLMI_TYPE_Q8_0, true><<<grid, block, l.lds, s>>>(f);
         else qgemv_few_narrow<LLMI_TYPE_Q4_0, true><<<grid, block, l.lds, s>>>(f);

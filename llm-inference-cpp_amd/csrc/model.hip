@@ -1309,6 +1309,11 @@ unsigned blocks_for(std::size_t n) { return static_cast<unsigned>(ceil_div(n, kT
 struct DeviceLayer {
   float *attn_norm = nullptr, *mlp_norm = nullptr, *bq = nullptr, *bk = nullptr, *bv = nullptr;
   DeviceMatrix wq, wk, wv, wo, gate, up, down;
+  // q|k|v and gate|up as one matrix each (consecutive tiles of one
+  // allocation that wq, wk, wv / gate, up view), when every part has a
+  // multiple of 64 rows; out == 0 otherwise.  bqkv: the biases likewise.
+  DeviceMatrix wqkv, gate_up_w;
+  float* bqkv = nullptr;
   // The fused one-token step's launches (see decode_step); o_comb is the
   // tolerance-mode step's o_proj, which stages the attention output from
   // the chunk partials (kAttnCombine).
@@ -1431,6 +1436,60 @@ int dev_matrix(llmi_hip_model* m, const float* src, std::size_t out, std::size_t
   return LLMI_OK;
 }
 
+// Quantizes n fp32 matrices of the same `in` (host or device) into
+// consecutive tiles of one allocation when every one has a multiple of 64
+// rows -- each *dms[i] views its tiles and *fused views them all as one
+// matrix of sum(outs) rows -- else one by one (fused->out = 0).
+int dev_matrices(llmi_hip_model* m, const float* const* src, const std::size_t* outs, int n, std::size_t in,
+                 bool src_on_device, float* staging, DeviceMatrix* const* dms, DeviceMatrix* fused) {
+  *fused = DeviceMatrix{};
+  bool whole = m->type != LLMI_TYPE_F32;
+  std::size_t total = 0;
+  for (int i = 0; i < n; ++i) {
+    whole = whole && outs[i] % kTileRows == 0;
+    total += outs[i];
+  }
+  if (!whole) {
+    for (int i = 0; i < n; ++i)
+      if (int rc = dev_matrix(m, src[i], outs[i], in, src_on_device, staging, dms[i])) return rc;
+    return LLMI_OK;
+  }
+  fused->type = m->type;
+  fused->out = total;
+  fused->in = in;
+  fused->nblk = ceil_div(in, kBlock);
+  fused->ntiles = total / kTileRows;
+  fused->code_bytes = fused->ntiles * fused->nblk * kTileRows * block_code_bytes(m->type);
+  fused->scale_bytes = fused->ntiles * fused->nblk * kTileRows * sizeof(float);
+  if (int rc = dev_alloc(m, reinterpret_cast<void**>(&fused->codes), fused->code_bytes)) return rc;
+  if (int rc = dev_alloc(m, reinterpret_cast<void**>(&fused->scales), fused->scale_bytes)) return rc;
+  LLMI_TRY_HIP(hipMemsetAsync(fused->codes, 0, fused->code_bytes, library_stream()));
+  LLMI_TRY_HIP(hipMemsetAsync(fused->scales, 0, fused->scale_bytes, library_stream()));
+  std::size_t tile0 = 0;
+  for (int i = 0; i < n; ++i) {
+    DeviceMatrix* dm = dms[i];
+    dm->type = m->type;
+    dm->out = outs[i];
+    dm->in = in;
+    dm->nblk = fused->nblk;
+    dm->ntiles = outs[i] / kTileRows;
+    dm->code_bytes = dm->ntiles * dm->nblk * kTileRows * block_code_bytes(m->type);
+    dm->scale_bytes = dm->ntiles * dm->nblk * kTileRows * sizeof(float);
+    dm->codes = fused->codes + tile0 * fused->nblk * kTileRows * block_code_bytes(m->type);
+    dm->scales = fused->scales + tile0 * fused->nblk * kTileRows;
+    tile0 += dm->ntiles;
+    const float* w = src[i];
+    if (!src_on_device) {
+      LLMI_TRY_HIP(hipMemcpyAsync(staging, src[i], outs[i] * in * sizeof(float), hipMemcpyHostToDevice,
+                                  library_stream()));
+      w = staging;
+    }
+    if (int rc = launch_quantize(w, outs[i], in, m->type, nullptr, nullptr, dm, library_stream())) return rc;
+    LLMI_TRY_HIP(hipStreamSynchronize(library_stream()));
+  }
+  return LLMI_OK;
+}
+
 int check_config(const llmi_model_config& c) {
   LLMI_REQUIRE(c.arch == 0 || c.arch == 1, "model: arch must be 0 (Llama) or 1 (Qwen2)");
   LLMI_REQUIRE(c.vocab_size > 0 && c.hidden_size > 0 && c.intermediate_size > 0 && c.num_layers > 0,
@@ -1456,12 +1515,13 @@ int build_decode(llmi_hip_model* m) {
   const auto get = [&](float** p, std::size_t n) { return dev_alloc(m, reinterpret_cast<void**>(p), n * sizeof(float)); };
   if (int rc = get(&d.x, m->H)) return rc;
   if (int rc = get(&d.h, m->H)) return rc;
-  if (int rc = get(&d.q, m->Q)) return rc;
-  if (int rc = get(&d.k, m->KV)) return rc;
-  if (int rc = get(&d.v, m->KV)) return rc;
+  // q|k|v and g|u contiguous: the fused products write them in one go.
+  if (int rc = get(&d.q, m->Q + 2 * m->KV)) return rc;
+  d.k = d.q + m->Q;
+  d.v = d.k + m->KV;
   if (int rc = get(&d.att, m->Q)) return rc;
-  if (int rc = get(&d.g, m->F)) return rc;
-  if (int rc = get(&d.u, m->F)) return rc;
+  if (int rc = get(&d.g, 2 * m->F)) return rc;
+  d.u = d.g + m->F;
   if (int rc = get(&d.part, static_cast<std::size_t>(kAttnMaxChunks) * m->c.num_heads * (m->hd + 2))) return rc;
   const float eps = static_cast<float>(m->c.rms_norm_eps);
   // The tolerance-mode step: head sizes of attn_part_1, and an o_proj whose
@@ -1476,8 +1536,12 @@ int build_decode(llmi_hip_model* m) {
     const GroupEntry gu[2] = {{&l.gate, d.x, nullptr, d.g, 1, false, kRmsNorm, l.mlp_norm, eps},
                               {&l.up, d.x, nullptr, d.u, 1, false, kRmsNorm, l.mlp_norm, eps}};
     const GroupEntry dn[1] = {{&l.down, d.g, nullptr, d.x, 1, true, kSiluUp, d.u, 0.0f}};
-    if (int rc = l.qkv.build(qkv, 3)) return rc;
-    if (int rc = l.gate_up.build(gu, 2)) return rc;
+    // One fused product each where the weights are fused (its rows are
+    // q|k|v and gate|up, its output the contiguous buffers).
+    const GroupEntry qkv1[1] = {{&l.wqkv, d.x, l.bqkv, d.q, 1, false, kRmsNorm, l.attn_norm, eps}};
+    const GroupEntry gu1[1] = {{&l.gate_up_w, d.x, nullptr, d.g, 1, false, kRmsNorm, l.mlp_norm, eps}};
+    if (int rc = l.wqkv.out != 0 ? l.qkv.build(qkv1, 1) : l.qkv.build(qkv, 3)) return rc;
+    if (int rc = l.gate_up_w.out != 0 ? l.gate_up.build(gu1, 1) : l.gate_up.build(gu, 2)) return rc;
     if (int rc = l.down_silu.build(dn, 1)) return rc;
     if (tol) {
       GroupEntry oc{&l.wo, d.part, nullptr, d.x, 1, true, kAttnCombine, d.part, 0.0f};
@@ -1533,18 +1597,43 @@ int create_model(const llmi_model_config* cfg, const float* const* t, int type, 
   m->layers.resize(c.num_layers);
   for (auto& l : m->layers) {
     if (rc == LLMI_OK) rc = dev_vector(m.get(), t[k++], m->H, on_device, &l.attn_norm);
-    if (rc == LLMI_OK) rc = dev_matrix(m.get(), t[k++], m->Q, m->H, on_device, staging, &l.wq);
-    if (rc == LLMI_OK) rc = dev_matrix(m.get(), t[k++], m->KV, m->H, on_device, staging, &l.wk);
-    if (rc == LLMI_OK) rc = dev_matrix(m.get(), t[k++], m->KV, m->H, on_device, staging, &l.wv);
+    {
+      const float* src[3] = {t[k], t[k + 1], t[k + 2]};
+      const std::size_t outs[3] = {m->Q, m->KV, m->KV};
+      DeviceMatrix* const dms[3] = {&l.wq, &l.wk, &l.wv};
+      if (rc == LLMI_OK) rc = dev_matrices(m.get(), src, outs, 3, m->H, on_device, staging, dms, &l.wqkv);
+      k += 3;
+    }
     if (c.qkv_bias) {
-      if (rc == LLMI_OK) rc = dev_vector(m.get(), t[k++], m->Q, on_device, &l.bq);
-      if (rc == LLMI_OK) rc = dev_vector(m.get(), t[k++], m->KV, on_device, &l.bk);
-      if (rc == LLMI_OK) rc = dev_vector(m.get(), t[k++], m->KV, on_device, &l.bv);
+      if (rc == LLMI_OK && l.wqkv.out != 0) {
+        // One bias vector for the fused q|k|v product; bq, bk, bv view it.
+        rc = dev_alloc(m.get(), reinterpret_cast<void**>(&l.bqkv), (m->Q + 2 * m->KV) * sizeof(float));
+        if (rc == LLMI_OK) {
+          l.bq = l.bqkv;
+          l.bk = l.bqkv + m->Q;
+          l.bv = l.bk + m->KV;
+          const auto kind = on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice;
+          if (hipMemcpyAsync(l.bq, t[k], m->Q * sizeof(float), kind, library_stream()) != hipSuccess ||
+              hipMemcpyAsync(l.bk, t[k + 1], m->KV * sizeof(float), kind, library_stream()) != hipSuccess ||
+              hipMemcpyAsync(l.bv, t[k + 2], m->KV * sizeof(float), kind, library_stream()) != hipSuccess)
+            rc = fail(LLMI_ERR_HIP, "model_create: bias copy");
+        }
+        k += 3;
+      } else {
+        if (rc == LLMI_OK) rc = dev_vector(m.get(), t[k++], m->Q, on_device, &l.bq);
+        if (rc == LLMI_OK) rc = dev_vector(m.get(), t[k++], m->KV, on_device, &l.bk);
+        if (rc == LLMI_OK) rc = dev_vector(m.get(), t[k++], m->KV, on_device, &l.bv);
+      }
     }
     if (rc == LLMI_OK) rc = dev_matrix(m.get(), t[k++], m->H, m->Q, on_device, staging, &l.wo);
     if (rc == LLMI_OK) rc = dev_vector(m.get(), t[k++], m->H, on_device, &l.mlp_norm);
-    if (rc == LLMI_OK) rc = dev_matrix(m.get(), t[k++], m->F, m->H, on_device, staging, &l.gate);
-    if (rc == LLMI_OK) rc = dev_matrix(m.get(), t[k++], m->F, m->H, on_device, staging, &l.up);
+    {
+      const float* src[2] = {t[k], t[k + 1]};
+      const std::size_t outs[2] = {m->F, m->F};
+      DeviceMatrix* const dms[2] = {&l.gate, &l.up};
+      if (rc == LLMI_OK) rc = dev_matrices(m.get(), src, outs, 2, m->H, on_device, staging, dms, &l.gate_up_w);
+      k += 2;
+    }
     if (rc == LLMI_OK) rc = dev_matrix(m.get(), t[k++], m->H, m->F, on_device, staging, &l.down);
   }
   if (rc == LLMI_OK) rc = dev_vector(m.get(), t[k++], m->H, on_device, &m->final_norm);
