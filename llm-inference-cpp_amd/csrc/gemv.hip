@@ -383,24 +383,13 @@ constexpr int kStageBatch = 8;
 // `wgt` (nh * 16 floats of LDS).  Ends with a barrier.
 constexpr int kCombinePer = 4;  // elements per thread per round
 
-__device__ __forceinline__ float row16_max(float v) {
-#pragma unroll
-  for (int o = 8; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 16));
-  return v;
-}
-__device__ __forceinline__ float row16_sum(float v) {
-#pragma unroll
-  for (int o = 8; o >= 1; o >>= 1) v += __shfl_xor(v, o, 16);
-  return v;
-}
-
 __device__ __forceinline__ void stage_combine(const GMEM float* __restrict__ pw, int in, int hd, int nch, float* xs,
                                               float* wgt) {
   const int tid = threadIdx.x, nthreads = blockDim.x;
   const int nh = in / hd;
   const GMEM float* ms = pw + static_cast<std::size_t>(kAttnMaxChunks) * nh * hd;
   const GMEM float* ls = ms + kAttnMaxChunks * nh;
-  for (int i0 = 0; i0 < in; i0 += kCombinePer * nthreads) {
+  const auto round = [&](int i0) {
     float ov[kCombinePer][kAttnMaxChunks];
 #pragma unroll
     for (int k = 0; k < kCombinePer; ++k) {
@@ -411,14 +400,17 @@ __device__ __forceinline__ void stage_combine(const GMEM float* __restrict__ pw,
       for (int c = 0; c < kAttnMaxChunks; ++c) ov[k][c] = i < in && c < nch ? oh[c * hd] : 0.0f;
     }
     if (i0 == 0) {
-      for (int t = tid; t < nh * kAttnMaxChunks; t += nthreads) {
+      const int lane = tid & 63;
+      // Whole wavefronts take part (the DPP row reductions read every lane of a row).
+      for (int t = tid; t < ((nh * kAttnMaxChunks + 63) & ~63); t += nthreads) {
         const int c = t % kAttnMaxChunks;
-        const float m = c < nch ? ms[t] : -__builtin_inff();
-        const float l = c < nch ? ls[t] : 0.0f;
-        const float mx = row16_max(m);
-        const float w = c < nch ? __expf(m - mx) : 0.0f;
-        const float den = row16_sum(w * l);
-        wgt[t] = w / den;
+        const bool live = t < nh * kAttnMaxChunks && c < nch;
+        const float m = live ? ms[t] : -__builtin_inff();
+        const float l = live ? ls[t] : 0.0f;
+        const float mx = row_last_bcast(row_max16_f32(m), lane);
+        const float w = live ? __expf(m - mx) : 0.0f;
+        const float den = row_last_bcast(row_sum16_f32(w * l), lane);
+        if (t < nh * kAttnMaxChunks) wgt[t] = w / den;
       }
       __syncthreads();
     }
@@ -433,7 +425,10 @@ __device__ __forceinline__ void stage_combine(const GMEM float* __restrict__ pw,
         xs[i] = a;
       }
     }
-  }
+  };
+  // The first round outside the loop (see stage_x).
+  round(0);
+  for (int i0 = kCombinePer * nthreads; i0 < in; i0 += kCombinePer * nthreads) round(i0);
   __syncthreads();
 }
 
@@ -446,7 +441,7 @@ __device__ __forceinline__ void stage_x(const GMEM float* __restrict__ x, int in
   const bool one_round = in <= nthreads * kStageBatch;
   float v[kStageBatch], w[kStageBatch];
   double part = 0.0;
-  for (int i0 = 0; i0 < in; i0 += nthreads * kStageBatch) {
+  const auto round = [&](int i0) {
 #pragma unroll
     for (int u = 0; u < kStageBatch; ++u) {
       const int i = i0 + u * nthreads + tid;
@@ -470,7 +465,12 @@ __device__ __forceinline__ void stage_x(const GMEM float* __restrict__ x, int in
         }
       }
     }
-  }
+  };
+  // The first round outside the loop: a loop header makes the compiler wait
+  // for every load in flight (the caller's weight loads, issued just
+  // before), which would put the activations' round trip after theirs.
+  round(0);
+  for (int i0 = nthreads * kStageBatch; i0 < in; i0 += nthreads * kStageBatch) round(i0);
   if (prologue != kRmsNorm) {
     __syncthreads();
     return;

@@ -100,4 +100,39 @@ __device__ __forceinline__ double row_sum16_f64(double v) {
   return v;
 }
 
+// Float reductions over each row of 16 lanes with DPP row shifts (complete
+// in the row's last lane: 15, 31, 47, 63), and over the wavefront (the four
+// row results read into scalars, so the result is uniform).  Tree orders:
+// for the tolerance paths only.
+template <int N>
+__device__ __forceinline__ float row_shr_f32(float v, float fill) {
+  return __int_as_float(
+      __builtin_amdgcn_update_dpp(__float_as_int(fill), __float_as_int(v), 0x110 + N, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float row_max16_f32(float v) {
+  v = fmaxf(v, row_shr_f32<1>(v, v));
+  v = fmaxf(v, row_shr_f32<2>(v, v));
+  v = fmaxf(v, row_shr_f32<4>(v, v));
+  return fmaxf(v, row_shr_f32<8>(v, v));
+}
+__device__ __forceinline__ float row_sum16_f32(float v) {
+  v += row_shr_f32<1>(v, 0.0f);
+  v += row_shr_f32<2>(v, 0.0f);
+  v += row_shr_f32<4>(v, 0.0f);
+  return v + row_shr_f32<8>(v, 0.0f);
+}
+// Each lane gets its row's value from the row's last lane.
+__device__ __forceinline__ float row_last_bcast(float v, int lane) {
+  const float r0 = readlane_f32(v, 15), r1 = readlane_f32(v, 31), r2 = readlane_f32(v, 47), r3 = readlane_f32(v, 63);
+  return lane < 32 ? (lane < 16 ? r0 : r1) : (lane < 48 ? r2 : r3);
+}
+__device__ __forceinline__ float wave_max_dpp(float v) {
+  v = row_max16_f32(v);
+  return fmaxf(fmaxf(readlane_f32(v, 15), readlane_f32(v, 31)), fmaxf(readlane_f32(v, 47), readlane_f32(v, 63)));
+}
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+  v = row_sum16_f32(v);
+  return (readlane_f32(v, 15) + readlane_f32(v, 31)) + (readlane_f32(v, 47) + readlane_f32(v, 63));
+}
+
 }  // namespace llmi_hip

@@ -913,17 +913,6 @@ void launch_decode_attention(const float* q, const float* knew, const float* vne
 constexpr int kAttnSub = 64;    // positions per staged sub-block = lanes of a wavefront
 constexpr int kAttnHeads = 4;   // query heads (wavefronts) per workgroup
 
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
-  return v;
-}
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
-  return v;
-}
-
 template <int NCH>
 __global__ void __launch_bounds__(kAttnHeads * 64) attn_part_1(const float* __restrict__ q,
                                                                const float* __restrict__ knew,
@@ -1030,10 +1019,10 @@ __global__ void __launch_bounds__(kAttnHeads * 64) attn_part_1(const float* __re
         a3 = __builtin_fmaf(qg[i + 3], kq[i + 3], a3);
       }
       const float sc = lane < n ? ((a0 + a1) + (a2 + a3)) * scale : -__builtin_inff();
-      const float mnew = fmaxf(mrun, wave_max(sc));
+      const float mnew = fmaxf(mrun, wave_max_dpp(sc));
       const float e = lane < n ? __expf(sc - mnew) : 0.0f;
       const float f = __expf(mrun - mnew);  // 0 on the first sub-block (mrun = -inf)
-      lrun = __builtin_fmaf(lrun, f, wave_sum(e));
+      lrun = __builtin_fmaf(lrun, f, wave_sum_dpp(e));
       mrun = mnew;
       pw[lane] = e;
       __builtin_amdgcn_wave_barrier();
