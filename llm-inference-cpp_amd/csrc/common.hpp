@@ -147,6 +147,7 @@ struct GemmProblem {
   const std::uint8_t* codes;
   const float* scales;
   const std::uint16_t* xb;
+  const float* xf;  // the fp32 activations, read directly by launches with GemmLaunch::f32x
   const float* bias;
   float* y;
   int rows, in, ldx, out, nblk, ntiles, mtiles, first_wg, input;
@@ -182,6 +183,10 @@ struct GemmInput {
 struct GemmLaunch {
   int type = 0, total_wgs = 0;
   std::size_t prob_offset = 0, map_offset = 0;
+  // The GEMM reads the fp32 activations itself and rounds them to bf16 as it
+  // stages them (every product's K a multiple of 64, rows 16-byte aligned):
+  // no conversion launch, no bf16 copy.
+  bool f32x = false;
 };
 struct GemmPlan {
   std::vector<GemmProblem> probs;
@@ -191,6 +196,7 @@ struct GemmPlan {
   std::size_t scratch_elems = 0;  // bf16 elements of scratch the inputs need
   std::vector<std::size_t> part_off;  // per problem: float offset of its partials (split problems)
   std::size_t part_floats = 0;        // fp32 partials the split problems need
+  bool f32x = false;                  // the launches read fp32 activations (GemmLaunch::f32x)
 };
 // Bytes of a plan's scratch: the bf16 inputs, then (256-byte aligned) the
 // fp32 partials.

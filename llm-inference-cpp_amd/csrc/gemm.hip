@@ -147,7 +147,11 @@ struct XStage {
 // double-buffered LDS tile that all wavefronts fill together (also two steps
 // ahead through registers).  One barrier per K-step publishes the next
 // activation tile and frees the one just read.
-template <int TYPE>
+// F32X: the activations come as fp32 (p.xf, K a multiple of 64, rows
+// 16-byte aligned) and are rounded to bf16 (the same rounding as
+// x_to_bf16_batch) when staged in LDS; they are loaded one K-step ahead
+// instead of two, which keeps the registers of the bf16 ring.
+template <int TYPE, bool F32X = false>
 __global__ void __launch_bounds__(kGemmThreads) qgemm_mfma(const GemmProblem* __restrict__ probs,
                                                            const std::uint32_t* __restrict__ work_prob, int total,
                                                            GemmFew few) {
@@ -203,6 +207,30 @@ __global__ void __launch_bounds__(kGemmThreads) qgemm_mfma(const GemmProblem* __
   const auto xstore = [&](const XStage& st, int buf) {
 #pragma unroll
     for (int u = 0; u < 2; ++u) *reinterpret_cast<u32x4*>(&xs[buf][xlds[u]]) = st.v[u];
+  };
+  // F32X: the same chunks of 8 elements from the fp32 rows (two 16-byte
+  // loads each), converted when stored.
+  const GMEM f32x4* xf = (const GMEM f32x4*)p.xf;
+  std::size_t xfoff[2];
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int c = t + 512 * u, row = c >> 3, col = c & 7;
+    xfoff[u] = (static_cast<std::size_t>(min(m0 + row, M - 1)) * p.in + col * 8) / 4;
+  }
+  const auto xloadf = [&](f32x4 (&st)[2][2], int j) {
+    const int k = kb + min(j, nk - 1);
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      st[u][0] = xf[xfoff[u] + static_cast<std::size_t>(k) * (kBK / 4)];
+      st[u][1] = xf[xfoff[u] + static_cast<std::size_t>(k) * (kBK / 4) + 1];
+    }
+  };
+  const auto xstoref = [&](const f32x4 (&st)[2][2], int buf) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+      *reinterpret_cast<u32x4*>(&xs[buf][xlds[u]]) =
+          u32x4{pack_bf16(st[u][0][0], st[u][0][1]), pack_bf16(st[u][0][2], st[u][0][3]),
+                pack_bf16(st[u][1][0], st[u][1][1]), pack_bf16(st[u][1][2], st[u][1][3])};
   };
 
   // This lane's weight rows (columns of the tile): n0 + wn0 + 16j + lane%16,
@@ -284,11 +312,38 @@ __global__ void __launch_bounds__(kGemmThreads) qgemm_mfma(const GemmProblem* __
           acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bf[s][j], a[s][i], acc[i][j], 0, 0, 0);
   };
 
+  WStage<TYPE> WA, WB;
+  bf16x8 BA[2][2], BB[2][2];
+  if constexpr (F32X) {
+    // Activations one step ahead in X; weights as below.
+    f32x4 X[2][2];
+    xloadf(X, 0);
+    wload(WA, 0);
+    wload(WB, 1);
+    xstoref(X, 0);
+    xloadf(X, 1);
+    dequant(WA, BA);
+    wload(WA, 2);
+    __syncthreads();  // step 0's activations staged
+    for (int k = 0; k < nk; k += 2) {
+      if (k + 1 < nk) xstoref(X, 1);
+      xloadf(X, k + 2);
+      dequant(WB, BB);
+      wload(WB, k + 3);
+      step(0, BA);
+      __syncthreads();
+      if (k + 1 >= nk) break;
+      if (k + 2 < nk) xstoref(X, 0);
+      xloadf(X, k + 3);
+      dequant(WA, BA);
+      wload(WA, k + 4);
+      step(1, BB);
+      __syncthreads();
+    }
+  } else {
   // Rings: activations of step k in XA (even k) / XB (odd), raw weights in
   // WA / WB likewise, dequantized weights of step k in BA / BB.
   XStage XA, XB;
-  WStage<TYPE> WA, WB;
-  bf16x8 BA[2][2], BB[2][2];
   xload(XA, 0);
   xload(XB, 1);
   wload(WA, 0);
@@ -312,6 +367,7 @@ __global__ void __launch_bounds__(kGemmThreads) qgemm_mfma(const GemmProblem* __
     wload(WA, k + 4);
     step(1, BB);
     __syncthreads();
+  }
   }
 
   // Rows of y / part are 16-byte aligned when N is a multiple of 4: a lane's
@@ -437,6 +493,11 @@ std::size_t gemm_ldx(std::size_t in) { return (in + kBK - 1) / kBK * kBK; }
 
 int plan_gemm_group(const GroupEntry* entries, std::size_t count, GemmPlan* plan) {
   *plan = GemmPlan{};
+  // fp32 activations read directly when every product allows it.
+  plan->f32x = true;
+  for (std::size_t i = 0; i < count; ++i)
+    if (entries[i].m != nullptr && entries[i].rows > 0 && entries[i].m->out > 0)
+      plan->f32x = plan->f32x && entries[i].m->in % kBK == 0 && reinterpret_cast<std::uintptr_t>(entries[i].x) % 16 == 0;
   // Distinct activation matrices, each converted to bf16 once per launch.
   for (std::size_t i = 0; i < count; ++i) {
     const GroupEntry& e = entries[i];
@@ -460,7 +521,7 @@ int plan_gemm_group(const GroupEntry* entries, std::size_t count, GemmPlan* plan
       in.in = m.in;
       in.ldx = gemm_ldx(m.in);
       in.offset = plan->scratch_elems;
-      plan->scratch_elems += in.rows * in.ldx;
+      if (!plan->f32x) plan->scratch_elems += in.rows * in.ldx;
       plan->inputs.push_back(in);
     }
   }
@@ -484,6 +545,7 @@ int plan_gemm_group(const GroupEntry* entries, std::size_t count, GemmPlan* plan
       GemmProblem p{};
       p.codes = m.codes;
       p.scales = m.scales;
+      p.xf = e.x;
       p.bias = e.bias;
       p.y = e.y;
       p.rows = static_cast<int>(e.rows);
@@ -512,6 +574,7 @@ int plan_gemm_group(const GroupEntry* entries, std::size_t count, GemmPlan* plan
     }
     if (nprob == 0) continue;
     l.total_wgs = static_cast<int>(wg);
+    l.f32x = plan->f32x;
     plan->launches.push_back(l);
   }
   return LLMI_OK;
@@ -544,6 +607,7 @@ int launch_gemm_reduces(const GemmPlan& plan, hipStream_t s) {
 }
 
 int launch_gemm_inputs(const GemmPlan& plan, std::uint16_t* scratch, hipStream_t s) {
+  if (plan.f32x) return LLMI_OK;  // the GEMM reads the fp32 activations itself
   // The inputs in batches of kConvBatch per launch, each batch's octets
   // counted in 32 bits (a batch is cut short before it would overflow).
   std::size_t i0 = 0;
@@ -680,10 +744,16 @@ int launch_gemm(const GemmProblem* probs_dev, const std::uint32_t* map_dev, cons
     for (int i = 0; i < nfew; ++i) few.p[i] = one[i];
     few.count = nfew;
   }
-  if (l.type == LLMI_TYPE_Q8_0)
+  if (l.f32x) {
+    if (l.type == LLMI_TYPE_Q8_0)
+      qgemm_mfma<LLMI_TYPE_Q8_0, true><<<l.total_wgs, kGemmThreads, 0, s>>>(probs, map, l.total_wgs, few);
+    else
+      qgemm_mfma<LLMI_TYPE_Q4_0, true><<<l.total_wgs, kGemmThreads, 0, s>>>(probs, map, l.total_wgs, few);
+  } else if (l.type == LLMI_TYPE_Q8_0) {
     qgemm_mfma<LLMI_TYPE_Q8_0><<<l.total_wgs, kGemmThreads, 0, s>>>(probs, map, l.total_wgs, few);
-  else
+  } else {
     qgemm_mfma<LLMI_TYPE_Q4_0><<<l.total_wgs, kGemmThreads, 0, s>>>(probs, map, l.total_wgs, few);
+  }
   LLMI_TRY_HIP(hipGetLastError());
   return LLMI_OK;
 }
