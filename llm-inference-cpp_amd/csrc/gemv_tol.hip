@@ -412,7 +412,11 @@ __global__ void __launch_bounds__(1024) qgemv_tol_wide(const TolProblem* __restr
                                                        TolSplit single_split) {
   static_assert(R == 4 || R == 8, "batches of three to eight rows");
   constexpr int kC = wide_chunk(R);  // blocks per chunk (registers: eight rows keep fewer in flight)
-  constexpr int kRegionSlots = kZeroSlots + R * kC * kSlotsPerBlock;
+  // A row's kC * 8 slots are followed by one slot of padding: the active
+  // lanes of an A read fetch one slot of each of 8 rows, which at a stride
+  // of 8 slots (128 bytes) fall into the same LDS banks.
+  constexpr int kRowSlots = kC * kSlotsPerBlock + 1;
+  constexpr int kRegionSlots = kZeroSlots + R * kRowSlots;
   extern __shared__ tu32x4 lds[];
   const int wg = blockIdx.x;
   TolProblem p = single;
@@ -464,7 +468,10 @@ __global__ void __launch_bounds__(1024) qgemv_tol_wide(const TolProblem* __restr
   const auto stage_chunk = [&]() {
 #pragma unroll
     for (int k = 0; k < kCopy; ++k)
-      if (lane + 64 * k < kChunkSlots) wl[kZeroSlots + lane + 64 * k] = xs[k];
+      if (lane + 64 * k < kChunkSlots) {
+        const int i = lane + 64 * k, r = i / (kC * kSlotsPerBlock);
+        wl[kZeroSlots + r * kRowSlots + (i - r * kC * kSlotsPerBlock)] = xs[k];
+      }
     if (lane < kC * R) wsx[lane] = sxv;
   };
 
@@ -474,7 +481,7 @@ __global__ void __launch_bounds__(1024) qgemv_tol_wide(const TolProblem* __restr
   int part, arow;
   a_role<true>(lane, &active, &part, &arow);
   const bool on = active && arow < nr;
-  const int base = on ? kZeroSlots + arow * kC * kSlotsPerBlock + part : 0;
+  const int base = on ? kZeroSlots + arow * kRowSlots + part : 0;
   const int step = on ? kSlotsPerBlock : 0;
   const TolMagic mk = tol_magic();
 
@@ -567,8 +574,10 @@ int tol_waves(std::size_t nblk) {
 // reduction area.
 std::size_t tol_lds(int waves, int R, int bpw) {
   const std::size_t blocks = R <= 2 ? static_cast<std::size_t>(bpw) : static_cast<std::size_t>(wide_chunk(R));
+  // qgemv_tol_wide pads each row of its chunk by one slot.
+  const std::size_t pad = R <= 2 ? 0 : static_cast<std::size_t>(R);
   return static_cast<std::size_t>(waves) *
-         ((kZeroSlots + static_cast<std::size_t>(R) * blocks * kSlotsPerBlock) * sizeof(tu32x4) +
+         ((kZeroSlots + static_cast<std::size_t>(R) * blocks * kSlotsPerBlock + pad) * sizeof(tu32x4) +
           static_cast<std::size_t>(R) * blocks * sizeof(float) + static_cast<std::size_t>(R) * kTileRows * sizeof(float));
 }
 // Row chunk R (1, 2, 4, 8): the smallest covering `rows`.
