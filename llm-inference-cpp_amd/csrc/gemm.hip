@@ -45,7 +45,13 @@ constexpr int kBM = 128, kBN = 256, kBK = 64;
 // K of more than kSplitMinSteps steps of kBK may be split over workgroups;
 // kCus is MI355X's CU count.
 constexpr std::size_t kSplitMinSteps = 24, kCus = 256;
-constexpr int kGemmThreads = 512;  // 8 wavefronts
+constexpr int kGemmThreads = 512;  // 8 wavefronts: 2 (tokens) x 4 (outputs)
+constexpr int kWavesN = 8;
+constexpr int kWaveN = kBN / kWavesN;                      // outputs per wavefront (64)
+constexpr int kWaveM = kBM / (kGemmThreads / 64 / kWavesN);  // tokens per wavefront (64)
+constexpr int kJ = kWaveN / 16;                            // 16-output MFMA blocks per wavefront
+constexpr int kI = kWaveM / 16;                            // 16-token MFMA blocks per wavefront
+constexpr int kXPer = kBM * kBK / 8 / kGemmThreads;        // 16-byte chunks of the activation tile per thread
 constexpr int kLdsRow = kBK + 8;  // bf16 per LDS row (16 bytes of padding)
 constexpr int kXcds = 8;
 
@@ -122,21 +128,25 @@ __global__ void __launch_bounds__(256) x_to_bf16_batch(ConvBatch c) {
   }
 }
 
-// One K-step (64) of a wavefront's weights as loaded: for each K-slice s (a
-// quantization block) and column group j, the 8 codes a lane feeds the MFMA
-// (Q8_0: 8 bytes, Q4_0: 8 nibbles in one word) and the row's block scale;
-// live[s]: block s exists (else its scale counts as 0).
+// One K-step (64 = two quantization blocks) of a wavefront's weights as
+// loaded.  The step's K order is permuted (the same permutation for the
+// activations, so the sums are unchanged): lane quarter q holds 16
+// consecutive codes of block q/2 -- elements 16(q%2) .. 16(q%2)+15, one
+// 16-byte load for Q8_0, 8 bytes for Q4_0 -- and feeds the first 8 to the
+// step's first MFMA and the other 8 to its second; so for each column group
+// j a lane needs one code load and one scale (its block's).  live: the
+// lane's block exists (else its scale counts as 0).
 template <int TYPE>
 struct WStage {
-  using Code = std::conditional_t<TYPE == LLMI_TYPE_Q8_0, u32x2, std::uint32_t>;
-  Code c[2][2];
-  float sc[2][2];
-  bool live[2];
+  using Code = std::conditional_t<TYPE == LLMI_TYPE_Q8_0, u32x4, u32x2>;
+  Code c[kJ];
+  float sc[kJ];
+  bool live;
 };
-// One K-step of the activation tile held by one thread: chunks t and t+512
+// One K-step of the activation tile held by one thread: chunks t + 256u
 // (16 bytes each) of the 128 x 64 bf16 tile.
 struct XStage {
-  u32x4 v[2];
+  u32x4 v[kXPer];
 };
 
 // qgemm_mfma: a workgroup computes a 128-token x 256-output tile of y = x W^T
@@ -183,102 +193,101 @@ __global__ void __launch_bounds__(kGemmThreads) qgemm_mfma(const GemmProblem* __
   const int t = threadIdx.x;
   const int lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
-  const int wn0 = wave * 32;
+  const int wn0 = (wave % kWavesN) * kWaveN, wm0 = (wave / kWavesN) * kWaveM;
   const int arow = lane & 15, q = lane >> 4;
 
   // Every load is issued unconditionally from an address inside the
   // operands (rows past M or N are clamped to the last one; their results
   // are never stored; steps past the last re-read it), so no load sits
   // behind a branch.
-  const GMEM u32x4* xb = (const GMEM u32x4*)p.xb;
-  std::size_t xoff[2];
-  int xlds[2];
+  // Each load addresses a base common to the wavefront (the operand, the
+  // tile and the K-step: SGPR arithmetic) plus a lane offset in bytes fixed
+  // for the whole loop, so a step's loads take no per-lane address work.
+  using GB = const GMEM unsigned char*;
+  std::uint32_t xoff[kXPer], xfoff[kXPer];
+  int xlds[kXPer];
 #pragma unroll
-  for (int u = 0; u < 2; ++u) {
-    const int c = t + 512 * u, row = c >> 3, col = c & 7;
-    xoff[u] = (static_cast<std::size_t>(min(m0 + row, M - 1)) * ldx + col * 8) / 8;
+  for (int u = 0; u < kXPer; ++u) {
+    const int c = t + kGemmThreads * u, row = c >> 3, col = c & 7;
+    const int r = min(m0 + row, M - 1) - m0;  // the tile's row, clamped
+    xoff[u] = static_cast<std::uint32_t>((r * ldx + col * 8) * 2);
+    xfoff[u] = static_cast<std::uint32_t>((r * p.in + col * 8) * 4);
     xlds[u] = row * kLdsRow + col * 8;
   }
+  const GB xb_tile = (GB)p.xb + static_cast<std::size_t>(m0) * ldx * 2;
+  const GB xf_tile = (GB)p.xf + static_cast<std::size_t>(m0) * p.in * 4;
   const auto xload = [&](XStage& st, int j) {
-    const int k = kb + min(j, nk - 1);
+    const GB base = xb_tile + static_cast<std::size_t>(kb + min(j, nk - 1)) * (kBK * 2);
 #pragma unroll
-    for (int u = 0; u < 2; ++u) st.v[u] = xb[xoff[u] + static_cast<std::size_t>(k) * (kBK / 8)];
+    for (int u = 0; u < kXPer; ++u) st.v[u] = *(const GMEM u32x4*)(base + xoff[u]);
   };
   const auto xstore = [&](const XStage& st, int buf) {
 #pragma unroll
-    for (int u = 0; u < 2; ++u) *reinterpret_cast<u32x4*>(&xs[buf][xlds[u]]) = st.v[u];
+    for (int u = 0; u < kXPer; ++u) *reinterpret_cast<u32x4*>(&xs[buf][xlds[u]]) = st.v[u];
   };
   // F32X: the same chunks of 8 elements from the fp32 rows (two 16-byte
   // loads each), converted when stored.
-  const GMEM f32x4* xf = (const GMEM f32x4*)p.xf;
-  std::size_t xfoff[2];
+  const auto xloadf = [&](f32x4 (&st)[kXPer][2], int j) {
+    const GB base = xf_tile + static_cast<std::size_t>(kb + min(j, nk - 1)) * (kBK * 4);
 #pragma unroll
-  for (int u = 0; u < 2; ++u) {
-    const int c = t + 512 * u, row = c >> 3, col = c & 7;
-    xfoff[u] = (static_cast<std::size_t>(min(m0 + row, M - 1)) * p.in + col * 8) / 4;
-  }
-  const auto xloadf = [&](f32x4 (&st)[2][2], int j) {
-    const int k = kb + min(j, nk - 1);
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      st[u][0] = xf[xfoff[u] + static_cast<std::size_t>(k) * (kBK / 4)];
-      st[u][1] = xf[xfoff[u] + static_cast<std::size_t>(k) * (kBK / 4) + 1];
+    for (int u = 0; u < kXPer; ++u) {
+      st[u][0] = *(const GMEM f32x4*)(base + xfoff[u]);
+      st[u][1] = *(const GMEM f32x4*)(base + xfoff[u] + 16);
     }
   };
-  const auto xstoref = [&](const f32x4 (&st)[2][2], int buf) {
+  const auto xstoref = [&](const f32x4 (&st)[kXPer][2], int buf) {
 #pragma unroll
-    for (int u = 0; u < 2; ++u)
+    for (int u = 0; u < kXPer; ++u)
       *reinterpret_cast<u32x4*>(&xs[buf][xlds[u]]) =
           u32x4{pack_bf16(st[u][0][0], st[u][0][1]), pack_bf16(st[u][0][2], st[u][0][3]),
                 pack_bf16(st[u][1][0], st[u][1][1]), pack_bf16(st[u][1][2], st[u][1][3])};
   };
 
   // This lane's weight rows (columns of the tile): n0 + wn0 + 16j + lane%16,
-  // clamped into the padded matrix; the wavefront's 32 rows lie in one
-  // 64-row tile.
-  const int wrow0 = min(n0 + wn0 + arow, p.ntiles * kTileRows - 1);
-  const int wrow1 = min(n0 + wn0 + 16 + arow, p.ntiles * kTileRows - 1);
-  const std::size_t wt0 = static_cast<std::size_t>(wrow0 / kTileRows) * nblk,
-                    wt1 = static_cast<std::size_t>(wrow1 / kTileRows) * nblk;
-  const int wl0 = wrow0 % kTileRows, wl1 = wrow1 % kTileRows;
-  const GMEM float* scales = (const GMEM float*)p.scales;
+  // clamped into the padded matrix.  A wavefront's rows are 32 aligned rows,
+  // so they lie in one 64-row tile (the last one for rows past the matrix).
+  const int wtile = min((n0 + wn0) / kTileRows, p.ntiles - 1);
+  std::uint32_t wco[kJ], wso[kJ];  // lane offsets (bytes) of codes and scales in a block
+#pragma unroll
+  for (int jj = 0; jj < kJ; ++jj) {
+    const int r = min(n0 + wn0 + 16 * jj + arow, p.ntiles * kTileRows - 1) - wtile * kTileRows;
+    if constexpr (TYPE == LLMI_TYPE_Q8_0)
+      wco[jj] = static_cast<std::uint32_t>((q & 1) * kTileRows * 16 + r * 16);  // 16-byte half q%2 of the row
+    else
+      wco[jj] = static_cast<std::uint32_t>(r * 16 + (q & 1) * 8);  // bytes 8(q%2) .. of the row
+    wso[jj] = static_cast<std::uint32_t>(r * 4);
+  }
+  constexpr std::size_t kBlockBytes = (TYPE == LLMI_TYPE_Q8_0 ? 32 : 16) * kTileRows;  // codes of one 64-row block
+  const GB wcodes = (GB)p.codes + static_cast<std::size_t>(wtile) * nblk * kBlockBytes;
+  const GB wscales = (GB)p.scales + static_cast<std::size_t>(wtile) * nblk * kTileRows * 4;
   const auto wload = [&](WStage<TYPE>& st, int j) {
     const int k = kb + min(j, nk - 1);
+    const int blk = 2 * k + (q >> 1);
+    st.live = blk < nblk;
+    const int bc = min(blk, nblk - 1);
+    const GB cb = wcodes + static_cast<std::size_t>(bc) * kBlockBytes;
+    const GB sb = wscales + static_cast<std::size_t>(bc) * kTileRows * 4;
 #pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      const int blk = 2 * k + s;
-      st.live[s] = blk < nblk;
-      const int bc = min(blk, nblk - 1);
-#pragma unroll
-      for (int jj = 0; jj < 2; ++jj) {
-        const std::size_t sl = (jj == 0 ? wt0 : wt1) + bc;
-        const int wl = jj == 0 ? wl0 : wl1;
-        if constexpr (TYPE == LLMI_TYPE_Q8_0) {
-          // Block = two 16-byte halves of 64 rows; codes 8q..8q+7.
-          const GMEM u32x2* codes = (const GMEM u32x2*)p.codes;
-          st.c[s][jj] = codes[((sl * 2 + (q >> 1)) * kTileRows + wl) * 2 + (q & 1)];
-        } else {
-          // Block = 16 bytes per row; codes 8q..8q+7 are word q.
-          const GMEM std::uint32_t* codes = (const GMEM std::uint32_t*)p.codes;
-          st.c[s][jj] = codes[(sl * kTileRows + wl) * 4 + q];
-        }
-        st.sc[s][jj] = scales[sl * kTileRows + wl];
-      }
+    for (int jj = 0; jj < kJ; ++jj) {
+      if constexpr (TYPE == LLMI_TYPE_Q8_0) st.c[jj] = *(const GMEM u32x4*)(cb + wco[jj]);
+      else st.c[jj] = *(const GMEM u32x2*)(cb + wco[jj]);
+      st.sc[jj] = *(const GMEM float*)(sb + wso[jj]);
     }
   };
   // bf16(code * scale), the operand of the fp32 restatement rounded once.
-  const auto dequant = [&](const WStage<TYPE>& st, bf16x8 (&bf)[2][2]) {
+  // bf[t][j]: the codes the lane feeds the step's MFMA t for column group j.
+  const auto dequant = [&](const WStage<TYPE>& st, bf16x8 (&bf)[2][kJ]) {
 #pragma unroll
     for (int s = 0; s < 2; ++s)
 #pragma unroll
-      for (int jj = 0; jj < 2; ++jj) {
-        const float sc = st.live[s] ? st.sc[s][jj] : 0.0f;
+      for (int jj = 0; jj < kJ; ++jj) {
+        const float sc = st.live ? st.sc[jj] : 0.0f;
         float c[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           int code;
-          if constexpr (TYPE == LLMI_TYPE_Q8_0) code = sbyte(st.c[s][jj][e >> 2], e & 3);
-          else code = snib(st.c[s][jj], e);
+          if constexpr (TYPE == LLMI_TYPE_Q8_0) code = sbyte(st.c[jj][2 * s + (e >> 2)], e & 3);
+          else code = snib(st.c[jj][s], e);
           c[e] = static_cast<float>(code) * sc;
         }
         const u32x4 pk{pack_bf16(c[0], c[1]), pack_bf16(c[2], c[3]), pack_bf16(c[4], c[5]), pack_bf16(c[6], c[7])};
@@ -286,95 +295,127 @@ __global__ void __launch_bounds__(kGemmThreads) qgemm_mfma(const GemmProblem* __
       }
   };
 
-  f32x4 acc[8][2];
+  f32x4 acc[kI][kJ];
 #pragma unroll
-  for (int i = 0; i < 8; ++i)
+  for (int i = 0; i < kI; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int j = 0; j < kJ; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-  // One K-step: the 16 activation fragments of the step (two K-slices of
-  // 32), then 32 MFMAs.  The product is W x^T: acc[i][j][e] holds token
-  // m0 + 16i + lane%16 and output n0 + wn0 + 16j + 4*(lane/16) + e, so a
-  // lane's four values are consecutive outputs of one token.
-  const auto step = [&](int buf, const bf16x8 (&bf)[2][2]) {
-    bf16x8 a[2][8];
+  // One K-step: 2 kI activation fragments (lane quarter q reads the step's
+  // elements 32(q/2) + 16(q%2) + 8s .. + 7 for MFMA s, the K order of its
+  // weights), then 2 kI kJ MFMAs.  The product is W x^T: acc[i][j][e] holds
+  // token m0 + wm0 + 16i + lane%16 and output n0 + wn0 + 16j + 4*(lane/16) +
+  // e, so a lane's four values are consecutive outputs of one token.
+  const auto step = [&](int buf, const bf16x8 (&bf)[2][kJ]) {
+    // Token group i's two fragments, issued kAhead groups before its MFMAs.
+    const auto frag = [&](bf16x8* a, int i) {
 #pragma unroll
-    for (int s = 0; s < 2; ++s)
+      for (int s = 0; s < 2; ++s)
+        a[s] = *reinterpret_cast<const bf16x8*>(
+            &xs[buf][(wm0 + 16 * i + arow) * kLdsRow + 32 * (q >> 1) + 16 * (q & 1) + 8 * s]);
+    };
+    constexpr int kAhead = 3;  // token groups read ahead of their MFMAs
+    bf16x8 a[kAhead + 1][2];
 #pragma unroll
-      for (int i = 0; i < 8; ++i)
-        a[s][i] = *reinterpret_cast<const bf16x8*>(&xs[buf][(16 * i + arow) * kLdsRow + 32 * s + 8 * q]);
+    for (int i = 0; i < kAhead; ++i) frag(a[i], i);
 #pragma unroll
-    for (int s = 0; s < 2; ++s)
+    for (int i = 0; i < kI; ++i) {
+      if (i + kAhead < kI) frag(a[(i + kAhead) % (kAhead + 1)], i + kAhead);
 #pragma unroll
-      for (int i = 0; i < 8; ++i)
+      for (int s = 0; s < 2; ++s)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bf[s][j], a[s][i], acc[i][j], 0, 0, 0);
+        for (int j = 0; j < kJ; ++j)
+          acc[i][j] =
+              __builtin_amdgcn_mfma_f32_16x16x32_bf16(bf[s][j], a[i % (kAhead + 1)][s], acc[i][j], 0, 0, 0);
+    }
   };
 
+  // The K loop runs whole pairs of steps with no conditions inside: a store
+  // or load meant for a step past the last writes an LDS buffer no later
+  // step reads, or re-reads the last step (clamped).  With one exit, the
+  // loads in flight at the loop head are the same on every entry, so each
+  // use waits only for its own loads, not for the ones issued after them.
   WStage<TYPE> WA, WB;
-  bf16x8 BA[2][2], BB[2][2];
+  bf16x8 BA[2][kJ], BB[2][kJ];
+  // Each half of the loop dequantizes the next step's weights, runs the
+  // current step and stages the next step's activations (all three from
+  // loads issued two halves earlier), and only then issues its own loads,
+  // two steps ahead.  The scheduling fences keep the loads at the end of the
+  // half: then every use waits only for loads at least one half old, never
+  // for the ones just issued.
+  const auto fence = [] { __builtin_amdgcn_sched_barrier(0); };
   if constexpr (F32X) {
-    // Activations one step ahead in X; weights as below.
-    f32x4 X[2][2];
-    xloadf(X, 0);
+    // Rings: activations of step k in XA (even k) / XB (odd) as loaded
+    // (fp32), raw weights in WA / WB likewise, dequantized weights of step k
+    // in BA / BB.
+    f32x4 XA[kXPer][2], XB[kXPer][2];
+    xloadf(XA, 0);
+    xloadf(XB, 1);
     wload(WA, 0);
     wload(WB, 1);
-    xstoref(X, 0);
-    xloadf(X, 1);
+    xstoref(XA, 0);
+    xloadf(XA, 2);
     dequant(WA, BA);
     wload(WA, 2);
     __syncthreads();  // step 0's activations staged
-    for (int k = 0; k < nk; k += 2) {
-      if (k + 1 < nk) xstoref(X, 1);
-      xloadf(X, k + 2);
+    int k = 0;
+    for (; k + 2 <= nk; k += 2) {
       dequant(WB, BB);
-      wload(WB, k + 3);
       step(0, BA);
+      xstoref(XB, 1);
+      fence();
+      wload(WB, k + 3);
+      xloadf(XB, k + 3);
+      fence();
       __syncthreads();
-      if (k + 1 >= nk) break;
-      if (k + 2 < nk) xstoref(X, 0);
-      xloadf(X, k + 3);
       dequant(WA, BA);
-      wload(WA, k + 4);
       step(1, BB);
+      xstoref(XA, 0);
+      fence();
+      wload(WA, k + 4);
+      xloadf(XA, k + 4);
+      fence();
       __syncthreads();
     }
+    if (k < nk) step(0, BA);  // an odd step count's last step (staged in buffer 0)
   } else {
-  // Rings: activations of step k in XA (even k) / XB (odd), raw weights in
-  // WA / WB likewise, dequantized weights of step k in BA / BB.
-  XStage XA, XB;
-  xload(XA, 0);
-  xload(XB, 1);
-  wload(WA, 0);
-  wload(WB, 1);
-  xstore(XA, 0);
-  xload(XA, 2);
-  dequant(WA, BA);
-  wload(WA, 2);
-  __syncthreads();  // step 0's activations staged
-  for (int k = 0; k < nk; k += 2) {
-    if (k + 1 < nk) xstore(XB, 1);
-    xload(XB, k + 3);
-    dequant(WB, BB);
-    wload(WB, k + 3);
-    step(0, BA);
-    __syncthreads();
-    if (k + 1 >= nk) break;
-    if (k + 2 < nk) xstore(XA, 0);
-    xload(XA, k + 4);
+    XStage XA, XB;
+    xload(XA, 0);
+    xload(XB, 1);
+    wload(WA, 0);
+    wload(WB, 1);
+    xstore(XA, 0);
+    xload(XA, 2);
     dequant(WA, BA);
-    wload(WA, k + 4);
-    step(1, BB);
-    __syncthreads();
-  }
+    wload(WA, 2);
+    __syncthreads();  // step 0's activations staged
+    int k = 0;
+    for (; k + 2 <= nk; k += 2) {
+      dequant(WB, BB);
+      step(0, BA);
+      xstore(XB, 1);
+      fence();
+      wload(WB, k + 3);
+      xload(XB, k + 3);
+      fence();
+      __syncthreads();
+      dequant(WA, BA);
+      step(1, BB);
+      xstore(XA, 0);
+      fence();
+      wload(WA, k + 4);
+      xload(XA, k + 4);
+      fence();
+      __syncthreads();
+    }
+    if (k < nk) step(0, BA);  // an odd step count's last step (staged in buffer 0)
   }
 
   // Rows of y / part are 16-byte aligned when N is a multiple of 4: a lane's
   // four outputs then go out as one 16-byte store (the only case in which
   // n < N implies n + 3 < N, since n is a multiple of 4).
   const bool vec = (N & 3) == 0;
-  const int mrow = m0 + arow, ncol = n0 + wn0 + 4 * q;
+  const int mrow = m0 + wm0 + arow, ncol = n0 + wn0 + 4 * q;
   const auto store4 = [&](GMEM float* dst, const f32x4& v, int n) {
     if (vec) {
       *(GMEM f32x4*)dst = v;
@@ -388,11 +429,11 @@ __global__ void __launch_bounds__(kGemmThreads) qgemm_mfma(const GemmProblem* __
     // A K chunk: the partial tile as it is (gemm_reduce adds the rest).
     GMEM float* part = (GMEM float*)(p.part + static_cast<std::size_t>(kc) * M * N);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < kI; ++i) {
       const int m = mrow + 16 * i;
       if (m >= M) continue;
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
+      for (int j = 0; j < kJ; ++j) {
         const int n = ncol + 16 * j;
         if (n < N) store4(part + static_cast<std::size_t>(m) * N + n, acc[i][j], n);
       }
@@ -401,9 +442,9 @@ __global__ void __launch_bounds__(kGemmThreads) qgemm_mfma(const GemmProblem* __
   }
   GMEM float* y = (GMEM float*)p.y;
   const GMEM float* bias = (const GMEM float*)p.bias;
-  f32x4 add[2];
+  f32x4 add[kJ];
 #pragma unroll
-  for (int j = 0; j < 2; ++j)
+  for (int j = 0; j < kJ; ++j)
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int n = ncol + 16 * j + e;
@@ -412,13 +453,13 @@ __global__ void __launch_bounds__(kGemmThreads) qgemm_mfma(const GemmProblem* __
   // With accumulate, a token row's old vectors are loaded (clamped to a row
   // and column inside y) before any is used, so their latencies overlap.
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
+  for (int i = 0; i < kI; ++i) {
     const int m = mrow + 16 * i;
-    f32x4 old[2];
+    f32x4 old[kJ];
     if (p.accumulate) {
       const std::size_t row = static_cast<std::size_t>(min(m, M - 1)) * N;
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
+      for (int j = 0; j < kJ; ++j) {
         const int n = ncol + 16 * j;
         if (vec) {
           old[j] = *(const GMEM f32x4*)(y + row + min(n, N - 4));
@@ -430,7 +471,7 @@ __global__ void __launch_bounds__(kGemmThreads) qgemm_mfma(const GemmProblem* __
     }
     if (m >= M) continue;
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+    for (int j = 0; j < kJ; ++j) {
       const int n = ncol + 16 * j;
       if (n >= N) continue;
       const f32x4 v = acc[i][j] + add[j];
