@@ -455,7 +455,8 @@ def decode_runs(max_steps: int | None = None, greedy_only: bool = False):
               f"{res[key]['ids_match_reference']}", file=sys.stderr, flush=True)
         # The same greedy run with the tolerance-mode decode step
         # (llmi_hip_model_set_decode_mode): position-chunked attention merged
-        # in o_proj; logits within the fp32 tolerance, not bit-identical.
+        # in o_proj, the products split over K with atomic adds; logits
+        # within the fp32 tolerance, not bit-identical.
         m.set_decode_mode(H.DECODE_TOLERANCE)
         m.generate_greedy(prompt, 4)
         ids_t = m.generate_greedy(prompt, rec["n_steps"])
@@ -467,8 +468,10 @@ def decode_runs(max_steps: int | None = None, greedy_only: bool = False):
             decode_tok_s=round(tok_t, 1), frac_of_roofline=round(tok_t / roof, 4),
             ids_match_first64=bool(np.array_equal(ids_t[:64], want[:64])),
             ids_match_reference=bool(np.array_equal(ids_t, want)),
-            what="attention split over position chunks (softmax per chunk, merged in the o_proj launch); the "
-                 "quantized matmuls exact; logits within 1e-4 * max|logit| of the exact step (tests)")
+            what="attention split over position chunks (softmax per chunk, merged in the o_proj launch); each "
+                 "matmul split over K into ~1k one-wavefront workgroups whose partial sums (the exact block "
+                 "chains within a split) meet by atomic adds; logits within 1e-4 * max|logit| of the exact step "
+                 "(tests)")
         print(f"[bench] {key}: tolerance-mode decode {tok_t:.1f} tok/s, first 64 ids match "
               f"{res[key]['tolerance_mode']['ids_match_first64']}", file=sys.stderr, flush=True)
         if not greedy_only:

@@ -285,6 +285,31 @@ int launch_matmul_shared(const DeviceMatrix* const* ms, const float* const* bias
 // launched and the caller takes the unfused path).
 int launch_gate_up_silu(const DeviceMatrix& gate, const DeviceMatrix& up, const float* x, std::size_t rows,
                         float* y, hipStream_t s, bool* fused);
+// The tolerance-mode one-token step's products (gemv.hip): y += W x' split
+// over K into about kSplitTarget workgroups of one wavefront, each adding
+// its partial sums to y with atomic adds (so y must hold the residual, or
+// zeros, beforehand; the bias is added by the first split).  x' is x under
+// `prologue`: kRmsNorm (pw = the norm weight), kSiluUp (pw = up) or
+// kAttnCombine (pw = x = the attention partials, comb_hd = head_dim).  zero
+// (may be null): nzero floats the launch clears besides, for a product
+// later in the step that accumulates into them.  Within a split the sums
+// are the exact kernels'; the splits land in no fixed order, so results are
+// within the fp32-accumulate tolerance and not reproducible bit for bit.
+struct SplitProduct {
+  const DeviceMatrix* m = nullptr;
+  const float* x = nullptr;
+  const float* pw = nullptr;
+  const float* bias = nullptr;
+  float* y = nullptr;
+  int prologue = kPlain;
+  float eps = 0.0f;
+  int comb_hd = 0;
+  float* zero = nullptr;
+  int nzero = 0;
+  int bps = 0, splits = 0;  // set by plan_split: blocks per split, splits per 64-row tile
+};
+int plan_split(SplitProduct* p);
+int launch_split(const SplitProduct& p, hipStream_t s, int comb_nch = 0);
 // Frees the sampling workspace (llmi_hip_shutdown; the stream is idle).
 void release_sampling_workspace();
 // Frees the tolerance-mode product's split activations (likewise).

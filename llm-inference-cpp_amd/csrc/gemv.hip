@@ -760,6 +760,139 @@ __global__ void __launch_bounds__(COMBINE ? kCombineMaxThreads : 1024)
                              comb_nch);
 }
 
+// The tolerance-mode one-token product split over K (SplitProduct):
+// workgroup (tile, split), one wavefront, computes rows tile * 64 + lane over
+// blocks [split * BPS, ...): the weights of all its blocks are loaded first,
+// the activations of its range staged in LDS under the prologue meanwhile,
+// the block sums and the chain over its blocks are the exact kernels', and
+// the partial sums go to y by atomic adds.
+constexpr int kSplitMaxHeads = 8;  // kAttnCombine: whole heads per split (16 blocks of head_dim 64)
+template <int TYPE, int PRO, int BPS>
+__global__ void __launch_bounds__(64) tsplit_gemv(const uint4* __restrict__ codes, const float* __restrict__ scales,
+                                                  const float* __restrict__ x, const float* __restrict__ pw, int nblk,
+                                                  int in, float eps, int out, const float* __restrict__ bias,
+                                                  float* __restrict__ y, float* __restrict__ zero, int nzero,
+                                                  int comb_hd, int comb_nch) {
+  __shared__ __attribute__((aligned(16))) float xs[BPS * kBlock];
+  __shared__ float wgt[PRO == kAttnCombine ? kSplitMaxHeads * kAttnMaxChunks : 1];
+  const int lane = threadIdx.x;
+  const int tile = blockIdx.x;
+  const int b0 = blockIdx.y * BPS;
+  const int nb = min(BPS, nblk - b0);
+  const GMEM uint4* cg = gmem(codes);
+  const GMEM float* sg = gmem(scales);
+  Block<TYPE> blk[BPS];
+  float sc[BPS];
+#pragma unroll
+  for (int j = 0; j < BPS; ++j) {
+    // Past the range: the range's last block again (unused).
+    const std::size_t slot = static_cast<std::size_t>(tile) * nblk + static_cast<std::size_t>(b0 + min(j, nb - 1));
+    blk[j] = load_block<TYPE, true>(cg, slot, lane);
+    sc[j] = loadf<true>(sg + slot * kTileRows + lane);
+  }
+  if (zero != nullptr) {
+    const int wg = static_cast<int>(blockIdx.y * gridDim.x + blockIdx.x);
+    const int stride = static_cast<int>(gridDim.x * gridDim.y) * 64;
+    for (int i = wg * 64 + lane; i < nzero; i += stride) zero[i] = 0.0f;
+  }
+  // x' over the range [k0, k0 + n): each lane's elements (and, for
+  // RMSNorm, its share of the whole row's squares) are loaded in batches
+  // before any is used, so the staging costs one memory round trip per
+  // batch rather than one per element.
+  constexpr int kPer = (BPS * kBlock + 63) / 64;  // range elements per lane
+  const int k0 = b0 * kBlock, n = min(nb * kBlock, in - k0);
+  const GMEM float* xg = gmem(x);
+  const GMEM float* pg = gmem(pw);
+  if constexpr (PRO == kRmsNorm || PRO == kSiluUp || PRO == kPlain) {
+    float xv[kPer], pv[kPer];
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+      const int i = u * 64 + lane;
+      xv[u] = i < n ? xg[k0 + i] : 0.0f;
+      if constexpr (PRO != kPlain) pv[u] = i < n ? pg[k0 + i] : 0.0f;
+    }
+    if constexpr (PRO == kRmsNorm) {
+      constexpr int kBatch = 16;
+      float ss = 0.0f;
+      for (int i0 = 0; i0 < in; i0 += 64 * kBatch) {
+        float v[kBatch];
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) {
+          const int i = i0 + u * 64 + lane;
+          v[u] = i < in ? xg[i] : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) ss = __builtin_fmaf(v[u], v[u], ss);
+      }
+      ss = wave_sum_dpp(ss);
+      const float scale = 1.0f / __builtin_sqrtf(ss / static_cast<float>(in) + eps);
+#pragma unroll
+      for (int u = 0; u < kPer; ++u) xv[u] = pv[u] * (xv[u] * scale);
+    } else if constexpr (PRO == kSiluUp) {
+#pragma unroll
+      for (int u = 0; u < kPer; ++u) xv[u] = xv[u] / (1.0f + __expf(-xv[u])) * pv[u];
+    }
+#pragma unroll
+    for (int u = 0; u < kPer; ++u)
+      if (u * 64 + lane < n) xs[u * 64 + lane] = xv[u];
+  } else {
+    // kAttnCombine: the range is whole heads h0 .. h0 + nhh - 1; lanes 16r ..
+    // 16r + 15 form the chunk weights of head hb + r.
+    const int hd = comb_hd, nh_all = in / hd, h0 = k0 / hd, nhh = n / hd;
+    const GMEM float* ms = xg + static_cast<std::size_t>(kAttnMaxChunks) * nh_all * hd;
+    const GMEM float* ls = ms + kAttnMaxChunks * nh_all;
+    float ov[kPer][kAttnMaxChunks];
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+      const int i = u * 64 + lane;
+      const int hh = i / hd, d = i - hh * hd;
+      const GMEM float* oh = xg + static_cast<std::size_t>(h0 + min(hh, nhh - 1)) * kAttnMaxChunks * hd + d;
+#pragma unroll
+      for (int c = 0; c < kAttnMaxChunks; ++c) ov[u][c] = i < n && c < comb_nch ? oh[c * hd] : 0.0f;
+    }
+    for (int hb = 0; hb < nhh; hb += 4) {
+      const int hh = hb + (lane >> 4), c = lane & 15;
+      const bool live = hh < nhh && c < comb_nch;
+      const int t = (h0 + hh) * kAttnMaxChunks + c;
+      const float mv = live ? ms[t] : -__builtin_inff();
+      const float lv = live ? ls[t] : 0.0f;
+      const float mx = row_last_bcast(row_max16_f32(mv), lane);
+      const float w = live ? __expf(mv - mx) : 0.0f;
+      const float den = row_last_bcast(row_sum16_f32(w * lv), lane);
+      if (hh < nhh) wgt[hh * kAttnMaxChunks + c] = live ? w / den : 0.0f;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+      const int i = u * 64 + lane;
+      if (i < n) {
+        const float* wh = wgt + (i / hd) * kAttnMaxChunks;
+        float acc_c = 0.0f;
+#pragma unroll
+        for (int c = 0; c < kAttnMaxChunks; ++c) acc_c = __builtin_fmaf(wh[c], ov[u][c], acc_c);
+        xs[i] = acc_c;
+      }
+    }
+  }
+  __syncthreads();
+  const Q4Magic k = q4_magic();
+  const int nfull = in / kBlock - b0;  // whole blocks of the range
+  float acc = 0.0f;
+#pragma unroll
+  for (int j = 0; j < BPS; ++j) {
+    if (j < nb) {
+      const float part = j < nfull ? full_block_dot<TYPE>(blk[j], xs + j * kBlock, k)
+                                   : tail_block_dot<TYPE>(blk[j], xs + j * kBlock, in - (b0 + j) * kBlock);
+      acc = __builtin_fmaf(part, sc[j], acc);
+    }
+  }
+  const int row = tile * kTileRows + lane;
+  if (row < out) {
+    if (blockIdx.y == 0 && bias != nullptr) acc += bias[row];
+    unsafeAtomicAdd(y + row, acc);
+  }
+}
+
 // ------------------------------------------------------------ batch > 8
 // The exact multi-row product on many tiles: one workgroup per MR = 64
 // input rows x one 64-row tile of the matrix (64 outputs).  Per quantization
@@ -1672,6 +1805,78 @@ int DeviceGroup::launch(hipStream_t s, int chunks) const {
     }
     if (int rc = launch_group(probs, map, l, s)) return rc;
   }
+  return LLMI_OK;
+}
+
+// Splits of a SplitProduct: about kSplitTarget workgroups, BPS (the
+// kernel's blocks per split) one of 2, 4, 8, 16.
+constexpr int kSplitTarget = 1024;
+
+int plan_split(SplitProduct* p) {
+  LLMI_REQUIRE(p->m != nullptr && p->x != nullptr && p->y != nullptr, "split product: null operand");
+  const DeviceMatrix& m = *p->m;
+  LLMI_REQUIRE(m.type == LLMI_TYPE_Q8_0 || m.type == LLMI_TYPE_Q4_0, "split product: Q8_0 or Q4_0 weights only");
+  LLMI_REQUIRE(p->prologue == kRmsNorm || p->prologue == kSiluUp || p->prologue == kAttnCombine ||
+                   p->prologue == kPlain,
+               "split product: unknown prologue");
+  LLMI_REQUIRE(p->prologue == kPlain || p->pw != nullptr, "split product: null prologue operand");
+  const int nblk = static_cast<int>(m.nblk), ntiles = static_cast<int>(m.ntiles);
+  LLMI_REQUIRE(nblk >= 1 && ntiles >= 1, "split product: empty matrix");
+  const int want = std::max(1, kSplitTarget / ntiles);
+  int bps = static_cast<int>(ceil_div(static_cast<std::size_t>(nblk), static_cast<std::size_t>(want)));
+  int unit = 1;
+  if (p->prologue == kAttnCombine) {
+    LLMI_REQUIRE(p->comb_hd >= 32 && p->comb_hd % kBlock == 0 && m.in % static_cast<std::size_t>(p->comb_hd) == 0,
+                 "split product: an attention-combine product needs in = heads * head_dim, head_dim % 32 == 0");
+    unit = p->comb_hd / kBlock;
+  }
+  int pick = 2;
+  while (pick < 16 && (2 * pick <= bps || pick % unit != 0)) pick *= 2;
+  LLMI_REQUIRE(pick % unit == 0 && (p->prologue != kAttnCombine || pick * kBlock / p->comb_hd <= kSplitMaxHeads),
+               "split product: head_dim too large for a split");
+  p->bps = pick;
+  p->splits = static_cast<int>(ceil_div(static_cast<std::size_t>(nblk), static_cast<std::size_t>(pick)));
+  return LLMI_OK;
+}
+
+namespace {
+
+template <int TYPE, int PRO>
+void launch_split_bps(const SplitProduct& p, hipStream_t s, int comb_nch) {
+  const DeviceMatrix& m = *p.m;
+  const dim3 grid(static_cast<unsigned>(m.ntiles), static_cast<unsigned>(p.splits));
+#define LLMI_SPLIT_ARGS                                                                                            \
+  reinterpret_cast<const uint4*>(m.codes), m.scales, p.x, p.pw, static_cast<int>(m.nblk), static_cast<int>(m.in), \
+      p.eps, static_cast<int>(m.out), p.bias, p.y, p.zero, p.nzero, p.comb_hd, comb_nch
+  switch (p.bps) {
+    case 2: tsplit_gemv<TYPE, PRO, 2><<<grid, 64, 0, s>>>(LLMI_SPLIT_ARGS); break;
+    case 4: tsplit_gemv<TYPE, PRO, 4><<<grid, 64, 0, s>>>(LLMI_SPLIT_ARGS); break;
+    case 8: tsplit_gemv<TYPE, PRO, 8><<<grid, 64, 0, s>>>(LLMI_SPLIT_ARGS); break;
+    default: tsplit_gemv<TYPE, PRO, 16><<<grid, 64, 0, s>>>(LLMI_SPLIT_ARGS); break;
+  }
+#undef LLMI_SPLIT_ARGS
+}
+
+template <int TYPE>
+void launch_split_type(const SplitProduct& p, hipStream_t s, int comb_nch) {
+  switch (p.prologue) {
+    case kRmsNorm: launch_split_bps<TYPE, kRmsNorm>(p, s, comb_nch); break;
+    case kSiluUp: launch_split_bps<TYPE, kSiluUp>(p, s, comb_nch); break;
+    case kAttnCombine: launch_split_bps<TYPE, kAttnCombine>(p, s, comb_nch); break;
+    default: launch_split_bps<TYPE, kPlain>(p, s, comb_nch); break;
+  }
+}
+
+}  // namespace
+
+int launch_split(const SplitProduct& p, hipStream_t s, int comb_nch) {
+  LLMI_REQUIRE(p.m != nullptr && p.splits >= 1 && (p.bps == 2 || p.bps == 4 || p.bps == 8 || p.bps == 16),
+               "split product: not planned");
+  LLMI_REQUIRE(p.prologue != kAttnCombine || (comb_nch >= 1 && comb_nch <= kAttnMaxChunks),
+               "split product: attention chunks out of range");
+  if (p.m->type == LLMI_TYPE_Q8_0) launch_split_type<LLMI_TYPE_Q8_0>(p, s, comb_nch);
+  else launch_split_type<LLMI_TYPE_Q4_0>(p, s, comb_nch);
+  LLMI_TRY_HIP(hipGetLastError());
   return LLMI_OK;
 }
 

@@ -1285,6 +1285,11 @@ __global__ void __launch_bounds__(kThreads) softmax_rows(float* __restrict__ x, 
   for (int s = threadIdx.x; s < n; s += kThreads) row[s] = sc[s];
 }
 
+__global__ void __launch_bounds__(kThreads) zero_floats(float* __restrict__ x, int n) {
+  const int i = static_cast<int>(blockIdx.x * blockDim.x + threadIdx.x);
+  if (i < n) x[i] = 0.0f;
+}
+
 __global__ void __launch_bounds__(kThreads) silu_inplace(float* __restrict__ x, std::size_t n) {
   const std::size_t i = static_cast<std::size_t>(blockIdx.x) * kThreads + threadIdx.x;
   if (i < n) x[i] = x[i] / (1.0f + exact::expf(-x[i]));
@@ -1307,6 +1312,10 @@ struct DeviceLayer {
   // tolerance-mode step's o_proj, which stages the attention output from
   // the chunk partials (kAttnCombine).
   DeviceGroup qkv, gate_up, down_silu, o_comb;
+  // The tolerance-mode step's products split over K (with fused q|k|v and
+  // gate|up weights): q|k|v (clearing g|u), o_proj (clearing q|k|v for the
+  // next layer), gate|up, down_proj.
+  SplitProduct s_qkv, s_o, s_gu, s_dn;
 };
 
 // Fixed one-token buffers of the fused decode step.
@@ -1359,6 +1368,7 @@ struct llmi_hip_model {
   double last_prefill_ms = 0.0, last_decode_ms = 0.0;  // of the last greedy run
   int decode_mode = LLMI_DECODE_EXACT;  // llmi_hip_model_set_decode_mode
   bool tol_ready = false;               // build_decode made the tolerance-mode step
+  bool split_ready = false;             // ... with its products split over K (SplitProduct)
   std::size_t last_redraws = 0;  // generate_sampled: queued draws redrawn step by step
 };
 
@@ -1539,6 +1549,25 @@ int build_decode(llmi_hip_model* m) {
     }
   }
   m->tol_ready = tol;
+  // The split products need the fused weights and a head_dim that splits
+  // into whole blocks.
+  bool split = tol && m->hd % kBlock == 0;
+  for (const DeviceLayer& l : m->layers) split = split && l.wqkv.out != 0 && l.gate_up_w.out != 0;
+  for (DeviceLayer& l : m->layers) {
+    if (!split) break;
+    l.s_qkv = SplitProduct{&l.wqkv, d.x, l.attn_norm, l.bqkv, d.q, kRmsNorm, eps};
+    l.s_qkv.zero = d.g;
+    l.s_qkv.nzero = static_cast<int>(2 * m->F);
+    l.s_o = SplitProduct{&l.wo, d.part, d.part, nullptr, d.x, kAttnCombine};
+    l.s_o.comb_hd = static_cast<int>(m->hd);
+    l.s_o.zero = d.q;
+    l.s_o.nzero = static_cast<int>(m->Q + 2 * m->KV);
+    l.s_gu = SplitProduct{&l.gate_up_w, d.x, l.mlp_norm, nullptr, d.g, kRmsNorm, eps};
+    l.s_dn = SplitProduct{&l.down, d.g, d.u, nullptr, d.x, kSiluUp};
+    for (SplitProduct* sp : {&l.s_qkv, &l.s_o, &l.s_gu, &l.s_dn})
+      if (int rc = plan_split(sp)) return rc;
+  }
+  m->split_ready = split;
   return LLMI_OK;
 }
 
@@ -1742,6 +1771,19 @@ int decode_step(llmi_hip_model* m, llmi_hip_cache* cache, hipStream_t s, bool to
   if (int rc = launch_dequantize_rows(m->embed, w.ids, 1, d.x, s)) return rc;
   for (std::size_t li = 0; li < m->layers.size(); ++li) {
     const DeviceLayer& l = m->layers[li];
+    if (tolerance && m->split_ready) {
+      // q|k|v start at zero: cleared by the previous layer's o_proj launch,
+      // or here before the first layer.
+      if (li == 0) zero_floats<<<blocks_for(m->Q + 2 * m->KV), kThreads, 0, s>>>(d.q, static_cast<int>(m->Q + 2 * m->KV));
+      if (int rc = launch_split(l.s_qkv, s)) return rc;
+      const int nch = launch_tol_attention(d.q, d.k, d.v, cache->k + li * per_layer, cache->v + li * per_layer,
+                                           m->cos_t, m->sin_t, d.part, nh, nkv, hd, static_cast<int>(cache->cap),
+                                           static_cast<int>(pos + 1), scale, s);
+      if (int rc = launch_split(l.s_o, s, nch)) return rc;
+      if (int rc = launch_split(l.s_gu, s)) return rc;
+      if (int rc = launch_split(l.s_dn, s)) return rc;
+      continue;
+    }
     if (int rc = l.qkv.launch(s)) return rc;
     if (tolerance) {
       const int nch = launch_tol_attention(d.q, d.k, d.v, cache->k + li * per_layer, cache->v + li * per_layer,
