@@ -1208,8 +1208,21 @@ __global__ void __launch_bounds__(kThreads) argmax_many(const float* __restrict_
   const int per = (n + gridDim.x - 1) / gridDim.x;
   const int lo = blockIdx.x * per;
   const int hi = min(n, lo + per);
+  // Each thread's elements in increasing order, kBatch loads issued before
+  // the first comparison (one memory round trip per batch).
+  constexpr int kBatch = 8;
   Best b{-__builtin_inff(), -1};
-  for (int i = lo + threadIdx.x; i < hi; i += kThreads) b = better(b, Best{x[i], i});
+  for (int i0 = lo + threadIdx.x; i0 < hi; i0 += kBatch * kThreads) {
+    float v[kBatch];
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      const int i = i0 + u * kThreads;
+      v[u] = i < hi ? x[i] : 0.0f;
+    }
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u)
+      if (i0 + u * kThreads < hi) b = better(b, Best{v[u], i0 + u * kThreads});
+  }
   b = block_best<kThreads>(b, bv, bi);
   if (threadIdx.x == 0) {
     part_v[blockIdx.x] = b.v;
@@ -1369,6 +1382,7 @@ struct llmi_hip_model {
   int decode_mode = LLMI_DECODE_EXACT;  // llmi_hip_model_set_decode_mode
   bool tol_ready = false;               // build_decode made the tolerance-mode step
   bool split_ready = false;             // ... with its products split over K (SplitProduct)
+  bool qkv_clear = false;               // the last queued step left dec.q|k|v at zero (split step)
   std::size_t last_redraws = 0;  // generate_sampled: queued draws redrawn step by step
 };
 
@@ -1769,12 +1783,16 @@ int decode_step(llmi_hip_model* m, llmi_hip_cache* cache, hipStream_t s, bool to
   const float scale = 1.0F / std::sqrt(static_cast<float>(m->hd));
   const std::size_t per_layer = static_cast<std::size_t>(c.num_kv_heads) * cache->cap * m->hd;
   if (int rc = launch_dequantize_rows(m->embed, w.ids, 1, d.x, s)) return rc;
+  const bool split = tolerance && m->split_ready;
+  // q|k|v start at zero in a split step: cleared by the previous layer's
+  // o_proj launch (the previous split step's last layer for the first), or
+  // here when the step before was not a split step.
+  if (split && !m->qkv_clear)
+    zero_floats<<<blocks_for(m->Q + 2 * m->KV), kThreads, 0, s>>>(d.q, static_cast<int>(m->Q + 2 * m->KV));
+  m->qkv_clear = false;
   for (std::size_t li = 0; li < m->layers.size(); ++li) {
     const DeviceLayer& l = m->layers[li];
-    if (tolerance && m->split_ready) {
-      // q|k|v start at zero: cleared by the previous layer's o_proj launch,
-      // or here before the first layer.
-      if (li == 0) zero_floats<<<blocks_for(m->Q + 2 * m->KV), kThreads, 0, s>>>(d.q, static_cast<int>(m->Q + 2 * m->KV));
+    if (split) {
       if (int rc = launch_split(l.s_qkv, s)) return rc;
       const int nch = launch_tol_attention(d.q, d.k, d.v, cache->k + li * per_layer, cache->v + li * per_layer,
                                            m->cos_t, m->sin_t, d.part, nh, nkv, hd, static_cast<int>(cache->cap),
@@ -1803,6 +1821,7 @@ int decode_step(llmi_hip_model* m, llmi_hip_cache* cache, hipStream_t s, bool to
   const DeviceMatrix& head = m->tied ? m->embed : m->lm_head;
   if (int rc = launch_matmul(head, d.h, 1, nullptr, w.logits, s)) return rc;
   LLMI_TRY_HIP(hipGetLastError());
+  m->qkv_clear = split;
   cache->len = pos + 1;
   return LLMI_OK;
 }
