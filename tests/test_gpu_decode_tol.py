@@ -1,5 +1,6 @@
 """The tolerance-mode decode step (llmi_hip_model_set_decode_mode): attention
-split over position chunks, merged in the o_proj launch's staging.  Its
+split over position chunks, merged in the o_proj launch's staging, and the
+matmuls split over K (partial sums added atomically).  Its
 logits are held to the path's floating-point contract against the exact
 step, whose logits equal the reference's bit for bit (tests/test_gpu_model.py
 pins them at the full-size models' recorded steps):
@@ -8,7 +9,8 @@ pins them at the full-size models' recorded steps):
   (the relative-error bar the north star states for fp32-accumulate paths),
   fed the same tokens, on small models with head sizes 64 and 128, GQA groups
   1, 3 and 7, and contexts from 1 to past 2048 positions (one chunk of 64 up
-  to sixteen chunks of 192);
+  to sixteen chunks of 192), and on one-layer models with MLPs of 8192 and
+  16384 (every split width of the matmuls);
 * on the synthetic SmolLM2-135M and Qwen2.5-0.5B:
   the greedy ids of the first 64 steps equal the compiled reference's, and
   every step's logits, fed the reference's ids, are within the bar.
@@ -71,6 +73,30 @@ def test_tolerance_steps_match_exact_steps(hidden, heads, kv, qt):
         ct.free()
     m.free()
     print(f"hidden {hidden} heads {heads}/{kv}: worst relative logit error {worst:.3e}")
+
+
+@pytest.mark.parametrize("inter,qt", [(8192, H.Q4_0), (16384, H.Q8_0)])
+def test_wide_mlp_splits_match_exact_steps(inter, qt):
+    """Matrices whose K splits take the wider per-workgroup block counts (8
+    and 16 blocks: gate|up over 256 / 512 row tiles, down_proj over 256 / 512
+    blocks), one layer, both modes fed the same tokens."""
+    cfg = cfg_of(1024, 16, 4, layers=1)
+    cfg["intermediate_size"] = inter
+    m = H.synthetic_model_dev(cfg, 900 + inter % 7, qt, "bench")
+    ce, ct = m.new_cache(40), m.new_cache(40)
+    worst = 0.0
+    for tok in synth.uniform_ids(inter, 32, cfg["vocab_size"]):
+        m.set_decode_mode(H.DECODE_EXACT)
+        le = m.forward_cached(ce, [tok])
+        m.set_decode_mode(H.DECODE_TOLERANCE)
+        lt = m.forward_cached(ct, [tok])
+        err = rel_err(lt, le)
+        assert err <= TOL, err
+        worst = max(worst, err)
+    ce.free()
+    ct.free()
+    m.free()
+    print(f"intermediate {inter}: worst relative logit error {worst:.3e}")
 
 
 def test_tolerance_mode_is_rejected_when_unknown():
