@@ -421,13 +421,15 @@ int llmi_hip_model_last_redraws(const llmi_hip_model* model, size_t* steps);
  * one token, generate_greedy / generate_sampled after the prompt).
  * LLMI_DECODE_EXACT (the default): the reference's operations in its order,
  * logits bit-identical to transformer.cpp:192-306.  LLMI_DECODE_TOLERANCE:
- * the same quantized matmuls (still exact), but attention split over
- * position chunks (at most 16 per head), each chunk's softmax taken against
- * its own maximum with the hardware exponential, and the chunks merged in
- * the o_proj launch's staging -- one launch per layer fewer; logits within
- * the path's floating-point tolerance of the exact ones, not bit-identical.
- * Applies to head_dim 64 / 128 with at most 16 query heads per KV head (other
- * models keep the exact step); the prompt's prefill is exact in both modes.
+ * attention split over position chunks (at most 16 per head), each chunk's
+ * softmax taken against its own maximum with the hardware exponential, the
+ * chunks merged in the o_proj product's staging, and every matmul split
+ * over K into one-wavefront workgroups whose partial sums meet by atomic
+ * adds; logits within the path's floating-point tolerance of the exact
+ * ones, neither bit-identical nor reproducible bit for bit.  Applies to
+ * head_dim 64 / 128 with at most 16 query heads per KV head and row counts
+ * of q, k, v, gate and up that are multiples of 64 (other models keep the
+ * exact step); the prompt's prefill is exact in both modes.
  * No counterpart in the reference (whose decode is exact by construction):
  * a speed option for callers that accept the tolerance. */
 enum { LLMI_DECODE_EXACT = 0, LLMI_DECODE_TOLERANCE = 1 };

@@ -72,9 +72,10 @@ struct DeviceMatrix {
 // (kernels.cpp:115-120) with pw = w; kSiluUp silu(x) * pw, the reference's
 // SiLU times up (transformer.cpp:290, kernels.cpp:148).  Either one is the
 // same arithmetic as the separate glue kernel it replaces.
-// kAttnCombine (tolerance-mode decode only): the attention output assembled
-// from per-chunk partial softmax states (attn_part_1): pw points to the
-// partials (layout at kAttnMaxChunks); GroupEntry::pa = head_dim.
+// kAttnCombine (the tolerance-mode decode's split products only, see
+// SplitProduct): the attention output assembled from per-chunk partial
+// softmax states (attn_part_1); pw points to the partials (layout at
+// kAttnMaxChunks).
 enum { kPlain = 0, kRmsNorm = 1, kSiluUp = 2, kAttnCombine = 3 };
 
 // Partial attention states of the tolerance-mode decode, per query head h
@@ -109,7 +110,6 @@ struct GroupEntry {
   int prologue = kPlain;
   const float* pw = nullptr;
   float eps = 0.0f;
-  int pa = 0;  // kAttnCombine: head_dim
 };
 // One kernel launch of a group: the products of weight type `type` and row
 // chunk `rchunk` (GroupProblem::kNarrow: the 16-row tiles), at
@@ -133,11 +133,8 @@ struct DeviceGroup {
   const std::uint32_t* map = nullptr;
   std::vector<GroupLaunch> launches;
   std::vector<GroupProblem> host_probs;  // the table's host copy (few-product launches pass them by value)
-  int comb_hd = 0;                       // head_dim of a kAttnCombine product (0: none)
   int build(const GroupEntry* entries, std::size_t count);
-  // chunks >= 0: the number of attention chunks for the kAttnCombine
-  // products (set per launch; such products run on the by-value path).
-  int launch(hipStream_t s, int chunks = -1) const;
+  int launch(hipStream_t s) const;
   void release();
 };
 

@@ -374,64 +374,6 @@ __device__ __forceinline__ void wide_tile(const GMEM uint4* __restrict__ codes, 
 // one memory round trip while in <= kStageBatch * blockDim.x.
 constexpr int kStageBatch = 8;
 
-// kAttnCombine staging (tolerance-mode decode): the attention output
-// x[h * hd + d] = sum_c w[h][c] o[h][c][d], w[h][c] = exp(m[h][c] - M_h) /
-// sum_c' exp(m[h][c'] - M_h) l[h][c'], M_h = max_c m[h][c], from the chunk
-// partials at pw (the layout at kAttnMaxChunks).  Each thread issues the o
-// loads of its (up to kCombinePer) elements first; the 16 lanes of a row
-// hold one head's 16 chunks and form its weights with row reductions, into
-// `wgt` (nh * 16 floats of LDS).  Ends with a barrier.
-constexpr int kCombinePer = 4;  // elements per thread per round
-
-__device__ __forceinline__ void stage_combine(const GMEM float* __restrict__ pw, int in, int hd, int nch, float* xs,
-                                              float* wgt) {
-  const int tid = threadIdx.x, nthreads = blockDim.x;
-  const int nh = in / hd;
-  const GMEM float* ms = pw + static_cast<std::size_t>(kAttnMaxChunks) * nh * hd;
-  const GMEM float* ls = ms + kAttnMaxChunks * nh;
-  const auto round = [&](int i0) {
-    float ov[kCombinePer][kAttnMaxChunks];
-#pragma unroll
-    for (int k = 0; k < kCombinePer; ++k) {
-      const int i = i0 + k * nthreads + tid;
-      const int h = i / hd, d = i - h * hd;
-      const GMEM float* oh = pw + static_cast<std::size_t>(h) * kAttnMaxChunks * hd + d;
-#pragma unroll
-      for (int c = 0; c < kAttnMaxChunks; ++c) ov[k][c] = i < in && c < nch ? oh[c * hd] : 0.0f;
-    }
-    if (i0 == 0) {
-      const int lane = tid & 63;
-      // Whole wavefronts take part (the DPP row reductions read every lane of a row).
-      for (int t = tid; t < ((nh * kAttnMaxChunks + 63) & ~63); t += nthreads) {
-        const int c = t % kAttnMaxChunks;
-        const bool live = t < nh * kAttnMaxChunks && c < nch;
-        const float m = live ? ms[t] : -__builtin_inff();
-        const float l = live ? ls[t] : 0.0f;
-        const float mx = row_last_bcast(row_max16_f32(m), lane);
-        const float w = live ? __expf(m - mx) : 0.0f;
-        const float den = row_last_bcast(row_sum16_f32(w * l), lane);
-        if (t < nh * kAttnMaxChunks) wgt[t] = w / den;
-      }
-      __syncthreads();
-    }
-#pragma unroll
-    for (int k = 0; k < kCombinePer; ++k) {
-      const int i = i0 + k * nthreads + tid;
-      if (i < in) {
-        const float* wh = wgt + (i / hd) * kAttnMaxChunks;
-        float a = 0.0f;
-#pragma unroll
-        for (int c = 0; c < kAttnMaxChunks; ++c) a = __builtin_fmaf(wh[c], ov[k][c], a);
-        xs[i] = a;
-      }
-    }
-  };
-  // The first round outside the loop (see stage_x).
-  round(0);
-  for (int i0 = kCombinePer * nthreads; i0 < in; i0 += kCombinePer * nthreads) round(i0);
-  __syncthreads();
-}
-
 __device__ __forceinline__ void stage_x(const GMEM float* __restrict__ x, int in, int prologue,
                                         const GMEM float* __restrict__ pw, float eps, float* xs) {
   __shared__ double red[64];
@@ -580,13 +522,12 @@ __device__ __forceinline__ float chain_pairs(const float* row, int nblk) {
 // in LDS and are read with broadcast loads (16 lanes per address); block
 // sums and scales go to LDS as pairs, and lanes 0-15 run the chains.  LDS:
 // x[in (padded to 4)], then 16 rows of pair_stride(nblk) floats.
-template <int TYPE, bool COMBINE = false>
+template <int TYPE>
 __device__ __forceinline__ void narrow_tile(const GMEM uint4* __restrict__ codes, const GMEM float* __restrict__ scales,
                                             const GMEM float* __restrict__ x, const GMEM float* __restrict__ bias,
                                             GMEM float* __restrict__ y, int in, int nblk, int out, int bpg, int accumulate,
                                             std::size_t tile16, float* lds, int prologue = kPlain,
-                                            const GMEM float* __restrict__ pw = nullptr, float eps = 0.0f,
-                                            int pa = 0, int pb = 0) {
+                                            const GMEM float* __restrict__ pw = nullptr, float eps = 0.0f) {
   constexpr int kHoist = 4;
   const Q4Magic k = q4_magic();
   float* xs = lds;
@@ -620,11 +561,7 @@ __device__ __forceinline__ void narrow_tile(const GMEM uint4* __restrict__ codes
     if (bias != nullptr) add = bias[row];
     if (accumulate) old = y[row];
   }
-  // The combine's head weights use the pairs region before the block sums
-  // do: nh * 16 floats, and a row of pairs alone holds pair_stride(nblk) >=
-  // 2 * nblk = nh * hd / 16 >= 4 * nh floats (hd >= 64).
-  if constexpr (COMBINE) stage_combine(pw, in, pa, pb, xs, pairs);
-  else stage_x(x, in, prologue, pw, eps, xs);
+  stage_x(x, in, prologue, pw, eps, xs);
   float2* mine = reinterpret_cast<float2*>(pairs + r * stride);
 #pragma unroll
   for (int j = 0; j < kHoist; ++j) {
@@ -720,26 +657,19 @@ constexpr int kFewProblems = 3;
 struct FewProblems {
   GroupProblem p[kFewProblems];
   int count;
-  int comb_hd, comb_nch;  // COMBINE: head_dim and the number of attention chunks
 };
-// COMBINE: the kAttnCombine staging (an instance of its own, so that its
-// registers do not weigh on the other prologues' launches).
-// kCombineMaxThreads: the COMBINE instance's workgroup limit, which leaves
-// it 256 VGPRs.
-constexpr int kCombineMaxThreads = 512;
-template <int TYPE, bool COMBINE = false>
-__global__ void __launch_bounds__(COMBINE ? kCombineMaxThreads : 1024) qgemv_few_narrow(FewProblems f) {
+template <int TYPE>
+__global__ void __launch_bounds__(1024) qgemv_few_narrow(FewProblems f) {
   extern __shared__ float4 lds4[];
   const int wg = blockIdx.x;
   // The product by comparisons (uniform), each field by selects, so the
   // argument block is never indexed dynamically.
   const int i = (f.count > 2 && wg >= f.p[2].first_wg) ? 2 : (f.count > 1 && wg >= f.p[1].first_wg) ? 1 : 0;
 #define LLMI_PICK(fld) (i == 2 ? f.p[2].fld : i == 1 ? f.p[1].fld : f.p[0].fld)
-  narrow_tile<TYPE, COMBINE>(gmem(reinterpret_cast<const uint4*>(LLMI_PICK(codes))), gmem(LLMI_PICK(scales)),
-                             gmem(LLMI_PICK(x)),
-                    gmem(LLMI_PICK(bias)), gmem_out(LLMI_PICK(y)), LLMI_PICK(in), LLMI_PICK(nblk), LLMI_PICK(out),
-                    LLMI_PICK(bpw), LLMI_PICK(accumulate), wg - LLMI_PICK(first_wg), reinterpret_cast<float*>(lds4),
-                    LLMI_PICK(prologue), gmem(LLMI_PICK(pw)), LLMI_PICK(eps), f.comb_hd, f.comb_nch);
+  narrow_tile<TYPE>(gmem(reinterpret_cast<const uint4*>(LLMI_PICK(codes))), gmem(LLMI_PICK(scales)),
+                    gmem(LLMI_PICK(x)), gmem(LLMI_PICK(bias)), gmem_out(LLMI_PICK(y)), LLMI_PICK(in), LLMI_PICK(nblk),
+                    LLMI_PICK(out), LLMI_PICK(bpw), LLMI_PICK(accumulate), wg - LLMI_PICK(first_wg),
+                    reinterpret_cast<float*>(lds4), LLMI_PICK(prologue), gmem(LLMI_PICK(pw)), LLMI_PICK(eps));
 #undef LLMI_PICK
 }
 
@@ -748,16 +678,14 @@ __global__ void __launch_bounds__(COMBINE ? kCombineMaxThreads : 1024) qgemv_few
 // the prologue operand) is among the first 14 dwords, which arrive
 // preloaded in SGPRs (-amdgpu-kernarg-preload-count); the one-token step's
 // launches of one product take it.
-template <int TYPE, bool COMBINE = false>
-__global__ void __launch_bounds__(COMBINE ? kCombineMaxThreads : 1024)
+template <int TYPE>
+__global__ void __launch_bounds__(1024)
     qgemv_one_narrow(const uint4* __restrict__ codes, const float* __restrict__ scales, const float* __restrict__ x,
                      const float* __restrict__ pw, int nblk, int bpw, int in, int prologue, float eps, int out,
-                     const float* __restrict__ bias, float* __restrict__ y, int accumulate, int comb_hd,
-                     int comb_nch) {
+                     const float* __restrict__ bias, float* __restrict__ y, int accumulate) {
   extern __shared__ float4 lds4[];
-  narrow_tile<TYPE, COMBINE>(gmem(codes), gmem(scales), gmem(x), gmem(bias), gmem_out(y), in, nblk, out, bpw,
-                             accumulate, blockIdx.x, reinterpret_cast<float*>(lds4), prologue, gmem(pw), eps, comb_hd,
-                             comb_nch);
+  narrow_tile<TYPE>(gmem(codes), gmem(scales), gmem(x), gmem(bias), gmem_out(y), in, nblk, out, bpw, accumulate,
+                    blockIdx.x, reinterpret_cast<float*>(lds4), prologue, gmem(pw), eps);
 }
 
 // The tolerance-mode one-token product split over K (SplitProduct):
@@ -1629,10 +1557,8 @@ int plan_group(const GroupEntry* entries, std::size_t count, GroupPlan* plan) {
           (e.prologue != kPlain ||
            (wide_total < kNarrowBelow && (m.nblk <= kNarrowMaxBlocks || wide_total < kLongRowsNarrowBelow)));
       LLMI_REQUIRE(e.prologue == kPlain || narrow, "group: a prologue needs batch 1 and in <= ~20k");
-      LLMI_REQUIRE(e.prologue != kAttnCombine || (e.pa >= 64 && m.in % static_cast<std::size_t>(e.pa) == 0 &&
-                                                  m.in / static_cast<std::size_t>(e.pa) <=
-                                                      static_cast<std::size_t>(pair_stride(static_cast<int>(m.nblk)))),
-                   "group: an attention-combine product needs in = heads * head_dim, head_dim >= 64");
+      LLMI_REQUIRE(e.prologue == kPlain || e.prologue == kRmsNorm || e.prologue == kSiluUp,
+                   "group: unknown prologue");
       int r = narrow ? int{GroupProblem::kNarrow} : pick_chunk(e.rows, m.nblk, kLdsTarget);
       if (r == 0) r = pick_chunk(1, m.nblk, max_lds_per_block());
       LLMI_REQUIRE(r != 0, "group: rows too long for the grouped GEMV (in above ~10k)");
@@ -1698,10 +1624,6 @@ int plan_group(const GroupEntry* entries, std::size_t count, GroupPlan* plan) {
       plan->wg_prob.insert(plan->wg_prob.end(), wgs, static_cast<std::uint32_t>(j));
     }
     LLMI_REQUIRE(l.lds <= max_lds_per_block(), "group: a product needs more LDS than one workgroup may use");
-    for (const GroupProblem& p : probs)
-      LLMI_REQUIRE(p.prologue != kAttnCombine ||
-                       (R == GroupProblem::kNarrow && probs.size() == 1 && waves * 64 <= kCombineMaxThreads),
-                   "group: an attention-combine product launches alone, with in <= 2048");
     l.total_wgs = static_cast<int>(wg);
     l.nprob = static_cast<int>(probs.size());
     plan->probs.insert(plan->probs.end(), probs.begin(), probs.end());
@@ -1743,9 +1665,6 @@ int DeviceGroup::build(const GroupEntry* entries, std::size_t count) {
   if (int rc = plan_group(entries, count, &plan)) return rc;
   launches = plan.launches;
   host_probs = plan.probs;
-  comb_hd = 0;
-  for (std::size_t i = 0; i < count; ++i)
-    if (entries[i].prologue == kAttnCombine) comb_hd = entries[i].pa;
   const std::size_t pbytes = plan.probs.size() * sizeof(GroupProblem);
   const std::size_t mbytes = plan.wg_prob.size() * sizeof(std::uint32_t);
   if (pbytes + mbytes == 0) return LLMI_OK;
@@ -1758,32 +1677,21 @@ int DeviceGroup::build(const GroupEntry* entries, std::size_t count) {
   return LLMI_OK;
 }
 
-int DeviceGroup::launch(hipStream_t s, int chunks) const {
+int DeviceGroup::launch(hipStream_t s) const {
   for (const GroupLaunch& l : launches) {
     if (l.rchunk == GroupProblem::kNarrow && l.nprob >= 1 && l.nprob <= kFewProblems && l.total_wgs > 0) {
       // Few products: descriptors by value (qgemv_few_narrow).
       FewProblems f{};
       f.count = l.nprob;
       for (int k = 0; k < l.nprob; ++k) f.p[k] = host_probs[l.prob_offset + static_cast<std::size_t>(k)];
-      bool comb = false;
-      for (int k = 0; k < l.nprob; ++k) comb = comb || f.p[k].prologue == kAttnCombine;
-      if (comb) {
-        LLMI_REQUIRE(chunks >= 1 && chunks <= kAttnMaxChunks, "group: attention chunks out of range");
-        f.comb_hd = comb_hd;
-        f.comb_nch = chunks;
-      }
       const dim3 grid(static_cast<unsigned>(l.total_wgs)), block(static_cast<unsigned>(l.waves * 64));
       if (l.nprob == 1) {
         // One product: scalar arguments (preloaded), qgemv_one_narrow.
         const GroupProblem& p = f.p[0];
         const auto* codes = reinterpret_cast<const uint4*>(p.codes);
-#define LLMI_ONE_ARGS                                                                                    \
-  codes, p.scales, p.x, p.pw, p.nblk, p.bpw, p.in, p.prologue, p.eps, p.out, p.bias, p.y, p.accumulate, \
-      f.comb_hd, f.comb_nch
-        if (comb) {
-          if (l.type == LLMI_TYPE_Q8_0) qgemv_one_narrow<LLMI_TYPE_Q8_0, true><<<grid, block, l.lds, s>>>(LLMI_ONE_ARGS);
-          else qgemv_one_narrow<LLMI_TYPE_Q4_0, true><<<grid, block, l.lds, s>>>(LLMI_ONE_ARGS);
-        } else if (l.type == LLMI_TYPE_Q8_0) {
+#define LLMI_ONE_ARGS \
+  codes, p.scales, p.x, p.pw, p.nblk, p.bpw, p.in, p.prologue, p.eps, p.out, p.bias, p.y, p.accumulate
+        if (l.type == LLMI_TYPE_Q8_0) {
           qgemv_one_narrow<LLMI_TYPE_Q8_0><<<grid, block, l.lds, s>>>(LLMI_ONE_ARGS);
         } else {
           qgemv_one_narrow<LLMI_TYPE_Q4_0><<<grid, block, l.lds, s>>>(LLMI_ONE_ARGS);
@@ -1792,10 +1700,7 @@ int DeviceGroup::launch(hipStream_t s, int chunks) const {
         LLMI_TRY_HIP(hipGetLastError());
         continue;
       }
-      if (comb) {
-        if (l.type == LLMI_TYPE_Q8_0) qgemv_few_narrow<LLMI_TYPE_Q8_0, true><<<grid, block, l.lds, s>>>(f);
-        else qgemv_few_narrow<LLMI_TYPE_Q4_0, true><<<grid, block, l.lds, s>>>(f);
-      } else if (l.type == LLMI_TYPE_Q8_0) {
+      if (l.type == LLMI_TYPE_Q8_0) {
         qgemv_few_narrow<LLMI_TYPE_Q8_0><<<grid, block, l.lds, s>>>(f);
       } else {
         qgemv_few_narrow<LLMI_TYPE_Q4_0><<<grid, block, l.lds, s>>>(f);
@@ -1887,7 +1792,6 @@ void DeviceGroup::release() {
   map = nullptr;
   launches.clear();
   host_probs.clear();
-  comb_hd = 0;
 }
 
 }  // namespace llmi_hip

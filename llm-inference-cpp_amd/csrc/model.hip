@@ -1321,10 +1321,8 @@ struct DeviceLayer {
   // multiple of 64 rows; out == 0 otherwise.  bqkv: the biases likewise.
   DeviceMatrix wqkv, gate_up_w;
   float* bqkv = nullptr;
-  // The fused one-token step's launches (see decode_step); o_comb is the
-  // tolerance-mode step's o_proj, which stages the attention output from
-  // the chunk partials (kAttnCombine).
-  DeviceGroup qkv, gate_up, down_silu, o_comb;
+  // The fused one-token step's launches (see decode_step).
+  DeviceGroup qkv, gate_up, down_silu;
   // The tolerance-mode step's products split over K (with fused q|k|v and
   // gate|up weights): q|k|v (clearing g|u), o_proj (clearing q|k|v for the
   // next layer), gate|up, down_proj.
@@ -1381,7 +1379,6 @@ struct llmi_hip_model {
   double last_prefill_ms = 0.0, last_decode_ms = 0.0;  // of the last greedy run
   int decode_mode = LLMI_DECODE_EXACT;  // llmi_hip_model_set_decode_mode
   bool tol_ready = false;               // build_decode made the tolerance-mode step
-  bool split_ready = false;             // ... with its products split over K (SplitProduct)
   bool qkv_clear = false;               // the last queued step left dec.q|k|v at zero (split step)
   std::size_t last_redraws = 0;  // generate_sampled: queued draws redrawn step by step
 };
@@ -1537,11 +1534,6 @@ int build_decode(llmi_hip_model* m) {
   d.u = d.g + m->F;
   if (int rc = get(&d.part, static_cast<std::size_t>(kAttnMaxChunks) * m->c.num_heads * (m->hd + 2))) return rc;
   const float eps = static_cast<float>(m->c.rms_norm_eps);
-  // The tolerance-mode step: head sizes of attn_part_1, and an o_proj whose
-  // combine staging fits one workgroup of up to 512 threads (in <= 2048).
-  const bool tol = tol_attention_fits(static_cast<int>(m->c.num_heads), static_cast<int>(m->c.num_kv_heads),
-                                      static_cast<int>(m->hd)) &&
-                   m->Q <= 2048;
   for (DeviceLayer& l : m->layers) {
     const GroupEntry qkv[3] = {{&l.wq, d.x, l.bq, d.q, 1, false, kRmsNorm, l.attn_norm, eps},
                                {&l.wk, d.x, l.bk, d.k, 1, false, kRmsNorm, l.attn_norm, eps},
@@ -1556,19 +1548,16 @@ int build_decode(llmi_hip_model* m) {
     if (int rc = l.wqkv.out != 0 ? l.qkv.build(qkv1, 1) : l.qkv.build(qkv, 3)) return rc;
     if (int rc = l.gate_up_w.out != 0 ? l.gate_up.build(gu1, 1) : l.gate_up.build(gu, 2)) return rc;
     if (int rc = l.down_silu.build(dn, 1)) return rc;
-    if (tol) {
-      GroupEntry oc{&l.wo, d.part, nullptr, d.x, 1, true, kAttnCombine, d.part, 0.0f};
-      oc.pa = static_cast<int>(m->hd);
-      if (int rc = l.o_comb.build(&oc, 1)) return rc;
-    }
   }
-  m->tol_ready = tol;
-  // The split products need the fused weights and a head_dim that splits
-  // into whole blocks.
-  bool split = tol && m->hd % kBlock == 0;
-  for (const DeviceLayer& l : m->layers) split = split && l.wqkv.out != 0 && l.gate_up_w.out != 0;
+  // The tolerance-mode step: head sizes attn_part_1 takes, whole blocks per
+  // head (the o_proj splits take whole heads), and the fused q|k|v and
+  // gate|up weights its split products run on.
+  bool tol = tol_attention_fits(static_cast<int>(m->c.num_heads), static_cast<int>(m->c.num_kv_heads),
+                                static_cast<int>(m->hd)) &&
+             m->hd % kBlock == 0;
+  for (const DeviceLayer& l : m->layers) tol = tol && l.wqkv.out != 0 && l.gate_up_w.out != 0;
   for (DeviceLayer& l : m->layers) {
-    if (!split) break;
+    if (!tol) break;
     l.s_qkv = SplitProduct{&l.wqkv, d.x, l.attn_norm, l.bqkv, d.q, kRmsNorm, eps};
     l.s_qkv.zero = d.g;
     l.s_qkv.nzero = static_cast<int>(2 * m->F);
@@ -1581,7 +1570,7 @@ int build_decode(llmi_hip_model* m) {
     for (SplitProduct* sp : {&l.s_qkv, &l.s_o, &l.s_gu, &l.s_dn})
       if (int rc = plan_split(sp)) return rc;
   }
-  m->split_ready = split;
+  m->tol_ready = tol;
   return LLMI_OK;
 }
 
@@ -1590,7 +1579,6 @@ void release_decode(llmi_hip_model* m) {
     l.qkv.release();
     l.gate_up.release();
     l.down_silu.release();
-    l.o_comb.release();
   }
 }
 
@@ -1768,9 +1756,9 @@ int ensure_workspace(llmi_hip_model* m, std::size_t T) {
 // One token (T = 1) through the fused per-layer launches built by
 // build_decode; the same arithmetic as forward_device.  Logits land in
 // ws.logits.
-// tolerance: the attention of llmi_hip_model_set_decode_mode's tolerance
-// mode (position chunks merged in o_proj's staging); everything else is the
-// exact step.
+// tolerance: llmi_hip_model_set_decode_mode's tolerance-mode step (needs
+// tol_ready): the attention over position chunks, merged in the o_proj
+// product's staging, and every matmul split over K (SplitProduct).
 int decode_step(llmi_hip_model* m, llmi_hip_cache* cache, hipStream_t s, bool tolerance = false) {
   const auto& c = m->c;
   Workspace& w = m->ws;
@@ -1783,7 +1771,7 @@ int decode_step(llmi_hip_model* m, llmi_hip_cache* cache, hipStream_t s, bool to
   const float scale = 1.0F / std::sqrt(static_cast<float>(m->hd));
   const std::size_t per_layer = static_cast<std::size_t>(c.num_kv_heads) * cache->cap * m->hd;
   if (int rc = launch_dequantize_rows(m->embed, w.ids, 1, d.x, s)) return rc;
-  const bool split = tolerance && m->split_ready;
+  const bool split = tolerance && m->tol_ready;
   // q|k|v start at zero in a split step: cleared by the previous layer's
   // o_proj launch (the previous split step's last layer for the first), or
   // here when the step before was not a split step.
@@ -1803,17 +1791,10 @@ int decode_step(llmi_hip_model* m, llmi_hip_cache* cache, hipStream_t s, bool to
       continue;
     }
     if (int rc = l.qkv.launch(s)) return rc;
-    if (tolerance) {
-      const int nch = launch_tol_attention(d.q, d.k, d.v, cache->k + li * per_layer, cache->v + li * per_layer,
-                                           m->cos_t, m->sin_t, d.part, nh, nkv, hd, static_cast<int>(cache->cap),
-                                           static_cast<int>(pos + 1), scale, s);
-      if (int rc = l.o_comb.launch(s, nch)) return rc;
-    } else {
-      launch_decode_attention(d.q, d.k, d.v, cache->k + li * per_layer, cache->v + li * per_layer, m->cos_t,
-                              m->sin_t, cache->scores, d.att, nh, nkv, hd, static_cast<int>(cache->cap),
-                              static_cast<int>(pos + 1), scale, s);
-      if (int rc = launch_matmul(l.wo, d.att, 1, nullptr, d.x, s, true)) return rc;
-    }
+    launch_decode_attention(d.q, d.k, d.v, cache->k + li * per_layer, cache->v + li * per_layer, m->cos_t,
+                            m->sin_t, cache->scores, d.att, nh, nkv, hd, static_cast<int>(cache->cap),
+                            static_cast<int>(pos + 1), scale, s);
+    if (int rc = launch_matmul(l.wo, d.att, 1, nullptr, d.x, s, true)) return rc;
     if (int rc = l.gate_up.launch(s)) return rc;
     if (int rc = l.down_silu.launch(s)) return rc;
   }
