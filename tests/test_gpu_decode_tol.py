@@ -8,9 +8,11 @@ pins them at the full-size models' recorded steps):
 * per step, max|logits_tol - logits_exact| <= 1e-4 * max|logits_exact|
   (the relative-error bar the north star states for fp32-accumulate paths),
   fed the same tokens, on small models with head sizes 64 and 128, GQA groups
-  1, 3 and 7, and contexts from 1 to past 2048 positions (one chunk of 64 up
-  to sixteen chunks of 192), and on one-layer models with MLPs of 8192 and
-  16384 (every split width of the matmuls);
+  1, 2, 3 and 7, two and three layers, and contexts from 1 to past 2048
+  positions (one chunk of 64 up to sixteen chunks of 192), and on one-layer
+  models with MLPs of 8192 and 16384 (every split width of the matmuls);
+  an intermediate size that is not a multiple of 64 leaves gate and up as
+  two matrices, and the tolerance mode then keeps the exact step;
 * on the synthetic SmolLM2-135M and Qwen2.5-0.5B:
   the greedy ids of the first 64 steps equal the compiled reference's, and
   every step's logits, fed the reference's ids, are within the bar.
@@ -42,13 +44,17 @@ def cfg_of(hidden, heads, kv, arch=1, ctx=4096, layers=2, vocab=512):
                 rope_theta=10000.0, tie_word_embeddings=1, qkv_bias=int(arch == 1))
 
 
-@pytest.mark.parametrize("hidden,heads,kv,qt", [(128, 2, 2, H.Q8_0), (448, 7, 1, H.Q4_0), (576, 9, 3, H.Q8_0),
-                                                (256, 2, 1, H.Q4_0)])
-def test_tolerance_steps_match_exact_steps(hidden, heads, kv, qt):
+@pytest.mark.parametrize("hidden,heads,kv,qt,layers,inter_pad",
+                         [(128, 2, 2, H.Q8_0, 2, 0), (448, 7, 1, H.Q4_0, 2, 0), (576, 9, 3, H.Q8_0, 2, 0),
+                          (256, 2, 1, H.Q4_0, 2, 0), (192, 3, 1, H.Q8_0, 3, 0), (128, 2, 1, H.Q4_0, 2, 16)])
+def test_tolerance_steps_match_exact_steps(hidden, heads, kv, qt, layers, inter_pad):
     """Steps at positions 1..80 after a one-token prompt, then steps at
     positions ~1000-1100 and ~2100 after longer prompts (chunks of 64, 128 and
-    192 positions); both modes fed the same tokens."""
-    cfg = cfg_of(hidden, heads, kv)
+    192 positions); both modes fed the same tokens; two and three layers.
+    The intermediate size 272 (not a multiple of 64: no fused gate|up
+    matrix) keeps the exact step, so its logits are bit-identical."""
+    cfg = cfg_of(hidden, heads, kv, layers=layers)
+    cfg["intermediate_size"] += inter_pad
     m = H.Model(cfg, synth.make_tensors(cfg, 500 + hidden + heads, "bench"), qt)
     worst = 0.0
     for n_prompt, n_steps in ((1, 80), (1000, 100), (2100, 20)):
@@ -68,6 +74,8 @@ def test_tolerance_steps_match_exact_steps(hidden, heads, kv, qt):
             lt = m.forward_cached(ct, [tok])
             err = rel_err(lt, le)
             assert err <= TOL, (n_prompt, i, err)
+            if inter_pad:
+                assert err == 0.0, (n_prompt, i, err)
             worst = max(worst, err)
         ce.free()
         ct.free()
