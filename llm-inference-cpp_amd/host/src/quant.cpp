@@ -67,10 +67,18 @@ QuantizedMatrix quantize(const float* w, std::size_t out, std::size_t in, Type t
   return m;
 }
 
+// Only the row travels to the device, as a one-row matrix: a loop over the
+// rows of a large matrix then moves each row once, not the whole matrix per
+// row.
 void dequantize_row(const QuantizedMatrix& m, std::size_t row, float* dst) {
+  ensure_init();
+  if (row >= m.out) throw std::runtime_error("llmi_hip_dequantize_row: dequantize_row: row out of range");
+  const std::size_t rb = llmi_hip_row_bytes(m.in, abi_type(m.type));
   Uploaded u;
-  upload(m, u);
-  check(llmi_hip_dequantize_row(u.w, row, dst), "llmi_hip_dequantize_row");
+  check(llmi_hip_weight_upload(m.data.data() + row * rb, m.scales.data() + row * m.blocks_per_row, 1, m.in,
+                               abi_type(m.type), &u.w),
+        "llmi_hip_weight_upload");
+  check(llmi_hip_dequantize_row(u.w, 0, dst), "llmi_hip_dequantize_row");
 }
 
 void matmul(const float* x, std::size_t rows, std::size_t in, const QuantizedMatrix& w, std::size_t out,

@@ -7,6 +7,7 @@
 // must be the oracle's bit for bit.
 #include <algorithm>
 #include <cstring>
+#include <stdexcept>
 
 #include "check.hpp"
 #include "llmi/model/quant.hpp"
@@ -74,6 +75,14 @@ TEST(QuantDiff, PackingDequantAndProductsEqualTheOracle) {
       oracle_dequantize_row(data.data(), scales.data(), c.in, abi_type(c.type), r, want.data());
       EXPECT_TRUE(bits_equal(got.data(), want.data(), c.in));
     }
+    // Only the row is uploaded; a row past the matrix is an error, not a read.
+    bool threw = false;
+    try {
+      q::dequantize_row(m, c.out, got.data());
+    } catch (const std::runtime_error&) {
+      threw = true;
+    }
+    EXPECT_TRUE(threw);
 
     const std::vector<float> bias = check::normal(seed + 7, c.out, 0.0, 0.1);
     for (std::size_t rows : c.rows) {
