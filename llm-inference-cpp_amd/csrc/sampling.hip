@@ -28,7 +28,9 @@
 //     smp_sel_merge  the first k among those, ranked
 //   else, when something is filtered (the whole ranking):
 //     smp_scale  p = e * inv and the ranking keys (float bits, index)
-//     [rocprim radix sort, descending, stable: std::stable_sort's order]
+//     smp_sort_hist / smp_sort_scan / smp_sort_scatter, four times: the
+//                ranking by a stable LSD radix sort (descending p, ties in
+//                index order: std::stable_sort's order)
 //   (nothing filtered: the later kernels scale e on the fly)
 //   smp_keep   top-k, top-p, bounds on the renormalisation sum
 //   smp_draw   the filtered probabilities (bounded) and the first index whose
@@ -38,9 +40,6 @@
 // again.  sampling_probabilities always takes the exact sum.
 
 #include <hip/hip_runtime.h>
-
-#include <cstring>  // rocprim's headers use memset on the host
-#include <rocprim/device/device_radix_sort.hpp>
 
 #include <cstdint>
 #include <vector>
@@ -981,12 +980,158 @@ __global__ void __launch_bounds__(kSmpThreads) smp_write(int n, SmpWork w, float
   out[i] = kept(x, i, w.st->p_thr, w.st->idx_last) ? renorm(x, w.st->s2_lo) : 0.0f;
 }
 
+// ------------------------------------------------------------ ranking sort
+// The ranking of smp_scale's keys (the bits of p >= +0, so key order is p
+// order): descending key, ties in ascending index, i.e. the order
+// std::stable_sort gives with p[a] > p[b].  A stable LSD radix sort of
+// k' = ~key ascending over four 8-bit digits; each pass takes three launches
+// over tiles of per_tile consecutive elements: smp_sort_hist (the tile's
+// digit counts, and how many of the tile's elements have a smaller digit),
+// smp_sort_scan (each digit's start in each tile: digits in order, tiles in
+// order within a digit) and smp_sort_scatter (every element to its digit's
+// next slot, in index order within the tile).  The first pass reads the keys
+// and takes the element's index as its value, the last writes ~k' (the key
+// again).  Counts are kept [digit][tile].
+constexpr int kSortThreads = 256;
+constexpr int kSortWaves = kSortThreads / 64;
+constexpr int kSortDigits = 256;
+constexpr int kSortMaxTiles = 4096;
+
+// Exclusive prefix sum of v over the workgroup's threads in thread order
+// (kSortThreads of them); *total receives the sum of all.  Ends with every
+// thread past its reads of the LDS scratch.
+__device__ __forceinline__ unsigned block_excl_scan(unsigned v, unsigned* scratch, unsigned* total) {
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  unsigned incl = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const unsigned u = __shfl_up(incl, o, 64);
+    if (lane >= o) incl += u;
+  }
+  if (lane == 63) scratch[w] = incl;
+  __syncthreads();
+  unsigned base = 0, all = 0;
+#pragma unroll
+  for (int x = 0; x < kSortWaves; ++x) {
+    if (x < w) base += scratch[x];
+    all += scratch[x];
+  }
+  *total = all;
+  __syncthreads();
+  return base + incl - v;
+}
+
+__global__ void __launch_bounds__(kSortThreads) smp_sort_hist(const std::uint32_t* __restrict__ keys, int n,
+                                                              int per_tile, int shift, int invert,
+                                                              unsigned* __restrict__ hist, unsigned* __restrict__ below,
+                                                              int tiles) {
+  __shared__ unsigned h[kSortDigits];
+  __shared__ unsigned scratch[kSortWaves];
+  const int t = blockIdx.x, tid = threadIdx.x;
+  h[tid] = 0;
+  __syncthreads();
+  const int lo = t * per_tile, hi = min(n, lo + per_tile);
+  for (int i = lo + tid; i < hi; i += kSortThreads) {
+    const std::uint32_t k = invert ? ~keys[i] : keys[i];
+    atomicAdd(&h[(k >> shift) & 255u], 1u);
+  }
+  __syncthreads();
+  const unsigned c = h[tid];
+  unsigned all;
+  const unsigned smaller = block_excl_scan(c, scratch, &all);
+  hist[static_cast<std::size_t>(tid) * tiles + t] = c;
+  below[static_cast<std::size_t>(tid) * tiles + t] = smaller;
+}
+
+// One workgroup per digit d: its start = the elements of all tiles with a
+// smaller digit (the sum of `below` over the tiles), then hist[d][t] becomes
+// that start plus the digit's count in tiles 0 .. t-1.
+__global__ void __launch_bounds__(kSortThreads) smp_sort_scan(unsigned* __restrict__ hist,
+                                                              const unsigned* __restrict__ below, int tiles) {
+  __shared__ unsigned scratch[kSortWaves];
+  const int d = blockIdx.x, tid = threadIdx.x;
+  unsigned* row = hist + static_cast<std::size_t>(d) * tiles;
+  const unsigned* brow = below + static_cast<std::size_t>(d) * tiles;
+  unsigned part = 0;
+  for (int t = tid; t < tiles; t += kSortThreads) part += brow[t];
+  unsigned carry;
+  (void)block_excl_scan(part, scratch, &carry);
+  for (int t0 = 0; t0 < tiles; t0 += kSortThreads) {
+    const int t = t0 + tid;
+    const unsigned c = t < tiles ? row[t] : 0u;
+    unsigned all;
+    const unsigned excl = block_excl_scan(c, scratch, &all);
+    if (t < tiles) row[t] = carry + excl;
+    carry += all;
+  }
+}
+
+// Rounds of 256 consecutive elements: a lane's rank among the lanes of its
+// wavefront with the same digit from eight ballots, the wavefronts' counts
+// per digit through LDS (earlier wavefronts first), then the digit's running
+// position advanced by the round's count.
+__global__ void __launch_bounds__(kSortThreads) smp_sort_scatter(const std::uint32_t* __restrict__ kin,
+                                                                 const std::int32_t* __restrict__ iin,
+                                                                 std::uint32_t* __restrict__ kout,
+                                                                 std::int32_t* __restrict__ iout, int n, int per_tile,
+                                                                 int shift, int first, int last,
+                                                                 const unsigned* __restrict__ offs, int tiles) {
+  __shared__ unsigned base[kSortDigits];
+  __shared__ unsigned wcnt[kSortWaves][kSortDigits];
+  const int t = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  base[tid] = offs[static_cast<std::size_t>(tid) * tiles + t];
+  const unsigned long long below = lane == 0 ? 0ull : ~0ull >> (64 - lane);
+  const int lo = t * per_tile, hi = min(n, lo + per_tile);
+  for (int r0 = lo; r0 < hi; r0 += kSortThreads) {
+    const int i = r0 + tid;
+    const bool live = i < hi;
+    std::uint32_t k = 0;
+    std::int32_t v = 0;
+    if (live) {
+      k = first ? ~kin[i] : kin[i];
+      v = first ? i : iin[i];
+    }
+    const unsigned d = (k >> shift) & 255u;
+    unsigned long long peers = __ballot(live);
+#pragma unroll
+    for (int b = 0; b < 8; ++b) {
+      const unsigned long long set = __ballot((d >> b) & 1u);
+      peers &= ((d >> b) & 1u) ? set : ~set;
+    }
+    const unsigned rank = static_cast<unsigned>(__popcll(peers & below));
+#pragma unroll
+    for (int x = 0; x < kSortWaves; ++x) wcnt[x][tid] = 0;
+    __syncthreads();  // zeros (and, in the first round, base) visible
+    if (live && rank == 0) wcnt[w][d] = static_cast<unsigned>(__popcll(peers));
+    __syncthreads();
+    if (live) {
+      unsigned pos = base[d] + rank;
+      for (int x = 0; x < w; ++x) pos += wcnt[x][d];
+      kout[pos] = last ? ~k : k;
+      iout[pos] = v;
+    }
+    __syncthreads();  // every position taken before base moves
+    unsigned sum = 0;
+#pragma unroll
+    for (int x = 0; x < kSortWaves; ++x) sum += wcnt[x][tid];
+    base[tid] += sum;
+  }
+}
+
+// Elements per tile: 1024, or more so that there are at most kSortMaxTiles.
+int sort_per_tile(std::size_t n) {
+  const std::size_t per = std::max<std::size_t>(1024, ceil_div(n, static_cast<std::size_t>(kSortMaxTiles)));
+  return static_cast<int>(ceil_div(per, static_cast<std::size_t>(kSortThreads)) * kSortThreads);
+}
+
 // ------------------------------------------------------------------- host
 struct SmpBuffers {
   std::size_t cap = 0;
   void* base = nullptr;
-  void* sort_tmp = nullptr;
-  std::size_t sort_bytes = 0;
+  std::uint32_t* sort_keys = nullptr;  // the ranking sort's second buffer of keys,
+  std::int32_t* sort_idx = nullptr;    // of indices,
+  unsigned* sort_hist = nullptr;       // and its digit counts ([digit][tile])
+  unsigned* sort_below = nullptr;      // and the tiles' counts of smaller digits
   float* host_io = nullptr;  // staging for the host-pointer entry points (device)
   std::int32_t* id_dev = nullptr;
   SmpWork w{};
@@ -998,26 +1143,16 @@ int smp_reserve(std::size_t n, hipStream_t s) {
   if (n <= g_smp.cap) return LLMI_OK;
   LLMI_TRY_HIP(hipStreamSynchronize(s));
   if (g_smp.base != nullptr) LLMI_TRY_HIP(hipFree(g_smp.base));
-  if (g_smp.sort_tmp != nullptr) LLMI_TRY_HIP(hipFree(g_smp.sort_tmp));
   g_smp = SmpBuffers{};
-  std::size_t sort_bytes = 0;
-  LLMI_TRY_HIP(rocprim::radix_sort_pairs_desc(nullptr, sort_bytes, static_cast<const std::uint32_t*>(nullptr),
-                                              static_cast<std::uint32_t*>(nullptr),
-                                              static_cast<const std::int32_t*>(nullptr),
-                                              static_cast<std::int32_t*>(nullptr), static_cast<unsigned>(n), 0, 32, s));
+  const std::size_t tiles = ceil_div(n, static_cast<std::size_t>(sort_per_tile(n)));
   auto al = [](std::size_t b) { return (b + 255) & ~static_cast<std::size_t>(255); };
   // The top-k selection writes up to kCandMax candidates into keys / idx.
   const std::size_t vn = n > static_cast<std::size_t>(kCandMax) ? n : static_cast<std::size_t>(kCandMax);
   const std::size_t vec = al(vn * 4);
-  const std::size_t bytes = 7 * vec + al(sizeof(double) * 2 * kSmpBlocks) + al(sizeof(int) * 2 * kSmpBlocks) +
+  const std::size_t bytes = 9 * vec + 2 * al(sizeof(unsigned) * kSortDigits * tiles) +
+                            al(sizeof(double) * 2 * kSmpBlocks) + al(sizeof(int) * 2 * kSmpBlocks) +
                             al(sizeof(float) * kSmpBlocks) + al(sizeof(SmpState)) + al(sizeof(std::int32_t));
   LLMI_TRY_HIP(hipMalloc(&g_smp.base, bytes));
-  const hipError_t e = hipMalloc(&g_smp.sort_tmp, sort_bytes == 0 ? 1 : sort_bytes);
-  if (e != hipSuccess) {
-    (void)hipFree(g_smp.base);
-    g_smp.base = nullptr;
-    return fail(LLMI_ERR_HIP, std::string("sampling workspace: ") + hipGetErrorString(e));
-  }
   char* c = static_cast<char*>(g_smp.base);
   auto take = [&c, &al](std::size_t b) {
     void* r = c;
@@ -1032,13 +1167,16 @@ int smp_reserve(std::size_t n, hipStream_t s) {
   w.idx_sorted = static_cast<std::int32_t*>(take(vn * 4));
   g_smp.host_io = static_cast<float*>(take(vn * 4));
   (void)take(vn * 4);  // spare
+  g_smp.sort_keys = static_cast<std::uint32_t*>(take(vn * 4));
+  g_smp.sort_idx = static_cast<std::int32_t*>(take(vn * 4));
+  g_smp.sort_hist = static_cast<unsigned*>(take(sizeof(unsigned) * kSortDigits * tiles));
+  g_smp.sort_below = static_cast<unsigned*>(take(sizeof(unsigned) * kSortDigits * tiles));
   w.part_d = static_cast<double*>(take(sizeof(double) * 2 * kSmpBlocks));
   w.part_i = static_cast<int*>(take(sizeof(int) * 2 * kSmpBlocks));
   w.part_f = static_cast<float*>(take(sizeof(float) * kSmpBlocks));
   w.st = static_cast<SmpState*>(take(sizeof(SmpState)));
   g_smp.id_dev = static_cast<std::int32_t*>(take(sizeof(std::int32_t)));
   LLMI_TRY_HIP(hipMemsetAsync(w.st, 0, sizeof(SmpState), s));
-  g_smp.sort_bytes = sort_bytes;
   g_smp.cap = n;
   return LLMI_OK;
 }
@@ -1049,10 +1187,28 @@ int smp_check_cfg(const llmi_hip_sampling* cfg, std::size_t n) {
   return LLMI_OK;
 }
 
+// The ranking of keys[0, n) into keys_sorted / idx_sorted (the sort kernels
+// above): passes 0 and 2 write the sort's own buffers, 1 and 3 the sorted
+// ones; keys is only read.
 int smp_sort(std::size_t n, hipStream_t s) {
-  std::size_t bytes = g_smp.sort_bytes;
-  LLMI_TRY_HIP(rocprim::radix_sort_pairs_desc(g_smp.sort_tmp, bytes, g_smp.w.keys, g_smp.w.keys_sorted, g_smp.w.idx,
-                                              g_smp.w.idx_sorted, static_cast<unsigned>(n), 0, 32, s));
+  const SmpWork& w = g_smp.w;
+  const int ni = static_cast<int>(n), per = sort_per_tile(n);
+  const int tiles = static_cast<int>(ceil_div(n, static_cast<std::size_t>(per)));
+  LLMI_REQUIRE(n <= g_smp.cap && tiles <= kSortMaxTiles, "sampling: ranking larger than its workspace");
+  const std::uint32_t* kin = w.keys;
+  const std::int32_t* iin = nullptr;
+  for (int pass = 0; pass < 4; ++pass) {
+    std::uint32_t* kout = pass % 2 == 0 ? g_smp.sort_keys : w.keys_sorted;
+    std::int32_t* iout = pass % 2 == 0 ? g_smp.sort_idx : w.idx_sorted;
+    smp_sort_hist<<<tiles, kSortThreads, 0, s>>>(kin, ni, per, 8 * pass, pass == 0 ? 1 : 0, g_smp.sort_hist,
+                                                 g_smp.sort_below, tiles);
+    smp_sort_scan<<<kSortDigits, kSortThreads, 0, s>>>(g_smp.sort_hist, g_smp.sort_below, tiles);
+    smp_sort_scatter<<<tiles, kSortThreads, 0, s>>>(kin, iin, kout, iout, ni, per, 8 * pass, pass == 0 ? 1 : 0,
+                                                    pass == 3 ? 1 : 0, g_smp.sort_hist, tiles);
+    kin = kout;
+    iin = iout;
+  }
+  LLMI_TRY_HIP(hipGetLastError());
   return LLMI_OK;
 }
 
@@ -1112,7 +1268,6 @@ int smp_bad_input(const SmpState& st) {
 
 void release_sampling_workspace() {
   if (g_smp.base != nullptr) (void)hipFree(g_smp.base);
-  if (g_smp.sort_tmp != nullptr) (void)hipFree(g_smp.sort_tmp);
   g_smp = SmpBuffers{};
 }
 

@@ -138,6 +138,22 @@ def test_draws_on_a_running_sum_take_the_sequential_pass(cfg):
     assert seen & (4 | 8 | 16)
 
 
+@pytest.mark.parametrize("kind", ["normal", "ties", "masked"])
+@pytest.mark.parametrize("n", [1000, 49152, 151936])
+def test_top_p_sweep_over_the_ranking(kind, n):
+    """top_p alone (and with a top_k above the selection limit) ranks the
+    whole vocabulary with the radix sort: kept prefixes from one entry to
+    nearly all of them, cut inside groups of tied logits, must be the
+    reference's (descending p, ties in index order)."""
+    o = O.oracle()
+    lg = logits_case(kind, n, 11 * n + len(kind))
+    for top_p in (0.001, 0.05, 0.2, 0.45, 0.6, 0.8, 0.9, 0.97, 0.995, 0.99999):
+        for temp, top_k in ((1.0, 0), (0.5, 0), (1.0, 700)):
+            want = o.sampling_probabilities(lg, temp, top_k, top_p)
+            got = H.sampling_probabilities(lg, H.Sampling(temp, top_k, top_p))
+            assert np.array_equal(bits(got), bits(want)), (top_p, temp, top_k)
+
+
 def test_top_p_on_a_running_sum():
     """Probabilities that are exact binary fractions put top_p exactly on a
     ranked running sum (keep = 2 for top_p 0.5 over four equal logits)."""
