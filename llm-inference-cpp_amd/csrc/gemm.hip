@@ -505,6 +505,56 @@ __global__ void __launch_bounds__(256) gemm_reduce(const float* __restrict__ par
   }
 }
 
+// gemm_reduce for four consecutive outputs per thread (16-byte loads and
+// stores): out a multiple of 4 and part, y and bias 16-byte aligned.  The
+// same sums in the same order.
+__global__ void __launch_bounds__(256) gemm_reduce4(const float4* __restrict__ part, int kchunks, int rows, int out,
+                                                    const float4* __restrict__ bias, float4* __restrict__ y,
+                                                    int accumulate) {
+  const std::size_t n4 = static_cast<std::size_t>(rows) * out / 4;
+  const int out4 = out / 4;
+  for (std::size_t i = static_cast<std::size_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n4;
+       i += static_cast<std::size_t>(gridDim.x) * blockDim.x) {
+    float4 v[8];
+    const int kc = min(kchunks, 8);
+#pragma unroll
+    for (int c = 0; c < 8; ++c)
+      if (c < kc) v[c] = part[c * n4 + i];
+    float4 sum = v[0];
+#pragma unroll
+    for (int c = 1; c < 8; ++c)
+      if (c < kc) sum = make_float4(sum.x + v[c].x, sum.y + v[c].y, sum.z + v[c].z, sum.w + v[c].w);
+    for (int c = 8; c < kchunks; ++c) {
+      const float4 u = part[c * n4 + i];
+      sum = make_float4(sum.x + u.x, sum.y + u.y, sum.z + u.z, sum.w + u.w);
+    }
+    const float4 add = bias != nullptr ? bias[i % out4] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    float4 val = make_float4(sum.x + add.x, sum.y + add.y, sum.z + add.z, sum.w + add.w);
+    if (accumulate) {
+      const float4 o = y[i];
+      val = make_float4(o.x + val.x, o.y + val.y, o.z + val.z, o.w + val.w);
+    }
+    y[i] = val;
+  }
+}
+
+// The reduce of one split product: the 16-byte form where the shapes and
+// pointers allow it.
+void launch_reduce(const float* part, int kchunks, int rows, int out, const float* bias, float* y, int accumulate,
+                   hipStream_t s) {
+  const auto a16 = [](const void* q) { return reinterpret_cast<std::uintptr_t>(q) % 16 == 0; };
+  const std::size_t n = static_cast<std::size_t>(rows) * out;
+  if (out % 4 == 0 && a16(part) && a16(y) && (bias == nullptr || a16(bias))) {
+    const unsigned blocks = static_cast<unsigned>(std::min<std::size_t>(ceil_div(n / 4, 256), 8192));
+    gemm_reduce4<<<blocks, 256, 0, s>>>(reinterpret_cast<const float4*>(part), kchunks, rows, out,
+                                        reinterpret_cast<const float4*>(bias), reinterpret_cast<float4*>(y),
+                                        accumulate);
+    return;
+  }
+  const unsigned blocks = static_cast<unsigned>(std::min<std::size_t>(ceil_div(n, 256), 8192));
+  gemm_reduce<<<blocks, 256, 0, s>>>(part, kchunks, rows, out, bias, y, accumulate);
+}
+
 }  // namespace
 
 int gemm_kchunks(std::size_t in, std::size_t launch_tiles, std::size_t split_tiles) {
@@ -639,9 +689,7 @@ void bind_gemm_scratch(GemmPlan* plan, std::uint16_t* scratch) {
 int launch_gemm_reduces(const GemmPlan& plan, hipStream_t s) {
   for (const GemmProblem& p : plan.probs) {
     if (p.kchunks <= 1) continue;
-    const std::size_t n = static_cast<std::size_t>(p.rows) * p.out;
-    const unsigned blocks = static_cast<unsigned>(std::min<std::size_t>(ceil_div(n, 256), 8192));
-    gemm_reduce<<<blocks, 256, 0, s>>>(p.part, p.kchunks, p.rows, p.out, p.bias, p.y, p.accumulate);
+    launch_reduce(p.part, p.kchunks, p.rows, p.out, p.bias, p.y, p.accumulate, s);
   }
   LLMI_TRY_HIP(hipGetLastError());
   return LLMI_OK;
@@ -766,9 +814,7 @@ int launch_gemm_noalloc(int device, const DeviceMatrix& m, const float* x, std::
   LLMI_TRY_HIP(hipGetLastError());
   if (int rc = launch_gemm(nullptr, nullptr, l, s, &p)) return rc;
   if (p.kchunks > 1) {
-    const std::size_t n = rows * m.out;
-    const unsigned rblocks = static_cast<unsigned>(std::min<std::size_t>(ceil_div(n, 256), 8192));
-    gemm_reduce<<<rblocks, 256, 0, s>>>(p.part, p.kchunks, p.rows, p.out, p.bias, p.y, p.accumulate);
+    launch_reduce(p.part, p.kchunks, p.rows, p.out, p.bias, p.y, p.accumulate, s);
     LLMI_TRY_HIP(hipGetLastError());
   }
   return LLMI_OK;
