@@ -1714,8 +1714,13 @@ int DeviceGroup::launch(hipStream_t s) const {
 }
 
 // Splits of a SplitProduct: about kSplitTarget workgroups, BPS (the
-// kernel's blocks per split) one of 2, 4, 8, 16.
+// kernel's blocks per split) one of 2, 4, 8, 16, and the power of two is
+// taken below max(nblk / (kSplitTarget / tiles), nblk / kSplitMaxPerOutput):
+// the atomic adds into one cache line of y are applied one after another
+// (152 per output cost ~3 us more than plain stores on MI355X), so long rows
+// take wider splits.
 constexpr int kSplitTarget = 1024;
+constexpr int kSplitMaxPerOutput = 40;
 
 int plan_split(SplitProduct* p) {
   LLMI_REQUIRE(p->m != nullptr && p->x != nullptr && p->y != nullptr, "split product: null operand");
@@ -1729,6 +1734,8 @@ int plan_split(SplitProduct* p) {
   LLMI_REQUIRE(nblk >= 1 && ntiles >= 1, "split product: empty matrix");
   const int want = std::max(1, kSplitTarget / ntiles);
   int bps = static_cast<int>(ceil_div(static_cast<std::size_t>(nblk), static_cast<std::size_t>(want)));
+  bps = std::max(bps, static_cast<int>(ceil_div(static_cast<std::size_t>(nblk),
+                                                static_cast<std::size_t>(kSplitMaxPerOutput))));
   int unit = 1;
   if (p->prologue == kAttnCombine) {
     LLMI_REQUIRE(p->comb_hd >= 32 && p->comb_hd % kBlock == 0 && m.in % static_cast<std::size_t>(p->comb_hd) == 0,
