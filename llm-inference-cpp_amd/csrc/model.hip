@@ -928,7 +928,7 @@ __global__ void __launch_bounds__(kAttnHeads * 64) attn_part_1(const float* __re
   __shared__ float qs[kAttnHeads * hd];
   __shared__ float kt[kAttnSub * (hd + 1)];
   __shared__ float vt[kAttnSub * hd];
-  __shared__ float ps[kAttnHeads * kAttnSub];
+  __shared__ __attribute__((aligned(16))) float ps[kAttnHeads * kAttnSub];
   __shared__ float kn[hd];
   const int c = blockIdx.x, kvh = blockIdx.y;
   const int G = nh / nkv;
@@ -1026,18 +1026,32 @@ __global__ void __launch_bounds__(kAttnHeads * 64) attn_part_1(const float* __re
       mrun = mnew;
       pw[lane] = e;
       __builtin_amdgcn_wave_barrier();
-      // Column lane (+ 64): the sub-block's P.V.
+      // Column lane (+ 64): the sub-block's P.V -- a whole sub-block fully
+      // unrolled (four chains, p read four at a time by broadcast), so its
+      // LDS reads are in flight together rather than one round trip per
+      // position.
 #pragma unroll
       for (int k = 0; k < kCols; ++k) {
         const int d = lane + 64 * k;
-        float b0 = acc[k] * f, b1 = 0.0f;
-        int r = 0;
-        for (; r + 1 < n; r += 2) {
-          b0 = __builtin_fmaf(pw[r], vt[r * hd + d], b0);
-          b1 = __builtin_fmaf(pw[r + 1], vt[(r + 1) * hd + d], b1);
+        float b0 = acc[k] * f, b1 = 0.0f, b2 = 0.0f, b3 = 0.0f;
+        if (n == kAttnSub) {
+#pragma unroll
+          for (int r = 0; r < kAttnSub; r += 4) {
+            const float4 p4 = *reinterpret_cast<const float4*>(pw + r);
+            b0 = __builtin_fmaf(p4.x, vt[r * hd + d], b0);
+            b1 = __builtin_fmaf(p4.y, vt[(r + 1) * hd + d], b1);
+            b2 = __builtin_fmaf(p4.z, vt[(r + 2) * hd + d], b2);
+            b3 = __builtin_fmaf(p4.w, vt[(r + 3) * hd + d], b3);
+          }
+        } else {
+          int r = 0;
+          for (; r + 1 < n; r += 2) {
+            b0 = __builtin_fmaf(pw[r], vt[r * hd + d], b0);
+            b1 = __builtin_fmaf(pw[r + 1], vt[(r + 1) * hd + d], b1);
+          }
+          if (r < n) b0 = __builtin_fmaf(pw[r], vt[r * hd + d], b0);
         }
-        if (r < n) b0 = __builtin_fmaf(pw[r], vt[r * hd + d], b0);
-        acc[k] = b0 + b1;
+        acc[k] = (b0 + b1) + (b2 + b3);
       }
     }
   }
