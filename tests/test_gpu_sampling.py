@@ -154,6 +154,19 @@ def test_top_p_sweep_over_the_ranking(kind, n):
             assert np.array_equal(bits(got), bits(want)), (top_p, temp, top_k)
 
 
+@pytest.mark.parametrize("kind", ["ties", "normal"])
+def test_ranking_past_a_thousand_tiles_of_1024(kind):
+    """5,000,000 logits: the ranking sort's tiles grow past 1024 elements
+    (at most 4096 tiles), so each workgroup of its passes walks several
+    rounds of 256; top-p cuts inside groups of tied logits."""
+    o = O.oracle()
+    lg = logits_case(kind, 5_000_000, 17)
+    for cfg in ((1.0, 0, 0.3), (0.8, 2000, 0.99)):
+        want = o.sampling_probabilities(lg, *cfg)
+        got = H.sampling_probabilities(lg, H.Sampling(*cfg))
+        assert np.array_equal(bits(got), bits(want)), cfg
+
+
 def test_top_p_on_a_running_sum():
     """Probabilities that are exact binary fractions put top_p exactly on a
     ranked running sum (keep = 2 for top_p 0.5 over four equal logits)."""
