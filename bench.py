@@ -409,12 +409,14 @@ def prefill_flops(cfg, T):
     return 2 * T * L * per_layer + 2 * cfg["vocab_size"] * H + attn
 
 
-def decode_runs(max_steps: int | None = None, greedy_only: bool = False):
+def decode_runs(max_steps: int | None = None, greedy_only: bool = False, graphs: bool = True):
     """Full-model greedy decode on the synthetic models: prefill the prompt,
     then the configured number of greedy steps (at most max_steps, for
     profiling runs); ids are checked against the reference's (tests/golden),
     a shortened run against their prefix.  Then the sampled decode and the
-    perplexity chunk, unless greedy_only (profiling passes)."""
+    perplexity chunk, unless greedy_only (profiling passes).  graphs: the
+    tolerance-mode greedy steps replay one captured graph (off for profilers
+    that do not follow graphs)."""
     res = {}
     for key, golden, cfg, qt in DECODE_RUNS:
         with open(os.path.join(ROOT, "tests", "golden", golden + ".json")) as f:
@@ -424,6 +426,7 @@ def decode_runs(max_steps: int | None = None, greedy_only: bool = False):
         H.synchronize()
         t0 = time.perf_counter()
         m = H.synthetic_model_dev(cfg, rec["seed"], qt, rec["convention"])
+        m.set_decode_graph(graphs)
         H.synchronize()
         load_s = time.perf_counter() - t0
         prompt = synth.uniform_ids(rec["prompt_seed"], rec["n_prompt"], cfg["vocab_size"])
@@ -857,7 +860,8 @@ def main():
                     help="also run one plain 256 MiB device-to-device copy, the reference kernel for scaling "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE readings")
     ap.add_argument("--no-graphs", action="store_true",
-                    help="time the linear pass with plain launches only (for profilers that do not follow graphs)")
+                    help="plain launches only: the linear pass's graph leg and the tolerance-mode greedy decode's "
+                         "graph replay are skipped (for profilers that do not follow graphs)")
     ap.add_argument("--no-shapes", action="store_true", help="skip the per-shape table (C1, C2 shapes)")
     ap.add_argument("--decode-steps", type=int, default=None,
                     help="cap the greedy decode runs at this many steps (profiling; ids checked as a prefix)")
@@ -941,7 +945,7 @@ def main():
 
     per_shape = {} if args.no_shapes else per_shape_gpu()
     targets = {} if args.no_targets else target_shapes()
-    decode = {} if args.no_decode else decode_runs(args.decode_steps, args.greedy_only)
+    decode = {} if args.no_decode else decode_runs(args.decode_steps, args.greedy_only, not args.no_graphs)
     decode_tol = {k: r.pop("tolerance_mode") for k, r in decode.items() if "tolerance_mode" in r}
     gemm = {} if args.no_gemm else prefill_gemm()
     gguf = gguf_upload()

@@ -435,6 +435,15 @@ int llmi_hip_model_last_redraws(const llmi_hip_model* model, size_t* steps);
 enum { LLMI_DECODE_EXACT = 0, LLMI_DECODE_TOLERANCE = 1 };
 int llmi_hip_model_set_decode_mode(llmi_hip_model* model, int mode);
 
+/* Whether generate_greedy replays its tolerance-mode steps (no stop ids, at
+ * least 8 new tokens) from one captured HIP graph -- the step's positions
+ * and output slot read from device memory, one host launch per token
+ * instead of ~5 per layer -- (enable != 0, the default) or launches every
+ * kernel of every step (0; e.g. under profilers that do not follow graphs).
+ * The same kernels and results either way.  No counterpart in the
+ * reference: a launch-overhead option. */
+int llmi_hip_model_set_decode_graph(llmi_hip_model* model, int enable);
+
 #ifdef __cplusplus
 } /* extern "C" */
 #endif

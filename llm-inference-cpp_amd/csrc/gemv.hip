@@ -700,7 +700,7 @@ __global__ void __launch_bounds__(64) tsplit_gemv(const uint4* __restrict__ code
                                                   const float* __restrict__ x, const float* __restrict__ pw, int nblk,
                                                   int in, float eps, int out, const float* __restrict__ bias,
                                                   float* __restrict__ y, float* __restrict__ zero, int nzero,
-                                                  int comb_hd, int comb_nch) {
+                                                  int comb_hd, int comb_nch, const int* __restrict__ npos_dev) {
   __shared__ __attribute__((aligned(16))) float xs[BPS * kBlock];
   __shared__ float wgt[PRO == kAttnCombine ? kSplitMaxHeads * kAttnMaxChunks : 1];
   const int lane = threadIdx.x;
@@ -765,7 +765,11 @@ __global__ void __launch_bounds__(64) tsplit_gemv(const uint4* __restrict__ code
       if (u * 64 + lane < n) xs[u * 64 + lane] = xv[u];
   } else {
     // kAttnCombine: the range is whole heads h0 .. h0 + nhh - 1; lanes 16r ..
-    // 16r + 15 form the chunk weights of head hb + r.
+    // 16r + 15 form the chunk weights of head hb + r.  Every chunk slot's
+    // partials are loaded (slots past the step's chunks hold finite values
+    // -- zeros or an earlier step's -- and get weight 0), so no load waits
+    // for the chunk count, which a graph-replayed step reads from memory.
+    if (npos_dev != nullptr) comb_nch = attn_chunk_count(__builtin_amdgcn_readfirstlane(*npos_dev));
     const int hd = comb_hd, nh_all = in / hd, h0 = k0 / hd, nhh = n / hd;
     const GMEM float* ms = xg + static_cast<std::size_t>(kAttnMaxChunks) * nh_all * hd;
     const GMEM float* ls = ms + kAttnMaxChunks * nh_all;
@@ -776,14 +780,15 @@ __global__ void __launch_bounds__(64) tsplit_gemv(const uint4* __restrict__ code
       const int hh = i / hd, d = i - hh * hd;
       const GMEM float* oh = xg + static_cast<std::size_t>(h0 + min(hh, nhh - 1)) * kAttnMaxChunks * hd + d;
 #pragma unroll
-      for (int c = 0; c < kAttnMaxChunks; ++c) ov[u][c] = i < n && c < comb_nch ? oh[c * hd] : 0.0f;
+      for (int c = 0; c < kAttnMaxChunks; ++c) ov[u][c] = i < n ? oh[c * hd] : 0.0f;
     }
     for (int hb = 0; hb < nhh; hb += 4) {
       const int hh = hb + (lane >> 4), c = lane & 15;
+      const int t = (h0 + min(hh, nhh - 1)) * kAttnMaxChunks + c;
+      const float m_all = ms[t], l_all = ls[t];
       const bool live = hh < nhh && c < comb_nch;
-      const int t = (h0 + hh) * kAttnMaxChunks + c;
-      const float mv = live ? ms[t] : -__builtin_inff();
-      const float lv = live ? ls[t] : 0.0f;
+      const float mv = live ? m_all : -__builtin_inff();
+      const float lv = live ? l_all : 0.0f;
       const float mx = row_last_bcast(row_max16_f32(mv), lane);
       const float w = live ? __expf(mv - mx) : 0.0f;
       const float den = row_last_bcast(row_sum16_f32(w * lv), lane);
@@ -1754,12 +1759,12 @@ int plan_split(SplitProduct* p) {
 namespace {
 
 template <int TYPE, int PRO>
-void launch_split_bps(const SplitProduct& p, hipStream_t s, int comb_nch) {
+void launch_split_bps(const SplitProduct& p, hipStream_t s, int comb_nch, const int* npos_dev) {
   const DeviceMatrix& m = *p.m;
   const dim3 grid(static_cast<unsigned>(m.ntiles), static_cast<unsigned>(p.splits));
 #define LLMI_SPLIT_ARGS                                                                                            \
   reinterpret_cast<const uint4*>(m.codes), m.scales, p.x, p.pw, static_cast<int>(m.nblk), static_cast<int>(m.in), \
-      p.eps, static_cast<int>(m.out), p.bias, p.y, p.zero, p.nzero, p.comb_hd, comb_nch
+      p.eps, static_cast<int>(m.out), p.bias, p.y, p.zero, p.nzero, p.comb_hd, comb_nch, npos_dev
   switch (p.bps) {
     case 2: tsplit_gemv<TYPE, PRO, 2><<<grid, 64, 0, s>>>(LLMI_SPLIT_ARGS); break;
     case 4: tsplit_gemv<TYPE, PRO, 4><<<grid, 64, 0, s>>>(LLMI_SPLIT_ARGS); break;
@@ -1770,24 +1775,24 @@ void launch_split_bps(const SplitProduct& p, hipStream_t s, int comb_nch) {
 }
 
 template <int TYPE>
-void launch_split_type(const SplitProduct& p, hipStream_t s, int comb_nch) {
+void launch_split_type(const SplitProduct& p, hipStream_t s, int comb_nch, const int* npos_dev) {
   switch (p.prologue) {
-    case kRmsNorm: launch_split_bps<TYPE, kRmsNorm>(p, s, comb_nch); break;
-    case kSiluUp: launch_split_bps<TYPE, kSiluUp>(p, s, comb_nch); break;
-    case kAttnCombine: launch_split_bps<TYPE, kAttnCombine>(p, s, comb_nch); break;
-    default: launch_split_bps<TYPE, kPlain>(p, s, comb_nch); break;
+    case kRmsNorm: launch_split_bps<TYPE, kRmsNorm>(p, s, comb_nch, nullptr); break;
+    case kSiluUp: launch_split_bps<TYPE, kSiluUp>(p, s, comb_nch, nullptr); break;
+    case kAttnCombine: launch_split_bps<TYPE, kAttnCombine>(p, s, comb_nch, npos_dev); break;
+    default: launch_split_bps<TYPE, kPlain>(p, s, comb_nch, nullptr); break;
   }
 }
 
 }  // namespace
 
-int launch_split(const SplitProduct& p, hipStream_t s, int comb_nch) {
+int launch_split(const SplitProduct& p, hipStream_t s, int comb_nch, const int* npos_dev) {
   LLMI_REQUIRE(p.m != nullptr && p.splits >= 1 && (p.bps == 2 || p.bps == 4 || p.bps == 8 || p.bps == 16),
                "split product: not planned");
-  LLMI_REQUIRE(p.prologue != kAttnCombine || (comb_nch >= 1 && comb_nch <= kAttnMaxChunks),
+  LLMI_REQUIRE(p.prologue != kAttnCombine || npos_dev != nullptr || (comb_nch >= 1 && comb_nch <= kAttnMaxChunks),
                "split product: attention chunks out of range");
-  if (p.m->type == LLMI_TYPE_Q8_0) launch_split_type<LLMI_TYPE_Q8_0>(p, s, comb_nch);
-  else launch_split_type<LLMI_TYPE_Q4_0>(p, s, comb_nch);
+  if (p.m->type == LLMI_TYPE_Q8_0) launch_split_type<LLMI_TYPE_Q8_0>(p, s, comb_nch, npos_dev);
+  else launch_split_type<LLMI_TYPE_Q4_0>(p, s, comb_nch, npos_dev);
   LLMI_TRY_HIP(hipGetLastError());
   return LLMI_OK;
 }

@@ -920,7 +920,8 @@ __global__ void __launch_bounds__(kAttnHeads * 64) attn_part_1(const float* __re
                                                                float* __restrict__ vc, const float* __restrict__ cos_t,
                                                                const float* __restrict__ sin_t,
                                                                float* __restrict__ part, int nh, int nkv, int cap,
-                                                               int npos, int chunk, float scale) {
+                                                               int npos, int chunk, float scale,
+                                                               const int* __restrict__ npos_dev) {
   constexpr int hd = 16 * NCH, half = hd / 2;
   constexpr int kT = kAttnHeads * 64;
   constexpr int kLd = kAttnSub * hd / 4 / kT;  // float4 of K (and of V) per thread per sub-block
@@ -930,6 +931,13 @@ __global__ void __launch_bounds__(kAttnHeads * 64) attn_part_1(const float* __re
   __shared__ float vt[kAttnSub * hd];
   __shared__ __attribute__((aligned(16))) float ps[kAttnHeads * kAttnSub];
   __shared__ float kn[hd];
+  // A step replayed from a graph takes its positions from device memory and
+  // runs kAttnMaxChunks chunks' workgroups, those past the last exiting.
+  if (npos_dev != nullptr) {
+    npos = __builtin_amdgcn_readfirstlane(*npos_dev);
+    chunk = attn_chunk_len(npos);
+  }
+  if (static_cast<int>(blockIdx.x) * chunk >= npos) return;
   const int c = blockIdx.x, kvh = blockIdx.y;
   const int G = nh / nkv;
   const int g0 = blockIdx.z * kAttnHeads;
@@ -1069,12 +1077,7 @@ __global__ void __launch_bounds__(kAttnHeads * 64) attn_part_1(const float* __re
   }
 }
 
-// Positions per chunk of the tolerance-mode attention for npos positions:
-// a multiple of kAttnSub giving at most kAttnMaxChunks chunks.
-int attn_chunk(int npos) {
-  const int subs = (npos + kAttnSub - 1) / kAttnSub;
-  return kAttnSub * ((subs + kAttnMaxChunks - 1) / kAttnMaxChunks);
-}
+static_assert(kAttnSub == kAttnChunkUnit, "chunks are whole sub-blocks");
 
 // The tolerance-mode decode path applies to head_dim 64 or 128 and at most
 // 16 query heads per KV head (any number of positions).
@@ -1083,19 +1086,23 @@ bool tol_attention_fits(int nh, int nkv, int hd) {
   return (hd == 64 || hd == 128) && G >= 1 && G <= 16 && nh % nkv == 0;
 }
 
-// Returns the number of chunks written.
+// Returns the number of chunks written.  npos_dev (may be null): the
+// positions in device memory instead (a step replayed from a graph: the
+// grid is then kAttnMaxChunks chunks wide and the return value unused).
 int launch_tol_attention(const float* q, const float* knew, const float* vnew, float* kc, float* vc,
                          const float* cos_t, const float* sin_t, float* part, int nh, int nkv, int hd, int cap,
-                         int npos, float scale, hipStream_t s) {
-  const int chunk = attn_chunk(npos);
+                         int npos, float scale, hipStream_t s, const int* npos_dev = nullptr) {
+  const int chunk = attn_chunk_len(npos);
   const int nch = (npos + chunk - 1) / chunk;
   const int G = nh / nkv;
-  const dim3 grid(static_cast<unsigned>(nch), static_cast<unsigned>(nkv),
+  const dim3 grid(static_cast<unsigned>(npos_dev != nullptr ? kAttnMaxChunks : nch), static_cast<unsigned>(nkv),
                   static_cast<unsigned>((G + kAttnHeads - 1) / kAttnHeads));
   if (hd == 64)
-    attn_part_1<4><<<grid, kAttnHeads * 64, 0, s>>>(q, knew, vnew, kc, vc, cos_t, sin_t, part, nh, nkv, cap, npos, chunk, scale);
+    attn_part_1<4><<<grid, kAttnHeads * 64, 0, s>>>(q, knew, vnew, kc, vc, cos_t, sin_t, part, nh, nkv, cap, npos, chunk,
+                                                    scale, npos_dev);
   else
-    attn_part_1<8><<<grid, kAttnHeads * 64, 0, s>>>(q, knew, vnew, kc, vc, cos_t, sin_t, part, nh, nkv, cap, npos, chunk, scale);
+    attn_part_1<8><<<grid, kAttnHeads * 64, 0, s>>>(q, knew, vnew, kc, vc, cos_t, sin_t, part, nh, nkv, cap, npos, chunk,
+                                                    scale, npos_dev);
   return nch;
 }
 
@@ -1215,7 +1222,8 @@ constexpr int kArgmaxBlocks = 128;
 __global__ void __launch_bounds__(kThreads) argmax_many(const float* __restrict__ x, int n, float* __restrict__ part_v,
                                                         int* __restrict__ part_i, unsigned* __restrict__ counter,
                                                         std::int32_t* __restrict__ out,
-                                                        std::int32_t* __restrict__ also) {
+                                                        std::int32_t* __restrict__ also,
+                                                        const int* __restrict__ also_idx) {
   __shared__ float bv[kThreads];
   __shared__ int bi[kThreads];
   __shared__ bool last;
@@ -1260,9 +1268,21 @@ __global__ void __launch_bounds__(kThreads) argmax_many(const float* __restrict_
   if (threadIdx.x == 0) {
     const int idx = r.i < 0 ? 0 : r.i;
     *out = idx;
-    if (also != nullptr) *also = idx;
+    // also_idx (may be null): the slot of `also` in device memory (a step
+    // replayed from a graph).
+    if (also != nullptr) also[also_idx != nullptr ? *also_idx : 0] = idx;
     __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
+}
+
+// The state of a graph-replayed tolerance step: st[0] = the step's positions
+// (the cache length after it), st[1] = the generated token's slot.  Set
+// before the first replay; advanced by the last kernel of each replay.
+__global__ void step_state_set(int* st, int npos, int slot) {
+  if (threadIdx.x < 2) st[threadIdx.x] = threadIdx.x == 0 ? npos : slot;
+}
+__global__ void step_state_advance(int* st) {
+  if (threadIdx.x < 2) st[threadIdx.x] += 1;
 }
 
 // Standalone glue kernels (the device counterparts of kernels.hpp:13-32).
@@ -1367,6 +1387,7 @@ struct Workspace {
   float* am_v = nullptr;         // argmax partials and completion counter
   int* am_i = nullptr;
   unsigned* am_count = nullptr;
+  int* step_state = nullptr;     // a graph-replayed step's positions and output slot (step_advance)
 };
 
 }  // namespace llmi_hip
@@ -1394,6 +1415,7 @@ struct llmi_hip_model {
   int decode_mode = LLMI_DECODE_EXACT;  // llmi_hip_model_set_decode_mode
   bool tol_ready = false;               // build_decode made the tolerance-mode step
   bool qkv_clear = false;               // the last queued step left dec.q|k|v at zero (split step)
+  bool decode_graph = true;             // llmi_hip_model_set_decode_graph
   std::size_t last_redraws = 0;  // generate_sampled: queued draws redrawn step by step
 };
 
@@ -1547,6 +1569,10 @@ int build_decode(llmi_hip_model* m) {
   if (int rc = get(&d.g, 2 * m->F)) return rc;
   d.u = d.g + m->F;
   if (int rc = get(&d.part, static_cast<std::size_t>(kAttnMaxChunks) * m->c.num_heads * (m->hd + 2))) return rc;
+  // The o_proj combine reads every chunk slot (unused ones with weight 0):
+  // they start as zeros, never as uninitialised bits.
+  LLMI_TRY_HIP(hipMemsetAsync(d.part, 0, static_cast<std::size_t>(kAttnMaxChunks) * m->c.num_heads * (m->hd + 2) *
+                                             sizeof(float), library_stream()));
   const float eps = static_cast<float>(m->c.rms_norm_eps);
   for (DeviceLayer& l : m->layers) {
     const GroupEntry qkv[3] = {{&l.wq, d.x, l.bq, d.q, 1, false, kRmsNorm, l.attn_norm, eps},
@@ -1728,7 +1754,7 @@ void free_workspace(Workspace& w) {
                   static_cast<void*>(w.gen), static_cast<void*>(w.slog), static_cast<void*>(w.nll),
                   static_cast<void*>(w.am_v),
                   static_cast<void*>(w.am_i),
-                  static_cast<void*>(w.am_count)})
+                  static_cast<void*>(w.am_count), static_cast<void*>(w.step_state)})
     if (p != nullptr) (void)hipFree(p);
   w = Workspace{};
 }
@@ -1757,6 +1783,7 @@ int ensure_workspace(llmi_hip_model* m, std::size_t T) {
   if (rc == LLMI_OK) rc = get(&w.am_v, kArgmaxBlocks, 4);
   if (rc == LLMI_OK) rc = get(&w.am_i, kArgmaxBlocks, 4);
   if (rc == LLMI_OK) rc = get(&w.am_count, 1, 4);
+  if (rc == LLMI_OK) rc = get(&w.step_state, 2, 4);
   if (rc == LLMI_OK && hipMemsetAsync(w.am_count, 0, sizeof(unsigned), library_stream()) != hipSuccess)
     rc = fail(LLMI_ERR_HIP, "workspace: memset");
   if (rc != LLMI_OK) {
@@ -1773,7 +1800,11 @@ int ensure_workspace(llmi_hip_model* m, std::size_t T) {
 // tolerance: llmi_hip_model_set_decode_mode's tolerance-mode step (needs
 // tol_ready): the attention over position chunks, merged in the o_proj
 // product's staging, and every matmul split over K (SplitProduct).
-int decode_step(llmi_hip_model* m, llmi_hip_cache* cache, hipStream_t s, bool tolerance = false) {
+// npos_dev (tolerance mode only; may be null): the step's positions in
+// device memory, for a step captured once and replayed from a graph; the
+// caller then advances cache->len itself.
+int decode_step(llmi_hip_model* m, llmi_hip_cache* cache, hipStream_t s, bool tolerance = false,
+                const int* npos_dev = nullptr) {
   const auto& c = m->c;
   Workspace& w = m->ws;
   DecodeBuffers& d = m->dec;
@@ -1798,8 +1829,8 @@ int decode_step(llmi_hip_model* m, llmi_hip_cache* cache, hipStream_t s, bool to
       if (int rc = launch_split(l.s_qkv, s)) return rc;
       const int nch = launch_tol_attention(d.q, d.k, d.v, cache->k + li * per_layer, cache->v + li * per_layer,
                                            m->cos_t, m->sin_t, d.part, nh, nkv, hd, static_cast<int>(cache->cap),
-                                           static_cast<int>(pos + 1), scale, s);
-      if (int rc = launch_split(l.s_o, s, nch)) return rc;
+                                           static_cast<int>(pos + 1), scale, s, npos_dev);
+      if (int rc = launch_split(l.s_o, s, nch, npos_dev)) return rc;
       if (int rc = launch_split(l.s_gu, s)) return rc;
       if (int rc = launch_split(l.s_dn, s)) return rc;
       continue;
@@ -1817,7 +1848,7 @@ int decode_step(llmi_hip_model* m, llmi_hip_cache* cache, hipStream_t s, bool to
   if (int rc = launch_matmul(head, d.h, 1, nullptr, w.logits, s)) return rc;
   LLMI_TRY_HIP(hipGetLastError());
   m->qkv_clear = split;
-  cache->len = pos + 1;
+  if (npos_dev == nullptr) cache->len = pos + 1;
   return LLMI_OK;
 }
 
@@ -2157,6 +2188,71 @@ int llmi_hip_model_forward_cached(llmi_hip_model* m, llmi_hip_cache* cache, cons
 // runs on the device and feeds the next step's embedding gather directly.
 // Without stop ids nothing waits for the host between steps: the ids collect
 // in device memory and are copied back once.
+// The tolerance-mode greedy loop from a graph (generate_greedy).  Capture
+// (before the prompt's prefill, so that its host time is not in the decode
+// span): argmax of the logits into ids and gen[state[1]], the decode step
+// with its positions from state[0], the state's advance.  A capture the
+// runtime refuses leaves exec null (the eager loop runs).  Replay (after the
+// prefill): the state set, the graph once per token but the last, the last
+// argmax; the caller synchronizes before the destructor frees the graph.
+constexpr std::size_t kGraphMinSteps = 8;
+struct GreedyGraph {
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+  GreedyGraph() = default;
+  GreedyGraph(const GreedyGraph&) = delete;
+  GreedyGraph& operator=(const GreedyGraph&) = delete;
+  ~GreedyGraph() {
+    if (exec != nullptr) (void)hipGraphExecDestroy(exec);
+    if (graph != nullptr) (void)hipGraphDestroy(graph);
+  }
+};
+void greedy_graph_capture(llmi_hip_model* m, llmi_hip_cache* cache, hipStream_t s, GreedyGraph* g) {
+  Workspace& w = m->ws;
+  const int V = static_cast<int>(m->V);
+  if (hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal) != hipSuccess) {
+    (void)hipGetLastError();
+    return;
+  }
+  const bool clear = m->qkv_clear;
+  m->qkv_clear = true;  // the replays' q|k|v are cleared by the step before (or before the first)
+  argmax_many<<<kArgmaxBlocks, kThreads, 0, s>>>(w.logits, V, w.am_v, w.am_i, w.am_count, w.ids, w.gen,
+                                                 w.step_state + 1);
+  bool ok = hipGetLastError() == hipSuccess;
+  if (ok) ok = decode_step(m, cache, s, true, w.step_state) == LLMI_OK;
+  if (ok) {
+    step_state_advance<<<1, 64, 0, s>>>(w.step_state);
+    ok = hipGetLastError() == hipSuccess;
+  }
+  m->qkv_clear = clear;
+  const hipError_t ended = hipStreamEndCapture(s, &g->graph);
+  if (!ok || ended != hipSuccess || g->graph == nullptr ||
+      hipGraphInstantiate(&g->exec, g->graph, nullptr, nullptr, 0) != hipSuccess) {
+    (void)hipGetLastError();
+    if (g->exec != nullptr) (void)hipGraphExecDestroy(g->exec);
+    g->exec = nullptr;
+  }
+}
+int greedy_graph_run(llmi_hip_model* m, llmi_hip_cache* cache, std::size_t max_new, hipStream_t s,
+                     const GreedyGraph& g) {
+  Workspace& w = m->ws;
+  DecodeBuffers& d = m->dec;
+  const int V = static_cast<int>(m->V);
+  if (cache->len + max_new > cache->cap || cache->len + max_new > m->table_len)
+    return fail(LLMI_ERR_STATE, "forward_cached: cache is full");
+  if (!m->qkv_clear)
+    zero_floats<<<blocks_for(m->Q + 2 * m->KV), kThreads, 0, s>>>(d.q, static_cast<int>(m->Q + 2 * m->KV));
+  step_state_set<<<1, 64, 0, s>>>(w.step_state, static_cast<int>(cache->len + 1), 0);
+  LLMI_TRY_HIP(hipGetLastError());
+  for (std::size_t k = 0; k + 1 < max_new; ++k) LLMI_TRY_HIP(hipGraphLaunch(g.exec, s));
+  argmax_many<<<kArgmaxBlocks, kThreads, 0, s>>>(w.logits, V, w.am_v, w.am_i, w.am_count, w.ids, w.gen,
+                                                 w.step_state + 1);
+  LLMI_TRY_HIP(hipGetLastError());
+  cache->len += max_new - 1;
+  m->qkv_clear = true;
+  return LLMI_OK;
+}
+
 int llmi_hip_model_generate_greedy(llmi_hip_model* m, const int32_t* prompt, size_t n, size_t max_new,
                                    const int32_t* stop_ids, size_t n_stop, int32_t* ids, size_t* n_ids) {
   LLMI_REQUIRE_INIT();
@@ -2185,14 +2281,26 @@ int llmi_hip_model_generate_greedy(llmi_hip_model* m, const int32_t* prompt, siz
         if (e[i] != nullptr) (void)hipEventDestroy(e[i]);
     }
   } ev_guard{ev};
+  // Tolerance-mode steps (no stop ids) replay one captured graph: the host
+  // then enqueues one launch per token instead of ~5 per layer.  Anything
+  // the capture does not take leaves the eager loop below.
+  GreedyGraph graph;
+  if (m->decode_graph && m->decode_mode == LLMI_DECODE_TOLERANCE && m->tol_ready && n_stop == 0 &&
+      max_new >= kGraphMinSteps)
+    greedy_graph_capture(m, cache, s, &graph);
   LLMI_TRY_HIP(hipMemcpyAsync(w.ids, prompt, n * sizeof(std::int32_t), hipMemcpyHostToDevice, s));
   LLMI_TRY_HIP(hipEventRecord(ev[0], s));
   if (int rc = forward_device(m, cache, n, false, s)) return rc;
   LLMI_TRY_HIP(hipEventRecord(ev[1], s));
   const int V = static_cast<int>(m->V);
   std::size_t produced = 0;
-  for (std::size_t step = 0; step < max_new; ++step) {
-    argmax_many<<<kArgmaxBlocks, kThreads, 0, s>>>(w.logits, V, w.am_v, w.am_i, w.am_count, w.ids, w.gen + step);
+  if (graph.exec != nullptr) {
+    if (int rc = greedy_graph_run(m, cache, max_new, s, graph)) return rc;
+    produced = max_new;
+  }
+  for (std::size_t step = produced; step < max_new; ++step) {
+    argmax_many<<<kArgmaxBlocks, kThreads, 0, s>>>(w.logits, V, w.am_v, w.am_i, w.am_count, w.ids, w.gen + step,
+                                                   nullptr);
     LLMI_TRY_HIP(hipGetLastError());
     produced = step + 1;
     if (n_stop > 0) {
@@ -2398,6 +2506,12 @@ int llmi_hip_model_set_decode_mode(llmi_hip_model* m, int mode) {
   LLMI_REQUIRE(m != nullptr, "set_decode_mode: null model");
   LLMI_REQUIRE(mode == LLMI_DECODE_EXACT || mode == LLMI_DECODE_TOLERANCE, "set_decode_mode: unknown mode");
   m->decode_mode = mode;
+  return LLMI_OK;
+}
+
+int llmi_hip_model_set_decode_graph(llmi_hip_model* m, int enable) {
+  LLMI_REQUIRE(m != nullptr, "set_decode_graph: null model");
+  m->decode_graph = enable != 0;
   return LLMI_OK;
 }
 

@@ -95,6 +95,7 @@ SIGNATURES = {
     "llmi_hip_model_last_timing": (_i, [_vp, C.POINTER(_d), C.POINTER(_d)]),
     "llmi_hip_model_last_redraws": (_i, [_vp, C.POINTER(_sz)]),
     "llmi_hip_model_set_decode_mode": (_i, [_vp, _i]),
+    "llmi_hip_model_set_decode_graph": (_i, [_vp, _i]),
     "llmi_hip_sample": (_i, [_vp, _sz, _vp, _d, C.POINTER(C.c_int32)]),
     "llmi_hip_sample_dev": (_i, [_vp, _sz, _vp, _d, C.POINTER(C.c_int32), _vp]),
     "llmi_hip_sampling_probabilities": (_i, [_vp, _sz, _vp, _vp]),
@@ -515,6 +516,11 @@ class Model:
         """DECODE_EXACT (bit-identical, the default) or DECODE_TOLERANCE
         (position-chunked attention merged in o_proj; llmi_hip.h)."""
         check(self.lib.llmi_hip_model_set_decode_mode(self.h, int(mode)))
+
+    def set_decode_graph(self, enable: bool) -> None:
+        """Whether generate_greedy replays tolerance-mode steps from one
+        captured graph (the default) or launches every kernel (llmi_hip.h)."""
+        check(self.lib.llmi_hip_model_set_decode_graph(self.h, 1 if enable else 0))
 
     def free(self) -> None:
         if self.h:

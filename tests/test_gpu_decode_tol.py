@@ -160,3 +160,32 @@ def test_full_size_tolerance_decode(name):
     ct.free()
     m.free()
     print(f"{name}: worst relative logit error over {n - 1} steps {worst:.3e}")
+
+
+def test_greedy_from_a_graph_equals_the_eager_loop():
+    """generate_greedy in tolerance mode captures one step (argmax, the step
+    with its positions read from device memory, the positions' advance) and
+    replays it once per token.  With the graph and without, twice in a row
+    with eager single steps between the runs, around the 8-step threshold
+    below which it stays eager, and with stop ids (eager), the greedy ids
+    are the reference's."""
+    with open(os.path.join(GOLDEN, "c3_smollm2_q8.json")) as f:
+        rec = json.load(f)
+    cfg = rec["cfg"]
+    m = H.synthetic_model_dev(cfg, rec["seed"], rec["type"], rec["convention"])
+    prompt = synth.uniform_ids(rec["prompt_seed"], rec["n_prompt"], cfg["vocab_size"])
+    want = rec["ids"]
+    m.set_decode_mode(H.DECODE_TOLERANCE)
+    for graph in (True, False, True, True):
+        m.set_decode_graph(graph)
+        assert list(m.generate_greedy(prompt, rec["n_steps"])) == want, graph
+        c = m.new_cache(rec["n_prompt"] + 2)
+        m.forward_cached(c, prompt)
+        m.forward_cached(c, [want[0]])
+        c.free()
+    for n in (7, 8, 9, 40):
+        assert list(m.generate_greedy(prompt, n)) == want[:n], n
+    stop = want[-1]  # first reached late in the run
+    assert list(m.generate_greedy(prompt, rec["n_steps"], stop_ids=[stop])) == want[:want.index(stop) + 1]
+    m.free()
+
