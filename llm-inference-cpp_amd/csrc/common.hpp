@@ -85,15 +85,11 @@ enum { kPlain = 0, kRmsNorm = 1, kSiluUp = 2, kAttnCombine = 3 };
 // l[h][c] (its sum of exp(score - m)).
 constexpr int kAttnMaxChunks = 16;
 constexpr int kAttnChunkUnit = 64;  // chunks are whole multiples of this many positions
-// Positions per chunk for npos positions (the fewest multiples of
-// kAttnChunkUnit that give at most kAttnMaxChunks chunks), and the chunks.
+// Positions per chunk for npos positions: the fewest multiples of
+// kAttnChunkUnit that give at most kAttnMaxChunks chunks.
 __host__ __device__ inline int attn_chunk_len(int npos) {
   const int units = (npos + kAttnChunkUnit - 1) / kAttnChunkUnit;
   return kAttnChunkUnit * ((units + kAttnMaxChunks - 1) / kAttnMaxChunks);
-}
-__host__ __device__ inline int attn_chunk_count(int npos) {
-  const int c = attn_chunk_len(npos);
-  return (npos + c - 1) / c;
 }
 
 // One product of a grouped launch (qgemv_group), as the kernel reads it.
@@ -318,8 +314,8 @@ struct SplitProduct {
 };
 int plan_split(SplitProduct* p);
 // comb_nch: kAttnCombine's chunk count; npos_dev (may be null): the
-// positions of the step in device memory, from which the kernel takes the
-// chunk count instead (a step replayed from a graph).
+// positions of the step in device memory (a step replayed from a graph),
+// comb_nch then being the chunk length and the count taken on the device.
 int launch_split(const SplitProduct& p, hipStream_t s, int comb_nch = 0, const int* npos_dev = nullptr);
 // Frees the sampling workspace (llmi_hip_shutdown; the stream is idle).
 void release_sampling_workspace();

@@ -769,7 +769,9 @@ __global__ void __launch_bounds__(64) tsplit_gemv(const uint4* __restrict__ code
     // partials are loaded (slots past the step's chunks hold finite values
     // -- zeros or an earlier step's -- and get weight 0), so no load waits
     // for the chunk count, which a graph-replayed step reads from memory.
-    if (npos_dev != nullptr) comb_nch = attn_chunk_count(__builtin_amdgcn_readfirstlane(*npos_dev));
+    // From a graph, comb_nch carries the run's chunk length and the count
+    // follows from the positions.
+    if (npos_dev != nullptr) comb_nch = (__builtin_amdgcn_readfirstlane(*npos_dev) + comb_nch - 1) / comb_nch;
     const int hd = comb_hd, nh_all = in / hd, h0 = k0 / hd, nhh = n / hd;
     const GMEM float* ms = xg + static_cast<std::size_t>(kAttnMaxChunks) * nh_all * hd;
     const GMEM float* ls = ms + kAttnMaxChunks * nh_all;

@@ -913,7 +913,15 @@ void launch_decode_attention(const float* q, const float* knew, const float* vne
 constexpr int kAttnSub = 64;    // positions per staged sub-block = lanes of a wavefront
 constexpr int kAttnHeads = 4;   // query heads (wavefronts) per workgroup
 
-template <int NCH>
+// GRAPH (a step replayed from a graph): the positions come from device
+// memory (npos_dev), the chunk length is the run's (fixed when the graph
+// was captured), RoPE's cos / sin row from rope_dev (the state kernels keep
+// it at the step's position), and kAttnMaxChunks chunks' workgroups run,
+// those past the last exiting.  Every load that starts the workgroup is
+// then independent of the positions: the chunk's first K / V rows (clamped
+// into the cache; rows past the last position are zeroed when staged), the
+// new v, q and the cos / sin row.
+template <int NCH, bool GRAPH>
 __global__ void __launch_bounds__(kAttnHeads * 64) attn_part_1(const float* __restrict__ q,
                                                                const float* __restrict__ knew,
                                                                const float* __restrict__ vnew, float* __restrict__ kc,
@@ -921,7 +929,8 @@ __global__ void __launch_bounds__(kAttnHeads * 64) attn_part_1(const float* __re
                                                                const float* __restrict__ sin_t,
                                                                float* __restrict__ part, int nh, int nkv, int cap,
                                                                int npos, int chunk, float scale,
-                                                               const int* __restrict__ npos_dev) {
+                                                               const int* __restrict__ npos_dev,
+                                                               const float* __restrict__ rope_dev) {
   constexpr int hd = 16 * NCH, half = hd / 2;
   constexpr int kT = kAttnHeads * 64;
   constexpr int kLd = kAttnSub * hd / 4 / kT;  // float4 of K (and of V) per thread per sub-block
@@ -931,37 +940,41 @@ __global__ void __launch_bounds__(kAttnHeads * 64) attn_part_1(const float* __re
   __shared__ float vt[kAttnSub * hd];
   __shared__ __attribute__((aligned(16))) float ps[kAttnHeads * kAttnSub];
   __shared__ float kn[hd];
-  // A step replayed from a graph takes its positions from device memory and
-  // runs kAttnMaxChunks chunks' workgroups, those past the last exiting.
-  if (npos_dev != nullptr) {
-    npos = __builtin_amdgcn_readfirstlane(*npos_dev);
-    chunk = attn_chunk_len(npos);
+  if constexpr (!GRAPH) {
+    if (static_cast<int>(blockIdx.x) * chunk >= npos) return;
   }
-  if (static_cast<int>(blockIdx.x) * chunk >= npos) return;
   const int c = blockIdx.x, kvh = blockIdx.y;
   const int G = nh / nkv;
   const int g0 = blockIdx.z * kAttnHeads;
   const int ng = min(kAttnHeads, G - g0);
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int pos = npos - 1;
-  const int s_begin = c * chunk, s_end = min(npos, s_begin + chunk);
+  const int s_begin = c * chunk;
   const float* kh = kc + static_cast<std::size_t>(kvh) * cap * hd;
   const float* vh = vc + static_cast<std::size_t>(kvh) * cap * hd;
   const float* vn = vnew + static_cast<std::size_t>(kvh) * hd;
 
   // Element e of a sub-block: row e / (hd / 4), columns 4 * (e % (hd / 4)) ..
-  float4 kr[kLd], vr[kLd];
+  // (GRAPH: every row loaded, clamped into the cache, and the rows at or
+  // past the newest position replaced when staged.)
+  float4 kr[kLd], vr[kLd], vnr[kLd];
+  int s_end = GRAPH ? 0 : min(npos, s_begin + chunk), pos = npos - 1;
   const auto load_sub = [&](int sb) {
 #pragma unroll
     for (int u = 0; u < kLd; ++u) {
       const int e = u * kT + tid;
       const int r = e / (hd / 4), c4 = 4 * (e - r * (hd / 4));
       const int sp = sb + r;
-      const bool cached = sp < s_end && sp != pos;
-      kr[u] = cached ? *reinterpret_cast<const float4*>(kh + static_cast<std::size_t>(sp) * hd + c4)
-                     : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-      vr[u] = cached ? *reinterpret_cast<const float4*>(vh + static_cast<std::size_t>(sp) * hd + c4)
-                     : sp == pos ? *reinterpret_cast<const float4*>(vn + c4) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      if constexpr (GRAPH) {
+        const std::size_t row = static_cast<std::size_t>(min(sp, cap - 1)) * hd + c4;
+        kr[u] = *reinterpret_cast<const float4*>(kh + row);
+        vr[u] = *reinterpret_cast<const float4*>(vh + row);
+      } else {
+        const bool cached = sp < s_end && sp != pos;
+        kr[u] = cached ? *reinterpret_cast<const float4*>(kh + static_cast<std::size_t>(sp) * hd + c4)
+                       : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        vr[u] = cached ? *reinterpret_cast<const float4*>(vh + static_cast<std::size_t>(sp) * hd + c4)
+                       : sp == pos ? *reinterpret_cast<const float4*>(vn + c4) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      }
     }
   };
   const auto store_sub = [&](int sb) {
@@ -969,20 +982,36 @@ __global__ void __launch_bounds__(kAttnHeads * 64) attn_part_1(const float* __re
     for (int u = 0; u < kLd; ++u) {
       const int e = u * kT + tid;
       const int r = e / (hd / 4), c4 = 4 * (e - r * (hd / 4));
-      float4 kv = kr[u];
+      float4 kv = kr[u], vv = vr[u];
       if (sb + r == pos) kv = make_float4(kn[c4], kn[c4 + 1], kn[c4 + 2], kn[c4 + 3]);
+      if constexpr (GRAPH) {
+        const float4 z = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (sb + r == pos) vv = vnr[u];
+        else if (sb + r >= s_end) kv = vv = z;
+      }
       float* kd = kt + r * (hd + 1) + c4;
       kd[0] = kv.x;
       kd[1] = kv.y;
       kd[2] = kv.z;
       kd[3] = kv.w;
-      *reinterpret_cast<float4*>(vt + r * hd + c4) = vr[u];
+      *reinterpret_cast<float4*>(vt + r * hd + c4) = vv;
     }
   };
   load_sub(s_begin);
+  if constexpr (GRAPH) {
+#pragma unroll
+    for (int u = 0; u < kLd; ++u) {
+      const int e = u * kT + tid;
+      vnr[u] = *reinterpret_cast<const float4*>(vn + 4 * (e % (hd / 4)));
+    }
+    npos = __builtin_amdgcn_readfirstlane(*npos_dev);
+    pos = npos - 1;
+    s_end = min(npos, s_begin + chunk);
+    if (s_begin >= npos) return;  // a chunk past the last (after its loads were issued)
+  }
 
-  const float* cr = cos_t + static_cast<std::size_t>(pos) * half;
-  const float* sr = sin_t + static_cast<std::size_t>(pos) * half;
+  const float* cr = GRAPH ? rope_dev : cos_t + static_cast<std::size_t>(pos) * half;
+  const float* sr = GRAPH ? rope_dev + half : sin_t + static_cast<std::size_t>(pos) * half;
   for (int e = tid; e < ng * half; e += kT) {
     const int g = e / half, i = e - g * half;
     const float* qh = q + static_cast<std::size_t>(kvh * G + g0 + g) * hd;
@@ -1086,23 +1115,34 @@ bool tol_attention_fits(int nh, int nkv, int hd) {
   return (hd == 64 || hd == 128) && G >= 1 && G <= 16 && nh % nkv == 0;
 }
 
-// Returns the number of chunks written.  npos_dev (may be null): the
-// positions in device memory instead (a step replayed from a graph: the
-// grid is then kAttnMaxChunks chunks wide and the return value unused).
+// Returns the number of chunks written.  g (may be null): a step replayed
+// from a graph (GraphStep: positions in device memory, the run's chunk
+// length, the cos / sin row; the grid is kAttnMaxChunks chunks wide and
+// the return value unused).
+struct GraphStep {
+  const int* npos_dev;
+  const float* rope_dev;
+  int chunk;
+};
 int launch_tol_attention(const float* q, const float* knew, const float* vnew, float* kc, float* vc,
                          const float* cos_t, const float* sin_t, float* part, int nh, int nkv, int hd, int cap,
-                         int npos, float scale, hipStream_t s, const int* npos_dev = nullptr) {
-  const int chunk = attn_chunk_len(npos);
+                         int npos, float scale, hipStream_t s, const GraphStep* g = nullptr) {
+  const int chunk = g != nullptr ? g->chunk : attn_chunk_len(npos);
   const int nch = (npos + chunk - 1) / chunk;
   const int G = nh / nkv;
-  const dim3 grid(static_cast<unsigned>(npos_dev != nullptr ? kAttnMaxChunks : nch), static_cast<unsigned>(nkv),
+  const dim3 grid(static_cast<unsigned>(g != nullptr ? kAttnMaxChunks : nch), static_cast<unsigned>(nkv),
                   static_cast<unsigned>((G + kAttnHeads - 1) / kAttnHeads));
-  if (hd == 64)
-    attn_part_1<4><<<grid, kAttnHeads * 64, 0, s>>>(q, knew, vnew, kc, vc, cos_t, sin_t, part, nh, nkv, cap, npos, chunk,
-                                                    scale, npos_dev);
-  else
-    attn_part_1<8><<<grid, kAttnHeads * 64, 0, s>>>(q, knew, vnew, kc, vc, cos_t, sin_t, part, nh, nkv, cap, npos, chunk,
-                                                    scale, npos_dev);
+  const int* nd = g != nullptr ? g->npos_dev : nullptr;
+  const float* rd = g != nullptr ? g->rope_dev : nullptr;
+#define LLMI_ATTN_ARGS q, knew, vnew, kc, vc, cos_t, sin_t, part, nh, nkv, cap, npos, chunk, scale, nd, rd
+  if (g != nullptr) {
+    if (hd == 64) attn_part_1<4, true><<<grid, kAttnHeads * 64, 0, s>>>(LLMI_ATTN_ARGS);
+    else attn_part_1<8, true><<<grid, kAttnHeads * 64, 0, s>>>(LLMI_ATTN_ARGS);
+  } else {
+    if (hd == 64) attn_part_1<4, false><<<grid, kAttnHeads * 64, 0, s>>>(LLMI_ATTN_ARGS);
+    else attn_part_1<8, false><<<grid, kAttnHeads * 64, 0, s>>>(LLMI_ATTN_ARGS);
+  }
+#undef LLMI_ATTN_ARGS
   return nch;
 }
 
@@ -1278,11 +1318,28 @@ __global__ void __launch_bounds__(kThreads) argmax_many(const float* __restrict_
 // The state of a graph-replayed tolerance step: st[0] = the step's positions
 // (the cache length after it), st[1] = the generated token's slot.  Set
 // before the first replay; advanced by the last kernel of each replay.
-__global__ void step_state_set(int* st, int npos, int slot) {
-  if (threadIdx.x < 2) st[threadIdx.x] = threadIdx.x == 0 ? npos : slot;
+// rope[0, half) / rope[half, hd): the cos / sin row of the step's newest
+// position (npos - 1), which the replayed attention reads.  One workgroup
+// of at least max(2, half) threads.
+__global__ void step_state_set(int* st, int npos, int slot, const float* __restrict__ cos_t,
+                               const float* __restrict__ sin_t, float* __restrict__ rope, int half) {
+  const int t = threadIdx.x;
+  if (t < 2) st[t] = t == 0 ? npos : slot;
+  if (t < half) {
+    rope[t] = cos_t[static_cast<std::size_t>(npos - 1) * half + t];
+    rope[half + t] = sin_t[static_cast<std::size_t>(npos - 1) * half + t];
+  }
 }
-__global__ void step_state_advance(int* st) {
-  if (threadIdx.x < 2) st[threadIdx.x] += 1;
+__global__ void step_state_advance(int* st, const float* __restrict__ cos_t, const float* __restrict__ sin_t,
+                                   float* __restrict__ rope, int half) {
+  const int t = threadIdx.x;
+  const int npos = st[0];  // the step just run; the next one's newest position is npos
+  __syncthreads();         // every thread has read st before it moves
+  if (t < 2) st[t] += 1;
+  if (t < half) {
+    rope[t] = cos_t[static_cast<std::size_t>(npos) * half + t];
+    rope[half + t] = sin_t[static_cast<std::size_t>(npos) * half + t];
+  }
 }
 
 // Standalone glue kernels (the device counterparts of kernels.hpp:13-32).
@@ -1387,7 +1444,8 @@ struct Workspace {
   float* am_v = nullptr;         // argmax partials and completion counter
   int* am_i = nullptr;
   unsigned* am_count = nullptr;
-  int* step_state = nullptr;     // a graph-replayed step's positions and output slot (step_advance)
+  int* step_state = nullptr;     // a graph-replayed step's positions and output slot (step_state_*)
+  float* step_rope = nullptr;    // and its newest position's cos / sin row
 };
 
 }  // namespace llmi_hip
@@ -1754,7 +1812,8 @@ void free_workspace(Workspace& w) {
                   static_cast<void*>(w.gen), static_cast<void*>(w.slog), static_cast<void*>(w.nll),
                   static_cast<void*>(w.am_v),
                   static_cast<void*>(w.am_i),
-                  static_cast<void*>(w.am_count), static_cast<void*>(w.step_state)})
+                  static_cast<void*>(w.am_count), static_cast<void*>(w.step_state),
+                  static_cast<void*>(w.step_rope)})
     if (p != nullptr) (void)hipFree(p);
   w = Workspace{};
 }
@@ -1784,6 +1843,7 @@ int ensure_workspace(llmi_hip_model* m, std::size_t T) {
   if (rc == LLMI_OK) rc = get(&w.am_i, kArgmaxBlocks, 4);
   if (rc == LLMI_OK) rc = get(&w.am_count, 1, 4);
   if (rc == LLMI_OK) rc = get(&w.step_state, 2, 4);
+  if (rc == LLMI_OK) rc = get(&w.step_rope, m->hd, 4);
   if (rc == LLMI_OK && hipMemsetAsync(w.am_count, 0, sizeof(unsigned), library_stream()) != hipSuccess)
     rc = fail(LLMI_ERR_HIP, "workspace: memset");
   if (rc != LLMI_OK) {
@@ -1800,11 +1860,11 @@ int ensure_workspace(llmi_hip_model* m, std::size_t T) {
 // tolerance: llmi_hip_model_set_decode_mode's tolerance-mode step (needs
 // tol_ready): the attention over position chunks, merged in the o_proj
 // product's staging, and every matmul split over K (SplitProduct).
-// npos_dev (tolerance mode only; may be null): the step's positions in
-// device memory, for a step captured once and replayed from a graph; the
-// caller then advances cache->len itself.
+// g (tolerance mode only; may be null): a step captured once and replayed
+// from a graph (its positions in device memory, GraphStep); the caller then
+// advances cache->len itself.
 int decode_step(llmi_hip_model* m, llmi_hip_cache* cache, hipStream_t s, bool tolerance = false,
-                const int* npos_dev = nullptr) {
+                const GraphStep* g = nullptr) {
   const auto& c = m->c;
   Workspace& w = m->ws;
   DecodeBuffers& d = m->dec;
@@ -1829,8 +1889,11 @@ int decode_step(llmi_hip_model* m, llmi_hip_cache* cache, hipStream_t s, bool to
       if (int rc = launch_split(l.s_qkv, s)) return rc;
       const int nch = launch_tol_attention(d.q, d.k, d.v, cache->k + li * per_layer, cache->v + li * per_layer,
                                            m->cos_t, m->sin_t, d.part, nh, nkv, hd, static_cast<int>(cache->cap),
-                                           static_cast<int>(pos + 1), scale, s, npos_dev);
-      if (int rc = launch_split(l.s_o, s, nch, npos_dev)) return rc;
+                                           static_cast<int>(pos + 1), scale, s, g);
+      // From a graph the combine takes the chunk count from the positions
+      // in device memory and the run's chunk length (passed in its place).
+      if (int rc = g != nullptr ? launch_split(l.s_o, s, g->chunk, g->npos_dev) : launch_split(l.s_o, s, nch))
+        return rc;
       if (int rc = launch_split(l.s_gu, s)) return rc;
       if (int rc = launch_split(l.s_dn, s)) return rc;
       continue;
@@ -1848,7 +1911,7 @@ int decode_step(llmi_hip_model* m, llmi_hip_cache* cache, hipStream_t s, bool to
   if (int rc = launch_matmul(head, d.h, 1, nullptr, w.logits, s)) return rc;
   LLMI_TRY_HIP(hipGetLastError());
   m->qkv_clear = split;
-  if (npos_dev == nullptr) cache->len = pos + 1;
+  if (g == nullptr) cache->len = pos + 1;
   return LLMI_OK;
 }
 
@@ -2188,49 +2251,66 @@ int llmi_hip_model_forward_cached(llmi_hip_model* m, llmi_hip_cache* cache, cons
 // runs on the device and feeds the next step's embedding gather directly.
 // Without stop ids nothing waits for the host between steps: the ids collect
 // in device memory and are copied back once.
-// The tolerance-mode greedy loop from a graph (generate_greedy).  Capture
+// The tolerance-mode greedy loop from graphs (generate_greedy).  Capture
 // (before the prompt's prefill, so that its host time is not in the decode
-// span): argmax of the logits into ids and gen[state[1]], the decode step
-// with its positions from state[0], the state's advance.  A capture the
-// runtime refuses leaves exec null (the eager loop runs).  Replay (after the
-// prefill): the state set, the graph once per token but the last, the last
-// argmax; the caller synchronizes before the destructor frees the graph.
+// span) of one token -- argmax of the logits into ids and gen[state[1]],
+// the decode step with its positions from state[0], the state's advance --
+// once into a one-token graph and kGraphTokens times into another (a
+// replay's fixed cost, once per kGraphTokens tokens).  A capture the runtime
+// refuses leaves the graphs null (the eager loop runs).  Replay (after the
+// prefill): the state set, the graphs for every token but the last, the
+// last argmax; the caller synchronizes before the destructor frees them.
 constexpr std::size_t kGraphMinSteps = 8;
+constexpr int kGraphTokens = 4;
 struct GreedyGraph {
-  hipGraph_t graph = nullptr;
-  hipGraphExec_t exec = nullptr;
+  hipGraph_t graph[2] = {nullptr, nullptr};
+  hipGraphExec_t exec[2] = {nullptr, nullptr};  // one token, kGraphTokens tokens
   GreedyGraph() = default;
   GreedyGraph(const GreedyGraph&) = delete;
   GreedyGraph& operator=(const GreedyGraph&) = delete;
+  bool ready() const { return exec[0] != nullptr && exec[1] != nullptr; }
   ~GreedyGraph() {
-    if (exec != nullptr) (void)hipGraphExecDestroy(exec);
-    if (graph != nullptr) (void)hipGraphDestroy(graph);
+    for (int i = 0; i < 2; ++i) {
+      if (exec[i] != nullptr) (void)hipGraphExecDestroy(exec[i]);
+      if (graph[i] != nullptr) (void)hipGraphDestroy(graph[i]);
+    }
   }
 };
-void greedy_graph_capture(llmi_hip_model* m, llmi_hip_cache* cache, hipStream_t s, GreedyGraph* g) {
+void greedy_graph_capture(llmi_hip_model* m, llmi_hip_cache* cache, std::size_t last_npos, hipStream_t s,
+                          GreedyGraph* g) {
   Workspace& w = m->ws;
   const int V = static_cast<int>(m->V);
-  if (hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal) != hipSuccess) {
-    (void)hipGetLastError();
-    return;
-  }
+  const int half = static_cast<int>(m->hd / 2);
+  // The run's chunk length: that of its last step, so every step's positions
+  // fit kAttnMaxChunks chunks.
+  const GraphStep gs{w.step_state, w.step_rope, attn_chunk_len(static_cast<int>(last_npos))};
   const bool clear = m->qkv_clear;
-  m->qkv_clear = true;  // the replays' q|k|v are cleared by the step before (or before the first)
-  argmax_many<<<kArgmaxBlocks, kThreads, 0, s>>>(w.logits, V, w.am_v, w.am_i, w.am_count, w.ids, w.gen,
-                                                 w.step_state + 1);
-  bool ok = hipGetLastError() == hipSuccess;
-  if (ok) ok = decode_step(m, cache, s, true, w.step_state) == LLMI_OK;
-  if (ok) {
-    step_state_advance<<<1, 64, 0, s>>>(w.step_state);
-    ok = hipGetLastError() == hipSuccess;
+  for (int i = 0; i < 2; ++i) {
+    if (hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal) != hipSuccess) break;
+    m->qkv_clear = true;  // the replays' q|k|v are cleared by the step before (or before the first)
+    bool ok = true;
+    for (int t = 0; ok && t < (i == 0 ? 1 : kGraphTokens); ++t) {
+      argmax_many<<<kArgmaxBlocks, kThreads, 0, s>>>(w.logits, V, w.am_v, w.am_i, w.am_count, w.ids, w.gen,
+                                                     w.step_state + 1);
+      ok = hipGetLastError() == hipSuccess;
+      if (ok) ok = decode_step(m, cache, s, true, &gs) == LLMI_OK;
+      if (ok) {
+        step_state_advance<<<1, 64, 0, s>>>(w.step_state, m->cos_t, m->sin_t, w.step_rope, half);
+        ok = hipGetLastError() == hipSuccess;
+      }
+    }
+    const hipError_t ended = hipStreamEndCapture(s, &g->graph[i]);
+    if (!ok || ended != hipSuccess || g->graph[i] == nullptr ||
+        hipGraphInstantiate(&g->exec[i], g->graph[i], nullptr, nullptr, 0) != hipSuccess)
+      break;
   }
   m->qkv_clear = clear;
-  const hipError_t ended = hipStreamEndCapture(s, &g->graph);
-  if (!ok || ended != hipSuccess || g->graph == nullptr ||
-      hipGraphInstantiate(&g->exec, g->graph, nullptr, nullptr, 0) != hipSuccess) {
-    (void)hipGetLastError();
-    if (g->exec != nullptr) (void)hipGraphExecDestroy(g->exec);
-    g->exec = nullptr;
+  (void)hipGetLastError();
+  if (!g->ready()) {
+    for (int i = 0; i < 2; ++i) {
+      if (g->exec[i] != nullptr) (void)hipGraphExecDestroy(g->exec[i]);
+      g->exec[i] = nullptr;
+    }
   }
 }
 int greedy_graph_run(llmi_hip_model* m, llmi_hip_cache* cache, std::size_t max_new, hipStream_t s,
@@ -2242,9 +2322,12 @@ int greedy_graph_run(llmi_hip_model* m, llmi_hip_cache* cache, std::size_t max_n
     return fail(LLMI_ERR_STATE, "forward_cached: cache is full");
   if (!m->qkv_clear)
     zero_floats<<<blocks_for(m->Q + 2 * m->KV), kThreads, 0, s>>>(d.q, static_cast<int>(m->Q + 2 * m->KV));
-  step_state_set<<<1, 64, 0, s>>>(w.step_state, static_cast<int>(cache->len + 1), 0);
+  step_state_set<<<1, 64, 0, s>>>(w.step_state, static_cast<int>(cache->len + 1), 0, m->cos_t, m->sin_t, w.step_rope,
+                                  static_cast<int>(m->hd / 2));
   LLMI_TRY_HIP(hipGetLastError());
-  for (std::size_t k = 0; k + 1 < max_new; ++k) LLMI_TRY_HIP(hipGraphLaunch(g.exec, s));
+  std::size_t k = 0;
+  for (; k + kGraphTokens + 1 <= max_new; k += kGraphTokens) LLMI_TRY_HIP(hipGraphLaunch(g.exec[1], s));
+  for (; k + 1 < max_new; ++k) LLMI_TRY_HIP(hipGraphLaunch(g.exec[0], s));
   argmax_many<<<kArgmaxBlocks, kThreads, 0, s>>>(w.logits, V, w.am_v, w.am_i, w.am_count, w.ids, w.gen,
                                                  w.step_state + 1);
   LLMI_TRY_HIP(hipGetLastError());
@@ -2287,14 +2370,14 @@ int llmi_hip_model_generate_greedy(llmi_hip_model* m, const int32_t* prompt, siz
   GreedyGraph graph;
   if (m->decode_graph && m->decode_mode == LLMI_DECODE_TOLERANCE && m->tol_ready && n_stop == 0 &&
       max_new >= kGraphMinSteps)
-    greedy_graph_capture(m, cache, s, &graph);
+    greedy_graph_capture(m, cache, n + max_new - 1, s, &graph);
   LLMI_TRY_HIP(hipMemcpyAsync(w.ids, prompt, n * sizeof(std::int32_t), hipMemcpyHostToDevice, s));
   LLMI_TRY_HIP(hipEventRecord(ev[0], s));
   if (int rc = forward_device(m, cache, n, false, s)) return rc;
   LLMI_TRY_HIP(hipEventRecord(ev[1], s));
   const int V = static_cast<int>(m->V);
   std::size_t produced = 0;
-  if (graph.exec != nullptr) {
+  if (graph.ready()) {
     if (int rc = greedy_graph_run(m, cache, max_new, s, graph)) return rc;
     produced = max_new;
   }
