@@ -328,7 +328,7 @@ __global__ void __launch_bounds__(1024) qgemv_tol_small(const TolProblem* __rest
 #pragma unroll
           for (int h = 0; h < 2; ++h) {
             const int rr = 2 * t + h;
-            if (rr < R && rr < nr) {
+            if (rr < R && (R == 1 || rr < nr)) {  // a launch's rows are at least one
               const float blk = __builtin_fmaf(16.0f, d[t][2 * h] + d[t][2 * h + 1], -wsx[rr * nwb + jb0 + j]);
               acc[rr] = __builtin_fmaf(blk, cur_s[j], acc[rr]);
             }
@@ -527,13 +527,15 @@ __global__ void __launch_bounds__(1024) qgemv_tol_wide(const TolProblem* __restr
           const tbf16x8 aq = __builtin_bit_cast(tbf16x8, wl[base + j * step + 2 * q]);
           d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(aq, bq, d, 0, 0, 0);
         }
+        // Every row, also those past nr: their A slots and block sums are
+        // zeros (so their sums stay zero and are never stored), and the
+        // loop keeps no branch per row.
 #pragma unroll
-        for (int r = 0; r < R; ++r)
-          if (r < nr) {
-            const int rh = 8 * (r >> 2) + (r & 3);
-            const float blk = __builtin_fmaf(16.0f, d[rh] + d[rh + 4], -wsx[r * kC + j]);
-            acc[r] = __builtin_fmaf(blk, cur_s[j], acc[r]);
-          }
+        for (int r = 0; r < R; ++r) {
+          const int rh = 8 * (r >> 2) + (r & 3);
+          const float blk = __builtin_fmaf(16.0f, d[rh] + d[rh + 4], -wsx[r * kC + j]);
+          acc[r] = __builtin_fmaf(blk, cur_s[j], acc[r]);
+        }
       }
       if (bn < b_end) {
 #pragma unroll
