@@ -45,10 +45,10 @@ constexpr int kBM = 128, kBN = 256, kBK = 64;
 // K of more than kSplitMinSteps steps of kBK may be split over workgroups;
 // kCus is MI355X's CU count.
 constexpr std::size_t kSplitMinSteps = 24, kCus = 256;
-constexpr int kGemmThreads = 512;  // 8 wavefronts: 2 (tokens) x 4 (outputs)
+constexpr int kGemmThreads = 512;  // 8 wavefronts side by side over the outputs
 constexpr int kWavesN = 8;
-constexpr int kWaveN = kBN / kWavesN;                      // outputs per wavefront (64)
-constexpr int kWaveM = kBM / (kGemmThreads / 64 / kWavesN);  // tokens per wavefront (64)
+constexpr int kWaveN = kBN / kWavesN;                      // outputs per wavefront (32)
+constexpr int kWaveM = kBM / (kGemmThreads / 64 / kWavesN);  // tokens per wavefront (128)
 constexpr int kJ = kWaveN / 16;                            // 16-output MFMA blocks per wavefront
 constexpr int kI = kWaveM / 16;                            // 16-token MFMA blocks per wavefront
 constexpr int kXPer = kBM * kBK / 8 / kGemmThreads;        // 16-byte chunks of the activation tile per thread
@@ -143,7 +143,7 @@ struct WStage {
   float sc[kJ];
   bool live;
 };
-// One K-step of the activation tile held by one thread: chunks t + 256u
+// One K-step of the activation tile held by one thread: chunks t + 512u
 // (16 bytes each) of the 128 x 64 bf16 tile.
 struct XStage {
   u32x4 v[kXPer];
