@@ -690,17 +690,24 @@ __global__ void __launch_bounds__(1024)
 
 // The tolerance-mode one-token product split over K (SplitProduct):
 // workgroup (tile, split), one wavefront, computes rows tile * 64 + lane over
-// blocks [split * BPS, ...): the weights of all its blocks are loaded first,
-// the activations of its range staged in LDS under the prologue meanwhile,
-// the block sums and the chain over its blocks are the exact kernels', and
-// the partial sums go to y by atomic adds.
+// blocks [split * BPS, ...): the prologue's loads (the range's activations,
+// and for RMSNorm the row's first batch of squares, for the combine the
+// chunk partials) are issued first and the weights of all its blocks right
+// after them -- loads complete in issue order, so the prologue then waits for
+// its own data only and its arithmetic overlaps the weights' trip from HBM;
+// the activations of its range are staged in LDS under the prologue, the
+// block sums and the chain over its blocks are the exact kernels', and the
+// partial sums go to y by atomic adds.
 constexpr int kSplitMaxHeads = 8;  // kAttnCombine: whole heads per split (16 blocks of head_dim 64)
 template <int TYPE, int PRO, int BPS>
+// What the first loads' addresses need comes first: the first 14 dwords of
+// the arguments arrive preloaded in SGPRs.
 __global__ void __launch_bounds__(64) tsplit_gemv(const uint4* __restrict__ codes, const float* __restrict__ scales,
                                                   const float* __restrict__ x, const float* __restrict__ pw, int nblk,
-                                                  int in, float eps, int out, const float* __restrict__ bias,
-                                                  float* __restrict__ y, float* __restrict__ zero, int nzero,
-                                                  int comb_hd, int comb_nch, const int* __restrict__ npos_dev) {
+                                                  int in, int out, int comb_hd, float eps, int comb_nch,
+                                                  const float* __restrict__ bias, float* __restrict__ y,
+                                                  float* __restrict__ zero, int nzero,
+                                                  const int* __restrict__ npos_dev) {
   __shared__ __attribute__((aligned(16))) float xs[BPS * kBlock];
   __shared__ float wgt[PRO == kAttnCombine ? kSplitMaxHeads * kAttnMaxChunks : 1];
   const int lane = threadIdx.x;
@@ -711,43 +718,57 @@ __global__ void __launch_bounds__(64) tsplit_gemv(const uint4* __restrict__ code
   const GMEM float* sg = gmem(scales);
   Block<TYPE> blk[BPS];
   float sc[BPS];
+  const auto load_weights = [&]() {
+    __builtin_amdgcn_sched_barrier(0);  // the prologue's loads stay in front
 #pragma unroll
-  for (int j = 0; j < BPS; ++j) {
-    // Past the range: the range's last block again (unused).
-    const std::size_t slot = static_cast<std::size_t>(tile) * nblk + static_cast<std::size_t>(b0 + min(j, nb - 1));
-    blk[j] = load_block<TYPE, true>(cg, slot, lane);
-    sc[j] = loadf<true>(sg + slot * kTileRows + lane);
-  }
-  if (zero != nullptr) {
-    const int wg = static_cast<int>(blockIdx.y * gridDim.x + blockIdx.x);
-    const int stride = static_cast<int>(gridDim.x * gridDim.y) * 64;
-    for (int i = wg * 64 + lane; i < nzero; i += stride) zero[i] = 0.0f;
-  }
+    for (int j = 0; j < BPS; ++j) {
+      // Past the range: the range's last block again (unused).
+      const std::size_t slot = static_cast<std::size_t>(tile) * nblk + static_cast<std::size_t>(b0 + min(j, nb - 1));
+      blk[j] = load_block<TYPE, true>(cg, slot, lane);
+      sc[j] = loadf<true>(sg + slot * kTileRows + lane);
+    }
+  };
   // x' over the range [k0, k0 + n): each lane's elements (and, for
   // RMSNorm, its share of the whole row's squares) are loaded in batches
   // before any is used, so the staging costs one memory round trip per
   // batch rather than one per element.
   constexpr int kPer = (BPS * kBlock + 63) / 64;  // range elements per lane
+  static_assert(kPer * 64 == BPS * kBlock, "every lane's slots lie inside xs");
   const int k0 = b0 * kBlock, n = min(nb * kBlock, in - k0);
   const GMEM float* xg = gmem(x);
   const GMEM float* pg = gmem(pw);
+  // Every load is unconditional, from an index clamped into the row (a load
+  // behind a per-lane condition becomes a branch, and the compiler may then
+  // wait for it on the spot); values past the range are never stored.
   if constexpr (PRO == kRmsNorm || PRO == kSiluUp || PRO == kPlain) {
     float xv[kPer], pv[kPer];
 #pragma unroll
     for (int u = 0; u < kPer; ++u) {
-      const int i = u * 64 + lane;
-      xv[u] = i < n ? xg[k0 + i] : 0.0f;
-      if constexpr (PRO != kPlain) pv[u] = i < n ? pg[k0 + i] : 0.0f;
+      const int i = min(k0 + u * 64 + lane, in - 1);
+      xv[u] = xg[i];
+      if constexpr (PRO != kPlain) pv[u] = pg[i];
     }
     if constexpr (PRO == kRmsNorm) {
+      // The row's squares in batches of kBatch per lane; the first batch's
+      // loads go out before the weights'.
       constexpr int kBatch = 16;
+      float v[kBatch];
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) {
+        const int i = u * 64 + lane;
+        const float t = xg[min(i, in - 1)];
+        v[u] = i < in ? t : 0.0f;
+      }
+      load_weights();
       float ss = 0.0f;
-      for (int i0 = 0; i0 < in; i0 += 64 * kBatch) {
-        float v[kBatch];
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) ss = __builtin_fmaf(v[u], v[u], ss);
+      for (int i0 = 64 * kBatch; i0 < in; i0 += 64 * kBatch) {
 #pragma unroll
         for (int u = 0; u < kBatch; ++u) {
           const int i = i0 + u * 64 + lane;
-          v[u] = i < in ? xg[i] : 0.0f;
+          const float t = xg[min(i, in - 1)];
+          v[u] = i < in ? t : 0.0f;
         }
 #pragma unroll
         for (int u = 0; u < kBatch; ++u) ss = __builtin_fmaf(v[u], v[u], ss);
@@ -756,13 +777,17 @@ __global__ void __launch_bounds__(64) tsplit_gemv(const uint4* __restrict__ code
       const float scale = 1.0f / __builtin_sqrtf(ss / static_cast<float>(in) + eps);
 #pragma unroll
       for (int u = 0; u < kPer; ++u) xv[u] = pv[u] * (xv[u] * scale);
-    } else if constexpr (PRO == kSiluUp) {
+    } else {
+      load_weights();
+      if constexpr (PRO == kSiluUp) {
 #pragma unroll
-      for (int u = 0; u < kPer; ++u) xv[u] = xv[u] / (1.0f + __expf(-xv[u])) * pv[u];
+        for (int u = 0; u < kPer; ++u) xv[u] = xv[u] / (1.0f + __expf(-xv[u])) * pv[u];
+      }
     }
+    // Every slot is stored (xs holds kPer * 64 = BPS * kBlock floats; the
+    // block sums read the first n), so no load is sunk behind a condition.
 #pragma unroll
-    for (int u = 0; u < kPer; ++u)
-      if (u * 64 + lane < n) xs[u * 64 + lane] = xv[u];
+    for (int u = 0; u < kPer; ++u) xs[u * 64 + lane] = xv[u];
   } else {
     // kAttnCombine: the range is whole heads h0 .. h0 + nhh - 1; lanes 16r ..
     // 16r + 15 form the chunk weights of head hb + r.  Every chunk slot's
@@ -770,8 +795,7 @@ __global__ void __launch_bounds__(64) tsplit_gemv(const uint4* __restrict__ code
     // -- zeros or an earlier step's -- and get weight 0), so no load waits
     // for the chunk count, which a graph-replayed step reads from memory.
     // From a graph, comb_nch carries the run's chunk length and the count
-    // follows from the positions.
-    if (npos_dev != nullptr) comb_nch = (__builtin_amdgcn_readfirstlane(*npos_dev) + comb_nch - 1) / comb_nch;
+    // follows from the positions (read after every load is issued).
     const int hd = comb_hd, nh_all = in / hd, h0 = k0 / hd, nhh = n / hd;
     const GMEM float* ms = xg + static_cast<std::size_t>(kAttnMaxChunks) * nh_all * hd;
     const GMEM float* ls = ms + kAttnMaxChunks * nh_all;
@@ -782,15 +806,29 @@ __global__ void __launch_bounds__(64) tsplit_gemv(const uint4* __restrict__ code
       const int hh = i / hd, d = i - hh * hd;
       const GMEM float* oh = xg + static_cast<std::size_t>(h0 + min(hh, nhh - 1)) * kAttnMaxChunks * hd + d;
 #pragma unroll
-      for (int c = 0; c < kAttnMaxChunks; ++c) ov[u][c] = i < n ? oh[c * hd] : 0.0f;
+      for (int c = 0; c < kAttnMaxChunks; ++c) ov[u][c] = oh[c * hd];  // a clamped head's for i >= n (unused)
     }
-    for (int hb = 0; hb < nhh; hb += 4) {
+    // m and l of both groups of four heads (at most kSplitMaxHeads = 8),
+    // then the weights.
+    static_assert(kSplitMaxHeads <= 8, "two groups of four heads");
+    float m_all[2], l_all[2];
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+      const int t = (h0 + min(4 * g + (lane >> 4), nhh - 1)) * kAttnMaxChunks + (lane & 15);
+      m_all[g] = ms[t];
+      l_all[g] = ls[t];
+    }
+    load_weights();
+    if (npos_dev != nullptr) comb_nch = (__builtin_amdgcn_readfirstlane(*npos_dev) + comb_nch - 1) / comb_nch;
+    // Both groups always (a lane whose head is past the range is not live
+    // and stores nothing), so the loads above have a use on every path.
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+      const int hb = 4 * g;
       const int hh = hb + (lane >> 4), c = lane & 15;
-      const int t = (h0 + min(hh, nhh - 1)) * kAttnMaxChunks + c;
-      const float m_all = ms[t], l_all = ls[t];
       const bool live = hh < nhh && c < comb_nch;
-      const float mv = live ? m_all : -__builtin_inff();
-      const float lv = live ? l_all : 0.0f;
+      const float mv = live ? m_all[g] : -__builtin_inff();
+      const float lv = live ? l_all[g] : 0.0f;
       const float mx = row_last_bcast(row_max16_f32(mv), lane);
       const float w = live ? __expf(mv - mx) : 0.0f;
       const float den = row_last_bcast(row_sum16_f32(w * lv), lane);
@@ -800,31 +838,44 @@ __global__ void __launch_bounds__(64) tsplit_gemv(const uint4* __restrict__ code
 #pragma unroll
     for (int u = 0; u < kPer; ++u) {
       const int i = u * 64 + lane;
-      if (i < n) {
-        const float* wh = wgt + (i / hd) * kAttnMaxChunks;
-        float acc_c = 0.0f;
+      const float* wh = wgt + min(i / hd, nhh - 1) * kAttnMaxChunks;  // past n: a clamped head's (unused)
+      float acc_c = 0.0f;
 #pragma unroll
-        for (int c = 0; c < kAttnMaxChunks; ++c) acc_c = __builtin_fmaf(wh[c], ov[u][c], acc_c);
-        xs[i] = acc_c;
-      }
+      for (int c = 0; c < kAttnMaxChunks; ++c) acc_c = __builtin_fmaf(wh[c], ov[u][c], acc_c);
+      xs[i] = acc_c;
     }
   }
   __syncthreads();
   const Q4Magic k = q4_magic();
   const int nfull = in / kBlock - b0;  // whole blocks of the range
   float acc = 0.0f;
+  if (nb == BPS && nfull >= BPS) {
+    // A range of BPS whole blocks (uniform): no condition per block, so every
+    // block's loads have a use on this path and none is sunk past the prologue.
 #pragma unroll
-  for (int j = 0; j < BPS; ++j) {
-    if (j < nb) {
-      const float part = j < nfull ? full_block_dot<TYPE>(blk[j], xs + j * kBlock, k)
-                                   : tail_block_dot<TYPE>(blk[j], xs + j * kBlock, in - (b0 + j) * kBlock);
-      acc = __builtin_fmaf(part, sc[j], acc);
+    for (int j = 0; j < BPS; ++j) acc = __builtin_fmaf(full_block_dot<TYPE>(blk[j], xs + j * kBlock, k), sc[j], acc);
+  } else {
+#pragma unroll
+    for (int j = 0; j < BPS; ++j) {
+      if (j < nb) {
+        const float part = j < nfull ? full_block_dot<TYPE>(blk[j], xs + j * kBlock, k)
+                                     : tail_block_dot<TYPE>(blk[j], xs + j * kBlock, in - (b0 + j) * kBlock);
+        acc = __builtin_fmaf(part, sc[j], acc);
+      }
     }
   }
   const int row = tile * kTileRows + lane;
   if (row < out) {
     if (blockIdx.y == 0 && bias != nullptr) acc += bias[row];
     unsafeAtomicAdd(y + row, acc);
+  }
+  // Clearing the next product's output (a buffer this launch does not
+  // read): last, so that its stores are not ahead of any load in the
+  // counter the waits above use.
+  if (zero != nullptr) {
+    const int wg = static_cast<int>(blockIdx.y * gridDim.x + blockIdx.x);
+    const int stride = static_cast<int>(gridDim.x * gridDim.y) * 64;
+    for (int i = wg * 64 + lane; i < nzero; i += stride) zero[i] = 0.0f;
   }
 }
 
@@ -1766,7 +1817,7 @@ void launch_split_bps(const SplitProduct& p, hipStream_t s, int comb_nch, const 
   const dim3 grid(static_cast<unsigned>(m.ntiles), static_cast<unsigned>(p.splits));
 #define LLMI_SPLIT_ARGS                                                                                            \
   reinterpret_cast<const uint4*>(m.codes), m.scales, p.x, p.pw, static_cast<int>(m.nblk), static_cast<int>(m.in), \
-      p.eps, static_cast<int>(m.out), p.bias, p.y, p.zero, p.nzero, p.comb_hd, comb_nch, npos_dev
+      static_cast<int>(m.out), p.comb_hd, p.eps, comb_nch, p.bias, p.y, p.zero, p.nzero, npos_dev
   switch (p.bps) {
     case 2: tsplit_gemv<TYPE, PRO, 2><<<grid, 64, 0, s>>>(LLMI_SPLIT_ARGS); break;
     case 4: tsplit_gemv<TYPE, PRO, 4><<<grid, 64, 0, s>>>(LLMI_SPLIT_ARGS); break;
