@@ -1222,21 +1222,24 @@ __device__ __forceinline__ Best better(Best a, Best b) {
   return a;
 }
 
+// The workgroup's best, returned to every thread: within each wavefront by
+// lane exchanges (no barrier), then over the NT / 64 wavefronts' bests in LDS
+// (one barrier).  With finite values the result -- the maximum, and the
+// lowest index among its ties -- does not depend on the order of the pairings.
 template <int NT>
 __device__ __forceinline__ Best block_best(Best b, float* bv, int* bi) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) b = better(b, Best{__shfl_xor(b.v, off, 64), __shfl_xor(b.i, off, 64)});
   const int tid = threadIdx.x;
-  bv[tid] = b.v;
-  bi[tid] = b.i;
-  __syncthreads();
-  for (int stride = NT / 2; stride > 0; stride >>= 1) {
-    if (tid < stride) {
-      const Best o = better(Best{bv[tid], bi[tid]}, Best{bv[tid + stride], bi[tid + stride]});
-      bv[tid] = o.v;
-      bi[tid] = o.i;
-    }
-    __syncthreads();
+  if ((tid & 63) == 0) {
+    bv[tid >> 6] = b.v;
+    bi[tid >> 6] = b.i;
   }
-  return Best{bv[0], bi[0]};
+  __syncthreads();
+  Best r{bv[0], bi[0]};
+#pragma unroll
+  for (int w = 1; w < NT / 64; ++w) r = better(r, Best{bv[w], bi[w]});
+  return r;
 }
 
 // One block over all of x (small n, and the standalone entry point).
