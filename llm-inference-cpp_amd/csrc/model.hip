@@ -1260,13 +1260,21 @@ __global__ void __launch_bounds__(1024) argmax_first(const float* __restrict__ x
 // Many blocks, each over a contiguous slice; each block publishes its best
 // and the last block to finish (counted with a device-scope atomic) combines
 // them and resets the counter for the next launch.  No block waits.
+// adv (may be null; a step replayed from a graph): the state of the step
+// about to run, moved on by the last block once the id is recorded -- st[0]
+// (the positions) and st[1] (the output slot, also_idx) each up by one, and
+// rope set to the cos / sin row of the new step's newest position -- so no
+// launch of its own does it (the layout at step_state_set).
 constexpr int kArgmaxBlocks = 128;
 
 __global__ void __launch_bounds__(kThreads) argmax_many(const float* __restrict__ x, int n, float* __restrict__ part_v,
                                                         int* __restrict__ part_i, unsigned* __restrict__ counter,
                                                         std::int32_t* __restrict__ out,
                                                         std::int32_t* __restrict__ also,
-                                                        const int* __restrict__ also_idx) {
+                                                        const int* __restrict__ also_idx, int* __restrict__ adv,
+                                                        const float* __restrict__ cos_t,
+                                                        const float* __restrict__ sin_t, float* __restrict__ rope,
+                                                        int half) {
   __shared__ float bv[kThreads];
   __shared__ int bi[kThreads];
   __shared__ bool last;
@@ -1316,14 +1324,25 @@ __global__ void __launch_bounds__(kThreads) argmax_many(const float* __restrict_
     if (also != nullptr) also[also_idx != nullptr ? *also_idx : 0] = idx;
     __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
+  if (adv != nullptr) {
+    const int np = adv[0];  // the step before; the next one's newest position is np
+    __syncthreads();        // every thread has read st[0], thread 0 the slot, before they move
+    const int t = threadIdx.x;
+    if (t < 2) adv[t] += 1;
+    if (t < half) {
+      rope[t] = cos_t[static_cast<std::size_t>(np) * half + t];
+      rope[half + t] = sin_t[static_cast<std::size_t>(np) * half + t];
+    }
+  }
 }
 
 // The state of a graph-replayed tolerance step: st[0] = the step's positions
 // (the cache length after it), st[1] = the generated token's slot.  Set
-// before the first replay; advanced by the last kernel of each replay.
-// rope[0, half) / rope[half, hd): the cos / sin row of the step's newest
-// position (npos - 1), which the replayed attention reads.  One workgroup
-// of at least max(2, half) threads.
+// before the first replay to the step before the first (its argmax moves it
+// on); advanced by the argmax that starts each replayed step (argmax_many's
+// adv).  rope[0, half) / rope[half, hd): the cos / sin row of the step's
+// newest position (npos - 1), which the replayed attention reads.  One
+// workgroup of at least max(2, half) threads.
 __global__ void step_state_set(int* st, int npos, int slot, const float* __restrict__ cos_t,
                                const float* __restrict__ sin_t, float* __restrict__ rope, int half) {
   const int t = threadIdx.x;
@@ -1331,17 +1350,6 @@ __global__ void step_state_set(int* st, int npos, int slot, const float* __restr
   if (t < half) {
     rope[t] = cos_t[static_cast<std::size_t>(npos - 1) * half + t];
     rope[half + t] = sin_t[static_cast<std::size_t>(npos - 1) * half + t];
-  }
-}
-__global__ void step_state_advance(int* st, const float* __restrict__ cos_t, const float* __restrict__ sin_t,
-                                   float* __restrict__ rope, int half) {
-  const int t = threadIdx.x;
-  const int npos = st[0];  // the step just run; the next one's newest position is npos
-  __syncthreads();         // every thread has read st before it moves
-  if (t < 2) st[t] += 1;
-  if (t < half) {
-    rope[t] = cos_t[static_cast<std::size_t>(npos) * half + t];
-    rope[half + t] = sin_t[static_cast<std::size_t>(npos) * half + t];
   }
 }
 
@@ -2257,8 +2265,8 @@ int llmi_hip_model_forward_cached(llmi_hip_model* m, llmi_hip_cache* cache, cons
 // The tolerance-mode greedy loop from graphs (generate_greedy).  Capture
 // (before the prompt's prefill, so that its host time is not in the decode
 // span) of one token -- argmax of the logits into ids and gen[state[1]],
-// the decode step with its positions from state[0], the state's advance --
-// once into a one-token graph and kGraphTokens times into another (a
+// which then advances the state, and the decode step with its positions from
+// state[0] -- once into a one-token graph and kGraphTokens times into another (a
 // replay's fixed cost, once per kGraphTokens tokens).  A capture the runtime
 // refuses leaves the graphs null (the eager loop runs).  Replay (after the
 // prefill): the state set, the graphs for every token but the last, the
@@ -2294,13 +2302,10 @@ void greedy_graph_capture(llmi_hip_model* m, llmi_hip_cache* cache, std::size_t 
     bool ok = true;
     for (int t = 0; ok && t < (i == 0 ? 1 : kGraphTokens); ++t) {
       argmax_many<<<kArgmaxBlocks, kThreads, 0, s>>>(w.logits, V, w.am_v, w.am_i, w.am_count, w.ids, w.gen,
-                                                     w.step_state + 1);
+                                                     w.step_state + 1, w.step_state, m->cos_t, m->sin_t, w.step_rope,
+                                                     half);
       ok = hipGetLastError() == hipSuccess;
       if (ok) ok = decode_step(m, cache, s, true, &gs) == LLMI_OK;
-      if (ok) {
-        step_state_advance<<<1, 64, 0, s>>>(w.step_state, m->cos_t, m->sin_t, w.step_rope, half);
-        ok = hipGetLastError() == hipSuccess;
-      }
     }
     const hipError_t ended = hipStreamEndCapture(s, &g->graph[i]);
     if (!ok || ended != hipSuccess || g->graph[i] == nullptr ||
@@ -2325,14 +2330,16 @@ int greedy_graph_run(llmi_hip_model* m, llmi_hip_cache* cache, std::size_t max_n
     return fail(LLMI_ERR_STATE, "forward_cached: cache is full");
   if (!m->qkv_clear)
     zero_floats<<<blocks_for(m->Q + 2 * m->KV), kThreads, 0, s>>>(d.q, static_cast<int>(m->Q + 2 * m->KV));
-  step_state_set<<<1, 64, 0, s>>>(w.step_state, static_cast<int>(cache->len + 1), 0, m->cos_t, m->sin_t, w.step_rope,
+  // The state of the step before the first replayed one (cache->len >= 1
+  // after the prefill): the first replay's argmax moves it on.
+  step_state_set<<<1, 64, 0, s>>>(w.step_state, static_cast<int>(cache->len), 0, m->cos_t, m->sin_t, w.step_rope,
                                   static_cast<int>(m->hd / 2));
   LLMI_TRY_HIP(hipGetLastError());
   std::size_t k = 0;
   for (; k + kGraphTokens + 1 <= max_new; k += kGraphTokens) LLMI_TRY_HIP(hipGraphLaunch(g.exec[1], s));
   for (; k + 1 < max_new; ++k) LLMI_TRY_HIP(hipGraphLaunch(g.exec[0], s));
   argmax_many<<<kArgmaxBlocks, kThreads, 0, s>>>(w.logits, V, w.am_v, w.am_i, w.am_count, w.ids, w.gen,
-                                                 w.step_state + 1);
+                                                 w.step_state + 1, nullptr, nullptr, nullptr, nullptr, 0);
   LLMI_TRY_HIP(hipGetLastError());
   cache->len += max_new - 1;
   m->qkv_clear = true;
@@ -2386,7 +2393,7 @@ int llmi_hip_model_generate_greedy(llmi_hip_model* m, const int32_t* prompt, siz
   }
   for (std::size_t step = produced; step < max_new; ++step) {
     argmax_many<<<kArgmaxBlocks, kThreads, 0, s>>>(w.logits, V, w.am_v, w.am_i, w.am_count, w.ids, w.gen + step,
-                                                   nullptr);
+                                                   nullptr, nullptr, nullptr, nullptr, nullptr, 0);
     LLMI_TRY_HIP(hipGetLastError());
     produced = step + 1;
     if (n_stop > 0) {
