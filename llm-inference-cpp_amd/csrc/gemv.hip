@@ -699,9 +699,9 @@ __global__ void __launch_bounds__(1024)
 // block sums and the chain over its blocks are the exact kernels', and the
 // partial sums go to y by atomic adds.
 constexpr int kSplitMaxHeads = 8;  // kAttnCombine: whole heads per split (16 blocks of head_dim 64)
+// What the first loads' addresses need comes first in the arguments: their
+// first 14 dwords arrive preloaded in SGPRs.
 template <int TYPE, int PRO, int BPS>
-// What the first loads' addresses need comes first: the first 14 dwords of
-// the arguments arrive preloaded in SGPRs.
 __global__ void __launch_bounds__(64) tsplit_gemv(const uint4* __restrict__ codes, const float* __restrict__ scales,
                                                   const float* __restrict__ x, const float* __restrict__ pw, int nblk,
                                                   int in, int out, int comb_hd, float eps, int comb_nch,
