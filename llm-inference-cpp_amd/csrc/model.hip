@@ -982,8 +982,10 @@ __global__ void __launch_bounds__(kAttnHeads * 64) attn_part_1(const float* __re
     for (int u = 0; u < kLd; ++u) {
       const int e = u * kT + tid;
       const int r = e / (hd / 4), c4 = 4 * (e - r * (hd / 4));
+      // The newest position's k row is not used from here: its score
+      // reads the rotated new k (kn) itself, so staging needs no barrier
+      // after kn is written.
       float4 kv = kr[u], vv = vr[u];
-      if (sb + r == pos) kv = make_float4(kn[c4], kn[c4 + 1], kn[c4 + 2], kn[c4 + 3]);
       if constexpr (GRAPH) {
         const float4 z = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         if (sb + r == pos) vv = vnr[u];
@@ -1026,7 +1028,11 @@ __global__ void __launch_bounds__(kAttnHeads * 64) attn_part_1(const float* __re
     kn[tid] = __builtin_fmaf(a, cs, -(b * sn));
     kn[tid + half] = __builtin_fmaf(b, cs, a * sn);
   }
-  __syncthreads();  // qs, kn
+  // The first sub-block staged (and the next one's loads issued) before the
+  // one barrier that publishes it together with qs and kn.
+  store_sub(s_begin);
+  if (s_begin + kAttnSub < s_end) load_sub(s_begin + kAttnSub);
+  __syncthreads();  // qs, kn, the first sub-block
   if (has_new && blockIdx.z == 0 && tid < hd) {
     kc[(static_cast<std::size_t>(kvh) * cap + pos) * hd + tid] = kn[tid];
     vc[(static_cast<std::size_t>(kvh) * cap + pos) * hd + tid] = vn[tid];
@@ -1040,13 +1046,15 @@ __global__ void __launch_bounds__(kAttnHeads * 64) attn_part_1(const float* __re
   for (int k = 0; k < kCols; ++k) acc[k] = 0.0f;
   for (int sb = s_begin; sb < s_end; sb += kAttnSub) {
     const int n = min(kAttnSub, s_end - sb);
-    if (sb != s_begin) __syncthreads();  // every wavefront is done with the previous sub-block
-    store_sub(sb);
-    if (sb + kAttnSub < s_end) load_sub(sb + kAttnSub);
-    __syncthreads();  // the sub-block in LDS
+    if (sb != s_begin) {
+      __syncthreads();  // every wavefront is done with the previous sub-block
+      store_sub(sb);
+      if (sb + kAttnSub < s_end) load_sub(sb + kAttnSub);
+      __syncthreads();  // the sub-block in LDS
+    }
     if (active) {
-      // Score of position `lane`.
-      const float* kq = kt + lane * (hd + 1);
+      // Score of position `lane` (the newest position's from kn).
+      const float* kq = sb + lane == pos ? kn : kt + lane * (hd + 1);
       float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
 #pragma unroll
       for (int i = 0; i < hd; i += 4) {
