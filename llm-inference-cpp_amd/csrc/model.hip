@@ -999,6 +999,18 @@ __global__ void __launch_bounds__(kAttnHeads * 64) attn_part_1(const float* __re
       *reinterpret_cast<float4*>(vt + r * hd + c4) = vv;
     }
   };
+  // q's pair, the new k's pair and their cos / sin first (at most one pair
+  // per thread: ng * half <= kT), unconditional from clamped indices, so
+  // that the rotations below wait for them only and overlap the K / V trip.
+  static_assert(kAttnHeads * 64 <= kT, "one q pair per thread");
+  const float* cr = GRAPH ? rope_dev : cos_t + static_cast<std::size_t>(pos) * half;
+  const float* sr = GRAPH ? rope_dev + half : sin_t + static_cast<std::size_t>(pos) * half;
+  const bool has_q = tid < ng * half;
+  const int gq = has_q ? tid / half : 0, iq = tid % half;
+  const float* qh = q + static_cast<std::size_t>(kvh * G + g0 + gq) * hd;
+  const float* kq = knew + static_cast<std::size_t>(kvh) * hd;
+  const float qa = qh[iq], qb = qh[iq + half], ka = kq[iq], kb = kq[iq + half], cs = cr[iq], sn = sr[iq];
+  __builtin_amdgcn_sched_barrier(0);  // these loads stay in front of the sub-block's
   load_sub(s_begin);
   if constexpr (GRAPH) {
 #pragma unroll
@@ -1006,27 +1018,25 @@ __global__ void __launch_bounds__(kAttnHeads * 64) attn_part_1(const float* __re
       const int e = u * kT + tid;
       vnr[u] = *reinterpret_cast<const float4*>(vn + 4 * (e % (hd / 4)));
     }
+  }
+  // q rotated before the positions are read (its cos / sin row does not
+  // depend on them): these LDS stores, ahead of the exit below, keep the
+  // loads they use from being sunk past it.
+  if (has_q) {
+    qs[gq * hd + iq] = __builtin_fmaf(qa, cs, -(qb * sn));
+    qs[gq * hd + iq + half] = __builtin_fmaf(qb, cs, qa * sn);
+  }
+  if constexpr (GRAPH) {
     npos = __builtin_amdgcn_readfirstlane(*npos_dev);
     pos = npos - 1;
     s_end = min(npos, s_begin + chunk);
     if (s_begin >= npos) return;  // a chunk past the last (after its loads were issued)
   }
 
-  const float* cr = GRAPH ? rope_dev : cos_t + static_cast<std::size_t>(pos) * half;
-  const float* sr = GRAPH ? rope_dev + half : sin_t + static_cast<std::size_t>(pos) * half;
-  for (int e = tid; e < ng * half; e += kT) {
-    const int g = e / half, i = e - g * half;
-    const float* qh = q + static_cast<std::size_t>(kvh * G + g0 + g) * hd;
-    const float a = qh[i], b = qh[i + half], cs = cr[i], sn = sr[i];
-    qs[g * hd + i] = __builtin_fmaf(a, cs, -(b * sn));
-    qs[g * hd + i + half] = __builtin_fmaf(b, cs, a * sn);
-  }
   const bool has_new = pos >= s_begin && pos < s_end;
-  if (has_new && tid < half) {
-    const float* kq = knew + static_cast<std::size_t>(kvh) * hd;
-    const float a = kq[tid], b = kq[tid + half], cs = cr[tid], sn = sr[tid];
-    kn[tid] = __builtin_fmaf(a, cs, -(b * sn));
-    kn[tid + half] = __builtin_fmaf(b, cs, a * sn);
+  if (has_new && tid < half) {  // iq = tid here, so cs / sn are this column's
+    kn[tid] = __builtin_fmaf(ka, cs, -(kb * sn));
+    kn[tid + half] = __builtin_fmaf(kb, cs, ka * sn);
   }
   // The first sub-block staged (and the next one's loads issued) before the
   // one barrier that publishes it together with qs and kn.
