@@ -922,15 +922,18 @@ constexpr int kAttnHeads = 4;   // query heads (wavefronts) per workgroup
 // into the cache; rows past the last position are zeroed when staged), the
 // new v, q and the cos / sin row.
 template <int NCH, bool GRAPH>
+// The arguments the first loads need come first (q, the cos / sin row, the
+// cache, the new v, its shape, the chunk, G = query heads per KV head, the
+// positions): the first 14 dwords arrive preloaded in SGPRs.
 __global__ void __launch_bounds__(kAttnHeads * 64) attn_part_1(const float* __restrict__ q,
-                                                               const float* __restrict__ knew,
-                                                               const float* __restrict__ vnew, float* __restrict__ kc,
-                                                               float* __restrict__ vc, const float* __restrict__ cos_t,
-                                                               const float* __restrict__ sin_t,
-                                                               float* __restrict__ part, int nh, int nkv, int cap,
-                                                               int npos, int chunk, float scale,
+                                                               const float* __restrict__ rope_dev,
+                                                               float* __restrict__ kc, float* __restrict__ vc,
+                                                               const float* __restrict__ vnew, int cap, int chunk,
+                                                               int G, int npos, const float* __restrict__ knew,
                                                                const int* __restrict__ npos_dev,
-                                                               const float* __restrict__ rope_dev) {
+                                                               const float* __restrict__ cos_t,
+                                                               const float* __restrict__ sin_t,
+                                                               float* __restrict__ part, int nh, float scale) {
   constexpr int hd = 16 * NCH, half = hd / 2;
   constexpr int kT = kAttnHeads * 64;
   constexpr int kLd = kAttnSub * hd / 4 / kT;  // float4 of K (and of V) per thread per sub-block
@@ -944,7 +947,6 @@ __global__ void __launch_bounds__(kAttnHeads * 64) attn_part_1(const float* __re
     if (static_cast<int>(blockIdx.x) * chunk >= npos) return;
   }
   const int c = blockIdx.x, kvh = blockIdx.y;
-  const int G = nh / nkv;
   const int g0 = blockIdx.z * kAttnHeads;
   const int ng = min(kAttnHeads, G - g0);
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
@@ -1152,7 +1154,7 @@ int launch_tol_attention(const float* q, const float* knew, const float* vnew, f
                   static_cast<unsigned>((G + kAttnHeads - 1) / kAttnHeads));
   const int* nd = g != nullptr ? g->npos_dev : nullptr;
   const float* rd = g != nullptr ? g->rope_dev : nullptr;
-#define LLMI_ATTN_ARGS q, knew, vnew, kc, vc, cos_t, sin_t, part, nh, nkv, cap, npos, chunk, scale, nd, rd
+#define LLMI_ATTN_ARGS q, rd, kc, vc, vnew, cap, chunk, G, npos, knew, nd, cos_t, sin_t, part, nh, scale
   if (g != nullptr) {
     if (hd == 64) attn_part_1<4, true><<<grid, kAttnHeads * 64, 0, s>>>(LLMI_ATTN_ARGS);
     else attn_part_1<8, true><<<grid, kAttnHeads * 64, 0, s>>>(LLMI_ATTN_ARGS);
